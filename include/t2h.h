@@ -1,0 +1,143 @@
+/*
+ * libt2h - MI355X (gfx950) kernels for torch2vk's quantized Qwen3 hot path.
+ *
+ * C ABI: plain device pointers, sizes and a hipStream_t passed as void*.
+ * Every entry point enqueues work on the caller's stream and returns a status
+ * (0 = ok).  Nothing here allocates device memory or synchronises the host:
+ * scratch space is a caller-provided workspace of a queried size, and dynamic
+ * scalars (cache position, token index) are device pointers, so a caller can
+ * capture any sequence of calls into a HIP graph and replay it.
+ *
+ * Packed weight formats are the GGUF blocks the reference's kernels read
+ * (src/torch2vk/checkpoints/gguf.py:79-95, src/torch2vk/vulkan/types.py:64-82):
+ *   Q4_K: 144 B / 256 values, Q6_K: 210 B / 256 values, Q8_0: 34 B / 32 values,
+ * row-major, one row per output feature.  Activations are bf16 (reference:
+ * fp16, src/torch2vk/export/dtype_policy.py:23-36); accumulation is fp32.
+ *
+ * Citations are to files under the reference tree taowen/torch2vk.
+ */
+#ifndef T2H_H
+#define T2H_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ status ---- */
+/* The reference raises ValueError/TypeError before a launch
+ * (src/torch2vk/runtime/dispatcher.py:35-53); these are the same checks. */
+enum {
+    T2H_OK = 0,
+    T2H_ERR_NULL = 1,        /* a required pointer is null */
+    T2H_ERR_SHAPE = 2,       /* shape violates the contract (e.g. K % 256 != 0) */
+    T2H_ERR_DTYPE = 3,       /* unsupported dtype combination */
+    T2H_ERR_UNSUPPORTED = 4, /* valid but not built (e.g. head_dim != 128) */
+    T2H_ERR_ARG = 5,         /* other invalid argument */
+    T2H_ERR_WORKSPACE = 6,   /* workspace smaller than the queried size */
+    T2H_ERR_ALIGN = 7,       /* pointer not 16-byte aligned */
+    T2H_ERR_HIP_BASE = 1000  /* 1000 + hipError_t of a failed launch */
+};
+
+enum { T2H_DTYPE_F32 = 0, T2H_DTYPE_BF16 = 1 };
+enum { T2H_WTYPE_Q4_K = 12, T2H_WTYPE_Q6_K = 14, T2H_WTYPE_Q8_0 = 8 }; /* GGUF type ids, gguf.py:19-53 */
+
+int t2h_abi_version(void);
+const char* t2h_status_string(int status);
+
+/* --------------------------------------------------------- quantizers --- */
+/* fp32 [rows, k] -> packed GGUF rows, bit-identical to the reference GLSL
+ * restated with IEEE RNE rounding and no fma contraction. */
+/* replaces quantize_q4_k_vulkan / GGUF_QUANTIZE_Q4_K_F32, src/torch2vk/quantize/vulkan.py:39-50,188-419 */
+int t2h_quantize_q4_k(const float* x, uint32_t rows, uint32_t k, void* out, void* stream);
+/* replaces quantize_q6_k_vulkan / GGUF_QUANTIZE_Q6_K_F32, src/torch2vk/quantize/vulkan.py:53-66,422-636 */
+int t2h_quantize_q6_k(const float* x, uint32_t rows, uint32_t k, void* out, void* stream);
+/* replaces quantize_q8_0_vulkan / GGUF_QUANTIZE_Q8_0_F32, src/torch2vk/quantize/vulkan.py:25-36,91-185
+ * (k must already be padded to a multiple of 32, as gguf.py:125-127 declares) */
+int t2h_quantize_q8_0(const float* x, uint32_t rows, uint32_t k, void* out, void* stream);
+/* packed rows -> fp32 [rows, k]; the reference decoders' value formula
+ * (src/models/quantized_qwen3/shaders/embedding_q4_k_f32.py:97-110 and the K6/K7 decoders) */
+int t2h_dequantize(int wtype, const void* w, uint32_t rows, uint32_t k, float* out, void* stream);
+
+/* ------------------------------------------------------ decode GEMVs ---- */
+/* y[m, n] = x[m, k] . deq(W[n, k])^T (+ residual[m, n]); x bf16, out fp32 or bf16.
+ * replaces LINEAR_NOBIAS_Q4_K_MATVEC_F32 (src/models/optimized_qwen3/shaders/linear_nobias_q4_k_matvec_f32.py:26-197)
+ * and, with residual != NULL (fp32 out), LINEAR_NOBIAS_Q4_K_MATVEC_ADD_F32
+ * (src/models/optimized_qwen3/shaders/linear_nobias_q4_k_matvec_add_f32.py:23-100).  residual may alias y. */
+int t2h_q4k_matvec(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                   uint32_t k, uint32_t n, void* stream);
+
+/* Up to 3 weights sharing one x read: Q|K|V or gate|up.  With norm_w != NULL,
+ * x is the fp32 residual stream and RMSNorm(x)*norm_w is fused as a prologue.
+ * replaces LINEAR_NOBIAS_Q4_K_QKV_MATVEC_F32 (src/models/optimized_qwen3/shaders/linear_nobias_q4_k_qkv_matvec_f32.py:22-430),
+ * LINEAR_NOBIAS_Q4_K_QK_MATVEC_F32 (.../linear_nobias_q4_k_qk_matvec_f32.py:22-315) and, fused in front,
+ * RMS_NORM_MUL_F16_F32 (.../rms_norm_mul_f16_f32.py:22-115). */
+int t2h_q4k_matvec_multi(const void* x, const float* norm_w, float eps, uint32_t n_parts, const void* const* w,
+                         void* const* y, const uint32_t* n, uint32_t k, int out_dtype, void* stream);
+
+/* act[n] = silu(g) * u with g|u = RMSNorm(h)*norm_w . deq(W_gate|W_up)^T; act bf16.
+ * replaces RMS_NORM_MUL_F16_F32 + LINEAR_NOBIAS_Q4_K_QK_MATVEC_F32 + SWIGLU_F16
+ * (src/models/optimized_qwen3/dispatch/decode_layer.py:107-121). */
+int t2h_q4k_rmsnorm_swiglu_matvec(const float* h, const float* norm_w, float eps, const void* w_gate,
+                                  const void* w_up, void* act_out, uint32_t k, uint32_t n, void* stream);
+
+/* LM head GEMV fused with a per-block argmax; logits are never materialised.
+ * x: bf16 normed hidden (norm_w == NULL) or fp32 residual stream with the
+ * final RMSNorm fused (norm_w != NULL).  Writes num_partials (score, token)
+ * pairs; ties go to the lower token id.
+ * replaces LM_HEAD_Q6_K_ARGMAX_PARTIAL_F16 (src/torch2vk/export/shaders/lm_head_q6_k_argmax_partial_f16.py:24-209)
+ * for Q4_K weights, plus run_decode_norm in front (src/models/optimized_qwen3/dispatch/decode_norm.py). */
+int t2h_q4k_lm_head_argmax_partial(const void* x, const float* norm_w, float eps, const void* w, uint32_t k,
+                                   uint32_t n, float* partial_scores, uint32_t* partial_tokens,
+                                   uint32_t num_partials, void* stream);
+
+/* Grid cap of the GEMV launches (tuning knob; default 2048 blocks of 4 waves). */
+int t2h_set_gemv_max_blocks(uint32_t max_blocks);
+
+/* ---------------------------------------------------- token selection --- */
+/* replaces QWEN3_TOKEN_SELECT_REDUCE_CHUNKS_F32 + QWEN3_TOKEN_SELECT_REDUCE_F32
+ * (src/torch2vk/export/shaders/qwen3_token_select_reduce_f32.py:22-241): one pass over g partials. */
+int t2h_token_select(const float* scores, const uint32_t* tokens, uint32_t g, const int64_t* eos, uint32_t n_eos,
+                     int64_t* next_token, uint32_t* done, void* stream);
+
+/* replaces QWEN3_TOKEN_STORE_EOS_F32 (src/models/optimized_qwen3/shaders/qwen3_token_store_eos_f32.py:21-140).
+ * token_index_ptr (device, nullable) overrides token_index; advance (device,
+ * nullable) is incremented once per call for graph-replayed loops. */
+int t2h_token_store(const int64_t* next_token, const uint32_t* done, int64_t* generated, uint32_t g,
+                    uint32_t* length, uint32_t* stopped, uint32_t stop_on_eos, const uint32_t* token_index_ptr,
+                    uint32_t token_index, int32_t* advance, void* stream);
+
+/* ------------------------------------------------- decode attention ---- */
+/* Split-K flash decoding over a bf16 token-major cache [s_cap, nk, d] (d = 128).
+ * q [nh, d], k_new/v_new [nk, d] fp32 projections.  With q_norm_w/k_norm_w,
+ * per-head RMSNorm is applied; with theta > 0, rotate-half RoPE at
+ * *cache_position.  The new K/V row is written at *cache_position (if
+ * < s_cap) and attention covers positions 0..min(*cache_position, s_cap-1).
+ * out bf16 [nh, d].  workspace: t2h_attn_decode_workspace_bytes(), zeroed once
+ * by the caller before first use (the kernel leaves it reusable).
+ * replaces RMS_NORM_ROPE_TRANSPOSE_F16 x2 (src/models/optimized_qwen3/shaders/rms_norm_rope_transpose_f16.py:22-145),
+ * ROPE_TABLE_F32 (src/torch2vk/runtime/rope_table.py:32-122) and
+ * SDPA_DECODE_CACHE_WRITE_F32 (src/models/optimized_qwen3/shaders/sdpa_decode_cache_write_f32.py:22-170). */
+size_t t2h_attn_decode_workspace_bytes(uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap);
+int t2h_attn_decode(const float* q, const float* k_new, const float* v_new, const float* q_norm_w,
+                    const float* k_norm_w, float eps, float theta, void* k_cache, void* v_cache, void* out,
+                    uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap, const int32_t* cache_position,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------ small ops ------ */
+/* replaces EMBEDDING_Q4_K_F32 (src/models/quantized_qwen3/shaders/embedding_q4_k_f32.py:62-121); out fp32 [n_ids, dim] */
+int t2h_embedding_q4_k(const void* w, uint64_t vocab, const int64_t* ids, uint32_t n_ids, uint32_t dim, float* out,
+                       void* stream);
+/* replaces RMS_NORM_MUL_F16_F32 / RMS_NORM_MUL_F32 (src/models/optimized_qwen3/shaders/rms_norm_mul_f16_f32.py:22-115) */
+int t2h_rms_norm(const void* x, int x_dtype, const float* w, void* out, int out_dtype, uint32_t rows, uint32_t h,
+                 float eps, void* stream);
+/* replaces SWIGLU_F16 / SWIGLU_F32 (src/models/optimized_qwen3/shaders/swiglu_f16.py:20-81); out bf16 */
+int t2h_swiglu(const void* gate, const void* up, int in_dtype, void* out, uint64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* T2H_H */

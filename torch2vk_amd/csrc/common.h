@@ -1,0 +1,120 @@
+// Device helpers shared by the gfx950 kernels of libt2h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "t2h.h"
+
+#define T2H_WAVE 64
+
+namespace t2h {
+
+// ---------------------------------------------------------------- numbers --
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float v) {
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// IEEE binary16 -> fp32 (exact).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffffu));
+}
+
+// fp32 -> binary16 bits, round to nearest even, subnormals kept.  Written out
+// bit by bit so that it matches the CPU oracle exactly, independent of the
+// hardware conversion's denormal mode.
+__device__ __forceinline__ uint32_t f32_to_f16_bits_rne(float value) {
+    uint32_t bits = __float_as_uint(value);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const uint32_t exp = (bits >> 23) & 0xffu;
+    uint32_t mant = bits & 0x7fffffu;
+    if (exp == 0xffu) return sign | 0x7c00u | (mant ? 0x200u : 0u);
+    const int e = (int)exp - 127 + 15;
+    if (e >= 31) return sign | 0x7c00u;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        mant |= 0x800000u;
+        const uint32_t shift = (uint32_t)(14 - e);
+        uint32_t half_mant = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u);
+        const uint32_t halfway = 1u << (shift - 1u);
+        if (rem > halfway || (rem == halfway && (half_mant & 1u))) half_mant += 1u;
+        return sign | half_mant;
+    }
+    uint32_t half = ((uint32_t)e << 10) | (mant >> 13);
+    const uint32_t rem = mant & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (half & 1u))) half += 1u;
+    return sign | half;
+}
+
+// ------------------------------------------------------------- reductions --
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, T2H_WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, T2H_WAVE));
+    return v;
+}
+
+// (score, token) argmax with the reference tie rule: higher score wins, equal
+// scores go to the lower token id.
+__device__ __forceinline__ bool better_pair(float ls, uint32_t lt, float rs, uint32_t rt) {
+    return ls > rs || (ls == rs && lt < rt);
+}
+
+__device__ __forceinline__ void wave_argmax(float& score, uint32_t& token) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float os = __shfl_xor(score, off, T2H_WAVE);
+        const uint32_t ot = (uint32_t)__shfl_xor((int)token, off, T2H_WAVE);
+        if (better_pair(os, ot, score, token)) {
+            score = os;
+            token = ot;
+        }
+    }
+}
+
+// --------------------------------------------------------------- loads -----
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Streaming 16-byte load for weights that are read exactly once per pass.
+__device__ __forceinline__ uint4 load_nt_u4(const void* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float2 load_nt_f2(const float* p) {
+    const f32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const f32x2_t*>(p));
+    return make_float2(v.x, v.y);
+}
+
+__device__ __forceinline__ uint4 load_u4(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+}  // namespace t2h
+
+// Launch-result helper for the C-ABI layer.
+#define T2H_LAUNCH_CHECK()                                     \
+    do {                                                       \
+        hipError_t _e = hipGetLastError();                     \
+        if (_e != hipSuccess) return T2H_ERR_HIP_BASE + (int)_e; \
+    } while (0)

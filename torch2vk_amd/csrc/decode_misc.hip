@@ -1,0 +1,208 @@
+// Small decode-step kernels: embedding gather, greedy token select, token
+// store, standalone RMSNorm and SwiGLU.
+//
+//   EMBEDDING_Q4_K_F32                   src/models/quantized_qwen3/shaders/embedding_q4_k_f32.py:62-121
+//   QWEN3_TOKEN_SELECT_REDUCE_{CHUNKS_,}F32  src/torch2vk/export/shaders/qwen3_token_select_reduce_f32.py:22-241
+//   QWEN3_TOKEN_STORE_EOS_F32            src/models/optimized_qwen3/shaders/qwen3_token_store_eos_f32.py:21-140
+//   RMS_NORM_MUL_F16_F32                 src/models/optimized_qwen3/shaders/rms_norm_mul_f16_f32.py:22-115
+//   SWIGLU_F16                           src/models/optimized_qwen3/shaders/swiglu_f16.py:20-81
+#include "common.h"
+
+namespace t2h {
+
+// One block per token: dequantise the token's Q4_K embedding row into fp32.
+__global__ __launch_bounds__(256) void embedding_q4_k_kernel(const uint8_t* __restrict__ w,
+                                                             const int64_t* __restrict__ ids, uint32_t dim,
+                                                             uint64_t vocab, float* __restrict__ out) {
+    const uint32_t t = blockIdx.x;
+    int64_t id = ids[t];
+    if (id < 0 || (uint64_t)id >= vocab) id = 0;  // the host validates host-side ids; device ids are clamped
+    const uint8_t* row = w + (uint64_t)id * (dim / 256) * 144;
+    for (uint32_t h = threadIdx.x; h < dim; h += blockDim.x) {
+        const uint8_t* blk = row + (h >> 8) * 144;
+        const int i = h & 255;
+        const int sb = i >> 5;
+        uint32_t sc, m;
+        if (sb < 4) {
+            sc = blk[4 + sb] & 63u;
+            m = blk[8 + sb] & 63u;
+        } else {
+            sc = (blk[12 + sb - 4] & 15u) | ((uint32_t)(blk[4 + sb - 4] >> 6) << 4);
+            m = ((uint32_t)blk[12 + sb - 4] >> 4) | ((uint32_t)(blk[8 + sb - 4] >> 6) << 4);
+        }
+        const int byte = ((i >> 6) * 32) + (i & 31);
+        const uint32_t q = (i & 32) ? ((uint32_t)blk[16 + byte] >> 4) : (blk[16 + byte] & 15u);
+        const float d = f16_bits_to_f32(blk[0] | ((uint32_t)blk[1] << 8));
+        const float dmin = f16_bits_to_f32(blk[2] | ((uint32_t)blk[3] << 8));
+        out[(uint64_t)t * dim + h] = d * (float)sc * (float)q - dmin * (float)m;
+    }
+}
+
+// Reduce G (score, token) partials to one greedy token; flag EOS.
+__global__ __launch_bounds__(1024) void token_select_kernel(const float* __restrict__ scores,
+                                                            const uint32_t* __restrict__ tokens, uint32_t g,
+                                                            const int64_t* __restrict__ eos, uint32_t n_eos,
+                                                            int64_t* __restrict__ next_token,
+                                                            uint32_t* __restrict__ done) {
+    __shared__ float ss[16];
+    __shared__ uint32_t st[16];
+    float bs = -3.4028234663852886e38f;
+    uint32_t bt = 0xffffffffu;
+    for (uint32_t i = threadIdx.x; i < g; i += blockDim.x) {
+        if (better_pair(scores[i], tokens[i], bs, bt)) {
+            bs = scores[i];
+            bt = tokens[i];
+        }
+    }
+    wave_argmax(bs, bt);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        ss[wave] = bs;
+        st[wave] = bt;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float s = ss[0];
+        uint32_t t = st[0];
+        for (int i = 1; i < (int)(blockDim.x >> 6); ++i) {
+            if (better_pair(ss[i], st[i], s, t)) {
+                s = ss[i];
+                t = st[i];
+            }
+        }
+        next_token[0] = (int64_t)t;
+        uint32_t is_done = 0;
+        for (uint32_t i = 0; i < n_eos; ++i) is_done |= ((int64_t)t == eos[i]) ? 1u : 0u;
+        if (done) done[0] = is_done;
+    }
+}
+
+// generated_tokens[index] = next_token; length = index + 1; stop on EOS.
+// index comes from token_index_ptr (device) when given, else token_index.
+// advance (optional, device) is incremented after a store: the caller's
+// cache-position counter for graph-replayed decode loops.
+__global__ void token_store_kernel(const int64_t* __restrict__ next_token, const uint32_t* __restrict__ done,
+                                   int64_t* __restrict__ generated, uint32_t g, uint32_t* __restrict__ length,
+                                   uint32_t* __restrict__ stopped, uint32_t stop_on_eos,
+                                   const uint32_t* __restrict__ token_index_ptr, uint32_t token_index,
+                                   int32_t* __restrict__ advance) {
+    const uint32_t index = token_index_ptr ? *token_index_ptr : token_index;
+    if (advance) advance[0] += 1;
+    if (index >= g) return;
+    if (stop_on_eos && stopped[0] != 0u) return;
+    generated[index] = next_token[0];
+    length[0] = index + 1u;
+    if (stop_on_eos && done && done[0] != 0u) stopped[0] = 1u;
+}
+
+// rows x H RMSNorm; x and out are fp32 or bf16, weight fp32.
+template <bool XBF16, bool OBF16>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const void* __restrict__ xv, const float* __restrict__ w,
+                                                       void* __restrict__ outv, uint32_t h, float eps) {
+    __shared__ float red[4];
+    const uint64_t base = (uint64_t)blockIdx.x * h;
+    auto ld = [&](uint32_t i) -> float {
+        if constexpr (XBF16) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(xv)[base + i]);
+        else return reinterpret_cast<const float*>(xv)[base + i];
+    };
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < h; i += 256) {
+        const float v = ld(i);
+        ss = fmaf(v, v, ss);
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = red[0] + red[1] + red[2] + red[3];
+    const float inv = 1.0f / sqrtf(total / (float)h + eps);
+    for (uint32_t i = threadIdx.x; i < h; i += 256) {
+        const float v = ld(i) * inv * w[i];
+        if constexpr (OBF16) reinterpret_cast<uint16_t*>(outv)[base + i] = (uint16_t)f32_to_bf16_bits(v);
+        else reinterpret_cast<float*>(outv)[base + i] = v;
+    }
+}
+
+template <bool GBF16>
+__global__ void swiglu_kernel(const void* __restrict__ gate, const void* __restrict__ up,
+                              uint16_t* __restrict__ out, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float g, u;
+    if constexpr (GBF16) {
+        g = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(gate)[i]);
+        u = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(up)[i]);
+    } else {
+        g = reinterpret_cast<const float*>(gate)[i];
+        u = reinterpret_cast<const float*>(up)[i];
+    }
+    out[i] = (uint16_t)f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
+}
+
+}  // namespace t2h
+
+using namespace t2h;
+
+extern "C" int t2h_embedding_q4_k(const void* w, uint64_t vocab, const int64_t* ids, uint32_t n_ids, uint32_t dim,
+                                  float* out, void* stream) {
+    if (!w || !ids || !out) return T2H_ERR_NULL;
+    if (dim == 0 || dim % 256 != 0 || vocab == 0) return T2H_ERR_SHAPE;
+    if (n_ids == 0) return T2H_OK;
+    hipLaunchKernelGGL(embedding_q4_k_kernel, dim3(n_ids), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)w, ids, dim, vocab, out);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+extern "C" int t2h_token_select(const float* scores, const uint32_t* tokens, uint32_t g, const int64_t* eos,
+                                uint32_t n_eos, int64_t* next_token, uint32_t* done, void* stream) {
+    if (!scores || !tokens || !next_token) return T2H_ERR_NULL;
+    if (n_eos && !eos) return T2H_ERR_NULL;
+    if (g == 0) return T2H_ERR_SHAPE;
+    hipLaunchKernelGGL(token_select_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, scores, tokens, g, eos,
+                       n_eos, next_token, done);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+extern "C" int t2h_token_store(const int64_t* next_token, const uint32_t* done, int64_t* generated, uint32_t g,
+                               uint32_t* length, uint32_t* stopped, uint32_t stop_on_eos,
+                               const uint32_t* token_index_ptr, uint32_t token_index, int32_t* advance,
+                               void* stream) {
+    if (!next_token || !generated || !length || !stopped) return T2H_ERR_NULL;
+    hipLaunchKernelGGL(token_store_kernel, dim3(1), dim3(1), 0, (hipStream_t)stream, next_token, done, generated, g,
+                       length, stopped, stop_on_eos, token_index_ptr, token_index, advance);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+extern "C" int t2h_rms_norm(const void* x, int x_dtype, const float* w, void* out, int out_dtype, uint32_t rows,
+                            uint32_t h, float eps, void* stream) {
+    if (!x || !w || !out) return T2H_ERR_NULL;
+    if (h == 0) return T2H_ERR_SHAPE;
+    if (rows == 0) return T2H_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const bool xb = x_dtype == T2H_DTYPE_BF16, ob = out_dtype == T2H_DTYPE_BF16;
+    if ((!xb && x_dtype != T2H_DTYPE_F32) || (!ob && out_dtype != T2H_DTYPE_F32)) return T2H_ERR_DTYPE;
+    if (xb && ob) hipLaunchKernelGGL((rms_norm_kernel<true, true>), dim3(rows), dim3(256), 0, s, x, w, out, h, eps);
+    else if (xb) hipLaunchKernelGGL((rms_norm_kernel<true, false>), dim3(rows), dim3(256), 0, s, x, w, out, h, eps);
+    else if (ob) hipLaunchKernelGGL((rms_norm_kernel<false, true>), dim3(rows), dim3(256), 0, s, x, w, out, h, eps);
+    else hipLaunchKernelGGL((rms_norm_kernel<false, false>), dim3(rows), dim3(256), 0, s, x, w, out, h, eps);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+extern "C" int t2h_swiglu(const void* gate, const void* up, int in_dtype, void* out, uint64_t n, void* stream) {
+    if (!gate || !up || !out) return T2H_ERR_NULL;
+    if (n == 0) return T2H_OK;
+    const uint64_t grid = (n + 255) / 256;
+    if (grid > 0x7fffffffull) return T2H_ERR_SHAPE;
+    hipStream_t s = (hipStream_t)stream;
+    if (in_dtype == T2H_DTYPE_BF16)
+        hipLaunchKernelGGL(swiglu_kernel<true>, dim3((uint32_t)grid), dim3(256), 0, s, gate, up, (uint16_t*)out, n);
+    else if (in_dtype == T2H_DTYPE_F32)
+        hipLaunchKernelGGL(swiglu_kernel<false>, dim3((uint32_t)grid), dim3(256), 0, s, gate, up, (uint16_t*)out, n);
+    else
+        return T2H_ERR_DTYPE;
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}

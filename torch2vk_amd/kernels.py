@@ -1,0 +1,303 @@
+"""Checked torch-tensor wrappers over the libt2h C ABI.
+
+Each function validates device, dtype, shape, contiguity and alignment on the
+host (the reference does the same before a launch, src/torch2vk/runtime/dispatcher.py:35-53)
+and then enqueues one C-ABI call on the current HIP stream.  Nothing here
+computes on the CPU: there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from torch2vk_amd import _lib
+from torch2vk_amd._lib import T2H_DTYPE_BF16, T2H_DTYPE_F32, call, ptr, stream_handle
+
+Q4_K_BYTES = 144
+Q6_K_BYTES = 210
+Q8_0_BYTES = 34
+RMS_EPS = 1e-6
+
+_OUT_DTYPES = {torch.float32: T2H_DTYPE_F32, torch.bfloat16: T2H_DTYPE_BF16}
+WTYPES = {"q4_k": _lib.T2H_WTYPE_Q4_K, "q6_k": _lib.T2H_WTYPE_Q6_K, "q8_0": _lib.T2H_WTYPE_Q8_0}
+
+
+def _check(t: torch.Tensor, name: str, dtype: torch.dtype | tuple[torch.dtype, ...], *, align: int = 16) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must live on a HIP device, got {t.device}")
+    dtypes = dtype if isinstance(dtype, tuple) else (dtype,)
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name} dtype {t.dtype} not in {dtypes}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.data_ptr() % align:
+        raise ValueError(f"{name} must be {align}-byte aligned")
+
+
+def q4_k_row_bytes(k: int) -> int:
+    if k % 256:
+        raise ValueError(f"Q4_K needs K % 256 == 0, got {k}")
+    return k // 256 * Q4_K_BYTES
+
+
+def _check_q4(w: torch.Tensor, name: str, n: int | None, k: int) -> int:
+    _check(w, name, torch.uint8)
+    if w.dim() != 2 or w.shape[1] != q4_k_row_bytes(k):
+        raise ValueError(f"{name} must be uint8 [N, {q4_k_row_bytes(k)}] for K={k}, got {tuple(w.shape)}")
+    if n is not None and w.shape[0] != n:
+        raise ValueError(f"{name} has {w.shape[0]} rows, expected {n}")
+    return int(w.shape[0])
+
+
+# ------------------------------------------------------------ quantizers --
+
+
+def quantize(x: torch.Tensor, wtype: str) -> torch.Tensor:
+    """fp32 [R, K] -> packed GGUF rows (uint8), bit-identical to the CPU oracle."""
+    _check(x, "x", torch.float32)
+    if x.dim() != 2:
+        raise ValueError(f"x must be rank 2, got {tuple(x.shape)}")
+    rows, k = x.shape
+    if wtype == "q8_0":
+        padded = (k + 31) // 32 * 32
+        if padded != k:
+            x = torch.nn.functional.pad(x, (0, padded - k)).contiguous()
+        out = torch.empty(rows, padded // 32 * Q8_0_BYTES, dtype=torch.uint8, device=x.device)
+        call("t2h_quantize_q8_0", ptr(x), rows, padded, ptr(out), stream_handle())
+        return out
+    if k % 256:
+        raise ValueError(f"{wtype} needs K % 256 == 0, got {k}")
+    if wtype == "q4_k":
+        out = torch.empty(rows, k // 256 * Q4_K_BYTES, dtype=torch.uint8, device=x.device)
+        call("t2h_quantize_q4_k", ptr(x), rows, k, ptr(out), stream_handle())
+    elif wtype == "q6_k":
+        out = torch.empty(rows, k // 256 * Q6_K_BYTES, dtype=torch.uint8, device=x.device)
+        call("t2h_quantize_q6_k", ptr(x), rows, k, ptr(out), stream_handle())
+    else:
+        raise ValueError(f"unknown weight type {wtype!r}")
+    return out
+
+
+def dequantize(w: torch.Tensor, wtype: str, k: int) -> torch.Tensor:
+    """Packed GGUF rows -> fp32 [R, K]."""
+    _check(w, "w", torch.uint8, align=1)
+    rows = int(w.shape[0])
+    out = torch.empty(rows, k, dtype=torch.float32, device=w.device)
+    call("t2h_dequantize", WTYPES[wtype], ptr(w), rows, k, ptr(out), stream_handle())
+    return out
+
+
+# ------------------------------------------------------------ GEMV family --
+
+
+def q4k_matvec(x: torch.Tensor, w: torch.Tensor, *, out: torch.Tensor | None = None,
+               out_dtype: torch.dtype = torch.float32, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """y[M, N] = x[M, K] . deq(W)^T (+ residual); x bf16."""
+    _check(x, "x", torch.bfloat16)
+    k = int(x.shape[-1])
+    m = x.numel() // k
+    n = _check_q4(w, "weight", None, k)
+    if out is None:
+        out = torch.empty(*x.shape[:-1], n, dtype=out_dtype, device=x.device)
+    _check(out, "output", tuple(_OUT_DTYPES), align=4)
+    if out.numel() != m * n:
+        raise ValueError(f"output has {out.numel()} elements, expected {m * n}")
+    if residual is not None:
+        _check(residual, "residual", torch.float32, align=4)
+        if residual.numel() != m * n or out.dtype != torch.float32:
+            raise ValueError("residual must be fp32 with the output's shape; output must be fp32")
+    call("t2h_q4k_matvec", ptr(x), ptr(w), ptr(out), _OUT_DTYPES[out.dtype], ptr(residual), m, k, n,
+         stream_handle())
+    return out
+
+
+def _ptr_array(values):
+    arr = (_lib.ctypes.c_void_p * len(values))(*values)
+    return arr
+
+
+def q4k_matvec_multi(x: torch.Tensor, weights: list[torch.Tensor], outs: list[torch.Tensor], *,
+                     norm_weight: torch.Tensor | None = None, eps: float = RMS_EPS) -> None:
+    """Q|K|V (or gate|up) sharing one x; with norm_weight, x is the fp32 residual stream normalised in-kernel."""
+    if norm_weight is None:
+        _check(x, "x", torch.bfloat16)
+    else:
+        _check(x, "x", torch.float32)
+        _check(norm_weight, "norm_weight", torch.float32)
+        if norm_weight.numel() != x.numel():
+            raise ValueError("norm_weight must have K elements")
+    k = int(x.numel())
+    if len(weights) != len(outs) or not 1 <= len(weights) <= 3:
+        raise ValueError("need 1..3 weights and as many outputs")
+    ns = []
+    out_dtype = outs[0].dtype
+    for i, (w, o) in enumerate(zip(weights, outs)):
+        n = _check_q4(w, f"weight[{i}]", None, k)
+        _check(o, f"output[{i}]", out_dtype, align=4)
+        if o.numel() != n:
+            raise ValueError(f"output[{i}] has {o.numel()} elements, expected {n}")
+        ns.append(n)
+    if out_dtype not in _OUT_DTYPES:
+        raise TypeError(f"unsupported output dtype {out_dtype}")
+    wp = _ptr_array([ptr(w) for w in weights])
+    yp = _ptr_array([ptr(o) for o in outs])
+    nn = (_lib.ctypes.c_uint32 * len(ns))(*ns)
+    call("t2h_q4k_matvec_multi", ptr(x), ptr(norm_weight), eps, len(weights), wp, yp, nn, k,
+         _OUT_DTYPES[out_dtype], stream_handle())
+
+
+def q4k_rmsnorm_swiglu(h: torch.Tensor, norm_weight: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
+                       out: torch.Tensor, eps: float = RMS_EPS) -> torch.Tensor:
+    """act = silu(g) * u, g|u = RMSNorm(h) . deq(W_gate|W_up)^T; act bf16 [N]."""
+    _check(h, "h", torch.float32)
+    _check(norm_weight, "norm_weight", torch.float32)
+    k = int(h.numel())
+    n = _check_q4(w_gate, "gate_weight", None, k)
+    _check_q4(w_up, "up_weight", n, k)
+    _check(out, "output", torch.bfloat16, align=4)
+    if out.numel() != n:
+        raise ValueError(f"output must have {n} elements")
+    call("t2h_q4k_rmsnorm_swiglu_matvec", ptr(h), ptr(norm_weight), eps, ptr(w_gate), ptr(w_up), ptr(out), k, n,
+         stream_handle())
+    return out
+
+
+def q4k_lm_head_argmax_partial(x: torch.Tensor, w: torch.Tensor, partial_scores: torch.Tensor,
+                               partial_tokens: torch.Tensor, *, norm_weight: torch.Tensor | None = None,
+                               eps: float = RMS_EPS) -> None:
+    if norm_weight is None:
+        _check(x, "x", torch.bfloat16)
+    else:
+        _check(x, "x", torch.float32)
+        _check(norm_weight, "norm_weight", torch.float32)
+    k = int(x.numel())
+    n = _check_q4(w, "weight", None, k)
+    _check(partial_scores, "partial_scores", torch.float32, align=4)
+    _check(partial_tokens, "partial_tokens", torch.int32, align=4)
+    g = int(partial_scores.numel())
+    if partial_tokens.numel() != g or g == 0:
+        raise ValueError("partial_scores and partial_tokens must have the same non-zero length")
+    call("t2h_q4k_lm_head_argmax_partial", ptr(x), ptr(norm_weight), eps, ptr(w), k, n, ptr(partial_scores),
+         ptr(partial_tokens), g, stream_handle())
+
+
+def set_gemv_max_blocks(max_blocks: int) -> None:
+    call("t2h_set_gemv_max_blocks", int(max_blocks))
+
+
+# ------------------------------------------------------- token selection --
+
+
+def token_select(partial_scores: torch.Tensor, partial_tokens: torch.Tensor, eos_ids: torch.Tensor,
+                 next_token: torch.Tensor, done: torch.Tensor) -> None:
+    _check(partial_scores, "scores", torch.float32, align=4)
+    _check(partial_tokens, "tokens", torch.int32, align=4)
+    _check(eos_ids, "eos_token_ids", torch.int64, align=8)
+    _check(next_token, "next_token", torch.int64, align=8)
+    _check(done, "done", torch.int32, align=4)
+    call("t2h_token_select", ptr(partial_scores), ptr(partial_tokens), partial_scores.numel(), ptr(eos_ids),
+         eos_ids.numel(), ptr(next_token), ptr(done), stream_handle())
+
+
+def token_store(next_token: torch.Tensor, done: torch.Tensor, generated: torch.Tensor, length: torch.Tensor,
+                stopped: torch.Tensor, *, stop_on_eos: bool = True, token_index: int = 0,
+                token_index_ptr: torch.Tensor | None = None, advance: torch.Tensor | None = None) -> None:
+    _check(next_token, "next_token", torch.int64, align=8)
+    _check(done, "done", torch.int32, align=4)
+    _check(generated, "generated_tokens", torch.int64, align=8)
+    _check(length, "generated_length", torch.int32, align=4)
+    _check(stopped, "stopped", torch.int32, align=4)
+    if token_index_ptr is not None:
+        _check(token_index_ptr, "token_index", torch.int32, align=4)
+    if advance is not None:
+        _check(advance, "advance", torch.int32, align=4)
+    call("t2h_token_store", ptr(next_token), ptr(done), ptr(generated), generated.numel(), ptr(length),
+         ptr(stopped), int(stop_on_eos), ptr(token_index_ptr), int(token_index), ptr(advance), stream_handle())
+
+
+# ------------------------------------------------------ decode attention --
+
+
+def attn_decode_workspace_bytes(nh: int, nk: int, d: int, s_cap: int) -> int:
+    n = int(_lib.lib().t2h_attn_decode_workspace_bytes(nh, nk, d, s_cap))
+    if n == 0:
+        raise ValueError(f"unsupported attention shape nh={nh} nk={nk} d={d}")
+    return n
+
+
+def attn_decode_workspace(nh: int, nk: int, d: int, s_cap: int, device) -> torch.Tensor:
+    """Zeroed workspace; the kernel leaves it reusable across calls."""
+    return torch.zeros(attn_decode_workspace_bytes(nh, nk, d, s_cap), dtype=torch.uint8, device=device)
+
+
+def attn_decode(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                v_cache: torch.Tensor, out: torch.Tensor, cache_position: torch.Tensor, workspace: torch.Tensor, *,
+                q_norm_weight: torch.Tensor | None = None, k_norm_weight: torch.Tensor | None = None,
+                theta: float = 0.0, eps: float = RMS_EPS) -> torch.Tensor:
+    """One-token split-K attention; q [NH, D], k_new/v_new [NK, D] fp32; caches bf16 [S, NK, D]."""
+    for t, name in ((q, "q"), (k_new, "new_k"), (v_new, "new_v")):
+        _check(t, name, torch.float32, align=4)
+    _check(k_cache, "k_cache", torch.bfloat16)
+    _check(v_cache, "v_cache", torch.bfloat16)
+    _check(out, "output", torch.bfloat16, align=4)
+    _check(cache_position, "cache_position", torch.int32, align=4)
+    _check(workspace, "workspace", torch.uint8)
+    if k_cache.dim() != 3 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache/v_cache must both be [S, NK, D]")
+    s_cap, nk, d = k_cache.shape
+    nh = q.numel() // d
+    if q.numel() != nh * d or k_new.numel() != nk * d or v_new.numel() != nk * d or out.numel() != nh * d:
+        raise ValueError("q/new_k/new_v/output sizes do not match the cache's NK and D")
+    for t, name in ((q_norm_weight, "q_norm"), (k_norm_weight, "k_norm")):
+        if t is not None:
+            _check(t, name, torch.float32, align=4)
+            if t.numel() != d:
+                raise ValueError(f"{name} weight must have D elements")
+    call("t2h_attn_decode", ptr(q), ptr(k_new), ptr(v_new), ptr(q_norm_weight), ptr(k_norm_weight), eps, theta,
+         ptr(k_cache), ptr(v_cache), ptr(out), nh, nk, d, s_cap, ptr(cache_position), ptr(workspace),
+         workspace.numel(), stream_handle())
+    return out
+
+
+# -------------------------------------------------------------- small ops --
+
+
+def embedding_q4_k(w: torch.Tensor, ids: torch.Tensor, dim: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    _check(w, "weight", torch.uint8, align=1)
+    _check(ids, "indices", torch.int64, align=8)
+    if w.shape[1] != q4_k_row_bytes(dim):
+        raise ValueError("embedding weight width does not match dim")
+    if out is None:
+        out = torch.empty(ids.numel(), dim, dtype=torch.float32, device=w.device)
+    _check(out, "output", torch.float32, align=4)
+    call("t2h_embedding_q4_k", ptr(w), int(w.shape[0]), ptr(ids), ids.numel(), dim, ptr(out), stream_handle())
+    return out
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
+             eps: float = RMS_EPS) -> torch.Tensor:
+    _check(x, "x", tuple(_OUT_DTYPES), align=2)
+    _check(weight, "weight", torch.float32, align=4)
+    h = int(x.shape[-1])
+    if weight.numel() != h:
+        raise ValueError("weight must have H elements")
+    if out is None:
+        out = torch.empty_like(x)
+    _check(out, "output", tuple(_OUT_DTYPES), align=2)
+    call("t2h_rms_norm", ptr(x), _OUT_DTYPES[x.dtype], ptr(weight), ptr(out), _OUT_DTYPES[out.dtype],
+         x.numel() // h, h, eps, stream_handle())
+    return out
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    _check(gate, "gate", tuple(_OUT_DTYPES), align=2)
+    _check(up, "up", gate.dtype, align=2)
+    if up.shape != gate.shape:
+        raise ValueError("gate and up must have the same shape")
+    if out is None:
+        out = torch.empty(gate.shape, dtype=torch.bfloat16, device=gate.device)
+    _check(out, "output", torch.bfloat16, align=2)
+    call("t2h_swiglu", ptr(gate), ptr(up), _OUT_DTYPES[gate.dtype], ptr(out), gate.numel(), stream_handle())
+    return out
