@@ -1,0 +1,296 @@
+"""Headline benchmark: Qwen3-8B-shape int4 (Q4_K) greedy decode at batch 1 on one MI355X.
+
+Workload: 36 layers, hidden 4096, MLP 12288, 32 q / 8 kv heads,
+head_dim 128, vocab 151936, seeded N(0, 0.02) weights quantized to Q4_K on the GPU, bf16 KV cache
+prefilled to 4096 positions with N(0, 1) values, then K timed greedy decode steps (default 256).
+
+A step is one full token: embed, 36 layers, final norm + LM head + argmax, token store, all in HIP
+graphs (8 steps per graph).  value = tokens/s over the timed steps.
+
+roofline: the dominant kernel (fused RMSNorm + gate|up GEMV + SwiGLU) timed live with HIP events on
+the stream it runs on, over all 36 layers' weights (2 GB, well above the 256 MB MALL);
+achieved = algorithmic bytes per launch / average launch time.
+
+cpu_baseline: the CPU oracle's Qwen3 decoder (oracle.reference.Qwen3CpuModel, dense fp32 weights
+dequantized by the oracle) on a bounded sample of the same workload, scaled to tokens/s.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+PROMPT_POSITIONS = 4096
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=256)
+    p.add_argument("--warmup", type=int, default=16)
+    p.add_argument("--steps-per-graph", type=int, default=8)
+    p.add_argument("--model", choices=("8b", "0.6b"), default="8b")
+    p.add_argument("--positions", type=int, default=PROMPT_POSITIONS, help="KV positions prefilled before timing")
+    p.add_argument("--kernel-reps", type=int, default=5)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-sample-steps", type=int, default=3)
+    p.add_argument("--no-graph", action="store_true")
+    return p.parse_args()
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build is single-GPU); got --gpus {args.gpus}", file=sys.stderr)
+        return 2
+    import torch
+
+    from torch2vk_amd import kernels
+    from torch2vk_amd.qwen3.config import QWEN3_0_6B, QWEN3_8B
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+    from torch2vk_amd.qwen3.weights import synthetic_weights
+
+    if not torch.cuda.is_available():
+        print("no HIP device", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    cfg = QWEN3_8B if args.model == "8b" else QWEN3_0_6B
+    t_setup = time.time()
+    weights = synthetic_weights(cfg, device=dev, seed=0)
+    total_steps = args.warmup + args.steps + args.steps_per_graph
+    s_cap = args.positions + total_steps + 64
+    dec = Qwen3Decoder(weights, max_positions=s_cap, max_new_tokens=total_steps + 8, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    for layer in range(cfg.layers):
+        dec.k_cache[layer, :args.positions].normal_(generator=gen)
+        dec.v_cache[layer, :args.positions].normal_(generator=gen)
+    first_token = int(torch.randint(0, cfg.vocab, (1,), generator=gen, device=dev).item())
+    dec.reset(position=args.positions, token=first_token)
+    dec.stop_on_eos = False
+    torch.cuda.synchronize()
+    print(f"[bench] setup {time.time() - t_setup:.1f}s: {cfg.name} packed weights "
+          f"{weights.packed_bytes() / 1e9:.3f} GB, KV capacity {s_cap}", file=sys.stderr, flush=True)
+
+    use_graph = not args.no_graph
+    spg = args.steps_per_graph
+    if use_graph:
+        dec.graph(spg)
+    dec.run_steps(args.warmup, steps_per_graph=spg, use_graph=use_graph)
+    torch.cuda.synchronize()
+    print(f"[bench] warmup {args.warmup} steps done", file=sys.stderr, flush=True)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.run_steps(args.steps, steps_per_graph=spg, use_graph=use_graph)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    elapsed = t1 - t0
+    tok_s = args.steps / elapsed
+    ms_per_step = elapsed * 1000.0 / args.steps
+    n_generated = int(dec.length.item())
+    print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/token, {tok_s:.1f} tok/s "
+          f"({n_generated} tokens stored)", file=sys.stderr, flush=True)
+
+    kern = kernel_timing(dec, weights, args.kernel_reps)
+    print(f"[bench] kernel timing: {json.dumps(kern['per_launch_us'])}", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(cfg, weights, args.positions, args.cpu_sample_steps)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+
+    dom = kern["dominant"]
+    line = {
+        "metric": "Qwen3-8B-shape int4 decode tok/s @bs1" if args.model == "8b" else "Qwen3-0.6B int4 decode tok/s @bs1",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights quantized to Q4_K on the GPU; KV cache N(0,1))",
+        "config": {
+            "workload": f"{cfg.name} int4 (Q4_K, uniform) greedy decode, batch 1, KV prefilled to "
+                        f"{args.positions}, {args.steps} timed steps, HIP graphs of {spg} steps"
+                        if use_graph else "eager launches",
+            "model": cfg.name,
+            "global_batch": 1,
+            "seq_len": args.positions,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom["kernel"],
+            "achieved": round(dom["gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": dom["bytes"],
+            "avg_launch_us": round(dom["us"], 3),
+        },
+        "qmatmul_gbs": round(kern["qmatmul_gbs"], 1),
+        "kernel_us_per_token": round(kern["us_per_token"], 1),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def kernel_timing(dec, weights, reps: int) -> dict:
+    """Per-launch HIP-event timing of each decode kernel class, sweeping all layers' weights."""
+    import torch
+
+    from torch2vk_amd import kernels
+
+    c = dec.config
+    stream = torch.cuda.current_stream()
+    L = c.layers
+    # bytes per launch (algorithmic: packed weights + activations read + outputs written)
+    wb = lambda n: weights.packed[n].numel()  # noqa: E731
+    classes = {
+        "qkv_rmsnorm_gemv": (lambda i: kernels.q4k_matvec_multi(
+            dec.h, [weights.packed[f"layers.{i}.q"], weights.packed[f"layers.{i}.k"], weights.packed[f"layers.{i}.v"]],
+            [dec.q, dec.k, dec.v], norm_weight=weights.norms[f"layers.{i}.input_norm"]),
+            lambda i: wb(f"layers.{i}.q") + wb(f"layers.{i}.k") + wb(f"layers.{i}.v") + c.hidden * 8
+            + (c.q_dim + 2 * c.kv_dim) * 4),
+        "attn_decode": (lambda i: kernels.attn_decode(
+            dec.q, dec.k, dec.v, dec.k_cache[i], dec.v_cache[i], dec.attn, dec.position, dec.attn_ws,
+            q_norm_weight=weights.norms[f"layers.{i}.q_norm"], k_norm_weight=weights.norms[f"layers.{i}.k_norm"],
+            theta=c.rope_theta),
+            lambda i: None),
+        "o_gemv_residual": (lambda i: kernels.q4k_matvec(dec.attn, weights.packed[f"layers.{i}.o"], out=dec.h,
+                                                         residual=dec.h),
+                            lambda i: wb(f"layers.{i}.o") + c.q_dim * 2 + c.hidden * 8),
+        "gate_up_rmsnorm_swiglu_gemv": (lambda i: kernels.q4k_rmsnorm_swiglu(
+            dec.h, weights.norms[f"layers.{i}.post_norm"], weights.packed[f"layers.{i}.gate"],
+            weights.packed[f"layers.{i}.up"], dec.act),
+            lambda i: wb(f"layers.{i}.gate") + wb(f"layers.{i}.up") + c.hidden * 8 + c.mlp * 2),
+        "down_gemv_residual": (lambda i: kernels.q4k_matvec(dec.act, weights.packed[f"layers.{i}.down"], out=dec.h,
+                                                            residual=dec.h),
+                               lambda i: wb(f"layers.{i}.down") + c.mlp * 2 + c.hidden * 8),
+    }
+    pos = int(dec.position.item())
+    kv_len = min(pos + 1, dec.max_positions)
+    attn_bytes = 2 * kv_len * c.kv_dim * 2 + (c.q_dim + 2 * c.kv_dim) * 4 + c.q_dim * 2
+    per_launch_us, gbs, bytes_per = {}, {}, {}
+    total_us = 0.0
+    q_bytes = 0.0
+    q_us = 0.0
+    for name, (fn, nbytes) in classes.items():
+        for i in range(L):  # warm
+            fn(i)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            for i in range(L):
+                fn(i)
+        end.record(stream)
+        end.synchronize()
+        us = start.elapsed_time(end) * 1000.0 / (reps * L)
+        b = attn_bytes if name == "attn_decode" else sum(nbytes(i) for i in range(L)) / L
+        per_launch_us[name] = round(us, 3)
+        bytes_per[name] = int(b)
+        gbs[name] = b / (us * 1e-6) / 1e9
+        total_us += us * L
+        if name != "attn_decode":
+            q_bytes += b * L
+            q_us += us * L
+    # LM head (fused final norm + GEMV + argmax) and the select
+    lm = lambda: kernels.q4k_lm_head_argmax_partial(dec.h, weights.packed["lm_head"], dec.partial_scores,  # noqa: E731
+                                                   dec.partial_tokens, norm_weight=weights.norms["norm"])
+    lm()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        lm()
+    end.record(stream)
+    end.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / reps
+    b = weights.packed["lm_head"].numel() + c.hidden * 8 + dec.partial_scores.numel() * 8
+    per_launch_us["lm_head_rmsnorm_argmax_gemv"] = round(us, 3)
+    bytes_per["lm_head_rmsnorm_argmax_gemv"] = int(b)
+    gbs["lm_head_rmsnorm_argmax_gemv"] = b / (us * 1e-6) / 1e9
+    total_us += us
+    q_bytes += b
+    q_us += us
+    dominant = "gate_up_rmsnorm_swiglu_gemv"
+    return {
+        "per_launch_us": per_launch_us,
+        "gbs": {k: round(v, 1) for k, v in gbs.items()},
+        "bytes": bytes_per,
+        "us_per_token": total_us,
+        "qmatmul_gbs": q_bytes / (q_us * 1e-6) / 1e9,
+        "dominant": {"kernel": dominant, "us": per_launch_us[dominant], "bytes": bytes_per[dominant],
+                     "gbs": gbs[dominant]},
+    }
+
+
+def cpu_baseline(cfg, weights, positions: int, steps: int) -> dict:
+    """The CPU oracle's decoder on one layer + the LM head at full 8B shapes, scaled to a token."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from oracle.reference import Qwen3CpuModel, Qwen3Shape
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    c = cfg
+    dense = {}
+    for name in ("q", "k", "v", "o", "gate", "up", "down"):
+        packed = weights.packed[f"layers.0.{name}"].cpu().numpy()
+        k = c.hidden if name != "o" and name != "down" else (c.q_dim if name == "o" else c.mlp)
+        dense[f"layers.0.{name}"] = torch.from_numpy(oracle.dequant_q4_k(packed, k))
+    for name in ("input_norm", "post_norm", "q_norm", "k_norm"):
+        dense[f"layers.0.{name}"] = weights.norms[f"layers.0.{name}"].cpu()
+    dense["norm"] = weights.norms["norm"].cpu()
+    dense["embed"] = torch.zeros(8, c.hidden)
+    lm = torch.from_numpy(oracle.dequant_q4_k(weights.packed["lm_head"].cpu().numpy(), c.hidden))
+    dense["lm_head"] = lm
+    shape = Qwen3Shape(hidden=c.hidden, layers=1, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
+                       mlp=c.mlp, vocab=c.vocab, rope_theta=c.rope_theta)
+    model = Qwen3CpuModel(shape, dense, max_positions=positions + steps + 1)
+    g = torch.Generator().manual_seed(1)
+    model.k_cache[:, :positions].normal_(generator=g)
+    model.v_cache[:, :positions].normal_(generator=g)
+    layer_times = []
+    for s in range(steps):
+        t0 = time.perf_counter()
+        hidden = model.forward(torch.tensor([s % 8]), start=positions + s)
+        layer_times.append(time.perf_counter() - t0)
+    lm_times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        logits = model.logits(hidden)
+        int(torch.argmax(logits))
+        lm_times.append(time.perf_counter() - t0)
+    t_layer = statistics.median(layer_times)
+    t_lm = statistics.median(lm_times)
+    t_token = c.layers * t_layer + t_lm
+    del np
+    return {
+        "value": round(1.0 / t_token, 4),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"CPU oracle decoder (torch {torch.__version__}, fp32 dense weights dequantized by the oracle): "
+                  f"1 of {c.layers} layers at KV position {positions} timed over {steps} steps (median "
+                  f"{t_layer * 1e3:.1f} ms) x {c.layers} + LM head+argmax (median {t_lm * 1e3:.1f} ms)",
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,98 @@
+"""End-to-end greedy decode on the GPU against the CPU oracle decoder (exact tokens, near-tie aware)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.qwen3_check import check_greedy_tokens, dense_weights
+from oracle.reference import Qwen3Shape
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(cfg, device, seed, std):
+    from torch2vk_amd.qwen3.weights import matrix_shapes, synthetic_weights
+
+    w = synthetic_weights(cfg, device=device, seed=seed, std=std, norm_std=0.1)
+    dense = dense_weights({k: v.cpu().numpy() for k, v in w.packed.items()}, w.types,
+                          {k: v.cpu().numpy() for k, v in w.norms.items()}, matrix_shapes(cfg))
+    shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
+                       head_dim=cfg.head_dim, mlp=cfg.mlp, vocab=cfg.vocab, rope_theta=cfg.rope_theta)
+    return w, dense, shape
+
+
+TINY = dict(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=128, mlp=768, vocab=1024)
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_tiny_decode_matches_oracle(device, use_graph):
+    from torch2vk_amd.qwen3.config import Qwen3Config
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg = Qwen3Config("tiny", **TINY, eos_token_ids=(1023,))
+    w, dense, shape = _setup(cfg, device, seed=11, std=0.08)
+    rng = np.random.default_rng(0)
+    prompt = rng.integers(0, cfg.vocab, 7).tolist()
+    dec = Qwen3Decoder(w, max_positions=64, max_new_tokens=16)
+    dec.stop_on_eos = False
+    toks = dec.generate(torch.tensor(prompt), 13, steps_per_graph=4, use_graph=use_graph)
+    print(f"tiny decode graph={use_graph}: {toks}", flush=True)
+    assert len(toks) == 13
+    stats = check_greedy_tokens(shape, dense, prompt, toks)
+    print(stats)
+
+
+def test_graph_replay_equals_eager(device):
+    """Every graph replay reproduces the eager step sequence bit-for-bit (tokens and KV cache)."""
+    from torch2vk_amd.qwen3.config import Qwen3Config
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg = Qwen3Config("tiny", **TINY, eos_token_ids=(1023,))
+    w, _, _ = _setup(cfg, device, seed=3, std=0.08)
+    prompt = torch.tensor([5, 9, 100, 7])
+    a = Qwen3Decoder(w, max_positions=64, max_new_tokens=24)
+    b = Qwen3Decoder(w, max_positions=64, max_new_tokens=24)
+    a.stop_on_eos = b.stop_on_eos = False
+    ta = a.generate(prompt, 21, use_graph=False)
+    tb = b.generate(prompt, 21, steps_per_graph=5, use_graph=True)
+    assert ta == tb
+    n = prompt.numel() + 21
+    torch.testing.assert_close(a.k_cache[:, :n], b.k_cache[:, :n], rtol=0, atol=0)
+    torch.testing.assert_close(a.v_cache[:, :n], b.v_cache[:, :n], rtol=0, atol=0)
+
+
+def test_eos_stops_generation(device):
+    from torch2vk_amd.qwen3.config import Qwen3Config
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg = Qwen3Config("tiny", **TINY)
+    w, _, _ = _setup(cfg, device, seed=11, std=0.08)
+    dec = Qwen3Decoder(w, max_positions=64, max_new_tokens=16)
+    dec.stop_on_eos = False
+    toks = dec.generate(torch.tensor([1, 2, 3]), 8, use_graph=False)
+    eos = toks[3]
+    cfg2 = Qwen3Config("tiny", **TINY, eos_token_ids=(eos,))
+    dec2 = Qwen3Decoder(w, max_positions=64, max_new_tokens=16)
+    dec2.config = cfg2
+    dec2.eos = torch.tensor([eos], dtype=torch.int64, device=device)
+    toks2 = dec2.generate(torch.tensor([1, 2, 3]), 8, steps_per_graph=2, use_graph=True)
+    assert toks2 == toks[:toks.index(eos) + 1]
+
+
+def test_qwen3_0_6b_shape_two_layers(device):
+    """Real 0.6B shapes (hidden 1024, MLP 3072, 16/8 heads, vocab 151936) with 2 layers."""
+    from torch2vk_amd.qwen3.config import QWEN3_0_6B
+    from dataclasses import replace
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg = replace(QWEN3_0_6B, layers=2)
+    w, dense, shape = _setup(cfg, device, seed=5, std=0.04)
+    prompt = [11, 2024, 151000, 77, 5]
+    dec = Qwen3Decoder(w, max_positions=64, max_new_tokens=8)
+    dec.stop_on_eos = False
+    toks = dec.generate(torch.tensor(prompt), 6, steps_per_graph=3)
+    print(f"0.6B-shape decode: {toks}", flush=True)
+    stats = check_greedy_tokens(shape, dense, prompt, toks, tie_tol=2e-3)
+    print(stats)

@@ -1,0 +1,200 @@
+"""Qwen3 greedy decode on MI355X: the reference's decode-step surface over libt2h.
+
+One decode step (src/models/optimized_qwen3/run.py:142-172) is, per token:
+
+    embed                                   1 launch   (EMBEDDING_Q4_K_F32)
+    per layer                               5 launches:
+      RMSNorm + Q|K|V GEMV                  (RMS_NORM_MUL + LINEAR_NOBIAS_Q4_K_QKV_MATVEC)
+      q/k-norm + RoPE + KV write + attention (RMS_NORM_ROPE_TRANSPOSE x2 + SDPA_DECODE_CACHE_WRITE)
+      o_proj GEMV + residual                (LINEAR_NOBIAS_Q4_K_MATVEC_ADD)
+      RMSNorm + gate|up GEMV + SwiGLU       (RMS_NORM_MUL + LINEAR_NOBIAS_Q4_K_QK_MATVEC + SWIGLU)
+      down GEMV + residual                  (LINEAR_NOBIAS_Q4_K_MATVEC_ADD)
+    final RMSNorm + LM head + argmax        1 launch   (run_decode_norm + LM_HEAD_*_ARGMAX_PARTIAL)
+    token select + EOS                      1 launch   (QWEN3_TOKEN_SELECT_REDUCE_{CHUNKS_,}F32)
+    token store + position advance          1 launch   (QWEN3_TOKEN_STORE_EOS_F32)
+
+The reference runs 10 dispatches per layer and waits on the host every token
+(src/torch2vk/runtime/replay.py:260-261).  Here every dynamic scalar (cache
+position, token index, the token itself) lives in device memory, so whole
+steps are captured into one HIP graph and replayed with no host round trip.
+
+The residual stream is fp32; GEMV inputs are bf16; the KV cache is bf16
+token-major [S, NK, D] per layer (the reference's optimized cache layout,
+src/models/optimized_qwen3/tensors/model.py:104-150, in bf16 instead of fp16).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from torch2vk_amd import kernels
+from torch2vk_amd.qwen3.config import Qwen3Config
+from torch2vk_amd.qwen3.weights import Qwen3Weights
+
+LM_HEAD_PARTIALS = 2048
+
+
+class Qwen3Decoder:
+    def __init__(self, weights: Qwen3Weights, *, max_positions: int, max_new_tokens: int, device=None) -> None:
+        c = weights.config
+        self.config: Qwen3Config = c
+        self.weights = weights
+        for name, t in weights.types.items():
+            if t != "q4_k":
+                raise NotImplementedError(f"{name}: {t} decode GEMV is not built yet (uniform Q4_K only)")
+        dev = torch.device(device) if device is not None else weights.packed["embed"].device
+        self.device = dev
+        self.max_positions = max_positions
+        bf, f32 = torch.bfloat16, torch.float32
+        self.k_cache = torch.zeros(c.layers, max_positions, c.kv_heads, c.head_dim, dtype=bf, device=dev)
+        self.v_cache = torch.zeros_like(self.k_cache)
+        self.h = torch.zeros(c.hidden, dtype=f32, device=dev)
+        self.q = torch.zeros(c.q_dim, dtype=f32, device=dev)
+        self.k = torch.zeros(c.kv_dim, dtype=f32, device=dev)
+        self.v = torch.zeros(c.kv_dim, dtype=f32, device=dev)
+        self.attn = torch.zeros(c.q_dim, dtype=bf, device=dev)
+        self.act = torch.zeros(c.mlp, dtype=bf, device=dev)
+        self.attn_ws = kernels.attn_decode_workspace(c.heads, c.kv_heads, c.head_dim, max_positions, dev)
+        self.partial_scores = torch.zeros(LM_HEAD_PARTIALS, dtype=f32, device=dev)
+        self.partial_tokens = torch.zeros(LM_HEAD_PARTIALS, dtype=torch.int32, device=dev)
+        self.next_token = torch.zeros(1, 1, dtype=torch.int64, device=dev)
+        self.done = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.generated = torch.full((max_new_tokens,), -1, dtype=torch.int64, device=dev)
+        self.length = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.stopped = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.position = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.eos = torch.tensor(c.eos_token_ids, dtype=torch.int64, device=dev)
+        self.stop_on_eos = True
+        self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+
+    # ----------------------------------------------------------- state --
+
+    def reset(self, position: int = 0, token: int | None = None) -> None:
+        self.position.fill_(position)
+        self.length.zero_()
+        self.stopped.zero_()
+        self.done.zero_()
+        self.generated.fill_(-1)
+        if token is not None:
+            self.next_token.fill_(token)
+
+    def _w(self, name: str) -> torch.Tensor:
+        return self.weights.packed[name]
+
+    def _n(self, name: str) -> torch.Tensor:
+        return self.weights.norms[name]
+
+    # ------------------------------------------- reference op surface --
+
+    def run_decode_embed(self) -> None:
+        """Token -> fp32 residual stream (run_decode_embed, EMBEDDING_Q4_K_F32)."""
+        kernels.embedding_q4_k(self._w("embed"), self.next_token.view(-1), self.config.hidden, out=self.h.view(1, -1))
+
+    def run_decode_layer(self, layer_idx: int, *, cache_position: int | None = None) -> None:
+        """One decoder layer at the device-resident position
+        (run_decode_layer, src/models/optimized_qwen3/dispatch/decode_layer.py:131-136).
+        A Python ``cache_position`` is written to the device counter first."""
+        c = self.config
+        if cache_position is not None:
+            self.position.fill_(cache_position)
+        p = f"layers.{layer_idx}."
+        kernels.q4k_matvec_multi(self.h, [self._w(p + "q"), self._w(p + "k"), self._w(p + "v")],
+                                 [self.q, self.k, self.v], norm_weight=self._n(p + "input_norm"), eps=c.rms_eps)
+        kernels.attn_decode(self.q, self.k, self.v, self.k_cache[layer_idx], self.v_cache[layer_idx], self.attn,
+                            self.position, self.attn_ws, q_norm_weight=self._n(p + "q_norm"),
+                            k_norm_weight=self._n(p + "k_norm"), theta=c.rope_theta, eps=c.rms_eps)
+        kernels.q4k_matvec(self.attn, self._w(p + "o"), out=self.h, residual=self.h)
+        kernels.q4k_rmsnorm_swiglu(self.h, self._n(p + "post_norm"), self._w(p + "gate"), self._w(p + "up"),
+                                   self.act, eps=c.rms_eps)
+        kernels.q4k_matvec(self.act, self._w(p + "down"), out=self.h, residual=self.h)
+
+    def run_lm_head_select(self) -> None:
+        """Final RMSNorm + LM head + argmax + EOS flag (run_decode_norm + _run_lm_head_select,
+        src/models/optimized_qwen3/run.py:116-139); logits are never materialised."""
+        kernels.q4k_lm_head_argmax_partial(self.h, self._w("lm_head"), self.partial_scores, self.partial_tokens,
+                                           norm_weight=self._n("norm"), eps=self.config.rms_eps)
+        kernels.token_select(self.partial_scores, self.partial_tokens, self.eos, self.next_token, self.done)
+
+    def run_token_store(self, advance: bool = True) -> None:
+        """QWEN3_TOKEN_STORE_EOS_F32 with the token index read from the device length counter."""
+        kernels.token_store(self.next_token, self.done, self.generated, self.length, self.stopped,
+                            stop_on_eos=self.stop_on_eos, token_index_ptr=self.length,
+                            advance=self.position if advance else None)
+
+    def forward_token(self) -> None:
+        """Embed next_token at the current position, run every layer, select the next token."""
+        self.run_decode_embed()
+        for i in range(self.config.layers):
+            self.run_decode_layer(i)
+        self.run_lm_head_select()
+
+    def decode_step(self) -> None:
+        """One full greedy step: forward, store the token, advance the position."""
+        self.forward_token()
+        self.run_token_store(advance=True)
+
+    # ------------------------------------------------------ HIP graphs --
+
+    def graph(self, steps: int) -> torch.cuda.CUDAGraph:
+        """A graph of ``steps`` consecutive decode steps (captured once per step count)."""
+        if steps not in self._graphs:
+            saved = self._save_state()
+            side = torch.cuda.Stream(device=self.device)
+            side.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(side):
+                self.decode_step()  # warm-up launch outside capture
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(steps):
+                    self.decode_step()
+            self._restore_state(saved)
+            self._graphs[steps] = g
+        return self._graphs[steps]
+
+    def _save_state(self):
+        return [t.clone() for t in (self.position, self.length, self.stopped, self.done, self.next_token,
+                                    self.generated)]
+
+    def _restore_state(self, saved) -> None:
+        for dst, src in zip((self.position, self.length, self.stopped, self.done, self.next_token, self.generated),
+                            saved):
+            dst.copy_(src)
+
+    def run_steps(self, n: int, steps_per_graph: int = 8, use_graph: bool = True) -> None:
+        if not use_graph:
+            for _ in range(n):
+                self.decode_step()
+            return
+        full, rest = divmod(n, steps_per_graph)
+        if full:
+            g = self.graph(steps_per_graph)
+            for _ in range(full):
+                g.replay()
+        for _ in range(rest):
+            self.decode_step()
+
+    # ------------------------------------------------------- generate --
+
+    def prefill(self, prompt_ids: torch.Tensor, start: int = 0) -> None:
+        """Feed the prompt one token at a time (KV cache fill); the last prompt token's step stores the
+        first generated token."""
+        ids = prompt_ids.to(device=self.device, dtype=torch.int64).view(-1)
+        self.reset(position=start)
+        for i in range(ids.numel()):
+            self.next_token.view(-1).copy_(ids[i:i + 1])
+            self.forward_token()
+            if i + 1 < ids.numel():
+                self.position.add_(1)
+        self.run_token_store(advance=True)
+
+    def generate(self, prompt_ids: torch.Tensor, max_new_tokens: int, *, steps_per_graph: int = 8,
+                 use_graph: bool = True) -> list[int]:
+        if max_new_tokens > self.generated.numel():
+            raise ValueError("max_new_tokens exceeds the decoder's generated-token buffer")
+        if prompt_ids.numel() + max_new_tokens > self.max_positions:
+            raise ValueError("prompt + new tokens exceed the KV cache capacity")
+        self.prefill(prompt_ids)
+        self.run_steps(max_new_tokens - 1, steps_per_graph=steps_per_graph, use_graph=use_graph)
+        n = int(self.length.item())
+        return self.generated[:n].tolist()
