@@ -93,8 +93,10 @@ int t2h_q4k_lm_head_argmax_partial(const void* x, const float* norm_w, float eps
                                    uint32_t n, float* partial_scores, uint32_t* partial_tokens,
                                    uint32_t num_partials, void* stream);
 
-/* Grid cap of the GEMV launches (tuning knob; default 2048 blocks of 4 waves). */
-int t2h_set_gemv_max_blocks(uint32_t max_blocks);
+/* Grid caps of the GEMV launches, in blocks of 4 waves (tuning knob, process-wide):
+ * max_blocks for plain bf16 x (default 1024), max_blocks_norm for the fused
+ * RMSNorm prologue (default 512; 0 = same as max_blocks). */
+int t2h_set_gemv_max_blocks(uint32_t max_blocks, uint32_t max_blocks_norm);
 
 /* ---------------------------------------------------- token selection --- */
 /* replaces QWEN3_TOKEN_SELECT_REDUCE_CHUNKS_F32 + QWEN3_TOKEN_SELECT_REDUCE_F32
@@ -109,14 +111,23 @@ int t2h_token_store(const int64_t* next_token, const uint32_t* done, int64_t* ge
                     uint32_t* length, uint32_t* stopped, uint32_t stop_on_eos, const uint32_t* token_index_ptr,
                     uint32_t token_index, int32_t* advance, void* stream);
 
+/* Select and store fused into one launch (the same two reference shaders):
+ * next_token/done as t2h_token_select; the token is appended at
+ * generated[*length] (if < gen_cap and not stopped), *length += 1, *stopped set
+ * on EOS when stop_on_eos; *advance (nullable) += 1 on every call. */
+int t2h_token_select_store(const float* scores, const uint32_t* tokens, uint32_t g, const int64_t* eos,
+                           uint32_t n_eos, int64_t* next_token, uint32_t* done, int64_t* generated, uint32_t gen_cap,
+                           uint32_t* length, uint32_t* stopped, uint32_t stop_on_eos, int32_t* advance, void* stream);
+
 /* ------------------------------------------------- decode attention ---- */
 /* Split-K flash decoding over a bf16 token-major cache [s_cap, nk, d] (d = 128).
  * q [nh, d], k_new/v_new [nk, d] fp32 projections.  With q_norm_w/k_norm_w,
  * per-head RMSNorm is applied; with theta > 0, rotate-half RoPE at
  * *cache_position.  The new K/V row is written at *cache_position (if
  * < s_cap) and attention covers positions 0..min(*cache_position, s_cap-1).
- * out bf16 [nh, d].  workspace: t2h_attn_decode_workspace_bytes(), zeroed once
- * by the caller before first use (the kernel leaves it reusable).
+ * out bf16 [nh, d].  workspace: t2h_attn_decode_workspace_bytes() bytes of
+ * per-chunk partials (no initialisation needed).  Two launches: the split-K
+ * pass and a log-sum-exp merge.
  * replaces RMS_NORM_ROPE_TRANSPOSE_F16 x2 (src/models/optimized_qwen3/shaders/rms_norm_rope_transpose_f16.py:22-145),
  * ROPE_TABLE_F32 (src/torch2vk/runtime/rope_table.py:32-122) and
  * SDPA_DECODE_CACHE_WRITE_F32 (src/models/optimized_qwen3/shaders/sdpa_decode_cache_write_f32.py:22-170). */

@@ -8,11 +8,20 @@
 //       src/models/optimized_qwen3/shaders/sdpa_decode_cache_write_f32.py:22-170
 //
 // The reference walks the whole cache serially in one workgroup per q head.
-// Here a block owns (kv head, 64-position chunk): it stages the chunk's K and
-// V rows in LDS once for all GROUP q heads of the kv head, computes a partial
-// softmax (max, sum, unnormalised output), and the last block of each kv
-// head to finish (atomic ticket) merges the partials with the log-sum-exp
-// rule and resets its ticket, so a single launch is graph-replayable.
+// Here a block of two waves owns (kv head, 128-position chunk); each wave
+// takes 64 positions for all GROUP q heads of the kv head, so every K/V byte
+// is read once per token:
+//   * K rows are loaded coalesced (4 rows per instruction) and staged in a
+//     padded LDS tile; a lane then owns one position and dots its row with
+//     the GROUP q vectors (broadcast from LDS);
+//   * V is loaded coalesced straight into registers in the P.V layout (lane
+//     owns two dims, one register per position);
+//   * the two waves' partial softmax states are merged in LDS and the block's
+//     (max, sum, unnormalised output) is published;
+//   * a second small kernel merges the partials of each q head with the
+//     log-sum-exp rule.  Merging in a separate launch, rather than in the
+//     last block to finish, keeps device-scope fences (an L2 write-back and
+//     invalidate per block on this multi-XCD part) out of the main kernel.
 //
 // Cache layout (as the reference's optimized decode cache): bf16
 // [S_cap, NK, D], token-major.  q/k/v inputs are the fp32 QKV projections.
@@ -23,8 +32,13 @@
 namespace t2h {
 
 constexpr int AD_D = 128;
-constexpr int AD_CH = 64;    // positions per block
-constexpr int AD_KROW = 68;  // LDS K row stride in dwords (256 B + 16 B pad: conflict-free column reads)
+constexpr int AD_WAVE_POS = 16;               // positions per wave
+constexpr int AD_WAVES = 8;                   // waves per block
+constexpr int AD_CH = AD_WAVE_POS * AD_WAVES; // positions per block
+constexpr int AD_QROW = 36;                   // LDS q row: 32 dims + 4 pad (conflict-free quarter reads)
+constexpr int AD_MAX_PARTS = 512;             // s_cap <= 65536
+constexpr int AD_MERGE_WAVES = 4;
+constexpr int AD_MERGE_BATCH = 16;            // partial loads in flight per merge wave
 
 struct AttnDecodeArgs {
     const float* q;         // [NH, D] fp32
@@ -36,7 +50,6 @@ struct AttnDecodeArgs {
     uint16_t* v_cache;
     uint16_t* out;          // bf16 [NH, D]
     const int32_t* pos_ptr; // current position (device)
-    uint32_t* tickets;      // [NK]
     float* part_ml;         // [NK, max_chunks, GROUP, 2]
     float* part_o;          // [NK, max_chunks, GROUP, D]
     uint32_t nk;
@@ -47,14 +60,14 @@ struct AttnDecodeArgs {
     float scale;            // softmax scale, 1/sqrt(D)
 };
 
-__device__ __forceinline__ void norm_rope_pair(float x0, float x1, const float* w, int lane, float eps, float cs,
-                                               float sn, bool rope, float& r0, float& r1) {
+__device__ __forceinline__ void norm_rope_pair(float x0, float x1, bool has_w, float w0, float w1, float eps,
+                                               float cs, float sn, bool rope, float& r0, float& r1) {
     float n0 = x0, n1 = x1;
-    if (w) {
+    if (has_w) {
         const float ss = wave_sum(x0 * x0 + x1 * x1);
         const float inv = 1.0f / sqrtf(ss / (float)AD_D + eps);
-        n0 = x0 * inv * w[lane];
-        n1 = x1 * inv * w[lane + 64];
+        n0 = x0 * inv * w0;
+        n1 = x1 * inv * w1;
     }
     if (rope) {
         // rotate_half pairs d with d + D/2: out[d] = n[d]cos - n[d+D/2]sin, out[d+D/2] = n[d+D/2]cos + n[d]sin
@@ -66,14 +79,23 @@ __device__ __forceinline__ void norm_rope_pair(float x0, float x1, const float* 
     }
 }
 
+// Split-K pass.  Block (chunk c, kv head) covers AD_CH positions with AD_WAVES
+// waves of AD_WAVE_POS positions each.  Scores: lane = (position p, quarter
+// part) dots 32 dims of the K row with the GROUP q vectors, a quad DPP
+// reduction completes the dot.  P.V: lane owns dims 2*lane, 2*lane+1 with V
+// rows loaded coalesced (one row per instruction).  The waves' softmax states
+// are merged in LDS and one (max, sum, output) partial per head is published.
 template <int GROUP>
-__global__ __launch_bounds__(64) void attn_decode_kernel(const AttnDecodeArgs a) {
-    __shared__ __align__(16) uint32_t ks[AD_CH * AD_KROW];
-    __shared__ __align__(16) uint32_t vs[AD_CH * (AD_D / 2)];
-    __shared__ __align__(16) float qs[GROUP][AD_D];
-    __shared__ __align__(16) float ps[AD_CH][GROUP];
+__global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDecodeArgs a) {
+    __shared__ __align__(16) float qs[GROUP][4][AD_QROW];
+    __shared__ __align__(16) float ps[AD_WAVES][AD_WAVE_POS][GROUP];
+    __shared__ float wml[AD_WAVES][GROUP][2];
+    __shared__ __align__(16) float2 wo[AD_WAVES][GROUP][64];
+    __shared__ __align__(16) uint16_t knew[AD_D];
 
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, scalar
     const int c = blockIdx.x;
     const int kvh = blockIdx.y;
     const int pos = *a.pos_ptr;
@@ -81,28 +103,62 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const AttnDecodeArgs a)
     const int L = pos + 1 < S ? pos + 1 : S;
     const int n_chunks = (L + AD_CH - 1) / AD_CH;
     if (c >= n_chunks) return;
-    const int p0 = c * AD_CH;
-    const int rows = (L - p0) < AD_CH ? (L - p0) : AD_CH;
+    const int pw = c * AD_CH + wave * AD_WAVE_POS;  // first position of this wave
+    int rows = L - pw;
+    rows = rows < 0 ? 0 : (rows > AD_WAVE_POS ? AD_WAVE_POS : rows);
     const size_t row_stride = (size_t)a.nk * AD_D;  // elements between positions
+    const uint16_t* kbase = a.k_cache + (size_t)kvh * AD_D;
+    const uint16_t* vbase = a.v_cache + (size_t)kvh * AD_D;
+    const int last_pos = L - 1;
+    const bool has_new = pos < S && pos >= pw && pos < pw + AD_WAVE_POS;  // wave-uniform
+    const int rnew = pos - pw;
 
-    // 1. issue the chunk's K/V loads: 4 rows per instruction, 16 B per lane
-    uint4 kr[16], vr[16];
-    const int rsub = lane >> 4;
-    const int col = (lane & 15) * 8;  // bf16 element offset within the row
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int r = i * 4 + rsub;
-        if (r < rows) {
-            const size_t off = (size_t)(p0 + r) * row_stride + (size_t)kvh * AD_D + col;
-            kr[i] = load_nt_u4(a.k_cache + off);
-            vr[i] = load_nt_u4(a.v_cache + off);
-        } else {
-            kr[i] = make_uint4(0, 0, 0, 0);
-            vr[i] = make_uint4(0, 0, 0, 0);
-        }
+    // 0. the small operands first: vmcnt retires in order, so anything loaded
+    //    after the cache stream would wait for all of it
+    const bool has_w = a.q_norm_w != nullptr;
+    float qx0 = 0.0f, qx1 = 0.0f;
+    if (wave < GROUP) {
+        const int h = kvh * GROUP + wave;
+        qx0 = a.q[h * AD_D + lane];
+        qx1 = a.q[h * AD_D + lane + 64];
+    }
+    float qw0 = 1.0f, qw1 = 1.0f, kw0 = 1.0f, kw1 = 1.0f;
+    if (has_w) {
+        qw0 = a.q_norm_w[lane];
+        qw1 = a.q_norm_w[lane + 64];
+        kw0 = a.k_norm_w[lane];
+        kw1 = a.k_norm_w[lane + 64];
+    }
+    float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f;
+    if (has_new) {
+        kx0 = a.k_new[kvh * AD_D + lane];
+        kx1 = a.k_new[kvh * AD_D + lane + 64];
+        vx0 = a.v_new[kvh * AD_D + 2 * lane];
+        vx1 = a.v_new[kvh * AD_D + 2 * lane + 1];
     }
 
-    // 2. q: per-head RMSNorm + RoPE at `pos`, pre-scaled by 1/sqrt(D)
+    // 1. K: lane (p_k, part) loads 4 x 16 B = dims part*32..+31 of row p_k;
+    //    V: one row per instruction, lane owns dims 2*lane, 2*lane+1.
+    //    Rows past the end are clamped to position L-1 (always valid) instead of
+    //    branching, so every load is in flight at once; they are masked below.
+    const int p_k = lane >> 2;
+    const int part = lane & 3;
+    uint4 kr[4];
+    {
+        const int p = min(pw + p_k, last_pos);
+        const uint16_t* krow = kbase + (size_t)p * row_stride + part * 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[i] = load_u4(krow + 8 * i);
+    }
+    uint32_t vr[AD_WAVE_POS];
+#pragma unroll
+    for (int i = 0; i < AD_WAVE_POS; ++i) {
+        const int p = min(pw + i, last_pos);
+        vr[i] = reinterpret_cast<const uint32_t*>(vbase + (size_t)p * row_stride)[lane];
+    }
+
+    // 2. RoPE at `pos` (lane = frequency index); q head `wave` normalised,
+    //    rotated, pre-scaled by 1/sqrt(D) into LDS
     const bool rope = a.theta > 0.0f;
     float cs = 1.0f, sn = 0.0f;
     if (rope) {
@@ -111,140 +167,206 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const AttnDecodeArgs a)
         const float angle = (float)pos * inv_freq;
         sincosf(angle, &sn, &cs);
     }
-#pragma unroll
-    for (int g = 0; g < GROUP; ++g) {
-        const int h = kvh * GROUP + g;
+    if (wave < GROUP) {
         float r0, r1;
-        norm_rope_pair(a.q[h * AD_D + lane], a.q[h * AD_D + lane + 64], a.q_norm_w, lane, a.eps, cs, sn, rope, r0, r1);
-        qs[g][lane] = r0 * a.scale;
-        qs[g][lane + 64] = r1 * a.scale;
+        norm_rope_pair(qx0, qx1, has_w, qw0, qw1, a.eps, cs, sn, rope, r0, r1);
+        qs[wave][lane >> 5][lane & 31] = r0 * a.scale;
+        qs[wave][2 + (lane >> 5)][lane & 31] = r1 * a.scale;
     }
 
-    // 3. stage K/V in LDS
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int r = i * 4 + rsub;
-        *reinterpret_cast<uint4*>(&ks[r * AD_KROW + (lane & 15) * 4]) = kr[i];
-        *reinterpret_cast<uint4*>(&vs[r * (AD_D / 2) + (lane & 15) * 4]) = vr[i];
-    }
-
-    // 4. the chunk holding `pos` produces the new K/V row and writes it back
-    if (pos < S && pos >= p0 && pos < p0 + AD_CH) {
-        const int r = pos - p0;
+    // 3. the wave holding `pos` produces the new K/V row and writes it back
+    uint32_t vnew = 0;
+    if (has_new) {
         float k0, k1;
-        norm_rope_pair(a.k_new[kvh * AD_D + lane], a.k_new[kvh * AD_D + lane + 64], a.k_norm_w, lane, a.eps, cs, sn,
-                       rope, k0, k1);
+        norm_rope_pair(kx0, kx1, has_w, kw0, kw1, a.eps, cs, sn, rope, k0, k1);
         const uint16_t kb0 = (uint16_t)f32_to_bf16_bits(k0);
         const uint16_t kb1 = (uint16_t)f32_to_bf16_bits(k1);
-        const uint16_t vb0 = (uint16_t)f32_to_bf16_bits(a.v_new[kvh * AD_D + lane]);
-        const uint16_t vb1 = (uint16_t)f32_to_bf16_bits(a.v_new[kvh * AD_D + lane + 64]);
-        uint16_t* krow = reinterpret_cast<uint16_t*>(&ks[r * AD_KROW]);
-        uint16_t* vrow = reinterpret_cast<uint16_t*>(&vs[r * (AD_D / 2)]);
-        krow[lane] = kb0;
-        krow[lane + 64] = kb1;
-        vrow[lane] = vb0;
-        vrow[lane + 64] = vb1;
+        knew[lane] = kb0;
+        knew[lane + 64] = kb1;
+        vnew = pack_bf16x2(vx0, vx1);
         const size_t off = (size_t)pos * row_stride + (size_t)kvh * AD_D;
         a.k_cache[off + lane] = kb0;
         a.k_cache[off + lane + 64] = kb1;
-        a.v_cache[off + lane] = vb0;
-        a.v_cache[off + lane + 64] = vb1;
+        reinterpret_cast<uint32_t*>(a.v_cache + off)[lane] = vnew;
     }
     __syncthreads();
+    if (has_new && p_k == rnew) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const uint4*>(&knew[part * 32 + 8 * i]);
+    }
 
-    // 5. scores: lane <-> position
+    // 4. scores: 32-dim partial dots, completed across the 4 lanes of a position
     float s[GROUP];
 #pragma unroll
     for (int g = 0; g < GROUP; ++g) s[g] = 0.0f;
-    if (lane < rows) {
-        const uint32_t* krow = &ks[lane * AD_KROW];
-#pragma unroll 4
-        for (int j = 0; j < AD_D / 8; ++j) {
-            const uint4 kk = *reinterpret_cast<const uint4*>(&krow[j * 4]);
-            float kf[8];
-            kf[0] = bf16_bits_to_f32(kk.x & 0xffffu); kf[1] = bf16_bits_to_f32(kk.x >> 16);
-            kf[2] = bf16_bits_to_f32(kk.y & 0xffffu); kf[3] = bf16_bits_to_f32(kk.y >> 16);
-            kf[4] = bf16_bits_to_f32(kk.z & 0xffffu); kf[5] = bf16_bits_to_f32(kk.z >> 16);
-            kf[6] = bf16_bits_to_f32(kk.w & 0xffffu); kf[7] = bf16_bits_to_f32(kk.w >> 16);
 #pragma unroll
-            for (int g = 0; g < GROUP; ++g) {
-                const float4 qa = *reinterpret_cast<const float4*>(&qs[g][j * 8]);
-                const float4 qb = *reinterpret_cast<const float4*>(&qs[g][j * 8 + 4]);
-                float t = s[g];
-                t = fmaf(qa.x, kf[0], t); t = fmaf(qa.y, kf[1], t);
-                t = fmaf(qa.z, kf[2], t); t = fmaf(qa.w, kf[3], t);
-                t = fmaf(qb.x, kf[4], t); t = fmaf(qb.y, kf[5], t);
-                t = fmaf(qb.z, kf[6], t); t = fmaf(qb.w, kf[7], t);
-                s[g] = t;
-            }
+    for (int i = 0; i < 4; ++i) {
+        const uint4 kk = kr[i];
+        float kf[8];
+        kf[0] = bf16_bits_to_f32(kk.x & 0xffffu); kf[1] = bf16_bits_to_f32(kk.x >> 16);
+        kf[2] = bf16_bits_to_f32(kk.y & 0xffffu); kf[3] = bf16_bits_to_f32(kk.y >> 16);
+        kf[4] = bf16_bits_to_f32(kk.z & 0xffffu); kf[5] = bf16_bits_to_f32(kk.z >> 16);
+        kf[6] = bf16_bits_to_f32(kk.w & 0xffffu); kf[7] = bf16_bits_to_f32(kk.w >> 16);
+#pragma unroll
+        for (int g = 0; g < GROUP; ++g) {
+            const float4 qa = *reinterpret_cast<const float4*>(&qs[g][part][8 * i]);
+            const float4 qb = *reinterpret_cast<const float4*>(&qs[g][part][8 * i + 4]);
+            float t = s[g];
+            t = fmaf(qa.x, kf[0], t); t = fmaf(qa.y, kf[1], t);
+            t = fmaf(qa.z, kf[2], t); t = fmaf(qa.w, kf[3], t);
+            t = fmaf(qb.x, kf[4], t); t = fmaf(qb.y, kf[5], t);
+            t = fmaf(qb.z, kf[6], t); t = fmaf(qb.w, kf[7], t);
+            s[g] = t;
         }
     }
+#pragma unroll
+    for (int g = 0; g < GROUP; ++g) {
+        s[g] += dpp_f32<0xB1>(s[g]);  // quad_perm [1,0,3,2]
+        s[g] += dpp_f32<0x4E>(s[g]);  // quad_perm [2,3,0,1]
+    }
 
-    // 6. chunk-local softmax statistics
+    // 5. wave-local softmax statistics over its positions (a wave with no rows has m = -inf, l = 0)
+    const bool valid = p_k < rows;
     float mg[GROUP], lg[GROUP];
 #pragma unroll
     for (int g = 0; g < GROUP; ++g) {
-        const float sv = lane < rows ? s[g] : -INFINITY;
+        const float sv = valid ? s[g] : -INFINITY;
         const float m = wave_max(sv);
-        const float e = lane < rows ? expf(sv - m) : 0.0f;
+        const float e = valid ? expf(sv - m) : 0.0f;
         mg[g] = m;
-        lg[g] = wave_sum(e);
-        ps[lane][g] = e;
+        lg[g] = wave_sum(part == 0 ? e : 0.0f);
+        if (part == 0) ps[wave][p_k][g] = e;
     }
-    __syncthreads();
+    // ps is produced and consumed by the same wave: LDS order within a wave suffices
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // 7. P.V: lane <-> dims (2*lane, 2*lane+1)
+    // 6. P.V: lane <-> dims (2*lane, 2*lane+1), V from registers
     float o0[GROUP], o1[GROUP];
 #pragma unroll
     for (int g = 0; g < GROUP; ++g) o0[g] = o1[g] = 0.0f;
-    for (int p = 0; p < rows; ++p) {
-        const uint32_t vv = vs[p * (AD_D / 2) + lane];
+#pragma unroll
+    for (int p = 0; p < AD_WAVE_POS; ++p) {
+        const uint32_t vv = (has_new && p == rnew) ? vnew : vr[p];
         const float v0 = bf16_bits_to_f32(vv & 0xffffu);
         const float v1 = bf16_bits_to_f32(vv >> 16);
 #pragma unroll
         for (int g = 0; g < GROUP; ++g) {
-            const float pr = ps[p][g];
+            const float pr = ps[wave][p][g];
             o0[g] = fmaf(pr, v0, o0[g]);
             o1[g] = fmaf(pr, v1, o1[g]);
         }
     }
 
-    // 8. publish the partial
-    const size_t cbase = ((size_t)kvh * a.max_chunks + c) * GROUP;
+    // 7. merge the waves in LDS and publish the block's partial
 #pragma unroll
     for (int g = 0; g < GROUP; ++g) {
-        *reinterpret_cast<float2*>(&a.part_o[(cbase + g) * AD_D + 2 * lane]) = make_float2(o0[g], o1[g]);
-        if (lane == 0) *reinterpret_cast<float2*>(&a.part_ml[(cbase + g) * 2]) = make_float2(mg[g], lg[g]);
-    }
-    __threadfence();
-    uint32_t ticket = 0;
-    if (lane == 0) ticket = atomicAdd(&a.tickets[kvh], 1u);
-    ticket = (uint32_t)__shfl((int)ticket, 0, 64);
-    if (ticket != (uint32_t)(n_chunks - 1)) return;
-    __threadfence();
-
-    // 9. last block of this kv head: log-sum-exp merge of all chunks
-    const size_t hbase = (size_t)kvh * a.max_chunks * GROUP;
-#pragma unroll
-    for (int g = 0; g < GROUP; ++g) {
-        float M = -INFINITY;
-        for (int cc = 0; cc < n_chunks; ++cc) M = fmaxf(M, __builtin_nontemporal_load(&a.part_ml[(hbase + (size_t)cc * GROUP + g) * 2]));
-        float lsum = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
-        for (int cc = 0; cc < n_chunks; ++cc) {
-            const size_t idx = hbase + (size_t)cc * GROUP + g;
-            const float m = __builtin_nontemporal_load(&a.part_ml[idx * 2]);
-            const float l = __builtin_nontemporal_load(&a.part_ml[idx * 2 + 1]);
-            const float f = expf(m - M);
-            lsum = fmaf(f, l, lsum);
-            const float2 ov = load_nt_f2(&a.part_o[idx * AD_D + 2 * lane]);
-            acc0 = fmaf(f, ov.x, acc0);
-            acc1 = fmaf(f, ov.y, acc1);
+        wo[wave][g][lane] = make_float2(o0[g], o1[g]);
+        if (lane == 0) {
+            wml[wave][g][0] = mg[g];
+            wml[wave][g][1] = lg[g];
         }
-        const float inv = 1.0f / lsum;
-        const int h = kvh * GROUP + g;
-        reinterpret_cast<uint32_t*>(a.out)[(h * AD_D) / 2 + lane] = pack_bf16x2(acc0 * inv, acc1 * inv);
     }
-    if (lane == 0) a.tickets[kvh] = 0u;
+    __syncthreads();
+    const size_t cbase = ((size_t)kvh * a.max_chunks + c) * GROUP;
+    for (int idx = tid; idx < GROUP * 64; idx += AD_WAVES * 64) {
+        const int g = idx >> 6;
+        const int dl = idx & 63;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < AD_WAVES; ++w) M = fmaxf(M, wml[w][g][0]);
+        float l = 0.0f, r0 = 0.0f, r1 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < AD_WAVES; ++w) {
+            const float m = wml[w][g][0];
+            const float f = m == -INFINITY ? 0.0f : expf(m - M);
+            l = fmaf(f, wml[w][g][1], l);
+            const float2 ov = wo[w][g][dl];
+            r0 = fmaf(f, ov.x, r0);
+            r1 = fmaf(f, ov.y, r1);
+        }
+        *reinterpret_cast<float2*>(&a.part_o[(cbase + g) * AD_D + 2 * dl]) = make_float2(r0, r1);
+        if (dl == 0) *reinterpret_cast<float2*>(&a.part_ml[(cbase + g) * 2]) = make_float2(M, l);
+    }
+}
+
+// Log-sum-exp merge of the per-chunk partials: one block per q head, each of
+// its AD_MERGE_WAVES waves folds a slab of up to AD_MERGE_BATCH chunks at a
+// time (loads issued together; indices past the end re-read the last chunk and
+// get weight 0), then the waves' states are combined in LDS.  Lane t owns dims
+// 2t and 2t+1.
+template <int GROUP>
+__global__ __launch_bounds__(AD_MERGE_WAVES * 64) void attn_decode_merge_kernel(const AttnDecodeArgs a) {
+    __shared__ float fs[AD_MERGE_WAVES][AD_MERGE_BATCH];
+    __shared__ float wst[AD_MERGE_WAVES][2];
+    __shared__ float2 wacc[AD_MERGE_WAVES][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = blockIdx.x;
+    const int kvh = h / GROUP;
+    const int g = h % GROUP;
+    const int pos = *a.pos_ptr;
+    const int S = (int)a.s_cap;
+    const int L = pos + 1 < S ? pos + 1 : S;
+    const int n_chunks = (L + AD_CH - 1) / AD_CH;
+    const size_t hbase = (size_t)kvh * a.max_chunks * GROUP + g;
+    float M = -INFINITY, lsum = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
+    for (int cb = wave * AD_MERGE_BATCH; cb < n_chunks; cb += AD_MERGE_WAVES * AD_MERGE_BATCH) {
+        float2 ov[AD_MERGE_BATCH];
+        float mv = -INFINITY, lv = 0.0f;
+        if (lane < AD_MERGE_BATCH) {
+            const int cc = min(cb + lane, n_chunks - 1);
+            const float2 ml = load_nt_f2(&a.part_ml[(hbase + (size_t)cc * GROUP) * 2]);
+            if (cb + lane < n_chunks) {
+                mv = ml.x;
+                lv = ml.y;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < AD_MERGE_BATCH; ++i) {
+            const int cc = min(cb + i, n_chunks - 1);
+            ov[i] = load_nt_f2(&a.part_o[(hbase + (size_t)cc * GROUP) * AD_D + 2 * lane]);
+        }
+        const float mb = fmaxf(M, wave_max(mv));
+        const float rescale = M == -INFINITY ? 0.0f : expf(M - mb);
+        const float f = mv == -INFINITY ? 0.0f : expf(mv - mb);
+        lsum = lsum * rescale + wave_sum(f * lv);
+        acc0 *= rescale;
+        acc1 *= rescale;
+        M = mb;
+        if (lane < AD_MERGE_BATCH) fs[wave][lane] = f;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < AD_MERGE_BATCH; ++i) {
+            acc0 = fmaf(fs[wave][i], ov[i].x, acc0);
+            acc1 = fmaf(fs[wave][i], ov[i].y, acc1);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    wacc[wave][lane] = make_float2(acc0, acc1);
+    if (lane == 0) {
+        wst[wave][0] = M;
+        wst[wave][1] = lsum;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float Mt = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < AD_MERGE_WAVES; ++w) Mt = fmaxf(Mt, wst[w][0]);
+        float lt = 0.0f, r0 = 0.0f, r1 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < AD_MERGE_WAVES; ++w) {
+            const float f = wst[w][0] == -INFINITY ? 0.0f : expf(wst[w][0] - Mt);
+            lt = fmaf(f, wst[w][1], lt);
+            r0 = fmaf(f, wacc[w][lane].x, r0);
+            r1 = fmaf(f, wacc[w][lane].y, r1);
+        }
+        const float inv = 1.0f / lt;
+        reinterpret_cast<uint32_t*>(a.out)[(h * AD_D) / 2 + lane] = pack_bf16x2(r0 * inv, r1 * inv);
+    }
 }
 
 }  // namespace t2h
@@ -256,11 +378,10 @@ static uint32_t ad_max_chunks(uint32_t s_cap) { return (s_cap + AD_CH - 1) / AD_
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 extern "C" size_t t2h_attn_decode_workspace_bytes(uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap) {
-    if (nk == 0 || nh % nk != 0 || d != AD_D) return 0;
+    if (nk == 0 || nh % nk != 0 || d != AD_D || s_cap == 0 || ad_max_chunks(s_cap) > AD_MAX_PARTS) return 0;
     const size_t group = nh / nk;
     const size_t mc = ad_max_chunks(s_cap);
-    return align256(nk * sizeof(uint32_t)) + align256(nk * mc * group * 2 * sizeof(float)) +
-           align256(nk * mc * group * d * sizeof(float));
+    return align256(nk * mc * group * 2 * sizeof(float)) + align256(nk * mc * group * d * sizeof(float));
 }
 
 extern "C" int t2h_attn_decode(const float* q, const float* k_new, const float* v_new, const float* q_norm_w,
@@ -271,6 +392,7 @@ extern "C" int t2h_attn_decode(const float* q, const float* k_new, const float* 
     if (!q || !k_new || !v_new || !k_cache || !v_cache || !out || !cache_position || !workspace) return T2H_ERR_NULL;
     if (d != AD_D) return T2H_ERR_UNSUPPORTED;
     if (nk == 0 || nh == 0 || nh % nk != 0 || s_cap == 0) return T2H_ERR_SHAPE;
+    if (ad_max_chunks(s_cap) > AD_MAX_PARTS) return T2H_ERR_UNSUPPORTED;
     if ((q_norm_w == nullptr) != (k_norm_w == nullptr)) return T2H_ERR_ARG;
     const uint32_t group = nh / nk;
     if (workspace_bytes < t2h_attn_decode_workspace_bytes(nh, nk, d, s_cap)) return T2H_ERR_WORKSPACE;
@@ -286,8 +408,6 @@ extern "C" int t2h_attn_decode(const float* q, const float* k_new, const float* 
     a.out = reinterpret_cast<uint16_t*>(out);
     a.pos_ptr = cache_position;
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-    a.tickets = reinterpret_cast<uint32_t*>(ws);
-    ws += align256(nk * sizeof(uint32_t));
     a.part_ml = reinterpret_cast<float*>(ws);
     ws += align256((size_t)nk * mc * group * 2 * sizeof(float));
     a.part_o = reinterpret_cast<float*>(ws);
@@ -297,14 +417,23 @@ extern "C" int t2h_attn_decode(const float* q, const float* k_new, const float* 
     a.theta = theta;
     a.eps = eps;
     a.scale = 1.0f / sqrtf((float)d);
-    const dim3 grid(mc, nk), block(64);
+    const dim3 grid(mc, nk), block(AD_WAVES * 64);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const dim3 mgrid(nh), mblock(AD_MERGE_WAVES * 64);
     switch (group) {
-        case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, block, 0, s, a); break;
-        case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, block, 0, s, a); break;
-        case 4: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, block, 0, s, a); break;
-        case 8: hipLaunchKernelGGL(attn_decode_kernel<8>, grid, block, 0, s, a); break;
-        default: return T2H_ERR_UNSUPPORTED;
+#define T2H_AD_CASE(G)                                                                   \
+    case G:                                                                              \
+        hipLaunchKernelGGL(attn_decode_kernel<G>, grid, block, 0, s, a);                 \
+        T2H_LAUNCH_CHECK();                                                              \
+        hipLaunchKernelGGL(attn_decode_merge_kernel<G>, mgrid, mblock, 0, s, a);         \
+        break;
+        T2H_AD_CASE(1)
+        T2H_AD_CASE(2)
+        T2H_AD_CASE(4)
+        T2H_AD_CASE(8)
+#undef T2H_AD_CASE
+        default:
+            return T2H_ERR_UNSUPPORTED;
     }
     T2H_LAUNCH_CHECK();
     return T2H_OK;

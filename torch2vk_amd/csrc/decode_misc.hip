@@ -11,30 +11,56 @@
 namespace t2h {
 
 // One block per token: dequantise the token's Q4_K embedding row into fp32.
+// Thread t handles nibble group (t & 3) of superblock (t >> 2): one 16-B
+// header and 32 B of nibbles -> 64 values, written as 16 float4 stores.
 __global__ __launch_bounds__(256) void embedding_q4_k_kernel(const uint8_t* __restrict__ w,
                                                              const int64_t* __restrict__ ids, uint32_t dim,
                                                              uint64_t vocab, float* __restrict__ out) {
     const uint32_t t = blockIdx.x;
     int64_t id = ids[t];
     if (id < 0 || (uint64_t)id >= vocab) id = 0;  // the host validates host-side ids; device ids are clamped
-    const uint8_t* row = w + (uint64_t)id * (dim / 256) * 144;
-    for (uint32_t h = threadIdx.x; h < dim; h += blockDim.x) {
-        const uint8_t* blk = row + (h >> 8) * 144;
-        const int i = h & 255;
-        const int sb = i >> 5;
-        uint32_t sc, m;
-        if (sb < 4) {
-            sc = blk[4 + sb] & 63u;
-            m = blk[8 + sb] & 63u;
-        } else {
-            sc = (blk[12 + sb - 4] & 15u) | ((uint32_t)(blk[4 + sb - 4] >> 6) << 4);
-            m = ((uint32_t)blk[12 + sb - 4] >> 4) | ((uint32_t)(blk[8 + sb - 4] >> 6) << 4);
+    const uint32_t nsb = dim / 256;
+    const uint8_t* row = w + (uint64_t)id * nsb * 144;
+    for (uint32_t item = threadIdx.x; item < nsb * 4; item += blockDim.x) {
+        const uint32_t sb = item >> 2;
+        const int g = item & 3;
+        const uint8_t* blk = row + (size_t)sb * 144;
+        const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
+        const uint4 q0 = *reinterpret_cast<const uint4*>(blk + 16 + 32 * g);
+        const uint4 q1 = *reinterpret_cast<const uint4*>(blk + 32 + 32 * g);
+        const float d = f16_bits_to_f32(hdr.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(hdr.x >> 16);
+        const uint8_t* sc8 = blk + 4;
+        uint32_t sc[2], m[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int j = 2 * g + h;
+            if (j < 4) {
+                sc[h] = sc8[j] & 63u;
+                m[h] = sc8[4 + j] & 63u;
+            } else {
+                sc[h] = (sc8[8 + j - 4] & 15u) | ((uint32_t)(sc8[j - 4] >> 6) << 4);
+                m[h] = ((uint32_t)sc8[8 + j - 4] >> 4) | ((uint32_t)(sc8[4 + j - 4] >> 6) << 4);
+            }
         }
-        const int byte = ((i >> 6) * 32) + (i & 31);
-        const uint32_t q = (i & 32) ? ((uint32_t)blk[16 + byte] >> 4) : (blk[16 + byte] & 15u);
-        const float d = f16_bits_to_f32(blk[0] | ((uint32_t)blk[1] << 8));
-        const float dmin = f16_bits_to_f32(blk[2] | ((uint32_t)blk[3] << 8));
-        out[(uint64_t)t * dim + h] = d * (float)sc * (float)q - dmin * (float)m;
+        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        float* o = out + (uint64_t)t * dim + sb * 256 + 64 * g;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float a = d * (float)sc[h];
+            const float b = dmin * (float)m[h];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                // (d*sc)*q - dmin*m with no contraction: the decoders' exact fp32 order
+                const uint32_t wq = h ? (q[c] >> 4) : q[c];
+                float4 v;
+                v.x = __fsub_rn(__fmul_rn(a, (float)(wq & 15u)), b);
+                v.y = __fsub_rn(__fmul_rn(a, (float)((wq >> 8) & 15u)), b);
+                v.z = __fsub_rn(__fmul_rn(a, (float)((wq >> 16) & 15u)), b);
+                v.w = __fsub_rn(__fmul_rn(a, (float)((wq >> 24) & 15u)), b);
+                *reinterpret_cast<float4*>(o + 32 * h + 4 * c) = v;
+            }
+        }
     }
 }
 
@@ -93,6 +119,53 @@ __global__ void token_store_kernel(const int64_t* __restrict__ next_token, const
     generated[index] = next_token[0];
     length[0] = index + 1u;
     if (stop_on_eos && done && done[0] != 0u) stopped[0] = 1u;
+}
+
+// Greedy select fused with the token store: one launch per decode step for
+// both QWEN3_TOKEN_SELECT_REDUCE_F32 and QWEN3_TOKEN_STORE_EOS_F32.
+__global__ __launch_bounds__(1024) void token_select_store_kernel(
+    const float* __restrict__ scores, const uint32_t* __restrict__ tokens, uint32_t g,
+    const int64_t* __restrict__ eos, uint32_t n_eos, int64_t* __restrict__ next_token, uint32_t* __restrict__ done,
+    int64_t* __restrict__ generated, uint32_t gen_cap, uint32_t* __restrict__ length, uint32_t* __restrict__ stopped,
+    uint32_t stop_on_eos, int32_t* __restrict__ advance) {
+    __shared__ float ss[16];
+    __shared__ uint32_t st[16];
+    float bs = -3.4028234663852886e38f;
+    uint32_t bt = 0xffffffffu;
+    for (uint32_t i = threadIdx.x; i < g; i += blockDim.x) {
+        if (better_pair(scores[i], tokens[i], bs, bt)) {
+            bs = scores[i];
+            bt = tokens[i];
+        }
+    }
+    wave_argmax(bs, bt);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        ss[wave] = bs;
+        st[wave] = bt;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float s = ss[0];
+        uint32_t t = st[0];
+        for (int i = 1; i < (int)(blockDim.x >> 6); ++i) {
+            if (better_pair(ss[i], st[i], s, t)) {
+                s = ss[i];
+                t = st[i];
+            }
+        }
+        next_token[0] = (int64_t)t;
+        uint32_t is_done = 0;
+        for (uint32_t i = 0; i < n_eos; ++i) is_done |= ((int64_t)t == eos[i]) ? 1u : 0u;
+        if (done) done[0] = is_done;
+        if (advance) advance[0] += 1;
+        const uint32_t index = length[0];
+        if (index < gen_cap && !(stop_on_eos && stopped[0] != 0u)) {
+            generated[index] = (int64_t)t;
+            length[0] = index + 1u;
+            if (stop_on_eos && is_done) stopped[0] = 1u;
+        }
+    }
 }
 
 // rows x H RMSNorm; x and out are fp32 or bf16, weight fp32.
@@ -160,6 +233,19 @@ extern "C" int t2h_token_select(const float* scores, const uint32_t* tokens, uin
     if (g == 0) return T2H_ERR_SHAPE;
     hipLaunchKernelGGL(token_select_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, scores, tokens, g, eos,
                        n_eos, next_token, done);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+extern "C" int t2h_token_select_store(const float* scores, const uint32_t* tokens, uint32_t g,
+                                      const int64_t* eos, uint32_t n_eos, int64_t* next_token, uint32_t* done,
+                                      int64_t* generated, uint32_t gen_cap, uint32_t* length, uint32_t* stopped,
+                                      uint32_t stop_on_eos, int32_t* advance, void* stream) {
+    if (!scores || !tokens || !next_token || !generated || !length || !stopped) return T2H_ERR_NULL;
+    if (n_eos && !eos) return T2H_ERR_NULL;
+    if (g == 0) return T2H_ERR_SHAPE;
+    hipLaunchKernelGGL(token_select_store_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, scores, tokens, g, eos,
+                       n_eos, next_token, done, generated, gen_cap, length, stopped, stop_on_eos, advance);
     T2H_LAUNCH_CHECK();
     return T2H_OK;
 }

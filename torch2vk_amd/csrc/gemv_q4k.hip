@@ -11,19 +11,19 @@
 // Weight layout: GGUF Q4_K rows, 144 B per 256-value superblock
 // (fp16 d | fp16 dmin | 12 B 6-bit scale/min codes | 128 B nibbles).
 //
-// Work mapping.  A wave streams 8 superblocks per step: lane l reads the 16-B
-// header and the 16-B nibble chunk (l & 7) of superblock (l >> 3).  Chunk c
-// holds bytes 16*(c&1)..+15 of nibble group g = c>>1, i.e. 16 values of
-// sub-block 2g (low nibbles) and 16 values of sub-block 2g+1 (high nibbles).
-// A "row group" is RPW consecutive rows covered by NIT such steps, with
-// RPW = 8/gcd(NSB,8) and NIT = NSB*RPW/8, so no lane idles for any K.
+// Work mapping.  A wave streams 16 superblocks per step: lanes 4s..4s+3 own
+// superblock s, and lane l reads the 16-B header plus the 32-B nibble group
+// g = l & 3, i.e. all 32 values of sub-block 2g (low nibbles) and of
+// sub-block 2g+1 (high nibbles).  One header decode therefore serves 64
+// weights.  A "row group" is RPW consecutive rows covered by NIT such steps,
+// RPW = 16/gcd(NSB,16) and NIT = NSB*RPW/16, so no lane idles for any K.
 //
 // Arithmetic.  Nibble pairs become bf16 values 128+q with one and-or
 // (0x4300 | q), and v_dot2_f32_bf16 accumulates x*(128+q) in fp32; the 128*Σx
 // offset is removed with the per-lane Σx the min term needs anyway:
 //   Σ x*w = d*(sc_lo*(S_lo - 128 Σx_lo) + sc_hi*(S_hi - 128 Σx_hi)) - dmin*(m_lo Σx_lo + m_hi Σx_hi)
 // x is the same for every row, so each lane keeps its x slice in registers
-// for the whole launch.
+// for the whole launch; the weight stream is software pipelined.
 #include "common.h"
 
 namespace t2h {
@@ -45,6 +45,7 @@ struct Q4GemvArgs {
     Q4Part parts[3];
     uint32_t n_parts;
     uint32_t n_units;       // row groups (Q4EPI_SWIGLU: row groups of the gate)
+    uint32_t units_per_wave;  // every wave runs this many units (rounded up to the ring size, clamped)
     float* partial_scores;  // Q4EPI_ARGMAX: [gridDim.x]
     uint32_t* partial_tokens;
     float eps;
@@ -59,28 +60,32 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 
 constexpr int cgcd(int a, int b) { return b == 0 ? a : cgcd(b, a % b); }
 
+constexpr int GEMV_THREADS = 512;  // 8 waves per block share one staged copy of x
+constexpr uint32_t GEMV_WAVES = GEMV_THREADS / 64;
+
 template <int NSB>
 struct Q4Geom {
     static constexpr int K = NSB * 256;
-    static constexpr int RPW = 8 / cgcd(NSB, 8);
-    static constexpr int NIT = NSB * RPW / 8;
+    static constexpr int RPW = 16 / cgcd(NSB, 16);
+    static constexpr int NIT = NSB * RPW / 16;
     static constexpr int ROW_BYTES = NSB * 144;
 };
 
-// Per-lane x slice for one step: 16 low-sub-block values and 16 high-sub-block
-// values, stored as bf16 pairs (e0,e2),(e1,e3),(e4,e6),... to match the
-// nibble pairs the and-or trick produces.
+// Per-lane x slice for one step: the 32 values of sub-block 2g and the 32 of
+// sub-block 2g+1, stored as bf16 pairs (e0,e2),(e1,e3),(e4,e6),... to match
+// the nibble pairs the and-or trick produces, plus their sums.
 struct XSlice {
-    uint32_t lo[8];
-    uint32_t hi[8];
+    uint32_t lo[16];
+    uint32_t hi[16];
     float sum_lo;
     float sum_hi;
 };
 
-__device__ __forceinline__ void pair_up(const uint32_t (&raw)[8], uint32_t (&out)[8], float& sum) {
+// 32 bf16 values (16 dwords, natural order) -> 16 pairs + their sum
+__device__ __forceinline__ void pair_up(const uint32_t (&raw)[16], uint32_t (&out)[16], float& sum) {
     float s = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < 8; ++c) {
         const uint32_t x0 = raw[2 * c];      // (e0, e1)
         const uint32_t x1 = raw[2 * c + 1];  // (e2, e3)
         out[2 * c] = (x0 & 0xffffu) | (x1 << 16);
@@ -91,22 +96,46 @@ __device__ __forceinline__ void pair_up(const uint32_t (&raw)[8], uint32_t (&out
     sum = s;
 }
 
-__device__ __forceinline__ void load_xslice(const uint16_t* xb, int off_lo, XSlice& xs) {
-    uint32_t raw[8];
-    const uint4 a = load_u4(xb + off_lo);
-    const uint4 b = load_u4(xb + off_lo + 8);
-    raw[0] = a.x; raw[1] = a.y; raw[2] = a.z; raw[3] = a.w;
-    raw[4] = b.x; raw[5] = b.y; raw[6] = b.z; raw[7] = b.w;
+__device__ __forceinline__ void unpack_u4x4(const uint4 (&v)[4], uint32_t (&raw)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        raw[4 * i] = v[i].x;
+        raw[4 * i + 1] = v[i].y;
+        raw[4 * i + 2] = v[i].z;
+        raw[4 * i + 3] = v[i].w;
+    }
+}
+
+// x slice of nibble group g starting at element off (= 64 g within a superblock)
+__device__ __forceinline__ void load_xslice(const uint16_t* xb, int off, XSlice& xs) {
+    uint4 v[4];
+    uint32_t raw[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = load_u4(xb + off + 8 * i);
+    unpack_u4x4(v, raw);
     pair_up(raw, xs.lo, xs.sum_lo);
-    const uint4 c = load_u4(xb + off_lo + 32);
-    const uint4 d = load_u4(xb + off_lo + 40);
-    raw[0] = c.x; raw[1] = c.y; raw[2] = c.z; raw[3] = c.w;
-    raw[4] = d.x; raw[5] = d.y; raw[6] = d.z; raw[7] = d.w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = load_u4(xb + off + 32 + 8 * i);
+    unpack_u4x4(v, raw);
     pair_up(raw, xs.hi, xs.sum_hi);
 }
 
-// Partial dot of one lane's 32 values of one superblock.
-__device__ __forceinline__ float q4k_lane_dot(const uint4 hdr, const uint4 qs, const XSlice& xs, int g) {
+__device__ __forceinline__ void dot_nibble_word(uint32_t w, uint32_t xa, uint32_t xb, uint32_t xc, uint32_t xd,
+                                                float& s_lo, float& s_hi) {
+    const uint32_t w4 = w >> 4;
+    const uint32_t pa = (w & 0x000f000fu) | 0x43004300u;
+    const uint32_t pb = ((w >> 8) & 0x000f000fu) | 0x43004300u;
+    const uint32_t pc = (w4 & 0x000f000fu) | 0x43004300u;
+    const uint32_t pd = ((w4 >> 8) & 0x000f000fu) | 0x43004300u;
+    s_lo = dot2_bf16(pa, xa, s_lo);
+    s_lo = dot2_bf16(pb, xb, s_lo);
+    s_hi = dot2_bf16(pc, xc, s_hi);
+    s_hi = dot2_bf16(pd, xd, s_hi);
+}
+
+// Partial dot of one lane's 64 values of one superblock (nibble group g).
+__device__ __forceinline__ float q4k_lane_dot(const uint4 hdr, const uint4 q0, const uint4 q1, const XSlice& xs,
+                                              int g) {
     const float d = f16_bits_to_f32(hdr.x & 0xffffu);
     const float dmin = f16_bits_to_f32(hdr.x >> 16);
     // 6-bit scale/min codes of sub-blocks 2g and 2g+1 (two bytes each)
@@ -125,20 +154,10 @@ __device__ __forceinline__ float q4k_lane_dot(const uint4 hdr, const uint4 qs, c
     const float m_hi = (float)((M >> 8) & 0xffu);
 
     float s_lo = 0.0f, s_hi = 0.0f;
-    const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+    const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint32_t w = q[c];
-        const uint32_t w4 = w >> 4;
-        const uint32_t pa = (w & 0x000f000fu) | 0x43004300u;
-        const uint32_t pb = ((w >> 8) & 0x000f000fu) | 0x43004300u;
-        const uint32_t pc = (w4 & 0x000f000fu) | 0x43004300u;
-        const uint32_t pd = ((w4 >> 8) & 0x000f000fu) | 0x43004300u;
-        s_lo = dot2_bf16(pa, xs.lo[2 * c], s_lo);
-        s_lo = dot2_bf16(pb, xs.lo[2 * c + 1], s_lo);
-        s_hi = dot2_bf16(pc, xs.hi[2 * c], s_hi);
-        s_hi = dot2_bf16(pd, xs.hi[2 * c + 1], s_hi);
-    }
+    for (int c = 0; c < 8; ++c)
+        dot_nibble_word(q[c], xs.lo[2 * c], xs.lo[2 * c + 1], xs.hi[2 * c], xs.hi[2 * c + 1], s_lo, s_hi);
     const float xq_lo = fmaf(-128.0f, xs.sum_lo, s_lo);
     const float xq_hi = fmaf(-128.0f, xs.sum_hi, s_hi);
     const float scaled = fmaf(sc_lo, xq_lo, sc_hi * xq_hi);
@@ -149,148 +168,221 @@ __device__ __forceinline__ float q4k_lane_dot(const uint4 hdr, const uint4 qs, c
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 template <int NSB, int PRO, int EPI>
-__global__ __launch_bounds__(256) void q4k_gemv_kernel(const Q4GemvArgs a) {
+__global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs a) {
     using Geo = Q4Geom<NSB>;
     constexpr int K = Geo::K;
     constexpr int RPW = Geo::RPW;
     constexpr int NIT = Geo::NIT;
     constexpr int ROW_BYTES = Geo::ROW_BYTES;
+    constexpr int NG = EPI == Q4EPI_SWIGLU ? 2 : 1;  // row groups per unit (gate and up)
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, scalar
     const int waves_per_block = blockDim.x >> 6;
-    const int sbo = lane >> 3;
-    const int chunk = lane & 7;
-    const int g = chunk >> 1;
-    const int hh = chunk & 1;
+    const int sbo = lane >> 2;  // superblock slot of this lane within a step
+    const int g = lane & 3;     // nibble group: sub-blocks 2g (low nibbles) and 2g+1 (high)
 
     int rloc[NIT];
     int sbi[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-        const int f = it * 8 + sbo;
+        const int f = it * 16 + sbo;
         rloc[it] = f / NSB;
         sbi[it] = f % NSB;
     }
 
+    // Weight stream, software pipelined over a ring of NSTAGE stages: a stage
+    // holds the header and nibble chunks of one unit (NG row groups) and
+    // NSTAGE-1 units are in flight while one is reduced.  Every wave runs the
+    // same number of units; units past the end are clamped to the last one and
+    // their results dropped, so the load stream has no divergent branches.
+    constexpr int NSTAGE = (NG * NIT <= 2) ? 3 : 2;
+    struct Stage {
+        uint4 hdr[NG][NIT];
+        uint4 q0[NG][NIT];
+        uint4 q1[NG][NIT];
+    };
+    auto issue = [&](uint32_t unit, Stage& st) {
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const uint8_t* base;
+                if constexpr (EPI == Q4EPI_SWIGLU) {
+                    const uint32_t row = unit * RPW + (uint32_t)rloc[it];
+                    base = a.parts[gi].w + (size_t)row * ROW_BYTES;
+                } else {
+                    const uint32_t row = unit * RPW + (uint32_t)rloc[it];
+                    int pi = 0;
+                    pi += (a.n_parts > 1 && row >= a.parts[1].row_begin) ? 1 : 0;
+                    pi += (a.n_parts > 2 && row >= a.parts[2].row_begin) ? 1 : 0;
+                    const Q4Part& p = a.parts[pi];
+                    base = p.w + (size_t)(row - p.row_begin) * ROW_BYTES;
+                }
+                base += (size_t)sbi[it] * 144;
+                st.hdr[gi][it] = load_u4(base);
+                // plain (temporal) loads: the two 16-B chunks of a lane are 32 B
+                // apart, so each instruction uses half of every line it touches
+                // and the other half must still be cached for the next one;
+                // non-temporal loads measured ~25% slower here
+                st.q0[gi][it] = load_u4(base + 16 + g * 32);
+                st.q1[gi][it] = load_u4(base + 32 + g * 32);
+            }
+        }
+    };
+
+    const uint32_t wave_global = blockIdx.x * waves_per_block + wave;
+    const uint32_t total_waves = gridDim.x * waves_per_block;
+    const uint32_t last_unit = a.n_units - 1;
+    auto clamp_unit = [&](uint32_t u) { return u < a.n_units ? u : last_unit; };
+    const uint32_t n_iter = (a.units_per_wave + NSTAGE - 1) / NSTAGE * NSTAGE;
+    Stage st[NSTAGE];
+
     // ---------------------------------------------------------- x slice --
-    XSlice xs[NIT];
+    // x is staged once per block in LDS (bf16, coalesced loads shared by the
+    // block's waves) and each lane then reads its slices from LDS.  The x-side
+    // loads are issued before the first weight stages: vmcnt retires in order,
+    // so the prologue waits for them alone while the weight loads stay in flight.
+    __shared__ __align__(16) uint16_t xsh[K];
     if constexpr (PRO == Q4PRO_RMSNORM) {
-        __shared__ __align__(16) uint16_t xsh[K];
-        __shared__ float red[16];
+        // one pass: h and norm weight loaded once, sum of squares reduced over
+        // the block, normalised bf16 x written to LDS
+        constexpr int PT = (K + 4 * GEMV_THREADS - 1) / (4 * GEMV_THREADS);  // float4s per thread
+        __shared__ float red[GEMV_THREADS / 64];
         const float* h = reinterpret_cast<const float*>(a.x);
+        float4 hv[PT], wv[PT];
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            const int k = (j * GEMV_THREADS + (int)threadIdx.x) * 4;
+            if (K % (4 * GEMV_THREADS) == 0 || k < K) {
+                hv[j] = *reinterpret_cast<const float4*>(h + k);
+                wv[j] = *reinterpret_cast<const float4*>(a.norm_w + k);
+            } else {
+                hv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                wv[j] = hv[j];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s + 1 < NSTAGE; ++s) issue(clamp_unit(wave_global + s * total_waves), st[s]);
         float ss = 0.0f;
-        for (int k = threadIdx.x * 4; k < K; k += blockDim.x * 4) {
-            const float4 v = *reinterpret_cast<const float4*>(h + k);
-            ss = fmaf(v.x, v.x, ss);
-            ss = fmaf(v.y, v.y, ss);
-            ss = fmaf(v.z, v.z, ss);
-            ss = fmaf(v.w, v.w, ss);
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            ss = fmaf(hv[j].x, hv[j].x, ss);
+            ss = fmaf(hv[j].y, hv[j].y, ss);
+            ss = fmaf(hv[j].z, hv[j].z, ss);
+            ss = fmaf(hv[j].w, hv[j].w, ss);
         }
         ss = wave_sum(ss);
         if (lane == 0) red[wave] = ss;
         __syncthreads();
         float total = 0.0f;
-        for (int i = 0; i < waves_per_block; ++i) total += red[i];
+#pragma unroll
+        for (int i = 0; i < GEMV_THREADS / 64; ++i) total += red[i];
         const float inv = 1.0f / sqrtf(total / (float)K + a.eps);
-        for (int k = threadIdx.x * 4; k < K; k += blockDim.x * 4) {
-            const float4 v = *reinterpret_cast<const float4*>(h + k);
-            const float4 w = *reinterpret_cast<const float4*>(a.norm_w + k);
-            const uint32_t p0 = pack_bf16x2(v.x * inv * w.x, v.y * inv * w.y);
-            const uint32_t p1 = pack_bf16x2(v.z * inv * w.z, v.w * inv * w.w);
-            *reinterpret_cast<uint2*>(&xsh[k]) = make_uint2(p0, p1);
-        }
-        __syncthreads();
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) load_xslice(xsh, sbi[it] * 256 + 64 * g + 16 * hh, xs[it]);
+        for (int j = 0; j < PT; ++j) {
+            const int k = (j * GEMV_THREADS + (int)threadIdx.x) * 4;
+            if (K % (4 * GEMV_THREADS) == 0 || k < K) {
+                const uint32_t p0 = pack_bf16x2(hv[j].x * inv * wv[j].x, hv[j].y * inv * wv[j].y);
+                const uint32_t p1 = pack_bf16x2(hv[j].z * inv * wv[j].z, hv[j].w * inv * wv[j].w);
+                *reinterpret_cast<uint2*>(&xsh[k]) = make_uint2(p0, p1);
+            }
+        }
     } else {
+        constexpr int PT = (K + 8 * GEMV_THREADS - 1) / (8 * GEMV_THREADS);  // 16-B chunks per thread
         const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x);
+        uint4 xv[PT];
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) load_xslice(xb, sbi[it] * 256 + 64 * g + 16 * hh, xs[it]);
+        for (int j = 0; j < PT; ++j) {
+            const int k = (j * GEMV_THREADS + (int)threadIdx.x) * 8;
+            xv[j] = (K % (8 * GEMV_THREADS) == 0 || k < K) ? load_u4(xb + k) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s + 1 < NSTAGE; ++s) issue(clamp_unit(wave_global + s * total_waves), st[s]);
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            const int k = (j * GEMV_THREADS + (int)threadIdx.x) * 8;
+            if (K % (8 * GEMV_THREADS) == 0 || k < K) *reinterpret_cast<uint4*>(&xsh[k]) = xv[j];
+        }
     }
-
-    // ------------------------------------------------------- row groups --
-    auto row_group = [&](int part_lo, int part_hi, uint32_t row0, float (&res)[RPW]) {
-        uint4 hdr[NIT];
-        uint4 qs[NIT];
+    __syncthreads();
+    XSlice xs[NIT];
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-            const uint32_t row = row0 + (uint32_t)rloc[it];
-            int pi = part_lo;
-            if (part_hi > part_lo) {
-                pi += (a.n_parts > 1 && row >= a.parts[1].row_begin) ? 1 : 0;
-                pi += (a.n_parts > 2 && row >= a.parts[2].row_begin) ? 1 : 0;
-            }
-            const Q4Part& p = a.parts[pi];
-            const uint8_t* base = p.w + (size_t)(row - p.row_begin) * ROW_BYTES + (size_t)sbi[it] * 144;
-            hdr[it] = load_u4(base);
-            qs[it] = load_nt_u4(base + 16 + chunk * 16);
-        }
-        float acc[RPW];
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-#pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-            const float c = q4k_lane_dot(hdr[it], qs[it], xs[it], g);
-            if constexpr (RPW == 1) {
-                acc[0] += c;
-            } else {
-#pragma unroll
-                for (int r = 0; r < RPW; ++r) acc[r] += (rloc[it] == r) ? c : 0.0f;
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) res[r] = wave_sum(acc[r]);
-    };
-
-    const int wave_global = blockIdx.x * waves_per_block + wave;
-    const int total_waves = gridDim.x * waves_per_block;
+    for (int it = 0; it < NIT; ++it) load_xslice(xsh, sbi[it] * 256 + 64 * g, xs[it]);
 
     float best_score = -3.4028234663852886e38f;
     uint32_t best_token = 0xffffffffu;
 
-    for (uint32_t unit = (uint32_t)wave_global; unit < a.n_units; unit += (uint32_t)total_waves) {
-        const uint32_t row0 = unit * RPW;
+    auto consume = [&](uint32_t u, const Stage& st) {
+        const bool live = u < a.n_units;
+        float res[NG][RPW];
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+            float acc[RPW];
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const float c = q4k_lane_dot(st.hdr[gi][it], st.q0[gi][it], st.q1[gi][it], xs[it], g);
+                if constexpr (RPW == 1) {
+                    acc[0] += c;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < RPW; ++r) acc[r] += (rloc[it] == r) ? c : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) res[gi][r] = wave_sum(acc[r]);
+        }
+        const uint32_t row0 = u * RPW;
+        if (!live) return;
         if constexpr (EPI == Q4EPI_SWIGLU) {
-            float gres[RPW];
-            float ures[RPW];
-            row_group(0, 0, row0, gres);
-            row_group(1, 1, row0 + a.parts[1].row_begin, ures);
-            if (lane == 0) {
-                uint16_t* y = reinterpret_cast<uint16_t*>(a.parts[0].y);
+            if (lane < RPW) {
+                float gv = res[0][0], uv = res[1][0];
 #pragma unroll
-                for (int r = 0; r < RPW; ++r) y[row0 + r] = (uint16_t)f32_to_bf16_bits(silu(gres[r]) * ures[r]);
-            }
-        } else {
-            float res[RPW];
-            row_group(0, (int)a.n_parts - 1, row0, res);
-            if constexpr (EPI == Q4EPI_ARGMAX) {
-#pragma unroll
-                for (int r = 0; r < RPW; ++r) {
-                    if (better_pair(res[r], row0 + r, best_score, best_token)) {
-                        best_score = res[r];
-                        best_token = row0 + r;
-                    }
+                for (int r = 1; r < RPW; ++r) {
+                    gv = (lane == r) ? res[0][r] : gv;
+                    uv = (lane == r) ? res[1][r] : uv;
                 }
-            } else if (lane < RPW) {
-                // lane r stores row r of the group (res[] is wave-uniform)
-                float v = res[0];
+                reinterpret_cast<uint16_t*>(a.parts[0].y)[row0 + lane] = (uint16_t)f32_to_bf16_bits(silu(gv) * uv);
+            }
+        } else if constexpr (EPI == Q4EPI_ARGMAX) {
 #pragma unroll
-                for (int r = 1; r < RPW; ++r) v = (lane == r) ? res[r] : v;
-                const uint32_t row = row0 + lane;
-                int pi = 0;
-                pi += (a.n_parts > 1 && row >= a.parts[1].row_begin) ? 1 : 0;
-                pi += (a.n_parts > 2 && row >= a.parts[2].row_begin) ? 1 : 0;
-                const Q4Part& p = a.parts[pi];
-                const uint32_t local = row - p.row_begin;
-                if constexpr (EPI == Q4EPI_F32) {
-                    reinterpret_cast<float*>(p.y)[local] = v;
-                } else if constexpr (EPI == Q4EPI_BF16) {
-                    reinterpret_cast<uint16_t*>(p.y)[local] = (uint16_t)f32_to_bf16_bits(v);
-                } else if constexpr (EPI == Q4EPI_RESID) {
-                    reinterpret_cast<float*>(p.y)[local] = a.residual[local] + v;
+            for (int r = 0; r < RPW; ++r) {
+                if (better_pair(res[0][r], row0 + r, best_score, best_token)) {
+                    best_score = res[0][r];
+                    best_token = row0 + r;
                 }
             }
+        } else if (lane < RPW) {
+            // lane r stores row r of the group (res[] is wave-uniform)
+            float v = res[0][0];
+#pragma unroll
+            for (int r = 1; r < RPW; ++r) v = (lane == r) ? res[0][r] : v;
+            const uint32_t row = row0 + lane;
+            int pi = 0;
+            pi += (a.n_parts > 1 && row >= a.parts[1].row_begin) ? 1 : 0;
+            pi += (a.n_parts > 2 && row >= a.parts[2].row_begin) ? 1 : 0;
+            const Q4Part& p = a.parts[pi];
+            const uint32_t local = row - p.row_begin;
+            if constexpr (EPI == Q4EPI_F32) {
+                reinterpret_cast<float*>(p.y)[local] = v;
+            } else if constexpr (EPI == Q4EPI_BF16) {
+                reinterpret_cast<uint16_t*>(p.y)[local] = (uint16_t)f32_to_bf16_bits(v);
+            } else if constexpr (EPI == Q4EPI_RESID) {
+                reinterpret_cast<float*>(p.y)[local] = a.residual[local] + v;
+            }
+        }
+    };
+
+    // ring over the units of this wave: issue unit i+NSTAGE-1, reduce unit i
+    for (uint32_t i = 0; i < n_iter; i += NSTAGE) {
+#pragma unroll
+        for (int s = 0; s < NSTAGE; ++s) {
+            const uint32_t ui = i + s;
+            if (ui + NSTAGE - 1 < n_iter)
+                issue(clamp_unit(wave_global + (ui + NSTAGE - 1) * total_waves), st[(s + NSTAGE - 1) % NSTAGE]);
+            consume(wave_global + ui * total_waves, st[s]);
         }
     }
 
@@ -350,26 +442,32 @@ static bool nsb_supported(uint32_t nsb) {
 }
 
 static uint32_t rows_per_group(uint32_t nsb) {
-    uint32_t a = nsb, b = 8;
+    uint32_t a = nsb, b = 16;
     while (b) {
         const uint32_t t = a % b;
         a = b;
         b = t;
     }
-    return 8u / a;
+    return 16u / a;
 }
 
 // Grid: enough blocks of 4 waves that every wave gets about `units_per_wave`
 // row groups, capped so that the launch stays a few blocks per CU.
+static uint32_t units_per_wave(uint32_t n_units, uint32_t blocks) {
+    const uint32_t waves = blocks * GEMV_WAVES;
+    return (n_units + waves - 1u) / waves;
+}
+
 static uint32_t pick_blocks(uint32_t n_units, uint32_t max_blocks) {
-    const uint32_t waves_needed = n_units;
-    uint32_t blocks = (waves_needed + 3u) / 4u;
-    if (blocks > max_blocks) blocks = max_blocks;
+    if (max_blocks == 0) max_blocks = 1;
+    const uint32_t u = units_per_wave(n_units, max_blocks);
+    uint32_t blocks = (n_units + GEMV_WAVES * u - 1u) / (GEMV_WAVES * u);
     if (blocks == 0) blocks = 1;
     return blocks;
 }
 
-static uint32_t g_max_blocks = 2048;
+static uint32_t g_max_blocks = 256;        // blocks of GEMV_WAVES waves, plain x input
+static uint32_t g_max_blocks_norm = 256;   // RMSNorm prologue: each block re-reads h and the norm weight
 
 }  // namespace t2h
 
@@ -381,14 +479,17 @@ static int validate_q4(uint32_t k) {
     return T2H_OK;
 }
 
-extern "C" int t2h_set_gemv_max_blocks(uint32_t max_blocks) {
+extern "C" int t2h_set_gemv_max_blocks(uint32_t max_blocks, uint32_t max_blocks_norm) {
     if (max_blocks == 0) return T2H_ERR_ARG;
     g_max_blocks = max_blocks;
+    g_max_blocks_norm = max_blocks_norm ? max_blocks_norm : max_blocks;
     return T2H_OK;
 }
 
-static int q4k_launch(int pro, int epi, const Q4GemvArgs& a, uint32_t nsb, uint32_t blocks, hipStream_t s) {
-    const dim3 grid(blocks), block(256);
+static int q4k_launch(int pro, int epi, Q4GemvArgs a, uint32_t nsb, uint32_t blocks, hipStream_t s) {
+    if (a.n_units == 0) return T2H_OK;
+    a.units_per_wave = units_per_wave(a.n_units, blocks);
+    const dim3 grid(blocks), block(GEMV_THREADS);
     hipError_t e = hipErrorInvalidValue;
     if (pro == Q4PRO_BF16) {
         switch (epi) {
@@ -494,7 +595,8 @@ extern "C" int t2h_q4k_matvec_multi(const void* x, const float* norm_w, float ep
     } else {
         return T2H_ERR_DTYPE;
     }
-    return q4k_launch(pro, epi, a, nsb, pick_blocks(a.n_units, g_max_blocks), reinterpret_cast<hipStream_t>(stream));
+    return q4k_launch(pro, epi, a, nsb, pick_blocks(a.n_units, norm_w ? g_max_blocks_norm : g_max_blocks),
+                      reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int t2h_q4k_rmsnorm_swiglu_matvec(const float* h, const float* norm_w, float eps, const void* w_gate,
@@ -516,7 +618,7 @@ extern "C" int t2h_q4k_rmsnorm_swiglu_matvec(const float* h, const float* norm_w
     a.norm_w = norm_w;
     a.eps = eps;
     a.n_units = n / rpw;
-    return q4k_launch(Q4PRO_RMSNORM, Q4EPI_SWIGLU, a, nsb, pick_blocks(a.n_units, g_max_blocks),
+    return q4k_launch(Q4PRO_RMSNORM, Q4EPI_SWIGLU, a, nsb, pick_blocks(a.n_units, g_max_blocks_norm),
                       reinterpret_cast<hipStream_t>(stream));
 }
 

@@ -183,8 +183,9 @@ def q4k_lm_head_argmax_partial(x: torch.Tensor, w: torch.Tensor, partial_scores:
          ptr(partial_tokens), g, stream_handle())
 
 
-def set_gemv_max_blocks(max_blocks: int) -> None:
-    call("t2h_set_gemv_max_blocks", int(max_blocks))
+def set_gemv_max_blocks(max_blocks: int, max_blocks_norm: int = 0) -> None:
+    """Grid caps (blocks of 4 waves) for plain and RMSNorm-prologue GEMV launches."""
+    call("t2h_set_gemv_max_blocks", int(max_blocks), int(max_blocks_norm))
 
 
 # ------------------------------------------------------- token selection --
@@ -215,6 +216,25 @@ def token_store(next_token: torch.Tensor, done: torch.Tensor, generated: torch.T
         _check(advance, "advance", torch.int32, align=4)
     call("t2h_token_store", ptr(next_token), ptr(done), ptr(generated), generated.numel(), ptr(length),
          ptr(stopped), int(stop_on_eos), ptr(token_index_ptr), int(token_index), ptr(advance), stream_handle())
+
+
+def token_select_store(partial_scores: torch.Tensor, partial_tokens: torch.Tensor, eos_ids: torch.Tensor,
+                       next_token: torch.Tensor, done: torch.Tensor, generated: torch.Tensor, length: torch.Tensor,
+                       stopped: torch.Tensor, *, stop_on_eos: bool = True, advance: torch.Tensor | None = None) -> None:
+    """token_select + token_store (index from the device length counter) in one launch."""
+    _check(partial_scores, "scores", torch.float32, align=4)
+    _check(partial_tokens, "tokens", torch.int32, align=4)
+    _check(eos_ids, "eos_token_ids", torch.int64, align=8)
+    _check(next_token, "next_token", torch.int64, align=8)
+    _check(done, "done", torch.int32, align=4)
+    _check(generated, "generated_tokens", torch.int64, align=8)
+    _check(length, "generated_length", torch.int32, align=4)
+    _check(stopped, "stopped", torch.int32, align=4)
+    if advance is not None:
+        _check(advance, "advance", torch.int32, align=4)
+    call("t2h_token_select_store", ptr(partial_scores), ptr(partial_tokens), partial_scores.numel(), ptr(eos_ids),
+         eos_ids.numel(), ptr(next_token), ptr(done), ptr(generated), generated.numel(), ptr(length), ptr(stopped),
+         int(stop_on_eos), ptr(advance), stream_handle())
 
 
 # ------------------------------------------------------ decode attention --

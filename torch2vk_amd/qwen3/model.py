@@ -31,7 +31,7 @@ from torch2vk_amd import kernels
 from torch2vk_amd.qwen3.config import Qwen3Config
 from torch2vk_amd.qwen3.weights import Qwen3Weights
 
-LM_HEAD_PARTIALS = 2048
+LM_HEAD_PARTIALS = 512
 
 
 class Qwen3Decoder:
@@ -129,9 +129,15 @@ class Qwen3Decoder:
         self.run_lm_head_select()
 
     def decode_step(self) -> None:
-        """One full greedy step: forward, store the token, advance the position."""
-        self.forward_token()
-        self.run_token_store(advance=True)
+        """One full greedy step: forward, select + store the token, advance the position."""
+        self.run_decode_embed()
+        for i in range(self.config.layers):
+            self.run_decode_layer(i)
+        kernels.q4k_lm_head_argmax_partial(self.h, self._w("lm_head"), self.partial_scores, self.partial_tokens,
+                                           norm_weight=self._n("norm"), eps=self.config.rms_eps)
+        kernels.token_select_store(self.partial_scores, self.partial_tokens, self.eos, self.next_token, self.done,
+                                   self.generated, self.length, self.stopped, stop_on_eos=self.stop_on_eos,
+                                   advance=self.position)
 
     # ------------------------------------------------------ HIP graphs --
 
