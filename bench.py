@@ -8,8 +8,9 @@ A step is one full token: embed, 36 layers, final norm + LM head + argmax, token
 graphs (8 steps per graph).  value = tokens/s over the timed steps.
 
 roofline: the dominant kernel (fused RMSNorm + gate|up GEMV + SwiGLU) timed live with HIP events on
-the stream it runs on, over all 36 layers' weights (2 GB, well above the 256 MB MALL);
-achieved = algorithmic bytes per launch / average launch time.
+the stream a HIP graph of its 36 launches (one per layer, 2 GB of weights, well above the 256 MB
+MALL) is replayed on; achieved = algorithmic bytes per launch / average launch time; traffic = HBM
+bytes per launch from the committed FETCH_SIZE/WRITE_SIZE counter summary under profiles/.
 
 cpu_baseline: the CPU oracle's Qwen3 decoder (oracle.reference.Qwen3CpuModel, dense fp32 weights
 dequantized by the oracle) on a bounded sample of the same workload, scaled to tokens/s.
@@ -20,11 +21,14 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
+from pathlib import Path
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_PROFILE = Path(__file__).resolve().parent / "profiles" / "gate_up_gemv_qwen3_8b_pmc.md"
 PROMPT_POSITIONS = 4096
 
 
@@ -40,7 +44,37 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample-steps", type=int, default=3)
     p.add_argument("--no-graph", action="store_true")
+    p.add_argument("--profile-kernel", action="store_true",
+                   help="counter-collection target: run the dominant kernel over all layers plus a 256 MiB copy "
+                        "(the calibration for FETCH_SIZE/WRITE_SIZE), no timing, no JSON line")
     return p.parse_args()
+
+
+def profile_kernel_target() -> int:
+    """Launch sequence for `rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE`: 36 dominant-kernel launches
+    (one per layer) x 2, then one plain 256 MiB device copy whose traffic is known (256 MiB read +
+    256 MiB written), so counter readings can be scaled to bytes."""
+    import torch
+
+    from torch2vk_amd import kernels
+    from torch2vk_amd.qwen3.config import QWEN3_8B
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+    from torch2vk_amd.qwen3.weights import synthetic_weights
+
+    dev = torch.device("cuda:0")
+    w = synthetic_weights(QWEN3_8B, device=dev, seed=0)
+    dec = Qwen3Decoder(w, max_positions=64, max_new_tokens=4, device=dev)
+    dec.h.normal_()
+    for _ in range(2):
+        for i in range(QWEN3_8B.layers):
+            kernels.q4k_rmsnorm_swiglu(dec.h, w.norms[f"layers.{i}.post_norm"], w.packed[f"layers.{i}.gate"],
+                                       w.packed[f"layers.{i}.up"], dec.act)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print("[bench] profile-kernel target done", file=sys.stderr, flush=True)
+    return 0
 
 
 def main() -> int:
@@ -48,6 +82,8 @@ def main() -> int:
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build is single-GPU); got --gpus {args.gpus}", file=sys.stderr)
         return 2
+    if args.profile_kernel:
+        return profile_kernel_target()
     import torch
 
     from torch2vk_amd import kernels
@@ -135,7 +171,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(TRAFFIC_PROFILE) if args.model == "8b" else None,
+            "traffic_source": TRAFFIC_PROFILE.name if args.model == "8b" else None,
             "bytes_per_launch": dom["bytes"],
             "avg_launch_us": round(dom["us"], 3),
         },
@@ -147,59 +184,75 @@ def main() -> int:
     return 0
 
 
-def kernel_timing(dec, weights, reps: int) -> dict:
-    """Per-launch HIP-event timing of each decode kernel class, sweeping all layers' weights."""
+def _graph_us_per_call(calls, reps: int) -> float:
+    """Average duration of one call in `calls` when they run back to back inside a HIP graph, the way
+    the decode step runs them.  Timed with HIP events on the stream the graph is replayed on."""
     import torch
 
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):                      # warm outside capture
+        for f in calls:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for f in calls:
+            f()
+    stream = torch.cuda.current_stream()
+    graph.replay()
+    stream.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    end.record(stream)
+    end.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / (reps * len(calls))
+    del graph
+    return us
+
+
+def kernel_timing(dec, weights, reps: int) -> dict:
+    """Per-launch timing of each decode kernel class: each class's launches over all layers' weights
+    captured in one HIP graph (as in the decode step, so launch gaps match it) and replayed `reps` times."""
     from torch2vk_amd import kernels
 
     c = dec.config
-    stream = torch.cuda.current_stream()
     L = c.layers
-    # bytes per launch (algorithmic: packed weights + activations read + outputs written)
-    wb = lambda n: weights.packed[n].numel()  # noqa: E731
-    classes = {
-        "qkv_rmsnorm_gemv": (lambda i: kernels.q4k_matvec_multi(
-            dec.h, [weights.packed[f"layers.{i}.q"], weights.packed[f"layers.{i}.k"], weights.packed[f"layers.{i}.v"]],
-            [dec.q, dec.k, dec.v], norm_weight=weights.norms[f"layers.{i}.input_norm"]),
-            lambda i: wb(f"layers.{i}.q") + wb(f"layers.{i}.k") + wb(f"layers.{i}.v") + c.hidden * 8
-            + (c.q_dim + 2 * c.kv_dim) * 4),
-        "attn_decode": (lambda i: kernels.attn_decode(
-            dec.q, dec.k, dec.v, dec.k_cache[i], dec.v_cache[i], dec.attn, dec.position, dec.attn_ws,
-            q_norm_weight=weights.norms[f"layers.{i}.q_norm"], k_norm_weight=weights.norms[f"layers.{i}.k_norm"],
-            theta=c.rope_theta),
-            lambda i: None),
-        "o_gemv_residual": (lambda i: kernels.q4k_matvec(dec.attn, weights.packed[f"layers.{i}.o"], out=dec.h,
-                                                         residual=dec.h),
-                            lambda i: wb(f"layers.{i}.o") + c.q_dim * 2 + c.hidden * 8),
-        "gate_up_rmsnorm_swiglu_gemv": (lambda i: kernels.q4k_rmsnorm_swiglu(
-            dec.h, weights.norms[f"layers.{i}.post_norm"], weights.packed[f"layers.{i}.gate"],
-            weights.packed[f"layers.{i}.up"], dec.act),
-            lambda i: wb(f"layers.{i}.gate") + wb(f"layers.{i}.up") + c.hidden * 8 + c.mlp * 2),
-        "down_gemv_residual": (lambda i: kernels.q4k_matvec(dec.act, weights.packed[f"layers.{i}.down"], out=dec.h,
-                                                            residual=dec.h),
-                               lambda i: wb(f"layers.{i}.down") + c.mlp * 2 + c.hidden * 8),
-    }
+    P, N = weights.packed, weights.norms
+    wb = lambda n: P[n].numel()  # noqa: E731
     pos = int(dec.position.item())
     kv_len = min(pos + 1, dec.max_positions)
-    attn_bytes = 2 * kv_len * c.kv_dim * 2 + (c.q_dim + 2 * c.kv_dim) * 4 + c.q_dim * 2
+    # algorithmic bytes per launch: packed weights + activations read + outputs written
+    classes = {
+        "qkv_rmsnorm_gemv": (
+            lambda i: kernels.q4k_matvec_multi(dec.h, [P[f"layers.{i}.q"], P[f"layers.{i}.k"], P[f"layers.{i}.v"]],
+                                               [dec.q, dec.k, dec.v], norm_weight=N[f"layers.{i}.input_norm"]),
+            lambda i: wb(f"layers.{i}.q") + wb(f"layers.{i}.k") + wb(f"layers.{i}.v") + c.hidden * 8
+            + (c.q_dim + 2 * c.kv_dim) * 4),
+        "attn_decode": (
+            lambda i: kernels.attn_decode(dec.q, dec.k, dec.v, dec.k_cache[i], dec.v_cache[i], dec.attn, dec.position,
+                                          dec.attn_ws, q_norm_weight=N[f"layers.{i}.q_norm"],
+                                          k_norm_weight=N[f"layers.{i}.k_norm"], theta=c.rope_theta),
+            lambda i: 2 * kv_len * c.kv_dim * 2 + (c.q_dim + 2 * c.kv_dim) * 4 + c.q_dim * 2),
+        "o_gemv_residual": (
+            lambda i: kernels.q4k_matvec(dec.attn, P[f"layers.{i}.o"], out=dec.h, residual=dec.h),
+            lambda i: wb(f"layers.{i}.o") + c.q_dim * 2 + c.hidden * 8),
+        "gate_up_rmsnorm_swiglu_gemv": (
+            lambda i: kernels.q4k_rmsnorm_swiglu(dec.h, N[f"layers.{i}.post_norm"], P[f"layers.{i}.gate"],
+                                                 P[f"layers.{i}.up"], dec.act),
+            lambda i: wb(f"layers.{i}.gate") + wb(f"layers.{i}.up") + c.hidden * 8 + c.mlp * 2),
+        "down_gemv_residual": (
+            lambda i: kernels.q4k_matvec(dec.act, P[f"layers.{i}.down"], out=dec.h, residual=dec.h),
+            lambda i: wb(f"layers.{i}.down") + c.mlp * 2 + c.hidden * 8),
+    }
     per_launch_us, gbs, bytes_per = {}, {}, {}
-    total_us = 0.0
-    q_bytes = 0.0
-    q_us = 0.0
+    total_us = q_bytes = q_us = 0.0
     for name, (fn, nbytes) in classes.items():
-        for i in range(L):  # warm
-            fn(i)
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(reps):
-            for i in range(L):
-                fn(i)
-        end.record(stream)
-        end.synchronize()
-        us = start.elapsed_time(end) * 1000.0 / (reps * L)
-        b = attn_bytes if name == "attn_decode" else sum(nbytes(i) for i in range(L)) / L
+        us = _graph_us_per_call([lambda i=i: fn(i) for i in range(L)], reps)
+        b = sum(nbytes(i) for i in range(L)) / L
         per_launch_us[name] = round(us, 3)
         bytes_per[name] = int(b)
         gbs[name] = b / (us * 1e-6) / 1e9
@@ -207,22 +260,15 @@ def kernel_timing(dec, weights, reps: int) -> dict:
         if name != "attn_decode":
             q_bytes += b * L
             q_us += us * L
-    # LM head (fused final norm + GEMV + argmax) and the select
-    lm = lambda: kernels.q4k_lm_head_argmax_partial(dec.h, weights.packed["lm_head"], dec.partial_scores,  # noqa: E731
-                                                   dec.partial_tokens, norm_weight=weights.norms["norm"])
-    lm()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(reps):
-        lm()
-    end.record(stream)
-    end.synchronize()
-    us = start.elapsed_time(end) * 1000.0 / reps
-    b = weights.packed["lm_head"].numel() + c.hidden * 8 + dec.partial_scores.numel() * 8
-    per_launch_us["lm_head_rmsnorm_argmax_gemv"] = round(us, 3)
-    bytes_per["lm_head_rmsnorm_argmax_gemv"] = int(b)
-    gbs["lm_head_rmsnorm_argmax_gemv"] = b / (us * 1e-6) / 1e9
+    # LM head (fused final norm + GEMV + per-block argmax)
+    name = "lm_head_rmsnorm_argmax_gemv"
+    us = _graph_us_per_call([lambda: kernels.q4k_lm_head_argmax_partial(dec.h, P["lm_head"], dec.partial_scores,
+                                                                        dec.partial_tokens, norm_weight=N["norm"])] * 4,
+                            reps)
+    b = wb("lm_head") + c.hidden * 8 + dec.partial_scores.numel() * 8
+    per_launch_us[name] = round(us, 3)
+    bytes_per[name] = int(b)
+    gbs[name] = b / (us * 1e-6) / 1e9
     total_us += us
     q_bytes += b
     q_us += us
@@ -236,6 +282,17 @@ def kernel_timing(dec, weights, reps: int) -> dict:
         "dominant": {"kernel": dominant, "us": per_launch_us[dominant], "bytes": bytes_per[dominant],
                      "gbs": gbs[dominant]},
     }
+
+
+def profiled_traffic(profile: Path) -> int | None:
+    """HBM bytes per launch of the dominant kernel, from the committed counter summary (two
+    rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by a 256 MiB copy's readings)."""
+    try:
+        text = profile.read_text()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def cpu_baseline(cfg, weights, positions: int, steps: int) -> dict:

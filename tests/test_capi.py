@@ -1,0 +1,83 @@
+"""The C ABI library on the CPU: it loads, exports every declared symbol, and rejects bad arguments
+before any launch (no GPU is touched: every call here returns from host-side validation)."""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+
+import pytest
+
+from torch2vk_amd import _lib
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libt2h.so not built")
+    return _lib.lib()
+
+
+def test_exports_every_declared_symbol(lib):
+    declared = _lib.declared_symbols()
+    assert len(declared) >= 15
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [s for s in declared if s not in exported]
+    assert not missing, f"declared in include/t2h.h but not exported: {missing}"
+    # and the Python binding covers every entry point
+    assert set(declared) <= set(_lib.SIGNATURES), set(declared) - set(_lib.SIGNATURES)
+
+
+def test_status_strings(lib):
+    assert lib.t2h_abi_version() == 1
+    assert lib.t2h_status_string(0) == b"ok"
+    assert b"null" in lib.t2h_status_string(1)
+    assert lib.t2h_status_string(1000 + 1) == b"HIP launch error"
+
+
+def test_argument_validation_returns_status(lib):
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    # null pointers
+    assert lib.t2h_q4k_matvec(None, fake, fake, 0, None, 1, 4096, 16, None) == 1
+    assert lib.t2h_quantize_q4_k(None, 4, 256, fake, None) == 1
+    # K not a multiple of 256
+    assert lib.t2h_q4k_matvec(fake, fake, fake, 0, None, 1, 1000, 16, None) == 2
+    assert lib.t2h_quantize_q4_k(fake, 4, 300, fake, None) == 2
+    assert lib.t2h_quantize_q8_0(fake, 4, 33, fake, None) == 2
+    # K a multiple of 256 but not built (NSB 5)
+    assert lib.t2h_q4k_matvec(fake, fake, fake, 0, None, 1, 1280, 16, None) == 4
+    # N not a multiple of the row group (K=256 -> 16 rows per group)
+    assert lib.t2h_q4k_matvec(fake, fake, fake, 0, None, 1, 256, 10, None) == 2
+    # bad dtype combination: bf16 output with a residual
+    assert lib.t2h_q4k_matvec(fake, fake, fake, 1, fake, 1, 4096, 16, None) == 3
+    # attention: head_dim other than 128, GQA not dividing, too-small workspace
+    assert lib.t2h_attn_decode(fake, fake, fake, None, None, 1e-6, 0.0, fake, fake, fake, 32, 8, 64, 64, fake, fake,
+                               1 << 20, None) == 4
+    assert lib.t2h_attn_decode(fake, fake, fake, None, None, 1e-6, 0.0, fake, fake, fake, 30, 8, 128, 64, fake, fake,
+                               1 << 20, None) == 2
+    assert lib.t2h_attn_decode(fake, fake, fake, None, None, 1e-6, 0.0, fake, fake, fake, 32, 8, 128, 4096, fake, fake,
+                               16, None) == 6
+    # workspace sizing is pure host arithmetic
+    assert lib.t2h_attn_decode_workspace_bytes(32, 8, 128, 4352) > 0
+    assert lib.t2h_attn_decode_workspace_bytes(32, 8, 64, 4352) == 0
+    assert lib.t2h_set_gemv_max_blocks(0, 0) == 5
+
+
+def test_python_wrappers_reject_host_tensors():
+    import torch
+
+    from torch2vk_amd import kernels
+
+    with pytest.raises(ValueError, match="HIP device"):
+        kernels.quantize(torch.zeros(4, 256), "q4_k")
+    with pytest.raises(ValueError, match="HIP device"):
+        kernels.q4k_matvec(torch.zeros(256, dtype=torch.bfloat16), torch.zeros(16, 144, dtype=torch.uint8))
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libt2h.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.lib()
