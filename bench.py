@@ -28,6 +28,7 @@ import time
 from pathlib import Path
 
 HBM_PEAK_GBS = 8000.0
+HEADLINE_METRIC = "Qwen3-8B-shape int4 decode tok/s @bs1; q-matmul HBM GB/s vs ~8 TB/s peak"
 TRAFFIC_PROFILE = Path(__file__).resolve().parent / "profiles" / "gate_up_gemv_qwen3_8b_pmc.md"
 PROMPT_POSITIONS = 4096
 
@@ -39,6 +40,8 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=16)
     p.add_argument("--steps-per-graph", type=int, default=8)
     p.add_argument("--model", choices=("8b", "0.6b"), default="8b")
+    p.add_argument("--policy", choices=("uniform", "q4_k_m"), default="uniform",
+                   help="weight types: uniform Q4_K (the headline int4 config) or the Q4_K_M mix")
     p.add_argument("--positions", type=int, default=PROMPT_POSITIONS, help="KV positions prefilled before timing")
     p.add_argument("--kernel-reps", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -97,7 +100,7 @@ def main() -> int:
     dev = torch.device("cuda:0")
     cfg = QWEN3_8B if args.model == "8b" else QWEN3_0_6B
     t_setup = time.time()
-    weights = synthetic_weights(cfg, device=dev, seed=0)
+    weights = synthetic_weights(cfg, device=dev, seed=0, policy=args.policy)
     total_steps = args.warmup + args.steps + args.steps_per_graph
     s_cap = args.positions + total_steps + 64
     dec = Qwen3Decoder(weights, max_positions=s_cap, max_new_tokens=total_steps + 8, device=dev)
@@ -142,8 +145,10 @@ def main() -> int:
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
 
     dom = kern["dominant"]
+    headline = args.model == "8b" and args.policy == "uniform"
+    policy_text = "Q4_K uniform int4" if args.policy == "uniform" else "Q4_K_M (Q4_K + Q6_K)"
     line = {
-        "metric": "Qwen3-8B-shape int4 decode tok/s @bs1" if args.model == "8b" else "Qwen3-0.6B int4 decode tok/s @bs1",
+        "metric": HEADLINE_METRIC if headline else f"Qwen3-{args.model.upper()}-shape {args.policy} decode tok/s @bs1",
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -154,15 +159,15 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,0.02) weights quantized to Q4_K on the GPU; KV cache N(0,1))",
+        "data": f"synthetic (seeded N(0,0.02) weights quantized on the GPU, {policy_text}; KV cache N(0,1))",
         "config": {
-            "workload": f"{cfg.name} int4 (Q4_K, uniform) greedy decode, batch 1, KV prefilled to "
-                        f"{args.positions}, {args.steps} timed steps, HIP graphs of {spg} steps"
-                        if use_graph else "eager launches",
-            "model": cfg.name,
-            "global_batch": 1,
-            "seq_len": args.positions,
-            "parallelism": "single GPU",
+            "workload": f"{cfg.name}-shape {policy_text} greedy decode, batch 1, KV prefilled to "
+                        f"{args.positions} positions, {args.steps} timed steps"
+                        + (f", HIP graphs of {spg} steps" if use_graph else ", eager launches"),
+            "weights": args.policy,
+            "kv_positions": args.positions,
+            "batch": 1,
+            "graph_steps": spg if use_graph else 0,
         },
         "roofline": {
             "bound": "hbm",
@@ -171,8 +176,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": profiled_traffic(TRAFFIC_PROFILE) if args.model == "8b" else None,
-            "traffic_source": TRAFFIC_PROFILE.name if args.model == "8b" else None,
+            "traffic": profiled_traffic(TRAFFIC_PROFILE) if headline else None,
+            "traffic_source": TRAFFIC_PROFILE.name if headline else None,
             "bytes_per_launch": dom["bytes"],
             "avg_launch_us": round(dom["us"], 3),
         },
@@ -217,35 +222,29 @@ def _graph_us_per_call(calls, reps: int) -> float:
 def kernel_timing(dec, weights, reps: int) -> dict:
     """Per-launch timing of each decode kernel class: each class's launches over all layers' weights
     captured in one HIP graph (as in the decode step, so launch gaps match it) and replayed `reps` times."""
-    from torch2vk_amd import kernels
-
     c = dec.config
     L = c.layers
-    P, N = weights.packed, weights.norms
-    wb = lambda n: P[n].numel()  # noqa: E731
+    wb = lambda n: weights.packed[n].numel()  # noqa: E731
     pos = int(dec.position.item())
     kv_len = min(pos + 1, dec.max_positions)
-    # algorithmic bytes per launch: packed weights + activations read + outputs written
+    # algorithmic bytes per launch: packed weights + activations read + outputs written.  Each class
+    # runs through the decoder's own sub-step, so the GEMV of each tensor's type is the one timed.
     classes = {
         "qkv_rmsnorm_gemv": (
-            lambda i: kernels.q4k_matvec_multi(dec.h, [P[f"layers.{i}.q"], P[f"layers.{i}.k"], P[f"layers.{i}.v"]],
-                                               [dec.q, dec.k, dec.v], norm_weight=N[f"layers.{i}.input_norm"]),
+            dec._qkv,
             lambda i: wb(f"layers.{i}.q") + wb(f"layers.{i}.k") + wb(f"layers.{i}.v") + c.hidden * 8
             + (c.q_dim + 2 * c.kv_dim) * 4),
         "attn_decode": (
-            lambda i: kernels.attn_decode(dec.q, dec.k, dec.v, dec.k_cache[i], dec.v_cache[i], dec.attn, dec.position,
-                                          dec.attn_ws, q_norm_weight=N[f"layers.{i}.q_norm"],
-                                          k_norm_weight=N[f"layers.{i}.k_norm"], theta=c.rope_theta),
+            dec._attention,
             lambda i: 2 * kv_len * c.kv_dim * 2 + (c.q_dim + 2 * c.kv_dim) * 4 + c.q_dim * 2),
         "o_gemv_residual": (
-            lambda i: kernels.q4k_matvec(dec.attn, P[f"layers.{i}.o"], out=dec.h, residual=dec.h),
+            lambda i: dec._linear_residual(dec.attn, f"layers.{i}.o"),
             lambda i: wb(f"layers.{i}.o") + c.q_dim * 2 + c.hidden * 8),
         "gate_up_rmsnorm_swiglu_gemv": (
-            lambda i: kernels.q4k_rmsnorm_swiglu(dec.h, N[f"layers.{i}.post_norm"], P[f"layers.{i}.gate"],
-                                                 P[f"layers.{i}.up"], dec.act),
+            dec._gate_up,
             lambda i: wb(f"layers.{i}.gate") + wb(f"layers.{i}.up") + c.hidden * 8 + c.mlp * 2),
         "down_gemv_residual": (
-            lambda i: kernels.q4k_matvec(dec.act, P[f"layers.{i}.down"], out=dec.h, residual=dec.h),
+            lambda i: dec._linear_residual(dec.act, f"layers.{i}.down"),
             lambda i: wb(f"layers.{i}.down") + c.mlp * 2 + c.hidden * 8),
     }
     per_launch_us, gbs, bytes_per = {}, {}, {}
@@ -262,9 +261,7 @@ def kernel_timing(dec, weights, reps: int) -> dict:
             q_us += us * L
     # LM head (fused final norm + GEMV + per-block argmax)
     name = "lm_head_rmsnorm_argmax_gemv"
-    us = _graph_us_per_call([lambda: kernels.q4k_lm_head_argmax_partial(dec.h, P["lm_head"], dec.partial_scores,
-                                                                        dec.partial_tokens, norm_weight=N["norm"])] * 4,
-                            reps)
+    us = _graph_us_per_call([dec._lm_head] * 4, reps)
     b = wb("lm_head") + c.hidden * 8 + dec.partial_scores.numel() * 8
     per_launch_us[name] = round(us, 3)
     bytes_per[name] = int(b)
@@ -310,12 +307,14 @@ def cpu_baseline(cfg, weights, positions: int, steps: int) -> dict:
     for name in ("q", "k", "v", "o", "gate", "up", "down"):
         packed = weights.packed[f"layers.0.{name}"].cpu().numpy()
         k = c.hidden if name != "o" and name != "down" else (c.q_dim if name == "o" else c.mlp)
-        dense[f"layers.0.{name}"] = torch.from_numpy(oracle.dequant_q4_k(packed, k))
+        dense[f"layers.0.{name}"] = torch.from_numpy(getattr(oracle, f"dequant_{weights.types[f'layers.0.{name}']}")(
+            packed, k))
     for name in ("input_norm", "post_norm", "q_norm", "k_norm"):
         dense[f"layers.0.{name}"] = weights.norms[f"layers.0.{name}"].cpu()
     dense["norm"] = weights.norms["norm"].cpu()
     dense["embed"] = torch.zeros(8, c.hidden)
-    lm = torch.from_numpy(oracle.dequant_q4_k(weights.packed["lm_head"].cpu().numpy(), c.hidden))
+    lm = torch.from_numpy(getattr(oracle, f"dequant_{weights.types['lm_head']}")(
+        weights.packed["lm_head"].cpu().numpy(), c.hidden))
     dense["lm_head"] = lm
     shape = Qwen3Shape(hidden=c.hidden, layers=1, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
                        mlp=c.mlp, vocab=c.vocab, rope_theta=c.rope_theta)

@@ -93,9 +93,37 @@ int t2h_q4k_lm_head_argmax_partial(const void* x, const float* norm_w, float eps
                                    uint32_t n, float* partial_scores, uint32_t* partial_tokens,
                                    uint32_t num_partials, void* stream);
 
-/* Grid caps of the GEMV launches, in blocks of 4 waves (tuning knob, process-wide):
- * max_blocks for plain bf16 x (default 1024), max_blocks_norm for the fused
- * RMSNorm prologue (default 512; 0 = same as max_blocks). */
+/* Q6_K GEMV: y[m, n] = x[m, k] . deq(W)^T (+ residual), x bf16, k % 256 == 0,
+ * k <= 12288 (longer rows: T2H_ERR_UNSUPPORTED).
+ * replaces LINEAR_NOBIAS_Q6_K_MATVEC_F32 (src/models/quantized_qwen3/shaders/linear_nobias_q6_k_matvec_f32.py:20-193)
+ * and, with residual, LINEAR_NOBIAS_Q6_K_MATVEC_ADD_F32
+ * (src/models/optimized_qwen3/shaders/linear_nobias_q6_k_matvec_add_f32.py:23-100). */
+int t2h_q6k_matvec(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                   uint32_t k, uint32_t n, void* stream);
+
+/* Q6_K GEMV of RMSNorm(h)*norm_w for one token (h fp32 residual stream):
+ * the v_proj of the Q4_K_M "more bits" layers.
+ * replaces RMS_NORM_MUL_F16_F32 + the Q6_K part of LINEAR_NOBIAS_Q4_QK_Q6_V_MATVEC_F32
+ * (src/models/optimized_qwen3/shaders/linear_nobias_q4_qk_q6_v_matvec_f32.py:103-160). */
+int t2h_q6k_rmsnorm_matvec(const float* h, const float* norm_w, float eps, const void* w, void* y, int out_dtype,
+                           uint32_t k, uint32_t n, void* stream);
+
+/* Q8_0 GEMV: y[m, n] = x[m, k] . deq(W)^T (+ residual), x bf16 (converted to
+ * fp16 in-kernel, the reference's activation type), k % 32 == 0, k <= 12288.
+ * replaces LINEAR_NOBIAS_Q8_0_MATVEC_F32 (src/models/quantized_qwen3/shaders/linear_nobias_q8_0_matvec_f32.py:24-119). */
+int t2h_q8_0_matvec(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                    uint32_t k, uint32_t n, void* stream);
+
+/* Q6_K LM head + per-block argmax, as t2h_q4k_lm_head_argmax_partial.
+ * replaces LM_HEAD_Q6_K_ARGMAX_PARTIAL_F16 (src/torch2vk/export/shaders/lm_head_q6_k_argmax_partial_f16.py:24-209). */
+int t2h_q6k_lm_head_argmax_partial(const void* x, const float* norm_w, float eps, const void* w, uint32_t k,
+                                   uint32_t n, float* partial_scores, uint32_t* partial_tokens,
+                                   uint32_t num_partials, void* stream);
+
+/* Grid caps of the GEMV launches, in blocks of 8 waves (tuning knob, process-wide):
+ * max_blocks for plain bf16 x (default 256), max_blocks_norm for the fused
+ * RMSNorm prologue (default 256; 0 = same as max_blocks).  No reference
+ * counterpart: the reference fixes its grids in the shader variants. */
 int t2h_set_gemv_max_blocks(uint32_t max_blocks, uint32_t max_blocks_norm);
 
 /* ---------------------------------------------------- token selection --- */

@@ -63,6 +63,16 @@ def test_argument_validation_returns_status(lib):
     assert lib.t2h_attn_decode_workspace_bytes(32, 8, 128, 4352) > 0
     assert lib.t2h_attn_decode_workspace_bytes(32, 8, 64, 4352) == 0
     assert lib.t2h_set_gemv_max_blocks(0, 0) == 5
+    # Q6_K / Q8_0 GEMV: K rule, rows too long or too short for the built geometries, row-group multiple
+    assert lib.t2h_q6k_matvec(fake, fake, fake, 0, None, 1, 1000, 16, None) == 2
+    assert lib.t2h_q6k_matvec(fake, fake, fake, 0, None, 1, 16384, 16, None) == 4
+    assert lib.t2h_q6k_matvec(fake, fake, fake, 0, None, 1, 256, 16, None) == 4
+    assert lib.t2h_q6k_matvec(fake, fake, fake, 0, None, 1, 1024, 6, None) == 2   # 4 rows per group at K=1024
+    assert lib.t2h_q8_0_matvec(fake, fake, fake, 0, None, 1, 48, 16, None) == 2
+    assert lib.t2h_q8_0_matvec(fake, fake, fake, 0, None, 1, 256, 16, None) == 4
+    assert lib.t2h_q8_0_matvec(None, fake, fake, 0, None, 1, 1024, 16, None) == 1
+    assert lib.t2h_q6k_rmsnorm_matvec(fake, None, 1e-6, fake, fake, 0, 1024, 16, None) == 1
+    assert lib.t2h_q6k_lm_head_argmax_partial(fake, None, 1e-6, fake, 4096, 100, fake, fake, 0, None) == 5
 
 
 def test_python_wrappers_reject_host_tensors():

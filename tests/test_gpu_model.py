@@ -12,10 +12,10 @@ from oracle.reference import Qwen3Shape
 pytestmark = pytest.mark.gpu
 
 
-def _setup(cfg, device, seed, std):
+def _setup(cfg, device, seed, std, policy="uniform"):
     from torch2vk_amd.qwen3.weights import matrix_shapes, synthetic_weights
 
-    w = synthetic_weights(cfg, device=device, seed=seed, std=std, norm_std=0.1)
+    w = synthetic_weights(cfg, device=device, seed=seed, std=std, norm_std=0.1, policy=policy)
     dense = dense_weights({k: v.cpu().numpy() for k, v in w.packed.items()}, w.types,
                           {k: v.cpu().numpy() for k, v in w.norms.items()}, matrix_shapes(cfg))
     shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
@@ -42,6 +42,25 @@ def test_tiny_decode_matches_oracle(device, use_graph):
     assert len(toks) == 13
     stats = check_greedy_tokens(shape, dense, prompt, toks)
     print(stats)
+
+
+def test_q4_k_m_decode_matches_oracle(device):
+    """Q4_K_M policy: Q6_K v/down on the more-bits layers and a Q6_K LM head, graph-replayed."""
+    from torch2vk_amd.qwen3.config import Qwen3Config, q4_k_m_more_bits_layer_indices
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg = Qwen3Config("tiny-m", hidden=1024, layers=4, heads=8, kv_heads=2, head_dim=128, mlp=1024, vocab=1024,
+                      eos_token_ids=(1023,))
+    w, dense, shape = _setup(cfg, device, seed=21, std=0.05, policy="q4_k_m")
+    more = q4_k_m_more_bits_layer_indices(cfg.layers)
+    assert w.types["lm_head"] == "q6_k" and 0 < len(more) < cfg.layers
+    assert {w.types[f"layers.{i}.down"] for i in range(cfg.layers)} == {"q4_k", "q6_k"}
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, 6).tolist()
+    dec = Qwen3Decoder(w, max_positions=64, max_new_tokens=16)
+    dec.stop_on_eos = False
+    toks = dec.generate(torch.tensor(prompt), 12, steps_per_graph=4, use_graph=True)
+    print(f"q4_k_m decode: {toks}", flush=True)
+    print(check_greedy_tokens(shape, dense, prompt, toks))
 
 
 def test_graph_replay_equals_eager(device):

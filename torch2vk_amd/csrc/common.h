@@ -60,6 +60,20 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits_rne(float value) {
     return sign | half;
 }
 
+// Two-element dot products accumulated in fp32 (v_dot2_f32_bf16 / v_dot2_f32_f16):
+// a and b each hold two 16-bit values, low half first.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                           false);
+}
+
+__device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+}
+
 // ------------------------------------------------------------- reductions --
 
 // DPP move of a float within 16-lane rows (ctrl: quad_perm / row_mirror ...).
@@ -124,6 +138,27 @@ __device__ __forceinline__ float2 load_nt_f2(const float* p) {
 }
 
 __device__ __forceinline__ uint4 load_u4(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Loads at 2-byte-aligned addresses (Q6_K blocks are 210 B and Q8_0 blocks
+// 34 B, so their fields are only halfword aligned).  Under the HSA ABI the
+// backend runs in unaligned-access mode and emits one global_load_dwordx4 /
+// dwordx2 for these; the memory pipeline splits the access where it crosses
+// a dword boundary.
+__device__ __forceinline__ uint4 load_u4_ua(const uint8_t* p) {
+    u32x4_t v;
+    __builtin_memcpy(&v, p, 16);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint2 load_u2_ua(const uint8_t* p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t load_u16(const uint8_t* p) {
+    return *reinterpret_cast<const unsigned short*>(p);
+}
 
 }  // namespace t2h
 

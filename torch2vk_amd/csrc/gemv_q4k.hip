@@ -51,13 +51,6 @@ struct Q4GemvArgs {
     float eps;
 };
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
-                                           false);
-}
-
 constexpr int cgcd(int a, int b) { return b == 0 ? a : cgcd(b, a % b); }
 
 constexpr int GEMV_THREADS = 512;  // 8 waves per block share one staged copy of x

@@ -183,8 +183,90 @@ def q4k_lm_head_argmax_partial(x: torch.Tensor, w: torch.Tensor, partial_scores:
          ptr(partial_tokens), g, stream_handle())
 
 
+_BLOCK = {"q4_k": (256, Q4_K_BYTES), "q6_k": (256, Q6_K_BYTES), "q8_0": (32, Q8_0_BYTES)}
+
+
+def row_bytes(wtype: str, k: int) -> int:
+    values, nbytes = _BLOCK[wtype]
+    if k % values:
+        raise ValueError(f"{wtype} needs K % {values} == 0, got {k}")
+    return k // values * nbytes
+
+
+def _check_packed(w: torch.Tensor, name: str, wtype: str, k: int) -> int:
+    _check(w, name, torch.uint8)
+    rb = row_bytes(wtype, k)
+    if w.dim() != 2 or w.shape[1] != rb:
+        raise ValueError(f"{name} must be uint8 [N, {rb}] ({wtype}, K={k}), got {tuple(w.shape)}")
+    return int(w.shape[0])
+
+
+def qx_matvec(x: torch.Tensor, w: torch.Tensor, wtype: str, *, out: torch.Tensor | None = None,
+              out_dtype: torch.dtype = torch.float32, residual: torch.Tensor | None = None,
+              norm_weight: torch.Tensor | None = None, eps: float = RMS_EPS) -> torch.Tensor:
+    """Q6_K / Q8_0 GEMV: y[M, N] = x[M, K] . deq(W)^T (+ residual).  x bf16, or (Q6_K with
+    norm_weight) the fp32 residual stream [K] normalised in-kernel."""
+    if wtype not in ("q6_k", "q8_0"):
+        raise ValueError(f"qx_matvec handles q6_k and q8_0, got {wtype!r}")
+    if norm_weight is None:
+        _check(x, "x", torch.bfloat16)
+    else:
+        if wtype != "q6_k" or residual is not None:
+            raise ValueError("the fused RMSNorm prologue is built for Q6_K without residual")
+        _check(x, "x", torch.float32)
+        _check(norm_weight, "norm_weight", torch.float32)
+        if norm_weight.numel() != x.numel():
+            raise ValueError("norm_weight must have K elements")
+    k = int(x.shape[-1])
+    m = x.numel() // k
+    if norm_weight is not None and m != 1:
+        raise ValueError("the fused RMSNorm prologue takes one token")
+    n = _check_packed(w, "weight", wtype, k)
+    if out is None:
+        out = torch.empty(*x.shape[:-1], n, dtype=out_dtype, device=x.device)
+    _check(out, "output", tuple(_OUT_DTYPES), align=4)
+    if out.numel() != m * n:
+        raise ValueError(f"output has {out.numel()} elements, expected {m * n}")
+    if residual is not None:
+        _check(residual, "residual", torch.float32, align=4)
+        if residual.numel() != m * n or out.dtype != torch.float32:
+            raise ValueError("residual must be fp32 with the output's shape; output must be fp32")
+    if norm_weight is not None:
+        call("t2h_q6k_rmsnorm_matvec", ptr(x), ptr(norm_weight), eps, ptr(w), ptr(out), _OUT_DTYPES[out.dtype],
+             k, n, stream_handle())
+    else:
+        name = "t2h_q6k_matvec" if wtype == "q6_k" else "t2h_q8_0_matvec"
+        call(name, ptr(x), ptr(w), ptr(out), _OUT_DTYPES[out.dtype], ptr(residual), m, k, n, stream_handle())
+    return out
+
+
+def lm_head_argmax_partial(x: torch.Tensor, w: torch.Tensor, wtype: str, partial_scores: torch.Tensor,
+                           partial_tokens: torch.Tensor, *, norm_weight: torch.Tensor | None = None,
+                           eps: float = RMS_EPS) -> None:
+    """LM head GEMV + per-block argmax for a Q4_K or Q6_K head (logits never materialised)."""
+    if wtype == "q4_k":
+        q4k_lm_head_argmax_partial(x, w, partial_scores, partial_tokens, norm_weight=norm_weight, eps=eps)
+        return
+    if wtype != "q6_k":
+        raise ValueError(f"LM head argmax is built for q4_k and q6_k, got {wtype!r}")
+    if norm_weight is None:
+        _check(x, "x", torch.bfloat16)
+    else:
+        _check(x, "x", torch.float32)
+        _check(norm_weight, "norm_weight", torch.float32)
+    k = int(x.numel())
+    n = _check_packed(w, "weight", "q6_k", k)
+    _check(partial_scores, "partial_scores", torch.float32, align=4)
+    _check(partial_tokens, "partial_tokens", torch.int32, align=4)
+    g = int(partial_scores.numel())
+    if partial_tokens.numel() != g or g == 0:
+        raise ValueError("partial_scores and partial_tokens must have the same non-zero length")
+    call("t2h_q6k_lm_head_argmax_partial", ptr(x), ptr(norm_weight), eps, ptr(w), k, n, ptr(partial_scores),
+         ptr(partial_tokens), g, stream_handle())
+
+
 def set_gemv_max_blocks(max_blocks: int, max_blocks_norm: int = 0) -> None:
-    """Grid caps (blocks of 4 waves) for plain and RMSNorm-prologue GEMV launches."""
+    """Grid caps (blocks of 8 waves) for plain and RMSNorm-prologue Q4_K GEMV launches."""
     call("t2h_set_gemv_max_blocks", int(max_blocks), int(max_blocks_norm))
 
 

@@ -3,15 +3,20 @@
 One decode step (src/models/optimized_qwen3/run.py:142-172) is, per token:
 
     embed                                   1 launch   (EMBEDDING_Q4_K_F32)
-    per layer                               5 launches:
-      RMSNorm + Q|K|V GEMV                  (RMS_NORM_MUL + LINEAR_NOBIAS_Q4_K_QKV_MATVEC)
-      q/k-norm + RoPE + KV write + attention (RMS_NORM_ROPE_TRANSPOSE x2 + SDPA_DECODE_CACHE_WRITE)
-      o_proj GEMV + residual                (LINEAR_NOBIAS_Q4_K_MATVEC_ADD)
+    per layer                               5 launches (6 with a Q6_K v_proj):
+      RMSNorm + Q|K|V GEMV                  (RMS_NORM_MUL + LINEAR_NOBIAS_Q4_K_QKV_MATVEC, or
+                                             LINEAR_NOBIAS_Q4_QK_Q6_V_MATVEC as Q4_K q|k + Q6_K v)
+      q/k-norm + RoPE + KV write + attention (RMS_NORM_ROPE_TRANSPOSE x2 + SDPA_DECODE_CACHE_WRITE;
+                                             a split-K pass and a merge pass)
+      o_proj GEMV + residual                (LINEAR_NOBIAS_Q4_K_MATVEC_ADD / _Q6_K_)
       RMSNorm + gate|up GEMV + SwiGLU       (RMS_NORM_MUL + LINEAR_NOBIAS_Q4_K_QK_MATVEC + SWIGLU)
-      down GEMV + residual                  (LINEAR_NOBIAS_Q4_K_MATVEC_ADD)
-    final RMSNorm + LM head + argmax        1 launch   (run_decode_norm + LM_HEAD_*_ARGMAX_PARTIAL)
-    token select + EOS                      1 launch   (QWEN3_TOKEN_SELECT_REDUCE_{CHUNKS_,}F32)
-    token store + position advance          1 launch   (QWEN3_TOKEN_STORE_EOS_F32)
+      down GEMV + residual                  (LINEAR_NOBIAS_Q4_K_MATVEC_ADD / _Q6_K_)
+    final RMSNorm + LM head + argmax        1 launch   (run_decode_norm + LM_HEAD_{Q4_K,Q6_K}_ARGMAX_PARTIAL)
+    token select + store + advance          1 launch   (QWEN3_TOKEN_SELECT_REDUCE_* + QWEN3_TOKEN_STORE_EOS)
+
+Weights are Q4_K (uniform int4) or follow the Q4_K_M policy (Q6_K for v/down
+on the more-bits layers and for the LM head); each linear runs the GEMV of
+its own type.
 
 The reference runs 10 dispatches per layer and waits on the host every token
 (src/torch2vk/runtime/replay.py:260-261).  Here every dynamic scalar (cache
@@ -34,14 +39,27 @@ from torch2vk_amd.qwen3.weights import Qwen3Weights
 LM_HEAD_PARTIALS = 512
 
 
+def _check_types(c: Qwen3Config, types: dict[str, str]) -> None:
+    """The decode path runs Q4_K everywhere and Q6_K where the Q4_K_M policy puts it (v, down,
+    lm_head); anything else has no decode kernel here and is refused up front."""
+    allowed = {"embed": ("q4_k",), "lm_head": ("q4_k", "q6_k")}
+    for i in range(c.layers):
+        for n in ("q", "k", "gate", "up"):
+            allowed[f"layers.{i}.{n}"] = ("q4_k",)
+        for n in ("v", "o", "down"):
+            allowed[f"layers.{i}.{n}"] = ("q4_k", "q6_k")
+    for name, t in types.items():
+        if name in allowed and t not in allowed[name]:
+            raise NotImplementedError(f"{name}: no {t} decode kernel (built: {allowed[name]})")
+
+
 class Qwen3Decoder:
     def __init__(self, weights: Qwen3Weights, *, max_positions: int, max_new_tokens: int, device=None) -> None:
         c = weights.config
         self.config: Qwen3Config = c
         self.weights = weights
-        for name, t in weights.types.items():
-            if t != "q4_k":
-                raise NotImplementedError(f"{name}: {t} decode GEMV is not built yet (uniform Q4_K only)")
+        self.types = dict(weights.types)
+        _check_types(c, self.types)
         dev = torch.device(device) if device is not None else weights.packed["embed"].device
         self.device = dev
         self.max_positions = max_positions
@@ -94,25 +112,53 @@ class Qwen3Decoder:
         """One decoder layer at the device-resident position
         (run_decode_layer, src/models/optimized_qwen3/dispatch/decode_layer.py:131-136).
         A Python ``cache_position`` is written to the device counter first."""
-        c = self.config
         if cache_position is not None:
             self.position.fill_(cache_position)
         p = f"layers.{layer_idx}."
-        kernels.q4k_matvec_multi(self.h, [self._w(p + "q"), self._w(p + "k"), self._w(p + "v")],
-                                 [self.q, self.k, self.v], norm_weight=self._n(p + "input_norm"), eps=c.rms_eps)
+        self._qkv(layer_idx)
+        self._attention(layer_idx)
+        self._linear_residual(self.attn, p + "o")
+        self._gate_up(layer_idx)
+        self._linear_residual(self.act, p + "down")
+
+    def _qkv(self, layer_idx: int) -> None:
+        """RMSNorm + Q|K|V.  The Q4_K parts share one launch; a Q6_K v (Q4_K_M more-bits layers) runs
+        its own RMSNorm-prologue GEMV (the reference fuses it as LINEAR_NOBIAS_Q4_QK_Q6_V_MATVEC_F32)."""
+        c, t, p = self.config, self.types, f"layers.{layer_idx}."
+        q4 = [(n, o) for n, o in (("q", self.q), ("k", self.k), ("v", self.v)) if t[p + n] == "q4_k"]
+        kernels.q4k_matvec_multi(self.h, [self._w(p + n) for n, _ in q4], [o for _, o in q4],
+                                 norm_weight=self._n(p + "input_norm"), eps=c.rms_eps)
+        if t[p + "v"] == "q6_k":
+            kernels.qx_matvec(self.h, self._w(p + "v"), "q6_k", out=self.v, norm_weight=self._n(p + "input_norm"),
+                              eps=c.rms_eps)
+
+    def _attention(self, layer_idx: int) -> None:
+        c, p = self.config, f"layers.{layer_idx}."
         kernels.attn_decode(self.q, self.k, self.v, self.k_cache[layer_idx], self.v_cache[layer_idx], self.attn,
                             self.position, self.attn_ws, q_norm_weight=self._n(p + "q_norm"),
                             k_norm_weight=self._n(p + "k_norm"), theta=c.rope_theta, eps=c.rms_eps)
-        kernels.q4k_matvec(self.attn, self._w(p + "o"), out=self.h, residual=self.h)
+
+    def _gate_up(self, layer_idx: int) -> None:
+        p = f"layers.{layer_idx}."
         kernels.q4k_rmsnorm_swiglu(self.h, self._n(p + "post_norm"), self._w(p + "gate"), self._w(p + "up"),
-                                   self.act, eps=c.rms_eps)
-        kernels.q4k_matvec(self.act, self._w(p + "down"), out=self.h, residual=self.h)
+                                   self.act, eps=self.config.rms_eps)
+
+    def _linear_residual(self, x: torch.Tensor, name: str) -> None:
+        """h += x . deq(W)^T with the GEMV of W's type (_linear_q4_or_q6,
+        src/models/optimized_qwen3/dispatch/decode_layer.py:22-58)."""
+        if self.types[name] == "q4_k":
+            kernels.q4k_matvec(x, self._w(name), out=self.h, residual=self.h)
+        else:
+            kernels.qx_matvec(x, self._w(name), self.types[name], out=self.h, residual=self.h)
+
+    def _lm_head(self) -> None:
+        kernels.lm_head_argmax_partial(self.h, self._w("lm_head"), self.types["lm_head"], self.partial_scores,
+                                       self.partial_tokens, norm_weight=self._n("norm"), eps=self.config.rms_eps)
 
     def run_lm_head_select(self) -> None:
         """Final RMSNorm + LM head + argmax + EOS flag (run_decode_norm + _run_lm_head_select,
         src/models/optimized_qwen3/run.py:116-139); logits are never materialised."""
-        kernels.q4k_lm_head_argmax_partial(self.h, self._w("lm_head"), self.partial_scores, self.partial_tokens,
-                                           norm_weight=self._n("norm"), eps=self.config.rms_eps)
+        self._lm_head()
         kernels.token_select(self.partial_scores, self.partial_tokens, self.eos, self.next_token, self.done)
 
     def run_token_store(self, advance: bool = True) -> None:
@@ -133,8 +179,7 @@ class Qwen3Decoder:
         self.run_decode_embed()
         for i in range(self.config.layers):
             self.run_decode_layer(i)
-        kernels.q4k_lm_head_argmax_partial(self.h, self._w("lm_head"), self.partial_scores, self.partial_tokens,
-                                           norm_weight=self._n("norm"), eps=self.config.rms_eps)
+        self._lm_head()
         kernels.token_select_store(self.partial_scores, self.partial_tokens, self.eos, self.next_token, self.done,
                                    self.generated, self.length, self.stopped, stop_on_eos=self.stop_on_eos,
                                    advance=self.position)
