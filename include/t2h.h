@@ -126,6 +126,18 @@ int t2h_q6k_lm_head_argmax_partial(const void* x, const float* norm_w, float eps
  * counterpart: the reference fixes its grids in the shader variants. */
 int t2h_set_gemv_max_blocks(uint32_t max_blocks, uint32_t max_blocks_norm);
 
+/* ------------------------------------------------------ prefill GEMMs --- */
+/* y[m, n] = x[m, k] . deq(W[n, k])^T (+ residual) on the matrix cores: x bf16
+ * (16-byte aligned), W dequantised to bf16 tiles in LDS, fp32 accumulation,
+ * out fp32 or bf16 (fp32 with residual, which may alias y).  Any m and n; k % 64 == 0.
+ * replaces LINEAR_NOBIAS_Q8_0_F32 (src/models/quantized_qwen3/shaders/linear_nobias_q8_0_f32.py:24-209). */
+int t2h_q8_0_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                  uint32_t k, uint32_t n, void* stream);
+/* replaces LINEAR_NOBIAS_Q4_K_F32 (src/models/quantized_qwen3/shaders/linear_nobias_q4_k_f32.py:26-296) and
+ * LLAMA_MATMUL_Q4_K_F32_{M,L} (src/models/optimized_qwen3/shaders/llama_matmul_q4_k_f32.py:32-141); k % 256 == 0. */
+int t2h_q4k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                 uint32_t k, uint32_t n, void* stream);
+
 /* ---------------------------------------------------- token selection --- */
 /* replaces QWEN3_TOKEN_SELECT_REDUCE_CHUNKS_F32 + QWEN3_TOKEN_SELECT_REDUCE_F32
  * (src/torch2vk/export/shaders/qwen3_token_select_reduce_f32.py:22-241): one pass over g partials. */

@@ -1,0 +1,69 @@
+"""GPU parity of the prefill GEMMs (matrix cores, dequantised Q8_0 / Q4_K weight tiles) against the
+CPU oracle, through the C ABI."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import reference as R
+from tests.conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _problem(wtype, m, k, n, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w[0] = 0.0
+    if n > 3:
+        w[3] = np.abs(w[3]) * 40
+    packed = getattr(oracle, f"quantize_{wtype}")(w)
+    wd = getattr(oracle, f"dequant_{wtype}")(packed, k)
+    x = R.bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    return rng, packed, wd, x
+
+
+# (m, k, n): exact tiles, ragged M and N (partial 256-tiles), a handful of tokens, long K
+CASES = [("q8_0", 256, 256, 256), ("q8_0", 300, 1024, 520), ("q8_0", 17, 2048, 1024), ("q8_0", 512, 4096, 768),
+         ("q4_k", 256, 256, 256), ("q4_k", 300, 1024, 520), ("q4_k", 9, 4096, 1024), ("q4_k", 640, 3072, 256)]
+
+
+@pytest.mark.parametrize("wtype,m,k,n", CASES)
+def test_gemm_matches_oracle(device, wtype, m, k, n):
+    from torch2vk_amd import kernels
+
+    print(f"gemm {wtype} M={m} K={k} N={n}", flush=True)
+    rng, packed, wd, x = _problem(wtype, m, k, n, m + k + n)
+    xt = torch.from_numpy(x).to(device).to(torch.bfloat16)
+    wt = torch.from_numpy(packed).to(device)
+    got = kernels.gemm(xt, wt, wtype, out_dtype=torch.float32).cpu().numpy()
+    # the weight tile is dequantised to bf16: against x . bf16(deq W)^T only fp32 accumulation differs,
+    # which pins the tile layout and the dequantisation exactly
+    ref_tile = x.astype(np.float64) @ R.bf16_round(wd.astype(np.float32)).astype(np.float64).T
+    scale = np.abs(ref_tile).max()
+    assert_close(got, ref_tile, max_abs=1e-5 * scale + 1e-6, min_cos=0.999999, what="vs bf16 tile")
+    # and against the exact dequantised weights: the stated prefill tolerance
+    ref = x.astype(np.float64) @ wd.astype(np.float64).T
+    assert_close(got, ref, max_abs=1e-2 * np.abs(ref).max(), min_cos=0.9999, what="vs fp64 oracle")
+    # bf16 output and the residual epilogue (in place)
+    got16 = kernels.gemm(xt, wt, wtype).float().cpu().numpy()
+    assert_close(got16, ref_tile, max_abs=1e-2 * scale, min_cos=0.9999, what="bf16 out")
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    rt = torch.from_numpy(res).to(device)
+    kernels.gemm(xt, wt, wtype, out=rt, residual=rt)
+    assert_close(rt.cpu().numpy(), ref_tile + res, max_abs=1e-5 * scale + 1e-5, min_cos=0.999999, what="residual")
+
+
+def test_gemm_rejects_bad_shapes(device):
+    from torch2vk_amd import _lib, kernels
+
+    x = torch.zeros(4, 1056, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(64, 1056 // 32 * 34, dtype=torch.uint8, device=device)
+    with pytest.raises(ValueError, match="K % 64"):
+        kernels.gemm(x, w, "q8_0")
+    y = torch.empty(4, 64, dtype=torch.float32, device=device)
+    st = _lib.lib().t2h_q8_0_gemm(x.data_ptr(), w.data_ptr(), y.data_ptr(), 0, None, 4, 1056, 64, None)
+    assert st == 2

@@ -1,0 +1,333 @@
+// Prefill GEMM with block-quantized weights on the gfx950 matrix cores.
+//
+//   C[M, N] = A[M, K] . deq(W[N, K])^T      A bf16 row-major, W GGUF Q8_0 or Q4_K rows
+//
+// Replaces the reference's prefill matmuls (M > 8 tokens):
+//   LINEAR_NOBIAS_Q8_0_F32  (src/models/quantized_qwen3/shaders/linear_nobias_q8_0_f32.py:24-209)
+//   LINEAR_NOBIAS_Q4_K_F32  (src/models/quantized_qwen3/shaders/linear_nobias_q4_k_f32.py:26-296)
+//   LLAMA_MATMUL_Q4_K_F32_{M,L} (src/models/optimized_qwen3/shaders/llama_matmul_q4_k_f32.py:32-141)
+// They dequantise a weight tile into shared memory and run 16x16x16 fp16
+// cooperative-matrix products; here the tile is dequantised to bf16 in LDS
+// and fed to v_mfma_f32_32x32x16_bf16 with fp32 accumulation.
+//
+// Tiling.  A 512-thread block (8 waves, 2 x 4) computes a 256 x 256 tile of C;
+// each wave owns 128 x 64 = 4 x 2 MFMA tiles of 32 x 32 (128 accumulator
+// registers).  K advances 64 at a time through two LDS stages: while the
+// matrix cores work on one stage, the next stage's A rows and packed weight
+// blocks are already in flight to registers, and are dequantised into the
+// other stage before the block barrier.  LDS rows are padded to 72 bf16
+// (144 B) so the 16-B operand reads of 16 consecutive rows hit 16 distinct
+// 4-bank groups.
+//
+// Operand layout of v_mfma_f32_32x32x16_bf16 (checked on the device): lane l
+// supplies row (l % 32) of A and column (l % 32) of B, 8 consecutive k each,
+// k = 8 * (l / 32) + j; the 16 results of lane l are C[8(i/4) + 4(l/32) + i%4][l % 32].
+//
+// Tile order.  Blocks are dealt round-robin to the 8 XCDs; the tile index is
+// remapped so that each XCD walks a contiguous run of tiles, grouped 8 tiles
+// down M, so the A rows and weight rows a group shares stay in that XCD's L2.
+#include "common.h"
+
+namespace t2h {
+
+constexpr int GQ_THREADS = 512;
+constexpr int GQ_BM = 256;
+constexpr int GQ_BN = 256;
+constexpr int GQ_BK = 64;
+constexpr int GQ_LDS_ROW = GQ_BK + 8;  // bf16 elements per padded LDS row
+constexpr int GQ_GROUP_M = 8;
+
+enum GemmEpilogue { GQEPI_F32 = 0, GQEPI_BF16 = 1, GQEPI_RESID = 2 };
+
+struct GemmArgs {
+    const uint16_t* a;     // bf16 [M, K]
+    const uint8_t* w;      // packed rows [N, row_bytes]
+    void* c;               // [M, N] fp32 or bf16
+    const float* residual; // GQEPI_RESID: fp32 [M, N] (may alias c)
+    uint32_t m, n, k;
+    uint32_t row_bytes;
+    uint32_t tiles_m, tiles_n;
+};
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// ------------------------------------------------------ weight formats ----
+
+// Q8_0: thread t of the block dequantises block (t & 1) of the stage for row t >> 1.
+struct GemmQ80 {
+    static constexpr int BLOCK_VALUES = 32;
+    static constexpr int BLOCK_BYTES = 34;
+    struct Raw {
+        uint4 q0, q1;
+        uint32_t d;
+    };
+    __device__ static __forceinline__ void load(const GemmArgs& a, uint32_t n0, uint32_t k0, Raw& r) {
+        const uint32_t t = threadIdx.x;
+        uint32_t row = n0 + (t >> 1);
+        row = row < a.n ? row : a.n - 1;
+        const uint8_t* p = a.w + (size_t)row * a.row_bytes + (size_t)(k0 / 32 + (t & 1)) * 34;
+        r.d = load_u16(p);
+        r.q0 = load_u4_ua(p + 2);
+        r.q1 = load_u4_ua(p + 18);
+    }
+    // 32 bf16 values of this thread's block -> LDS row (t >> 1), columns 32 * (t & 1) ...
+    __device__ static __forceinline__ void store(const Raw& r, uint16_t* lds_b) {
+        const uint32_t t = threadIdx.x;
+        const float d = f16_bits_to_f32(r.d);
+        const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        uint32_t o[16];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint32_t w = q[c];
+            const float v0 = d * (float)(int8_t)(w & 0xffu);
+            const float v1 = d * (float)(int8_t)((w >> 8) & 0xffu);
+            const float v2 = d * (float)(int8_t)((w >> 16) & 0xffu);
+            const float v3 = d * (float)(int8_t)(w >> 24);
+            o[2 * c] = pack_bf16x2(v0, v1);
+            o[2 * c + 1] = pack_bf16x2(v2, v3);
+        }
+        uint16_t* dst = lds_b + (t >> 1) * GQ_LDS_ROW + (t & 1) * 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<uint4*>(dst + 8 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    }
+};
+
+// Q4_K: a 64-wide K stage is nibble group g = (k0 % 256) / 64 of superblock
+// k0 / 256; thread t dequantises sub-block 2g + (t & 1) of row t >> 1.
+struct GemmQ4K {
+    static constexpr int BLOCK_VALUES = 256;
+    static constexpr int BLOCK_BYTES = 144;
+    struct Raw {
+        uint4 hdr, q0, q1;
+    };
+    __device__ static __forceinline__ void load(const GemmArgs& a, uint32_t n0, uint32_t k0, Raw& r) {
+        const uint32_t t = threadIdx.x;
+        uint32_t row = n0 + (t >> 1);
+        row = row < a.n ? row : a.n - 1;
+        const uint8_t* p = a.w + (size_t)row * a.row_bytes + (size_t)(k0 / 256) * 144;
+        const uint32_t g = (k0 % 256) / 64;
+        r.hdr = load_u4(p);
+        r.q0 = load_u4(p + 16 + g * 32);
+        r.q1 = load_u4(p + 32 + g * 32);
+    }
+    __device__ static __forceinline__ void store(const Raw& r, uint16_t* lds_b, uint32_t k0) {
+        const uint32_t t = threadIdx.x;
+        const uint32_t g = (k0 % 256) / 64;
+        const uint32_t j = 2 * g + (t & 1);  // sub-block
+        const float d = f16_bits_to_f32(r.hdr.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(r.hdr.x >> 16);
+        // 6-bit scale/min of sub-block j (12 bytes at 4..15: hdr.y, hdr.z, hdr.w)
+        const uint8_t sb[12] = {
+            (uint8_t)r.hdr.y, (uint8_t)(r.hdr.y >> 8), (uint8_t)(r.hdr.y >> 16), (uint8_t)(r.hdr.y >> 24),
+            (uint8_t)r.hdr.z, (uint8_t)(r.hdr.z >> 8), (uint8_t)(r.hdr.z >> 16), (uint8_t)(r.hdr.z >> 24),
+            (uint8_t)r.hdr.w, (uint8_t)(r.hdr.w >> 8), (uint8_t)(r.hdr.w >> 16), (uint8_t)(r.hdr.w >> 24)};
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = sb[j] & 63u;
+            mn = sb[j + 4] & 63u;
+        } else {
+            sc = (sb[j + 4] & 0xfu) | ((sb[j - 4] >> 6) << 4);
+            mn = (sb[j + 4] >> 4) | ((sb[j] >> 6) << 4);
+        }
+        const float ds = d * (float)sc;
+        const float dm = dmin * (float)mn;
+        const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const int sh = (t & 1) * 4;  // low nibbles: sub-block 2g, high: 2g+1
+        uint32_t o[16];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint32_t w = q[c] >> sh;
+            const float v0 = ds * (float)(w & 0xfu) - dm;
+            const float v1 = ds * (float)((w >> 8) & 0xfu) - dm;
+            const float v2 = ds * (float)((w >> 16) & 0xfu) - dm;
+            const float v3 = ds * (float)((w >> 24) & 0xfu) - dm;
+            o[2 * c] = pack_bf16x2(v0, v1);
+            o[2 * c + 1] = pack_bf16x2(v2, v3);
+        }
+        uint16_t* dst = lds_b + (t >> 1) * GQ_LDS_ROW + (t & 1) * 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<uint4*>(dst + 8 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    }
+};
+
+template <class F>
+__device__ __forceinline__ void store_w(const typename F::Raw& r, uint16_t* lds_b, uint32_t k0) {
+    if constexpr (F::BLOCK_VALUES == 256) {
+        F::store(r, lds_b, k0);
+    } else {
+        F::store(r, lds_b);
+    }
+}
+
+// ---------------------------------------------------------------- kernel --
+
+template <class F, int EPI>
+__global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
+    __shared__ __align__(16) uint16_t lds_a[2][GQ_BM * GQ_LDS_ROW];
+    __shared__ __align__(16) uint16_t lds_b[2][GQ_BN * GQ_LDS_ROW];
+
+    // tile index: XCD-contiguous runs, then groups of GQ_GROUP_M tiles down M
+    const uint32_t total = a.tiles_m * a.tiles_n;
+    uint32_t pid = blockIdx.x;
+    if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;
+    const uint32_t per_group = GQ_GROUP_M * a.tiles_n;
+    const uint32_t first_m = (pid / per_group) * GQ_GROUP_M;
+    const uint32_t gsize = min(a.tiles_m - first_m, (uint32_t)GQ_GROUP_M);
+    const uint32_t tile_m = first_m + (pid % per_group) % gsize;
+    const uint32_t tile_n = (pid % per_group) / gsize;
+    const uint32_t m0 = tile_m * GQ_BM, n0 = tile_n * GQ_BN;
+
+    const uint32_t t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave >> 2;  // 0..1: rows wm*128
+    const int wn = wave & 3;   // 0..3: cols wn*64
+
+    // A stage load: 256 rows x 64 bf16 = 2048 chunks of 16 B, 4 per thread
+    const uint32_t KT = a.k / GQ_BK;
+    uint4 ra[4];
+    typename F::Raw rw;
+    auto load_stage = [&](uint32_t kt) {
+        const uint32_t k0 = kt * GQ_BK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t c = t + GQ_THREADS * i;
+            uint32_t row = m0 + (c >> 3);
+            row = row < a.m ? row : a.m - 1;
+            ra[i] = load_u4(a.a + (size_t)row * a.k + k0 + (c & 7) * 8);
+        }
+        F::load(a, n0, k0, rw);
+    };
+    auto store_stage = [&](uint32_t kt, int s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t c = t + GQ_THREADS * i;
+            *reinterpret_cast<uint4*>(&lds_a[s][(c >> 3) * GQ_LDS_ROW + (c & 7) * 8]) = ra[i];
+        }
+        store_w<F>(rw, lds_b[s], kt * GQ_BK);
+    };
+
+    f32x16_t acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    load_stage(0);
+    store_stage(0, 0);
+    __syncthreads();
+
+    const int frag_row = lane & 31;
+    const int frag_k = (lane >> 5) * 8;
+    for (uint32_t kt = 0; kt < KT; ++kt) {
+        const int s = kt & 1;
+        if (kt + 1 < KT) load_stage(kt + 1);
+        const uint16_t* sa = lds_a[s] + (wm * 128 + frag_row) * GQ_LDS_ROW + frag_k;
+        const uint16_t* sb = lds_b[s] + (wn * 64 + frag_row) * GQ_LDS_ROW + frag_k;
+#pragma unroll
+        for (int kk = 0; kk < GQ_BK; kk += 16) {
+            bf16x8_t fa[4], fb[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                fa[i] = *reinterpret_cast<const bf16x8_t*>(sa + i * 32 * GQ_LDS_ROW + kk);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                fb[j] = *reinterpret_cast<const bf16x8_t*>(sb + j * 32 * GQ_LDS_ROW + kk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < KT) store_stage(kt + 1, s ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds column (lane % 32) of each 32x32 tile, rows 8(e/4) + 4(lane/32) + e%4
+    const uint32_t col_base = n0 + wn * 64 + (lane & 31);
+    const uint32_t row_base = m0 + wm * 128 + (lane >> 5) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t col = col_base + j * 32;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t row = row_base + i * 32 + (e >> 2) * 8 + (e & 3);
+                if (row < a.m && col < a.n) {
+                    const size_t idx = (size_t)row * a.n + col;
+                    const float v = acc[i][j][e];
+                    if constexpr (EPI == GQEPI_F32) {
+                        reinterpret_cast<float*>(a.c)[idx] = v;
+                    } else if constexpr (EPI == GQEPI_BF16) {
+                        reinterpret_cast<uint16_t*>(a.c)[idx] = (uint16_t)f32_to_bf16_bits(v);
+                    } else {
+                        reinterpret_cast<float*>(a.c)[idx] = a.residual[idx] + v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <class F>
+static int gemm_q_launch(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                         uint32_t k, uint32_t n, void* stream) {
+    if (!x || !w || !y) return T2H_ERR_NULL;
+    if (k == 0 || k % GQ_BK != 0 || k % F::BLOCK_VALUES != 0) return T2H_ERR_SHAPE;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) return T2H_ERR_ALIGN;
+    if (F::BLOCK_VALUES == 256 && (reinterpret_cast<uintptr_t>(w) & 15) != 0) return T2H_ERR_ALIGN;
+    int epi;
+    if (residual) {
+        if (out_dtype != T2H_DTYPE_F32) return T2H_ERR_DTYPE;
+        epi = GQEPI_RESID;
+    } else if (out_dtype == T2H_DTYPE_F32) {
+        epi = GQEPI_F32;
+    } else if (out_dtype == T2H_DTYPE_BF16) {
+        epi = GQEPI_BF16;
+    } else {
+        return T2H_ERR_DTYPE;
+    }
+    if (m == 0 || n == 0) return T2H_OK;
+    GemmArgs a = {};
+    a.a = reinterpret_cast<const uint16_t*>(x);
+    a.w = reinterpret_cast<const uint8_t*>(w);
+    a.c = y;
+    a.residual = residual;
+    a.m = m;
+    a.n = n;
+    a.k = k;
+    a.row_bytes = k / F::BLOCK_VALUES * F::BLOCK_BYTES;
+    a.tiles_m = (m + GQ_BM - 1) / GQ_BM;
+    a.tiles_n = (n + GQ_BN - 1) / GQ_BN;
+    const size_t tiles = (size_t)a.tiles_m * a.tiles_n;
+    if (tiles > 0x7fffffffu) return T2H_ERR_SHAPE;
+    const dim3 grid((uint32_t)tiles), block(GQ_THREADS);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    switch (epi) {
+        case GQEPI_F32: hipLaunchKernelGGL((gemm_q_kernel<F, GQEPI_F32>), grid, block, 0, s, a); break;
+        case GQEPI_BF16: hipLaunchKernelGGL((gemm_q_kernel<F, GQEPI_BF16>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((gemm_q_kernel<F, GQEPI_RESID>), grid, block, 0, s, a); break;
+    }
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+}  // namespace t2h
+
+using namespace t2h;
+
+extern "C" int t2h_q8_0_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                             uint32_t k, uint32_t n, void* stream) {
+    return gemm_q_launch<GemmQ80>(x, w, y, out_dtype, residual, m, k, n, stream);
+}
+
+extern "C" int t2h_q4k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                            uint32_t k, uint32_t n, void* stream) {
+    return gemm_q_launch<GemmQ4K>(x, w, y, out_dtype, residual, m, k, n, stream);
+}

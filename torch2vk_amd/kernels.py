@@ -265,6 +265,31 @@ def lm_head_argmax_partial(x: torch.Tensor, w: torch.Tensor, wtype: str, partial
          ptr(partial_tokens), g, stream_handle())
 
 
+def gemm(x: torch.Tensor, w: torch.Tensor, wtype: str, *, out: torch.Tensor | None = None,
+         out_dtype: torch.dtype = torch.bfloat16, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """Prefill GEMM on the matrix cores: y[M, N] = x[M, K] . deq(W)^T (+ residual); x bf16, W Q8_0 or Q4_K."""
+    if wtype not in ("q8_0", "q4_k"):
+        raise ValueError(f"gemm handles q8_0 and q4_k weights, got {wtype!r}")
+    _check(x, "x", torch.bfloat16)
+    k = int(x.shape[-1])
+    if k % 64:
+        raise ValueError(f"gemm needs K % 64 == 0, got {k}")
+    m = x.numel() // k
+    n = _check_packed(w, "weight", wtype, k)
+    if out is None:
+        out = torch.empty(*x.shape[:-1], n, dtype=out_dtype, device=x.device)
+    _check(out, "output", tuple(_OUT_DTYPES), align=4)
+    if out.numel() != m * n:
+        raise ValueError(f"output has {out.numel()} elements, expected {m * n}")
+    if residual is not None:
+        _check(residual, "residual", torch.float32, align=4)
+        if residual.numel() != m * n or out.dtype != torch.float32:
+            raise ValueError("residual must be fp32 with the output's shape; output must be fp32")
+    name = "t2h_q8_0_gemm" if wtype == "q8_0" else "t2h_q4k_gemm"
+    call(name, ptr(x), ptr(w), ptr(out), _OUT_DTYPES[out.dtype], ptr(residual), m, k, n, stream_handle())
+    return out
+
+
 def set_gemv_max_blocks(max_blocks: int, max_blocks_norm: int = 0) -> None:
     """Grid caps (blocks of 8 waves) for plain and RMSNorm-prologue Q4_K GEMV launches."""
     call("t2h_set_gemv_max_blocks", int(max_blocks), int(max_blocks_norm))
