@@ -120,10 +120,11 @@ int t2h_q6k_lm_head_argmax_partial(const void* x, const float* norm_w, float eps
                                    uint32_t n, float* partial_scores, uint32_t* partial_tokens,
                                    uint32_t num_partials, void* stream);
 
-/* Grid caps of the GEMV launches, in blocks of 8 waves (tuning knob, process-wide):
+/* Grid caps of the Q4_K GEMV launches, in blocks (tuning knob, process-wide):
  * max_blocks for plain bf16 x (default 256), max_blocks_norm for the fused
- * RMSNorm prologue (default 256; 0 = same as max_blocks).  No reference
- * counterpart: the reference fixes its grids in the shader variants. */
+ * RMSNorm prologue (default 256; 0 = same as max_blocks).  Each wave gets
+ * ceil(units / (blocks * waves)) row units.  No reference counterpart: the
+ * reference fixes its grids in the shader variants. */
 int t2h_set_gemv_max_blocks(uint32_t max_blocks, uint32_t max_blocks_norm);
 
 /* ------------------------------------------------------ prefill GEMMs --- */

@@ -15,15 +15,26 @@
 // superblock s, and lane l reads the 16-B header plus the 32-B nibble group
 // g = l & 3, i.e. all 32 values of sub-block 2g (low nibbles) and of
 // sub-block 2g+1 (high nibbles).  One header decode therefore serves 64
-// weights.  A "row group" is RPW consecutive rows covered by NIT such steps,
-// RPW = 16/gcd(NSB,16) and NIT = NSB*RPW/16, so no lane idles for any K.
+// weights.  A "unit" is RPW consecutive rows covered by NIT such steps,
+// RPW = 16/gcd(NSBW,16) and NIT = NSBW*RPW/16, where NSBW is the number of
+// superblocks a wave covers per row: all NSB of them, or, for rows of 32 or
+// 48 superblocks, one 16-superblock chunk, with KS = NSB/16 waves splitting
+// each row and adding their partial sums in LDS.  No lane idles for any K.
 //
-// Arithmetic.  Nibble pairs become bf16 values 128+q with one and-or
-// (0x4300 | q), and v_dot2_f32_bf16 accumulates x*(128+q) in fp32; the 128*Σx
-// offset is removed with the per-lane Σx the min term needs anyway:
-//   Σ x*w = d*(sc_lo*(S_lo - 128 Σx_lo) + sc_hi*(S_hi - 128 Σx_hi)) - dmin*(m_lo Σx_lo + m_hi Σx_hi)
-// x is the same for every row, so each lane keeps its x slice in registers
-// for the whole launch; the weight stream is software pipelined.
+// Arithmetic.  A nibble pair becomes two fp16 operands of v_dot2_f32_f16 with
+// one and-or against the fp16 magic 64.0 (0x5400):
+//   (w & 0x000f000f) | 0x54005400 = (64 + q/16) x2   (low nibbles)
+//   (w & 0x00f000f0) | 0x54005400 = (64 + q)    x2   (high nibbles)
+// so 8 nibbles cost 5 bit operations and 4 dot2.  The 64*sum(x) offset comes
+// off with the per-sub-block sums of x that the min term needs anyway:
+//   sum x*q = 16*(S_lo - 64 sum x_lo)  and  S_hi - 64 sum x_hi.
+// Every product is exact in fp32; the offset cancels to a few fp32 ulps of
+// 64*sum|x| per sub-block.  x is bf16 by contract and enters the dot as fp16,
+// which holds every bf16 value of magnitude 2^-14..65504 exactly (the
+// reference's activations are fp16, so its range is the same).  The block
+// stages x once in LDS, already as fp16 pair words (e0,e2),(e1,e3) that line
+// up with the nibble pairs, plus the sum of every 32-value sub-block; each
+// lane then keeps its slices in registers for the whole launch.
 #include "common.h"
 
 namespace t2h {
@@ -44,103 +55,114 @@ struct Q4GemvArgs {
     const float* residual;  // Q4EPI_RESID: fp32 [N] (may alias y)
     Q4Part parts[3];
     uint32_t n_parts;
-    uint32_t n_units;       // row groups (Q4EPI_SWIGLU: row groups of the gate)
+    uint32_t n_units;         // units of RPW rows (Q4EPI_SWIGLU: units of the gate)
     uint32_t units_per_wave;  // every wave runs this many units (rounded up to the ring size, clamped)
-    float* partial_scores;  // Q4EPI_ARGMAX: [gridDim.x]
+    float* partial_scores;    // Q4EPI_ARGMAX: [gridDim.x]
     uint32_t* partial_tokens;
     float eps;
 };
 
 constexpr int cgcd(int a, int b) { return b == 0 ? a : cgcd(b, a % b); }
 
-constexpr int GEMV_THREADS = 512;  // 8 waves per block share one staged copy of x
-constexpr uint32_t GEMV_WAVES = GEMV_THREADS / 64;
+// Units one wave may own when KS > 1 (their partial sums wait in LDS).
+constexpr uint32_t Q4_KSPLIT_MAX_UNITS = 8;
 
-template <int NSB>
-struct Q4Geom {
-    static constexpr int K = NSB * 256;
-    static constexpr int RPW = 16 / cgcd(NSB, 16);
-    static constexpr int NIT = NSB * RPW / 16;
-    static constexpr int ROW_BYTES = NSB * 144;
-};
+// ---------------------------------------------------------------- x in LDS --
 
-// Per-lane x slice for one step: the 32 values of sub-block 2g and the 32 of
-// sub-block 2g+1, stored as bf16 pairs (e0,e2),(e1,e3),(e4,e6),... to match
-// the nibble pairs the and-or trick produces, plus their sums.
-struct XSlice {
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float v) {
+    return (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)v);
+}
+
+// A value known to be in a VGPR: VOP3 instructions (v_and_or_b32) take no
+// literal operand on gfx9, so a mask held in a VGPR lets one v_and_or_b32 do
+// the whole nibble expansion instead of an AND and an OR with literals.
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t v) {
+    uint32_t r;
+    asm("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
+    return r;
+}
+
+// Stage 4 consecutive x values (already bf16-exact) at element k: one fp16
+// pair word (e0,e2) and one (e1,e3), and, through the 8 threads that hold one
+// 32-value sub-block, that sub-block's sum.  All 8 threads of a sub-block call
+// this together.
+__device__ __forceinline__ void stage_x4(uint32_t* xp, float* xsum, int k, float v0, float v1, float v2, float v3) {
+    const uint32_t a = f32_to_f16_bits(v0) | (f32_to_f16_bits(v2) << 16);
+    const uint32_t b = f32_to_f16_bits(v1) | (f32_to_f16_bits(v3) << 16);
+    *reinterpret_cast<uint2*>(&xp[k / 2]) = make_uint2(a, b);
+    float s = (v0 + v1) + (v2 + v3);
+    s += dpp_f32<0xB1>(s);  // quad_perm [1,0,3,2]: lane ^ 1
+    s += dpp_f32<0x4E>(s);  // quad_perm [2,3,0,1]: lane ^ 2
+    s += __shfl_xor(s, 4, T2H_WAVE);
+    if (((k >> 2) & 7) == 0) xsum[k >> 5] = s;
+}
+
+// One lane's x slice for one step: sub-blocks 2g and 2g+1 of superblock sb,
+// as fp16 pair words, and 64 * each sub-block's sum.
+struct XSlice16 {
     uint32_t lo[16];
     uint32_t hi[16];
-    float sum_lo;
-    float sum_hi;
+    float sum_lo64;
+    float sum_hi64;
 };
 
-// 32 bf16 values (16 dwords, natural order) -> 16 pairs + their sum
-__device__ __forceinline__ void pair_up(const uint32_t (&raw)[16], uint32_t (&out)[16], float& sum) {
-    float s = 0.0f;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const uint32_t x0 = raw[2 * c];      // (e0, e1)
-        const uint32_t x1 = raw[2 * c + 1];  // (e2, e3)
-        out[2 * c] = (x0 & 0xffffu) | (x1 << 16);
-        out[2 * c + 1] = (x0 >> 16) | (x1 & 0xffff0000u);
-        s += bf16_bits_to_f32(x0 & 0xffffu) + bf16_bits_to_f32(x0 >> 16);
-        s += bf16_bits_to_f32(x1 & 0xffffu) + bf16_bits_to_f32(x1 >> 16);
-    }
-    sum = s;
-}
-
-__device__ __forceinline__ void unpack_u4x4(const uint4 (&v)[4], uint32_t (&raw)[16]) {
+__device__ __forceinline__ void load_xslice16(const uint32_t* xp, const float* xsum, int sb, int g, XSlice16& xs) {
+    const uint32_t* p = xp + (sb * 256 + 64 * g) / 2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        raw[4 * i] = v[i].x;
-        raw[4 * i + 1] = v[i].y;
-        raw[4 * i + 2] = v[i].z;
-        raw[4 * i + 3] = v[i].w;
+        const uint4 v = *reinterpret_cast<const uint4*>(p + 4 * i);
+        xs.lo[4 * i] = v.x;
+        xs.lo[4 * i + 1] = v.y;
+        xs.lo[4 * i + 2] = v.z;
+        xs.lo[4 * i + 3] = v.w;
     }
-}
-
-// x slice of nibble group g starting at element off (= 64 g within a superblock)
-__device__ __forceinline__ void load_xslice(const uint16_t* xb, int off, XSlice& xs) {
-    uint4 v[4];
-    uint32_t raw[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = load_u4(xb + off + 8 * i);
-    unpack_u4x4(v, raw);
-    pair_up(raw, xs.lo, xs.sum_lo);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = load_u4(xb + off + 32 + 8 * i);
-    unpack_u4x4(v, raw);
-    pair_up(raw, xs.hi, xs.sum_hi);
+    for (int i = 0; i < 4; ++i) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p + 16 + 4 * i);
+        xs.hi[4 * i] = v.x;
+        xs.hi[4 * i + 1] = v.y;
+        xs.hi[4 * i + 2] = v.z;
+        xs.hi[4 * i + 3] = v.w;
+    }
+    xs.sum_lo64 = 64.0f * xsum[sb * 8 + 2 * g];
+    xs.sum_hi64 = 64.0f * xsum[sb * 8 + 2 * g + 1];
 }
 
-__device__ __forceinline__ void dot_nibble_word(uint32_t w, uint32_t xa, uint32_t xb, uint32_t xc, uint32_t xd,
-                                                float& s_lo, float& s_hi) {
-    const uint32_t w4 = w >> 4;
-    const uint32_t pa = (w & 0x000f000fu) | 0x43004300u;
-    const uint32_t pb = ((w >> 8) & 0x000f000fu) | 0x43004300u;
-    const uint32_t pc = (w4 & 0x000f000fu) | 0x43004300u;
-    const uint32_t pd = ((w4 >> 8) & 0x000f000fu) | 0x43004300u;
-    s_lo = dot2_bf16(pa, xa, s_lo);
-    s_lo = dot2_bf16(pb, xb, s_lo);
-    s_hi = dot2_bf16(pc, xc, s_hi);
-    s_hi = dot2_bf16(pd, xd, s_hi);
+// ------------------------------------------------------------ dot product --
+
+// Per-lane constants of the header decode (nibble group g) and the masks.
+struct Q4LaneConsts {
+    uint32_t m_lo, m_hi;  // 0x000f000f / 0x00f000f0, in VGPRs
+    int sh;               // 16 * (g & 1): byte pair of sub-blocks 2g, 2g+1 within a dword
+    bool low;             // g < 2: 6-bit codes stored whole in bytes 4..11
+    uint32_t mask_lo, hi_en;
+    int sh_m;
+};
+
+__device__ __forceinline__ Q4LaneConsts q4k_lane_consts(int g) {
+    Q4LaneConsts c;
+    c.m_lo = in_vgpr(0x000f000fu);
+    c.m_hi = in_vgpr(0x00f000f0u);
+    c.sh = (g & 1) << 4;
+    c.low = g < 2;
+    c.mask_lo = c.low ? 0x3f3fu : 0x0f0fu;
+    c.hi_en = c.low ? 0u : 0x3030u;
+    c.sh_m = c.low ? c.sh : c.sh + 4;
+    return c;
 }
 
-// Partial dot of one lane's 64 values of one superblock (nibble group g).
-__device__ __forceinline__ float q4k_lane_dot(const uint4 hdr, const uint4 q0, const uint4 q1, const XSlice& xs,
-                                              int g) {
+// Partial dot of one lane's 64 values of one superblock (nibble group g):
+//   d*(sc_lo*sum(x q)_lo + sc_hi*sum(x q)_hi) - dmin*(m_lo*sum x_lo + m_hi*sum x_hi)
+__device__ __forceinline__ float q4k_lane_dot(const uint4 hdr, const uint4 q0, const uint4 q1, const XSlice16& xs,
+                                              const Q4LaneConsts& c) {
+    constexpr uint32_t MAGIC = 0x54005400u;  // fp16 64.0 in both halves
     const float d = f16_bits_to_f32(hdr.x & 0xffffu);
     const float dmin = f16_bits_to_f32(hdr.x >> 16);
-    // 6-bit scale/min codes of sub-blocks 2g and 2g+1 (two bytes each)
-    const int sh = (g & 1) << 4;
-    const bool low = g < 2;
-    const uint32_t mask_lo = low ? 0x3f3fu : 0x0f0fu;
-    const uint32_t hi_en = low ? 0u : 0x3030u;
-    const uint32_t src_s = low ? hdr.y : hdr.w;
-    const uint32_t src_m = low ? hdr.z : hdr.w;
-    const int sh_m = low ? sh : sh + 4;
-    const uint32_t S = ((src_s >> sh) & mask_lo) | ((hdr.y >> (sh + 2)) & hi_en);
-    const uint32_t M = ((src_m >> sh_m) & mask_lo) | ((hdr.z >> (sh + 2)) & hi_en);
+    // 6-bit scale/min codes of sub-blocks 2g and 2g+1 (get_scale_min_k4)
+    const uint32_t src_s = c.low ? hdr.y : hdr.w;
+    const uint32_t src_m = c.low ? hdr.z : hdr.w;
+    const uint32_t S = ((src_s >> c.sh) & c.mask_lo) | ((hdr.y >> (c.sh + 2)) & c.hi_en);
+    const uint32_t M = ((src_m >> c.sh_m) & c.mask_lo) | ((hdr.z >> (c.sh + 2)) & c.hi_en);
     const float sc_lo = (float)(S & 0xffu);
     const float sc_hi = (float)((S >> 8) & 0xffu);
     const float m_lo = (float)(M & 0xffu);
@@ -149,29 +171,43 @@ __device__ __forceinline__ float q4k_lane_dot(const uint4 hdr, const uint4 q0, c
     float s_lo = 0.0f, s_hi = 0.0f;
     const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
-        dot_nibble_word(q[c], xs.lo[2 * c], xs.lo[2 * c + 1], xs.hi[2 * c], xs.hi[2 * c + 1], s_lo, s_hi);
-    const float xq_lo = fmaf(-128.0f, xs.sum_lo, s_lo);
-    const float xq_hi = fmaf(-128.0f, xs.sum_hi, s_hi);
+    for (int w = 0; w < 8; ++w) {
+        const uint32_t b02 = q[w];       // bytes 0 and 2 of the word in the low bits of each half
+        const uint32_t b13 = q[w] >> 8;  // bytes 1 and 3
+        s_lo = dot2_f16((b02 & c.m_lo) | MAGIC, xs.lo[2 * w], s_lo);
+        s_hi = dot2_f16((b02 & c.m_hi) | MAGIC, xs.hi[2 * w], s_hi);
+        s_lo = dot2_f16((b13 & c.m_lo) | MAGIC, xs.lo[2 * w + 1], s_lo);
+        s_hi = dot2_f16((b13 & c.m_hi) | MAGIC, xs.hi[2 * w + 1], s_hi);
+    }
+    const float xq_lo = 16.0f * (s_lo - xs.sum_lo64);
+    const float xq_hi = s_hi - xs.sum_hi64;
     const float scaled = fmaf(sc_lo, xq_lo, sc_hi * xq_hi);
-    const float mins = fmaf(m_lo, xs.sum_lo, m_hi * xs.sum_hi);
+    const float mins = fmaf(m_lo, xs.sum_lo64, m_hi * xs.sum_hi64) * (1.0f / 64.0f);
     return fmaf(d, scaled, -dmin * mins);
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-template <int NSB, int PRO, int EPI>
-__global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs a) {
-    using Geo = Q4Geom<NSB>;
-    constexpr int K = Geo::K;
-    constexpr int RPW = Geo::RPW;
-    constexpr int NIT = Geo::NIT;
-    constexpr int ROW_BYTES = Geo::ROW_BYTES;
+__device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+template <int NSB, int KS, int WPB, int PRO, int EPI, int UPW = 0>
+__global__ __launch_bounds__(WPB * 64) void q4k_gemv_kernel(const Q4GemvArgs a) {
+    constexpr int K = NSB * 256;
+    constexpr int NT = WPB * 64;
+    constexpr int WR = WPB / KS;          // wave rows per block
+    constexpr int NSBW = NSB / KS;        // superblocks per wave and row
+    constexpr int RPW = 16 / cgcd(NSBW, 16);
+    constexpr int NIT = NSBW * RPW / 16;
+    constexpr int ROW_BYTES = NSB * 144;
     constexpr int NG = EPI == Q4EPI_SWIGLU ? 2 : 1;  // row groups per unit (gate and up)
+    static_assert(WPB % KS == 0 && NSB % KS == 0, "KS must divide the block and the row");
+    static_assert(KS == 1 || NSBW == 16, "split rows are cut into 16-superblock chunks");
+    static_assert(KS == 1 || (EPI != Q4EPI_SWIGLU && EPI != Q4EPI_ARGMAX), "split rows: plain epilogues only");
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, scalar
-    const int waves_per_block = blockDim.x >> 6;
+    const int ks = wave % KS;
+    const int wr = wave / KS;
     const int sbo = lane >> 2;  // superblock slot of this lane within a step
     const int g = lane & 3;     // nibble group: sub-blocks 2g (low nibbles) and 2g+1 (high)
 
@@ -180,16 +216,17 @@ __global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int f = it * 16 + sbo;
-        rloc[it] = f / NSB;
-        sbi[it] = f % NSB;
+        rloc[it] = f / NSBW;
+        sbi[it] = ks * NSBW + f % NSBW;
     }
 
     // Weight stream, software pipelined over a ring of NSTAGE stages: a stage
-    // holds the header and nibble chunks of one unit (NG row groups) and
-    // NSTAGE-1 units are in flight while one is reduced.  Every wave runs the
-    // same number of units; units past the end are clamped to the last one and
-    // their results dropped, so the load stream has no divergent branches.
-    constexpr int NSTAGE = (NG * NIT <= 2) ? 3 : 2;
+    // holds the header and nibble chunks of one unit (NG row groups).  The
+    // first NSTAGE units are issued before the x prologue; a stage is refilled
+    // with unit i+NSTAGE as soon as unit i has been reduced.  Every wave runs
+    // the same number of units; units past the end are clamped to the last one
+    // and their results dropped, so the load stream has no divergent branches.
+    constexpr int NSTAGE = UPW > 0 ? UPW : ((NG * NIT == 1) ? 4 : 2);
     struct Stage {
         uint4 hdr[NG][NIT];
         uint4 q0[NG][NIT];
@@ -201,11 +238,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs
 #pragma unroll
             for (int it = 0; it < NIT; ++it) {
                 const uint8_t* base;
+                const uint32_t row = unit * RPW + (uint32_t)rloc[it];
                 if constexpr (EPI == Q4EPI_SWIGLU) {
-                    const uint32_t row = unit * RPW + (uint32_t)rloc[it];
                     base = a.parts[gi].w + (size_t)row * ROW_BYTES;
                 } else {
-                    const uint32_t row = unit * RPW + (uint32_t)rloc[it];
                     int pi = 0;
                     pi += (a.n_parts > 1 && row >= a.parts[1].row_begin) ? 1 : 0;
                     pi += (a.n_parts > 2 && row >= a.parts[2].row_begin) ? 1 : 0;
@@ -216,38 +252,38 @@ __global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs
                 st.hdr[gi][it] = load_u4(base);
                 // plain (temporal) loads: the two 16-B chunks of a lane are 32 B
                 // apart, so each instruction uses half of every line it touches
-                // and the other half must still be cached for the next one;
-                // non-temporal loads measured ~25% slower here
+                // and the other half must still be cached for the next one
                 st.q0[gi][it] = load_u4(base + 16 + g * 32);
                 st.q1[gi][it] = load_u4(base + 32 + g * 32);
             }
         }
     };
 
-    const uint32_t wave_global = blockIdx.x * waves_per_block + wave;
-    const uint32_t total_waves = gridDim.x * waves_per_block;
+    const uint32_t wrow = blockIdx.x * WR + wr;
+    const uint32_t total_wrows = gridDim.x * WR;
     const uint32_t last_unit = a.n_units - 1;
     auto clamp_unit = [&](uint32_t u) { return u < a.n_units ? u : last_unit; };
-    const uint32_t n_iter = (a.units_per_wave + NSTAGE - 1) / NSTAGE * NSTAGE;
+    const uint32_t n_iter = UPW > 0 ? (uint32_t)UPW : a.units_per_wave;  // the same for every wave
     Stage st[NSTAGE];
 
     // ---------------------------------------------------------- x slice --
-    // x is staged once per block in LDS (bf16, coalesced loads shared by the
+    // x is staged once per block in LDS (coalesced loads shared by the
     // block's waves) and each lane then reads its slices from LDS.  The x-side
-    // loads are issued before the first weight stages: vmcnt retires in order,
-    // so the prologue waits for them alone while the weight loads stay in flight.
-    __shared__ __align__(16) uint16_t xsh[K];
+    // loads go first and only the first weight stage is issued before the
+    // prologue: vmcnt retires in order, so the prologue waits for x alone.
+    __shared__ __align__(16) uint32_t xp[K / 2];
+    __shared__ float xsum[K / 32];
+    constexpr int PT = (K + 4 * NT - 1) / (4 * NT);  // 4-value groups per thread
     if constexpr (PRO == Q4PRO_RMSNORM) {
         // one pass: h and norm weight loaded once, sum of squares reduced over
-        // the block, normalised bf16 x written to LDS
-        constexpr int PT = (K + 4 * GEMV_THREADS - 1) / (4 * GEMV_THREADS);  // float4s per thread
-        __shared__ float red[GEMV_THREADS / 64];
+        // the block, normalised x (rounded to bf16) staged in LDS
+        __shared__ float red[WPB];
         const float* h = reinterpret_cast<const float*>(a.x);
         float4 hv[PT], wv[PT];
 #pragma unroll
         for (int j = 0; j < PT; ++j) {
-            const int k = (j * GEMV_THREADS + (int)threadIdx.x) * 4;
-            if (K % (4 * GEMV_THREADS) == 0 || k < K) {
+            const int k = (j * NT + (int)threadIdx.x) * 4;
+            if (K % (4 * NT) == 0 || k < K) {
                 hv[j] = *reinterpret_cast<const float4*>(h + k);
                 wv[j] = *reinterpret_cast<const float4*>(a.norm_w + k);
             } else {
@@ -255,8 +291,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs
                 wv[j] = hv[j];
             }
         }
-#pragma unroll
-        for (int s = 0; s + 1 < NSTAGE; ++s) issue(clamp_unit(wave_global + s * total_waves), st[s]);
+        issue(clamp_unit(wrow), st[0]);
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < PT; ++j) {
@@ -270,43 +305,68 @@ __global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs
         __syncthreads();
         float total = 0.0f;
 #pragma unroll
-        for (int i = 0; i < GEMV_THREADS / 64; ++i) total += red[i];
+        for (int i = 0; i < WPB; ++i) total += red[i];
         const float inv = 1.0f / sqrtf(total / (float)K + a.eps);
 #pragma unroll
         for (int j = 0; j < PT; ++j) {
-            const int k = (j * GEMV_THREADS + (int)threadIdx.x) * 4;
-            if (K % (4 * GEMV_THREADS) == 0 || k < K) {
-                const uint32_t p0 = pack_bf16x2(hv[j].x * inv * wv[j].x, hv[j].y * inv * wv[j].y);
-                const uint32_t p1 = pack_bf16x2(hv[j].z * inv * wv[j].z, hv[j].w * inv * wv[j].w);
-                *reinterpret_cast<uint2*>(&xsh[k]) = make_uint2(p0, p1);
-            }
+            const int k = (j * NT + (int)threadIdx.x) * 4;
+            if (K % (4 * NT) == 0 || k < K)
+                stage_x4(xp, xsum, k, bf16_round(hv[j].x * inv * wv[j].x), bf16_round(hv[j].y * inv * wv[j].y),
+                         bf16_round(hv[j].z * inv * wv[j].z), bf16_round(hv[j].w * inv * wv[j].w));
         }
     } else {
-        constexpr int PT = (K + 8 * GEMV_THREADS - 1) / (8 * GEMV_THREADS);  // 16-B chunks per thread
         const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x);
-        uint4 xv[PT];
+        uint2 xv[PT];
 #pragma unroll
         for (int j = 0; j < PT; ++j) {
-            const int k = (j * GEMV_THREADS + (int)threadIdx.x) * 8;
-            xv[j] = (K % (8 * GEMV_THREADS) == 0 || k < K) ? load_u4(xb + k) : make_uint4(0, 0, 0, 0);
+            const int k = (j * NT + (int)threadIdx.x) * 4;
+            xv[j] = (K % (4 * NT) == 0 || k < K) ? *reinterpret_cast<const uint2*>(xb + k) : make_uint2(0, 0);
         }
-#pragma unroll
-        for (int s = 0; s + 1 < NSTAGE; ++s) issue(clamp_unit(wave_global + s * total_waves), st[s]);
+        issue(clamp_unit(wrow), st[0]);
 #pragma unroll
         for (int j = 0; j < PT; ++j) {
-            const int k = (j * GEMV_THREADS + (int)threadIdx.x) * 8;
-            if (K % (8 * GEMV_THREADS) == 0 || k < K) *reinterpret_cast<uint4*>(&xsh[k]) = xv[j];
+            const int k = (j * NT + (int)threadIdx.x) * 4;
+            if (K % (4 * NT) == 0 || k < K)
+                stage_x4(xp, xsum, k, bf16_bits_to_f32(xv[j].x & 0xffffu), bf16_bits_to_f32(xv[j].x >> 16),
+                         bf16_bits_to_f32(xv[j].y & 0xffffu), bf16_bits_to_f32(xv[j].y >> 16));
         }
     }
     __syncthreads();
-    XSlice xs[NIT];
+    // The other stages are issued only now: a wave's loads return in order and
+    // the CU's memory pipeline is shared, so x-side loads queued behind a deep
+    // weight stream would hold the whole block at the barrier above.
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) load_xslice(xsh, sbi[it] * 256 + 64 * g, xs[it]);
+    for (int s = 1; s < NSTAGE; ++s)
+        if ((uint32_t)s < n_iter) issue(clamp_unit(wrow + s * total_wrows), st[s]);
+    XSlice16 xs[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) load_xslice16(xp, xsum, sbi[it], g, xs[it]);
+    const Q4LaneConsts lc = q4k_lane_consts(g);
 
     float best_score = -3.4028234663852886e38f;
     uint32_t best_token = 0xffffffffu;
 
-    auto consume = [&](uint32_t u, const Stage& st) {
+    auto store_row = [&](uint32_t row, float v) {
+        int pi = 0;
+        pi += (a.n_parts > 1 && row >= a.parts[1].row_begin) ? 1 : 0;
+        pi += (a.n_parts > 2 && row >= a.parts[2].row_begin) ? 1 : 0;
+        const Q4Part& p = a.parts[pi];
+        const uint32_t local = row - p.row_begin;
+        if constexpr (EPI == Q4EPI_F32) {
+            reinterpret_cast<float*>(p.y)[local] = v;
+        } else if constexpr (EPI == Q4EPI_BF16) {
+            reinterpret_cast<uint16_t*>(p.y)[local] = (uint16_t)f32_to_bf16_bits(v);
+        } else if constexpr (EPI == Q4EPI_RESID) {
+            reinterpret_cast<float*>(p.y)[local] = a.residual[local] + v;
+        }
+    };
+
+    constexpr int PART_WR = KS > 1 ? WR : 1;
+    constexpr int PART_KS = KS > 1 ? KS : 1;
+    constexpr int PART_U = KS > 1 ? (int)Q4_KSPLIT_MAX_UNITS : 1;
+    __shared__ float part[PART_WR][PART_U][PART_KS];
+
+    auto consume = [&](uint32_t i, uint32_t u, const Stage& st) {
         const bool live = u < a.n_units;
         float res[NG][RPW];
 #pragma unroll
@@ -316,7 +376,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs
             for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
 #pragma unroll
             for (int it = 0; it < NIT; ++it) {
-                const float c = q4k_lane_dot(st.hdr[gi][it], st.q0[gi][it], st.q1[gi][it], xs[it], g);
+                const float c = q4k_lane_dot(st.hdr[gi][it], st.q0[gi][it], st.q1[gi][it], xs[it], lc);
                 if constexpr (RPW == 1) {
                     acc[0] += c;
                 } else {
@@ -329,7 +389,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs
         }
         const uint32_t row0 = u * RPW;
         if (!live) return;
-        if constexpr (EPI == Q4EPI_SWIGLU) {
+        if constexpr (KS > 1) {
+            // partial of chunk ks; the block adds the KS chunks after the loop
+            if (lane == 0) part[wr][i][ks] = res[0][0];
+        } else if constexpr (EPI == Q4EPI_SWIGLU) {
             if (lane < RPW) {
                 float gv = res[0][0], uv = res[1][0];
 #pragma unroll
@@ -348,40 +411,48 @@ __global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs
                 }
             }
         } else if (lane < RPW) {
-            // lane r stores row r of the group (res[] is wave-uniform)
+            // lane r stores row r of the unit (res[] is wave-uniform)
             float v = res[0][0];
 #pragma unroll
             for (int r = 1; r < RPW; ++r) v = (lane == r) ? res[0][r] : v;
-            const uint32_t row = row0 + lane;
-            int pi = 0;
-            pi += (a.n_parts > 1 && row >= a.parts[1].row_begin) ? 1 : 0;
-            pi += (a.n_parts > 2 && row >= a.parts[2].row_begin) ? 1 : 0;
-            const Q4Part& p = a.parts[pi];
-            const uint32_t local = row - p.row_begin;
-            if constexpr (EPI == Q4EPI_F32) {
-                reinterpret_cast<float*>(p.y)[local] = v;
-            } else if constexpr (EPI == Q4EPI_BF16) {
-                reinterpret_cast<uint16_t*>(p.y)[local] = (uint16_t)f32_to_bf16_bits(v);
-            } else if constexpr (EPI == Q4EPI_RESID) {
-                reinterpret_cast<float*>(p.y)[local] = a.residual[local] + v;
-            }
+            store_row(row0 + lane, v);
         }
     };
 
-    // ring over the units of this wave: issue unit i+NSTAGE-1, reduce unit i
+    if constexpr (UPW > 0) {
+        // every unit was issued up front: reduce them in order, no loop
+#pragma unroll
+        for (int s = 0; s < UPW; ++s) consume(s, wrow + s * total_wrows, st[s]);
+    } else
+    // ring over the units of this wave: reduce unit i, refill its stage with unit i+NSTAGE
     for (uint32_t i = 0; i < n_iter; i += NSTAGE) {
 #pragma unroll
         for (int s = 0; s < NSTAGE; ++s) {
             const uint32_t ui = i + s;
-            if (ui + NSTAGE - 1 < n_iter)
-                issue(clamp_unit(wave_global + (ui + NSTAGE - 1) * total_waves), st[(s + NSTAGE - 1) % NSTAGE]);
-            consume(wave_global + ui * total_waves, st[s]);
+            if (ui >= n_iter) break;  // wave-uniform
+            consume(ui, wrow + ui * total_wrows, st[s]);
+            if (ui + NSTAGE < n_iter) issue(clamp_unit(wrow + (ui + NSTAGE) * total_wrows), st[s]);
+        }
+    }
+
+    if constexpr (KS > 1) {
+        __syncthreads();
+        const uint32_t t = threadIdx.x;
+        if (t < (uint32_t)WR * a.units_per_wave) {
+            const uint32_t w = t / a.units_per_wave, i = t % a.units_per_wave;
+            const uint32_t u = (blockIdx.x * WR + w) + i * total_wrows;
+            if (u < a.n_units) {
+                float v = 0.0f;
+#pragma unroll
+                for (int k2 = 0; k2 < KS; ++k2) v += part[w][i][k2];
+                store_row(u, v);
+            }
         }
     }
 
     if constexpr (EPI == Q4EPI_ARGMAX) {
-        __shared__ float bs[16];
-        __shared__ uint32_t bt[16];
+        __shared__ float bs[WPB];
+        __shared__ uint32_t bt[WPB];
         if (lane == 0) {
             bs[wave] = best_score;
             bt[wave] = best_token;
@@ -390,7 +461,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs
         if (threadIdx.x == 0) {
             float s = bs[0];
             uint32_t t = bt[0];
-            for (int i = 1; i < waves_per_block; ++i) {
+            for (int i = 1; i < WPB; ++i) {
                 if (better_pair(bs[i], bt[i], s, t)) {
                     s = bs[i];
                     t = bt[i];
@@ -402,27 +473,22 @@ __global__ __launch_bounds__(GEMV_THREADS) void q4k_gemv_kernel(const Q4GemvArgs
     }
 }
 
-template <int PRO, int EPI>
-static hipError_t launch_nsb(uint32_t nsb, dim3 grid, dim3 block, const Q4GemvArgs& a, hipStream_t s) {
-    switch (nsb) {
-#define T2H_Q4_CASE(N)                                                                      \
-    case N:                                                                                 \
-        hipLaunchKernelGGL((q4k_gemv_kernel<N, PRO, EPI>), grid, block, 0, s, a); \
-        return hipGetLastError();
-        T2H_Q4_CASE(1)
-        T2H_Q4_CASE(2)
-        T2H_Q4_CASE(3)
-        T2H_Q4_CASE(4)
-        T2H_Q4_CASE(8)
-        T2H_Q4_CASE(12)
-        T2H_Q4_CASE(16)
-        T2H_Q4_CASE(24)
-        T2H_Q4_CASE(32)
-        T2H_Q4_CASE(48)
-#undef T2H_Q4_CASE
-        default:
-            return hipErrorInvalidValue;
+// Launch geometry of one row length: KS waves split each row when it is 32
+// or 48 superblocks long and the epilogue allows it; blocks hold WPB waves.
+struct Q4Geometry {
+    uint32_t ks;
+    uint32_t wpb;
+    uint32_t rpw;  // rows per unit
+    uint32_t wr() const { return wpb / ks; }
+};
+
+static uint32_t gcd_u32(uint32_t a, uint32_t b) {
+    while (b) {
+        const uint32_t t = a % b;
+        a = b;
+        b = t;
     }
+    return a;
 }
 
 static bool nsb_supported(uint32_t nsb) {
@@ -434,33 +500,82 @@ static bool nsb_supported(uint32_t nsb) {
     }
 }
 
-static uint32_t rows_per_group(uint32_t nsb) {
-    uint32_t a = nsb, b = 16;
-    while (b) {
-        const uint32_t t = a % b;
-        a = b;
-        b = t;
+static Q4Geometry q4_geometry(uint32_t nsb, int epi) {
+    Q4Geometry g;
+    const bool splittable = epi != Q4EPI_SWIGLU && epi != Q4EPI_ARGMAX;
+    g.ks = (splittable && (nsb == 32 || nsb == 48)) ? nsb / 16 : 1;
+    g.wpb = g.ks == 3 ? 12 : 8;
+    g.rpw = 16u / gcd_u32(nsb / g.ks, 16);
+    return g;
+}
+
+// Row lengths with straight-line kernels for 1..4 units per wave (the decode
+// shapes of Qwen3-0.6B and -8B); every other launch runs the ring loop.
+static bool q4_straight_line(uint32_t nsb, int epi) {
+    return epi != Q4EPI_ARGMAX && (nsb == 4 || nsb == 16 || nsb == 48);
+}
+
+template <int NSB, int KS, int WPB, int PRO, int EPI>
+static void launch_upw(uint32_t upw, dim3 grid, const Q4GemvArgs& a, hipStream_t s) {
+    const dim3 block(WPB * 64);
+    if constexpr (EPI != Q4EPI_ARGMAX && (NSB == 4 || NSB == 16 || NSB == 48)) {
+        switch (upw) {
+            case 1: hipLaunchKernelGGL((q4k_gemv_kernel<NSB, KS, WPB, PRO, EPI, 1>), grid, block, 0, s, a); return;
+            case 2: hipLaunchKernelGGL((q4k_gemv_kernel<NSB, KS, WPB, PRO, EPI, 2>), grid, block, 0, s, a); return;
+            case 3: hipLaunchKernelGGL((q4k_gemv_kernel<NSB, KS, WPB, PRO, EPI, 3>), grid, block, 0, s, a); return;
+            case 4: hipLaunchKernelGGL((q4k_gemv_kernel<NSB, KS, WPB, PRO, EPI, 4>), grid, block, 0, s, a); return;
+            default: break;
+        }
     }
-    return 16u / a;
+    hipLaunchKernelGGL((q4k_gemv_kernel<NSB, KS, WPB, PRO, EPI, 0>), grid, block, 0, s, a);
 }
 
-// Grid: enough blocks of 4 waves that every wave gets about `units_per_wave`
-// row groups, capped so that the launch stays a few blocks per CU.
-static uint32_t units_per_wave(uint32_t n_units, uint32_t blocks) {
-    const uint32_t waves = blocks * GEMV_WAVES;
-    return (n_units + waves - 1u) / waves;
+template <int PRO, int EPI>
+static hipError_t launch_nsb(uint32_t nsb, uint32_t ks, uint32_t upw, dim3 grid, const Q4GemvArgs& a,
+                             hipStream_t s) {
+    switch (nsb) {
+        case 1: launch_upw<1, 1, 8, PRO, EPI>(0, grid, a, s); break;
+        case 2: launch_upw<2, 1, 8, PRO, EPI>(0, grid, a, s); break;
+        case 3: launch_upw<3, 1, 8, PRO, EPI>(0, grid, a, s); break;
+        case 4: launch_upw<4, 1, 8, PRO, EPI>(upw, grid, a, s); break;
+        case 8: launch_upw<8, 1, 8, PRO, EPI>(0, grid, a, s); break;
+        case 12: launch_upw<12, 1, 8, PRO, EPI>(0, grid, a, s); break;
+        case 16: launch_upw<16, 1, 8, PRO, EPI>(upw, grid, a, s); break;
+        case 24: launch_upw<24, 1, 8, PRO, EPI>(0, grid, a, s); break;
+        case 32:
+            if constexpr (EPI == Q4EPI_SWIGLU || EPI == Q4EPI_ARGMAX) launch_upw<32, 1, 8, PRO, EPI>(0, grid, a, s);
+            else if (ks == 2) launch_upw<32, 2, 8, PRO, EPI>(0, grid, a, s);
+            else return hipErrorInvalidValue;
+            break;
+        case 48:
+            if constexpr (EPI == Q4EPI_SWIGLU || EPI == Q4EPI_ARGMAX) launch_upw<48, 1, 8, PRO, EPI>(0, grid, a, s);
+            else if (ks == 3) launch_upw<48, 3, 12, PRO, EPI>(upw, grid, a, s);
+            else return hipErrorInvalidValue;
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
-static uint32_t pick_blocks(uint32_t n_units, uint32_t max_blocks) {
-    if (max_blocks == 0) max_blocks = 1;
-    const uint32_t u = units_per_wave(n_units, max_blocks);
-    uint32_t blocks = (n_units + GEMV_WAVES * u - 1u) / (GEMV_WAVES * u);
-    if (blocks == 0) blocks = 1;
-    return blocks;
+// Grid: wave rows of `units_per_wave` units each, at most `max_blocks` blocks
+// (more when a split-row launch caps its units per wave).
+static uint32_t units_per_wave_for(uint32_t n_units, uint32_t blocks, const Q4Geometry& g) {
+    const uint32_t wrows = blocks * g.wr();
+    uint32_t u = (n_units + wrows - 1u) / wrows;
+    if (g.ks > 1 && u > Q4_KSPLIT_MAX_UNITS) u = Q4_KSPLIT_MAX_UNITS;
+    return u ? u : 1u;
 }
 
-static uint32_t g_max_blocks = 256;        // blocks of GEMV_WAVES waves, plain x input
-static uint32_t g_max_blocks_norm = 256;   // RMSNorm prologue: each block re-reads h and the norm weight
+static uint32_t blocks_for(uint32_t n_units, uint32_t upw, const Q4Geometry& g) {
+    const uint32_t per_block = g.wr() * upw;
+    const uint32_t b = (n_units + per_block - 1u) / per_block;
+    return b ? b : 1u;
+}
+
+// Grid caps in blocks (tuned on MI355X at the Qwen3-8B decode shapes).
+static uint32_t g_max_blocks = 256;       // plain bf16 x
+static uint32_t g_max_blocks_norm = 256;  // fused RMSNorm prologue
 
 }  // namespace t2h
 
@@ -479,24 +594,36 @@ extern "C" int t2h_set_gemv_max_blocks(uint32_t max_blocks, uint32_t max_blocks_
     return T2H_OK;
 }
 
-static int q4k_launch(int pro, int epi, Q4GemvArgs a, uint32_t nsb, uint32_t blocks, hipStream_t s) {
+// Launch over `max_blocks` (or exactly `fixed_blocks` blocks when non-zero).
+static int q4k_launch(int pro, int epi, Q4GemvArgs a, uint32_t nsb, uint32_t max_blocks, uint32_t fixed_blocks,
+                      hipStream_t s) {
     if (a.n_units == 0) return T2H_OK;
-    a.units_per_wave = units_per_wave(a.n_units, blocks);
-    const dim3 grid(blocks), block(GEMV_THREADS);
+    const Q4Geometry geo = q4_geometry(nsb, epi);
+    uint32_t blocks;
+    if (fixed_blocks) {
+        blocks = fixed_blocks;
+        a.units_per_wave = units_per_wave_for(a.n_units, blocks, geo);
+        if (blocks_for(a.n_units, a.units_per_wave, geo) > blocks) return T2H_ERR_ARG;
+    } else {
+        a.units_per_wave = units_per_wave_for(a.n_units, max_blocks ? max_blocks : 1u, geo);
+        blocks = blocks_for(a.n_units, a.units_per_wave, geo);
+    }
+    const dim3 grid(blocks);
+    const uint32_t upw = q4_straight_line(nsb, epi) && a.units_per_wave <= 4 ? a.units_per_wave : 0;
     hipError_t e = hipErrorInvalidValue;
     if (pro == Q4PRO_BF16) {
         switch (epi) {
-            case Q4EPI_F32: e = launch_nsb<Q4PRO_BF16, Q4EPI_F32>(nsb, grid, block, a, s); break;
-            case Q4EPI_BF16: e = launch_nsb<Q4PRO_BF16, Q4EPI_BF16>(nsb, grid, block, a, s); break;
-            case Q4EPI_RESID: e = launch_nsb<Q4PRO_BF16, Q4EPI_RESID>(nsb, grid, block, a, s); break;
-            case Q4EPI_ARGMAX: e = launch_nsb<Q4PRO_BF16, Q4EPI_ARGMAX>(nsb, grid, block, a, s); break;
+            case Q4EPI_F32: e = launch_nsb<Q4PRO_BF16, Q4EPI_F32>(nsb, geo.ks, upw, grid, a, s); break;
+            case Q4EPI_BF16: e = launch_nsb<Q4PRO_BF16, Q4EPI_BF16>(nsb, geo.ks, upw, grid, a, s); break;
+            case Q4EPI_RESID: e = launch_nsb<Q4PRO_BF16, Q4EPI_RESID>(nsb, geo.ks, upw, grid, a, s); break;
+            case Q4EPI_ARGMAX: e = launch_nsb<Q4PRO_BF16, Q4EPI_ARGMAX>(nsb, geo.ks, upw, grid, a, s); break;
             default: return T2H_ERR_ARG;
         }
     } else {
         switch (epi) {
-            case Q4EPI_F32: e = launch_nsb<Q4PRO_RMSNORM, Q4EPI_F32>(nsb, grid, block, a, s); break;
-            case Q4EPI_SWIGLU: e = launch_nsb<Q4PRO_RMSNORM, Q4EPI_SWIGLU>(nsb, grid, block, a, s); break;
-            case Q4EPI_ARGMAX: e = launch_nsb<Q4PRO_RMSNORM, Q4EPI_ARGMAX>(nsb, grid, block, a, s); break;
+            case Q4EPI_F32: e = launch_nsb<Q4PRO_RMSNORM, Q4EPI_F32>(nsb, geo.ks, upw, grid, a, s); break;
+            case Q4EPI_SWIGLU: e = launch_nsb<Q4PRO_RMSNORM, Q4EPI_SWIGLU>(nsb, geo.ks, upw, grid, a, s); break;
+            case Q4EPI_ARGMAX: e = launch_nsb<Q4PRO_RMSNORM, Q4EPI_ARGMAX>(nsb, geo.ks, upw, grid, a, s); break;
             default: return T2H_ERR_ARG;
         }
     }
@@ -532,8 +659,6 @@ extern "C" int t2h_q4k_matvec(const void* x, const void* w, void* y, int out_dty
     if (st) return st;
     if (m == 0 || n == 0) return T2H_OK;
     const uint32_t nsb = k / 256;
-    const uint32_t rpw = rows_per_group(nsb);
-    if (n % rpw != 0) return T2H_ERR_SHAPE;
     int epi;
     if (residual) {
         if (out_dtype != T2H_DTYPE_F32) return T2H_ERR_DTYPE;
@@ -545,6 +670,8 @@ extern "C" int t2h_q4k_matvec(const void* x, const void* w, void* y, int out_dty
     } else {
         return T2H_ERR_DTYPE;
     }
+    const uint32_t rpw = q4_geometry(nsb, epi).rpw;
+    if (n % rpw != 0) return T2H_ERR_SHAPE;
     const size_t out_size = out_dtype == T2H_DTYPE_F32 ? 4 : 2;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     for (uint32_t row = 0; row < m; ++row) {
@@ -557,7 +684,7 @@ extern "C" int t2h_q4k_matvec(const void* x, const void* w, void* y, int out_dty
         a.x = reinterpret_cast<const uint16_t*>(x) + (size_t)row * k;
         a.residual = residual ? residual + (size_t)row * n : nullptr;
         a.n_units = total / rpw;
-        st = q4k_launch(Q4PRO_BF16, epi, a, nsb, pick_blocks(a.n_units, g_max_blocks), s);
+        st = q4k_launch(Q4PRO_BF16, epi, a, nsb, g_max_blocks, 0, s);
         if (st) return st;
     }
     return T2H_OK;
@@ -570,16 +697,7 @@ extern "C" int t2h_q4k_matvec_multi(const void* x, const float* norm_w, float ep
     int st = validate_q4(k);
     if (st) return st;
     const uint32_t nsb = k / 256;
-    const uint32_t rpw = rows_per_group(nsb);
-    Q4GemvArgs a = {};
-    uint32_t total = 0;
-    st = fill_parts(a, n_parts, w, y, n, rpw, &total);
-    if (st) return st;
-    a.x = x;
-    a.norm_w = norm_w;
-    a.eps = eps;
-    a.n_units = total / rpw;
-    int pro = norm_w ? Q4PRO_RMSNORM : Q4PRO_BF16;
+    const int pro = norm_w ? Q4PRO_RMSNORM : Q4PRO_BF16;
     int epi;
     if (out_dtype == T2H_DTYPE_F32) {
         epi = Q4EPI_F32;
@@ -588,7 +706,16 @@ extern "C" int t2h_q4k_matvec_multi(const void* x, const float* norm_w, float ep
     } else {
         return T2H_ERR_DTYPE;
     }
-    return q4k_launch(pro, epi, a, nsb, pick_blocks(a.n_units, norm_w ? g_max_blocks_norm : g_max_blocks),
+    const uint32_t rpw = q4_geometry(nsb, epi).rpw;
+    Q4GemvArgs a = {};
+    uint32_t total = 0;
+    st = fill_parts(a, n_parts, w, y, n, rpw, &total);
+    if (st) return st;
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.n_units = total / rpw;
+    return q4k_launch(pro, epi, a, nsb, norm_w ? g_max_blocks_norm : g_max_blocks, 0,
                       reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -599,7 +726,7 @@ extern "C" int t2h_q4k_rmsnorm_swiglu_matvec(const float* h, const float* norm_w
     int st = validate_q4(k);
     if (st) return st;
     const uint32_t nsb = k / 256;
-    const uint32_t rpw = rows_per_group(nsb);
+    const uint32_t rpw = q4_geometry(nsb, Q4EPI_SWIGLU).rpw;
     Q4GemvArgs a = {};
     const void* wv[2] = {w_gate, w_up};
     void* yv[2] = {act_out, act_out};
@@ -611,7 +738,7 @@ extern "C" int t2h_q4k_rmsnorm_swiglu_matvec(const float* h, const float* norm_w
     a.norm_w = norm_w;
     a.eps = eps;
     a.n_units = n / rpw;
-    return q4k_launch(Q4PRO_RMSNORM, Q4EPI_SWIGLU, a, nsb, pick_blocks(a.n_units, g_max_blocks_norm),
+    return q4k_launch(Q4PRO_RMSNORM, Q4EPI_SWIGLU, a, nsb, g_max_blocks_norm, 0,
                       reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -622,7 +749,7 @@ extern "C" int t2h_q4k_lm_head_argmax_partial(const void* x, const float* norm_w
     int st = validate_q4(k);
     if (st) return st;
     const uint32_t nsb = k / 256;
-    const uint32_t rpw = rows_per_group(nsb);
+    const uint32_t rpw = q4_geometry(nsb, Q4EPI_ARGMAX).rpw;
     if (num_partials == 0) return T2H_ERR_ARG;
     Q4GemvArgs a = {};
     const void* wv[1] = {w};
@@ -635,6 +762,6 @@ extern "C" int t2h_q4k_lm_head_argmax_partial(const void* x, const float* norm_w
     a.n_units = n / rpw;
     a.partial_scores = partial_scores;
     a.partial_tokens = partial_tokens;
-    return q4k_launch(norm_w ? Q4PRO_RMSNORM : Q4PRO_BF16, Q4EPI_ARGMAX, a, nsb, num_partials,
+    return q4k_launch(norm_w ? Q4PRO_RMSNORM : Q4PRO_BF16, Q4EPI_ARGMAX, a, nsb, 0, num_partials,
                       reinterpret_cast<hipStream_t>(stream));
 }
