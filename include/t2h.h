@@ -167,8 +167,9 @@ int t2h_token_select_store(const float* scores, const uint32_t* tokens, uint32_t
  * *cache_position.  The new K/V row is written at *cache_position (if
  * < s_cap) and attention covers positions 0..min(*cache_position, s_cap-1).
  * out bf16 [nh, d].  workspace: t2h_attn_decode_workspace_bytes() bytes of
- * per-chunk partials (no initialisation needed).  Two launches: the split-K
- * pass and a log-sum-exp merge.
+ * per-chunk partials (no initialisation needed); calls sharing one workspace
+ * must not overlap in time.  Two launches: the split-K pass and a
+ * log-sum-exp merge.
  * replaces RMS_NORM_ROPE_TRANSPOSE_F16 x2 (src/models/optimized_qwen3/shaders/rms_norm_rope_transpose_f16.py:22-145),
  * ROPE_TABLE_F32 (src/torch2vk/runtime/rope_table.py:32-122) and
  * SDPA_DECODE_CACHE_WRITE_F32 (src/models/optimized_qwen3/shaders/sdpa_decode_cache_write_f32.py:22-170). */

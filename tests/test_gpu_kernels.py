@@ -294,6 +294,31 @@ def test_attn_decode_without_norm_rope_and_reuse(device):
     assert_close(got, ref, max_abs=2e-2, min_cos=0.999, what="second call")
 
 
+def test_attn_decode_workspace_reuse(device):
+    """One workspace across calls whose chunk counts differ: stale partials of a longer call must not leak."""
+    from torch2vk_amd import kernels
+
+    nh, nk, d, s_cap = 32, 8, 128, 1100
+    ws = kernels.attn_decode_workspace(nh, nk, d, s_cap, device)
+    for i, pos in enumerate((1000, 5, 640, 129, 1099, 0)):
+        print(f"attn_decode reuse call {i} pos={pos}", flush=True)
+        rng = np.random.default_rng(100 + i)
+        kc = R.bf16_round(rng.standard_normal((s_cap, nk, d)).astype(np.float32))
+        vc = R.bf16_round(rng.standard_normal((s_cap, nk, d)).astype(np.float32))
+        q = rng.standard_normal((nh, d)).astype(np.float32)
+        kn = rng.standard_normal((nk, d)).astype(np.float32)
+        vn = rng.standard_normal((nk, d)).astype(np.float32)
+        kref, vref = kc.copy(), vc.copy()
+        kref[pos] = R.bf16_round(kn)
+        vref[pos] = R.bf16_round(vn)
+        ref = R.attention_ref(q.astype(np.float64)[None], kref[:pos + 1], vref[:pos + 1])[0]
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+        out = torch.empty(nh, d, dtype=torch.bfloat16, device=device)
+        kernels.attn_decode(t(q), t(kn), t(vn), t(kc).to(torch.bfloat16), t(vc).to(torch.bfloat16), out,
+                            torch.tensor([pos], dtype=torch.int32, device=device), ws)
+        assert_close(out.float().cpu().numpy(), ref, max_abs=2e-2, min_cos=0.999, what=f"call {i}")
+
+
 def test_rms_norm_and_swiglu(device):
     from torch2vk_amd import kernels
 

@@ -8,20 +8,19 @@
 //       src/models/optimized_qwen3/shaders/sdpa_decode_cache_write_f32.py:22-170
 //
 // The reference walks the whole cache serially in one workgroup per q head.
-// Here a block of two waves owns (kv head, 128-position chunk); each wave
-// takes 64 positions for all GROUP q heads of the kv head, so every K/V byte
-// is read once per token:
-//   * K rows are loaded coalesced (4 rows per instruction) and staged in a
-//     padded LDS tile; a lane then owns one position and dots its row with
-//     the GROUP q vectors (broadcast from LDS);
+// Here a block of 8 waves owns (kv head, 128-position chunk); each wave takes
+// 16 positions for all GROUP q heads of the kv head, so every K/V byte is read
+// once per token:
+//   * K rows are loaded coalesced (4 lanes per row, 64 B each) and a lane
+//     dots its quarter row with the GROUP q vectors (broadcast from LDS);
 //   * V is loaded coalesced straight into registers in the P.V layout (lane
 //     owns two dims, one register per position);
-//   * the two waves' partial softmax states are merged in LDS and the block's
-//     (max, sum, unnormalised output) is published;
+//   * the waves' partial softmax states are merged in LDS and the block's
+//     (max, sum, unnormalised output) is published to the workspace;
 //   * a second small kernel merges the partials of each q head with the
-//     log-sum-exp rule.  Merging in a separate launch, rather than in the
-//     last block to finish, keeps device-scope fences (an L2 write-back and
-//     invalidate per block on this multi-XCD part) out of the main kernel.
+//     log-sum-exp rule.  Merging in the last block to finish would need
+//     device-scope release/acquire: on this multi-XCD part that is an L2
+//     write-back plus invalidate per block, measured far slower than a launch.
 //
 // Cache layout (as the reference's optimized decode cache): bf16
 // [S_cap, NK, D], token-major.  q/k/v inputs are the fp32 QKV projections.
@@ -112,6 +111,8 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
     const int last_pos = L - 1;
     const bool has_new = pos < S && pos >= pw && pos < pw + AD_WAVE_POS;  // wave-uniform
     const int rnew = pos - pw;
+    const bool rope = a.theta > 0.0f;
+    const bool needs_rope = wave < GROUP || has_new;  // wave-uniform
 
     // 0. the small operands first: vmcnt retires in order, so anything loaded
     //    after the cache stream would wait for all of it
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
         qx1 = a.q[h * AD_D + lane + 64];
     }
     float qw0 = 1.0f, qw1 = 1.0f, kw0 = 1.0f, kw1 = 1.0f;
-    if (has_w) {
+    if (has_w && needs_rope) {
         qw0 = a.q_norm_w[lane];
         qw1 = a.q_norm_w[lane + 64];
         kw0 = a.k_norm_w[lane];
@@ -157,13 +158,11 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
         vr[i] = reinterpret_cast<const uint32_t*>(vbase + (size_t)p * row_stride)[lane];
     }
 
-    // 2. RoPE at `pos` (lane = frequency index); q head `wave` normalised,
-    //    rotated, pre-scaled by 1/sqrt(D) into LDS
-    const bool rope = a.theta > 0.0f;
+    // 2. RoPE at `pos` (lane = frequency index, inv_freq = theta^(-2 lane / D));
+    //    q head `wave` normalised, rotated, pre-scaled by 1/sqrt(D) into LDS
     float cs = 1.0f, sn = 0.0f;
-    if (rope) {
-        const float exponent = (2.0f * (float)lane) / (float)AD_D;
-        const float inv_freq = powf(a.theta, -exponent);
+    if (rope && needs_rope) {
+        const float inv_freq = exp2f(-(2.0f * (float)lane / (float)AD_D) * log2f(a.theta));
         const float angle = (float)pos * inv_freq;
         sincosf(angle, &sn, &cs);
     }
@@ -269,7 +268,8 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
         }
     }
     __syncthreads();
-    const size_t cbase = ((size_t)kvh * a.max_chunks + c) * GROUP;
+    const size_t kv_base = (size_t)kvh * a.max_chunks * GROUP;  // first partial of this kv head
+    const size_t cbase = kv_base + (size_t)c * GROUP;
     for (int idx = tid; idx < GROUP * 64; idx += AD_WAVES * 64) {
         const int g = idx >> 6;
         const int dl = idx & 63;
@@ -289,6 +289,7 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
         *reinterpret_cast<float2*>(&a.part_o[(cbase + g) * AD_D + 2 * dl]) = make_float2(r0, r1);
         if (dl == 0) *reinterpret_cast<float2*>(&a.part_ml[(cbase + g) * 2]) = make_float2(M, l);
     }
+
 }
 
 // Log-sum-exp merge of the per-chunk partials: one block per q head, each of
