@@ -179,6 +179,25 @@ int t2h_attn_decode(const float* q, const float* k_new, const float* v_new, cons
                     uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap, const int32_t* cache_position,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* -------------------------------------------------- prefill attention --- */
+/* out = softmax(q.k^T * scale + mask) . v on the matrix cores (bf16 in, fp32
+ * scores and accumulation, bf16 out).  q, out: [batch, t_len, nh, d] and k, v:
+ * [batch, s_len, nk, d] addressed through strides (in elements, all >= 0):
+ *   strides[0..2]  q   (batch, token, head)     strides[3..5]  k
+ *   strides[6..8]  v                             strides[9..11] out
+ *   strides[12..13] mask (batch, query row); the key index is contiguous.
+ * The head dimension is contiguous (d = 64 or 128).  GQA: kv head = h / (nh/nk).
+ * causal != 0: query t sees keys <= t + causal_offset.  mask: additive fp32
+ * (natural-log units) or NULL.  scale <= 0 means 1/sqrt(d).  Alignment: q, k
+ * 16 B with their strides multiples of 8; v, out 8 B with strides multiples of 4.
+ * A query that sees no key gets zeros.
+ * replaces LLAMA_FLASH_ATTN_F32_F16_F16 (src/models/optimized_qwen3/shaders/llama_flash_attn_f32_f16_f16.py:35-175),
+ * SDPA_CAUSAL_F32 (src/models/quantized_qwen3/shaders/sdpa_causal_f32.py:22-142) and
+ * SDPA_MASKED_F32 (src/models/optimized_qwen3_asr/shaders/sdpa_masked_f32.py). */
+int t2h_flash_attn_prefill(const void* q, const void* k, const void* v, void* out, const float* mask, uint32_t batch,
+                           uint32_t nh, uint32_t nk, uint32_t t_len, uint32_t s_len, uint32_t d,
+                           const int64_t* strides, int causal, int32_t causal_offset, float scale, void* stream);
+
 /* ------------------------------------------------------ small ops ------ */
 /* replaces EMBEDDING_Q4_K_F32 (src/models/quantized_qwen3/shaders/embedding_q4_k_f32.py:62-121); out fp32 [n_ids, dim] */
 int t2h_embedding_q4_k(const void* w, uint64_t vocab, const int64_t* ids, uint32_t n_ids, uint32_t dim, float* out,

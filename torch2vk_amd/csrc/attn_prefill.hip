@@ -1,0 +1,349 @@
+// Flash attention for prefill / encoders on the gfx950 matrix cores.
+//
+// Replaces the reference's prefill attention shaders:
+//   LLAMA_FLASH_ATTN_F32_F16_F16 (+ FA_MASK_OPT_F16)  token-major q/k/v, additive mask
+//       src/models/optimized_qwen3/shaders/llama_flash_attn_f32_f16_f16.py:35-175
+//   SDPA_CAUSAL_F32      head-major, causal      src/models/quantized_qwen3/shaders/sdpa_causal_f32.py:22-142
+//   SDPA_MASKED_F32      head-major, additive mask (the Qwen3-ASR audio encoder)
+//       src/models/optimized_qwen3_asr/shaders/sdpa_masked_f32.py
+// Every tensor is addressed through (batch, token, head) strides with the
+// head dimension contiguous, so both layouts run through one kernel.
+//
+// Math: out[b,t,h] = softmax(q.k^T * scale + mask) v over the keys a query may
+// see (causal: key <= t + causal_offset), GQA kv head = h / (NH / NK); fp32
+// scores, running max and sum, bf16 P, fp32 output accumulation.
+//
+// Work mapping.  A block of 4 waves takes 128 queries of one (batch, head);
+// wave w owns 32 of them.  Keys stream through LDS 64 at a time, double
+// buffered: the next tile's K rows and V columns are in flight to registers
+// while the matrix cores work on the current one.
+//   * S^T = K . Q^T on v_mfma_f32_32x32x16_bf16: K rows come from LDS, the
+//     wave's Q^T columns stay in registers for the whole pass.  In the
+//     accumulator layout a lane then holds one query's scores for 16 keys, so
+//     the row max and sum are in-lane plus one exchange between the two
+//     half-waves (the other 16 keys of each 32).
+//   * O^T += V^T . P^T: the accumulator registers of S^T, scaled, exponentiated
+//     and packed to bf16, are already the B operand of the second product when
+//     its 16 k-slots are assigned to the keys each lane holds; the A operand
+//     reads V^T from LDS with the same key order.  V is transposed on its way
+//     into LDS: each thread loads a 4 keys x 4 dims block and swaps halves with
+//     v_perm_b32.
+// Operand layout of v_mfma_f32_32x32x16_bf16: lane l supplies row (l % 32) of
+// A and column (l % 32) of B, 8 consecutive k each, k = 8 (l / 32) + j; its 16
+// results are C[8(i/4) + 4(l/32) + i%4][l % 32].
+#include "common.h"
+
+namespace t2h {
+
+typedef __bf16 fa_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float fa_f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int FA_WAVES = 4;
+constexpr int FA_THREADS = FA_WAVES * 64;
+constexpr int FA_BM = 32 * FA_WAVES;  // queries per block
+constexpr int FA_BN = 64;             // keys per tile
+constexpr int FA_VROW = FA_BN + 8;    // LDS V^T row length (bf16)
+constexpr float FA_LOG2E = 1.4426950408889634f;
+
+struct FaArgs {
+    const uint16_t* q;  // bf16
+    const uint16_t* k;
+    const uint16_t* v;
+    uint16_t* out;
+    const float* mask;  // additive, natural-log units; null = none
+    size_t q_sb, q_st, q_sh;
+    size_t k_sb, k_st, k_sh;
+    size_t v_sb, v_st, v_sh;
+    size_t o_sb, o_st, o_sh;
+    size_t m_sb, m_st;
+    uint32_t nh;
+    uint32_t group;  // q heads per kv head
+    uint32_t t_len;
+    uint32_t s_len;
+    int32_t causal_offset;
+    float scale_log2;  // softmax scale * log2(e)
+};
+
+__device__ __forceinline__ fa_bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_bit_cast(fa_bf16x8_t, make_uint4(a, b, c, d));
+}
+
+template <int D, bool CAUSAL, bool MASK>
+__global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) {
+    constexpr int KROW = D + 8;                                // LDS K row length (bf16)
+    constexpr int DS = D / 16;                                 // k-steps of S^T
+    constexpr int DB = D / 32;                                 // 32-dim blocks of O^T
+    constexpr int KCH = FA_BN * D / 8 / FA_THREADS;            // 16-B K chunks per thread
+    constexpr int VBL = (FA_BN / 4) * (D / 4) / FA_THREADS;    // 4x4 V blocks per thread
+    static_assert(KCH >= 1 && VBL >= 1, "tile too small for the block");
+    __shared__ __align__(16) uint16_t ks[2][FA_BN * KROW];
+    __shared__ __align__(16) uint16_t vts[2][D * FA_VROW];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int half = lane >> 5;
+    const int h = blockIdx.y % a.nh;
+    const int b = blockIdx.y / a.nh;
+    const int kvh = h / a.group;
+    const int q0 = blockIdx.x * FA_BM;
+    const int qi = q0 + 32 * wave + (lane & 31);  // this lane's query
+    const bool q_valid = qi < (int)a.t_len;
+    const int qc = q_valid ? qi : (int)a.t_len - 1;
+    const int s_len = (int)a.s_len;
+
+    int s_end = s_len;
+    if constexpr (CAUSAL) {
+        const int q_last = min(q0 + FA_BM, (int)a.t_len) - 1;
+        s_end = min(s_end, q_last + a.causal_offset + 1);
+    }
+    const int n_tiles = s_end > 0 ? (s_end + FA_BN - 1) / FA_BN : 0;
+
+    // Q^T columns of this lane's query: dims 16 s + 8 half .. +7
+    const uint16_t* qrow = a.q + (size_t)b * a.q_sb + (size_t)qc * a.q_st + (size_t)h * a.q_sh;
+    fa_bf16x8_t qf[DS];
+#pragma unroll
+    for (int s = 0; s < DS; ++s) qf[s] = *reinterpret_cast<const fa_bf16x8_t*>(qrow + 16 * s + 8 * half);
+
+    const uint16_t* kb_ptr = a.k + (size_t)b * a.k_sb + (size_t)kvh * a.k_sh;
+    const uint16_t* vb_ptr = a.v + (size_t)b * a.v_sb + (size_t)kvh * a.v_sh;
+    uint4 kreg[KCH];
+    uint2 vreg[VBL][4];
+    auto load_tile = [&](int t0) {
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = tid + FA_THREADS * i;
+            const int key = min(t0 + c / (D / 8), s_len - 1);
+            kreg[i] = load_u4(kb_ptr + (size_t)key * a.k_st + (c % (D / 8)) * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < VBL; ++i) {
+            const int bi = tid + FA_THREADS * i;
+            const int dg = bi % (D / 4);
+            const int kg = bi / (D / 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = min(t0 + 4 * kg + r, s_len - 1);
+                vreg[i][r] = *reinterpret_cast<const uint2*>(vb_ptr + (size_t)key * a.v_st + 4 * dg);
+            }
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = tid + FA_THREADS * i;
+            *reinterpret_cast<uint4*>(&ks[buf][(c / (D / 8)) * KROW + (c % (D / 8)) * 8]) = kreg[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VBL; ++i) {
+            const int bi = tid + FA_THREADS * i;
+            const int dg = bi % (D / 4);
+            const int kg = bi / (D / 4);
+            const uint2* r = vreg[i];
+            // rows of 4 keys x (d0 d1 | d2 d3) -> columns of 4 dims x (k0 k1 | k2 k3)
+            const uint2 d0 = make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, 0x05040100u),
+                                        __builtin_amdgcn_perm(r[3].x, r[2].x, 0x05040100u));
+            const uint2 d1 = make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, 0x07060302u),
+                                        __builtin_amdgcn_perm(r[3].x, r[2].x, 0x07060302u));
+            const uint2 d2 = make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, 0x05040100u),
+                                        __builtin_amdgcn_perm(r[3].y, r[2].y, 0x05040100u));
+            const uint2 d3 = make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, 0x07060302u),
+                                        __builtin_amdgcn_perm(r[3].y, r[2].y, 0x07060302u));
+            uint16_t* dst = &vts[buf][(4 * dg) * FA_VROW + 4 * kg];
+            *reinterpret_cast<uint2*>(dst) = d0;
+            *reinterpret_cast<uint2*>(dst + FA_VROW) = d1;
+            *reinterpret_cast<uint2*>(dst + 2 * FA_VROW) = d2;
+            *reinterpret_cast<uint2*>(dst + 3 * FA_VROW) = d3;
+        }
+    };
+
+    fa_f32x16_t o[DB];
+#pragma unroll
+    for (int i = 0; i < DB; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[i][e] = 0.0f;
+    float m_run = -INFINITY;  // log2-domain running max of this lane's query
+    float l_part = 0.0f;      // this half-wave's share of the running sum
+
+    if (n_tiles > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    const float* mrow = nullptr;
+    if constexpr (MASK) mrow = a.mask + (size_t)b * a.m_sb + (size_t)qc * a.m_st;
+
+    for (int t = 0; t < n_tiles; ++t) {
+        const int buf = t & 1;
+        const int t0 = t * FA_BN;
+        if (t + 1 < n_tiles) load_tile(t0 + FA_BN);
+
+        // S^T for two 32-key blocks
+        fa_f32x16_t s[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
+            const uint16_t* krow = &ks[buf][(32 * kb + (lane & 31)) * KROW + 8 * half];
+#pragma unroll
+            for (int st = 0; st < DS; ++st) {
+                const fa_bf16x8_t kf = *reinterpret_cast<const fa_bf16x8_t*>(krow + 16 * st);
+                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kb], 0, 0, 0);
+            }
+        }
+
+        // scale to log2 units, mask, tile max of this query
+        float mt = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int key = t0 + 32 * kb + 8 * (e >> 2) + 4 * half + (e & 3);
+                float x = s[kb][e] * a.scale_log2;
+                if constexpr (MASK) x = fmaf(mrow[min(key, s_len - 1)], FA_LOG2E, x);
+                bool ok = key < s_len;
+                if constexpr (CAUSAL) ok = ok && key <= qi + a.causal_offset;
+                x = ok ? x : -INFINITY;
+                s[kb][e] = x;
+                mt = fmaxf(mt, x);
+            }
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 32, T2H_WAVE));
+        const float m_new = fmaxf(m_run, mt);
+        const bool none = m_new == -INFINITY;  // nothing visible yet: o and l stay zero
+        const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        const float msub = none ? 0.0f : m_new;
+        m_run = m_new;
+
+        // P = 2^(S - m), packed to bf16 in k-slot order, and its sum
+        uint32_t pk[2][8];
+        float lsum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int e = 0; e < 16; e += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(s[kb][e] - msub);
+                const float p1 = __builtin_amdgcn_exp2f(s[kb][e + 1] - msub);
+                lsum += p0 + p1;
+                pk[kb][e / 2] = pack_bf16x2(p0, p1);
+            }
+        }
+        l_part = fmaf(l_part, alpha, lsum);
+#pragma unroll
+        for (int i = 0; i < DB; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+
+        // O^T += V^T . P^T: k-step (kb, stp) covers the keys of accumulator
+        // entries 8 stp .. 8 stp + 7 of block kb:
+        //   32 kb + 16 stp + 4 half + 0..3  and  32 kb + 16 stp + 8 + 4 half + 0..3
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int stp = 0; stp < 2; ++stp) {
+                const fa_bf16x8_t pf =
+                    as_bf16x8(pk[kb][4 * stp], pk[kb][4 * stp + 1], pk[kb][4 * stp + 2], pk[kb][4 * stp + 3]);
+                const uint16_t* vcol = &vts[buf][(lane & 31) * FA_VROW + 32 * kb + 16 * stp + 4 * half];
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    const uint2 va = *reinterpret_cast<const uint2*>(vcol + 32 * db * FA_VROW);
+                    const uint2 vb = *reinterpret_cast<const uint2*>(vcol + 32 * db * FA_VROW + 8);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(va.x, va.y, vb.x, vb.y), pf, o[db],
+                                                                   0, 0, 0);
+                }
+            }
+        }
+        // the other buffer was last read in iteration t - 1, before the barrier that ended it
+        if (t + 1 < n_tiles) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    const float l = l_part + __shfl_xor(l_part, 32, T2H_WAVE);
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    if (q_valid) {
+        uint16_t* orow = a.out + (size_t)b * a.o_sb + (size_t)qi * a.o_st + (size_t)h * a.o_sh;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int dim = 32 * db + 8 * g + 4 * half;
+                const uint32_t lo = pack_bf16x2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
+                const uint32_t hi = pack_bf16x2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+                *reinterpret_cast<uint2*>(orow + dim) = make_uint2(lo, hi);
+            }
+        }
+    }
+}
+
+template <int D>
+static void fa_launch(bool causal, bool mask, dim3 grid, const FaArgs& a, hipStream_t s) {
+    const dim3 block(FA_THREADS);
+    if (causal) {
+        if (mask) hipLaunchKernelGGL((fa_prefill_kernel<D, true, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((fa_prefill_kernel<D, true, false>), grid, block, 0, s, a);
+    } else {
+        if (mask) hipLaunchKernelGGL((fa_prefill_kernel<D, false, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((fa_prefill_kernel<D, false, false>), grid, block, 0, s, a);
+    }
+}
+
+}  // namespace t2h
+
+using namespace t2h;
+
+extern "C" int t2h_flash_attn_prefill(const void* q, const void* k, const void* v, void* out, const float* mask,
+                                      uint32_t batch, uint32_t nh, uint32_t nk, uint32_t t_len, uint32_t s_len,
+                                      uint32_t d, const int64_t* strides, int causal, int32_t causal_offset,
+                                      float scale, void* stream) {
+    if (!q || !k || !v || !out || !strides) return T2H_ERR_NULL;
+    if (d != 64 && d != 128) return T2H_ERR_UNSUPPORTED;
+    if (nh == 0 || nk == 0 || nh % nk != 0) return T2H_ERR_SHAPE;
+    if (batch == 0 || t_len == 0) return T2H_OK;
+    if (s_len == 0) return T2H_ERR_SHAPE;
+    if ((size_t)batch * nh > 65535u || t_len > 0x7fffffffu - FA_BM || s_len > 0x7fffffffu) return T2H_ERR_SHAPE;
+    for (int i = 0; i < 14; ++i)
+        if (strides[i] < 0) return T2H_ERR_ARG;
+    // 16-B q/k rows, 8-B v and out rows: pointers and (b, t, h) strides in elements
+    const uintptr_t align_bits = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k);
+    if ((align_bits & 15) != 0 || (reinterpret_cast<uintptr_t>(v) & 7) != 0 ||
+        (reinterpret_cast<uintptr_t>(out) & 7) != 0)
+        return T2H_ERR_ALIGN;
+    for (int i = 0; i < 6; ++i)
+        if (strides[i] % 8 != 0) return T2H_ERR_ALIGN;
+    for (int i = 6; i < 12; ++i)
+        if (strides[i] % 4 != 0) return T2H_ERR_ALIGN;
+    FaArgs a;
+    a.q = reinterpret_cast<const uint16_t*>(q);
+    a.k = reinterpret_cast<const uint16_t*>(k);
+    a.v = reinterpret_cast<const uint16_t*>(v);
+    a.out = reinterpret_cast<uint16_t*>(out);
+    a.mask = mask;
+    a.q_sb = (size_t)strides[0];
+    a.q_st = (size_t)strides[1];
+    a.q_sh = (size_t)strides[2];
+    a.k_sb = (size_t)strides[3];
+    a.k_st = (size_t)strides[4];
+    a.k_sh = (size_t)strides[5];
+    a.v_sb = (size_t)strides[6];
+    a.v_st = (size_t)strides[7];
+    a.v_sh = (size_t)strides[8];
+    a.o_sb = (size_t)strides[9];
+    a.o_st = (size_t)strides[10];
+    a.o_sh = (size_t)strides[11];
+    a.m_sb = (size_t)strides[12];
+    a.m_st = (size_t)strides[13];
+    a.nh = nh;
+    a.group = nh / nk;
+    a.t_len = t_len;
+    a.s_len = s_len;
+    a.causal_offset = causal_offset;
+    const float sc = scale > 0.0f ? scale : 1.0f / sqrtf((float)d);
+    a.scale_log2 = sc * FA_LOG2E;
+    const dim3 grid((t_len + FA_BM - 1) / FA_BM, batch * nh);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (d == 128) fa_launch<128>(causal != 0, mask != nullptr, grid, a, s);
+    else fa_launch<64>(causal != 0, mask != nullptr, grid, a, s);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}

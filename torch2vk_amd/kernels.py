@@ -388,6 +388,55 @@ def attn_decode(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cac
     return out
 
 
+# ------------------------------------------------------ prefill attention --
+
+
+def _check_strided(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    """Device, dtype and a contiguous last dimension; other strides are free (the kernel takes them)."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must live on a HIP device, got {t.device}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} dtype {t.dtype}, expected {dtype}")
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name} needs a contiguous last dimension")
+
+
+def flash_attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None, *,
+                       causal: bool = True, causal_offset: int = 0, mask: torch.Tensor | None = None,
+                       scale: float | None = None) -> torch.Tensor:
+    """softmax(q k^T * scale + mask) v; q/out [B, T, NH, D], k/v [B, S, NK, D], bf16, any (batch, token, head)
+    strides with D contiguous -- token-major tensors as they are, head-major ones as ``x.transpose(1, 2)``.
+    ``mask``: additive fp32 [B or 1, T, S] (S contiguous).  Causal: query t sees keys <= t + causal_offset."""
+    for t, name in ((q, "q"), (k, "k"), (v, "v")):
+        _check_strided(t, name, torch.bfloat16)
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be rank 4 [B, T, H, D], got {tuple(t.shape)}")
+    b, t_len, nh, d = q.shape
+    _, s_len, nk, _ = k.shape
+    if k.shape[0] != b or v.shape != k.shape or k.shape[3] != d:
+        raise ValueError(f"shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if out is None:
+        out = torch.empty(b, t_len, nh, d, dtype=torch.bfloat16, device=q.device)
+    _check_strided(out, "output", torch.bfloat16)
+    if tuple(out.shape) != (b, t_len, nh, d):
+        raise ValueError(f"output must be {(b, t_len, nh, d)}, got {tuple(out.shape)}")
+    m_sb = m_st = 0
+    if mask is not None:
+        _check_strided(mask, "mask", torch.float32)
+        if mask.dim() != 3 or mask.shape[1] != t_len or mask.shape[2] != s_len or mask.shape[0] not in (1, b):
+            raise ValueError(f"mask must be [B or 1, {t_len}, {s_len}], got {tuple(mask.shape)}")
+        m_sb = mask.stride(0) if mask.shape[0] == b else 0
+        m_st = mask.stride(1)
+    strides = (_lib.ctypes.c_int64 * 14)(q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1),
+                                         k.stride(2), v.stride(0), v.stride(1), v.stride(2), out.stride(0),
+                                         out.stride(1), out.stride(2), m_sb, m_st)
+    call("t2h_flash_attn_prefill", ptr(q), ptr(k), ptr(v), ptr(out), ptr(mask), b, nh, nk, t_len, s_len, d,
+         strides, 1 if causal else 0, int(causal_offset), float(scale or 0.0), stream_handle())
+    return out
+
+
 # -------------------------------------------------------------- small ops --
 
 
