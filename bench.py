@@ -47,6 +47,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample-steps", type=int, default=3)
     p.add_argument("--no-graph", action="store_true")
+    p.add_argument("--persistent", action="store_true",
+                   help="run each token's layers as one persistent launch (t2h_qwen3_decode_layers)")
     p.add_argument("--profile-kernel", action="store_true",
                    help="counter-collection target: run the dominant kernel over all layers plus a 256 MiB copy "
                         "(the calibration for FETCH_SIZE/WRITE_SIZE), no timing, no JSON line")
@@ -103,7 +105,8 @@ def main() -> int:
     weights = synthetic_weights(cfg, device=dev, seed=0, policy=args.policy)
     total_steps = args.warmup + args.steps + args.steps_per_graph
     s_cap = args.positions + total_steps + 64
-    dec = Qwen3Decoder(weights, max_positions=s_cap, max_new_tokens=total_steps + 8, device=dev)
+    dec = Qwen3Decoder(weights, max_positions=s_cap, max_new_tokens=total_steps + 8, device=dev,
+                       persistent=args.persistent)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
     for layer in range(cfg.layers):
@@ -163,7 +166,9 @@ def main() -> int:
         "config": {
             "workload": f"{cfg.name}-shape {policy_text} greedy decode, batch 1, KV prefilled to "
                         f"{args.positions} positions, {args.steps} timed steps"
-                        + (f", HIP graphs of {spg} steps" if use_graph else ", eager launches"),
+                        + (f", HIP graphs of {spg} steps" if use_graph else ", eager launches")
+                        + (", persistent layers kernel" if dec.persistent else ", one launch per op"),
+            "layers_launch": "persistent" if dec.persistent else "per-op",
             "weights": args.policy,
             "kv_positions": args.positions,
             "batch": 1,

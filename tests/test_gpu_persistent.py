@@ -1,0 +1,124 @@
+"""The persistent decode-layers kernel (t2h_qwen3_decode_layers) against the one-launch-per-op path
+and the CPU oracle, at the Qwen3-8B layer shape (hidden 4096, MLP 12288, 32/8 heads) with 2 layers."""
+
+from __future__ import annotations
+
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.qwen3_check import check_greedy_tokens, dense_weights
+from oracle.reference import Qwen3Shape
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def setup_8b2(device):
+    from torch2vk_amd.qwen3.config import QWEN3_8B
+    from torch2vk_amd.qwen3.weights import matrix_shapes, synthetic_weights
+
+    cfg = replace(QWEN3_8B, layers=2, vocab=4096, eos_token_ids=(4095,))
+    w = synthetic_weights(cfg, device=device, seed=7, std=0.02, norm_std=0.1)
+    shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
+                       head_dim=cfg.head_dim, mlp=cfg.mlp, vocab=cfg.vocab, rope_theta=cfg.rope_theta)
+    return cfg, w, shape
+
+
+def _ws_view(dec, offset, n):
+    """fp32 view of the persistent kernel's workspace (layout of decode_layers.hip: barrier words,
+    then q|k|v, then the attention output)."""
+    return dec.layers_ws[offset:offset + 4 * n].view(torch.float32)
+
+
+@pytest.mark.parametrize("pos", [0, 5, 300])
+def test_persistent_layer_matches_per_op(device, setup_8b2, pos):
+    """One layer at one position on random caches: the Q|K|V projections are bit-identical to the
+    per-op GEMV (same lane mapping and reduction order); the attention output differs at most by
+    bf16 rounding of a differently ordered fp32 sum; h by what that rounding does downstream."""
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg, w, _ = setup_8b2
+    print(f"persistent vs per-op layer 0 at pos {pos}", flush=True)
+    a = Qwen3Decoder(w, max_positions=512, max_new_tokens=4, persistent=True)
+    b = Qwen3Decoder(w, max_positions=512, max_new_tokens=4, persistent=False)
+    g = torch.Generator(device=device)
+    g.manual_seed(3 + pos)
+    kc = torch.randn(a.k_cache.shape, generator=g, device=device).to(torch.bfloat16)
+    vc = torch.randn(a.v_cache.shape, generator=g, device=device).to(torch.bfloat16)
+    h0 = torch.randn(cfg.hidden, generator=g, device=device)
+    for d in (a, b):
+        d.k_cache.copy_(kc)
+        d.v_cache.copy_(vc)
+        d.h.copy_(h0)
+        d.position.fill_(pos)
+    # run only layer 0 on both sides
+    a.layer_table = a.layer_table[:1].contiguous()
+    a.run_decode_layers()
+    b.run_decode_layer(0)
+    torch.cuda.synchronize()
+    a.check_status()
+    qkv = _ws_view(a, 2816, 6144)
+    torch.testing.assert_close(qkv, torch.cat([b.q, b.k, b.v]), rtol=0, atol=0)
+    attn = _ws_view(a, 2816 + 6144 * 4, 4096).to(torch.bfloat16).float()
+    ref = b.attn.float()
+    assert (attn - ref).abs().max().item() <= 2 ** -7 * ref.abs().max().item()
+    torch.testing.assert_close(a.k_cache[0], b.k_cache[0], rtol=0, atol=0)
+    torch.testing.assert_close(a.v_cache[0], b.v_cache[0], rtol=0, atol=0)
+    herr = (a.h - b.h).abs().max().item()
+    assert herr <= 1e-3 * b.h.abs().max().item(), herr
+
+
+def test_persistent_prefill_close_to_per_op(device, setup_8b2):
+    """Both layers over a 6-token prompt: the two paths differ only by rounding order."""
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg, w, _ = setup_8b2
+    a = Qwen3Decoder(w, max_positions=128, max_new_tokens=16, persistent=True)
+    b = Qwen3Decoder(w, max_positions=128, max_new_tokens=16, persistent=False)
+    assert a.persistent and not b.persistent
+    prompt = torch.tensor([17, 4000, 5, 999, 123, 64])
+    for dec in (a, b):
+        dec.stop_on_eos = False
+        dec.prefill(prompt)
+    torch.cuda.synchronize()
+    a.check_status()
+    ha, hb = a.h.double().cpu().numpy(), b.h.double().cpu().numpy()
+    err = float(np.abs(ha - hb).max())
+    cos = float(ha @ hb / np.linalg.norm(ha) / np.linalg.norm(hb))
+    print(f"hidden after prefill: max-abs diff {err:.3e} (max |h| {np.abs(hb).max():.3e}), cos {cos:.8f}", flush=True)
+    assert err <= 5e-3 * float(np.abs(hb).max()) and cos >= 0.99999
+
+
+def test_persistent_decode_matches_oracle(device, setup_8b2):
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+    from torch2vk_amd.qwen3.weights import matrix_shapes
+
+    cfg, w, shape = setup_8b2
+    dense = dense_weights({k: v.cpu().numpy() for k, v in w.packed.items()}, w.types,
+                          {k: v.cpu().numpy() for k, v in w.norms.items()}, matrix_shapes(cfg))
+    prompt = np.random.default_rng(2).integers(0, cfg.vocab, 5).tolist()
+    dec = Qwen3Decoder(w, max_positions=128, max_new_tokens=16, persistent=True)
+    dec.stop_on_eos = False
+    toks = dec.generate(torch.tensor(prompt), 10, steps_per_graph=4, use_graph=True)
+    print(f"persistent 8B-shape decode: {toks}", flush=True)
+    print(check_greedy_tokens(shape, dense, prompt, toks, tie_tol=2e-3))
+
+
+def test_persistent_graph_replay_equals_eager(device, setup_8b2):
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg, w, _ = setup_8b2
+    prompt = torch.tensor([5, 9, 100, 7])
+    a = Qwen3Decoder(w, max_positions=128, max_new_tokens=24, persistent=True)
+    b = Qwen3Decoder(w, max_positions=128, max_new_tokens=24, persistent=True)
+    a.stop_on_eos = b.stop_on_eos = False
+    ta = a.generate(prompt, 17, use_graph=False)
+    tb = b.generate(prompt, 17, steps_per_graph=4, use_graph=True)
+    print(f"eager {ta}\ngraph {tb}", flush=True)
+    assert ta == tb
+    n = prompt.numel() + 17
+    torch.testing.assert_close(a.k_cache[:, :n], b.k_cache[:, :n], rtol=0, atol=0)
+    torch.testing.assert_close(a.v_cache[:, :n], b.v_cache[:, :n], rtol=0, atol=0)

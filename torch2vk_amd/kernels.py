@@ -388,6 +388,53 @@ def attn_decode(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cac
     return out
 
 
+# ------------------------------------------------ persistent decode layers --
+
+DECODE_LAYER_FIELDS = ("q", "k", "v", "o", "gate", "up", "down", "input_norm", "post_norm", "q_norm", "k_norm")
+
+
+def decode_layers_supported(hidden: int, mlp: int, nh: int, nk: int, d: int) -> bool:
+    return int(_lib.lib().t2h_qwen3_decode_layers_workspace_bytes(hidden, mlp, nh, nk, d)) > 0
+
+
+def decode_layers_workspace(hidden: int, mlp: int, nh: int, nk: int, d: int, device) -> torch.Tensor | None:
+    """Zeroed workspace of the persistent decode kernel, or None when the shape is not built."""
+    n = int(_lib.lib().t2h_qwen3_decode_layers_workspace_bytes(hidden, mlp, nh, nk, d))
+    return torch.zeros(n, dtype=torch.uint8, device=device) if n else None
+
+
+def decode_layer_table(packed: dict[str, torch.Tensor], norms: dict[str, torch.Tensor], layers: int,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor) -> torch.Tensor:
+    """Device int64 [layers, 13] pointer table (q, k, v, o, gate, up, down, norms, caches) for
+    :func:`decode_layers`; q, k and v must be consecutive rows of one allocation."""
+    rows = []
+    for i in range(layers):
+        p = f"layers.{i}."
+        q, k, v = packed[p + "q"], packed[p + "k"], packed[p + "v"]
+        if k.data_ptr() != q.data_ptr() + q.numel() or v.data_ptr() != k.data_ptr() + k.numel():
+            raise ValueError(f"layer {i}: q, k and v rows must be stacked in one allocation")
+        ptrs = [packed[p + n].data_ptr() for n in ("q", "k", "v", "o", "gate", "up", "down")]
+        ptrs += [norms[p + n].data_ptr() for n in ("input_norm", "post_norm", "q_norm", "k_norm")]
+        ptrs += [k_cache[i].data_ptr(), v_cache[i].data_ptr()]
+        rows.append(ptrs)
+    return torch.tensor(rows, dtype=torch.int64).to(k_cache.device)
+
+
+def decode_layers(table: torch.Tensor, h: torch.Tensor, cache_position: torch.Tensor, workspace: torch.Tensor,
+                  status: torch.Tensor, *, hidden: int, mlp: int, nh: int, nk: int, d: int, s_cap: int,
+                  eps: float = RMS_EPS, theta: float = 1.0e6) -> None:
+    """All decoder layers of one token in one persistent launch (h updated in place)."""
+    _check(table, "layer_table", torch.int64, align=8)
+    _check(h, "h", torch.float32)
+    _check(cache_position, "cache_position", torch.int32, align=4)
+    _check(workspace, "workspace", torch.uint8, align=256)
+    _check(status, "status", torch.int32, align=4)
+    if table.dim() != 2 or table.shape[1] != 13:
+        raise ValueError(f"layer_table must be int64 [layers, 13], got {tuple(table.shape)}")
+    call("t2h_qwen3_decode_layers", ptr(table), int(table.shape[0]), hidden, mlp, nh, nk, d, s_cap, ptr(h),
+         ptr(cache_position), eps, theta, ptr(workspace), workspace.numel(), ptr(status), stream_handle())
+
+
 # ------------------------------------------------------ prefill attention --
 
 

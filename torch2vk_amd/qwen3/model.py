@@ -54,7 +54,14 @@ def _check_types(c: Qwen3Config, types: dict[str, str]) -> None:
 
 
 class Qwen3Decoder:
-    def __init__(self, weights: Qwen3Weights, *, max_positions: int, max_new_tokens: int, device=None) -> None:
+    """Greedy decoder over libt2h.  ``persistent`` selects how a token's layers run: one persistent launch
+    for all of them (t2h_qwen3_decode_layers: the 8B shape with uniform Q4_K weights), or one launch per
+    op (run_decode_layer, every shape and weight mix, the default: measured faster on MI355X, since the
+    persistent kernel's grid barriers cost more than the launches they replace).  None picks the persistent
+    kernel when it applies."""
+
+    def __init__(self, weights: Qwen3Weights, *, max_positions: int, max_new_tokens: int, device=None,
+                 persistent: bool | None = False) -> None:
         c = weights.config
         self.config: Qwen3Config = c
         self.weights = weights
@@ -84,6 +91,37 @@ class Qwen3Decoder:
         self.eos = torch.tensor(c.eos_token_ids, dtype=torch.int64, device=dev)
         self.stop_on_eos = True
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self.persistent = False
+        self.status = torch.zeros(1, dtype=torch.int32, device=dev)
+        if persistent is not False:
+            why = self._persistent_unsupported()
+            if why is None:
+                self.layers_ws = kernels.decode_layers_workspace(c.hidden, c.mlp, c.heads, c.kv_heads, c.head_dim, dev)
+                self.layer_table = kernels.decode_layer_table(weights.packed, weights.norms, c.layers, self.k_cache,
+                                                              self.v_cache)
+                self.persistent = True
+            elif persistent:
+                raise NotImplementedError(f"persistent decode kernel: {why}")
+
+    def _persistent_unsupported(self) -> str | None:
+        c = self.config
+        if not kernels.decode_layers_supported(c.hidden, c.mlp, c.heads, c.kv_heads, c.head_dim):
+            return f"shape hidden={c.hidden} mlp={c.mlp} heads={c.heads}/{c.kv_heads} d={c.head_dim} not built"
+        if self.max_positions > 8192:
+            return "KV capacity above 8192 positions"
+        for i in range(c.layers):
+            for n in ("q", "k", "v", "o", "gate", "up", "down"):
+                if self.types[f"layers.{i}.{n}"] != "q4_k":
+                    return "weights other than uniform Q4_K"
+            q, k, v = (self.weights.packed[f"layers.{i}.{n}"] for n in ("q", "k", "v"))
+            if k.data_ptr() != q.data_ptr() + q.numel() or v.data_ptr() != k.data_ptr() + k.numel():
+                return "q, k and v rows are not stacked in one allocation"
+        return None
+
+    def check_status(self) -> None:
+        """Raise if a grid barrier of the persistent kernel ever timed out (its results are then invalid)."""
+        if self.persistent and int(self.status.item()) != 0:
+            raise RuntimeError("persistent decode kernel: a grid barrier timed out; results are invalid")
 
     # ----------------------------------------------------------- state --
 
@@ -167,18 +205,27 @@ class Qwen3Decoder:
                             stop_on_eos=self.stop_on_eos, token_index_ptr=self.length,
                             advance=self.position if advance else None)
 
+    def run_decode_layers(self) -> None:
+        """Every layer at the device-resident position: one persistent launch, or one launch per op."""
+        if self.persistent:
+            c = self.config
+            kernels.decode_layers(self.layer_table, self.h, self.position, self.layers_ws, self.status,
+                                  hidden=c.hidden, mlp=c.mlp, nh=c.heads, nk=c.kv_heads, d=c.head_dim,
+                                  s_cap=self.max_positions, eps=c.rms_eps, theta=c.rope_theta)
+        else:
+            for i in range(self.config.layers):
+                self.run_decode_layer(i)
+
     def forward_token(self) -> None:
         """Embed next_token at the current position, run every layer, select the next token."""
         self.run_decode_embed()
-        for i in range(self.config.layers):
-            self.run_decode_layer(i)
+        self.run_decode_layers()
         self.run_lm_head_select()
 
     def decode_step(self) -> None:
         """One full greedy step: forward, select + store the token, advance the position."""
         self.run_decode_embed()
-        for i in range(self.config.layers):
-            self.run_decode_layer(i)
+        self.run_decode_layers()
         self._lm_head()
         kernels.token_select_store(self.partial_scores, self.partial_tokens, self.eos, self.next_token, self.done,
                                    self.generated, self.length, self.stopped, stop_on_eos=self.stop_on_eos,
@@ -248,4 +295,5 @@ class Qwen3Decoder:
         self.prefill(prompt_ids)
         self.run_steps(max_new_tokens - 1, steps_per_graph=steps_per_graph, use_graph=use_graph)
         n = int(self.length.item())
+        self.check_status()
         return self.generated[:n].tolist()

@@ -67,9 +67,26 @@ def synthetic_weights(config: Qwen3Config, *, device, seed: int = 0, std: float 
         dense = torch.randn(rows, cols, generator=gen, device=device, dtype=torch.float32).mul_(std)
         w.packed[name] = kernels.quantize(dense, types[name])
         del dense
+    stack_qkv(w)
     for name, n in norm_shapes(config).items():
         t = torch.ones(n, dtype=torch.float32, device=device)
         if norm_std > 0:
             t.add_(torch.randn(n, generator=gen, device=device, dtype=torch.float32).mul_(norm_std))
         w.norms[name] = t
     return w
+
+
+def stack_qkv(w: Qwen3Weights) -> None:
+    """Keep each layer's q, k and v rows in one allocation (q, k, v become views of it) when they share a
+    GGUF type: the persistent decode kernel streams them as one 6144-row matrix.  Rows are quantized
+    independently, so the bytes are unchanged."""
+    for i in range(w.config.layers):
+        names = [f"layers.{i}.{n}" for n in ("q", "k", "v")]
+        if len({w.types[n] for n in names}) != 1:
+            continue
+        parts = [w.packed[n] for n in names]
+        fused = torch.cat(parts, dim=0)
+        begin = 0
+        for n, t in zip(names, parts):
+            w.packed[n] = fused[begin:begin + t.shape[0]]
+            begin += t.shape[0]
