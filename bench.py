@@ -47,8 +47,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample-steps", type=int, default=3)
     p.add_argument("--no-graph", action="store_true")
-    p.add_argument("--persistent", action="store_true",
-                   help="run each token's layers as one persistent launch (t2h_qwen3_decode_layers)")
+    p.add_argument("--per-op", action="store_true",
+                   help="one launch per op instead of the persistent layers kernel (t2h_qwen3_decode_layers)")
     p.add_argument("--profile-kernel", action="store_true",
                    help="counter-collection target: run the dominant kernel over all layers plus a 256 MiB copy "
                         "(the calibration for FETCH_SIZE/WRITE_SIZE), no timing, no JSON line")
@@ -106,7 +106,7 @@ def main() -> int:
     total_steps = args.warmup + args.steps + args.steps_per_graph
     s_cap = args.positions + total_steps + 64
     dec = Qwen3Decoder(weights, max_positions=s_cap, max_new_tokens=total_steps + 8, device=dev,
-                       persistent=args.persistent)
+                       persistent=False if args.per_op else None)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
     for layer in range(cfg.layers):

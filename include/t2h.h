@@ -184,20 +184,21 @@ int t2h_attn_decode(const float* q, const float* k_new, const float* v_new, cons
  * RMSNorm + Q|K|V GEMV, q/k-norm + RoPE + KV-cache write + split-K attention
  * and its merge, o_proj + residual, RMSNorm + gate|up + SwiGLU, down +
  * residual, on h (fp32 [hidden], updated in place), at *cache_position.
- * Same arithmetic as the per-op entry points; 256 resident blocks meet at grid
- * barriers between phases (no host sync, graph-capturable).  Measured slower
- * than one launch per op on MI355X (the barriers cost more than the launches),
- * so the decoder uses it only when asked.
+ * Same arithmetic as the per-op entry points; 256 resident blocks (one per CU)
+ * pass the activations between phases as epoch-tagged words and poll for them,
+ * with no grid barrier (no host sync, graph-capturable).  Calls on one
+ * workspace must not overlap in time.
  * Built for the Qwen3-8B shape: hidden 4096, mlp 12288, 32/8 heads, d 128,
- * uniform Q4_K weights, bf16 KV caches [s_cap, 8, 128] with s_cap <= 8192
+ * uniform Q4_K weights, bf16 KV caches [s_cap, 8, 128] with s_cap <= 7168
  * (other shapes: T2H_ERR_UNSUPPORTED; so is a GPU that cannot hold 256 blocks).
  * layer_table: device int64 [n_layers][13] pointers in the order
  *   wq, wk, wv, wo, w_gate, w_up, w_down, input_norm, post_norm, q_norm, k_norm, k_cache, v_cache,
  * where wq..wv must be one allocation of 6144 stacked rows (wk = wq + 4096 rows, wv = wq + 5120 rows).
  * workspace: t2h_qwen3_decode_layers_workspace_bytes() bytes, 256-B aligned,
- * zero-filled once before its first use (barrier words are reused by later
- * calls).  *status (device) is set non-zero if a grid barrier timed out, which
- * means the result is invalid; it is never cleared by the library.
+ * zero-filled once before its first use (it holds a launch counter that later
+ * calls advance).  *status (device) is set non-zero if a wait for another
+ * block's output timed out, which means the result is invalid; it is never
+ * cleared by the library.
  * replaces run_decode_layer for every layer (src/models/optimized_qwen3/dispatch/decode_layer.py:60-136;
  * decode step src/models/optimized_qwen3/run.py:142-172). */
 size_t t2h_qwen3_decode_layers_workspace_bytes(uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk, uint32_t d);

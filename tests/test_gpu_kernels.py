@@ -269,7 +269,11 @@ def _attn_case(nh, nk, s_cap, pos, seed, device, norm=True, theta=1e6):
 
 @pytest.mark.parametrize("nh,nk,s_cap,pos", [(32, 8, 4352, 4096), (16, 8, 512, 127), (32, 8, 300, 0),
                                              (32, 8, 256, 63), (32, 8, 256, 64), (16, 8, 200, 250),
-                                             (8, 8, 130, 129), (64, 8, 1024, 700)])
+                                             (8, 8, 130, 129), (64, 8, 1024, 700),
+                                             # spans past one 32-row tile per wave (L > 8192 at 256 blocks)
+                                             (32, 8, 9000, 8999), (32, 8, 20000, 17000), (64, 8, 9000, 8500),
+                                             # one kv head: 256 blocks over it
+                                             (4, 1, 3000, 2999), (8, 1, 600, 37)])
 def test_attn_decode(device, nh, nk, s_cap, pos):
     print(f"attn_decode nh={nh} nk={nk} S={s_cap} pos={pos}", flush=True)
     got, ref, kct, vct, kref, vref, L = _attn_case(nh, nk, s_cap, pos, seed=pos + nh, device=device)

@@ -27,10 +27,20 @@ def setup_8b2(device):
     return cfg, w, shape
 
 
-def _ws_view(dec, offset, n):
-    """fp32 view of the persistent kernel's workspace (layout of decode_layers.hip: barrier words,
-    then q|k|v, then the attention output)."""
-    return dec.layers_ws[offset:offset + 4 * n].view(torch.float32)
+# Workspace layout of decode_layers.hip: 256 B launch counter, then q|k|v as (fp32, u32 epoch) words,
+# then the attention output as (bf16, u16 epoch) words.
+WS_QKV = 256
+WS_ATTN = WS_QKV + 6144 * 8
+
+
+def _ws_ll32(dec, offset, n):
+    """fp32 values of n epoch-tagged (fp32, u32) words of the persistent kernel's workspace."""
+    return dec.layers_ws[offset:offset + 8 * n].view(torch.int32).view(n, 2)[:, 0].contiguous().view(torch.float32)
+
+
+def _ws_ll16(dec, offset, n):
+    """bf16 values of n epoch-tagged (bf16, u16) words of the persistent kernel's workspace."""
+    return dec.layers_ws[offset:offset + 4 * n].view(torch.int16).view(n, 2)[:, 0].contiguous().view(torch.bfloat16)
 
 
 @pytest.mark.parametrize("pos", [0, 5, 300])
@@ -60,9 +70,9 @@ def test_persistent_layer_matches_per_op(device, setup_8b2, pos):
     b.run_decode_layer(0)
     torch.cuda.synchronize()
     a.check_status()
-    qkv = _ws_view(a, 2816, 6144)
+    qkv = _ws_ll32(a, WS_QKV, 6144)
     torch.testing.assert_close(qkv, torch.cat([b.q, b.k, b.v]), rtol=0, atol=0)
-    attn = _ws_view(a, 2816 + 6144 * 4, 4096).to(torch.bfloat16).float()
+    attn = _ws_ll16(a, WS_ATTN, 4096).float()
     ref = b.attn.float()
     assert (attn - ref).abs().max().item() <= 2 ** -7 * ref.abs().max().item()
     torch.testing.assert_close(a.k_cache[0], b.k_cache[0], rtol=0, atol=0)

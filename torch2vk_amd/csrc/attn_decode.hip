@@ -8,16 +8,21 @@
 //       src/models/optimized_qwen3/shaders/sdpa_decode_cache_write_f32.py:22-170
 //
 // The reference walks the whole cache serially in one workgroup per q head.
-// Here a block of 8 waves owns (kv head, 128-position chunk); each wave takes
-// 16 positions for all GROUP q heads of the kv head, so every K/V byte is read
-// once per token:
-//   * K rows are loaded coalesced (4 lanes per row, 64 B each) and a lane
-//     dots its quarter row with the GROUP q vectors (broadcast from LDS);
+// Here the grid is fixed at (slots, nk) with slots * nk = 256 blocks, one per
+// CU, whatever the length: block (slot, kv head) has 8 waves and wave w covers
+// span = ceil(L / (slots * 8)) consecutive positions for all GROUP q heads of
+// the kv head, so every K/V byte is read once per token and every CU streams
+// an equal share:
+//   * K rows are loaded coalesced (4 lanes per row, 64 B each, 16 rows per
+//     load set) and a lane dots its quarter row with the GROUP q vectors
+//     (broadcast from LDS); a quad DPP reduction completes the dot;
 //   * V is loaded coalesced straight into registers in the P.V layout (lane
 //     owns two dims, one register per position);
+//   * a wave walks its span in tiles of 32 positions with an online softmax
+//     (one tile up to L = 8192 at 256 blocks), loading only rows < L;
 //   * the waves' partial softmax states are merged in LDS and the block's
 //     (max, sum, unnormalised output) is published to the workspace;
-//   * a second small kernel merges the partials of each q head with the
+//   * a second small kernel merges the slots' partials of each q head with the
 //     log-sum-exp rule.  Merging in the last block to finish would need
 //     device-scope release/acquire: on this multi-XCD part that is an L2
 //     write-back plus invalidate per block, measured far slower than a launch.
@@ -31,11 +36,10 @@
 namespace t2h {
 
 constexpr int AD_D = 128;
-constexpr int AD_WAVE_POS = 16;               // positions per wave
 constexpr int AD_WAVES = 8;                   // waves per block
-constexpr int AD_CH = AD_WAVE_POS * AD_WAVES; // positions per block
+constexpr int AD_TILE = 32;                   // positions per wave per tile (two 16-row K load sets; 16 for GROUP 8)
+constexpr int AD_GRID = 256;                  // split blocks per call (slots * nk), one per CU
 constexpr int AD_QROW = 36;                   // LDS q row: 32 dims + 4 pad (conflict-free quarter reads)
-constexpr int AD_MAX_PARTS = 512;             // s_cap <= 65536
 constexpr int AD_MERGE_WAVES = 4;
 constexpr int AD_MERGE_BATCH = 16;            // partial loads in flight per merge wave
 
@@ -49,11 +53,11 @@ struct AttnDecodeArgs {
     uint16_t* v_cache;
     uint16_t* out;          // bf16 [NH, D]
     const int32_t* pos_ptr; // current position (device)
-    float* part_ml;         // [NK, max_chunks, GROUP, 2]
-    float* part_o;          // [NK, max_chunks, GROUP, D]
+    float* part_ml;         // [NK, slots, GROUP, 2]
+    float* part_o;          // [NK, slots, GROUP, D]
     uint32_t nk;
     uint32_t s_cap;
-    uint32_t max_chunks;
+    uint32_t slots;         // split blocks per kv head
     float theta;            // <= 0: no RoPE
     float eps;
     float scale;            // softmax scale, 1/sqrt(D)
@@ -78,16 +82,45 @@ __device__ __forceinline__ void norm_rope_pair(float x0, float x1, bool has_w, f
     }
 }
 
-// Split-K pass.  Block (chunk c, kv head) covers AD_CH positions with AD_WAVES
-// waves of AD_WAVE_POS positions each.  Scores: lane = (position p, quarter
-// part) dots 32 dims of the K row with the GROUP q vectors, a quad DPP
-// reduction completes the dot.  P.V: lane owns dims 2*lane, 2*lane+1 with V
-// rows loaded coalesced (one row per instruction).  The waves' softmax states
-// are merged in LDS and one (max, sum, output) partial per head is published.
+// K and V rows of one tile: positions t + 16 r + p_k of the K quarter `part`,
+// and V rows t .. t + TILE - 1 (lane owns dims 2 lane, 2 lane + 1).
+template <int TILE>
+struct AdTile {
+    uint4 kr[TILE / 16][4];
+    uint32_t vr[TILE];
+};
+
+// Load the rows [t, t + n) of a tile (n >= 1, wave-uniform).  K lanes past the
+// end re-read row t + n - 1 (always valid) instead of branching, so all loads
+// of the tile are in flight at once; V rows past the end are not loaded.
+template <int TILE>
+__device__ __forceinline__ void ad_issue_tile(AdTile<TILE>& tl, const uint16_t* kbase, const uint16_t* vbase,
+                                              size_t row_stride, int t, int n) {
+    const int lane = threadIdx.x & 63;
+    const int p_k = lane >> 2, part = lane & 3;
+#pragma unroll
+    for (int r = 0; r < TILE / 16; ++r) {
+        if (r == 0 || n > 16 * r) {
+            const int p = t + min(16 * r + p_k, n - 1);
+            const uint16_t* krow = kbase + (size_t)p * row_stride + part * 32;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tl.kr[r][i] = load_u4(krow + 8 * i);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TILE; ++i)
+        if (i < n) tl.vr[i] = reinterpret_cast<const uint32_t*>(vbase + (size_t)(t + i) * row_stride)[lane];
+}
+
+// Split-K pass: see the file comment.  Block (slot, kv head); the new K/V row
+// at `pos` is produced by the wave whose span holds it, written to the cache
+// and substituted for the (stale) row it loaded.
 template <int GROUP>
 __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDecodeArgs a) {
+    constexpr int TILE = GROUP >= 8 ? 16 : AD_TILE;  // registers: TILE V rows + GROUP accumulators
+    constexpr int NR = TILE / 16;                     // 16-row K load sets per tile
     __shared__ __align__(16) float qs[GROUP][4][AD_QROW];
-    __shared__ __align__(16) float ps[AD_WAVES][AD_WAVE_POS][GROUP];
+    __shared__ __align__(16) float ps[AD_WAVES][TILE][GROUP];
     __shared__ float wml[AD_WAVES][GROUP][2];
     __shared__ __align__(16) float2 wo[AD_WAVES][GROUP][64];
     __shared__ __align__(16) uint16_t knew[AD_D];
@@ -95,22 +128,20 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, scalar
-    const int c = blockIdx.x;
+    const int slot = blockIdx.x;
     const int kvh = blockIdx.y;
     const int pos = *a.pos_ptr;
     const int S = (int)a.s_cap;
     const int L = pos + 1 < S ? pos + 1 : S;
-    const int n_chunks = (L + AD_CH - 1) / AD_CH;
-    if (c >= n_chunks) return;
-    const int pw = c * AD_CH + wave * AD_WAVE_POS;  // first position of this wave
+    const int waves_per_head = (int)a.slots * AD_WAVES;
+    const int span = (L + waves_per_head - 1) / waves_per_head;
+    const int pw = (slot * AD_WAVES + wave) * span;  // first position of this wave
     int rows = L - pw;
-    rows = rows < 0 ? 0 : (rows > AD_WAVE_POS ? AD_WAVE_POS : rows);
+    rows = rows < 0 ? 0 : (rows > span ? span : rows);
     const size_t row_stride = (size_t)a.nk * AD_D;  // elements between positions
     const uint16_t* kbase = a.k_cache + (size_t)kvh * AD_D;
     const uint16_t* vbase = a.v_cache + (size_t)kvh * AD_D;
-    const int last_pos = L - 1;
-    const bool has_new = pos < S && pos >= pw && pos < pw + AD_WAVE_POS;  // wave-uniform
-    const int rnew = pos - pw;
+    const bool has_new = pos < S && pos >= pw && pos < pw + rows;  // wave-uniform
     const bool rope = a.theta > 0.0f;
     const bool needs_rope = wave < GROUP || has_new;  // wave-uniform
 
@@ -138,25 +169,9 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
         vx1 = a.v_new[kvh * AD_D + 2 * lane + 1];
     }
 
-    // 1. K: lane (p_k, part) loads 4 x 16 B = dims part*32..+31 of row p_k;
-    //    V: one row per instruction, lane owns dims 2*lane, 2*lane+1.
-    //    Rows past the end are clamped to position L-1 (always valid) instead of
-    //    branching, so every load is in flight at once; they are masked below.
-    const int p_k = lane >> 2;
-    const int part = lane & 3;
-    uint4 kr[4];
-    {
-        const int p = min(pw + p_k, last_pos);
-        const uint16_t* krow = kbase + (size_t)p * row_stride + part * 32;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kr[i] = load_u4(krow + 8 * i);
-    }
-    uint32_t vr[AD_WAVE_POS];
-#pragma unroll
-    for (int i = 0; i < AD_WAVE_POS; ++i) {
-        const int p = min(pw + i, last_pos);
-        vr[i] = reinterpret_cast<const uint32_t*>(vbase + (size_t)p * row_stride)[lane];
-    }
+    // 1. the first tile's K/V rows
+    AdTile<TILE> tl;
+    if (rows > 0) ad_issue_tile(tl, kbase, vbase, row_stride, pw, min(rows, TILE));
 
     // 2. RoPE at `pos` (lane = frequency index, inv_freq = theta^(-2 lane / D));
     //    q head `wave` normalised, rotated, pre-scaled by 1/sqrt(D) into LDS
@@ -189,76 +204,119 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
         reinterpret_cast<uint32_t*>(a.v_cache + off)[lane] = vnew;
     }
     __syncthreads();
-    if (has_new && p_k == rnew) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const uint4*>(&knew[part * 32 + 8 * i]);
-    }
 
-    // 4. scores: 32-dim partial dots, completed across the 4 lanes of a position
-    float s[GROUP];
-#pragma unroll
-    for (int g = 0; g < GROUP; ++g) s[g] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint4 kk = kr[i];
-        float kf[8];
-        kf[0] = bf16_bits_to_f32(kk.x & 0xffffu); kf[1] = bf16_bits_to_f32(kk.x >> 16);
-        kf[2] = bf16_bits_to_f32(kk.y & 0xffffu); kf[3] = bf16_bits_to_f32(kk.y >> 16);
-        kf[4] = bf16_bits_to_f32(kk.z & 0xffffu); kf[5] = bf16_bits_to_f32(kk.z >> 16);
-        kf[6] = bf16_bits_to_f32(kk.w & 0xffffu); kf[7] = bf16_bits_to_f32(kk.w >> 16);
-#pragma unroll
-        for (int g = 0; g < GROUP; ++g) {
-            const float4 qa = *reinterpret_cast<const float4*>(&qs[g][part][8 * i]);
-            const float4 qb = *reinterpret_cast<const float4*>(&qs[g][part][8 * i + 4]);
-            float t = s[g];
-            t = fmaf(qa.x, kf[0], t); t = fmaf(qa.y, kf[1], t);
-            t = fmaf(qa.z, kf[2], t); t = fmaf(qa.w, kf[3], t);
-            t = fmaf(qb.x, kf[4], t); t = fmaf(qb.y, kf[5], t);
-            t = fmaf(qb.z, kf[6], t); t = fmaf(qb.w, kf[7], t);
-            s[g] = t;
-        }
-    }
+    // 4. tiles: scores, online softmax, P.V (a wave with no rows keeps m = -inf, l = 0, o = 0)
+    const int p_k = lane >> 2;
+    const int part = lane & 3;
+    float mg[GROUP], lg[GROUP], o0[GROUP], o1[GROUP];
 #pragma unroll
     for (int g = 0; g < GROUP; ++g) {
-        s[g] += dpp_f32<0xB1>(s[g]);  // quad_perm [1,0,3,2]
-        s[g] += dpp_f32<0x4E>(s[g]);  // quad_perm [2,3,0,1]
+        mg[g] = -INFINITY;
+        lg[g] = 0.0f;
+        o0[g] = o1[g] = 0.0f;
     }
-
-    // 5. wave-local softmax statistics over its positions (a wave with no rows has m = -inf, l = 0)
-    const bool valid = p_k < rows;
-    float mg[GROUP], lg[GROUP];
+    // one tile: rows [t0, t0 + n) of the wave's span, loaded into tl
+    auto tile = [&](AdTile<TILE>& tl, int t0, int n) {
+        const int tnew = pos - (pw + t0);  // row of the new position within the tile (if any)
+        float s[NR][GROUP];
 #pragma unroll
-    for (int g = 0; g < GROUP; ++g) {
-        const float sv = valid ? s[g] : -INFINITY;
-        const float m = wave_max(sv);
-        const float e = valid ? expf(sv - m) : 0.0f;
-        mg[g] = m;
-        lg[g] = wave_sum(part == 0 ? e : 0.0f);
-        if (part == 0) ps[wave][p_k][g] = e;
-    }
-    // ps is produced and consumed by the same wave: LDS order within a wave suffices
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // 6. P.V: lane <-> dims (2*lane, 2*lane+1), V from registers
-    float o0[GROUP], o1[GROUP];
+        for (int r = 0; r < NR; ++r) {
+            if (has_new && 16 * r + p_k == tnew) {
 #pragma unroll
-    for (int g = 0; g < GROUP; ++g) o0[g] = o1[g] = 0.0f;
+                for (int i = 0; i < 4; ++i) tl.kr[r][i] = *reinterpret_cast<const uint4*>(&knew[part * 32 + 8 * i]);
+            }
 #pragma unroll
-    for (int p = 0; p < AD_WAVE_POS; ++p) {
-        const uint32_t vv = (has_new && p == rnew) ? vnew : vr[p];
-        const float v0 = bf16_bits_to_f32(vv & 0xffffu);
-        const float v1 = bf16_bits_to_f32(vv >> 16);
+            for (int g = 0; g < GROUP; ++g) s[r][g] = 0.0f;
+        }
+        // each q fragment read from LDS once and used for both K rows
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float kf[NR][8];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const uint4 kk = tl.kr[r][i];
+                kf[r][0] = bf16_bits_to_f32(kk.x & 0xffffu); kf[r][1] = bf16_bits_to_f32(kk.x >> 16);
+                kf[r][2] = bf16_bits_to_f32(kk.y & 0xffffu); kf[r][3] = bf16_bits_to_f32(kk.y >> 16);
+                kf[r][4] = bf16_bits_to_f32(kk.z & 0xffffu); kf[r][5] = bf16_bits_to_f32(kk.z >> 16);
+                kf[r][6] = bf16_bits_to_f32(kk.w & 0xffffu); kf[r][7] = bf16_bits_to_f32(kk.w >> 16);
+            }
+#pragma unroll
+            for (int g = 0; g < GROUP; ++g) {
+                const float4 qa = *reinterpret_cast<const float4*>(&qs[g][part][8 * i]);
+                const float4 qb = *reinterpret_cast<const float4*>(&qs[g][part][8 * i + 4]);
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    float u = s[r][g];
+                    u = fmaf(qa.x, kf[r][0], u); u = fmaf(qa.y, kf[r][1], u);
+                    u = fmaf(qa.z, kf[r][2], u); u = fmaf(qa.w, kf[r][3], u);
+                    u = fmaf(qb.x, kf[r][4], u); u = fmaf(qb.y, kf[r][5], u);
+                    u = fmaf(qb.z, kf[r][6], u); u = fmaf(qb.w, kf[r][7], u);
+                    s[r][g] = u;
+                }
+            }
+        }
 #pragma unroll
         for (int g = 0; g < GROUP; ++g) {
-            const float pr = ps[wave][p][g];
-            o0[g] = fmaf(pr, v0, o0[g]);
-            o1[g] = fmaf(pr, v1, o1[g]);
+            float sc[NR];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                float u = s[r][g];
+                u += dpp_f32<0xB1>(u);  // quad_perm [1,0,3,2]
+                u += dpp_f32<0x4E>(u);  // quad_perm [2,3,0,1]
+                sc[r] = 16 * r + p_k < n ? u : -INFINITY;
+                tmax = fmaxf(tmax, sc[r]);
+            }
+            const float m = fmaxf(mg[g], wave_max(tmax));  // finite: the tile has >= 1 row
+            const float rescale = mg[g] == -INFINITY ? 0.0f : expf(mg[g] - m);
+            float esum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const float e = 16 * r + p_k < n ? expf(sc[r] - m) : 0.0f;
+                esum += e;
+                if (part == 0) ps[wave][16 * r + p_k][g] = e;
+            }
+            mg[g] = m;
+            lg[g] = fmaf(lg[g], rescale, wave_sum(part == 0 ? esum : 0.0f));
+            o0[g] *= rescale;
+            o1[g] *= rescale;
         }
+        // ps is produced and consumed by the same wave: LDS order within a wave suffices
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // P.V: lane <-> dims (2 lane, 2 lane + 1), V from registers (fully
+        // unrolled so they are indexed statically; rows >= n are skipped).  The
+        // scheduling fence every 8 rows keeps the P reads from all being hoisted
+        // into registers at once.
+#pragma unroll
+        for (int p = 0; p < TILE; ++p) {
+            if (p % 8 == 0) __builtin_amdgcn_sched_barrier(0);
+            if (p < n) {
+                const uint32_t vv = (has_new && p == tnew) ? vnew : tl.vr[p];
+                const float va = bf16_bits_to_f32(vv & 0xffffu);
+                const float vb = bf16_bits_to_f32(vv >> 16);
+#pragma unroll
+                for (int g = 0; g < GROUP; ++g) {
+                    const float pr = ps[wave][p][g];
+                    o0[g] = fmaf(pr, va, o0[g]);
+                    o1[g] = fmaf(pr, vb, o1[g]);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // the next tile's ps writes come after these reads
+    };
+    // the first tile was loaded before the q preparation; tiles past it (spans
+    // over 32 rows: L > 8192 at 256 blocks) load and then compute
+    if (rows > 0) tile(tl, 0, min(rows, TILE));
+    for (int t0 = TILE; t0 < rows; t0 += TILE) {
+        const int n = min(rows - t0, TILE);
+        AdTile<TILE> tn;
+        ad_issue_tile(tn, kbase, vbase, row_stride, pw + t0, n);
+        tile(tn, t0, n);
     }
 
-    // 7. merge the waves in LDS and publish the block's partial
+    // 5. merge the waves in LDS and publish the block's partial
 #pragma unroll
     for (int g = 0; g < GROUP; ++g) {
         wo[wave][g][lane] = make_float2(o0[g], o1[g]);
@@ -268,8 +326,7 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
         }
     }
     __syncthreads();
-    const size_t kv_base = (size_t)kvh * a.max_chunks * GROUP;  // first partial of this kv head
-    const size_t cbase = kv_base + (size_t)c * GROUP;
+    const size_t cbase = ((size_t)kvh * a.slots + slot) * GROUP;  // first partial of this block
     for (int idx = tid; idx < GROUP * 64; idx += AD_WAVES * 64) {
         const int g = idx >> 6;
         const int dl = idx & 63;
@@ -289,10 +346,9 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
         *reinterpret_cast<float2*>(&a.part_o[(cbase + g) * AD_D + 2 * dl]) = make_float2(r0, r1);
         if (dl == 0) *reinterpret_cast<float2*>(&a.part_ml[(cbase + g) * 2]) = make_float2(M, l);
     }
-
 }
 
-// Log-sum-exp merge of the per-chunk partials: one block per q head, each of
+// Log-sum-exp merge of the per-slot partials: one block per q head, each of
 // its AD_MERGE_WAVES waves folds a slab of up to AD_MERGE_BATCH chunks at a
 // time (loads issued together; indices past the end re-read the last chunk and
 // get weight 0), then the waves' states are combined in LDS.  Lane t owns dims
@@ -307,11 +363,8 @@ __global__ __launch_bounds__(AD_MERGE_WAVES * 64) void attn_decode_merge_kernel(
     const int h = blockIdx.x;
     const int kvh = h / GROUP;
     const int g = h % GROUP;
-    const int pos = *a.pos_ptr;
-    const int S = (int)a.s_cap;
-    const int L = pos + 1 < S ? pos + 1 : S;
-    const int n_chunks = (L + AD_CH - 1) / AD_CH;
-    const size_t hbase = (size_t)kvh * a.max_chunks * GROUP + g;
+    const int n_chunks = (int)a.slots;  // every slot publishes a partial (m = -inf, l = 0 when it saw no row)
+    const size_t hbase = (size_t)kvh * a.slots * GROUP + g;
     float M = -INFINITY, lsum = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
     for (int cb = wave * AD_MERGE_BATCH; cb < n_chunks; cb += AD_MERGE_WAVES * AD_MERGE_BATCH) {
         float2 ov[AD_MERGE_BATCH];
@@ -374,15 +427,15 @@ __global__ __launch_bounds__(AD_MERGE_WAVES * 64) void attn_decode_merge_kernel(
 
 using namespace t2h;
 
-static uint32_t ad_max_chunks(uint32_t s_cap) { return (s_cap + AD_CH - 1) / AD_CH; }
+// split blocks per kv head: AD_GRID blocks in all (one per CU), at least one per kv head
+static uint32_t ad_slots(uint32_t nk) { return nk >= (uint32_t)AD_GRID ? 1u : (uint32_t)AD_GRID / nk; }
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 extern "C" size_t t2h_attn_decode_workspace_bytes(uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap) {
-    if (nk == 0 || nh % nk != 0 || d != AD_D || s_cap == 0 || ad_max_chunks(s_cap) > AD_MAX_PARTS) return 0;
-    const size_t group = nh / nk;
-    const size_t mc = ad_max_chunks(s_cap);
-    return align256(nk * mc * group * 2 * sizeof(float)) + align256(nk * mc * group * d * sizeof(float));
+    if (nk == 0 || nh % nk != 0 || d != AD_D || s_cap == 0 || s_cap > (uint32_t)INT32_MAX) return 0;
+    const size_t parts = (size_t)nk * ad_slots(nk) * (nh / nk);
+    return align256(parts * 2 * sizeof(float)) + align256(parts * d * sizeof(float));
 }
 
 extern "C" int t2h_attn_decode(const float* q, const float* k_new, const float* v_new, const float* q_norm_w,
@@ -393,11 +446,11 @@ extern "C" int t2h_attn_decode(const float* q, const float* k_new, const float* 
     if (!q || !k_new || !v_new || !k_cache || !v_cache || !out || !cache_position || !workspace) return T2H_ERR_NULL;
     if (d != AD_D) return T2H_ERR_UNSUPPORTED;
     if (nk == 0 || nh == 0 || nh % nk != 0 || s_cap == 0) return T2H_ERR_SHAPE;
-    if (ad_max_chunks(s_cap) > AD_MAX_PARTS) return T2H_ERR_UNSUPPORTED;
+    if (s_cap > (uint32_t)INT32_MAX) return T2H_ERR_UNSUPPORTED;
     if ((q_norm_w == nullptr) != (k_norm_w == nullptr)) return T2H_ERR_ARG;
     const uint32_t group = nh / nk;
     if (workspace_bytes < t2h_attn_decode_workspace_bytes(nh, nk, d, s_cap)) return T2H_ERR_WORKSPACE;
-    const uint32_t mc = ad_max_chunks(s_cap);
+    const uint32_t slots = ad_slots(nk);
     AttnDecodeArgs a;
     a.q = q;
     a.k_new = k_new;
@@ -410,15 +463,15 @@ extern "C" int t2h_attn_decode(const float* q, const float* k_new, const float* 
     a.pos_ptr = cache_position;
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     a.part_ml = reinterpret_cast<float*>(ws);
-    ws += align256((size_t)nk * mc * group * 2 * sizeof(float));
+    ws += align256((size_t)nk * slots * group * 2 * sizeof(float));
     a.part_o = reinterpret_cast<float*>(ws);
     a.nk = nk;
     a.s_cap = s_cap;
-    a.max_chunks = mc;
+    a.slots = slots;
     a.theta = theta;
     a.eps = eps;
     a.scale = 1.0f / sqrtf((float)d);
-    const dim3 grid(mc, nk), block(AD_WAVES * 64);
+    const dim3 grid(slots, nk), block(AD_WAVES * 64);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const dim3 mgrid(nh), mblock(AD_MERGE_WAVES * 64);
     switch (group) {

@@ -15,21 +15,34 @@
 //
 // Why one launch.  On MI355X a dependent kernel in a HIP graph costs ~1.75 us
 // before its first wave runs, and each GEMV then ramps up and drains on its
-// own.  Here 256 resident blocks of 8 waves (one per CU) walk the phases and
-// meet at a grid barrier between them: per-XCD-group counters feeding one
-// global counter and a generation word, ~1.85 us, all with agent-scope
-// relaxed atomics and bounded spins (a timed-out spin sets the status word
-// and the block moves on, so the launch always ends).  Before each barrier a
-// wave issues the weight loads of its share of the next phase, which do not
-// depend on the barrier, so HBM keeps streaming while the grid waits.
+// own.  Here 256 resident blocks of 8 waves (one per CU) walk the phases of
+// every layer without a grid barrier: each phase first issues the weight (or
+// KV-cache) loads of its share, which depend on nothing, and only then waits
+// for its input vector, so HBM keeps streaming while the previous phase
+// finishes elsewhere on the chip.
 //
-// Coherence.  Activations that cross blocks (h, q|k|v, attention partials,
-// attention output, SwiGLU output) are written and read with agent-scope
-// atomic accesses (sc1): each XCD has its own L2, and plain accesses could hit
-// a stale line.  A block's stores are complete (s_waitcnt) before it arrives
-// at a barrier.  Weights and the KV cache rows read here are not written in
-// the same launch, so they use ordinary loads.
+// Data flow instead of barriers.  Every element of a vector that crosses
+// blocks (h, q|k|v, attention partials, attention output, SwiGLU output) is
+// stored together with an epoch in one single-copy-atomic word: fp32 + u32
+// epoch in 8 bytes, or bf16 + u16 epoch in 4 bytes.  A consumer loads the
+// words it needs and re-loads until every epoch is the one this (launch,
+// layer, phase) writes, so a producer never waits for its stores to complete
+// and no block waits for the whole grid.  Epochs come from a launch counter
+// in the workspace (advanced by block 0 at the end of every launch), so a
+// value left from an earlier write never carries the expected epoch.  Spins
+// are bounded: a consumer that gives up sets the status word and goes on, so
+// the launch always ends (its results are then invalid).
+//
+// A buffer is rewritten only after every reader of its previous contents has
+// finished: each phase reads the complete output of the phase before it, so a
+// block that has the input of phase P + 1 knows that every block has passed
+// phase P - 1.  Cross-block words are written and read with agent-scope atomic
+// accesses (sc1): each XCD has its own L2, and plain accesses could hit a stale
+// line.  Weights and the KV cache rows read here are not written in the same
+// launch (except the new row, which its owner substitutes), so they use
+// ordinary loads.
 #include "q4k_device.h"
+
 
 namespace t2h {
 
@@ -40,8 +53,20 @@ constexpr int DL_NW = DL_BLOCKS * DL_WAVES;    // waves in the grid
 constexpr int DL_D = 128;                      // head dim
 constexpr int DL_ATT_POS = 32;                 // positions per wave per attention pass (two rows per lane)
 constexpr int DL_ATT_SLOTS = DL_BLOCKS / 8;    // attention blocks per kv head (8 kv heads)
-constexpr int DL_GROUPS = 8;                   // barrier groups
-constexpr uint32_t DL_SPIN_LIMIT = 1u << 14;   // polls before a barrier gives up (~16 ms)
+constexpr uint32_t DL_SPIN_LIMIT = 1u << 14;
+// weight units per wave issued before a GEMV phase's input is awaited
+#ifndef DL_PRE_QKV
+#define DL_PRE_QKV 2
+#endif
+#ifndef DL_PRE_O
+#define DL_PRE_O 2
+#endif
+#ifndef DL_PRE_GU
+#define DL_PRE_GU 2
+#endif
+#ifndef DL_PRE_DOWN
+#define DL_PRE_DOWN 2
+#endif   // polls before a consumer gives up (~16 ms)
 
 // Per-layer pointer table (device memory, DL_LAYER_PTRS uint64 per layer).
 // DL_WQ points at the q, k and v rows stacked contiguously (6144 rows); DL_WK and
@@ -55,79 +80,81 @@ enum DlLayerPtr {
 struct DlArgs {
     const uint64_t* layers;   // [n_layers][DL_LAYER_PTRS]
     uint32_t n_layers;
-    float* h;                 // fp32 [HID] residual stream (in/out)
+    float* h;                 // fp32 [HID] residual stream (in/out, plain)
     const int32_t* pos_ptr;
     uint32_t s_cap;
     float eps;
     float theta;
-    float* qkv;               // fp32 [QD + 2 KVD]
-    float* attn;              // fp32 [QD]
-    float* act;               // fp32 [MLP]
-    float* part;              // attention partials [NK][SLOTS][GROUP][2 + D]
-    uint32_t* bar;            // barrier words (zero before first use, monotonic after)
-    uint32_t* status;         // set non-zero when a barrier spin timed out
+    uint32_t* ctl;            // [0]: launches completed (epoch base)
+    uint64_t* h_ll;           // [HID] fp32 + epoch: h after o_proj / down_proj
+    uint64_t* qkv_ll;         // [QD + 2 KVD] fp32 + epoch
+    uint64_t* part_ll;        // attention partials [NK][SLOTS][GROUP][2 + D], fp32 + epoch
+    uint32_t* attn_ll;        // [QD] bf16 + epoch16: attention output
+    uint32_t* act_ll;         // [MLP] bf16 + epoch16: SwiGLU output
+    uint32_t* status;         // set non-zero when a consumer spin timed out
 };
 
-// ------------------------------------------------------ coherent access ----
+// The thread index as an opaque value: per-lane offsets derived from it are
+// recomputed in every phase instead of being hoisted out of the layer loop,
+// where they would stay live across the attention phase (the kernel's
+// register peak) and be spilled.
+__device__ __forceinline__ int dl_tid() {
+    int t;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+    return t;
+}
 
-__device__ __forceinline__ float ld_coh(const float* p) {
+// ------------------------------------------------- epoch-tagged words ----
+
+// Epoch ids of the vectors a layer writes.
+enum DlEpoch { DL_E_QKV = 0, DL_E_PART, DL_E_ATTN, DL_E_H_O, DL_E_ACT, DL_E_H_DOWN, DL_E_PER_LAYER };
+
+__device__ __forceinline__ uint32_t dl_epoch(uint32_t seq, uint32_t layer, int id) {
+    return (seq + 1u) * 256u + layer * DL_E_PER_LAYER + (uint32_t)id;  // never 0 (zeroed workspace)
+}
+
+__device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float2 ld_coh2(const float* p) {
-    const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
-}
-__device__ __forceinline__ void st_coh(float* p, float v) {
+__device__ __forceinline__ void ll_store(uint64_t* p, uint64_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_coh2(float* p, float a, float b) {
-    const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
-    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// fp32 value + 32-bit epoch
+__device__ __forceinline__ void ll_put32(uint64_t* p, float v, uint32_t e) {
+    ll_store(p, (uint64_t)__float_as_uint(v) | ((uint64_t)e << 32));
+}
+__device__ __forceinline__ float ll_val32(uint64_t w) { return __uint_as_float((uint32_t)w); }
+__device__ __forceinline__ bool ll_ok32(uint64_t w, uint32_t e) { return (uint32_t)(w >> 32) == e; }
+// two bf16 values, each with a 16-bit epoch, in one 8-byte word (element 2i in the low half)
+__device__ __forceinline__ uint64_t ll_pack16x2(float a, float b, uint32_t e) {
+    const uint64_t lo = f32_to_bf16_bits(a) | ((e & 0xffffu) << 16);
+    const uint64_t hi = f32_to_bf16_bits(b) | ((e & 0xffffu) << 16);
+    return lo | (hi << 32);
+}
+__device__ __forceinline__ bool ll_ok16x2(uint64_t w, uint32_t e) {
+    const uint32_t e16 = e & 0xffffu;
+    return ((uint32_t)(w >> 16) & 0xffffu) == e16 && (uint32_t)(w >> 48) == e16;
+}
+__device__ __forceinline__ void ll_put16(uint32_t* p, float v, uint32_t e) {
+    __hip_atomic_store(p, f32_to_bf16_bits(v) | ((e & 0xffffu) << 16), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ------------------------------------------------------------- barrier ----
-
-struct DlBarrier {
-    uint32_t* group;  // [DL_GROUPS] counters, 256 B apart
-    uint32_t* all;    // group-complete counter
-    uint32_t* gen;    // generation released
-    uint32_t* status;
-    uint32_t base;    // generation at launch
-    uint32_t round;
-};
-
-__device__ __forceinline__ void dl_grid_barrier(DlBarrier& b) {
-    ++b.round;
-    // Every wave waits for its own stores to complete before the block
-    // arrives.  The shared vectors are written with agent-scope (sc1) stores,
-    // which complete once they are performed at the device coherence point, so
-    // a completed store is visible to every later sc1 load on any XCD; a
-    // workgroup-scope fence would not wait for them on this part.  The wait
-    // also covers any load still in flight (vector memory counts retire in
-    // order), so no weight load of the next phase is issued before a barrier.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t target = b.base + b.round;
-        constexpr uint32_t per_group = DL_BLOCKS / DL_GROUPS;
-        uint32_t* gc = b.group + 64 * (blockIdx.x % DL_GROUPS);
-        const uint32_t prev = __hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (prev + 1u == target * per_group) {
-            const uint32_t g = __hip_atomic_fetch_add(b.all, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (g + 1u == target * DL_GROUPS)
-                __hip_atomic_store(b.gen, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Load N words (addr(i)) until ok(i, word) holds for all of them; bounded.
+template <int N, class Addr, class Ok>
+__device__ __forceinline__ void ll_wait(uint64_t (&w)[N], Addr addr, Ok ok, uint32_t* status) {
+    for (uint32_t polls = 0;; ++polls) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) w[i] = ll_load(addr(i));
+        bool all = true;
+#pragma unroll
+        for (int i = 0; i < N; ++i) all = all && ok(i, w[i]);
+        if (all) break;
+        if (polls >= DL_SPIN_LIMIT) {
+            __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
         }
-        uint32_t polls = 0;
-        while ((int32_t)(__hip_atomic_load(b.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-            if (++polls > DL_SPIN_LIMIT) {
-                __hip_atomic_store(b.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
+        __builtin_amdgcn_s_sleep(1);
     }
-    __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
 struct DlAttnLds {
@@ -146,9 +173,10 @@ constexpr int DL_QKV_ROWS = 32 * DL_D + 2 * 8 * DL_D;  // 6144
 
 union DlShared {
     struct {
-        uint32_t xp[DL_MLP / 2];
+        uint32_t xp[xp_words(DL_MLP)];
         float xsum[DL_MLP / 32];
         float red[DL_WAVES];
+        float hold[DL_WAVES * 4];  // residual epilogue: the old h of the block's rows [wave][unit]
     } g;
     DlAttnLds at;
 };
@@ -176,7 +204,7 @@ struct DlRows {
 template <int NSB, int NG>
 __device__ __forceinline__ void dl_issue_unit(DlUnit<NSB, NG>& u, const DlRows& r, uint32_t row) {
     constexpr int ROW_BYTES = NSB * 144;
-    const int lane = threadIdx.x & 63;
+    const int lane = dl_tid() & 63;
     const int sbo = lane >> 2;
     const int g = lane & 3;
     row = row < r.n_rows ? row : r.n_rows - 1;
@@ -194,25 +222,78 @@ __device__ __forceinline__ void dl_issue_unit(DlUnit<NSB, NG>& u, const DlRows& 
     }
 }
 
+// Where a phase's input vector comes from.
+enum DlSrc {
+    DL_SRC_PLAIN = 0,  // fp32, written before the launch (h at layer 0)
+    DL_SRC_LL32,       // fp32 + epoch words
+    DL_SRC_LL16,       // bf16 + epoch16 words
+};
+
+// The old h of the block's rows for a residual epilogue: thread t < 8 upw
+// fetches row (blockIdx.x * 8 + t / upw) + (t % upw) * DL_NW into lds[t].
+struct DlHold {
+    int kind;         // DL_SRC_PLAIN or DL_SRC_LL32; < 0: no residual
+    const void* src;
+    uint32_t e;
+    float* lds;
+    int upw;
+};
+
 // Stage x (K values) in LDS as fp16 pair words + sub-block sums.  RMSNORM:
-// x = bf16(h * rsqrt(mean(h^2) + eps) * w), h read coherently; otherwise x =
-// bf16(src) with src an fp32 activation written by an earlier phase.
+// x = bf16(h * rsqrt(mean(h^2) + eps) * w); otherwise x = bf16(src).  The
+// residual values of the block's rows (hd) are awaited with the same loads.
 template <int K, bool RMSNORM>
-__device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red, const float* src,
-                                           const float* norm_w, float eps) {
+__device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red, int src_kind, const void* src,
+                                           uint32_t e, const float* norm_w, float eps, const DlHold& hd,
+                                           uint32_t* status) {
     constexpr int PT = K / (4 * DL_THREADS);
     static_assert(K % (4 * DL_THREADS) == 0, "K must fill the block");
-    const int tid = threadIdx.x;
+    const int tid = dl_tid();
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool has_hold = hd.kind >= 0 && tid < DL_WAVES * hd.upw;
+    const uint64_t* hold_ll = reinterpret_cast<const uint64_t*>(hd.src) +
+                              (has_hold ? (blockIdx.x * DL_WAVES + tid / hd.upw) + (tid % hd.upw) * DL_NW : 0);
+    const bool hold_ll_wait = has_hold && hd.kind == DL_SRC_LL32;
+    float hold = 0.0f;
+    if (has_hold && hd.kind == DL_SRC_PLAIN)
+        hold = reinterpret_cast<const float*>(hd.src)[(blockIdx.x * DL_WAVES + tid / hd.upw) + (tid % hd.upw) * DL_NW];
     float4 hv[PT];
+    if (src_kind == DL_SRC_PLAIN) {
+        const float* x = reinterpret_cast<const float*>(src);
 #pragma unroll
-    for (int j = 0; j < PT; ++j) {
-        const int k = (j * DL_THREADS + tid) * 4;
-        const float2 a = ld_coh2(src + k);
-        const float2 b = ld_coh2(src + k + 2);
-        hv[j] = make_float4(a.x, a.y, b.x, b.y);
+        for (int j = 0; j < PT; ++j) hv[j] = *reinterpret_cast<const float4*>(x + (j * DL_THREADS + tid) * 4);
+    } else if (src_kind == DL_SRC_LL32) {
+        const uint64_t* x = reinterpret_cast<const uint64_t*>(src);
+        uint64_t w[4 * PT];
+        ll_wait(w, [&](int i) { return x + ((i / 4) * DL_THREADS + tid) * 4 + (i % 4); },
+                [&](int, uint64_t v) { return ll_ok32(v, e); }, status);
+#pragma unroll
+        for (int j = 0; j < PT; ++j)
+            hv[j] = make_float4(ll_val32(w[4 * j]), ll_val32(w[4 * j + 1]), ll_val32(w[4 * j + 2]),
+                                ll_val32(w[4 * j + 3]));
+    } else {
+        // 2 elements per word; word 2 PT is the residual value (threads without one re-read word 0)
+        const uint64_t* x = reinterpret_cast<const uint64_t*>(src);
+        uint64_t w[2 * PT + 1];
+        ll_wait(w,
+                [&](int i) {
+                    return i < 2 * PT ? x + ((i / 2) * DL_THREADS + tid) * 2 + (i % 2)
+                                      : (hold_ll_wait ? hold_ll : x + tid * 2);
+                },
+                [&](int i, uint64_t v) {
+                    return i < 2 * PT || !hold_ll_wait ? ll_ok16x2(v, e) : ll_ok32(v, hd.e);
+                },
+                status);
+#pragma unroll
+        for (int j = 0; j < PT; ++j)
+            hv[j] = make_float4(bf16_bits_to_f32((uint32_t)w[2 * j] & 0xffffu),
+                                bf16_bits_to_f32((uint32_t)(w[2 * j] >> 32) & 0xffffu),
+                                bf16_bits_to_f32((uint32_t)w[2 * j + 1] & 0xffffu),
+                                bf16_bits_to_f32((uint32_t)(w[2 * j + 1] >> 32) & 0xffffu));
+        if (hold_ll_wait) hold = ll_val32(w[2 * PT]);
     }
+    if (has_hold) hd.lds[tid] = hold;
     if constexpr (RMSNORM) {
         float4 wv[PT];
 #pragma unroll
@@ -257,7 +338,7 @@ template <int NSB, int NG>
 __device__ __forceinline__ void dl_dot_unit(const DlUnit<NSB, NG>& u, const uint32_t* xp, const float* xsum,
                                             const Q4LaneConsts& lc, float (&res)[NG]) {
     constexpr int NIT = DlUnit<NSB, NG>::NIT;
-    const int lane = threadIdx.x & 63;
+    const int lane = dl_tid() & 63;
     const int sbo = lane >> 2;
     const int g = lane & 3;
     float acc[NG];
@@ -275,41 +356,66 @@ __device__ __forceinline__ void dl_dot_unit(const DlUnit<NSB, NG>& u, const uint
     for (int gi = 0; gi < NG; ++gi) res[gi] = wave_sum(acc[gi]);
 }
 
-//   STORE: y[row] = dot;  RESID: y[row] += dot;  SWIGLU: y[row] = bf16(silu(g) * u) (kept in fp32)
+// Where a phase's output goes.
+struct DlOut {
+    uint64_t* ll32;      // STORE / RESID: fp32 + epoch words
+    uint32_t* ll16;      // SWIGLU: bf16 + epoch16 words
+    float* plain;        // RESID on the last layer: the caller's h (no epoch)
+    DlHold hold;         // RESID: where the old h comes from (staged in LDS with x)
+    uint32_t e_out;      // epoch written
+};
+
+//   STORE: y[row] = dot;  RESID: y[row] = h_old[row] + dot;  SWIGLU: y[row] = bf16(silu(g) * u)
 template <int NG, int EPI>
-__device__ __forceinline__ void dl_store_row(float* y, uint32_t row, uint32_t n_rows, const float (&res)[NG]) {
-    if ((threadIdx.x & 63) == 0 && row < n_rows) {
+__device__ __forceinline__ void dl_store_row(const DlOut& o, uint32_t row, uint32_t n_rows, const float (&res)[NG],
+                                             const float* hold) {
+    if ((dl_tid() & 63) == 0 && row < n_rows) {
         if constexpr (EPI == DL_EPI_STORE) {
-            st_coh(y + row, res[0]);
+            ll_put32(o.ll32 + row, res[0], o.e_out);
         } else if constexpr (EPI == DL_EPI_RESID) {
-            st_coh(y + row, ld_coh(y + row) + res[0]);
+            const float old = *hold;
+            if (o.plain != nullptr)
+                o.plain[row] = old + res[0];
+            else
+                ll_put32(o.ll32 + row, old + res[0], o.e_out);
         } else {
-            st_coh(y + row, bf16_round(silu(res[0]) * res[NG - 1]));
+            ll_put16(o.ll16 + row, silu(res[0]) * res[NG - 1], o.e_out);
         }
     }
 }
 
 // One GEMV phase over the wave's UPW units (rows wrow + i * DL_NW), streamed
-// through a ring of R units.  The first R units are issued before x is
-// staged, so the weight stream is in flight while the block normalises x;
-// unit i + R is issued right after unit i has been reduced.  The loop is
+// through a ring of R units.  Vector memory returns in order on a CU, so the
+// input (polled after the weights already issued) arrives only after them:
+// PRE units are issued before the input is awaited, enough to keep HBM busy
+// while the rest of the chip finishes the previous phase, and units PRE .. R-1
+// right after it is staged, so they stream while the first units are reduced.
+// Unit i + R is issued right after unit i has been reduced.  The loop is
 // unrolled, so the ring is static registers, and the scheduling fences keep
 // each refill after the reduction that frees its registers.
-template <int NSB, int NG, int UPW, int R, int EPI, bool RMSNORM>
-__device__ __forceinline__ void dl_gemv_phase(DlShared& sm, const DlRows& rows, uint32_t wrow, const float* x_src,
-                                              const float* norm_w, float eps, float* y) {
-    static_assert(R >= 1 && R <= UPW, "ring size");
+template <int NSB, int NG, int UPW, int R, int PRE, int EPI, bool RMSNORM>
+__device__ __forceinline__ void dl_gemv_phase(DlShared& sm, const DlRows& rows, uint32_t wrow, int src_kind,
+                                              const void* x_src, uint32_t e_x, const float* norm_w, float eps,
+                                              const DlOut& out, uint32_t* status) {
+    static_assert(PRE >= 1 && PRE <= R && R <= UPW, "ring size");
     DlUnit<NSB, NG> u[UPW];
 #pragma unroll
-    for (int i = 0; i < R; ++i) dl_issue_unit(u[i], rows, wrow + (uint32_t)i * DL_NW);
-    dl_stage_x<NSB * 256, RMSNORM>(sm.g.xp, sm.g.xsum, sm.g.red, x_src, norm_w, eps);
-    const Q4LaneConsts lc = q4k_lane_consts(threadIdx.x & 3);
+    for (int i = 0; i < PRE; ++i) dl_issue_unit(u[i], rows, wrow + (uint32_t)i * DL_NW);
+    __syncthreads();  // every wave is done with the previous phase's LDS
+    DlHold hd = out.hold;
+    hd.lds = sm.g.hold;
+    if (EPI != DL_EPI_RESID) hd.kind = -1;
+    dl_stage_x<NSB * 256, RMSNORM>(sm.g.xp, sm.g.xsum, sm.g.red, src_kind, x_src, e_x, norm_w, eps, hd, status);
+#pragma unroll
+    for (int i = PRE; i < R; ++i) dl_issue_unit(u[i], rows, wrow + (uint32_t)i * DL_NW);
+    const Q4LaneConsts lc = q4k_lane_consts(dl_tid() & 3);
+    const int wave = __builtin_amdgcn_readfirstlane(dl_tid() >> 6);
 #pragma unroll
     for (int i = 0; i < UPW; ++i) {
         __builtin_amdgcn_sched_barrier(0);
         float res[NG];
         dl_dot_unit(u[i], sm.g.xp, sm.g.xsum, lc, res);
-        dl_store_row<NG, EPI>(y, wrow + (uint32_t)i * DL_NW, rows.n_rows, res);
+        dl_store_row<NG, EPI>(out, wrow + (uint32_t)i * DL_NW, rows.n_rows, res, &sm.g.hold[wave * UPW + i]);
         __builtin_amdgcn_sched_barrier(0);
         if (i + R < UPW) dl_issue_unit(u[i + R], rows, wrow + (uint32_t)(i + R) * DL_NW);
     }
@@ -330,7 +436,7 @@ __device__ __forceinline__ int dl_att_span(int L) {
 
 __device__ __forceinline__ void dl_attn_issue(DlAttnBank& bk, const uint16_t* kc, const uint16_t* vc, int kvh, int p0,
                                               int L) {
-    const int lane = threadIdx.x & 63;
+    const int lane = dl_tid() & 63;
     const int p_k = lane >> 2, part = lane & 3;
     const size_t stride = (size_t)8 * DL_D;
 #pragma unroll
@@ -349,7 +455,7 @@ __device__ __forceinline__ void dl_attn_issue(DlAttnBank& bk, const uint16_t* kc
 
 __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w, bool has_w, float eps, float cs,
                                              float sn, bool rope, float& r0, float& r1) {
-    const int lane = threadIdx.x & 63;
+    const int lane = dl_tid() & 63;
     float n0 = x0, n1 = x1;
     if (has_w) {
         const float ss = wave_sum(x0 * x0 + x1 * x1);
@@ -369,9 +475,9 @@ __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w,
 // Block (kv head kvh, slot bs): wave w covers positions [p0, p0 + span) of the
 // first L; the block's (max, sum, output) per q head goes to part[kvh][bs].
 __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds& sm, const DlArgs& a, const uint64_t* lp, int kvh,
-                              int bs, int pos, int L) {
+                              int bs, int pos, int L, uint32_t e_qkv, uint32_t e_part) {
     constexpr int GROUP = 4;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int span = dl_att_span(L);
     const int p0 = (bs * DL_WAVES + wave) * span;
     int rows = L - p0;
@@ -384,9 +490,11 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds& s
     const float* k_norm = reinterpret_cast<const float*>(lp[DL_K_NORM]);
     uint16_t* kc = reinterpret_cast<uint16_t*>(lp[DL_K_CACHE]);
     uint16_t* vc = reinterpret_cast<uint16_t*>(lp[DL_V_CACHE]);
-    const float* q = a.qkv;
-    const float* kn = a.qkv + 32 * DL_D;
-    const float* vn = a.qkv + 40 * DL_D;
+    const uint64_t* q = a.qkv_ll;
+    const uint64_t* kn = a.qkv_ll + 32 * DL_D;
+    const uint64_t* vn = a.qkv_ll + 40 * DL_D;
+    auto ok = [&](int, uint64_t v) { return ll_ok32(v, e_qkv); };
+    __syncthreads();  // every wave is done with the previous phase's LDS
 
     float cs = 1.0f, sn = 0.0f;
     if (rope && (wave < GROUP || has_new)) {
@@ -395,23 +503,25 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds& s
     }
     if (wave < GROUP) {
         const int hq = kvh * GROUP + wave;
+        uint64_t w[2];
+        ll_wait(w, [&](int i) { return q + hq * DL_D + lane + 64 * i; }, ok, a.status);
         float r0, r1;
-        dl_norm_rope(ld_coh(q + hq * DL_D + lane), ld_coh(q + hq * DL_D + lane + 64), q_norm, q_norm != nullptr,
-                     a.eps, cs, sn, rope, r0, r1);
+        dl_norm_rope(ll_val32(w[0]), ll_val32(w[1]), q_norm, q_norm != nullptr, a.eps, cs, sn, rope, r0, r1);
         const float scale = 1.0f / sqrtf((float)DL_D);
         sm.qs[wave][lane >> 5][lane & 31] = r0 * scale;
         sm.qs[wave][2 + (lane >> 5)][lane & 31] = r1 * scale;
     }
     uint32_t vnew = 0;
     if (has_new) {
+        uint64_t w[4];
+        ll_wait(w, [&](int i) { return i < 2 ? kn + kvh * DL_D + lane + 64 * i : vn + kvh * DL_D + 2 * lane + (i - 2); },
+                ok, a.status);
         float k0, k1;
-        dl_norm_rope(ld_coh(kn + kvh * DL_D + lane), ld_coh(kn + kvh * DL_D + lane + 64), k_norm, k_norm != nullptr,
-                     a.eps, cs, sn, rope, k0, k1);
+        dl_norm_rope(ll_val32(w[0]), ll_val32(w[1]), k_norm, k_norm != nullptr, a.eps, cs, sn, rope, k0, k1);
         const uint16_t kb0 = (uint16_t)f32_to_bf16_bits(k0), kb1 = (uint16_t)f32_to_bf16_bits(k1);
         sm.knew[lane] = kb0;
         sm.knew[lane + 64] = kb1;
-        const float2 vv = ld_coh2(vn + kvh * DL_D + 2 * lane);
-        vnew = pack_bf16x2(vv.x, vv.y);
+        vnew = pack_bf16x2(ll_val32(w[2]), ll_val32(w[3]));
         const size_t off = (size_t)pos * 8 * DL_D + (size_t)kvh * DL_D;
         kc[off + lane] = kb0;
         kc[off + lane + 64] = kb1;
@@ -439,9 +549,12 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds& s
 #pragma unroll
         for (int gg = 0; gg < GROUP; ++gg) s[r][gg] = 0.0f;
     }
-    // each q fragment read from LDS once and used for both K rows
+    // each q fragment read from LDS once and used for both K rows; the
+    // scheduling fence keeps the q reads of one quarter from being hoisted
+    // ahead of the previous one's products
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
         float kf[2][8];
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
@@ -518,7 +631,7 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds& s
     }
     __syncthreads();
     // block partial: [kvh][bs][g] = (M, l, o[128])
-    float* pb = a.part + (((size_t)kvh * DL_ATT_SLOTS + bs) * GROUP) * (2 + DL_D);
+    uint64_t* pb = a.part_ll + (((size_t)kvh * DL_ATT_SLOTS + bs) * GROUP) * (2 + DL_D);
     for (int idx = tid; idx < GROUP * 64; idx += DL_THREADS) {
         const int gg = idx >> 6, dl = idx & 63;
         float M = -INFINITY;
@@ -534,25 +647,36 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds& s
             r0 = fmaf(f, ov.x, r0);
             r1 = fmaf(f, ov.y, r1);
         }
-        float* pg = pb + gg * (2 + DL_D);
-        st_coh2(pg + 2 + 2 * dl, r0, r1);
-        if (dl == 0) st_coh2(pg, M, l);
+        uint64_t* pg = pb + gg * (2 + DL_D);
+        ll_put32(pg + 2 + 2 * dl, r0, e_part);
+        ll_put32(pg + 3 + 2 * dl, r1, e_part);
+        if (dl == 0) {
+            ll_put32(pg, M, e_part);
+            ll_put32(pg + 1, l, e_part);
+        }
     }
 }
 
 // Head hq = blockIdx.x (< 32): merge the DL_ATT_SLOTS block partials of its kv head.
-__device__ __forceinline__ void dl_merge_phase(DlAttnLds& sm, const DlArgs& a, int hq) {
+__device__ __forceinline__ void dl_merge_phase(DlAttnLds& sm, const DlArgs& a, int hq, uint32_t e_part,
+                                               uint32_t e_attn) {
     constexpr int GROUP = 4;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kvh = hq / GROUP, gg = hq % GROUP;
     constexpr int PER_WAVE = DL_ATT_SLOTS / DL_WAVES;  // 4 partials per wave
+    __syncthreads();  // every wave is done with the previous phase's LDS
+    uint64_t w[4 * PER_WAVE];
+    ll_wait(w, [&](int i) {
+                const int bs = wave * PER_WAVE + i / 4, k = i % 4;
+                const uint64_t* pg = a.part_ll + (((size_t)kvh * DL_ATT_SLOTS + bs) * GROUP + gg) * (2 + DL_D);
+                return k < 2 ? pg + k : pg + 2 + 2 * lane + (k - 2);
+            },
+            [&](int, uint64_t v) { return ll_ok32(v, e_part); }, a.status);
     float2 ml[PER_WAVE], ov[PER_WAVE];
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
-        const int bs = wave * PER_WAVE + i;
-        const float* pg = a.part + (((size_t)kvh * DL_ATT_SLOTS + bs) * GROUP + gg) * (2 + DL_D);
-        ml[i] = ld_coh2(pg);
-        ov[i] = ld_coh2(pg + 2 + 2 * lane);
+        ml[i] = make_float2(ll_val32(w[4 * i]), ll_val32(w[4 * i + 1]));
+        ov[i] = make_float2(ll_val32(w[4 * i + 2]), ll_val32(w[4 * i + 3]));
     }
     float M = -INFINITY;
 #pragma unroll
@@ -586,7 +710,7 @@ __device__ __forceinline__ void dl_merge_phase(DlAttnLds& sm, const DlArgs& a, i
             a1 = fmaf(f, o.y, a1);
         }
         const float inv = 1.0f / lt;
-        st_coh2(a.attn + hq * DL_D + 2 * lane, a0 * inv, a1 * inv);
+        ll_store(reinterpret_cast<uint64_t*>(a.attn_ll) + (hq * DL_D) / 2 + lane, ll_pack16x2(a0 * inv, a1 * inv, e_attn));
     }
 }
 
@@ -596,13 +720,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
     __shared__ __align__(16) DlShared sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t wrow = blockIdx.x * DL_WAVES + wave;
-    DlBarrier bar;
-    bar.group = a.bar;
-    bar.all = a.bar + 64 * DL_GROUPS;
-    bar.gen = a.bar + 64 * (DL_GROUPS + 1);
-    bar.status = a.status;
-    bar.base = __hip_atomic_load(bar.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bar.round = 0;
+    const uint32_t seq = a.ctl[0];  // written by the previous launch
     const int pos = *a.pos_ptr;
     const int L = pos + 1 < (int)a.s_cap ? pos + 1 : (int)a.s_cap;
     const int kvh = blockIdx.x % 8, bs = blockIdx.x / 8;
@@ -642,12 +760,21 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
     const int att_p0 = (bs * DL_WAVES + wave) * span;
 
     for (uint32_t layer = 0; layer < a.n_layers; ++layer) {
+        const bool first = layer == 0, last = layer + 1 == a.n_layers;
+        const uint32_t e_qkv = dl_epoch(seq, layer, DL_E_QKV), e_part = dl_epoch(seq, layer, DL_E_PART);
+        const uint32_t e_attn = dl_epoch(seq, layer, DL_E_ATTN), e_ho = dl_epoch(seq, layer, DL_E_H_O);
+        const uint32_t e_act = dl_epoch(seq, layer, DL_E_ACT), e_hd = dl_epoch(seq, layer, DL_E_H_DOWN);
+        const uint32_t e_hprev = first ? 0u : dl_epoch(seq, layer - 1, DL_E_H_DOWN);
+        DlOut out;
+        out.hold.kind = -1;
         // ---- Q|K|V: RMSNorm(h) . [Wq; Wk; Wv]^T
-        dl_gemv_phase<DL_HSB, 1, 3, 3, DL_EPI_STORE, true>(sm, qkv_rows(layer), wrow, a.h,
-                                                          reinterpret_cast<const float*>(layer_ptr(layer, DL_IN_NORM)),
-                                                          a.eps, a.qkv);
-        dl_grid_barrier(bar);
-        // ---- attention split
+        out.ll32 = a.qkv_ll;
+        out.e_out = e_qkv;
+        dl_gemv_phase<DL_HSB, 1, 3, 3, DL_PRE_QKV, DL_EPI_STORE, true>(
+            sm, qkv_rows(layer), wrow, first ? DL_SRC_PLAIN : DL_SRC_LL32,
+            first ? static_cast<const void*>(a.h) : static_cast<const void*>(a.h_ll), e_hprev,
+            reinterpret_cast<const float*>(layer_ptr(layer, DL_IN_NORM)), a.eps, out, a.status);
+        // ---- attention split: the K/V rows are loaded before q|k|v is awaited
         {
             uint64_t lp[DL_LAYER_PTRS];
 #pragma unroll
@@ -655,45 +782,64 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
             DlAttnBank bk;
             dl_attn_issue(bk, reinterpret_cast<const uint16_t*>(lp[DL_K_CACHE]),
                           reinterpret_cast<const uint16_t*>(lp[DL_V_CACHE]), kvh, att_p0, L);
-            dl_attn_phase(bk, sm.at, a, lp, kvh, bs, pos, L);
+            dl_attn_phase(bk, sm.at, a, lp, kvh, bs, pos, L, e_qkv, e_part);
         }
-        dl_grid_barrier(bar);
-        // ---- attention merge
-        if (blockIdx.x < 32) dl_merge_phase(sm.at, a, blockIdx.x);
-        dl_grid_barrier(bar);
+        // ---- attention merge (blocks 0..31, one q head each)
+        if (blockIdx.x < 32) dl_merge_phase(sm.at, a, blockIdx.x, e_part, e_attn);
         // ---- o_proj + residual
-        dl_gemv_phase<DL_HSB, 1, 2, 2, DL_EPI_RESID, false>(sm, o_rows(layer), wrow, a.attn, nullptr, a.eps, a.h);
-        dl_grid_barrier(bar);
+        out.ll32 = a.h_ll;
+        out.plain = nullptr;
+        out.hold.kind = first ? DL_SRC_PLAIN : DL_SRC_LL32;
+        out.hold.src = first ? static_cast<const void*>(a.h) : static_cast<const void*>(a.h_ll);
+        out.hold.e = e_hprev;
+        out.hold.upw = 2;
+        out.e_out = e_ho;
+        dl_gemv_phase<DL_HSB, 1, 2, 2, DL_PRE_O, DL_EPI_RESID, false>(sm, o_rows(layer), wrow, DL_SRC_LL16, a.attn_ll, e_attn,
+                                                           nullptr, a.eps, out, a.status);
         // ---- RMSNorm + gate|up + SwiGLU
-        dl_gemv_phase<DL_HSB, 2, 6, 3, DL_EPI_SWIGLU, true>(sm, gu_rows(layer), wrow, a.h,
-                                                           reinterpret_cast<const float*>(layer_ptr(layer, DL_POST_NORM)),
-                                                           a.eps, a.act);
-        dl_grid_barrier(bar);
-        // ---- down + residual
-        dl_gemv_phase<DL_MSB, 1, 2, 2, DL_EPI_RESID, false>(sm, down_rows(layer), wrow, a.act, nullptr, a.eps, a.h);
-        if (layer + 1 < a.n_layers) dl_grid_barrier(bar);
+        out.ll16 = a.act_ll;
+        out.e_out = e_act;
+        dl_gemv_phase<DL_HSB, 2, 6, 3, DL_PRE_GU, DL_EPI_SWIGLU, true>(
+            sm, gu_rows(layer), wrow, DL_SRC_LL32, a.h_ll, e_ho,
+            reinterpret_cast<const float*>(layer_ptr(layer, DL_POST_NORM)), a.eps, out, a.status);
+        // ---- down + residual (the last layer writes the caller's h)
+        out.ll32 = a.h_ll;
+        out.plain = last ? a.h : nullptr;
+        out.hold.kind = DL_SRC_LL32;
+        out.hold.src = a.h_ll;
+        out.hold.e = e_ho;
+        out.hold.upw = 2;
+        out.e_out = e_hd;
+        dl_gemv_phase<DL_MSB, 1, 2, 2, DL_PRE_DOWN, DL_EPI_RESID, false>(sm, down_rows(layer), wrow, DL_SRC_LL16, a.act_ll, e_act,
+                                                           nullptr, a.eps, out, a.status);
     }
+    // Every block has read the launch counter before block 0 can get here: its
+    // last phase consumed every block's output.
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.ctl[0] = seq + 1u;
 }
 
 static size_t dl_align(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct DlLayout {
-    size_t qkv, attn, act, part, bar, total;
+    size_t ctl, qkv, attn, act, h, part, total;
 };
 
+// Workspace: launch counter, then the epoch-tagged vectors.
 static DlLayout dl_layout() {
     DlLayout l;
     size_t off = 0;
-    l.bar = off;
-    off += dl_align(4 * 64 * (DL_GROUPS + 2) + 4);
+    l.ctl = off;
+    off += 256;
     l.qkv = off;
-    off += dl_align((size_t)DL_QKV_ROWS * 4);
+    off += dl_align((size_t)DL_QKV_ROWS * 8);
     l.attn = off;
     off += dl_align((size_t)32 * DL_D * 4);
     l.act = off;
     off += dl_align((size_t)DL_MLP * 4);
+    l.h = off;
+    off += dl_align((size_t)DL_HID * 8);
     l.part = off;
-    off += dl_align((size_t)8 * DL_ATT_SLOTS * 4 * (2 + DL_D) * 4);
+    off += dl_align((size_t)8 * DL_ATT_SLOTS * 4 * (2 + DL_D) * 8);
     l.total = off;
     return l;
 }
@@ -714,8 +860,8 @@ static bool dl_grid_fits() {
 }
 
 }  // namespace t2h
-
 using namespace t2h;
+
 
 extern "C" size_t t2h_qwen3_decode_layers_workspace_bytes(uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk,
                                                          uint32_t d) {
@@ -746,11 +892,12 @@ extern "C" int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_l
     a.s_cap = s_cap;
     a.eps = eps;
     a.theta = theta;
-    a.qkv = reinterpret_cast<float*>(ws + l.qkv);
-    a.attn = reinterpret_cast<float*>(ws + l.attn);
-    a.act = reinterpret_cast<float*>(ws + l.act);
-    a.part = reinterpret_cast<float*>(ws + l.part);
-    a.bar = reinterpret_cast<uint32_t*>(ws + l.bar);
+    a.ctl = reinterpret_cast<uint32_t*>(ws + l.ctl);
+    a.qkv_ll = reinterpret_cast<uint64_t*>(ws + l.qkv);
+    a.attn_ll = reinterpret_cast<uint32_t*>(ws + l.attn);
+    a.act_ll = reinterpret_cast<uint32_t*>(ws + l.act);
+    a.h_ll = reinterpret_cast<uint64_t*>(ws + l.h);
+    a.part_ll = reinterpret_cast<uint64_t*>(ws + l.part);
     a.status = status;
     hipLaunchKernelGGL(decode_layers_kernel, dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
                        reinterpret_cast<hipStream_t>(stream), a);

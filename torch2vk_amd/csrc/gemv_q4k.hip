@@ -146,7 +146,7 @@ __global__ __launch_bounds__(WPB * 64) void q4k_gemv_kernel(const Q4GemvArgs a) 
     // block's waves) and each lane then reads its slices from LDS.  The x-side
     // loads go first and only the first weight stage is issued before the
     // prologue: vmcnt retires in order, so the prologue waits for x alone.
-    __shared__ __align__(16) uint32_t xp[K / 2];
+    __shared__ __align__(16) uint32_t xp[xp_words(K)];
     __shared__ float xsum[K / 32];
     constexpr int PT = (K + 4 * NT - 1) / (4 * NT);  // 4-value groups per thread
     if constexpr (PRO == Q4PRO_RMSNORM) {

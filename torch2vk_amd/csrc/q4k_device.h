@@ -30,6 +30,14 @@ __device__ __forceinline__ uint32_t in_vgpr(uint32_t v) {
     return r;
 }
 
+// LDS layout of a staged x: fp16 pair words, 32 words (64 values) per group,
+// each group followed by 4 pad words.  A lane's x slice is one whole group
+// (superblock sb, nibble group g), and the pad puts the 8 lanes that share a
+// 128-byte LDS cycle (4 groups of 2 superblocks) on distinct banks: without it
+// every lane's slice starts on bank 0 and each 16-byte read is 8-way serialised.
+__host__ __device__ constexpr int xp_words(int k) { return k / 2 + (k / 64) * 4; }
+__device__ __forceinline__ int xp_word(int k) { return (k >> 1) + ((k >> 6) << 2); }
+
 // Stage 4 consecutive x values (already bf16-exact) at element k: one fp16
 // pair word (e0,e2) and one (e1,e3), and, through the 8 threads that hold one
 // 32-value sub-block, that sub-block's sum.  All 8 threads of a sub-block call
@@ -37,7 +45,7 @@ __device__ __forceinline__ uint32_t in_vgpr(uint32_t v) {
 __device__ __forceinline__ void stage_x4(uint32_t* xp, float* xsum, int k, float v0, float v1, float v2, float v3) {
     const uint32_t a = f32_to_f16_bits(v0) | (f32_to_f16_bits(v2) << 16);
     const uint32_t b = f32_to_f16_bits(v1) | (f32_to_f16_bits(v3) << 16);
-    *reinterpret_cast<uint2*>(&xp[k / 2]) = make_uint2(a, b);
+    *reinterpret_cast<uint2*>(&xp[xp_word(k)]) = make_uint2(a, b);
     float s = (v0 + v1) + (v2 + v3);
     s += dpp_f32<0xB1>(s);  // quad_perm [1,0,3,2]: lane ^ 1
     s += dpp_f32<0x4E>(s);  // quad_perm [2,3,0,1]: lane ^ 2
@@ -55,7 +63,7 @@ struct XSlice16 {
 };
 
 __device__ __forceinline__ void load_xslice16(const uint32_t* xp, const float* xsum, int sb, int g, XSlice16& xs) {
-    const uint32_t* p = xp + (sb * 256 + 64 * g) / 2;
+    const uint32_t* p = xp + xp_word(sb * 256 + 64 * g);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint4 v = *reinterpret_cast<const uint4*>(p + 4 * i);
