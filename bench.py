@@ -29,7 +29,12 @@ from pathlib import Path
 
 HBM_PEAK_GBS = 8000.0
 HEADLINE_METRIC = "Qwen3-8B-shape int4 decode tok/s @bs1; q-matmul HBM GB/s vs ~8 TB/s peak"
-TRAFFIC_PROFILE = Path(__file__).resolve().parent / "profiles" / "gate_up_gemv_qwen3_8b_pmc.md"
+PROFILES = Path(__file__).resolve().parent / "profiles"
+# HBM traffic of the dominant kernel (two rocprofv3 --pmc passes), per decode path
+TRAFFIC_PROFILES = {
+    "decode_layers_persistent": PROFILES / "decode_layers_qwen3_8b_int4_kv4096_pmc.md",
+    "gate_up_rmsnorm_swiglu_gemv": PROFILES / "gate_up_gemv_qwen3_8b_pmc.md",
+}
 PROMPT_POSITIONS = 4096
 
 
@@ -50,15 +55,17 @@ def parse_args():
     p.add_argument("--per-op", action="store_true",
                    help="one launch per op instead of the persistent layers kernel (t2h_qwen3_decode_layers)")
     p.add_argument("--profile-kernel", action="store_true",
-                   help="counter-collection target: run the dominant kernel over all layers plus a 256 MiB copy "
-                        "(the calibration for FETCH_SIZE/WRITE_SIZE), no timing, no JSON line")
+                   help="counter-collection target: run the dominant kernel (the persistent layers kernel, or "
+                        "with --per-op the gate|up GEMV over all layers) plus a 256 MiB copy (the calibration for "
+                        "FETCH_SIZE/WRITE_SIZE), no timing, no JSON line")
     return p.parse_args()
 
 
-def profile_kernel_target() -> int:
-    """Launch sequence for `rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE`: 36 dominant-kernel launches
-    (one per layer) x 2, then one plain 256 MiB device copy whose traffic is known (256 MiB read +
-    256 MiB written), so counter readings can be scaled to bytes."""
+def profile_kernel_target(per_op: bool) -> int:
+    """Launch sequence for `rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE`: the dominant kernel twice over all
+    layers (the persistent layers kernel at KV 4096, 2 dispatches; or, per op, the gate|up GEMV once per
+    layer, 72 dispatches), then one plain 256 MiB device copy whose traffic is known (256 MiB read + 256 MiB
+    written), so counter readings can be scaled to bytes."""
     import torch
 
     from torch2vk_amd import kernels
@@ -68,12 +75,24 @@ def profile_kernel_target() -> int:
 
     dev = torch.device("cuda:0")
     w = synthetic_weights(QWEN3_8B, device=dev, seed=0)
-    dec = Qwen3Decoder(w, max_positions=64, max_new_tokens=4, device=dev)
-    dec.h.normal_()
-    for _ in range(2):
-        for i in range(QWEN3_8B.layers):
-            kernels.q4k_rmsnorm_swiglu(dec.h, w.norms[f"layers.{i}.post_norm"], w.packed[f"layers.{i}.gate"],
-                                       w.packed[f"layers.{i}.up"], dec.act)
+    if per_op:
+        dec = Qwen3Decoder(w, max_positions=64, max_new_tokens=4, device=dev, persistent=False)
+        dec.h.normal_()
+        for _ in range(2):
+            for i in range(QWEN3_8B.layers):
+                kernels.q4k_rmsnorm_swiglu(dec.h, w.norms[f"layers.{i}.post_norm"], w.packed[f"layers.{i}.gate"],
+                                           w.packed[f"layers.{i}.up"], dec.act)
+    else:
+        dec = Qwen3Decoder(w, max_positions=PROMPT_POSITIONS + 64, max_new_tokens=4, device=dev, persistent=True)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1)
+        dec.k_cache[:, :PROMPT_POSITIONS].normal_(generator=gen)
+        dec.v_cache[:, :PROMPT_POSITIONS].normal_(generator=gen)
+        dec.h.normal_()
+        dec.position.fill_(PROMPT_POSITIONS)
+        for _ in range(2):
+            dec.run_decode_layers()
+        dec.check_status()
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     dst.copy_(src)
@@ -88,7 +107,7 @@ def main() -> int:
         print(f"bench.py measures one GPU only (this build is single-GPU); got --gpus {args.gpus}", file=sys.stderr)
         return 2
     if args.profile_kernel:
-        return profile_kernel_target()
+        return profile_kernel_target(args.per_op)
     import torch
 
     from torch2vk_amd import kernels
@@ -181,8 +200,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": profiled_traffic(TRAFFIC_PROFILE) if headline else None,
-            "traffic_source": TRAFFIC_PROFILE.name if headline else None,
+            "traffic": profiled_traffic(TRAFFIC_PROFILES[dom["kernel"]]) if headline else None,
+            "traffic_source": TRAFFIC_PROFILES[dom["kernel"]].name if headline else None,
             "bytes_per_launch": dom["bytes"],
             "avg_launch_us": round(dom["us"], 3),
         },
@@ -275,6 +294,26 @@ def kernel_timing(dec, weights, reps: int) -> dict:
     q_bytes += b
     q_us += us
     dominant = "gate_up_rmsnorm_swiglu_gemv"
+    if dec.persistent:
+        # the launch that runs every layer of a token: each layer's weights and norms, the K/V rows read
+        # and the new row written, the residual stream in and out
+        name = "decode_layers_persistent"
+        us = _graph_us_per_call([dec.run_decode_layers] * 2, reps)
+        b = 0
+        for i in range(L):
+            b += sum(wb(f"layers.{i}.{n}") for n in ("q", "k", "v", "o", "gate", "up", "down"))
+            b += sum(weights.norms[f"layers.{i}.{n}"].numel() * 4 for n in ("input_norm", "post_norm", "q_norm",
+                                                                              "k_norm"))
+        b += L * (2 * kv_len * c.kv_dim * 2 + 2 * c.kv_dim * 2) + 2 * c.hidden * 4
+        per_launch_us[name] = round(us, 3)
+        bytes_per[name] = int(b)
+        gbs[name] = b / (us * 1e-6) / 1e9
+        dominant = name
+        # what a token runs: this launch and the LM head (the per-op classes above are for comparison)
+        lm = "lm_head_rmsnorm_argmax_gemv"
+        total_us = us + per_launch_us[lm]
+        q_bytes = b + bytes_per[lm]
+        q_us = total_us
     return {
         "per_launch_us": per_launch_us,
         "gbs": {k: round(v, 1) for k, v in gbs.items()},
