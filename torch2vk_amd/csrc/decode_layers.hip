@@ -56,7 +56,7 @@ constexpr int DL_ATT_SLOTS = DL_BLOCKS / 8;    // attention blocks per kv head (
 constexpr uint32_t DL_SPIN_LIMIT = 1u << 14;
 // weight units per wave issued before a GEMV phase's input is awaited
 #ifndef DL_PRE_QKV
-#define DL_PRE_QKV 2
+#define DL_PRE_QKV 3
 #endif
 #ifndef DL_PRE_O
 #define DL_PRE_O 2
