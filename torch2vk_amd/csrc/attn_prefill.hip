@@ -44,6 +44,7 @@ constexpr int FA_BM = 32 * FA_WAVES;  // queries per block
 constexpr int FA_BN = 64;             // keys per tile
 constexpr int FA_VROW = FA_BN + 8;    // LDS V^T row length (bf16)
 constexpr float FA_LOG2E = 1.4426950408889634f;
+constexpr float FA_RESCALE = 8.0f;    // log2 headroom of the lazily updated running max
 
 struct FaArgs {
     const uint16_t* q;  // bf16
@@ -193,47 +194,78 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
             }
         }
 
-        // scale to log2 units, mask, tile max of this query
-        float mt = -INFINITY;
+        // Masking is needed only on tiles that cross the end of the keys or, for
+        // a causal pass, the diagonal of some query of this wave (wave-uniform).
+        bool edge = t0 + FA_BN > s_len;
+        if constexpr (CAUSAL) edge = edge || t0 + FA_BN - 1 > q0 + 32 * wave + a.causal_offset;
+        float mt = -INFINITY;  // tile max of this query, log2 units
+        if constexpr (MASK) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int key = t0 + 32 * kb + 8 * (e >> 2) + 4 * half + (e & 3);
-                float x = s[kb][e] * a.scale_log2;
-                if constexpr (MASK) x = fmaf(mrow[min(key, s_len - 1)], FA_LOG2E, x);
-                bool ok = key < s_len;
-                if constexpr (CAUSAL) ok = ok && key <= qi + a.causal_offset;
-                x = ok ? x : -INFINITY;
-                s[kb][e] = x;
-                mt = fmaxf(mt, x);
+                for (int e = 0; e < 16; ++e) {
+                    const int key = t0 + 32 * kb + 8 * (e >> 2) + 4 * half + (e & 3);
+                    float x = fmaf(mrow[min(key, s_len - 1)], FA_LOG2E, s[kb][e] * a.scale_log2);
+                    bool ok = key < s_len;
+                    if constexpr (CAUSAL) ok = ok && key <= qi + a.causal_offset;
+                    x = ok ? x : -INFINITY;
+                    s[kb][e] = x;
+                    mt = fmaxf(mt, x);
+                }
             }
+        } else {
+            // raw scores stay unscaled: the scale (> 0) is applied to the max and
+            // folded into the exponent below
+            if (edge) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int key = t0 + 32 * kb + 8 * (e >> 2) + 4 * half + (e & 3);
+                        bool ok = key < s_len;
+                        if constexpr (CAUSAL) ok = ok && key <= qi + a.causal_offset;
+                        s[kb][e] = ok ? s[kb][e] : -INFINITY;
+                    }
+                }
+            }
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[kb][e]);
+            mt *= a.scale_log2;
         }
         mt = fmaxf(mt, __shfl_xor(mt, 32, T2H_WAVE));
-        const float m_new = fmaxf(m_run, mt);
+        // The running max moves only when the tile's max exceeds it by more than
+        // FA_RESCALE (log2 units): P then stays below 2^FA_RESCALE, and the O
+        // rescale is skipped on the tiles where no lane of the wave needs it.
+        const bool grow = mt > m_run + FA_RESCALE;
+        const float m_new = grow ? mt : m_run;
         const bool none = m_new == -INFINITY;  // nothing visible yet: o and l stay zero
-        const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        const float alpha = grow && m_run != -INFINITY ? __builtin_amdgcn_exp2f(m_run - m_new) : (grow ? 0.0f : 1.0f);
         const float msub = none ? 0.0f : m_new;
         m_run = m_new;
 
         // P = 2^(S - m), packed to bf16 in k-slot order, and its sum
+        const float sc = MASK ? 1.0f : a.scale_log2;
         uint32_t pk[2][8];
         float lsum = 0.0f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
             for (int e = 0; e < 16; e += 2) {
-                const float p0 = __builtin_amdgcn_exp2f(s[kb][e] - msub);
-                const float p1 = __builtin_amdgcn_exp2f(s[kb][e + 1] - msub);
+                const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kb][e], sc, -msub));
+                const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kb][e + 1], sc, -msub));
                 lsum += p0 + p1;
                 pk[kb][e / 2] = pack_bf16x2(p0, p1);
             }
         }
         l_part = fmaf(l_part, alpha, lsum);
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
-        for (int i = 0; i < DB; ++i)
+            for (int i = 0; i < DB; ++i)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+                for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+        }
 
         // O^T += V^T . P^T: k-step (kb, stp) covers the keys of accumulator
         // entries 8 stp .. 8 stp + 7 of block kb:
