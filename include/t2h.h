@@ -138,6 +138,14 @@ int t2h_q8_0_gemm(const void* x, const void* w, void* y, int out_dtype, const fl
  * LLAMA_MATMUL_Q4_K_F32_{M,L} (src/models/optimized_qwen3/shaders/llama_matmul_q4_k_f32.py:32-141); k % 256 == 0. */
 int t2h_q4k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
                  uint32_t k, uint32_t n, void* stream);
+/* y[m, n] = act(x[m, k] . deq(W[n, w_k])^T + bias) (+ residual), W Q8_0 rows of w_k / 32 blocks, w_k <= k,
+ * w_k % 32 == 0, k % 64 == 0 (columns of x past w_k multiply zeros; keep them finite).  bias fp32 [n] or
+ * NULL; act 0 = none, 1 = GELU (exact erf); out fp32 or bf16 (fp32 with residual, which may alias y).
+ * replaces LINEAR_BIAS_Q8_0W_F32B_F32 (src/models/quantized_qwen3_asr/shaders/linear_bias_q8_0w_f32b_f32.py:27-213)
+ * and, after t2h_im2col, CONV2D_Q8_0W_F32B_F16{,_2,_3} (shaders/conv2d_q8_0w_f32b_f16.py:25-136); the GELU that
+ * follows each of them in the audio tower (dispatch/audio_encoder.py:27-63) is fused here. */
+int t2h_q8_0_linear(const void* x, const void* w, const float* bias, int act, void* y, int out_dtype,
+                    const float* residual, uint32_t m, uint32_t k, uint32_t n, uint32_t w_k, void* stream);
 
 /* ---------------------------------------------------- token selection --- */
 /* replaces QWEN3_TOKEN_SELECT_REDUCE_CHUNKS_F32 + QWEN3_TOKEN_SELECT_REDUCE_F32
@@ -224,6 +232,15 @@ int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_layers, uint
 int t2h_flash_attn_prefill(const void* q, const void* k, const void* v, void* out, const float* mask, uint32_t batch,
                            uint32_t nh, uint32_t nk, uint32_t t_len, uint32_t s_len, uint32_t d,
                            const int64_t* strides, int causal, int32_t causal_offset, float scale, void* stream);
+/* Self-attention within segments: token t attends to the keys of its own segment [cu[i], cu[i+1]),
+ * cu_seqlens int32 [n_seg + 1] on the device, ascending, cu[0] = 0, cu[n_seg] = t_len (a token outside
+ * [cu[0], cu[n_seg]) gets zeros).  Same tensors and strides[0..11] as t2h_flash_attn_prefill with
+ * s_len = t_len.  Equals SDPA_MASKED_F32 with the Qwen3-ASR block-diagonal window mask
+ * (src/models/quantized_qwen3_asr/pytorch_modules.py:95-114, shaders/sdpa_masked_f32.py) without reading a
+ * mask: key tiles outside a block's segments are skipped. */
+int t2h_flash_attn_segments(const void* q, const void* k, const void* v, void* out, const int32_t* cu_seqlens,
+                            uint32_t n_seg, uint32_t batch, uint32_t nh, uint32_t nk, uint32_t t_len, uint32_t d,
+                            const int64_t* strides, float scale, void* stream);
 
 /* ------------------------------------------------------ small ops ------ */
 /* replaces EMBEDDING_Q4_K_F32 (src/models/quantized_qwen3/shaders/embedding_q4_k_f32.py:62-121); out fp32 [n_ids, dim] */
@@ -234,6 +251,38 @@ int t2h_rms_norm(const void* x, int x_dtype, const float* w, void* out, int out_
                  float eps, void* stream);
 /* replaces SWIGLU_F16 / SWIGLU_F32 (src/models/optimized_qwen3/shaders/swiglu_f16.py:20-81); out bf16 */
 int t2h_swiglu(const void* gate, const void* up, int in_dtype, void* out, uint64_t n, void* stream);
+
+/* ------------------------------------------- Qwen3-ASR audio tower ----- */
+/* out[(b, oh, ow), (c, fh, fw)] = x[b, c, oh*stride_h + fh - pad_h, ow*stride_w + fw - pad_w] (0 outside),
+ * bf16 rows of out_cols >= channels*kh*kw (the rest zero-filled); x fp32 or bf16 addressed by element strides
+ * (b, c, h, w).  The conv2d front-end's patch gather (CONV2D_Q8_0W_F32B_F16, src/models/quantized_qwen3_asr/
+ * shaders/conv2d_q8_0w_f32b_f16.py:114-136) and, with an (F x 1) kernel, the flatten + transpose before conv_out
+ * (pytorch_modules.py:463-466). */
+int t2h_im2col(const void* x, int x_dtype, const int64_t* x_strides, uint32_t batch, uint32_t channels,
+               uint32_t in_h, uint32_t in_w, uint32_t kh, uint32_t kw, uint32_t stride_h, uint32_t stride_w,
+               uint32_t pad_h, uint32_t pad_w, uint32_t out_h, uint32_t out_w, void* out, uint32_t out_cols,
+               void* stream);
+/* out = (x - mean) / sqrt(var + eps) * w + b per row (biased variance, two passes); x, out fp32 or bf16,
+ * cols % 4 == 0, 16-B aligned.  replaces LAYER_NORM_F32W_F32B_F32
+ * (src/models/quantized_qwen3_asr/shaders/layer_norm_f32w_f32b_f32.py:20-105). */
+int t2h_layer_norm(const void* x, int x_dtype, const float* w, const float* b, void* out, int out_dtype,
+                   uint32_t rows, uint32_t cols, float eps, void* stream);
+/* out = x * (1 + erf(x / sqrt 2)) / 2; n % 4 == 0.  replaces GELU_F32 (src/models/quantized_qwen3_asr/shaders/
+ * gelu_f32.py:22-82) where it is not fused into t2h_q8_0_linear. */
+int t2h_gelu(const void* x, int x_dtype, void* out, int out_dtype, uint64_t n, void* stream);
+/* out[i] = src[idx[i]] for rows of row_bytes (% 4); an index outside [0, src_rows) gives a zero row.
+ * replaces INDEX_SELECT_F32 (src/models/quantized_qwen3_asr/shaders/index_select_f32_c6680f8d95.py). */
+int t2h_index_select_rows(const void* src, uint64_t src_rows, uint32_t row_bytes, const int64_t* idx, uint32_t n,
+                          void* out, void* stream);
+/* dst[idx[i]] = src[i] for rows of row_bytes (% 4); an index outside [0, dst_rows) is skipped.
+ * replaces INDEX_COPY_F32 (src/models/quantized_qwen3_asr/shaders/index_copy_f32_7ba4f1ff13.py; the audio
+ * injection, dispatch/audio_inject.py:11-13). */
+int t2h_index_copy_rows(void* dst, uint64_t dst_rows, uint32_t row_bytes, const int64_t* idx, uint32_t n,
+                        const void* src, void* stream);
+/* out fp32 [n_ids, dim] = deq(W[ids]) for Q8_0 rows of dim / 32 blocks; an id outside [0, vocab) gives zeros.
+ * replaces EMBEDDING_Q8_0_F32 (src/models/quantized_qwen3_asr/shaders/embedding_q8_0_f32.py:25-97). */
+int t2h_embedding_q8_0(const void* w, uint64_t vocab, const int64_t* ids, uint32_t n_ids, uint32_t dim, float* out,
+                       void* stream);
 
 #ifdef __cplusplus
 }

@@ -42,10 +42,12 @@ def dense_weights(packed: dict[str, np.ndarray], types: dict[str, str], norms: d
 
 
 def check_greedy_tokens(shape: Qwen3Shape, dense: dict[str, torch.Tensor], prompt: list[int], gpu_tokens: list[int],
-                        *, tie_tol: float = 5e-3, kv_bf16: bool = True) -> dict:
-    """Teacher-forced replay of ``gpu_tokens`` on the oracle; returns stats, raises AssertionError on mismatch."""
+                        *, tie_tol: float = 5e-3, kv_bf16: bool = True,
+                        prompt_embeds: torch.Tensor | None = None) -> dict:
+    """Teacher-forced replay of ``gpu_tokens`` on the oracle; returns stats, raises AssertionError on mismatch.
+    ``prompt_embeds`` [len(prompt), H] replaces the prompt's embedding lookup (injected audio features)."""
     model = Qwen3CpuModel(shape, dense, max_positions=len(prompt) + len(gpu_tokens) + 1)
-    hidden = model.forward(torch.tensor(prompt), start=0)
+    hidden = model.forward(torch.tensor(prompt), start=0, embeds=prompt_embeds)
     exact = 0
     near = 0
     min_margin = float("inf")

@@ -157,13 +157,15 @@ class Qwen3CpuModel:
         rot = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
         return x * cos + rot * sin
 
-    def forward(self, tokens: torch.Tensor, start: int, layers: int | None = None) -> torch.Tensor:
-        """Run T tokens at positions start..start+T-1, fill the KV cache, return last hidden [H] (post final norm)."""
+    def forward(self, tokens: torch.Tensor, start: int, layers: int | None = None,
+                embeds: torch.Tensor | None = None) -> torch.Tensor:
+        """Run T tokens at positions start..start+T-1, fill the KV cache, return last hidden [H] (post final norm).
+        ``embeds`` [T, H] replaces the embedding lookup (a prompt with injected audio features)."""
         s = self.shape
         w = self.w
-        t_len = tokens.shape[0]
+        t_len = tokens.shape[0] if embeds is None else embeds.shape[0]
         positions = torch.arange(start, start + t_len)
-        h = w["embed"][tokens]
+        h = w["embed"][tokens] if embeds is None else embeds.to(self.dtype)
         group = s.heads // s.kv_heads
         n_layers = s.layers if layers is None else layers
         for i in range(n_layers):

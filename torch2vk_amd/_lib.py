@@ -64,6 +64,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "t2h_embedding_q4_k": (_i32, [_vp, _u64, _vp, _u32, _u32, _vp, _vp]),
     "t2h_rms_norm": (_i32, [_vp, _i32, _vp, _vp, _i32, _u32, _u32, _f32, _vp]),
     "t2h_swiglu": (_i32, [_vp, _vp, _i32, _vp, _u64, _vp]),
+    "t2h_q8_0_linear": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "t2h_flash_attn_segments": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _f32,
+                                       _vp]),
+    "t2h_im2col": (_i32, [_vp, _i32, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                          _vp, _u32, _vp]),
+    "t2h_layer_norm": (_i32, [_vp, _i32, _vp, _vp, _vp, _i32, _u32, _u32, _f32, _vp]),
+    "t2h_gelu": (_i32, [_vp, _i32, _vp, _i32, _u64, _vp]),
+    "t2h_index_select_rows": (_i32, [_vp, _u64, _u32, _vp, _u32, _vp, _vp]),
+    "t2h_index_copy_rows": (_i32, [_vp, _u64, _u32, _vp, _u32, _vp, _vp]),
+    "t2h_embedding_q8_0": (_i32, [_vp, _u64, _vp, _u32, _u32, _vp, _vp]),
 }
 
 

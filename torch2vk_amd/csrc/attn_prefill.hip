@@ -10,8 +10,16 @@
 // head dimension contiguous, so both layouts run through one kernel.
 //
 // Math: out[b,t,h] = softmax(q.k^T * scale + mask) v over the keys a query may
-// see (causal: key <= t + causal_offset), GQA kv head = h / (NH / NK); fp32
-// scores, running max and sum, bf16 P, fp32 output accumulation.
+// see (causal: key <= t + causal_offset; segments: the keys of the query's own
+// segment), GQA kv head = h / (NH / NK); fp32 scores, running max and sum,
+// bf16 P, fp32 output accumulation.
+//
+// Segments.  The Qwen3-ASR encoder attends within windows: its additive mask is
+// 0 on diagonal blocks [cu[i], cu[i+1]) and -FLT_MAX elsewhere
+// (src/models/quantized_qwen3_asr/pytorch_modules.py:95-114).  Given the window
+// bounds cu[] instead of the mask, every query's keys are one interval
+// [lo, hi), a block visits only the key tiles its queries' intervals cover,
+// and only tiles that cross an interval end are masked.
 //
 // Work mapping.  A block of 4 waves takes 128 queries of one (batch, head);
 // wave w owns 32 of them.  Keys stream through LDS 64 at a time, double
@@ -52,6 +60,8 @@ struct FaArgs {
     const uint16_t* v;
     uint16_t* out;
     const float* mask;  // additive, natural-log units; null = none
+    const int32_t* cu;  // segment bounds [n_seg + 1] (SEG kernels)
+    uint32_t n_seg;
     size_t q_sb, q_st, q_sh;
     size_t k_sb, k_st, k_sh;
     size_t v_sb, v_st, v_sh;
@@ -69,7 +79,36 @@ __device__ __forceinline__ fa_bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_
     return __builtin_bit_cast(fa_bf16x8_t, make_uint4(a, b, c, d));
 }
 
-template <int D, bool CAUSAL, bool MASK>
+// Keys [lo, hi) of the segment holding token q: the last i with cu[i] <= q.
+// A token outside [cu[0], cu[n_seg]) sees nothing: an empty range at the
+// nearer end of the table, so that ranges still never shrink as q grows.
+__device__ __forceinline__ int2 fa_segment(const FaArgs& a, int q) {
+    const int n = (int)a.n_seg;
+    if (q < a.cu[0]) return make_int2(a.cu[0], a.cu[0]);
+    if (q >= a.cu[n]) return make_int2(a.cu[n], a.cu[n]);
+    int lo = 0, hi = n;  // cu[lo] <= q < cu[hi]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (a.cu[mid] <= q) lo = mid;
+        else hi = mid;
+    }
+    return make_int2(a.cu[lo], a.cu[lo + 1]);
+}
+
+// Keys [lo, hi) that query q may see, clamped to [0, s_len).
+template <bool CAUSAL, bool SEG>
+__device__ __forceinline__ int2 fa_key_range(const FaArgs& a, int q) {
+    int lo = 0, hi = (int)a.s_len;
+    if constexpr (SEG) {
+        const int2 r = fa_segment(a, q);
+        lo = max(r.x, 0);
+        hi = min(r.y, hi);
+    }
+    if constexpr (CAUSAL) hi = min(hi, q + a.causal_offset + 1);
+    return make_int2(lo, max(lo, hi));
+}
+
+template <int D, bool CAUSAL, bool MASK, bool SEG>
 __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) {
     constexpr int KROW = D + 8;                                // LDS K row length (bf16)
     constexpr int DS = D / 16;                                 // k-steps of S^T
@@ -93,12 +132,17 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
     const int qc = q_valid ? qi : (int)a.t_len - 1;
     const int s_len = (int)a.s_len;
 
-    int s_end = s_len;
-    if constexpr (CAUSAL) {
-        const int q_last = min(q0 + FA_BM, (int)a.t_len) - 1;
-        s_end = min(s_end, q_last + a.causal_offset + 1);
-    }
-    const int n_tiles = s_end > 0 ? (s_end + FA_BN - 1) / FA_BN : 0;
+    // Key ranges only grow with the query index, so the block's queries see
+    // [range(q0).lo, range(q_last).hi) and a wave's need no mask on the keys
+    // between its last query's lo and its first query's hi.
+    const int q_last = min(q0 + FA_BM, (int)a.t_len) - 1;
+    const int2 rq = fa_key_range<CAUSAL, SEG>(a, qc);
+    const int blk_lo = fa_key_range<CAUSAL, SEG>(a, q0).x;
+    const int blk_hi = fa_key_range<CAUSAL, SEG>(a, q_last).y;
+    const int t_first = blk_lo / FA_BN;
+    const int t_end = blk_hi > blk_lo ? (blk_hi + FA_BN - 1) / FA_BN : t_first;
+    const int wave_lo_max = __builtin_amdgcn_readlane(rq.x, 31);
+    const int wave_hi_min = __builtin_amdgcn_readlane(rq.y, 0);
 
     // Q^T columns of this lane's query: dims 16 s + 8 half .. +7
     const uint16_t* qrow = a.q + (size_t)b * a.q_sb + (size_t)qc * a.q_st + (size_t)h * a.q_sh;
@@ -166,8 +210,8 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
     float m_run = -INFINITY;  // log2-domain running max of this lane's query
     float l_part = 0.0f;      // this half-wave's share of the running sum
 
-    if (n_tiles > 0) {
-        load_tile(0);
+    if (t_end > t_first) {
+        load_tile(t_first * FA_BN);
         store_tile(0);
     }
     __syncthreads();
@@ -175,10 +219,10 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
     const float* mrow = nullptr;
     if constexpr (MASK) mrow = a.mask + (size_t)b * a.m_sb + (size_t)qc * a.m_st;
 
-    for (int t = 0; t < n_tiles; ++t) {
-        const int buf = t & 1;
+    for (int t = t_first; t < t_end; ++t) {
+        const int buf = (t - t_first) & 1;
         const int t0 = t * FA_BN;
-        if (t + 1 < n_tiles) load_tile(t0 + FA_BN);
+        if (t + 1 < t_end) load_tile(t0 + FA_BN);
 
         // S^T for two 32-key blocks
         fa_f32x16_t s[2];
@@ -194,10 +238,10 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
             }
         }
 
-        // Masking is needed only on tiles that cross the end of the keys or, for
-        // a causal pass, the diagonal of some query of this wave (wave-uniform).
-        bool edge = t0 + FA_BN > s_len;
-        if constexpr (CAUSAL) edge = edge || t0 + FA_BN - 1 > q0 + 32 * wave + a.causal_offset;
+        // Masking is needed only on tiles that cross an end of some query's key
+        // range in this wave: the end of the keys, a causal diagonal or a
+        // segment bound (wave-uniform).
+        const bool edge = t0 < wave_lo_max || t0 + FA_BN > wave_hi_min;
         float mt = -INFINITY;  // tile max of this query, log2 units
         if constexpr (MASK) {
 #pragma unroll
@@ -206,9 +250,7 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
                 for (int e = 0; e < 16; ++e) {
                     const int key = t0 + 32 * kb + 8 * (e >> 2) + 4 * half + (e & 3);
                     float x = fmaf(mrow[min(key, s_len - 1)], FA_LOG2E, s[kb][e] * a.scale_log2);
-                    bool ok = key < s_len;
-                    if constexpr (CAUSAL) ok = ok && key <= qi + a.causal_offset;
-                    x = ok ? x : -INFINITY;
+                    x = key >= rq.x && key < rq.y ? x : -INFINITY;
                     s[kb][e] = x;
                     mt = fmaxf(mt, x);
                 }
@@ -222,9 +264,7 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
 #pragma unroll
                     for (int e = 0; e < 16; ++e) {
                         const int key = t0 + 32 * kb + 8 * (e >> 2) + 4 * half + (e & 3);
-                        bool ok = key < s_len;
-                        if constexpr (CAUSAL) ok = ok && key <= qi + a.causal_offset;
-                        s[kb][e] = ok ? s[kb][e] : -INFINITY;
+                        s[kb][e] = key >= rq.x && key < rq.y ? s[kb][e] : -INFINITY;
                     }
                 }
             }
@@ -287,7 +327,7 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
             }
         }
         // the other buffer was last read in iteration t - 1, before the barrier that ended it
-        if (t + 1 < n_tiles) store_tile(buf ^ 1);
+        if (t + 1 < t_end) store_tile(buf ^ 1);
         __syncthreads();
     }
 
@@ -309,14 +349,16 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
 }
 
 template <int D>
-static void fa_launch(bool causal, bool mask, dim3 grid, const FaArgs& a, hipStream_t s) {
+static void fa_launch(bool causal, bool mask, bool seg, dim3 grid, const FaArgs& a, hipStream_t s) {
     const dim3 block(FA_THREADS);
-    if (causal) {
-        if (mask) hipLaunchKernelGGL((fa_prefill_kernel<D, true, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((fa_prefill_kernel<D, true, false>), grid, block, 0, s, a);
+    if (seg) {
+        hipLaunchKernelGGL((fa_prefill_kernel<D, false, false, true>), grid, block, 0, s, a);
+    } else if (causal) {
+        if (mask) hipLaunchKernelGGL((fa_prefill_kernel<D, true, true, false>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((fa_prefill_kernel<D, true, false, false>), grid, block, 0, s, a);
     } else {
-        if (mask) hipLaunchKernelGGL((fa_prefill_kernel<D, false, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((fa_prefill_kernel<D, false, false>), grid, block, 0, s, a);
+        if (mask) hipLaunchKernelGGL((fa_prefill_kernel<D, false, true, false>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((fa_prefill_kernel<D, false, false, false>), grid, block, 0, s, a);
     }
 }
 
@@ -324,17 +366,18 @@ static void fa_launch(bool causal, bool mask, dim3 grid, const FaArgs& a, hipStr
 
 using namespace t2h;
 
-extern "C" int t2h_flash_attn_prefill(const void* q, const void* k, const void* v, void* out, const float* mask,
-                                      uint32_t batch, uint32_t nh, uint32_t nk, uint32_t t_len, uint32_t s_len,
-                                      uint32_t d, const int64_t* strides, int causal, int32_t causal_offset,
-                                      float scale, void* stream) {
+static int fa_prefill(const void* q, const void* k, const void* v, void* out, const float* mask,
+                      const int32_t* cu, uint32_t n_seg, uint32_t batch, uint32_t nh, uint32_t nk, uint32_t t_len,
+                      uint32_t s_len, uint32_t d, const int64_t* strides, int causal, int32_t causal_offset,
+                      float scale, void* stream) {
     if (!q || !k || !v || !out || !strides) return T2H_ERR_NULL;
     if (d != 64 && d != 128) return T2H_ERR_UNSUPPORTED;
     if (nh == 0 || nk == 0 || nh % nk != 0) return T2H_ERR_SHAPE;
     if (batch == 0 || t_len == 0) return T2H_OK;
     if (s_len == 0) return T2H_ERR_SHAPE;
     if ((size_t)batch * nh > 65535u || t_len > 0x7fffffffu - FA_BM || s_len > 0x7fffffffu) return T2H_ERR_SHAPE;
-    for (int i = 0; i < 14; ++i)
+    const int n_strides = mask ? 14 : 12;
+    for (int i = 0; i < n_strides; ++i)
         if (strides[i] < 0) return T2H_ERR_ARG;
     // 16-B q/k rows, 8-B v and out rows: pointers and (b, t, h) strides in elements
     const uintptr_t align_bits = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k);
@@ -345,12 +388,14 @@ extern "C" int t2h_flash_attn_prefill(const void* q, const void* k, const void* 
         if (strides[i] % 8 != 0) return T2H_ERR_ALIGN;
     for (int i = 6; i < 12; ++i)
         if (strides[i] % 4 != 0) return T2H_ERR_ALIGN;
-    FaArgs a;
+    FaArgs a = {};
     a.q = reinterpret_cast<const uint16_t*>(q);
     a.k = reinterpret_cast<const uint16_t*>(k);
     a.v = reinterpret_cast<const uint16_t*>(v);
     a.out = reinterpret_cast<uint16_t*>(out);
     a.mask = mask;
+    a.cu = cu;
+    a.n_seg = n_seg;
     a.q_sb = (size_t)strides[0];
     a.q_st = (size_t)strides[1];
     a.q_sh = (size_t)strides[2];
@@ -363,8 +408,10 @@ extern "C" int t2h_flash_attn_prefill(const void* q, const void* k, const void* 
     a.o_sb = (size_t)strides[9];
     a.o_st = (size_t)strides[10];
     a.o_sh = (size_t)strides[11];
-    a.m_sb = (size_t)strides[12];
-    a.m_st = (size_t)strides[13];
+    if (mask) {
+        a.m_sb = (size_t)strides[12];
+        a.m_st = (size_t)strides[13];
+    }
     a.nh = nh;
     a.group = nh / nk;
     a.t_len = t_len;
@@ -374,8 +421,26 @@ extern "C" int t2h_flash_attn_prefill(const void* q, const void* k, const void* 
     a.scale_log2 = sc * FA_LOG2E;
     const dim3 grid((t_len + FA_BM - 1) / FA_BM, batch * nh);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (d == 128) fa_launch<128>(causal != 0, mask != nullptr, grid, a, s);
-    else fa_launch<64>(causal != 0, mask != nullptr, grid, a, s);
+    if (d == 128) fa_launch<128>(causal != 0, mask != nullptr, cu != nullptr, grid, a, s);
+    else fa_launch<64>(causal != 0, mask != nullptr, cu != nullptr, grid, a, s);
     T2H_LAUNCH_CHECK();
     return T2H_OK;
+}
+
+extern "C" int t2h_flash_attn_prefill(const void* q, const void* k, const void* v, void* out, const float* mask,
+                                      uint32_t batch, uint32_t nh, uint32_t nk, uint32_t t_len, uint32_t s_len,
+                                      uint32_t d, const int64_t* strides, int causal, int32_t causal_offset,
+                                      float scale, void* stream) {
+    return fa_prefill(q, k, v, out, mask, nullptr, 0, batch, nh, nk, t_len, s_len, d, strides, causal,
+                      causal_offset, scale, stream);
+}
+
+extern "C" int t2h_flash_attn_segments(const void* q, const void* k, const void* v, void* out,
+                                       const int32_t* cu_seqlens, uint32_t n_seg, uint32_t batch, uint32_t nh,
+                                       uint32_t nk, uint32_t t_len, uint32_t d, const int64_t* strides, float scale,
+                                       void* stream) {
+    if (!cu_seqlens) return T2H_ERR_NULL;
+    if (n_seg == 0 || n_seg > 0x7fffffffu) return T2H_ERR_SHAPE;
+    return fa_prefill(q, k, v, out, nullptr, cu_seqlens, n_seg, batch, nh, nk, t_len, t_len, d, strides, 0, 0,
+                      scale, stream);
 }

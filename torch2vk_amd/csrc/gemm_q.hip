@@ -31,7 +31,6 @@
 namespace t2h {
 
 constexpr int GQ_THREADS = 512;
-constexpr int GQ_BM = 256;
 constexpr int GQ_BN = 256;
 constexpr int GQ_BK = 64;
 constexpr int GQ_LDS_ROW = GQ_BK + 8;  // bf16 elements per padded LDS row
@@ -39,15 +38,24 @@ constexpr int GQ_GROUP_M = 8;
 
 enum GemmEpilogue { GQEPI_F32 = 0, GQEPI_BF16 = 1, GQEPI_RESID = 2 };
 
+enum GemmAct { GQACT_NONE = 0, GQACT_GELU = 1 };
+
 struct GemmArgs {
     const uint16_t* a;     // bf16 [M, K]
     const uint8_t* w;      // packed rows [N, row_bytes]
     void* c;               // [M, N] fp32 or bf16
     const float* residual; // GQEPI_RESID: fp32 [M, N] (may alias c)
+    const float* bias;     // fp32 [N] or null
+    int act;               // GemmAct, applied after the bias and before the residual
     uint32_t m, n, k;
     uint32_t row_bytes;
+    uint32_t w_blocks;     // quant blocks per weight row; K columns past them multiply zeros
     uint32_t tiles_m, tiles_n;
 };
+
+// GELU with the exact erf (the reference's GELU_F32 evaluates erf by
+// Abramowitz-Stegun 7.1.26, |error| < 1.5e-7: src/models/quantized_qwen3_asr/shaders/gelu_f32.py:61-76)
+__device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -66,8 +74,12 @@ struct GemmQ80 {
         const uint32_t t = threadIdx.x;
         uint32_t row = n0 + (t >> 1);
         row = row < a.n ? row : a.n - 1;
-        const uint8_t* p = a.w + (size_t)row * a.row_bytes + (size_t)(k0 / 32 + (t & 1)) * 34;
-        r.d = load_u16(p);
+        // a stage past the row's last block (K padded to the 64-wide stage) reads
+        // the last block again with a zero scale
+        const uint32_t blk = k0 / 32 + (t & 1);
+        const bool inside = blk < a.w_blocks;
+        const uint8_t* p = a.w + (size_t)row * a.row_bytes + (size_t)(inside ? blk : a.w_blocks - 1) * 34;
+        r.d = inside ? load_u16(p) : 0u;
         r.q0 = load_u4_ua(p + 2);
         r.q1 = load_u4_ua(p + 18);
     }
@@ -164,8 +176,12 @@ __device__ __forceinline__ void store_w(const typename F::Raw& r, uint16_t* lds_
 
 // ---------------------------------------------------------------- kernel --
 
-template <class F, int EPI>
+// MI = 32-row MFMA tiles per wave down M: 4 gives 256 x 256 block tiles, 2
+// gives 128 x 256 for problems with too few 256-row tiles to fill the chip.
+template <class F, int EPI, int MI>
 __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
+    constexpr int GQ_BM = 64 * MI;
+    constexpr int ACH = GQ_BM * GQ_BK / 8 / GQ_THREADS;  // 16-B A chunks per thread
     __shared__ __align__(16) uint16_t lds_a[2][GQ_BM * GQ_LDS_ROW];
     __shared__ __align__(16) uint16_t lds_b[2][GQ_BN * GQ_LDS_ROW];
 
@@ -183,17 +199,17 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
     const uint32_t t = threadIdx.x;
     const int lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int wm = wave >> 2;  // 0..1: rows wm*128
-    const int wn = wave & 3;   // 0..3: cols wn*64
+    const int wm = wave >> 2;  // 0..1: rows wm * 32 MI
+    const int wn = wave & 3;   // 0..3: cols wn * 64
 
-    // A stage load: 256 rows x 64 bf16 = 2048 chunks of 16 B, 4 per thread
+    // A stage load: GQ_BM rows x 64 bf16 in 16-B chunks, ACH per thread
     const uint32_t KT = a.k / GQ_BK;
-    uint4 ra[4];
+    uint4 ra[ACH];
     typename F::Raw rw;
     auto load_stage = [&](uint32_t kt) {
         const uint32_t k0 = kt * GQ_BK;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < ACH; ++i) {
             const uint32_t c = t + GQ_THREADS * i;
             uint32_t row = m0 + (c >> 3);
             row = row < a.m ? row : a.m - 1;
@@ -203,16 +219,16 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
     };
     auto store_stage = [&](uint32_t kt, int s) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < ACH; ++i) {
             const uint32_t c = t + GQ_THREADS * i;
             *reinterpret_cast<uint4*>(&lds_a[s][(c >> 3) * GQ_LDS_ROW + (c & 7) * 8]) = ra[i];
         }
         store_w<F>(rw, lds_b[s], kt * GQ_BK);
     };
 
-    f32x16_t acc[4][2];
+    f32x16_t acc[MI][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -227,19 +243,19 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
     for (uint32_t kt = 0; kt < KT; ++kt) {
         const int s = kt & 1;
         if (kt + 1 < KT) load_stage(kt + 1);
-        const uint16_t* sa = lds_a[s] + (wm * 128 + frag_row) * GQ_LDS_ROW + frag_k;
+        const uint16_t* sa = lds_a[s] + (wm * 32 * MI + frag_row) * GQ_LDS_ROW + frag_k;
         const uint16_t* sb = lds_b[s] + (wn * 64 + frag_row) * GQ_LDS_ROW + frag_k;
 #pragma unroll
         for (int kk = 0; kk < GQ_BK; kk += 16) {
-            bf16x8_t fa[4], fb[2];
+            bf16x8_t fa[MI], fb[2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
                 fa[i] = *reinterpret_cast<const bf16x8_t*>(sa + i * 32 * GQ_LDS_ROW + kk);
 #pragma unroll
             for (int j = 0; j < 2; ++j)
                 fb[j] = *reinterpret_cast<const bf16x8_t*>(sb + j * 32 * GQ_LDS_ROW + kk);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
@@ -250,18 +266,20 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
 
     // epilogue: lane holds column (lane % 32) of each 32x32 tile, rows 8(e/4) + 4(lane/32) + e%4
     const uint32_t col_base = n0 + wn * 64 + (lane & 31);
-    const uint32_t row_base = m0 + wm * 128 + (lane >> 5) * 4;
+    const uint32_t row_base = m0 + wm * 32 * MI + (lane >> 5) * 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t col = col_base + j * 32;
+        const float bj = a.bias != nullptr && col < a.n ? a.bias[col] : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t col = col_base + j * 32;
+        for (int i = 0; i < MI; ++i) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const uint32_t row = row_base + i * 32 + (e >> 2) * 8 + (e & 3);
                 if (row < a.m && col < a.n) {
                     const size_t idx = (size_t)row * a.n + col;
-                    const float v = acc[i][j][e];
+                    float v = acc[i][j][e] + bj;
+                    if (a.act == GQACT_GELU) v = gelu_erf(v);
                     if constexpr (EPI == GQEPI_F32) {
                         reinterpret_cast<float*>(a.c)[idx] = v;
                     } else if constexpr (EPI == GQEPI_BF16) {
@@ -275,11 +293,31 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
     }
 }
 
+template <class F, int EPI>
+static void gemm_q_dispatch(GemmArgs a, hipStream_t s) {
+    const dim3 block(GQ_THREADS);
+    a.tiles_n = (a.n + GQ_BN - 1) / GQ_BN;
+    // 256-row tiles unless that leaves most of the 256 CUs idle
+    const uint32_t tiles_256 = (a.m + 255) / 256 * a.tiles_n;
+    if (tiles_256 < 256 && a.m > 128) {
+        a.tiles_m = (a.m + 127) / 128;
+        hipLaunchKernelGGL((gemm_q_kernel<F, EPI, 2>), dim3(a.tiles_m * a.tiles_n), block, 0, s, a);
+    } else {
+        a.tiles_m = (a.m + 255) / 256;
+        hipLaunchKernelGGL((gemm_q_kernel<F, EPI, 4>), dim3(a.tiles_m * a.tiles_n), block, 0, s, a);
+    }
+}
+
+// k: the A row length (% 64); w_k: the weight rows' quantized length (<= k,
+// whole blocks); columns of A past w_k multiply zeros.
 template <class F>
-static int gemm_q_launch(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
-                         uint32_t k, uint32_t n, void* stream) {
+static int gemm_q_launch(const void* x, const void* w, const float* bias, int act, void* y, int out_dtype,
+                         const float* residual, uint32_t m, uint32_t k, uint32_t n, uint32_t w_k, void* stream) {
     if (!x || !w || !y) return T2H_ERR_NULL;
-    if (k == 0 || k % GQ_BK != 0 || k % F::BLOCK_VALUES != 0) return T2H_ERR_SHAPE;
+    if (k == 0 || k % GQ_BK != 0) return T2H_ERR_SHAPE;
+    if (w_k == 0 || w_k > k || w_k % F::BLOCK_VALUES != 0) return T2H_ERR_SHAPE;
+    if (F::BLOCK_VALUES == 256 && w_k != k) return T2H_ERR_SHAPE;
+    if (act != GQACT_NONE && act != GQACT_GELU) return T2H_ERR_ARG;
     if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) return T2H_ERR_ALIGN;
     if (F::BLOCK_VALUES == 256 && (reinterpret_cast<uintptr_t>(w) & 15) != 0) return T2H_ERR_ALIGN;
     int epi;
@@ -294,25 +332,24 @@ static int gemm_q_launch(const void* x, const void* w, void* y, int out_dtype, c
         return T2H_ERR_DTYPE;
     }
     if (m == 0 || n == 0) return T2H_OK;
+    if ((uint64_t)(m / 128 + 1) * (n / GQ_BN + 1) > 0x7fffffffu) return T2H_ERR_SHAPE;
     GemmArgs a = {};
     a.a = reinterpret_cast<const uint16_t*>(x);
     a.w = reinterpret_cast<const uint8_t*>(w);
     a.c = y;
     a.residual = residual;
+    a.bias = bias;
+    a.act = act;
     a.m = m;
     a.n = n;
     a.k = k;
-    a.row_bytes = k / F::BLOCK_VALUES * F::BLOCK_BYTES;
-    a.tiles_m = (m + GQ_BM - 1) / GQ_BM;
-    a.tiles_n = (n + GQ_BN - 1) / GQ_BN;
-    const size_t tiles = (size_t)a.tiles_m * a.tiles_n;
-    if (tiles > 0x7fffffffu) return T2H_ERR_SHAPE;
-    const dim3 grid((uint32_t)tiles), block(GQ_THREADS);
+    a.w_blocks = w_k / F::BLOCK_VALUES;
+    a.row_bytes = a.w_blocks * F::BLOCK_BYTES;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     switch (epi) {
-        case GQEPI_F32: hipLaunchKernelGGL((gemm_q_kernel<F, GQEPI_F32>), grid, block, 0, s, a); break;
-        case GQEPI_BF16: hipLaunchKernelGGL((gemm_q_kernel<F, GQEPI_BF16>), grid, block, 0, s, a); break;
-        default: hipLaunchKernelGGL((gemm_q_kernel<F, GQEPI_RESID>), grid, block, 0, s, a); break;
+        case GQEPI_F32: gemm_q_dispatch<F, GQEPI_F32>(a, s); break;
+        case GQEPI_BF16: gemm_q_dispatch<F, GQEPI_BF16>(a, s); break;
+        default: gemm_q_dispatch<F, GQEPI_RESID>(a, s); break;
     }
     T2H_LAUNCH_CHECK();
     return T2H_OK;
@@ -324,10 +361,16 @@ using namespace t2h;
 
 extern "C" int t2h_q8_0_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
                              uint32_t k, uint32_t n, void* stream) {
-    return gemm_q_launch<GemmQ80>(x, w, y, out_dtype, residual, m, k, n, stream);
+    return gemm_q_launch<GemmQ80>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
 }
 
 extern "C" int t2h_q4k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
                             uint32_t k, uint32_t n, void* stream) {
-    return gemm_q_launch<GemmQ4K>(x, w, y, out_dtype, residual, m, k, n, stream);
+    return gemm_q_launch<GemmQ4K>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
+}
+
+extern "C" int t2h_q8_0_linear(const void* x, const void* w, const float* bias, int act, void* y, int out_dtype,
+                               const float* residual, uint32_t m, uint32_t k, uint32_t n, uint32_t w_k,
+                               void* stream) {
+    return gemm_q_launch<GemmQ80>(x, w, bias, act, y, out_dtype, residual, m, k, n, w_k, stream);
 }

@@ -290,6 +290,49 @@ def gemm(x: torch.Tensor, w: torch.Tensor, wtype: str, *, out: torch.Tensor | No
     return out
 
 
+ACTS = {None: 0, "none": 0, "gelu": 1}
+
+
+def q8_0_linear(x: torch.Tensor, w: torch.Tensor, *, bias: torch.Tensor | None = None, act: str | None = None,
+                out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                residual: torch.Tensor | None = None) -> torch.Tensor:
+    """y[M, N] = act(x[M, K] . deq(W)^T + bias) (+ residual) on the matrix cores (LINEAR_BIAS_Q8_0W_F32B_F32).
+    x bf16 with K % 64 == 0; W Q8_0 rows of w_k = 32 * blocks <= K values (x's columns past w_k must be
+    finite: they multiply zeros); bias fp32 [N]; act None or "gelu" (exact erf)."""
+    _check(x, "x", torch.bfloat16)
+    _check(w, "weight", torch.uint8, align=1)
+    k = int(x.shape[-1])
+    if k % 64:
+        raise ValueError(f"q8_0_linear needs K % 64 == 0 (pad the rows with zeros), got {k}")
+    if w.dim() != 2 or w.shape[1] % Q8_0_BYTES or w.shape[1] == 0:
+        raise ValueError(f"weight must be uint8 [N, 34 * blocks], got {tuple(w.shape)}")
+    w_k = int(w.shape[1]) // Q8_0_BYTES * 32
+    if w_k > k:
+        raise ValueError(f"weight rows hold {w_k} values, more than x's {k} columns")
+    if w.data_ptr() % 2:
+        raise ValueError("weight must be 2-byte aligned")
+    if act not in ACTS:
+        raise ValueError(f"act must be one of {sorted(a for a in ACTS if a)} or None, got {act!r}")
+    m = x.numel() // k
+    n = int(w.shape[0])
+    if bias is not None:
+        _check(bias, "bias", torch.float32, align=4)
+        if bias.numel() != n:
+            raise ValueError(f"bias must have {n} elements, got {bias.numel()}")
+    if out is None:
+        out = torch.empty(*x.shape[:-1], n, dtype=out_dtype, device=x.device)
+    _check(out, "output", tuple(_OUT_DTYPES), align=4)
+    if out.numel() != m * n:
+        raise ValueError(f"output has {out.numel()} elements, expected {m * n}")
+    if residual is not None:
+        _check(residual, "residual", torch.float32, align=4)
+        if residual.numel() != m * n or out.dtype != torch.float32:
+            raise ValueError("residual must be fp32 with the output's shape; output must be fp32")
+    call("t2h_q8_0_linear", ptr(x), ptr(w), ptr(bias), ACTS[act], ptr(out), _OUT_DTYPES[out.dtype], ptr(residual),
+         m, k, n, w_k, stream_handle())
+    return out
+
+
 def set_gemv_max_blocks(max_blocks: int, max_blocks_norm: int = 0) -> None:
     """Grid caps (blocks of 8 waves) for plain and RMSNorm-prologue Q4_K GEMV launches."""
     call("t2h_set_gemv_max_blocks", int(max_blocks), int(max_blocks_norm))
@@ -484,6 +527,45 @@ def flash_attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: t
     return out
 
 
+def segment_bounds(cu_seqlens, t_len: int, device) -> torch.Tensor:
+    """Validated int32 segment bounds on the device: ascending, cu[0] == 0, cu[-1] == t_len.  A device tensor
+    is taken as it is (the kernel clamps every key range, so a bad table gives wrong windows, never a fault)."""
+    if isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.device.type == "cuda":
+        _check(cu_seqlens, "cu_seqlens", torch.int32, align=4)
+        return cu_seqlens
+    cu = torch.as_tensor(cu_seqlens, dtype=torch.int64).reshape(-1)
+    if cu.numel() < 2 or int(cu[0]) != 0 or int(cu[-1]) != t_len or bool((cu[1:] < cu[:-1]).any()):
+        raise ValueError(f"cu_seqlens must ascend from 0 to {t_len}, got {cu.tolist()[:8]}...")
+    return cu.to(device=device, dtype=torch.int32)
+
+
+def flash_attn_segments(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens, out: torch.Tensor | None = None,
+                        *, scale: float | None = None) -> torch.Tensor:
+    """Self-attention within segments: token t attends to the tokens of its own segment [cu[i], cu[i+1]).
+    q/out [B, T, NH, D], k/v [B, T, NK, D] bf16 with D contiguous (any other strides).  Equals SDPA_MASKED_F32
+    under the block-diagonal window mask of the Qwen3-ASR encoder, without the mask."""
+    for t, name in ((q, "q"), (k, "k"), (v, "v")):
+        _check_strided(t, name, torch.bfloat16)
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be rank 4 [B, T, H, D], got {tuple(t.shape)}")
+    b, t_len, nh, d = q.shape
+    nk = k.shape[2]
+    if k.shape[0] != b or k.shape[1] != t_len or v.shape != k.shape or k.shape[3] != d:
+        raise ValueError(f"shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    cu = segment_bounds(cu_seqlens, t_len, q.device)
+    if out is None:
+        out = torch.empty(b, t_len, nh, d, dtype=torch.bfloat16, device=q.device)
+    _check_strided(out, "output", torch.bfloat16)
+    if tuple(out.shape) != (b, t_len, nh, d):
+        raise ValueError(f"output must be {(b, t_len, nh, d)}, got {tuple(out.shape)}")
+    strides = (_lib.ctypes.c_int64 * 12)(q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1),
+                                         k.stride(2), v.stride(0), v.stride(1), v.stride(2), out.stride(0),
+                                         out.stride(1), out.stride(2))
+    call("t2h_flash_attn_segments", ptr(q), ptr(k), ptr(v), ptr(out), ptr(cu), cu.numel() - 1, b, nh, nk, t_len, d,
+         strides, float(scale or 0.0), stream_handle())
+    return out
+
+
 # -------------------------------------------------------------- small ops --
 
 
@@ -523,4 +605,129 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None
         out = torch.empty(gate.shape, dtype=torch.bfloat16, device=gate.device)
     _check(out, "output", torch.bfloat16, align=2)
     call("t2h_swiglu", ptr(gate), ptr(up), _OUT_DTYPES[gate.dtype], ptr(out), gate.numel(), stream_handle())
+    return out
+
+
+# ------------------------------------------------- Qwen3-ASR audio tower --
+
+_IN_DTYPES = {torch.float32: T2H_DTYPE_F32, torch.bfloat16: T2H_DTYPE_BF16}
+
+
+def conv_out_size(size: int, kernel: int, stride: int, pad: int) -> int:
+    return (size + 2 * pad - kernel) // stride + 1
+
+
+def im2col(x: torch.Tensor, kernel: tuple[int, int], stride: tuple[int, int] = (1, 1),
+           padding: tuple[int, int] = (0, 0), *, out_cols: int | None = None,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """Patch rows of a conv2d: x [B, C, H, W] fp32 or bf16 with any strides (a channels-last buffer is passed
+    as its permuted view) -> bf16 [B * Ho * Wo, out_cols], column (c, fh, fw) as in F.unfold; the columns past
+    C * kh * kw are zero (out_cols defaults to that count rounded up to 64, the GEMM's K step)."""
+    if not isinstance(x, torch.Tensor) or x.device.type != "cuda":
+        raise ValueError("x must be a tensor on a HIP device")
+    if x.dtype not in _IN_DTYPES:
+        raise TypeError(f"x dtype {x.dtype} not in {tuple(_IN_DTYPES)}")
+    if x.dim() != 4:
+        raise ValueError(f"x must be [B, C, H, W], got {tuple(x.shape)}")
+    b, c, h, w_ = (int(d) for d in x.shape)
+    kh, kw = kernel
+    sh, sw = stride
+    ph, pw = padding
+    ho, wo = conv_out_size(h, kh, sh, ph), conv_out_size(w_, kw, sw, pw)
+    if ho <= 0 or wo <= 0:
+        raise ValueError(f"kernel {kernel} does not fit input {(h, w_)} with padding {padding}")
+    cols = c * kh * kw
+    if out_cols is None:
+        out_cols = -(-cols // 64) * 64
+    if out_cols < cols:
+        raise ValueError(f"out_cols {out_cols} < C * kh * kw = {cols}")
+    rows = b * ho * wo
+    if out is None:
+        out = torch.empty(rows, out_cols, dtype=torch.bfloat16, device=x.device)
+    _check(out, "output", torch.bfloat16, align=2)
+    if tuple(out.shape) != (rows, out_cols):
+        raise ValueError(f"output must be {(rows, out_cols)}, got {tuple(out.shape)}")
+    strides = (_lib.ctypes.c_int64 * 4)(*(int(st) for st in x.stride()))
+    call("t2h_im2col", ptr(x), _IN_DTYPES[x.dtype], strides, b, c, h, w_, kh, kw, sh, sw, ph, pw, ho, wo, ptr(out),
+         out_cols, stream_handle())
+    return out
+
+
+def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out: torch.Tensor | None = None, *,
+               out_dtype: torch.dtype = torch.bfloat16, eps: float = 1e-5) -> torch.Tensor:
+    """LayerNorm over the last dimension (LAYER_NORM_F32W_F32B_F32); x fp32 or bf16, out fp32 or bf16."""
+    _check(x, "x", tuple(_IN_DTYPES))
+    cols = int(x.shape[-1])
+    for t, name in ((weight, "weight"), (bias, "bias")):
+        _check(t, name, torch.float32)
+        if t.numel() != cols:
+            raise ValueError(f"{name} must have {cols} elements")
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    _check(out, "output", tuple(_IN_DTYPES))
+    if out.numel() != x.numel():
+        raise ValueError("output must have x's shape")
+    call("t2h_layer_norm", ptr(x), _IN_DTYPES[x.dtype], ptr(weight), ptr(bias), ptr(out), _IN_DTYPES[out.dtype],
+         x.numel() // cols, cols, float(eps), stream_handle())
+    return out
+
+
+def gelu(x: torch.Tensor, out: torch.Tensor | None = None, *, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """x * (1 + erf(x / sqrt 2)) / 2 (GELU_F32); x, out fp32 or bf16, numel % 4 == 0."""
+    _check(x, "x", tuple(_IN_DTYPES), align=8)
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=x.device)
+    _check(out, "output", tuple(_IN_DTYPES), align=8)
+    if out.numel() != x.numel():
+        raise ValueError("output must have x's shape")
+    if x.numel() % 4:
+        raise ValueError("gelu needs numel % 4 == 0")
+    call("t2h_gelu", ptr(x), _IN_DTYPES[x.dtype], ptr(out), _IN_DTYPES[out.dtype], x.numel(), stream_handle())
+    return out
+
+
+def _row_bytes_of(t: torch.Tensor) -> int:
+    rb = t[0].numel() * t.element_size() if t.shape[0] else 0
+    if rb % 4:
+        raise ValueError("rows must be a multiple of 4 bytes")
+    return rb
+
+
+def index_select_rows(src: torch.Tensor, idx: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[i] = src[idx[i]] along dim 0 (INDEX_SELECT_F32); an index out of range gives a zero row."""
+    _check(src, "src", (torch.float32, torch.bfloat16, torch.int32), align=4)
+    _check(idx, "index", torch.int64, align=8)
+    if out is None:
+        out = torch.empty(idx.numel(), *src.shape[1:], dtype=src.dtype, device=src.device)
+    _check(out, "output", src.dtype, align=4)
+    if out.shape[0] != idx.numel() or out.shape[1:] != src.shape[1:]:
+        raise ValueError("output must be [len(index), *src.shape[1:]]")
+    call("t2h_index_select_rows", ptr(src), int(src.shape[0]), _row_bytes_of(src), ptr(idx), idx.numel(), ptr(out),
+         stream_handle())
+    return out
+
+
+def index_copy_rows(dst: torch.Tensor, idx: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
+    """dst[idx[i]] = src[i] along dim 0, in place (INDEX_COPY_F32, the audio injection); an index out of range
+    is skipped."""
+    _check(dst, "dst", (torch.float32, torch.bfloat16, torch.int32), align=4)
+    _check(src, "src", dst.dtype, align=4)
+    _check(idx, "index", torch.int64, align=8)
+    if src.shape[0] != idx.numel() or src.shape[1:] != dst.shape[1:]:
+        raise ValueError("src must be [len(index), *dst.shape[1:]]")
+    call("t2h_index_copy_rows", ptr(dst), int(dst.shape[0]), _row_bytes_of(dst), ptr(idx), idx.numel(), ptr(src),
+         stream_handle())
+    return dst
+
+
+def embedding_q8_0(w: torch.Tensor, ids: torch.Tensor, dim: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 rows of a Q8_0 embedding table (EMBEDDING_Q8_0_F32); an id out of range gives zeros."""
+    _check(w, "weight", torch.uint8, align=2)
+    _check(ids, "indices", torch.int64, align=8)
+    if dim % 32 or w.dim() != 2 or w.shape[1] != dim // 32 * Q8_0_BYTES:
+        raise ValueError("embedding weight width does not match dim")
+    if out is None:
+        out = torch.empty(ids.numel(), dim, dtype=torch.float32, device=w.device)
+    _check(out, "output", torch.float32)
+    call("t2h_embedding_q8_0", ptr(w), int(w.shape[0]), ptr(ids), ids.numel(), dim, ptr(out), stream_handle())
     return out

@@ -65,14 +65,17 @@ def gguf_type(shape: tuple[int, ...], *, force_q6: bool = False, force_q8: bool 
 
 
 def tensor_types(config: Qwen3Config, policy: str) -> dict[str, str]:
-    """GGUF type of every 2-D weight under ``policy`` ("uniform" int4 or "q4_k_m")."""
-    if policy not in ("uniform", "q4_k_m"):
+    """GGUF type of every 2-D weight under ``policy``: "uniform" int4, "q4_k_m", or "qwen3_asr" (Q4_K_M with
+    the token embedding forced to Q8_0, the Qwen3-ASR thinker's rule: src/models/quantized_qwen3_asr/
+    quantization.py:8,24-32)."""
+    if policy not in ("uniform", "q4_k_m", "qwen3_asr"):
         raise ValueError(f"unknown policy {policy!r}")
-    more_bits = set(q4_k_m_more_bits_layer_indices(config.layers)) if policy == "q4_k_m" else set()
+    km = policy in ("q4_k_m", "qwen3_asr")
+    more_bits = set(q4_k_m_more_bits_layer_indices(config.layers)) if km else set()
     c = config
     types = {
-        "embed": gguf_type((c.vocab, c.hidden)),
-        "lm_head": gguf_type((c.vocab, c.hidden), force_q6=policy == "q4_k_m"),
+        "embed": gguf_type((c.vocab, c.hidden), force_q8=policy == "qwen3_asr"),
+        "lm_head": gguf_type((c.vocab, c.hidden), force_q6=km),
     }
     for i in range(c.layers):
         p = f"layers.{i}."

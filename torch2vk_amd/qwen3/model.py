@@ -42,7 +42,7 @@ LM_HEAD_PARTIALS = 512
 def _check_types(c: Qwen3Config, types: dict[str, str]) -> None:
     """The decode path runs Q4_K everywhere and Q6_K where the Q4_K_M policy puts it (v, down,
     lm_head); anything else has no decode kernel here and is refused up front."""
-    allowed = {"embed": ("q4_k",), "lm_head": ("q4_k", "q6_k")}
+    allowed = {"embed": ("q4_k", "q8_0"), "lm_head": ("q4_k", "q6_k")}
     for i in range(c.layers):
         for n in ("q", "k", "gate", "up"):
             allowed[f"layers.{i}.{n}"] = ("q4_k",)
@@ -142,8 +142,13 @@ class Qwen3Decoder:
     # ------------------------------------------- reference op surface --
 
     def run_decode_embed(self) -> None:
-        """Token -> fp32 residual stream (run_decode_embed, EMBEDDING_Q4_K_F32)."""
-        kernels.embedding_q4_k(self._w("embed"), self.next_token.view(-1), self.config.hidden, out=self.h.view(1, -1))
+        """Token -> fp32 residual stream (run_decode_embed, EMBEDDING_Q4_K_F32 / EMBEDDING_Q8_0_F32)."""
+        self.embed_tokens(self.next_token.view(-1), out=self.h.view(1, -1))
+
+    def embed_tokens(self, ids: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """fp32 [len(ids), hidden] rows of the token embedding (run_embed_tokens)."""
+        fn = kernels.embedding_q8_0 if self.types["embed"] == "q8_0" else kernels.embedding_q4_k
+        return fn(self._w("embed"), ids, self.config.hidden, out=out)
 
     def run_decode_layer(self, layer_idx: int, *, cache_position: int | None = None) -> None:
         """One decoder layer at the device-resident position
@@ -285,14 +290,46 @@ class Qwen3Decoder:
                 self.position.add_(1)
         self.run_token_store(advance=True)
 
-    def generate(self, prompt_ids: torch.Tensor, max_new_tokens: int, *, steps_per_graph: int = 8,
-                 use_graph: bool = True) -> list[int]:
+    def prefill_embeds(self, embeds: torch.Tensor, start: int = 0) -> None:
+        """Feed a prompt given as fp32 input embeddings [T, hidden] -- a Qwen3-ASR prompt after the audio
+        features were injected (run_audio_inject) -- one position at a time; the last position's step selects
+        and stores the first generated token."""
+        c = self.config
+        e = embeds.reshape(-1, c.hidden)
+        if e.dtype != torch.float32 or e.device != self.device:
+            raise ValueError("embeds must be fp32 on the decoder's device")
+        if e.shape[0] == 0:
+            raise ValueError("empty prompt")
+        self.reset(position=start)
+        for i in range(e.shape[0]):
+            self.h.copy_(e[i])
+            self.run_decode_layers()
+            if i + 1 < e.shape[0]:
+                self.position.add_(1)
+        self.run_lm_head_select()
+        self.run_token_store(advance=True)
+
+    def _check_budget(self, prompt_len: int, max_new_tokens: int) -> None:
         if max_new_tokens > self.generated.numel():
             raise ValueError("max_new_tokens exceeds the decoder's generated-token buffer")
-        if prompt_ids.numel() + max_new_tokens > self.max_positions:
+        if prompt_len + max_new_tokens > self.max_positions:
             raise ValueError("prompt + new tokens exceed the KV cache capacity")
-        self.prefill(prompt_ids)
+
+    def _finish(self, max_new_tokens: int, steps_per_graph: int, use_graph: bool) -> list[int]:
         self.run_steps(max_new_tokens - 1, steps_per_graph=steps_per_graph, use_graph=use_graph)
         n = int(self.length.item())
         self.check_status()
         return self.generated[:n].tolist()
+
+    def generate(self, prompt_ids: torch.Tensor, max_new_tokens: int, *, steps_per_graph: int = 8,
+                 use_graph: bool = True) -> list[int]:
+        self._check_budget(prompt_ids.numel(), max_new_tokens)
+        self.prefill(prompt_ids)
+        return self._finish(max_new_tokens, steps_per_graph, use_graph)
+
+    def generate_from_embeds(self, embeds: torch.Tensor, max_new_tokens: int, *, steps_per_graph: int = 8,
+                             use_graph: bool = True) -> list[int]:
+        """Greedy decode after a prompt of input embeddings (the Qwen3-ASR transcription loop)."""
+        self._check_budget(embeds.reshape(-1, self.config.hidden).shape[0], max_new_tokens)
+        self.prefill_embeds(embeds)
+        return self._finish(max_new_tokens, steps_per_graph, use_graph)
