@@ -138,6 +138,10 @@ int t2h_q8_0_gemm(const void* x, const void* w, void* y, int out_dtype, const fl
  * LLAMA_MATMUL_Q4_K_F32_{M,L} (src/models/optimized_qwen3/shaders/llama_matmul_q4_k_f32.py:32-141); k % 256 == 0. */
 int t2h_q4k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
                  uint32_t k, uint32_t n, void* stream);
+/* replaces LLAMA_MATMUL_Q6_K_F32_{M,L} (src/models/optimized_qwen3/shaders/llama_matmul_q6_k_f32.py:27-141):
+ * the Q6_K v/down weights of the Q4_K_M more-bits layers; k % 256 == 0, W 2-byte aligned. */
+int t2h_q6k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                 uint32_t k, uint32_t n, void* stream);
 /* y[m, n] = act(x[m, k] . deq(W[n, w_k])^T + bias) (+ residual), W Q8_0 rows of w_k / 32 blocks, w_k <= k,
  * w_k % 32 == 0, k % 64 == 0 (columns of x past w_k multiply zeros; keep them finite).  bias fp32 [n] or
  * NULL; act 0 = none, 1 = GELU (exact erf); out fp32 or bf16 (fp32 with residual, which may alias y).
@@ -238,6 +242,16 @@ int t2h_flash_attn_prefill(const void* q, const void* k, const void* v, void* ou
  * s_len = t_len.  Equals SDPA_MASKED_F32 with the Qwen3-ASR block-diagonal window mask
  * (src/models/quantized_qwen3_asr/pytorch_modules.py:95-114, shaders/sdpa_masked_f32.py) without reading a
  * mask: key tiles outside a block's segments are skipped. */
+/* Prefill chunk prologue: for tokens t < n at positions start + t, per-head RMSNorm (q_norm_w / k_norm_w,
+ * both or neither) and rotate-half RoPE (theta <= 0: none) of q [n, q_row] and k [n, k_row] (fp32, head h at
+ * columns 128 h); q -> q_out bf16 [n, nh, 128], k and v [n, v_row] -> bf16 cache rows [s_cap, nk, 128] at the
+ * tokens' positions (start + n <= s_cap).  d must be 128.  Same per-token math as t2h_attn_decode's prologue.
+ * replaces RMS_NORM_ROPE_TOKEN_F32{,_TO_F16} (src/models/optimized_qwen3/shaders/rms_norm_rope_token_f32.py:22-99)
+ * and TOKEN_MAJOR_{KV,VALUE}_CACHE_WRITE_* (shaders/token_major_kv_cache_write_f16_pair.py:20-103). */
+int t2h_qk_norm_rope_cache(const float* q, uint64_t q_row, const float* k, uint64_t k_row, const float* v,
+                           uint64_t v_row, const float* q_norm_w, const float* k_norm_w, float eps, float theta,
+                           int32_t start, uint32_t n, uint32_t nh, uint32_t nk, uint32_t d, void* q_out,
+                           void* k_cache, void* v_cache, uint32_t s_cap, void* stream);
 int t2h_flash_attn_segments(const void* q, const void* k, const void* v, void* out, const int32_t* cu_seqlens,
                             uint32_t n_seg, uint32_t batch, uint32_t nh, uint32_t nk, uint32_t t_len, uint32_t d,
                             const int64_t* strides, float scale, void* stream);

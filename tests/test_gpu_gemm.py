@@ -28,7 +28,8 @@ def _problem(wtype, m, k, n, seed):
 
 # (m, k, n): exact tiles, ragged M and N (partial 256-tiles), a handful of tokens, long K
 CASES = [("q8_0", 256, 256, 256), ("q8_0", 300, 1024, 520), ("q8_0", 17, 2048, 1024), ("q8_0", 512, 4096, 768),
-         ("q4_k", 256, 256, 256), ("q4_k", 300, 1024, 520), ("q4_k", 9, 4096, 1024), ("q4_k", 640, 3072, 256)]
+         ("q4_k", 256, 256, 256), ("q4_k", 300, 1024, 520), ("q4_k", 9, 4096, 1024), ("q4_k", 640, 3072, 256),
+         ("q6_k", 256, 256, 256), ("q6_k", 300, 1024, 520), ("q6_k", 17, 4096, 1024), ("q6_k", 700, 3072, 384)]
 
 
 @pytest.mark.parametrize("wtype,m,k,n", CASES)

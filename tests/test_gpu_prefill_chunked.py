@@ -1,0 +1,123 @@
+"""GPU parity of the chunked matrix-core prefill: the chunk prologue kernel against the decode prologue
+(bit-exact cache rows) and the numpy oracle, and whole prompts prefilled in chunks against the CPU oracle
+decoder (greedy tokens, near-tie aware) and against the token-by-token prefill's KV cache."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference as R
+from oracle.qwen3_check import check_greedy_tokens, dense_weights
+from oracle.reference import Qwen3Shape
+from tests.conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def test_chunk_prologue_matches_decode_prologue_and_oracle(device):
+    from torch2vk_amd import kernels
+
+    nh, nk, d, n, start, s_cap, theta = 8, 2, 128, 37, 100, 256, 1e6
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((n, nh * d)).astype(np.float32)
+    k = rng.standard_normal((n, nk * d)).astype(np.float32) * 3
+    v = rng.standard_normal((n, nk * d)).astype(np.float32)
+    qw = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    kw = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    qkv = torch.from_numpy(np.concatenate([q, k, v], axis=1)).to(device)
+    kc = torch.zeros(s_cap, nk, d, dtype=torch.bfloat16, device=device)
+    vc = torch.zeros_like(kc)
+    qb = torch.empty(n, nh, d, dtype=torch.bfloat16, device=device)
+    qwt, kwt = torch.from_numpy(qw).to(device), torch.from_numpy(kw).to(device)
+    kernels.qk_norm_rope_cache(qkv[:, :nh * d], qkv[:, nh * d:(nh + nk) * d], qkv[:, (nh + nk) * d:], qb, kc, vc,
+                               start, q_norm_weight=qwt, k_norm_weight=kwt, theta=theta)
+    # numpy oracle
+    cos, sin = R.rope_cos_sin(np.arange(start, start + n), d, theta)
+    q_ref = R.qk_norm_rope(q.reshape(n, nh, d), qw, cos[:, None, :], sin[:, None, :])
+    k_ref = R.qk_norm_rope(k.reshape(n, nk, d), kw, cos[:, None, :], sin[:, None, :])
+    assert_close(qb.float().cpu().numpy(), q_ref, max_abs=3e-2, min_cos=0.9999, what="q")
+    assert_close(kc[start:start + n].float().cpu().numpy(), k_ref, max_abs=1e-1, min_cos=0.9999, what="k")
+    assert torch.equal(vc[start:start + n].cpu(), torch.from_numpy(v.reshape(n, nk, d)).to(torch.bfloat16))
+    assert not kc[:start].any() and not kc[start + n:].any()
+    # the decode prologue writes the same bits for the same token at the same position
+    kd = torch.zeros_like(kc)
+    vd = torch.zeros_like(kc)
+    ws = kernels.attn_decode_workspace(nh, nk, d, s_cap, device)
+    out = torch.empty(nh * d, dtype=torch.bfloat16, device=device)
+    for t in (0, 17, n - 1):
+        pos = torch.tensor([start + t], dtype=torch.int32, device=device)
+        kernels.attn_decode(qkv[t, :nh * d].contiguous(), qkv[t, nh * d:(nh + nk) * d].contiguous(),
+                            qkv[t, (nh + nk) * d:].contiguous(), kd, vd, out, pos, ws, q_norm_weight=qwt,
+                            k_norm_weight=kwt, theta=theta)
+        assert torch.equal(kd[start + t], kc[start + t]), t
+        assert torch.equal(vd[start + t], vc[start + t]), t
+
+
+def _setup(cfg, device, seed, std, policy):
+    from torch2vk_amd.qwen3.weights import matrix_shapes, synthetic_weights
+
+    w = synthetic_weights(cfg, device=device, seed=seed, std=std, norm_std=0.1, policy=policy)
+    dense = dense_weights({k: v.cpu().numpy() for k, v in w.packed.items()}, w.types,
+                          {k: v.cpu().numpy() for k, v in w.norms.items()}, matrix_shapes(cfg))
+    shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
+                       head_dim=cfg.head_dim, mlp=cfg.mlp, vocab=cfg.vocab, rope_theta=cfg.rope_theta)
+    return w, dense, shape
+
+
+@pytest.mark.parametrize("policy,chunk", [("uniform", 16), ("q4_k_m", 5), ("uniform", 4096)])
+def test_chunked_prefill_decode_matches_oracle(device, policy, chunk):
+    from torch2vk_amd.qwen3.config import Qwen3Config
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg = Qwen3Config("tiny-p", hidden=1024, layers=4, heads=8, kv_heads=2, head_dim=128, mlp=1024, vocab=1024,
+                      eos_token_ids=(1023,))
+    w, dense, shape = _setup(cfg, device, seed=31, std=0.05, policy=policy)
+    prompt = np.random.default_rng(2).integers(0, cfg.vocab, 37).tolist()
+    dec = Qwen3Decoder(w, max_positions=96, max_new_tokens=16)
+    dec.stop_on_eos = False
+    toks = dec.generate(torch.tensor(prompt), 10, steps_per_graph=4, prefill_chunk=chunk)
+    print(f"chunked prefill {policy} chunk={chunk}: {toks}", flush=True)
+    print(check_greedy_tokens(shape, dense, prompt, toks))
+
+
+def test_chunked_prefill_cache_matches_token_prefill(device):
+    from torch2vk_amd.qwen3.config import Qwen3Config
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg = Qwen3Config("tiny-p", hidden=1024, layers=3, heads=8, kv_heads=2, head_dim=128, mlp=1024, vocab=1024,
+                      eos_token_ids=(1023,))
+    w, _, _ = _setup(cfg, device, seed=41, std=0.05, policy="uniform")
+    prompt = torch.tensor(np.random.default_rng(3).integers(0, cfg.vocab, 50).tolist())
+    a = Qwen3Decoder(w, max_positions=64, max_new_tokens=4)
+    b = Qwen3Decoder(w, max_positions=64, max_new_tokens=4)
+    a.prefill(prompt)
+    b.prefill_chunked(prompt, chunk=20)
+    torch.cuda.synchronize()
+    n = prompt.numel()
+    for name in ("k_cache", "v_cache"):
+        ca = getattr(a, name)[:, :n].float().cpu().numpy()
+        cb = getattr(b, name)[:, :n].float().cpu().numpy()
+        assert_close(cb, ca, max_abs=0.1 * np.abs(ca).max(), min_cos=0.999, what=name)
+        assert not getattr(b, name)[:, n:].any()
+    assert int(a.position.item()) == int(b.position.item()) == n
+    assert int(a.length.item()) == int(b.length.item()) == 1
+
+
+def test_chunked_prefill_from_embeds_equals_ids(device):
+    """A prompt given as its own embedding rows prefills exactly like the ids (same kernels, same bits)."""
+    from torch2vk_amd.qwen3.config import Qwen3Config
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg = Qwen3Config("tiny-p", hidden=1024, layers=2, heads=8, kv_heads=2, head_dim=128, mlp=1024, vocab=1024,
+                      eos_token_ids=(1023,))
+    w, _, _ = _setup(cfg, device, seed=51, std=0.05, policy="qwen3_asr")
+    prompt = torch.tensor(np.random.default_rng(4).integers(0, cfg.vocab, 23).tolist(), device=device)
+    a = Qwen3Decoder(w, max_positions=48, max_new_tokens=8)
+    b = Qwen3Decoder(w, max_positions=48, max_new_tokens=8)
+    a.stop_on_eos = b.stop_on_eos = False
+    ta = a.generate(prompt, 6, prefill_chunk=8)
+    tb = b.generate_from_embeds(b.embed_tokens(prompt), 6, prefill_chunk=8)
+    assert ta == tb
+    assert torch.equal(a.k_cache, b.k_cache)

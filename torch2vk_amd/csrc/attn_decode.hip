@@ -32,6 +32,7 @@
 // The current position is read from device memory, so a captured graph can
 // replay the step with an advancing position.
 #include "common.h"
+#include "rope.h"
 
 namespace t2h {
 
@@ -62,25 +63,6 @@ struct AttnDecodeArgs {
     float eps;
     float scale;            // softmax scale, 1/sqrt(D)
 };
-
-__device__ __forceinline__ void norm_rope_pair(float x0, float x1, bool has_w, float w0, float w1, float eps,
-                                               float cs, float sn, bool rope, float& r0, float& r1) {
-    float n0 = x0, n1 = x1;
-    if (has_w) {
-        const float ss = wave_sum(x0 * x0 + x1 * x1);
-        const float inv = 1.0f / sqrtf(ss / (float)AD_D + eps);
-        n0 = x0 * inv * w0;
-        n1 = x1 * inv * w1;
-    }
-    if (rope) {
-        // rotate_half pairs d with d + D/2: out[d] = n[d]cos - n[d+D/2]sin, out[d+D/2] = n[d+D/2]cos + n[d]sin
-        r0 = n0 * cs - n1 * sn;
-        r1 = n1 * cs + n0 * sn;
-    } else {
-        r0 = n0;
-        r1 = n1;
-    }
-}
 
 // K and V rows of one tile: positions t + 16 r + p_k of the K quarter `part`,
 // and V rows t .. t + TILE - 1 (lane owns dims 2 lane, 2 lane + 1).
@@ -177,9 +159,7 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
     //    q head `wave` normalised, rotated, pre-scaled by 1/sqrt(D) into LDS
     float cs = 1.0f, sn = 0.0f;
     if (rope && needs_rope) {
-        const float inv_freq = exp2f(-(2.0f * (float)lane / (float)AD_D) * log2f(a.theta));
-        const float angle = (float)pos * inv_freq;
-        sincosf(angle, &sn, &cs);
+        rope_cos_sin(lane, pos, a.theta, cs, sn);
     }
     if (wave < GROUP) {
         float r0, r1;

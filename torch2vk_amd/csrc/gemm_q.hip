@@ -66,6 +66,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 struct GemmQ80 {
     static constexpr int BLOCK_VALUES = 32;
     static constexpr int BLOCK_BYTES = 34;
+    static constexpr int ALIGN = 2;
     struct Raw {
         uint4 q0, q1;
         uint32_t d;
@@ -111,6 +112,7 @@ struct GemmQ80 {
 struct GemmQ4K {
     static constexpr int BLOCK_VALUES = 256;
     static constexpr int BLOCK_BYTES = 144;
+    static constexpr int ALIGN = 16;
     struct Raw {
         uint4 hdr, q0, q1;
     };
@@ -157,6 +159,63 @@ struct GemmQ4K {
             const float v3 = ds * (float)((w >> 24) & 0xfu) - dm;
             o[2 * c] = pack_bf16x2(v0, v1);
             o[2 * c + 1] = pack_bf16x2(v2, v3);
+        }
+        uint16_t* dst = lds_b + (t >> 1) * GQ_LDS_ROW + (t & 1) * 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<uint4*>(dst + 8 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    }
+};
+
+// Q6_K: a 64-wide K stage is parts p0, p0 + 1 of half h of superblock k0 / 256
+// (value 128 h + 32 p + l, l < 32); thread t dequantises part p0 + (t & 1) of
+// row t >> 1:  value = (d * sc[8h + 2p + l/16]) * (q - 32),
+//   q = (ql[64h + 32(p&1) + l] >> 4(p>>1) & 15) | ((qh[32h + l] >> 2p) & 3) << 4.
+// Blocks are 210 B, so only halfword aligned: the 16-B loads are unaligned.
+struct GemmQ6K {
+    static constexpr int BLOCK_VALUES = 256;
+    static constexpr int BLOCK_BYTES = 210;
+    static constexpr int ALIGN = 2;
+    struct Raw {
+        uint4 ql0, ql1, qh0, qh1;
+        uint32_t sc, d;
+    };
+    __device__ static __forceinline__ void load(const GemmArgs& a, uint32_t n0, uint32_t k0, Raw& r) {
+        const uint32_t t = threadIdx.x;
+        uint32_t row = n0 + (t >> 1);
+        row = row < a.n ? row : a.n - 1;
+        const uint8_t* blk = a.w + (size_t)row * a.row_bytes + (size_t)(k0 / 256) * 210;
+        const uint32_t h = (k0 % 256) / 128;
+        const uint32_t p = (k0 % 128) / 32 + (t & 1);
+        const uint8_t* ql = blk + 64 * h + 32 * (p & 1);
+        r.ql0 = load_u4_ua(ql);
+        r.ql1 = load_u4_ua(ql + 16);
+        r.qh0 = load_u4_ua(blk + 128 + 32 * h);
+        r.qh1 = load_u4_ua(blk + 128 + 32 * h + 16);
+        r.sc = load_u16(blk + 192 + 8 * h + 2 * p);
+        r.d = load_u16(blk + 208);
+    }
+    __device__ static __forceinline__ void store(const Raw& r, uint16_t* lds_b, uint32_t k0) {
+        const uint32_t t = threadIdx.x;
+        const uint32_t p = (k0 % 128) / 32 + (t & 1);
+        const uint32_t shl = 4 * (p >> 1), shh = 2 * p;
+        const float d = f16_bits_to_f32(r.d);
+        const float a0 = d * (float)(int8_t)(r.sc & 0xffu);  // values l < 16
+        const float a1 = d * (float)(int8_t)(r.sc >> 8);     // values l >= 16
+        const uint32_t ql[8] = {r.ql0.x, r.ql0.y, r.ql0.z, r.ql0.w, r.ql1.x, r.ql1.y, r.ql1.z, r.ql1.w};
+        const uint32_t qh[8] = {r.qh0.x, r.qh0.y, r.qh0.z, r.qh0.w, r.qh1.x, r.qh1.y, r.qh1.z, r.qh1.w};
+        uint32_t o[16];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float a = c < 4 ? a0 : a1;
+            float v[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t q = ((ql[c] >> (8 * b + shl)) & 15u) | (((qh[c] >> (8 * b + shh)) & 3u) << 4);
+                v[b] = a * (float)((int)q - 32);
+            }
+            o[2 * c] = pack_bf16x2(v[0], v[1]);
+            o[2 * c + 1] = pack_bf16x2(v[2], v[3]);
         }
         uint16_t* dst = lds_b + (t >> 1) * GQ_LDS_ROW + (t & 1) * 32;
 #pragma unroll
@@ -319,7 +378,7 @@ static int gemm_q_launch(const void* x, const void* w, const float* bias, int ac
     if (F::BLOCK_VALUES == 256 && w_k != k) return T2H_ERR_SHAPE;
     if (act != GQACT_NONE && act != GQACT_GELU) return T2H_ERR_ARG;
     if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) return T2H_ERR_ALIGN;
-    if (F::BLOCK_VALUES == 256 && (reinterpret_cast<uintptr_t>(w) & 15) != 0) return T2H_ERR_ALIGN;
+    if ((reinterpret_cast<uintptr_t>(w) & (F::ALIGN - 1)) != 0) return T2H_ERR_ALIGN;
     int epi;
     if (residual) {
         if (out_dtype != T2H_DTYPE_F32) return T2H_ERR_DTYPE;
@@ -373,4 +432,9 @@ extern "C" int t2h_q8_0_linear(const void* x, const void* w, const float* bias, 
                                const float* residual, uint32_t m, uint32_t k, uint32_t n, uint32_t w_k,
                                void* stream) {
     return gemm_q_launch<GemmQ80>(x, w, bias, act, y, out_dtype, residual, m, k, n, w_k, stream);
+}
+
+extern "C" int t2h_q6k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                            uint32_t k, uint32_t n, void* stream) {
+    return gemm_q_launch<GemmQ6K>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
 }

@@ -267,9 +267,10 @@ def lm_head_argmax_partial(x: torch.Tensor, w: torch.Tensor, wtype: str, partial
 
 def gemm(x: torch.Tensor, w: torch.Tensor, wtype: str, *, out: torch.Tensor | None = None,
          out_dtype: torch.dtype = torch.bfloat16, residual: torch.Tensor | None = None) -> torch.Tensor:
-    """Prefill GEMM on the matrix cores: y[M, N] = x[M, K] . deq(W)^T (+ residual); x bf16, W Q8_0 or Q4_K."""
-    if wtype not in ("q8_0", "q4_k"):
-        raise ValueError(f"gemm handles q8_0 and q4_k weights, got {wtype!r}")
+    """Prefill GEMM on the matrix cores: y[M, N] = x[M, K] . deq(W)^T (+ residual); x bf16, W Q8_0, Q4_K or
+    Q6_K."""
+    if wtype not in ("q8_0", "q4_k", "q6_k"):
+        raise ValueError(f"gemm handles q8_0, q4_k and q6_k weights, got {wtype!r}")
     _check(x, "x", torch.bfloat16)
     k = int(x.shape[-1])
     if k % 64:
@@ -285,9 +286,47 @@ def gemm(x: torch.Tensor, w: torch.Tensor, wtype: str, *, out: torch.Tensor | No
         _check(residual, "residual", torch.float32, align=4)
         if residual.numel() != m * n or out.dtype != torch.float32:
             raise ValueError("residual must be fp32 with the output's shape; output must be fp32")
-    name = "t2h_q8_0_gemm" if wtype == "q8_0" else "t2h_q4k_gemm"
+    name = {"q8_0": "t2h_q8_0_gemm", "q4_k": "t2h_q4k_gemm", "q6_k": "t2h_q6k_gemm"}[wtype]
     call(name, ptr(x), ptr(w), ptr(out), _OUT_DTYPES[out.dtype], ptr(residual), m, k, n, stream_handle())
     return out
+
+
+def qk_norm_rope_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out: torch.Tensor,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor, start: int, *,
+                       q_norm_weight: torch.Tensor | None = None, k_norm_weight: torch.Tensor | None = None,
+                       theta: float = 1e6, eps: float = RMS_EPS) -> torch.Tensor:
+    """Prefill chunk prologue: q/k per-head RMSNorm + RoPE at positions start.., q -> q_out bf16 [n, nh, 128],
+    k/v -> bf16 rows of one layer's cache [s_cap, nk, 128].  q, k, v fp32 [n, heads * 128] with unit column
+    stride (row views of one wider buffer are fine)."""
+    n = int(q.shape[0])
+    for t, name in ((q, "q"), (k, "k"), (v, "v")):
+        _check_strided(t, name, torch.float32)
+        if t.dim() != 2 or t.shape[0] != n or t.shape[1] % 128:
+            raise ValueError(f"{name} must be fp32 [n, heads * 128], got {tuple(t.shape)}")
+    nh, nk = q.shape[1] // 128, k.shape[1] // 128
+    if v.shape[1] != k.shape[1]:
+        raise ValueError("k and v must have the same width")
+    _check(q_out, "q_out", torch.bfloat16)
+    if q_out.numel() != n * nh * 128:
+        raise ValueError(f"q_out must hold [{n}, {nh}, 128]")
+    for t, name in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        _check(t, name, torch.bfloat16)
+        if t.dim() != 3 or t.shape[1] != nk or t.shape[2] != 128:
+            raise ValueError(f"{name} must be bf16 [s_cap, {nk}, 128], got {tuple(t.shape)}")
+    if (q_norm_weight is None) != (k_norm_weight is None):
+        raise ValueError("pass both q and k norm weights or neither")
+    for t, name in ((q_norm_weight, "q_norm_weight"), (k_norm_weight, "k_norm_weight")):
+        if t is not None:
+            _check(t, name, torch.float32, align=4)
+            if t.numel() != 128:
+                raise ValueError(f"{name} must have 128 elements")
+    s_cap = int(k_cache.shape[0])
+    if start < 0 or start + n > s_cap:
+        raise ValueError(f"positions {start}..{start + n - 1} exceed the cache capacity {s_cap}")
+    call("t2h_qk_norm_rope_cache", ptr(q), q.stride(0), ptr(k), k.stride(0), ptr(v), v.stride(0), ptr(q_norm_weight),
+         ptr(k_norm_weight), eps, theta, int(start), n, nh, nk, 128, ptr(q_out), ptr(k_cache), ptr(v_cache), s_cap,
+         stream_handle())
+    return q_out
 
 
 ACTS = {None: 0, "none": 0, "gelu": 1}

@@ -290,6 +290,83 @@ class Qwen3Decoder:
                 self.position.add_(1)
         self.run_token_store(advance=True)
 
+    # ------------------------------------------------- chunked prefill --
+
+    def _fused_qkv(self, layer_idx: int) -> torch.Tensor | None:
+        """The layer's q|k|v rows as one matrix when they are stacked in one allocation of one type."""
+        p = f"layers.{layer_idx}."
+        q, k, v = (self._w(p + n) for n in ("q", "k", "v"))
+        if len({self.types[p + n] for n in ("q", "k", "v")}) != 1:
+            return None
+        if k.data_ptr() != q.data_ptr() + q.numel() or v.data_ptr() != k.data_ptr() + k.numel():
+            return None
+        rows = q.shape[0] + k.shape[0] + v.shape[0]
+        return q.as_strided((rows, q.shape[1]), (q.shape[1], 1))
+
+    def _prefill_layer(self, i: int, h: torch.Tensor, start: int) -> None:
+        """One layer over a chunk's fp32 residual stream h [n, hidden] at positions start.. (run_text_layer,
+        src/models/optimized_qwen3/dispatch/text_layer.py): RMSNorm rows -> q|k|v GEMM -> q/k norm + RoPE +
+        KV cache write -> causal flash attention over the cache -> o GEMM + residual -> RMSNorm -> gate, up
+        GEMMs -> SwiGLU -> down GEMM + residual.  GEMMs run on the matrix cores for any chunk length."""
+        c, t, p = self.config, self.types, f"layers.{i}."
+        n = h.shape[0]
+        x = kernels.rms_norm(h, self._n(p + "input_norm"), out=torch.empty(n, c.hidden, dtype=torch.bfloat16,
+                                                                           device=self.device), eps=c.rms_eps)
+        fused = self._fused_qkv(i)
+        if fused is not None:
+            qkv = kernels.gemm(x, fused, t[p + "q"], out_dtype=torch.float32)
+            q, k, v = qkv[:, :c.q_dim], qkv[:, c.q_dim:c.q_dim + c.kv_dim], qkv[:, c.q_dim + c.kv_dim:]
+        else:
+            q, k, v = (kernels.gemm(x, self._w(p + nm), t[p + nm], out_dtype=torch.float32) for nm in ("q", "k", "v"))
+        qb = torch.empty(n, c.heads, c.head_dim, dtype=torch.bfloat16, device=self.device)
+        kernels.qk_norm_rope_cache(q, k, v, qb, self.k_cache[i], self.v_cache[i], start,
+                                   q_norm_weight=self._n(p + "q_norm"), k_norm_weight=self._n(p + "k_norm"),
+                                   theta=c.rope_theta, eps=c.rms_eps)
+        keys = self.k_cache[i, :start + n].unsqueeze(0)
+        vals = self.v_cache[i, :start + n].unsqueeze(0)
+        attn = kernels.flash_attn_prefill(qb.unsqueeze(0), keys, vals, causal=True, causal_offset=start)
+        kernels.gemm(attn.view(n, c.q_dim), self._w(p + "o"), t[p + "o"], out=h, residual=h)
+        x = kernels.rms_norm(h, self._n(p + "post_norm"), out=x, eps=c.rms_eps)
+        gate = kernels.gemm(x, self._w(p + "gate"), t[p + "gate"], out_dtype=torch.float32)
+        up = kernels.gemm(x, self._w(p + "up"), t[p + "up"], out_dtype=torch.float32)
+        act = kernels.swiglu(gate, up)
+        del gate, up
+        kernels.gemm(act, self._w(p + "down"), t[p + "down"], out=h, residual=h)
+
+    def prefill_chunked(self, prompt_ids: torch.Tensor | None = None, *, embeds: torch.Tensor | None = None,
+                        start: int = 0, chunk: int = 2048) -> None:
+        """Prompt (token ids, or fp32 input embeddings [T, hidden]) through the matrix-core path ``chunk``
+        tokens at a time -- the reference's fixed-size chunk + tail prefill (src/models/optimized_qwen3/
+        run.py:395-471) with every chunk a plain GEMM pass and causal attention that visits only the key tiles
+        at or below each query tile's diagonal.  Then the last token's final norm, LM head and greedy select,
+        and the first generated token stored, as after ``prefill``."""
+        c = self.config
+        if (prompt_ids is None) == (embeds is None):
+            raise ValueError("pass prompt_ids or embeds")
+        if embeds is None:
+            ids = prompt_ids.to(device=self.device, dtype=torch.int64).view(-1)
+            e = self.embed_tokens(ids)
+        else:
+            e = embeds.reshape(-1, c.hidden)
+            if e.dtype != torch.float32 or e.device != self.device:
+                raise ValueError("embeds must be fp32 on the decoder's device")
+        total = e.shape[0]
+        if total == 0:
+            raise ValueError("empty prompt")
+        if start + total > self.max_positions:
+            raise ValueError("prompt exceeds the KV cache capacity")
+        if chunk <= 0:
+            raise ValueError("chunk must be positive")
+        self.reset(position=start)
+        for c0 in range(0, total, chunk):
+            h = e[c0:c0 + chunk].clone()
+            for i in range(c.layers):
+                self._prefill_layer(i, h, start + c0)
+        self.h.copy_(h[-1])
+        self.position.fill_(start + total - 1)
+        self.run_lm_head_select()
+        self.run_token_store(advance=True)
+
     def prefill_embeds(self, embeds: torch.Tensor, start: int = 0) -> None:
         """Feed a prompt given as fp32 input embeddings [T, hidden] -- a Qwen3-ASR prompt after the audio
         features were injected (run_audio_inject) -- one position at a time; the last position's step selects
@@ -322,14 +399,22 @@ class Qwen3Decoder:
         return self.generated[:n].tolist()
 
     def generate(self, prompt_ids: torch.Tensor, max_new_tokens: int, *, steps_per_graph: int = 8,
-                 use_graph: bool = True) -> list[int]:
+                 use_graph: bool = True, prefill_chunk: int | None = None) -> list[int]:
+        """Greedy decode.  ``prefill_chunk`` set: the prompt goes through the chunked matrix-core prefill;
+        None: one decode step per prompt token."""
         self._check_budget(prompt_ids.numel(), max_new_tokens)
-        self.prefill(prompt_ids)
+        if prefill_chunk:
+            self.prefill_chunked(prompt_ids, chunk=prefill_chunk)
+        else:
+            self.prefill(prompt_ids)
         return self._finish(max_new_tokens, steps_per_graph, use_graph)
 
     def generate_from_embeds(self, embeds: torch.Tensor, max_new_tokens: int, *, steps_per_graph: int = 8,
-                             use_graph: bool = True) -> list[int]:
+                             use_graph: bool = True, prefill_chunk: int | None = None) -> list[int]:
         """Greedy decode after a prompt of input embeddings (the Qwen3-ASR transcription loop)."""
         self._check_budget(embeds.reshape(-1, self.config.hidden).shape[0], max_new_tokens)
-        self.prefill_embeds(embeds)
+        if prefill_chunk:
+            self.prefill_chunked(embeds=embeds, chunk=prefill_chunk)
+        else:
+            self.prefill_embeds(embeds)
         return self._finish(max_new_tokens, steps_per_graph, use_graph)
