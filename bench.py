@@ -41,8 +41,13 @@ PROMPT_POSITIONS = 4096
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=256)
-    p.add_argument("--warmup", type=int, default=16)
+    p.add_argument("--config", choices=("decode", "prefill", "asr"), default="decode",
+                   help="decode: BASELINE configs[2], the headline (default); prefill: configs[3], 8 x 2048 tokens "
+                        "through the 36-layer 8B shape with Q8_0 weights; asr: configs[4], the 24-layer encoder over "
+                        "4 x 1500 frames then a 0.6B-shape int4 decoder for 64 tokens per utterance")
+    p.add_argument("--steps", type=int, default=None, help="timed steps (default 256 decode tokens, 5 prefill or "
+                                                           "asr passes)")
+    p.add_argument("--warmup", type=int, default=None, help="untimed steps (default 16 decode, 1 prefill/asr)")
     p.add_argument("--steps-per-graph", type=int, default=8)
     p.add_argument("--model", choices=("8b", "0.6b"), default="8b")
     p.add_argument("--policy", choices=("uniform", "q4_k_m"), default="uniform",
@@ -106,8 +111,16 @@ def main() -> int:
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build is single-GPU); got --gpus {args.gpus}", file=sys.stderr)
         return 2
+    if args.steps is None:
+        args.steps = 256 if args.config == "decode" else 5
+    if args.warmup is None:
+        args.warmup = 16 if args.config == "decode" else 1
     if args.profile_kernel:
         return profile_kernel_target(args.per_op)
+    if args.config == "prefill":
+        return bench_prefill(args)
+    if args.config == "asr":
+        return bench_asr(args)
     import torch
 
     from torch2vk_amd import kernels
@@ -389,6 +402,390 @@ def cpu_baseline(cfg, weights, positions: int, steps: int) -> dict:
         "sample": f"CPU oracle decoder (torch {torch.__version__}, fp32 dense weights dequantized by the oracle): "
                   f"1 of {c.layers} layers at KV position {positions} timed over {steps} steps (median "
                   f"{t_layer * 1e3:.1f} ms) x {c.layers} + LM head+argmax (median {t_lm * 1e3:.1f} ms)",
+    }
+
+
+# ----------------------------------------------------------------- prefill --
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def _events_us(fn, reps: int) -> float:
+    """Average duration of ``fn`` (one launch) over ``reps`` back-to-back calls, HIP events on the current
+    stream, which is the stream the launches go to."""
+    import torch
+
+    fn()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) * 1000.0 / reps
+
+
+def _timed_steps(step, warmup: int, steps: int) -> float:
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def bench_prefill(args) -> int:
+    """8 sequences x 2048 random token ids through the 36-layer Qwen3-8B shape, every
+    linear weight Q8_0 (int8, group 32) dequantised into the bf16 MFMA GEMM, causal flash attention, then
+    the final norm + LM head + greedy select of each sequence's first token.  A step is that whole prefill."""
+    import torch
+
+    from torch2vk_amd import kernels
+    from torch2vk_amd.qwen3.config import QWEN3_8B
+
+    if not torch.cuda.is_available():
+        print("no HIP device", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    c = QWEN3_8B
+    nb, tl = 8, 2048
+    m = nb * tl
+    t_setup = time.time()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+
+    def packed(rows: int, cols: int, wtype: str) -> torch.Tensor:
+        dense = torch.randn(rows, cols, generator=gen, device=dev).mul_(0.02)
+        out = kernels.quantize(dense, wtype)
+        del dense
+        return out
+
+    def norm(n: int) -> torch.Tensor:
+        return torch.ones(n, device=dev).add_(torch.randn(n, generator=gen, device=dev).mul_(0.1))
+
+    qkv_rows = c.q_dim + 2 * c.kv_dim
+    layers = [dict(qkv=packed(qkv_rows, c.hidden, "q8_0"), o=packed(c.hidden, c.q_dim, "q8_0"),
+                   gate=packed(c.mlp, c.hidden, "q8_0"), up=packed(c.mlp, c.hidden, "q8_0"),
+                   down=packed(c.hidden, c.mlp, "q8_0"), input_norm=norm(c.hidden), post_norm=norm(c.hidden),
+                   q_norm=norm(c.head_dim), k_norm=norm(c.head_dim)) for _ in range(c.layers)]
+    embed = packed(c.vocab, c.hidden, "q8_0")
+    lm_head = packed(c.vocab, c.hidden, "q4_k")
+    final_norm = norm(c.hidden)
+    ids = torch.randint(0, c.vocab, (m,), generator=gen, device=dev)
+    bf, f32 = torch.bfloat16, torch.float32
+    h = torch.empty(m, c.hidden, dtype=f32, device=dev)
+    x = torch.empty(m, c.hidden, dtype=bf, device=dev)
+    qkv = torch.empty(m, qkv_rows, dtype=f32, device=dev)
+    qb = torch.empty(m, c.heads, c.head_dim, dtype=bf, device=dev)
+    kc = torch.empty(nb, tl, c.kv_heads, c.head_dim, dtype=bf, device=dev)
+    vc = torch.empty_like(kc)
+    attn = torch.empty(nb, tl, c.heads, c.head_dim, dtype=bf, device=dev)
+    gate = torch.empty(m, c.mlp, dtype=f32, device=dev)
+    up = torch.empty_like(gate)
+    act = torch.empty(m, c.mlp, dtype=bf, device=dev)
+    ps = torch.empty(512, dtype=f32, device=dev)
+    pt = torch.empty(512, dtype=torch.int32, device=dev)
+    eos = torch.tensor(c.eos_token_ids, dtype=torch.int64, device=dev)
+    next_tok = torch.zeros(nb, 1, dtype=torch.int64, device=dev)
+    done = torch.zeros(nb, 1, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    print(f"[bench] prefill setup {time.time() - t_setup:.1f}s", file=sys.stderr, flush=True)
+
+    def layer_pass(lw) -> None:
+        kernels.rms_norm(h, lw["input_norm"], out=x)
+        kernels.gemm(x, lw["qkv"], "q8_0", out=qkv)
+        for b in range(nb):
+            r = slice(b * tl, (b + 1) * tl)
+            kernels.qk_norm_rope_cache(qkv[r, :c.q_dim], qkv[r, c.q_dim:c.q_dim + c.kv_dim],
+                                       qkv[r, c.q_dim + c.kv_dim:], qb[r], kc[b], vc[b], 0,
+                                       q_norm_weight=lw["q_norm"], k_norm_weight=lw["k_norm"], theta=c.rope_theta)
+        kernels.flash_attn_prefill(qb.view(nb, tl, c.heads, c.head_dim), kc, vc, out=attn, causal=True)
+        kernels.gemm(attn.view(m, c.q_dim), lw["o"], "q8_0", out=h, residual=h)
+        kernels.rms_norm(h, lw["post_norm"], out=x)
+        kernels.gemm(x, lw["gate"], "q8_0", out=gate)
+        kernels.gemm(x, lw["up"], "q8_0", out=up)
+        kernels.swiglu(gate, up, out=act)
+        kernels.gemm(act, lw["down"], "q8_0", out=h, residual=h)
+
+    def step() -> None:
+        kernels.embedding_q8_0(embed, ids, c.hidden, out=h)
+        for lw in layers:
+            layer_pass(lw)
+        for b in range(nb):
+            kernels.lm_head_argmax_partial(h[(b + 1) * tl - 1], lm_head, "q4_k", ps, pt, norm_weight=final_norm)
+            kernels.token_select(ps, pt, eos, next_tok[b], done[b])
+
+    per_step = _timed_steps(step, args.warmup, args.steps)
+    tok_s = m / per_step
+    params = qkv_rows * c.hidden + c.hidden * c.q_dim + 2 * c.mlp * c.hidden + c.hidden * c.mlp
+    linear_flop = 2.0 * m * params * c.layers
+    attn_flop = 4.0 * c.heads * c.head_dim * (tl * (tl + 1) / 2) * nb * c.layers
+    total_flop = linear_flop + attn_flop + 2.0 * nb * c.vocab * c.hidden
+    tflops = total_flop / per_step / 1e12
+    print(f"[bench] prefill {per_step * 1e3:.1f} ms per 8 x 2048 tokens: {tok_s:.0f} tok/s, {tflops:.1f} TFLOP/s",
+          file=sys.stderr, flush=True)
+
+    # dominant kernel: the MLP up-projection GEMM (M 16384, K 4096, N 12288), HIP events on its stream
+    gemm_us = _events_us(lambda: kernels.gemm(x, layers[0]["up"], "q8_0", out=up), args.kernel_reps * 4)
+    gemm_tflops = 2.0 * m * c.hidden * c.mlp / (gemm_us * 1e-6) / 1e12
+    fa_us = _events_us(lambda: kernels.flash_attn_prefill(qb.view(nb, tl, c.heads, c.head_dim), kc, vc, out=attn,
+                                                          causal=True), args.kernel_reps * 4)
+    fa_tflops = 4.0 * c.heads * c.head_dim * (tl * (tl + 1) / 2) * nb / (fa_us * 1e-6) / 1e12
+    cpu = None if args.no_cpu_baseline else cpu_baseline_prefill(layers[0], c)
+    line = {
+        "metric": "Qwen3-8B-shape int8 (Q8_0) prefill tok/s, 8 x 2048 tokens; MFMA utilisation vs bf16 dense peak",
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(per_step * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights quantized to Q8_0 on the GPU, random token ids)",
+        "config": {
+            "workload": "Qwen3-8B-shape prefill of 8 sequences x 2048 tokens: Q8_0 embedding, 36 layers (RMSNorm, "
+                        "q|k|v GEMM, q/k norm + RoPE + KV write, causal flash attention, o GEMM + residual, "
+                        "RMSNorm, gate and up GEMMs, SwiGLU, down GEMM + residual), final norm + Q4_K LM head + "
+                        "greedy select of each sequence's first token",
+            "batch": nb, "seq_len": tl, "weights": "q8_0",
+        },
+        "mfma_utilisation": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+        "achieved_tflops": round(tflops, 1),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm_q_kernel<GemmQ80> (MLP up-projection, M 16384 K 4096 N 12288)",
+            "achieved": round(gemm_tflops, 1),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "avg_launch_us": round(gemm_us, 1),
+        },
+        "flash_attention": {"avg_launch_us": round(fa_us, 1), "tflops": round(fa_tflops, 1)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline_prefill(lw, c) -> dict:
+    """The CPU oracle's Qwen3 forward of one 8B-shape layer (weights dequantized from the same Q8_0 bytes) over
+    one 256-token chunk, scaled to 36 layers: tokens/s of prefill on the host cores."""
+    import torch
+
+    import oracle
+    from oracle.reference import Qwen3CpuModel, Qwen3Shape
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    qkv = oracle.dequant_q8_0(lw["qkv"].cpu().numpy(), c.hidden)
+    dense = {"layers.0.q": torch.from_numpy(qkv[:c.q_dim]),
+             "layers.0.k": torch.from_numpy(qkv[c.q_dim:c.q_dim + c.kv_dim]),
+             "layers.0.v": torch.from_numpy(qkv[c.q_dim + c.kv_dim:]),
+             "layers.0.o": torch.from_numpy(oracle.dequant_q8_0(lw["o"].cpu().numpy(), c.q_dim)),
+             "layers.0.gate": torch.from_numpy(oracle.dequant_q8_0(lw["gate"].cpu().numpy(), c.hidden)),
+             "layers.0.up": torch.from_numpy(oracle.dequant_q8_0(lw["up"].cpu().numpy(), c.hidden)),
+             "layers.0.down": torch.from_numpy(oracle.dequant_q8_0(lw["down"].cpu().numpy(), c.mlp))}
+    for n in ("input_norm", "post_norm", "q_norm", "k_norm"):
+        dense[f"layers.0.{n}"] = lw[n].cpu()
+    dense["embed"] = torch.randn(256, c.hidden)
+    dense["norm"] = torch.ones(c.hidden)
+    dense["lm_head"] = torch.zeros(1, c.hidden)
+    shape = Qwen3Shape(hidden=c.hidden, layers=1, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
+                       mlp=c.mlp, vocab=c.vocab, rope_theta=c.rope_theta)
+    times = []
+    for _ in range(3):
+        model = Qwen3CpuModel(shape, dense, max_positions=256)
+        t0 = time.perf_counter()
+        model.forward(torch.arange(256), start=0)
+        times.append(time.perf_counter() - t0)
+    t_layer = statistics.median(times)
+    return {
+        "value": round(256 / (c.layers * t_layer), 2),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"CPU oracle Qwen3 forward (torch {torch.__version__}, fp32 dense weights dequantized from the "
+                  f"Q8_0 bytes) of 1 of {c.layers} layers over one 256-token chunk (median {t_layer * 1e3:.0f} ms), "
+                  f"x {c.layers}; attention at 256 rather than 2048 tokens, so this overstates the CPU rate",
+    }
+
+
+# --------------------------------------------------------------------- asr --
+
+
+def bench_asr(args) -> int:
+    """the 24-layer, 1024-wide, 16-head audio encoder (Q8_0 linears, FFN 4096) over
+    4 utterances x 1500 frames of N(0,1) features, attention within each utterance; then, per utterance, a
+    Qwen3-0.6B-shape uniform-int4 decoder whose prompt embeddings carry that utterance's 1500 encoder states
+    (injected at the audio placeholder positions), chunked prefill and 64 greedy tokens.  A step is the whole
+    job; value = audio frames per second through it."""
+    import torch
+
+    from torch2vk_amd import kernels
+    from torch2vk_amd.qwen3.config import QWEN3_0_6B
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+    from torch2vk_amd.qwen3.weights import synthetic_weights
+    from torch2vk_amd.qwen3_asr.config import ASR_C5_ENCODER
+    from torch2vk_amd.qwen3_asr.encoder import (Qwen3AudioEncoder, quantize_audio_weights, run_audio_inject,
+                                                synthetic_audio_dense)
+
+    if not torch.cuda.is_available():
+        print("no HIP device", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    ecfg, tcfg = ASR_C5_ENCODER, QWEN3_0_6B
+    nb, frames, new_tokens = 4, 1500, 64
+    t_setup = time.time()
+    enc = Qwen3AudioEncoder(quantize_audio_weights(synthetic_audio_dense(ecfg, seed=0), ecfg, dev))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    feats_in = torch.randn(nb * frames, ecfg.d_model, generator=gen, device=dev).to(torch.bfloat16).float()
+    cu = kernels.segment_bounds([frames * i for i in range(nb + 1)], nb * frames, dev)
+    tw = synthetic_weights(tcfg, device=dev, seed=2)
+    prefix, suffix = [151644, 8948, 198, 151669], [151670, 151645, 198]
+    prompt_len = len(prefix) + frames + len(suffix)
+    dec = Qwen3Decoder(tw, max_positions=prompt_len + new_tokens + 16, max_new_tokens=new_tokens + 8, device=dev)
+    dec.stop_on_eos = False
+    ids = torch.tensor(prefix + [ecfg_audio_id()] * frames + suffix, device=dev)
+    audio_pos = torch.arange(len(prefix), len(prefix) + frames, device=dev)
+    h = torch.empty_like(feats_in)
+    transcripts = []
+    torch.cuda.synchronize()
+    print(f"[bench] asr setup {time.time() - t_setup:.1f}s", file=sys.stderr, flush=True)
+
+    def encode() -> torch.Tensor:
+        h.copy_(feats_in)
+        enc.encoder_layers(h, cu)
+        return enc.head(h)
+
+    def step() -> None:
+        feats = encode()
+        transcripts.clear()
+        for b in range(nb):
+            emb = dec.embed_tokens(ids)
+            run_audio_inject(emb, audio_pos, feats[b * frames:(b + 1) * frames])
+            transcripts.append(dec.generate_from_embeds(emb, new_tokens, prefill_chunk=2048))
+
+    per_step = _timed_steps(step, args.warmup, args.steps)
+    frames_s = nb * frames / per_step
+    enc_s = _timed_steps(encode, 1, max(3, args.steps))
+    d, f, lay = ecfg.d_model, ecfg.ffn, ecfg.layers
+    enc_flop = 2.0 * nb * frames * lay * (4 * d * d + 2 * d * f) + 4.0 * nb * frames * frames * d * lay
+    enc_flop += 2.0 * nb * frames * (d * d + d * ecfg.output_dim)
+    enc_tflops = enc_flop / enc_s / 1e12
+    x_ln = torch.randn(nb * frames, d, generator=gen, device=dev).to(torch.bfloat16)
+    fc1 = enc.weights.packed["thinker.audio_tower.layers.0.fc1.weight"]
+    b1 = enc.weights.vectors["thinker.audio_tower.layers.0.fc1.bias"]
+    y = torch.empty(nb * frames, f, dtype=torch.bfloat16, device=dev)
+    fc1_us = _events_us(lambda: kernels.q8_0_linear(x_ln, fc1, bias=b1, act="gelu", out=y), args.kernel_reps * 4)
+    fc1_tflops = 2.0 * nb * frames * d * f / (fc1_us * 1e-6) / 1e12
+    print(f"[bench] asr step {per_step * 1e3:.1f} ms ({frames_s:.0f} frames/s); encoder {enc_s * 1e3:.2f} ms, "
+          f"{enc_tflops:.1f} TFLOP/s; fc1 {fc1_us:.1f} us {fc1_tflops:.1f} TFLOP/s; tokens {len(transcripts[0])}",
+          file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu_baseline else cpu_baseline_asr(enc, ecfg, frames)
+    line = {
+        "metric": "Qwen3-ASR-shape audio frames/s: 24-layer 1024-wide encoder over 4 x 1500 frames, then a "
+                  "0.6B-shape int4 decoder, 64 greedy tokens per utterance",
+        "value": round(frames_s, 1),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(per_step * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (encoder input frames N(0,1) in bf16; seeded random-init weights: Q8_0 encoder, "
+                "uniform Q4_K decoder)",
+        "config": {
+            "workload": "4 utterances x 1500 frames: encoder (24 layers, hidden 1024, 16 heads, FFN 4096, "
+                        "attention within each utterance) + ln_post/proj1/proj2, then per utterance the audio "
+                        "states injected into a 1507-position prompt, chunked prefill and 64 greedy tokens "
+                        "(Qwen3-0.6B shape, uniform Q4_K, HIP graphs of 8 steps)",
+            "batch": nb, "frames": frames, "decoder_tokens": new_tokens,
+        },
+        "encoder_ms": round(enc_s * 1e3, 3),
+        "encoder_tflops": round(enc_tflops, 1),
+        "mfma_utilisation": round(enc_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm_q_kernel<GemmQ80> (encoder fc1 + bias + GELU, M 6000 K 1024 N 4096)",
+            "achieved": round(fc1_tflops, 1),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(fc1_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "avg_launch_us": round(fc1_us, 1),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def ecfg_audio_id() -> int:
+    from torch2vk_amd.qwen3_asr.config import AUDIO_TOKEN_ID
+
+    return AUDIO_TOKEN_ID
+
+
+def cpu_baseline_asr(enc, ecfg, frames: int) -> dict:
+    """The CPU oracle's encoder layer (weights dequantized from the same Q8_0 bytes) over one 1500-frame
+    utterance, scaled to 24 layers x 4 utterances: encoder frames/s on the host cores."""
+    from dataclasses import replace
+
+    import numpy as np
+    import torch
+
+    from oracle import asr as oasr
+    from torch2vk_amd.qwen3_asr.encoder import PREFIX, audio_tensor_shapes
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    one = replace(ecfg, layers=1)
+    shapes = {k: v for k, v in audio_tensor_shapes(one).items() if ".layers.0." in k}
+    w = oasr.dense_from_packed({k: enc.weights.packed[k].cpu().numpy() for k in shapes if len(shapes[k]) > 1},
+                               {k: enc.weights.vectors[k].cpu().numpy() for k in shapes if len(shapes[k]) == 1},
+                               shapes)
+    h = torch.randn(frames, ecfg.d_model)
+    lp = f"{PREFIX}layers.0."
+    hd = ecfg.head_dim
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        y = torch.nn.functional.layer_norm(h, (ecfg.d_model,), w[lp + "self_attn_layer_norm.weight"],
+                                           w[lp + "self_attn_layer_norm.bias"], eps=ecfg.eps)
+        q, k, v = (y @ w[lp + f"self_attn.{n}.weight"].T + w[lp + f"self_attn.{n}.bias"] for n in
+                   ("q_proj", "k_proj", "v_proj"))
+        q, k, v = (t.reshape(frames, ecfg.heads, hd).transpose(0, 1) for t in (q, k, v))
+        a = oasr.masked_attention(q, k, v, None, hd ** -0.5).transpose(0, 1).reshape(frames, -1)
+        h2 = h + a @ w[lp + "self_attn.out_proj.weight"].T + w[lp + "self_attn.out_proj.bias"]
+        y = torch.nn.functional.layer_norm(h2, (ecfg.d_model,), w[lp + "final_layer_norm.weight"],
+                                           w[lp + "final_layer_norm.bias"], eps=ecfg.eps)
+        y = torch.nn.functional.gelu(y @ w[lp + "fc1.weight"].T + w[lp + "fc1.bias"])
+        _ = h2 + y @ w[lp + "fc2.weight"].T + w[lp + "fc2.bias"]
+        times.append(time.perf_counter() - t0)
+    t_layer = min(times)
+    del np
+    return {
+        "value": round(frames / (ecfg.layers * t_layer), 2),
+        "unit": "frames/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"CPU oracle encoder layer (torch {torch.__version__}, fp32, weights dequantized from the Q8_0 "
+                  f"bytes) over one {frames}-frame utterance (best of 2: {t_layer * 1e3:.0f} ms) x {ecfg.layers} "
+                  f"layers; encoder only, the decoder is not included",
     }
 
 
