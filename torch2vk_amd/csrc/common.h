@@ -16,16 +16,18 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
     return __uint_as_float(bits16 << 16);
 }
 
-// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float v) {
-    uint32_t u = __float_as_uint(v);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+typedef __bf16 t2h_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float t2h_f32x2_t __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16, round to nearest even, on the gfx950 converter
+// (v_cvt_pk_bf16_f32: one instruction per two values, no branch; a NaN stays a NaN).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const t2h_f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, t2h_bf16x2_t));
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float v) {
+    return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)v);
 }
 
 // IEEE binary16 -> fp32 (exact).
