@@ -486,8 +486,7 @@ def bench_prefill(args) -> int:
     kc = torch.empty(nb, tl, c.kv_heads, c.head_dim, dtype=bf, device=dev)
     vc = torch.empty_like(kc)
     attn = torch.empty(nb, tl, c.heads, c.head_dim, dtype=bf, device=dev)
-    gate = torch.empty(m, c.mlp, dtype=f32, device=dev)
-    up = torch.empty_like(gate)
+    up = torch.empty(m, c.mlp, dtype=f32, device=dev)
     act = torch.empty(m, c.mlp, dtype=bf, device=dev)
     ps = torch.empty(512, dtype=f32, device=dev)
     pt = torch.empty(512, dtype=torch.int32, device=dev)
@@ -508,9 +507,7 @@ def bench_prefill(args) -> int:
         kernels.flash_attn_prefill(qb.view(nb, tl, c.heads, c.head_dim), kc, vc, out=attn, causal=True)
         kernels.gemm(attn.view(m, c.q_dim), lw["o"], "q8_0", out=h, residual=h)
         kernels.rms_norm(h, lw["post_norm"], out=x)
-        kernels.gemm(x, lw["gate"], "q8_0", out=gate)
-        kernels.gemm(x, lw["up"], "q8_0", out=up)
-        kernels.swiglu(gate, up, out=act)
+        kernels.gemm_swiglu(x, lw["gate"], lw["up"], "q8_0", out=act)
         kernels.gemm(act, lw["down"], "q8_0", out=h, residual=h)
 
     def step() -> None:
@@ -554,7 +551,7 @@ def bench_prefill(args) -> int:
         "config": {
             "workload": "Qwen3-8B-shape prefill of 8 sequences x 2048 tokens: Q8_0 embedding, 36 layers (RMSNorm, "
                         "q|k|v GEMM, q/k norm + RoPE + KV write, causal flash attention, o GEMM + residual, "
-                        "RMSNorm, gate and up GEMMs, SwiGLU, down GEMM + residual), final norm + Q4_K LM head + "
+                        "RMSNorm, gate|up GEMM with SwiGLU in its epilogue, down GEMM + residual), final norm + Q4_K LM head + "
                         "greedy select of each sequence's first token",
             "batch": nb, "seq_len": tl, "weights": "q8_0",
         },

@@ -138,6 +138,13 @@ int t2h_q8_0_gemm(const void* x, const void* w, void* y, int out_dtype, const fl
  * LLAMA_MATMUL_Q4_K_F32_{M,L} (src/models/optimized_qwen3/shaders/llama_matmul_q4_k_f32.py:32-141); k % 256 == 0. */
 int t2h_q4k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
                  uint32_t k, uint32_t n, void* stream);
+/* y bf16 [m, n_ff] = silu(x . deq(W_gate)^T) * (x . deq(W_up)^T): the prefill MLP's gate and up GEMMs and
+ * the SwiGLU in one launch (each wave's tile columns pair 32 gate rows with the 32 up rows of the same
+ * features).  wtype T2H_WTYPE_Q8_0 / Q4_K / Q6_K, both weights [n_ff, k]; k % 64 == 0 (% 256 for the K
+ * types).  replaces LLAMA_MATMUL_Q4_K_F32_{M,L} x 2 + SWIGLU_F32 (src/models/optimized_qwen3/dispatch/
+ * text_layer.py; src/models/optimized_qwen3/shaders/swiglu_f32.py). */
+int t2h_gemm_swiglu(int wtype, const void* x, const void* w_gate, const void* w_up, void* y, uint32_t m, uint32_t k,
+                    uint32_t n_ff, void* stream);
 /* replaces LLAMA_MATMUL_Q6_K_F32_{M,L} (src/models/optimized_qwen3/shaders/llama_matmul_q6_k_f32.py:27-141):
  * the Q6_K v/down weights of the Q4_K_M more-bits layers; k % 256 == 0, W 2-byte aligned. */
 int t2h_q6k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,

@@ -68,3 +68,24 @@ def test_gemm_rejects_bad_shapes(device):
     y = torch.empty(4, 64, dtype=torch.float32, device=device)
     st = _lib.lib().t2h_q8_0_gemm(x.data_ptr(), w.data_ptr(), y.data_ptr(), 0, None, 4, 1056, 64, None)
     assert st == 2
+
+
+@pytest.mark.parametrize("wtype,m,k,n", [("q8_0", 300, 1024, 520), ("q4_k", 17, 2048, 1024), ("q8_0", 700, 512, 96),
+                                         ("q6_k", 260, 1024, 384), ("q4_k", 1030, 4096, 768)])
+def test_gemm_swiglu_matches_oracle(device, wtype, m, k, n):
+    """Gate and up products with SwiGLU in the epilogue, against silu(x Wg^T) * (x Wu^T) on the bf16 tiles."""
+    from torch2vk_amd import kernels
+
+    print(f"gemm_swiglu {wtype} M={m} K={k} F={n}", flush=True)
+    rng, pg, wg, x = _problem(wtype, m, k, n, m + k)
+    wu = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    pu = getattr(oracle, f"quantize_{wtype}")(wu)
+    wud = getattr(oracle, f"dequant_{wtype}")(pu, k)
+    xd = x.astype(np.float64)
+    g = xd @ R.bf16_round(wg.astype(np.float32)).astype(np.float64).T
+    u = xd @ R.bf16_round(wud.astype(np.float32)).astype(np.float64).T
+    ref = g / (1.0 + np.exp(-g)) * u
+    xt = torch.from_numpy(x).to(device).to(torch.bfloat16)
+    got = kernels.gemm_swiglu(xt, torch.from_numpy(pg).to(device), torch.from_numpy(pu).to(device), wtype)
+    assert_close(got.float().cpu().numpy(), ref, max_abs=8e-3 * np.abs(ref).max() + 1e-6, min_cos=0.9999,
+                 what="gemm_swiglu")

@@ -36,7 +36,7 @@ constexpr int GQ_BK = 64;
 constexpr int GQ_LDS_ROW = GQ_BK + 8;  // bf16 elements per padded LDS row
 constexpr int GQ_GROUP_M = 8;
 
-enum GemmEpilogue { GQEPI_F32 = 0, GQEPI_BF16 = 1, GQEPI_RESID = 2 };
+enum GemmEpilogue { GQEPI_F32 = 0, GQEPI_BF16 = 1, GQEPI_RESID = 2, GQEPI_SWIGLU = 3 };
 
 enum GemmAct { GQACT_NONE = 0, GQACT_GELU = 1 };
 
@@ -51,7 +51,26 @@ struct GemmArgs {
     uint32_t row_bytes;
     uint32_t w_blocks;     // quant blocks per weight row; K columns past them multiply zeros
     uint32_t tiles_m, tiles_n;
+    const uint8_t* w_up;   // GQEPI_SWIGLU: up rows (w holds the gate rows)
+    uint32_t n_ff;         // GQEPI_SWIGLU: features; n = 2 n_ff
 };
+
+// Packed row of B-tile row r (0..255) of the tile at n0.  Plain: weight row
+// n0 + r.  Gated (SwiGLU): each wave's 64 columns are 32 gate rows then the 32
+// up rows of the same features, so the epilogue finds g and u in one lane:
+// feature n0/2 + 32 (r / 64) + r % 32, from gate when (r / 32) is even.
+template <bool GATED>
+__device__ __forceinline__ const uint8_t* gemm_w_row(const GemmArgs& a, uint32_t n0, uint32_t r) {
+    if constexpr (GATED) {
+        uint32_t f = n0 / 2 + (r >> 6) * 32 + (r & 31);
+        f = f < a.n_ff ? f : a.n_ff - 1;
+        return ((r >> 5) & 1 ? a.w_up : a.w) + (size_t)f * a.row_bytes;
+    } else {
+        uint32_t row = n0 + r;
+        row = row < a.n ? row : a.n - 1;
+        return a.w + (size_t)row * a.row_bytes;
+    }
+}
 
 // GELU with the exact erf (the reference's GELU_F32 evaluates erf by
 // Abramowitz-Stegun 7.1.26, |error| < 1.5e-7: src/models/quantized_qwen3_asr/shaders/gelu_f32.py:61-76)
@@ -70,24 +89,25 @@ struct GemmQ80 {
     struct Raw {
         uint4 q0, q1;
         uint32_t d;
+        bool inside;  // false: a block past the row's end, dequantised as zeros
     };
+    template <bool GATED>
     __device__ static __forceinline__ void load(const GemmArgs& a, uint32_t n0, uint32_t k0, Raw& r) {
         const uint32_t t = threadIdx.x;
-        uint32_t row = n0 + (t >> 1);
-        row = row < a.n ? row : a.n - 1;
         // a stage past the row's last block (K padded to the 64-wide stage) reads
         // the last block again with a zero scale
         const uint32_t blk = k0 / 32 + (t & 1);
         const bool inside = blk < a.w_blocks;
-        const uint8_t* p = a.w + (size_t)row * a.row_bytes + (size_t)(inside ? blk : a.w_blocks - 1) * 34;
-        r.d = inside ? load_u16(p) : 0u;
+        const uint8_t* p = gemm_w_row<GATED>(a, n0, t >> 1) + (size_t)(inside ? blk : a.w_blocks - 1) * 34;
+        r.d = load_u16(p);  // unconditional (p is always inside the row) and not
+        r.inside = inside;  // selected here, so nothing waits on the load before its use
         r.q0 = load_u4_ua(p + 2);
         r.q1 = load_u4_ua(p + 18);
     }
     // 32 bf16 values of this thread's block -> LDS row (t >> 1), columns 32 * (t & 1) ...
     __device__ static __forceinline__ void store(const Raw& r, uint16_t* lds_b) {
         const uint32_t t = threadIdx.x;
-        const float d = f16_bits_to_f32(r.d);
+        const float d = r.inside ? f16_bits_to_f32(r.d) : 0.0f;
         const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
         uint32_t o[16];
 #pragma unroll
@@ -116,11 +136,10 @@ struct GemmQ4K {
     struct Raw {
         uint4 hdr, q0, q1;
     };
+    template <bool GATED>
     __device__ static __forceinline__ void load(const GemmArgs& a, uint32_t n0, uint32_t k0, Raw& r) {
         const uint32_t t = threadIdx.x;
-        uint32_t row = n0 + (t >> 1);
-        row = row < a.n ? row : a.n - 1;
-        const uint8_t* p = a.w + (size_t)row * a.row_bytes + (size_t)(k0 / 256) * 144;
+        const uint8_t* p = gemm_w_row<GATED>(a, n0, t >> 1) + (size_t)(k0 / 256) * 144;
         const uint32_t g = (k0 % 256) / 64;
         r.hdr = load_u4(p);
         r.q0 = load_u4(p + 16 + g * 32);
@@ -180,11 +199,10 @@ struct GemmQ6K {
         uint4 ql0, ql1, qh0, qh1;
         uint32_t sc, d;
     };
+    template <bool GATED>
     __device__ static __forceinline__ void load(const GemmArgs& a, uint32_t n0, uint32_t k0, Raw& r) {
         const uint32_t t = threadIdx.x;
-        uint32_t row = n0 + (t >> 1);
-        row = row < a.n ? row : a.n - 1;
-        const uint8_t* blk = a.w + (size_t)row * a.row_bytes + (size_t)(k0 / 256) * 210;
+        const uint8_t* blk = gemm_w_row<GATED>(a, n0, t >> 1) + (size_t)(k0 / 256) * 210;
         const uint32_t h = (k0 % 256) / 128;
         const uint32_t p = (k0 % 128) / 32 + (t & 1);
         const uint8_t* ql = blk + 64 * h + 32 * (p & 1);
@@ -236,7 +254,7 @@ __device__ __forceinline__ void store_w(const typename F::Raw& r, uint16_t* lds_
 // ---------------------------------------------------------------- kernel --
 
 // MI = 32-row MFMA tiles per wave down M: 4 gives 256 x 256 block tiles, 2
-// gives 128 x 256 for problems with too few 256-row tiles to fill the chip.
+// gives 128 x 256 for problems with few 256-row tiles.
 template <class F, int EPI, int MI>
 __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
     constexpr int GQ_BM = 64 * MI;
@@ -274,7 +292,7 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
             row = row < a.m ? row : a.m - 1;
             ra[i] = load_u4(a.a + (size_t)row * a.k + k0 + (c & 7) * 8);
         }
-        F::load(a, n0, k0, rw);
+        F::template load<EPI == GQEPI_SWIGLU>(a, n0, k0, rw);
     };
     auto store_stage = [&](uint32_t kt, int s) {
 #pragma unroll
@@ -293,15 +311,18 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
+    // Stage kt + 1's global loads are issued right after stage kt's LDS store,
+    // before the barrier, so they are in flight through the barrier and all of
+    // stage kt's matrix work.
     load_stage(0);
     store_stage(0, 0);
+    if (KT > 1) load_stage(1);
     __syncthreads();
 
     const int frag_row = lane & 31;
     const int frag_k = (lane >> 5) * 8;
     for (uint32_t kt = 0; kt < KT; ++kt) {
         const int s = kt & 1;
-        if (kt + 1 < KT) load_stage(kt + 1);
         const uint16_t* sa = lds_a[s] + (wm * 32 * MI + frag_row) * GQ_LDS_ROW + frag_k;
         const uint16_t* sb = lds_b[s] + (wn * 64 + frag_row) * GQ_LDS_ROW + frag_k;
 #pragma unroll
@@ -320,12 +341,31 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
         if (kt + 1 < KT) store_stage(kt + 1, s ^ 1);
+        if (kt + 2 < KT) load_stage(kt + 2);
         __syncthreads();
     }
 
     // epilogue: lane holds column (lane % 32) of each 32x32 tile, rows 8(e/4) + 4(lane/32) + e%4
     const uint32_t col_base = n0 + wn * 64 + (lane & 31);
     const uint32_t row_base = m0 + wm * 32 * MI + (lane >> 5) * 4;
+    if constexpr (EPI == GQEPI_SWIGLU) {
+        // tile column j = 0 holds gate, j = 1 up, of feature f
+        const uint32_t f = n0 / 2 + wn * 32 + (lane & 31);
+        if (f >= a.n_ff) return;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t row = row_base + i * 32 + (e >> 2) * 8 + (e & 3);
+                if (row < a.m) {
+                    const float g = acc[i][0][e];
+                    reinterpret_cast<uint16_t*>(a.c)[(size_t)row * a.n_ff + f] =
+                        (uint16_t)f32_to_bf16_bits(g / (1.0f + expf(-g)) * acc[i][1][e]);
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const uint32_t col = col_base + j * 32;
@@ -356,9 +396,10 @@ template <class F, int EPI>
 static void gemm_q_dispatch(GemmArgs a, hipStream_t s) {
     const dim3 block(GQ_THREADS);
     a.tiles_n = (a.n + GQ_BN - 1) / GQ_BN;
-    // 256-row tiles unless that leaves most of the 256 CUs idle
+    // 256-row tiles for big grids; below ~4 tiles per CU the 128-row tile's
+    // finer load balance wins over the bigger tile's operand reuse (measured)
     const uint32_t tiles_256 = (a.m + 255) / 256 * a.tiles_n;
-    if (tiles_256 < 256 && a.m > 128) {
+    if (tiles_256 < 1024 && a.m > 128) {
         a.tiles_m = (a.m + 127) / 128;
         hipLaunchKernelGGL((gemm_q_kernel<F, EPI, 2>), dim3(a.tiles_m * a.tiles_n), block, 0, s, a);
     } else {
@@ -437,4 +478,42 @@ extern "C" int t2h_q8_0_linear(const void* x, const void* w, const float* bias, 
 extern "C" int t2h_q6k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
                             uint32_t k, uint32_t n, void* stream) {
     return gemm_q_launch<GemmQ6K>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
+}
+
+// y[m, n_ff] = bf16(silu(x . deq(W_gate)^T) * (x . deq(W_up)^T)): the prefill MLP's gate and up products
+// in one launch, SwiGLU applied in the epilogue (no fp32 gate/up intermediates).
+template <class F>
+static int gemm_swiglu_launch(const void* x, const void* w_gate, const void* w_up, void* y, uint32_t m, uint32_t k,
+                              uint32_t n_ff, void* stream) {
+    if (!x || !w_gate || !w_up || !y) return T2H_ERR_NULL;
+    if (k == 0 || k % GQ_BK != 0 || k % F::BLOCK_VALUES != 0) return T2H_ERR_SHAPE;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) return T2H_ERR_ALIGN;
+    if (((reinterpret_cast<uintptr_t>(w_gate) | reinterpret_cast<uintptr_t>(w_up)) & (F::ALIGN - 1)) != 0)
+        return T2H_ERR_ALIGN;
+    if (n_ff > 0x3fffffffu) return T2H_ERR_SHAPE;
+    if (m == 0 || n_ff == 0) return T2H_OK;
+    GemmArgs a = {};
+    a.a = reinterpret_cast<const uint16_t*>(x);
+    a.w = reinterpret_cast<const uint8_t*>(w_gate);
+    a.w_up = reinterpret_cast<const uint8_t*>(w_up);
+    a.c = y;
+    a.m = m;
+    a.k = k;
+    a.n_ff = n_ff;
+    a.n = 2 * n_ff;
+    a.w_blocks = k / F::BLOCK_VALUES;
+    a.row_bytes = a.w_blocks * F::BLOCK_BYTES;
+    gemm_q_dispatch<F, GQEPI_SWIGLU>(a, reinterpret_cast<hipStream_t>(stream));
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+extern "C" int t2h_gemm_swiglu(int wtype, const void* x, const void* w_gate, const void* w_up, void* y, uint32_t m,
+                               uint32_t k, uint32_t n_ff, void* stream) {
+    switch (wtype) {
+        case T2H_WTYPE_Q8_0: return gemm_swiglu_launch<GemmQ80>(x, w_gate, w_up, y, m, k, n_ff, stream);
+        case T2H_WTYPE_Q4_K: return gemm_swiglu_launch<GemmQ4K>(x, w_gate, w_up, y, m, k, n_ff, stream);
+        case T2H_WTYPE_Q6_K: return gemm_swiglu_launch<GemmQ6K>(x, w_gate, w_up, y, m, k, n_ff, stream);
+        default: return T2H_ERR_DTYPE;
+    }
 }

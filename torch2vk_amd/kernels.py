@@ -291,6 +291,29 @@ def gemm(x: torch.Tensor, w: torch.Tensor, wtype: str, *, out: torch.Tensor | No
     return out
 
 
+def gemm_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, wtype: str, *,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 [M, F] = silu(x . deq(W_gate)^T) * (x . deq(W_up)^T) in one matrix-core launch (the prefill MLP's
+    gate and up GEMMs with SwiGLU in the epilogue); x bf16 [M, K], both weights [F, K] of type ``wtype``."""
+    if wtype not in ("q8_0", "q4_k", "q6_k"):
+        raise ValueError(f"gemm_swiglu handles q8_0, q4_k and q6_k weights, got {wtype!r}")
+    _check(x, "x", torch.bfloat16)
+    k = int(x.shape[-1])
+    if k % 64:
+        raise ValueError(f"gemm_swiglu needs K % 64 == 0, got {k}")
+    m = x.numel() // k
+    n = _check_packed(w_gate, "w_gate", wtype, k)
+    if _check_packed(w_up, "w_up", wtype, k) != n:
+        raise ValueError("w_gate and w_up must have the same number of rows")
+    if out is None:
+        out = torch.empty(*x.shape[:-1], n, dtype=torch.bfloat16, device=x.device)
+    _check(out, "output", torch.bfloat16, align=2)
+    if out.numel() != m * n:
+        raise ValueError(f"output has {out.numel()} elements, expected {m * n}")
+    call("t2h_gemm_swiglu", WTYPES[wtype], ptr(x), ptr(w_gate), ptr(w_up), ptr(out), m, k, n, stream_handle())
+    return out
+
+
 def qk_norm_rope_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out: torch.Tensor,
                        k_cache: torch.Tensor, v_cache: torch.Tensor, start: int, *,
                        q_norm_weight: torch.Tensor | None = None, k_norm_weight: torch.Tensor | None = None,

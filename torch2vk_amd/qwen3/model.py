@@ -306,8 +306,8 @@ class Qwen3Decoder:
     def _prefill_layer(self, i: int, h: torch.Tensor, start: int) -> None:
         """One layer over a chunk's fp32 residual stream h [n, hidden] at positions start.. (run_text_layer,
         src/models/optimized_qwen3/dispatch/text_layer.py): RMSNorm rows -> q|k|v GEMM -> q/k norm + RoPE +
-        KV cache write -> causal flash attention over the cache -> o GEMM + residual -> RMSNorm -> gate, up
-        GEMMs -> SwiGLU -> down GEMM + residual.  GEMMs run on the matrix cores for any chunk length."""
+        KV cache write -> causal flash attention over the cache -> o GEMM + residual -> RMSNorm -> gate|up
+        GEMM with SwiGLU in its epilogue -> down GEMM + residual.  GEMMs run on the matrix cores for any chunk length."""
         c, t, p = self.config, self.types, f"layers.{i}."
         n = h.shape[0]
         x = kernels.rms_norm(h, self._n(p + "input_norm"), out=torch.empty(n, c.hidden, dtype=torch.bfloat16,
@@ -327,10 +327,13 @@ class Qwen3Decoder:
         attn = kernels.flash_attn_prefill(qb.unsqueeze(0), keys, vals, causal=True, causal_offset=start)
         kernels.gemm(attn.view(n, c.q_dim), self._w(p + "o"), t[p + "o"], out=h, residual=h)
         x = kernels.rms_norm(h, self._n(p + "post_norm"), out=x, eps=c.rms_eps)
-        gate = kernels.gemm(x, self._w(p + "gate"), t[p + "gate"], out_dtype=torch.float32)
-        up = kernels.gemm(x, self._w(p + "up"), t[p + "up"], out_dtype=torch.float32)
-        act = kernels.swiglu(gate, up)
-        del gate, up
+        if t[p + "gate"] == t[p + "up"]:
+            act = kernels.gemm_swiglu(x, self._w(p + "gate"), self._w(p + "up"), t[p + "gate"])
+        else:
+            gate = kernels.gemm(x, self._w(p + "gate"), t[p + "gate"], out_dtype=torch.float32)
+            up = kernels.gemm(x, self._w(p + "up"), t[p + "up"], out_dtype=torch.float32)
+            act = kernels.swiglu(gate, up)
+            del gate, up
         kernels.gemm(act, self._w(p + "down"), t[p + "down"], out=h, residual=h)
 
     def prefill_chunked(self, prompt_ids: torch.Tensor | None = None, *, embeds: torch.Tensor | None = None,
