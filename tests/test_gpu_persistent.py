@@ -1,5 +1,6 @@
 """The persistent decode-layers kernel (t2h_qwen3_decode_layers) against the one-launch-per-op path
-and the CPU oracle, at the Qwen3-8B layer shape (hidden 4096, MLP 12288, 32/8 heads) with 2 layers."""
+and the CPU oracle, at the Qwen3-8B layer shape (hidden 4096, MLP 12288, 32/8 heads) and the Qwen3-0.6B
+layer shape (hidden 1024, MLP 3072, 16/8 heads), 2 layers each."""
 
 from __future__ import annotations
 
@@ -15,12 +16,13 @@ from oracle.reference import Qwen3Shape
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def setup_8b2(device):
-    from torch2vk_amd.qwen3.config import QWEN3_8B
-    from torch2vk_amd.qwen3.weights import matrix_shapes, synthetic_weights
+@pytest.fixture(scope="module", params=["8b", "0.6b"])
+def setup_8b2(device, request):
+    from torch2vk_amd.qwen3.config import QWEN3_0_6B, QWEN3_8B
+    from torch2vk_amd.qwen3.weights import synthetic_weights
 
-    cfg = replace(QWEN3_8B, layers=2, vocab=4096, eos_token_ids=(4095,))
+    base = QWEN3_8B if request.param == "8b" else QWEN3_0_6B
+    cfg = replace(base, layers=2, vocab=4096, eos_token_ids=(4095,))
     w = synthetic_weights(cfg, device=device, seed=7, std=0.02, norm_std=0.1)
     shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
                        head_dim=cfg.head_dim, mlp=cfg.mlp, vocab=cfg.vocab, rope_theta=cfg.rope_theta)
@@ -30,7 +32,10 @@ def setup_8b2(device):
 # Workspace layout of decode_layers.hip: 256 B launch counter, then q|k|v as (fp32, u32 epoch) words,
 # then the attention output as (bf16, u16 epoch) words.
 WS_QKV = 256
-WS_ATTN = WS_QKV + 6144 * 8
+
+
+def _ws_attn(cfg) -> int:
+    return WS_QKV + (cfg.q_dim + 2 * cfg.kv_dim) * 8
 
 
 def _ws_ll32(dec, offset, n):
@@ -70,9 +75,9 @@ def test_persistent_layer_matches_per_op(device, setup_8b2, pos):
     b.run_decode_layer(0)
     torch.cuda.synchronize()
     a.check_status()
-    qkv = _ws_ll32(a, WS_QKV, 6144)
+    qkv = _ws_ll32(a, WS_QKV, cfg.q_dim + 2 * cfg.kv_dim)
     torch.testing.assert_close(qkv, torch.cat([b.q, b.k, b.v]), rtol=0, atol=0)
-    attn = _ws_ll16(a, WS_ATTN, 4096).float()
+    attn = _ws_ll16(a, _ws_attn(cfg), cfg.q_dim).float()
     ref = b.attn.float()
     assert (attn - ref).abs().max().item() <= 2 ** -7 * ref.abs().max().item()
     torch.testing.assert_close(a.k_cache[0], b.k_cache[0], rtol=0, atol=0)
@@ -113,8 +118,10 @@ def test_persistent_decode_matches_oracle(device, setup_8b2):
     dec = Qwen3Decoder(w, max_positions=128, max_new_tokens=16, persistent=True)
     dec.stop_on_eos = False
     toks = dec.generate(torch.tensor(prompt), 10, steps_per_graph=4, use_graph=True)
-    print(f"persistent 8B-shape decode: {toks}", flush=True)
-    print(check_greedy_tokens(shape, dense, prompt, toks, tie_tol=2e-3))
+    print(f"persistent {cfg.name}-shape decode: {toks}", flush=True)
+    # near-tie tolerance: bf16 activation rounding moves the 0.6B shape's smaller logits by a few 1e-3
+    tie = 2e-3 if cfg.hidden == 4096 else 5e-3
+    print(check_greedy_tokens(shape, dense, prompt, toks, tie_tol=tie))
 
 
 def test_persistent_graph_replay_equals_eager(device, setup_8b2):

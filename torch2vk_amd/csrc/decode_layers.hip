@@ -1,5 +1,7 @@
 // Persistent decode kernel: every transformer layer of one Qwen3 decode token
-// in one launch (uniform Q4_K weights, bf16 KV cache, batch 1).
+// in one launch (uniform Q4_K weights, bf16 KV cache, batch 1).  Built for the
+// Qwen3-8B shape (hidden 4096, MLP 12288, 32/8 heads) and the Qwen3-0.6B shape
+// (hidden 1024, MLP 3072, 16/8 heads); head_dim 128 and 8 kv heads in both.
 //
 // Replaces the per-layer dispatch sequence of the reference's decode step,
 // run_decode_layer(rt, layer_idx, cache_position=...) for every layer
@@ -69,8 +71,9 @@ constexpr uint32_t DL_SPIN_LIMIT = 1u << 14;
 #endif   // polls before a consumer gives up (~16 ms)
 
 // Per-layer pointer table (device memory, DL_LAYER_PTRS uint64 per layer).
-// DL_WQ points at the q, k and v rows stacked contiguously (6144 rows); DL_WK and
-// DL_WV must point inside it at rows 4096 and 5120 (checked by the host).
+// DL_WQ points at the q, k and v rows stacked contiguously (q_dim + 2 kv_dim
+// rows); DL_WK and DL_WV must point inside it at rows q_dim and q_dim + kv_dim
+// (checked by the host).
 enum DlLayerPtr {
     DL_WQ = 0, DL_WK, DL_WV, DL_WO, DL_WGATE, DL_WUP, DL_WDOWN,
     DL_IN_NORM, DL_POST_NORM, DL_Q_NORM, DL_K_NORM, DL_K_CACHE, DL_V_CACHE,
@@ -157,42 +160,73 @@ __device__ __forceinline__ void ll_wait(uint64_t (&w)[N], Addr addr, Ok ok, uint
     }
 }
 
+template <int GROUP>
 struct DlAttnLds {
-    float qs[4][4][36];                 // GROUP=4 q heads x 4 quarters x (32 dims + pad)
-    float4 ps4[DL_WAVES][DL_ATT_POS];   // exp(score - m) per wave and position, one float per q head
-    float wml[DL_WAVES][4][2];
-    float2 wo[DL_WAVES][4][64];
+    float qs[GROUP][4][36];                // q heads x 4 quarters x (32 dims + pad)
+    float ps[DL_WAVES][DL_ATT_POS][GROUP]; // exp(score - m) per wave, position and q head
+    float wml[DL_WAVES][GROUP][2];
+    float2 wo[DL_WAVES][GROUP][64];
     uint16_t knew[DL_D];
 };
 
-constexpr int DL_HSB = 16;   // hidden 4096 = 16 superblocks
-constexpr int DL_MSB = 48;   // MLP 12288 = 48 superblocks
-constexpr int DL_HID = DL_HSB * 256;
-constexpr int DL_MLP = DL_MSB * 256;
-constexpr int DL_QKV_ROWS = 32 * DL_D + 2 * 8 * DL_D;  // 6144
+constexpr int dl_max3(int a, int b, int c) { return a > b ? (a > c ? a : c) : (b > c ? b : c); }
 
+// Model shape (8 kv heads of 128) and, per GEMV phase, the units per wave, the
+// ring depth and the units issued before the input is awaited.
+template <int HSB_, int MSB_, int NH_, int QKV_U, int QKV_R, int QKV_P, int O_U, int O_R, int O_P, int GU_U,
+          int GU_R, int GU_P, int DN_U, int DN_R, int DN_P>
+struct DlShape {
+    static constexpr int HSB = HSB_;             // hidden / 256 (superblocks)
+    static constexpr int MSB = MSB_;             // MLP / 256
+    static constexpr int NH = NH_;               // q heads
+    static constexpr int NK = 8;                 // kv heads
+    static constexpr int GROUP = NH / NK;
+    static constexpr int QSB = NH * DL_D / 256;  // q_dim / 256: the o_proj row length
+    static constexpr int HID = HSB * 256, MLP = MSB * 256, QD = NH * DL_D, KVD = NK * DL_D;
+    static constexpr int QKV_ROWS = QD + 2 * KVD;
+    static constexpr int KMAX = dl_max3(HID, MLP, QD);
+    static constexpr int qkv_u = QKV_U, qkv_r = QKV_R, qkv_p = QKV_P, o_u = O_U, o_r = O_R, o_p = O_P;
+    static constexpr int gu_u = GU_U, gu_r = GU_R, gu_p = GU_P, dn_u = DN_U, dn_r = DN_R, dn_p = DN_P;
+    static_assert(NH % NK == 0 && NH / NK <= 4, "GQA group of 1..4 q heads");
+};
+using DlQwen3_8B = DlShape<16, 48, 32, 3, 3, DL_PRE_QKV, 2, 2, DL_PRE_O, 6, 3, DL_PRE_GU, 2, 2, DL_PRE_DOWN>;
+using DlQwen3_0_6B = DlShape<4, 12, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1>;
+
+constexpr int DL_HOLD = 4;  // residual rows a wave owns in one phase, at most
+
+template <class S>
 union DlShared {
     struct {
-        uint32_t xp[xp_words(DL_MLP)];
-        float xsum[DL_MLP / 32];
+        uint32_t xp[xp_words(S::KMAX)];
+        float xsum[S::KMAX / 32];
         float red[DL_WAVES];
-        float hold[DL_WAVES * 4];  // residual epilogue: the old h of the block's rows [wave][unit]
+        float hold[DL_WAVES * DL_HOLD];  // residual epilogue: the old h of the block's rows [wave][row]
     } g;
-    DlAttnLds at;
+    DlAttnLds<S::GROUP> at;
 };
 
 // ------------------------------------------------------------ GEMV phase ----
 
-// Weights of one unit (one row of each of NG row groups), K = NSB*256: the
-// header and the two 16-B nibble chunks of this lane's superblock per
-// 16-superblock step.
+// Weights of one unit, K = NSB*256: RPW consecutive rows of each of NG row
+// groups, streamed in NIT steps of 16 superblocks; per step a lane holds the
+// header and the two 16-B nibble chunks of superblock (step * 16 + lane / 4) of
+// the unit (row = that / NSB).  RPW = 1 for rows of 16, 32, 48 superblocks.
 template <int NSB, int NG>
 struct DlUnit {
-    static constexpr int NIT = NSB / 16;
+    static constexpr int RPW = 16 / cgcd(NSB, 16);
+    static constexpr int NIT = NSB * RPW / 16;
     uint4 hdr[NG][NIT];
     uint4 q0[NG][NIT];
     uint4 q1[NG][NIT];
 };
+
+// Unit i of wave `wave` of this block.  Block-major when every wave has a unit;
+// SPREAD (fewer units than waves): across the blocks first, so that every CU
+// streams a share.
+template <bool SPREAD>
+__device__ __forceinline__ uint32_t dl_unit(uint32_t wave, uint32_t i) {
+    return SPREAD ? wave * DL_BLOCKS + blockIdx.x + i * DL_NW : blockIdx.x * DL_WAVES + wave + i * DL_NW;
+}
 
 // Row pointers of a GEMV phase: NG == 2 reads row `row` of w0 and w1.
 struct DlRows {
@@ -202,19 +236,21 @@ struct DlRows {
 };
 
 template <int NSB, int NG>
-__device__ __forceinline__ void dl_issue_unit(DlUnit<NSB, NG>& u, const DlRows& r, uint32_t row) {
+__device__ __forceinline__ void dl_issue_unit(DlUnit<NSB, NG>& u, const DlRows& r, uint32_t unit) {
     constexpr int ROW_BYTES = NSB * 144;
+    constexpr int RPW = DlUnit<NSB, NG>::RPW;
     const int lane = dl_tid() & 63;
     const int sbo = lane >> 2;
     const int g = lane & 3;
-    row = row < r.n_rows ? row : r.n_rows - 1;
 #pragma unroll
     for (int gi = 0; gi < NG; ++gi) {
-        const uint8_t* base;
-        base = (gi == 0 ? r.w0 : r.w1) + (size_t)row * ROW_BYTES;
 #pragma unroll
         for (int it = 0; it < DlUnit<NSB, NG>::NIT; ++it) {
-            const uint8_t* p = base + (size_t)(it * 16 + sbo) * 144;
+            const int sbu = it * 16 + sbo;  // superblock of the unit
+            uint32_t row = unit * RPW + (RPW == 1 ? 0 : sbu / NSB);
+            row = row < r.n_rows ? row : r.n_rows - 1;
+            const uint8_t* p = (gi == 0 ? r.w0 : r.w1) + (size_t)row * ROW_BYTES +
+                               (size_t)(RPW == 1 ? sbu : sbu % NSB) * 144;
             u.hdr[gi][it] = load_u4(p);
             u.q0[gi][it] = load_u4(p + 16 + g * 32);
             u.q1[gi][it] = load_u4(p + 32 + g * 32);
@@ -229,15 +265,26 @@ enum DlSrc {
     DL_SRC_LL16,       // bf16 + epoch16 words
 };
 
-// The old h of the block's rows for a residual epilogue: thread t < 8 upw
-// fetches row (blockIdx.x * 8 + t / upw) + (t % upw) * DL_NW into lds[t].
+// The old h of the block's rows for a residual epilogue: thread t < 8 upw rpw
+// fetches row r = t % rpw of unit (t / rpw) % upw of wave t / (upw rpw) into
+// lds[t].
 struct DlHold {
     int kind;         // DL_SRC_PLAIN or DL_SRC_LL32; < 0: no residual
     const void* src;
     uint32_t e;
     float* lds;
     int upw;
+    int rpw;
+    bool spread;      // the phase's unit mapping (dl_unit)
+    uint32_t n_rows;
 };
+
+__device__ __forceinline__ uint32_t dl_hold_row(const DlHold& hd, int t) {
+    const uint32_t w = (uint32_t)(t / (hd.upw * hd.rpw)), i = (uint32_t)((t / hd.rpw) % hd.upw);
+    const uint32_t unit = hd.spread ? dl_unit<true>(w, i) : dl_unit<false>(w, i);
+    const uint32_t row = unit * (uint32_t)hd.rpw + (uint32_t)(t % hd.rpw);
+    return row < hd.n_rows ? row : hd.n_rows - 1;
+}
 
 // Stage x (K values) in LDS as fp16 pair words + sub-block sums.  RMSNORM:
 // x = bf16(h * rsqrt(mean(h^2) + eps) * w); otherwise x = bf16(src).  The
@@ -246,28 +293,33 @@ template <int K, bool RMSNORM>
 __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red, int src_kind, const void* src,
                                            uint32_t e, const float* norm_w, float eps, const DlHold& hd,
                                            uint32_t* status) {
-    constexpr int PT = K / (4 * DL_THREADS);
-    static_assert(K % (4 * DL_THREADS) == 0, "K must fill the block");
+    // PT float4 per thread; when K does not fill the block, the threads past
+    // K/4 in the last step (whole waves, as K % 256 == 0) re-read element 0
+    // and stage nothing
+    constexpr int PT = (K + 4 * DL_THREADS - 1) / (4 * DL_THREADS);
+    constexpr bool FULL = K % (4 * DL_THREADS) == 0;
+    static_assert(K % 256 == 0, "K in whole superblocks");
     const int tid = dl_tid();
+    auto valid = [&](int j) { return FULL || (j * DL_THREADS + tid) * 4 < K; };
+    auto elem = [&](int j) { return valid(j) ? (j * DL_THREADS + tid) * 4 : 0; };
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool has_hold = hd.kind >= 0 && tid < DL_WAVES * hd.upw;
-    const uint64_t* hold_ll = reinterpret_cast<const uint64_t*>(hd.src) +
-                              (has_hold ? (blockIdx.x * DL_WAVES + tid / hd.upw) + (tid % hd.upw) * DL_NW : 0);
+    const bool has_hold = hd.kind >= 0 && tid < DL_WAVES * hd.upw * hd.rpw;
+    const uint32_t hold_row = has_hold ? dl_hold_row(hd, tid) : 0u;
+    const uint64_t* hold_ll = reinterpret_cast<const uint64_t*>(hd.src) + hold_row;
     const bool hold_ll_wait = has_hold && hd.kind == DL_SRC_LL32;
     float hold = 0.0f;
-    if (has_hold && hd.kind == DL_SRC_PLAIN)
-        hold = reinterpret_cast<const float*>(hd.src)[(blockIdx.x * DL_WAVES + tid / hd.upw) + (tid % hd.upw) * DL_NW];
+    if (has_hold && hd.kind == DL_SRC_PLAIN) hold = reinterpret_cast<const float*>(hd.src)[hold_row];
     float4 hv[PT];
     if (src_kind == DL_SRC_PLAIN) {
         const float* x = reinterpret_cast<const float*>(src);
 #pragma unroll
-        for (int j = 0; j < PT; ++j) hv[j] = *reinterpret_cast<const float4*>(x + (j * DL_THREADS + tid) * 4);
+        for (int j = 0; j < PT; ++j) hv[j] = *reinterpret_cast<const float4*>(x + elem(j));
     } else if (src_kind == DL_SRC_LL32) {
         const uint64_t* x = reinterpret_cast<const uint64_t*>(src);
         uint64_t w[4 * PT];
-        ll_wait(w, [&](int i) { return x + ((i / 4) * DL_THREADS + tid) * 4 + (i % 4); },
-                [&](int, uint64_t v) { return ll_ok32(v, e); }, status);
+        ll_wait(w, [&](int i) { return x + elem(i / 4) + (i % 4); }, [&](int, uint64_t v) { return ll_ok32(v, e); },
+                status);
 #pragma unroll
         for (int j = 0; j < PT; ++j)
             hv[j] = make_float4(ll_val32(w[4 * j]), ll_val32(w[4 * j + 1]), ll_val32(w[4 * j + 2]),
@@ -278,8 +330,7 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
         uint64_t w[2 * PT + 1];
         ll_wait(w,
                 [&](int i) {
-                    return i < 2 * PT ? x + ((i / 2) * DL_THREADS + tid) * 2 + (i % 2)
-                                      : (hold_ll_wait ? hold_ll : x + tid * 2);
+                    return i < 2 * PT ? x + elem(i / 2) / 2 + (i % 2) : (hold_ll_wait ? hold_ll : x + elem(0) / 2);
                 },
                 [&](int i, uint64_t v) {
                     return i < 2 * PT || !hold_ll_wait ? ll_ok16x2(v, e) : ll_ok32(v, hd.e);
@@ -294,10 +345,13 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
         if (hold_ll_wait) hold = ll_val32(w[2 * PT]);
     }
     if (has_hold) hd.lds[tid] = hold;
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+        if (!valid(j)) hv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if constexpr (RMSNORM) {
         float4 wv[PT];
 #pragma unroll
-        for (int j = 0; j < PT; ++j) wv[j] = *reinterpret_cast<const float4*>(norm_w + (j * DL_THREADS + tid) * 4);
+        for (int j = 0; j < PT; ++j) wv[j] = *reinterpret_cast<const float4*>(norm_w + elem(j));
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < PT; ++j) {
@@ -315,6 +369,7 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
         const float inv = 1.0f / sqrtf(total / (float)K + eps);
 #pragma unroll
         for (int j = 0; j < PT; ++j) {
+            if (!valid(j)) continue;
             const int k = (j * DL_THREADS + tid) * 4;
             stage_x4(xp, xsum, k, bf16_round(hv[j].x * inv * wv[j].x), bf16_round(hv[j].y * inv * wv[j].y),
                      bf16_round(hv[j].z * inv * wv[j].z), bf16_round(hv[j].w * inv * wv[j].w));
@@ -322,6 +377,7 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
     } else {
 #pragma unroll
         for (int j = 0; j < PT; ++j) {
+            if (!valid(j)) continue;
             const int k = (j * DL_THREADS + tid) * 4;
             stage_x4(xp, xsum, k, bf16_round(hv[j].x), bf16_round(hv[j].y), bf16_round(hv[j].z),
                      bf16_round(hv[j].w));
@@ -336,24 +392,36 @@ enum DlEpi { DL_EPI_STORE = 0, DL_EPI_RESID = 1, DL_EPI_SWIGLU = 2 };
 // live at a time.
 template <int NSB, int NG>
 __device__ __forceinline__ void dl_dot_unit(const DlUnit<NSB, NG>& u, const uint32_t* xp, const float* xsum,
-                                            const Q4LaneConsts& lc, float (&res)[NG]) {
+                                            const Q4LaneConsts& lc, float (&res)[NG][DlUnit<NSB, NG>::RPW]) {
     constexpr int NIT = DlUnit<NSB, NG>::NIT;
+    constexpr int RPW = DlUnit<NSB, NG>::RPW;
     const int lane = dl_tid() & 63;
     const int sbo = lane >> 2;
     const int g = lane & 3;
-    float acc[NG];
+    float acc[NG][RPW];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
+        const int sbu = it * 16 + sbo;
         XSlice16 xs;
-        load_xslice16(xp, xsum, it * 16 + sbo, g, xs);
+        load_xslice16(xp, xsum, RPW == 1 ? sbu : sbu % NSB, g, xs);
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
             const float c = q4k_lane_dot(u.hdr[gi][it], u.q0[gi][it], u.q1[gi][it], xs, lc);
-            acc[gi] = it == 0 ? c : acc[gi] + c;
+            if constexpr (RPW == 1) {
+                acc[gi][0] = it == 0 ? c : acc[gi][0] + c;
+            } else {
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const float v = sbu / NSB == r ? c : 0.0f;
+                    acc[gi][r] = it == 0 ? v : acc[gi][r] + v;
+                }
+            }
         }
     }
 #pragma unroll
-    for (int gi = 0; gi < NG; ++gi) res[gi] = wave_sum(acc[gi]);
+    for (int gi = 0; gi < NG; ++gi)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) res[gi][r] = wave_sum(acc[gi][r]);
 }
 
 // Where a phase's output goes.
@@ -366,20 +434,26 @@ struct DlOut {
 };
 
 //   STORE: y[row] = dot;  RESID: y[row] = h_old[row] + dot;  SWIGLU: y[row] = bf16(silu(g) * u)
-template <int NG, int EPI>
-__device__ __forceinline__ void dl_store_row(const DlOut& o, uint32_t row, uint32_t n_rows, const float (&res)[NG],
-                                             const float* hold) {
-    if ((dl_tid() & 63) == 0 && row < n_rows) {
-        if constexpr (EPI == DL_EPI_STORE) {
-            ll_put32(o.ll32 + row, res[0], o.e_out);
-        } else if constexpr (EPI == DL_EPI_RESID) {
-            const float old = *hold;
-            if (o.plain != nullptr)
-                o.plain[row] = old + res[0];
-            else
-                ll_put32(o.ll32 + row, old + res[0], o.e_out);
-        } else {
-            ll_put16(o.ll16 + row, silu(res[0]) * res[NG - 1], o.e_out);
+// for the RPW rows of one unit.
+template <int NG, int RPW, int EPI>
+__device__ __forceinline__ void dl_store_unit(const DlOut& o, uint32_t unit, uint32_t n_rows,
+                                              const float (&res)[NG][RPW], const float* hold) {
+    if ((dl_tid() & 63) == 0) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const uint32_t row = unit * RPW + r;
+            if (row >= n_rows) break;
+            if constexpr (EPI == DL_EPI_STORE) {
+                ll_put32(o.ll32 + row, res[0][r], o.e_out);
+            } else if constexpr (EPI == DL_EPI_RESID) {
+                const float old = hold[r];
+                if (o.plain != nullptr)
+                    o.plain[row] = old + res[0][r];
+                else
+                    ll_put32(o.ll32 + row, old + res[0][r], o.e_out);
+            } else {
+                ll_put16(o.ll16 + row, silu(res[0][r]) * res[NG - 1][r], o.e_out);
+            }
         }
     }
 }
@@ -393,31 +467,46 @@ __device__ __forceinline__ void dl_store_row(const DlOut& o, uint32_t row, uint3
 // Unit i + R is issued right after unit i has been reduced.  The loop is
 // unrolled, so the ring is static registers, and the scheduling fences keep
 // each refill after the reduction that frees its registers.
-template <int NSB, int NG, int UPW, int R, int PRE, int EPI, bool RMSNORM>
-__device__ __forceinline__ void dl_gemv_phase(DlShared& sm, const DlRows& rows, uint32_t wrow, int src_kind,
-                                              const void* x_src, uint32_t e_x, const float* norm_w, float eps,
-                                              const DlOut& out, uint32_t* status) {
+// SPREAD: fewer units than waves (dl_unit); a wave without a unit issues and
+// stores nothing.
+template <int NSB, int NG, int UPW, int R, int PRE, int EPI, bool RMSNORM, bool SPREAD, class SH>
+__device__ __forceinline__ void dl_gemv_phase(SH& sm, const DlRows& rows, int src_kind, const void* x_src,
+                                              uint32_t e_x, const float* norm_w, float eps, const DlOut& out,
+                                              uint32_t* status) {
     static_assert(PRE >= 1 && PRE <= R && R <= UPW, "ring size");
+    constexpr int RPW = DlUnit<NSB, NG>::RPW;
+    static_assert(EPI != DL_EPI_RESID || UPW * RPW <= DL_HOLD, "residual rows per wave");
+    static_assert(!SPREAD || UPW == 1, "spread phases have one unit per wave");
+    const int wave = __builtin_amdgcn_readfirstlane(dl_tid() >> 6);
+    const uint32_t n_units = (rows.n_rows + RPW - 1) / RPW;
+    const bool active = !SPREAD || dl_unit<SPREAD>(wave, 0) < n_units;  // wave-uniform
     DlUnit<NSB, NG> u[UPW];
+    if (active) {
 #pragma unroll
-    for (int i = 0; i < PRE; ++i) dl_issue_unit(u[i], rows, wrow + (uint32_t)i * DL_NW);
+        for (int i = 0; i < PRE; ++i) dl_issue_unit(u[i], rows, dl_unit<SPREAD>(wave, i));
+    }
     __syncthreads();  // every wave is done with the previous phase's LDS
     DlHold hd = out.hold;
     hd.lds = sm.g.hold;
+    hd.upw = UPW;
+    hd.rpw = RPW;
+    hd.spread = SPREAD;
+    hd.n_rows = rows.n_rows;
     if (EPI != DL_EPI_RESID) hd.kind = -1;
     dl_stage_x<NSB * 256, RMSNORM>(sm.g.xp, sm.g.xsum, sm.g.red, src_kind, x_src, e_x, norm_w, eps, hd, status);
+    if (!active) return;
 #pragma unroll
-    for (int i = PRE; i < R; ++i) dl_issue_unit(u[i], rows, wrow + (uint32_t)i * DL_NW);
+    for (int i = PRE; i < R; ++i) dl_issue_unit(u[i], rows, dl_unit<SPREAD>(wave, i));
     const Q4LaneConsts lc = q4k_lane_consts(dl_tid() & 3);
-    const int wave = __builtin_amdgcn_readfirstlane(dl_tid() >> 6);
 #pragma unroll
     for (int i = 0; i < UPW; ++i) {
         __builtin_amdgcn_sched_barrier(0);
-        float res[NG];
+        float res[NG][RPW];
         dl_dot_unit(u[i], sm.g.xp, sm.g.xsum, lc, res);
-        dl_store_row<NG, EPI>(out, wrow + (uint32_t)i * DL_NW, rows.n_rows, res, &sm.g.hold[wave * UPW + i]);
+        dl_store_unit<NG, RPW, EPI>(out, dl_unit<SPREAD>(wave, i), rows.n_rows, res,
+                                    &sm.g.hold[(wave * UPW + i) * RPW]);
         __builtin_amdgcn_sched_barrier(0);
-        if (i + R < UPW) dl_issue_unit(u[i + R], rows, wrow + (uint32_t)(i + R) * DL_NW);
+        if (i + R < UPW) dl_issue_unit(u[i + R], rows, dl_unit<SPREAD>(wave, i + R));
     }
 }
 
@@ -474,16 +563,17 @@ __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w,
 
 // Block (kv head kvh, slot bs): wave w covers positions [p0, p0 + span) of the
 // first L; the block's (max, sum, output) per q head goes to part[kvh][bs].
-__device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds& sm, const DlArgs& a, const uint64_t* lp, int kvh,
+template <class S>
+__device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds<S::GROUP>& sm, const DlArgs& a, const uint64_t* lp, int kvh,
                               int bs, int pos, int L, uint32_t e_qkv, uint32_t e_part) {
-    constexpr int GROUP = 4;
+    constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int span = dl_att_span(L);
     const int p0 = (bs * DL_WAVES + wave) * span;
     int rows = L - p0;
     rows = rows < 0 ? 0 : (rows > span ? span : rows);
-    const int S = (int)a.s_cap;
-    const bool has_new = pos < S && pos >= p0 && pos < p0 + rows;
+    const int s_cap = (int)a.s_cap;
+    const bool has_new = pos < s_cap && pos >= p0 && pos < p0 + rows;
     const int rnew = pos - p0;
     const bool rope = a.theta > 0.0f;
     const float* q_norm = reinterpret_cast<const float*>(lp[DL_Q_NORM]);
@@ -491,8 +581,8 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds& s
     uint16_t* kc = reinterpret_cast<uint16_t*>(lp[DL_K_CACHE]);
     uint16_t* vc = reinterpret_cast<uint16_t*>(lp[DL_V_CACHE]);
     const uint64_t* q = a.qkv_ll;
-    const uint64_t* kn = a.qkv_ll + 32 * DL_D;
-    const uint64_t* vn = a.qkv_ll + 40 * DL_D;
+    const uint64_t* kn = a.qkv_ll + S::QD;
+    const uint64_t* vn = a.qkv_ll + S::QD + S::KVD;
     auto ok = [&](int, uint64_t v) { return ll_ok32(v, e_qkv); };
     __syncthreads();  // every wave is done with the previous phase's LDS
 
@@ -597,8 +687,8 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds& s
         mg[gg] = m;
         lg[gg] = wave_sum(part == 0 ? e0 + e1 : 0.0f);
         if (part == 0) {
-            reinterpret_cast<float*>(&sm.ps4[wave][p_k])[gg] = e0;
-            reinterpret_cast<float*>(&sm.ps4[wave][16 + p_k])[gg] = e1;
+            sm.ps[wave][p_k][gg] = e0;
+            sm.ps[wave][16 + p_k][gg] = e1;
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -615,11 +705,22 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds& s
         if (p % 8 == 0) __builtin_amdgcn_sched_barrier(0);
         const uint32_t vv = (has_new && p == rnew) ? vnew : bk.vr[p];
         const float v0 = bf16_bits_to_f32(vv & 0xffffu), v1 = bf16_bits_to_f32(vv >> 16);
-        const float4 pr = sm.ps4[wave][p];
-        o0[0] = fmaf(pr.x, v0, o0[0]); o1[0] = fmaf(pr.x, v1, o1[0]);
-        o0[1] = fmaf(pr.y, v0, o0[1]); o1[1] = fmaf(pr.y, v1, o1[1]);
-        o0[2] = fmaf(pr.z, v0, o0[2]); o1[2] = fmaf(pr.z, v1, o1[2]);
-        o0[3] = fmaf(pr.w, v0, o0[3]); o1[3] = fmaf(pr.w, v1, o1[3]);
+        float pr[GROUP];
+        if constexpr (GROUP == 4) {
+            const float4 t = *reinterpret_cast<const float4*>(&sm.ps[wave][p][0]);
+            pr[0] = t.x; pr[1] = t.y; pr[2] = t.z; pr[3] = t.w;
+        } else if constexpr (GROUP == 2) {
+            const float2 t = *reinterpret_cast<const float2*>(&sm.ps[wave][p][0]);
+            pr[0] = t.x; pr[1] = t.y;
+        } else {
+#pragma unroll
+            for (int gg = 0; gg < GROUP; ++gg) pr[gg] = sm.ps[wave][p][gg];
+        }
+#pragma unroll
+        for (int gg = 0; gg < GROUP; ++gg) {
+            o0[gg] = fmaf(pr[gg], v0, o0[gg]);
+            o1[gg] = fmaf(pr[gg], v1, o1[gg]);
+        }
     }
 #pragma unroll
     for (int gg = 0; gg < GROUP; ++gg) {
@@ -657,10 +758,11 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds& s
     }
 }
 
-// Head hq = blockIdx.x (< 32): merge the DL_ATT_SLOTS block partials of its kv head.
-__device__ __forceinline__ void dl_merge_phase(DlAttnLds& sm, const DlArgs& a, int hq, uint32_t e_part,
+// Head hq = blockIdx.x (< NH): merge the DL_ATT_SLOTS block partials of its kv head.
+template <class S>
+__device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP>& sm, const DlArgs& a, int hq, uint32_t e_part,
                                                uint32_t e_attn) {
-    constexpr int GROUP = 4;
+    constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kvh = hq / GROUP, gg = hq % GROUP;
     constexpr int PER_WAVE = DL_ATT_SLOTS / DL_WAVES;  // 4 partials per wave
@@ -716,10 +818,10 @@ __device__ __forceinline__ void dl_merge_phase(DlAttnLds& sm, const DlArgs& a, i
 
 // ------------------------------------------------------------- the kernel ----
 
+template <class S>
 __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs a) {
-    __shared__ __align__(16) DlShared sm;
+    __shared__ __align__(16) DlShared<S> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t wrow = blockIdx.x * DL_WAVES + wave;
     const uint32_t seq = a.ctl[0];  // written by the previous launch
     const int pos = *a.pos_ptr;
     const int L = pos + 1 < (int)a.s_cap ? pos + 1 : (int)a.s_cap;
@@ -734,30 +836,35 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
     auto qkv_rows = [&](uint32_t layer) {
         DlRows r;
         r.w0 = r.w1 = reinterpret_cast<const uint8_t*>(layer_ptr(layer, DL_WQ));  // q | k | v rows, contiguous
-        r.n_rows = DL_QKV_ROWS;
+        r.n_rows = S::QKV_ROWS;
         return r;
     };
     auto o_rows = [&](uint32_t layer) {
         DlRows r;
         r.w0 = r.w1 = reinterpret_cast<const uint8_t*>(layer_ptr(layer, DL_WO));
-        r.n_rows = DL_HID;
+        r.n_rows = S::HID;
         return r;
     };
     auto gu_rows = [&](uint32_t layer) {
         DlRows r;
         r.w0 = reinterpret_cast<const uint8_t*>(layer_ptr(layer, DL_WGATE));
         r.w1 = reinterpret_cast<const uint8_t*>(layer_ptr(layer, DL_WUP));
-        r.n_rows = DL_MLP;
+        r.n_rows = S::MLP;
         return r;
     };
     auto down_rows = [&](uint32_t layer) {
         DlRows r;
         r.w0 = r.w1 = reinterpret_cast<const uint8_t*>(layer_ptr(layer, DL_WDOWN));
-        r.n_rows = DL_HID;
+        r.n_rows = S::HID;
         return r;
     };
     const int span = dl_att_span(L);
     const int att_p0 = (bs * DL_WAVES + wave) * span;
+    // phases with fewer units than waves spread them over the blocks
+    constexpr bool qkv_sp = S::QKV_ROWS / DlUnit<S::HSB, 1>::RPW < DL_NW;
+    constexpr bool o_sp = S::HID / DlUnit<S::QSB, 1>::RPW < DL_NW;
+    constexpr bool gu_sp = S::MLP / DlUnit<S::HSB, 2>::RPW < DL_NW;
+    constexpr bool dn_sp = S::HID / DlUnit<S::MSB, 1>::RPW < DL_NW;
 
     for (uint32_t layer = 0; layer < a.n_layers; ++layer) {
         const bool first = layer == 0, last = layer + 1 == a.n_layers;
@@ -770,8 +877,8 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         // ---- Q|K|V: RMSNorm(h) . [Wq; Wk; Wv]^T
         out.ll32 = a.qkv_ll;
         out.e_out = e_qkv;
-        dl_gemv_phase<DL_HSB, 1, 3, 3, DL_PRE_QKV, DL_EPI_STORE, true>(
-            sm, qkv_rows(layer), wrow, first ? DL_SRC_PLAIN : DL_SRC_LL32,
+        dl_gemv_phase<S::HSB, 1, S::qkv_u, S::qkv_r, S::qkv_p, DL_EPI_STORE, true, qkv_sp>(
+            sm, qkv_rows(layer), first ? DL_SRC_PLAIN : DL_SRC_LL32,
             first ? static_cast<const void*>(a.h) : static_cast<const void*>(a.h_ll), e_hprev,
             reinterpret_cast<const float*>(layer_ptr(layer, DL_IN_NORM)), a.eps, out, a.status);
         // ---- attention split: the K/V rows are loaded before q|k|v is awaited
@@ -782,25 +889,24 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
             DlAttnBank bk;
             dl_attn_issue(bk, reinterpret_cast<const uint16_t*>(lp[DL_K_CACHE]),
                           reinterpret_cast<const uint16_t*>(lp[DL_V_CACHE]), kvh, att_p0, L);
-            dl_attn_phase(bk, sm.at, a, lp, kvh, bs, pos, L, e_qkv, e_part);
+            dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, pos, L, e_qkv, e_part);
         }
-        // ---- attention merge (blocks 0..31, one q head each)
-        if (blockIdx.x < 32) dl_merge_phase(sm.at, a, blockIdx.x, e_part, e_attn);
+        // ---- attention merge (blocks 0..NH-1, one q head each)
+        if (blockIdx.x < S::NH) dl_merge_phase<S>(sm.at, a, blockIdx.x, e_part, e_attn);
         // ---- o_proj + residual
         out.ll32 = a.h_ll;
         out.plain = nullptr;
         out.hold.kind = first ? DL_SRC_PLAIN : DL_SRC_LL32;
         out.hold.src = first ? static_cast<const void*>(a.h) : static_cast<const void*>(a.h_ll);
         out.hold.e = e_hprev;
-        out.hold.upw = 2;
         out.e_out = e_ho;
-        dl_gemv_phase<DL_HSB, 1, 2, 2, DL_PRE_O, DL_EPI_RESID, false>(sm, o_rows(layer), wrow, DL_SRC_LL16, a.attn_ll, e_attn,
-                                                           nullptr, a.eps, out, a.status);
+        dl_gemv_phase<S::QSB, 1, S::o_u, S::o_r, S::o_p, DL_EPI_RESID, false, o_sp>(
+            sm, o_rows(layer), DL_SRC_LL16, a.attn_ll, e_attn, nullptr, a.eps, out, a.status);
         // ---- RMSNorm + gate|up + SwiGLU
         out.ll16 = a.act_ll;
         out.e_out = e_act;
-        dl_gemv_phase<DL_HSB, 2, 6, 3, DL_PRE_GU, DL_EPI_SWIGLU, true>(
-            sm, gu_rows(layer), wrow, DL_SRC_LL32, a.h_ll, e_ho,
+        dl_gemv_phase<S::HSB, 2, S::gu_u, S::gu_r, S::gu_p, DL_EPI_SWIGLU, true, gu_sp>(
+            sm, gu_rows(layer), DL_SRC_LL32, a.h_ll, e_ho,
             reinterpret_cast<const float*>(layer_ptr(layer, DL_POST_NORM)), a.eps, out, a.status);
         // ---- down + residual (the last layer writes the caller's h)
         out.ll32 = a.h_ll;
@@ -808,10 +914,9 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         out.hold.kind = DL_SRC_LL32;
         out.hold.src = a.h_ll;
         out.hold.e = e_ho;
-        out.hold.upw = 2;
         out.e_out = e_hd;
-        dl_gemv_phase<DL_MSB, 1, 2, 2, DL_PRE_DOWN, DL_EPI_RESID, false>(sm, down_rows(layer), wrow, DL_SRC_LL16, a.act_ll, e_act,
-                                                           nullptr, a.eps, out, a.status);
+        dl_gemv_phase<S::MSB, 1, S::dn_u, S::dn_r, S::dn_p, DL_EPI_RESID, false, dn_sp>(
+            sm, down_rows(layer), DL_SRC_LL16, a.act_ll, e_act, nullptr, a.eps, out, a.status);
     }
     // Every block has read the launch counter before block 0 can get here: its
     // last phase consumed every block's output.
@@ -825,64 +930,56 @@ struct DlLayout {
 };
 
 // Workspace: launch counter, then the epoch-tagged vectors.
+template <class S>
 static DlLayout dl_layout() {
     DlLayout l;
     size_t off = 0;
     l.ctl = off;
     off += 256;
     l.qkv = off;
-    off += dl_align((size_t)DL_QKV_ROWS * 8);
+    off += dl_align((size_t)S::QKV_ROWS * 8);
     l.attn = off;
-    off += dl_align((size_t)32 * DL_D * 4);
+    off += dl_align((size_t)S::QD * 4);
     l.act = off;
-    off += dl_align((size_t)DL_MLP * 4);
+    off += dl_align((size_t)S::MLP * 4);
     l.h = off;
-    off += dl_align((size_t)DL_HID * 8);
+    off += dl_align((size_t)S::HID * 8);
     l.part = off;
-    off += dl_align((size_t)8 * DL_ATT_SLOTS * 4 * (2 + DL_D) * 8);
+    off += dl_align((size_t)S::NK * DL_ATT_SLOTS * S::GROUP * (2 + DL_D) * 8);
     l.total = off;
     return l;
 }
 
-static int g_dl_fits = -1;  // cached residency check: 1 = 256 blocks fit at once
-
+// Cached residency check per shape: 1 = 256 blocks fit on the device at once.
+template <class S>
 static bool dl_grid_fits() {
-    if (g_dl_fits >= 0) return g_dl_fits == 1;
+    static int fits = -1;
+    if (fits >= 0) return fits == 1;
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_layers_kernel, DL_THREADS, 0) != hipSuccess) {
-        g_dl_fits = 0;
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_layers_kernel<S>, DL_THREADS, 0) != hipSuccess) {
+        fits = 0;
         return false;
     }
-    g_dl_fits = (cus * per_cu >= DL_BLOCKS) ? 1 : 0;
-    return g_dl_fits == 1;
+    fits = (cus * per_cu >= DL_BLOCKS) ? 1 : 0;
+    return fits == 1;
 }
 
-}  // namespace t2h
-using namespace t2h;
-
-
-extern "C" size_t t2h_qwen3_decode_layers_workspace_bytes(uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk,
-                                                         uint32_t d) {
-    if (hidden != DL_HID || mlp != DL_MLP || nh != 32 || nk != 8 || d != DL_D) return 0;
-    return dl_layout().total;
+template <class S>
+static bool dl_is(uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk, uint32_t d) {
+    return hidden == (uint32_t)S::HID && mlp == (uint32_t)S::MLP && nh == (uint32_t)S::NH && nk == (uint32_t)S::NK &&
+           d == (uint32_t)DL_D;
 }
 
-extern "C" int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden, uint32_t mlp,
-                                       uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap, float* h,
-                                       const int32_t* cache_position, float eps, float theta, void* workspace,
-                                       size_t workspace_bytes, uint32_t* status, void* stream) {
-    if (!layer_table || !h || !cache_position || !workspace || !status) return T2H_ERR_NULL;
-    if (hidden != DL_HID || mlp != DL_MLP || nh != 32 || nk != 8 || d != DL_D) return T2H_ERR_UNSUPPORTED;
-    if (n_layers == 0) return T2H_OK;
-    if (s_cap == 0) return T2H_ERR_SHAPE;
-    if ((size_t)(s_cap + DL_ATT_SLOTS * DL_WAVES - 1) / (DL_ATT_SLOTS * DL_WAVES) > DL_ATT_POS)
-        return T2H_ERR_UNSUPPORTED;  // more than 32 positions per wave
-    const DlLayout l = dl_layout();
+template <class S>
+static int dl_launch(const uint64_t* layer_table, uint32_t n_layers, uint32_t s_cap, float* h,
+                     const int32_t* cache_position, float eps, float theta, void* workspace, size_t workspace_bytes,
+                     uint32_t* status, void* stream) {
+    const DlLayout l = dl_layout<S>();
     if (workspace_bytes < l.total) return T2H_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return T2H_ERR_ALIGN;
-    if (!dl_grid_fits()) return T2H_ERR_UNSUPPORTED;
+    if (!dl_grid_fits<S>()) return T2H_ERR_UNSUPPORTED;
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     DlArgs a;
     a.layers = layer_table;
@@ -899,8 +996,36 @@ extern "C" int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_l
     a.h_ll = reinterpret_cast<uint64_t*>(ws + l.h);
     a.part_ll = reinterpret_cast<uint64_t*>(ws + l.part);
     a.status = status;
-    hipLaunchKernelGGL(decode_layers_kernel, dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
+    hipLaunchKernelGGL(decode_layers_kernel<S>, dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
                        reinterpret_cast<hipStream_t>(stream), a);
     T2H_LAUNCH_CHECK();
     return T2H_OK;
+}
+
+}  // namespace t2h
+using namespace t2h;
+
+
+extern "C" size_t t2h_qwen3_decode_layers_workspace_bytes(uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk,
+                                                         uint32_t d) {
+    if (dl_is<DlQwen3_8B>(hidden, mlp, nh, nk, d)) return dl_layout<DlQwen3_8B>().total;
+    if (dl_is<DlQwen3_0_6B>(hidden, mlp, nh, nk, d)) return dl_layout<DlQwen3_0_6B>().total;
+    return 0;
+}
+
+extern "C" int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden, uint32_t mlp,
+                                       uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap, float* h,
+                                       const int32_t* cache_position, float eps, float theta, void* workspace,
+                                       size_t workspace_bytes, uint32_t* status, void* stream) {
+    if (!layer_table || !h || !cache_position || !workspace || !status) return T2H_ERR_NULL;
+    const bool is8b = dl_is<DlQwen3_8B>(hidden, mlp, nh, nk, d);
+    if (!is8b && !dl_is<DlQwen3_0_6B>(hidden, mlp, nh, nk, d)) return T2H_ERR_UNSUPPORTED;
+    if (n_layers == 0) return T2H_OK;
+    if (s_cap == 0) return T2H_ERR_SHAPE;
+    if ((size_t)(s_cap + DL_ATT_SLOTS * DL_WAVES - 1) / (DL_ATT_SLOTS * DL_WAVES) > DL_ATT_POS)
+        return T2H_ERR_UNSUPPORTED;  // more than 32 positions per wave
+    return is8b ? dl_launch<DlQwen3_8B>(layer_table, n_layers, s_cap, h, cache_position, eps, theta, workspace,
+                                        workspace_bytes, status, stream)
+                : dl_launch<DlQwen3_0_6B>(layer_table, n_layers, s_cap, h, cache_position, eps, theta, workspace,
+                                          workspace_bytes, status, stream);
 }
