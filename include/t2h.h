@@ -209,16 +209,17 @@ int t2h_attn_decode(const float* q, const float* k_new, const float* v_new, cons
  * workspace must not overlap in time.
  * Built for the Qwen3-8B shape (hidden 4096, mlp 12288, 32/8 heads) and the Qwen3-0.6B shape (hidden
  * 1024, mlp 3072, 16/8 heads), d 128, uniform Q4_K weights, bf16 KV caches [s_cap, 8, 128] with
- * s_cap <= 7168 (other shapes: T2H_ERR_UNSUPPORTED; so is a GPU that cannot hold 256 blocks).
+ * s_cap <= 8192 (other shapes: T2H_ERR_UNSUPPORTED; so is a GPU that cannot hold 256 blocks).
  * layer_table: device int64 [n_layers][13] pointers in the order
  *   wq, wk, wv, wo, w_gate, w_up, w_down, input_norm, post_norm, q_norm, k_norm, k_cache, v_cache,
  * where wq..wv must be one allocation of q_dim + 2 kv_dim stacked rows (wk = wq + q_dim rows, wv = wk +
  * kv_dim rows).
  * workspace: t2h_qwen3_decode_layers_workspace_bytes() bytes, 256-B aligned,
  * zero-filled once before its first use (it holds a launch counter that later
- * calls advance).  *status (device) is set non-zero if a wait for another
- * block's output timed out, which means the result is invalid; it is never
- * cleared by the library.
+ * calls advance).  *status (device) is set to 0x80000000 | layer << 8 | phase
+ * (phase 1..7: qkv, attention q, attention k/v, merge, o, gate/up, down) if a
+ * wait for another block's output timed out, which means the result is
+ * invalid; it is never cleared by the library.
  * replaces run_decode_layer for every layer (src/models/optimized_qwen3/dispatch/decode_layer.py:60-136;
  * decode step src/models/optimized_qwen3/run.py:142-172). */
 size_t t2h_qwen3_decode_layers_workspace_bytes(uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk, uint32_t d);

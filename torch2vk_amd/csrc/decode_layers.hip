@@ -55,7 +55,10 @@ constexpr int DL_NW = DL_BLOCKS * DL_WAVES;    // waves in the grid
 constexpr int DL_D = 128;                      // head dim
 constexpr int DL_ATT_POS = 32;                 // positions per wave per attention pass (two rows per lane)
 constexpr int DL_ATT_SLOTS = DL_BLOCKS / 8;    // attention blocks per kv head (8 kv heads)
-constexpr uint32_t DL_SPIN_LIMIT = 1u << 14;
+#ifndef DL_SPIN_LOG2
+#define DL_SPIN_LOG2 14
+#endif
+constexpr uint32_t DL_SPIN_LIMIT = 1u << DL_SPIN_LOG2;
 // weight units per wave issued before a GEMV phase's input is awaited
 #ifndef DL_PRE_QKV
 #define DL_PRE_QKV 3
@@ -142,9 +145,13 @@ __device__ __forceinline__ void ll_put16(uint32_t* p, float v, uint32_t e) {
     __hip_atomic_store(p, f32_to_bf16_bits(v) | ((e & 0xffffu) << 16), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Where a wait gave up: status = DL_STATUS_TIMEOUT | layer << 8 | phase.
+enum DlWaitSite { DL_W_QKV = 1, DL_W_ATTN_Q, DL_W_ATTN_KV, DL_W_MERGE, DL_W_O, DL_W_GU, DL_W_DOWN };
+constexpr uint32_t DL_STATUS_TIMEOUT = 0x80000000u;
+
 // Load N words (addr(i)) until ok(i, word) holds for all of them; bounded.
 template <int N, class Addr, class Ok>
-__device__ __forceinline__ void ll_wait(uint64_t (&w)[N], Addr addr, Ok ok, uint32_t* status) {
+__device__ __forceinline__ void ll_wait(uint64_t (&w)[N], Addr addr, Ok ok, uint32_t* status, uint32_t site) {
     for (uint32_t polls = 0;; ++polls) {
 #pragma unroll
         for (int i = 0; i < N; ++i) w[i] = ll_load(addr(i));
@@ -153,7 +160,7 @@ __device__ __forceinline__ void ll_wait(uint64_t (&w)[N], Addr addr, Ok ok, uint
         for (int i = 0; i < N; ++i) all = all && ok(i, w[i]);
         if (all) break;
         if (polls >= DL_SPIN_LIMIT) {
-            __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(status, DL_STATUS_TIMEOUT | site, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -279,11 +286,15 @@ struct DlHold {
     uint32_t n_rows;
 };
 
+// Row of hold slot t, or n_rows when the slot's unit has no such row.  Only a
+// block's own rows may be read: the phase overwrites every row of h in place,
+// each by the block that computes it (reading a row clamped into range would
+// race with its owner's overwrite and wait for an epoch that is already gone).
 __device__ __forceinline__ uint32_t dl_hold_row(const DlHold& hd, int t) {
     const uint32_t w = (uint32_t)(t / (hd.upw * hd.rpw)), i = (uint32_t)((t / hd.rpw) % hd.upw);
     const uint32_t unit = hd.spread ? dl_unit<true>(w, i) : dl_unit<false>(w, i);
     const uint32_t row = unit * (uint32_t)hd.rpw + (uint32_t)(t % hd.rpw);
-    return row < hd.n_rows ? row : hd.n_rows - 1;
+    return row < hd.n_rows ? row : hd.n_rows;
 }
 
 // Stage x (K values) in LDS as fp16 pair words + sub-block sums.  RMSNORM:
@@ -292,7 +303,7 @@ __device__ __forceinline__ uint32_t dl_hold_row(const DlHold& hd, int t) {
 template <int K, bool RMSNORM>
 __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red, int src_kind, const void* src,
                                            uint32_t e, const float* norm_w, float eps, const DlHold& hd,
-                                           uint32_t* status) {
+                                           uint32_t* status, uint32_t site) {
     // PT float4 per thread; when K does not fill the block, the threads past
     // K/4 in the last step (whole waves, as K % 256 == 0) re-read element 0
     // and stage nothing
@@ -304,8 +315,8 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
     auto elem = [&](int j) { return valid(j) ? (j * DL_THREADS + tid) * 4 : 0; };
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool has_hold = hd.kind >= 0 && tid < DL_WAVES * hd.upw * hd.rpw;
-    const uint32_t hold_row = has_hold ? dl_hold_row(hd, tid) : 0u;
+    const uint32_t hold_row = hd.kind >= 0 && tid < DL_WAVES * hd.upw * hd.rpw ? dl_hold_row(hd, tid) : hd.n_rows;
+    const bool has_hold = hold_row < hd.n_rows;
     const uint64_t* hold_ll = reinterpret_cast<const uint64_t*>(hd.src) + hold_row;
     const bool hold_ll_wait = has_hold && hd.kind == DL_SRC_LL32;
     float hold = 0.0f;
@@ -319,7 +330,7 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
         const uint64_t* x = reinterpret_cast<const uint64_t*>(src);
         uint64_t w[4 * PT];
         ll_wait(w, [&](int i) { return x + elem(i / 4) + (i % 4); }, [&](int, uint64_t v) { return ll_ok32(v, e); },
-                status);
+                status, site);
 #pragma unroll
         for (int j = 0; j < PT; ++j)
             hv[j] = make_float4(ll_val32(w[4 * j]), ll_val32(w[4 * j + 1]), ll_val32(w[4 * j + 2]),
@@ -335,7 +346,7 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
                 [&](int i, uint64_t v) {
                     return i < 2 * PT || !hold_ll_wait ? ll_ok16x2(v, e) : ll_ok32(v, hd.e);
                 },
-                status);
+                status, site);
 #pragma unroll
         for (int j = 0; j < PT; ++j)
             hv[j] = make_float4(bf16_bits_to_f32((uint32_t)w[2 * j] & 0xffffu),
@@ -472,7 +483,7 @@ __device__ __forceinline__ void dl_store_unit(const DlOut& o, uint32_t unit, uin
 template <int NSB, int NG, int UPW, int R, int PRE, int EPI, bool RMSNORM, bool SPREAD, class SH>
 __device__ __forceinline__ void dl_gemv_phase(SH& sm, const DlRows& rows, int src_kind, const void* x_src,
                                               uint32_t e_x, const float* norm_w, float eps, const DlOut& out,
-                                              uint32_t* status) {
+                                              uint32_t* status, uint32_t site) {
     static_assert(PRE >= 1 && PRE <= R && R <= UPW, "ring size");
     constexpr int RPW = DlUnit<NSB, NG>::RPW;
     static_assert(EPI != DL_EPI_RESID || UPW * RPW <= DL_HOLD, "residual rows per wave");
@@ -493,7 +504,8 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, const DlRows& rows, int sr
     hd.spread = SPREAD;
     hd.n_rows = rows.n_rows;
     if (EPI != DL_EPI_RESID) hd.kind = -1;
-    dl_stage_x<NSB * 256, RMSNORM>(sm.g.xp, sm.g.xsum, sm.g.red, src_kind, x_src, e_x, norm_w, eps, hd, status);
+    dl_stage_x<NSB * 256, RMSNORM>(sm.g.xp, sm.g.xsum, sm.g.red, src_kind, x_src, e_x, norm_w, eps, hd, status,
+                                   site);
     if (!active) return;
 #pragma unroll
     for (int i = PRE; i < R; ++i) dl_issue_unit(u[i], rows, dl_unit<SPREAD>(wave, i));
@@ -565,7 +577,7 @@ __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w,
 // first L; the block's (max, sum, output) per q head goes to part[kvh][bs].
 template <class S>
 __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds<S::GROUP>& sm, const DlArgs& a, const uint64_t* lp, int kvh,
-                              int bs, int pos, int L, uint32_t e_qkv, uint32_t e_part) {
+                              int bs, int pos, int L, uint32_t e_qkv, uint32_t e_part, uint32_t site) {
     constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int span = dl_att_span(L);
@@ -594,7 +606,7 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds<S:
     if (wave < GROUP) {
         const int hq = kvh * GROUP + wave;
         uint64_t w[2];
-        ll_wait(w, [&](int i) { return q + hq * DL_D + lane + 64 * i; }, ok, a.status);
+        ll_wait(w, [&](int i) { return q + hq * DL_D + lane + 64 * i; }, ok, a.status, site | DL_W_ATTN_Q);
         float r0, r1;
         dl_norm_rope(ll_val32(w[0]), ll_val32(w[1]), q_norm, q_norm != nullptr, a.eps, cs, sn, rope, r0, r1);
         const float scale = 1.0f / sqrtf((float)DL_D);
@@ -605,7 +617,7 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds<S:
     if (has_new) {
         uint64_t w[4];
         ll_wait(w, [&](int i) { return i < 2 ? kn + kvh * DL_D + lane + 64 * i : vn + kvh * DL_D + 2 * lane + (i - 2); },
-                ok, a.status);
+                ok, a.status, site | DL_W_ATTN_KV);
         float k0, k1;
         dl_norm_rope(ll_val32(w[0]), ll_val32(w[1]), k_norm, k_norm != nullptr, a.eps, cs, sn, rope, k0, k1);
         const uint16_t kb0 = (uint16_t)f32_to_bf16_bits(k0), kb1 = (uint16_t)f32_to_bf16_bits(k1);
@@ -761,7 +773,7 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds<S:
 // Head hq = blockIdx.x (< NH): merge the DL_ATT_SLOTS block partials of its kv head.
 template <class S>
 __device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP>& sm, const DlArgs& a, int hq, uint32_t e_part,
-                                               uint32_t e_attn) {
+                                               uint32_t e_attn, uint32_t site) {
     constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kvh = hq / GROUP, gg = hq % GROUP;
@@ -773,7 +785,7 @@ __device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP>& sm, const Dl
                 const uint64_t* pg = a.part_ll + (((size_t)kvh * DL_ATT_SLOTS + bs) * GROUP + gg) * (2 + DL_D);
                 return k < 2 ? pg + k : pg + 2 + 2 * lane + (k - 2);
             },
-            [&](int, uint64_t v) { return ll_ok32(v, e_part); }, a.status);
+            [&](int, uint64_t v) { return ll_ok32(v, e_part); }, a.status, site | DL_W_MERGE);
     float2 ml[PER_WAVE], ov[PER_WAVE];
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
@@ -822,8 +834,14 @@ template <class S>
 __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs a) {
     __shared__ __align__(16) DlShared<S> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t seq = a.ctl[0];  // written by the previous launch
-    const int pos = *a.pos_ptr;
+    // The launch counter (written by block 0 of the previous launch) and the
+    // position (written by the token-store kernel) are read with agent-scope
+    // atomic loads: a plain scalar load can return a stale copy on another XCD,
+    // and a block with a stale counter computes every epoch for the wrong launch.
+    const uint32_t seq = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(a.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const int pos = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(const_cast<int32_t*>(a.pos_ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     const int L = pos + 1 < (int)a.s_cap ? pos + 1 : (int)a.s_cap;
     const int kvh = blockIdx.x % 8, bs = blockIdx.x / 8;
 
@@ -868,6 +886,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
 
     for (uint32_t layer = 0; layer < a.n_layers; ++layer) {
         const bool first = layer == 0, last = layer + 1 == a.n_layers;
+        const uint32_t lsite = layer << 8;  // status code of a wait that gives up: layer and phase
         const uint32_t e_qkv = dl_epoch(seq, layer, DL_E_QKV), e_part = dl_epoch(seq, layer, DL_E_PART);
         const uint32_t e_attn = dl_epoch(seq, layer, DL_E_ATTN), e_ho = dl_epoch(seq, layer, DL_E_H_O);
         const uint32_t e_act = dl_epoch(seq, layer, DL_E_ACT), e_hd = dl_epoch(seq, layer, DL_E_H_DOWN);
@@ -880,7 +899,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         dl_gemv_phase<S::HSB, 1, S::qkv_u, S::qkv_r, S::qkv_p, DL_EPI_STORE, true, qkv_sp>(
             sm, qkv_rows(layer), first ? DL_SRC_PLAIN : DL_SRC_LL32,
             first ? static_cast<const void*>(a.h) : static_cast<const void*>(a.h_ll), e_hprev,
-            reinterpret_cast<const float*>(layer_ptr(layer, DL_IN_NORM)), a.eps, out, a.status);
+            reinterpret_cast<const float*>(layer_ptr(layer, DL_IN_NORM)), a.eps, out, a.status, lsite | DL_W_QKV);
         // ---- attention split: the K/V rows are loaded before q|k|v is awaited
         {
             uint64_t lp[DL_LAYER_PTRS];
@@ -889,10 +908,10 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
             DlAttnBank bk;
             dl_attn_issue(bk, reinterpret_cast<const uint16_t*>(lp[DL_K_CACHE]),
                           reinterpret_cast<const uint16_t*>(lp[DL_V_CACHE]), kvh, att_p0, L);
-            dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, pos, L, e_qkv, e_part);
+            dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, pos, L, e_qkv, e_part, lsite);
         }
         // ---- attention merge (blocks 0..NH-1, one q head each)
-        if (blockIdx.x < S::NH) dl_merge_phase<S>(sm.at, a, blockIdx.x, e_part, e_attn);
+        if (blockIdx.x < S::NH) dl_merge_phase<S>(sm.at, a, blockIdx.x, e_part, e_attn, lsite);
         // ---- o_proj + residual
         out.ll32 = a.h_ll;
         out.plain = nullptr;
@@ -901,13 +920,13 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         out.hold.e = e_hprev;
         out.e_out = e_ho;
         dl_gemv_phase<S::QSB, 1, S::o_u, S::o_r, S::o_p, DL_EPI_RESID, false, o_sp>(
-            sm, o_rows(layer), DL_SRC_LL16, a.attn_ll, e_attn, nullptr, a.eps, out, a.status);
+            sm, o_rows(layer), DL_SRC_LL16, a.attn_ll, e_attn, nullptr, a.eps, out, a.status, lsite | DL_W_O);
         // ---- RMSNorm + gate|up + SwiGLU
         out.ll16 = a.act_ll;
         out.e_out = e_act;
         dl_gemv_phase<S::HSB, 2, S::gu_u, S::gu_r, S::gu_p, DL_EPI_SWIGLU, true, gu_sp>(
             sm, gu_rows(layer), DL_SRC_LL32, a.h_ll, e_ho,
-            reinterpret_cast<const float*>(layer_ptr(layer, DL_POST_NORM)), a.eps, out, a.status);
+            reinterpret_cast<const float*>(layer_ptr(layer, DL_POST_NORM)), a.eps, out, a.status, lsite | DL_W_GU);
         // ---- down + residual (the last layer writes the caller's h)
         out.ll32 = a.h_ll;
         out.plain = last ? a.h : nullptr;
@@ -916,11 +935,12 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         out.hold.e = e_ho;
         out.e_out = e_hd;
         dl_gemv_phase<S::MSB, 1, S::dn_u, S::dn_r, S::dn_p, DL_EPI_RESID, false, dn_sp>(
-            sm, down_rows(layer), DL_SRC_LL16, a.act_ll, e_act, nullptr, a.eps, out, a.status);
+            sm, down_rows(layer), DL_SRC_LL16, a.act_ll, e_act, nullptr, a.eps, out, a.status, lsite | DL_W_DOWN);
     }
     // Every block has read the launch counter before block 0 can get here: its
     // last phase consumed every block's output.
-    if (blockIdx.x == 0 && threadIdx.x == 0) a.ctl[0] = seq + 1u;
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_store(a.ctl, seq + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 static size_t dl_align(size_t v) { return (v + 255) & ~(size_t)255; }

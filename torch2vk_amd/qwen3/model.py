@@ -106,8 +106,8 @@ class Qwen3Decoder:
         c = self.config
         if not kernels.decode_layers_supported(c.hidden, c.mlp, c.heads, c.kv_heads, c.head_dim):
             return f"shape hidden={c.hidden} mlp={c.mlp} heads={c.heads}/{c.kv_heads} d={c.head_dim} not built"
-        if self.max_positions > 7168:
-            return "KV capacity above 7168 positions"
+        if self.max_positions > 8192:
+            return "KV capacity above 8192 positions"
         for i in range(c.layers):
             for n in ("q", "k", "v", "o", "gate", "up", "down"):
                 if self.types[f"layers.{i}.{n}"] != "q4_k":
@@ -119,8 +119,14 @@ class Qwen3Decoder:
 
     def check_status(self) -> None:
         """Raise if a grid barrier of the persistent kernel ever timed out (its results are then invalid)."""
-        if self.persistent and int(self.status.item()) != 0:
-            raise RuntimeError("persistent decode kernel: a grid barrier timed out; results are invalid")
+        if not self.persistent:
+            return
+        code = int(self.status.item())
+        if code != 0:
+            phases = {1: "qkv", 2: "attention q", 3: "attention k/v", 4: "merge", 5: "o", 6: "gate/up", 7: "down"}
+            where = f"layer {(code >> 8) & 0xff}, phase {phases.get(code & 0xff, code & 0xff)}"
+            raise RuntimeError(f"persistent decode kernel: a wait for another block timed out at {where} "
+                               f"(status {code:#x}); results are invalid")
 
     # ----------------------------------------------------------- state --
 
