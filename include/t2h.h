@@ -209,7 +209,7 @@ int t2h_attn_decode(const float* q, const float* k_new, const float* v_new, cons
  * workspace must not overlap in time.
  * Built for the Qwen3-8B shape (hidden 4096, mlp 12288, 32/8 heads) and the Qwen3-0.6B shape (hidden
  * 1024, mlp 3072, 16/8 heads), d 128, uniform Q4_K weights, bf16 KV caches [s_cap, 8, 128] with
- * s_cap <= 8192 (other shapes: T2H_ERR_UNSUPPORTED; so is a GPU that cannot hold 256 blocks).
+ * s_cap <= 8192, n_layers <= 64 (otherwise T2H_ERR_UNSUPPORTED; so is a GPU that cannot hold 256 blocks).
  * layer_table: device int64 [n_layers][13] pointers in the order
  *   wq, wk, wv, wo, w_gate, w_up, w_down, input_norm, post_norm, q_norm, k_norm, k_cache, v_cache,
  * where wq..wv must be one allocation of q_dim + 2 kv_dim stacked rows (wk = wq + q_dim rows, wv = wk +

@@ -61,16 +61,16 @@ constexpr int DL_ATT_SLOTS = DL_BLOCKS / 8;    // attention blocks per kv head (
 constexpr uint32_t DL_SPIN_LIMIT = 1u << DL_SPIN_LOG2;
 // weight units per wave issued before a GEMV phase's input is awaited
 #ifndef DL_PRE_QKV
-#define DL_PRE_QKV 3
+#define DL_PRE_QKV 1
 #endif
 #ifndef DL_PRE_O
-#define DL_PRE_O 2
+#define DL_PRE_O 1
 #endif
 #ifndef DL_PRE_GU
-#define DL_PRE_GU 2
+#define DL_PRE_GU 1
 #endif
 #ifndef DL_PRE_DOWN
-#define DL_PRE_DOWN 2
+#define DL_PRE_DOWN 1
 #endif   // polls before a consumer gives up (~16 ms)
 
 // Per-layer pointer table (device memory, DL_LAYER_PTRS uint64 per layer).
@@ -82,6 +82,7 @@ enum DlLayerPtr {
     DL_IN_NORM, DL_POST_NORM, DL_Q_NORM, DL_K_NORM, DL_K_CACHE, DL_V_CACHE,
     DL_LAYER_PTRS
 };
+constexpr uint32_t DL_MAX_LAYERS = 64;  // layers per launch (the table is held in LDS)
 
 struct DlArgs {
     const uint64_t* layers;   // [n_layers][DL_LAYER_PTRS]
@@ -108,6 +109,16 @@ __device__ __forceinline__ int dl_tid() {
     int t;
     asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
     return t;
+}
+
+// A device address from the layer table as a global-address-space pointer:
+// accesses through it compile to global_* instructions, which count only in
+// vmcnt.  Through a generic pointer they would be FLAT instructions, which
+// also count in lgkmcnt, so every LDS wait and every barrier would wait for
+// all weight loads still in flight, and no prefetch could run past one.
+template <class T>
+__device__ __forceinline__ T* dl_gptr(uint64_t v) {
+    return (T*)(__attribute__((address_space(1))) T*)v;
 }
 
 // ------------------------------------------------- epoch-tagged words ----
@@ -179,9 +190,12 @@ struct DlAttnLds {
 constexpr int dl_max3(int a, int b, int c) { return a > b ? (a > c ? a : c) : (b > c ? b : c); }
 
 // Model shape (8 kv heads of 128) and, per GEMV phase, the units per wave, the
-// ring depth and the units issued before the input is awaited.
+// ring depth and the units issued before the input is awaited.  V_LATE: the
+// attention V rows are issued once q|k|v has arrived instead of with the K
+// rows before the Q|K|V phase (measured faster for the 0.6B shape, slower for
+// the 8B one).
 template <int HSB_, int MSB_, int NH_, int QKV_U, int QKV_R, int QKV_P, int O_U, int O_R, int O_P, int GU_U,
-          int GU_R, int GU_P, int DN_U, int DN_R, int DN_P>
+          int GU_R, int GU_P, int DN_U, int DN_R, int DN_P, bool V_LATE>
 struct DlShape {
     static constexpr int HSB = HSB_;             // hidden / 256 (superblocks)
     static constexpr int MSB = MSB_;             // MLP / 256
@@ -194,10 +208,24 @@ struct DlShape {
     static constexpr int KMAX = dl_max3(HID, MLP, QD);
     static constexpr int qkv_u = QKV_U, qkv_r = QKV_R, qkv_p = QKV_P, o_u = O_U, o_r = O_R, o_p = O_P;
     static constexpr int gu_u = GU_U, gu_r = GU_R, gu_p = GU_P, dn_u = DN_U, dn_r = DN_R, dn_p = DN_P;
+    static constexpr bool v_late = V_LATE;
     static_assert(NH % NK == 0 && NH / NK <= 4, "GQA group of 1..4 q heads");
 };
-using DlQwen3_8B = DlShape<16, 48, 32, 3, 3, DL_PRE_QKV, 2, 2, DL_PRE_O, 6, 3, DL_PRE_GU, 2, 2, DL_PRE_DOWN>;
-using DlQwen3_0_6B = DlShape<4, 12, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1>;
+#ifndef DL_R_QKV
+#define DL_R_QKV 2
+#endif
+#ifndef DL_R_O
+#define DL_R_O 2
+#endif
+#ifndef DL_R_GU
+#define DL_R_GU 2
+#endif
+#ifndef DL_R_DOWN
+#define DL_R_DOWN 2
+#endif
+using DlQwen3_8B = DlShape<16, 48, 32, 3, DL_R_QKV, DL_PRE_QKV, 2, DL_R_O, DL_PRE_O, 6, DL_R_GU, DL_PRE_GU, 2, DL_R_DOWN,
+                           DL_PRE_DOWN, false>;
+using DlQwen3_0_6B = DlShape<4, 12, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, true>;
 
 constexpr int DL_HOLD = 4;  // residual rows a wave owns in one phase, at most
 
@@ -469,33 +497,38 @@ __device__ __forceinline__ void dl_store_unit(const DlOut& o, uint32_t unit, uin
     }
 }
 
+// The first PRE units of a GEMV phase.  SPREAD phases: waves without a unit
+// issue nothing.
+template <int NSB, int NG, int UPW, int PRE, bool SPREAD>
+__device__ __forceinline__ void dl_issue_pre(DlUnit<NSB, NG> (&u)[UPW], const DlRows& rows) {
+    constexpr int RPW = DlUnit<NSB, NG>::RPW;
+    const int wave = __builtin_amdgcn_readfirstlane(dl_tid() >> 6);
+    if (SPREAD && dl_unit<SPREAD>(wave, 0) >= (rows.n_rows + RPW - 1) / RPW) return;
+#pragma unroll
+    for (int i = 0; i < PRE; ++i) dl_issue_unit(u[i], rows, dl_unit<SPREAD>(wave, i));
+}
+
 // One GEMV phase over the wave's UPW units (rows wrow + i * DL_NW), streamed
-// through a ring of R units.  Vector memory returns in order on a CU, so the
-// input (polled after the weights already issued) arrives only after them:
-// PRE units are issued before the input is awaited, enough to keep HBM busy
-// while the rest of the chip finishes the previous phase, and units PRE .. R-1
-// right after it is staged, so they stream while the first units are reduced.
-// Unit i + R is issued right after unit i has been reduced.  The loop is
-// unrolled, so the ring is static registers, and the scheduling fences keep
-// each refill after the reduction that frees its registers.
+// through a ring of R units whose first PRE the caller issued (dl_issue_pre)
+// before the phase's input is awaited: they stream during the hand-off, and
+// the wait queues behind them, so PRE trades HBM occupancy at the phase
+// boundary against input latency.  Once the input is staged, units PRE .. R-1
+// are issued, then unit i + R right after unit i has been reduced.  The loop
+// is unrolled, so the ring is static registers, and the scheduling fences
+// keep each refill after the reduction that frees its registers.
 // SPREAD: fewer units than waves (dl_unit); a wave without a unit issues and
 // stores nothing.
 template <int NSB, int NG, int UPW, int R, int PRE, int EPI, bool RMSNORM, bool SPREAD, class SH>
-__device__ __forceinline__ void dl_gemv_phase(SH& sm, const DlRows& rows, int src_kind, const void* x_src,
-                                              uint32_t e_x, const float* norm_w, float eps, const DlOut& out,
-                                              uint32_t* status, uint32_t site) {
-    static_assert(PRE >= 1 && PRE <= R && R <= UPW, "ring size");
+__device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW], const DlRows& rows, int src_kind,
+                                              const void* x_src, uint32_t e_x, const float* norm_w, float eps,
+                                              const DlOut& out, uint32_t* status, uint32_t site) {
+    static_assert(PRE >= 0 && PRE <= R && R >= 1 && R <= UPW, "ring size");
     constexpr int RPW = DlUnit<NSB, NG>::RPW;
     static_assert(EPI != DL_EPI_RESID || UPW * RPW <= DL_HOLD, "residual rows per wave");
     static_assert(!SPREAD || UPW == 1, "spread phases have one unit per wave");
     const int wave = __builtin_amdgcn_readfirstlane(dl_tid() >> 6);
     const uint32_t n_units = (rows.n_rows + RPW - 1) / RPW;
     const bool active = !SPREAD || dl_unit<SPREAD>(wave, 0) < n_units;  // wave-uniform
-    DlUnit<NSB, NG> u[UPW];
-    if (active) {
-#pragma unroll
-        for (int i = 0; i < PRE; ++i) dl_issue_unit(u[i], rows, dl_unit<SPREAD>(wave, i));
-    }
     __syncthreads();  // every wave is done with the previous phase's LDS
     DlHold hd = out.hold;
     hd.lds = sm.g.hold;
@@ -535,23 +568,34 @@ __device__ __forceinline__ int dl_att_span(int L) {
     return (L + DL_ATT_SLOTS * DL_WAVES - 1) / (DL_ATT_SLOTS * DL_WAVES);
 }
 
-__device__ __forceinline__ void dl_attn_issue(DlAttnBank& bk, const uint16_t* kc, const uint16_t* vc, int kvh, int p0,
-                                              int L) {
+// Positions of the wave's span it covers: rows = clamp(L - p0, 0, span).
+__device__ __forceinline__ int dl_att_rows(int L, int p0, int span) {
+    const int rows = L - p0;
+    return rows < 0 ? 0 : (rows > span ? span : rows);
+}
+
+// Only the wave's own rows are loaded (rows of a short span would otherwise be
+// the next wave's, fetched twice); the registers of the others are zero, so
+// that P = 0 times V stays 0.
+__device__ __forceinline__ void dl_attn_issue_k(DlAttnBank& bk, const uint16_t* kc, int kvh, int p0, int rows) {
     const int lane = dl_tid() & 63;
     const int p_k = lane >> 2, part = lane & 3;
     const size_t stride = (size_t)8 * DL_D;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-        const int p = min(p0 + 16 * r + p_k, L - 1);
-        const uint16_t* krow = kc + (size_t)p * stride + (size_t)kvh * DL_D + part * 32;
+        const bool in = 16 * r + p_k < rows;
+        const uint16_t* krow = kc + (size_t)(in ? p0 + 16 * r + p_k : 0) * stride + (size_t)kvh * DL_D + part * 32;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) bk.kr[r][i] = load_u4(krow + 8 * i);
+        for (int i = 0; i < 4; ++i) bk.kr[r][i] = in ? load_u4(krow + 8 * i) : make_uint4(0u, 0u, 0u, 0u);
     }
+}
+
+__device__ __forceinline__ void dl_attn_issue_v(DlAttnBank& bk, const uint16_t* vc, int kvh, int p0, int rows) {
+    const int lane = dl_tid() & 63;
+    const size_t stride = (size_t)8 * DL_D;
+    const uint32_t* vrow = reinterpret_cast<const uint32_t*>(vc + (size_t)p0 * stride + (size_t)kvh * DL_D) + lane;
 #pragma unroll
-    for (int i = 0; i < DL_ATT_POS; ++i) {
-        const int p = min(p0 + i, L - 1);
-        bk.vr[i] = reinterpret_cast<const uint32_t*>(vc + (size_t)p * stride + (size_t)kvh * DL_D)[lane];
-    }
+    for (int i = 0; i < DL_ATT_POS; ++i) bk.vr[i] = i < rows ? vrow[(size_t)i * stride / 2] : 0u;
 }
 
 __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w, bool has_w, float eps, float cs,
@@ -576,22 +620,22 @@ __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w,
 // Block (kv head kvh, slot bs): wave w covers positions [p0, p0 + span) of the
 // first L; the block's (max, sum, output) per q head goes to part[kvh][bs].
 template <class S>
-__device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds<S::GROUP>& sm, const DlArgs& a, const uint64_t* lp, int kvh,
-                              int bs, int pos, int L, uint32_t e_qkv, uint32_t e_part, uint32_t site) {
+__device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP>& sm, const DlArgs& a,
+                                              const uint64_t* lp, int kvh, int bs, int pos, int L, uint32_t e_qkv,
+                                              uint32_t e_part, uint32_t site) {
     constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int span = dl_att_span(L);
     const int p0 = (bs * DL_WAVES + wave) * span;
-    int rows = L - p0;
-    rows = rows < 0 ? 0 : (rows > span ? span : rows);
+    const int rows = dl_att_rows(L, p0, span);
     const int s_cap = (int)a.s_cap;
     const bool has_new = pos < s_cap && pos >= p0 && pos < p0 + rows;
     const int rnew = pos - p0;
     const bool rope = a.theta > 0.0f;
-    const float* q_norm = reinterpret_cast<const float*>(lp[DL_Q_NORM]);
-    const float* k_norm = reinterpret_cast<const float*>(lp[DL_K_NORM]);
-    uint16_t* kc = reinterpret_cast<uint16_t*>(lp[DL_K_CACHE]);
-    uint16_t* vc = reinterpret_cast<uint16_t*>(lp[DL_V_CACHE]);
+    const float* q_norm = dl_gptr<const float>(lp[DL_Q_NORM]);
+    const float* k_norm = dl_gptr<const float>(lp[DL_K_NORM]);
+    uint16_t* kc = dl_gptr<uint16_t>(lp[DL_K_CACHE]);
+    uint16_t* vc = dl_gptr<uint16_t>(lp[DL_V_CACHE]);
     const uint64_t* q = a.qkv_ll;
     const uint64_t* kn = a.qkv_ll + S::QD;
     const uint64_t* vn = a.qkv_ll + S::QD + S::KVD;
@@ -630,6 +674,8 @@ __device__ __forceinline__ void dl_attn_phase(const DlAttnBank& bk, DlAttnLds<S:
         reinterpret_cast<uint32_t*>(vc + off)[lane] = vnew;
     }
     __syncthreads();
+    // V_LATE: V is needed only after the scores, issued behind every wait of the phase
+    if constexpr (S::v_late) dl_attn_issue_v(bk, vc, kvh, p0, rows);
 
     const int p_k = lane >> 2, part = lane & 3;
     float mg[GROUP], lg[GROUP];
@@ -845,45 +891,63 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
     const int L = pos + 1 < (int)a.s_cap ? pos + 1 : (int)a.s_cap;
     const int kvh = blockIdx.x % 8, bs = blockIdx.x / 8;
 
-    typedef const __attribute__((address_space(4))) uint64_t* const_table_t;
-    // the layer table is read-only for the launch: constant address space, scalar loads
+    // The layer table is copied into LDS once.  Read from memory, each layer's
+    // pointers would be a scalar-cache miss per launch, and a scalar load
+    // shares its wait counter with LDS: the LDS waits after it would stall for
+    // the miss (microseconds under load) wherever a phase first needs a pointer.
+    __shared__ uint64_t tbl[DL_MAX_LAYERS * DL_LAYER_PTRS];
+    for (uint32_t i = threadIdx.x; i < a.n_layers * DL_LAYER_PTRS; i += DL_THREADS) tbl[i] = a.layers[i];
+    __syncthreads();
     auto layer_ptr = [&](uint32_t layer, int field) -> uint64_t {
-        const const_table_t tbl = (const_table_t)(a.layers + (size_t)layer * DL_LAYER_PTRS);
-        return tbl[field];
+        const uint64_t v = tbl[layer * DL_LAYER_PTRS + field];
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+        return (uint64_t)hi << 32 | lo;
     };
     auto qkv_rows = [&](uint32_t layer) {
         DlRows r;
-        r.w0 = r.w1 = reinterpret_cast<const uint8_t*>(layer_ptr(layer, DL_WQ));  // q | k | v rows, contiguous
+        r.w0 = r.w1 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WQ));  // q | k | v rows, contiguous
         r.n_rows = S::QKV_ROWS;
         return r;
     };
     auto o_rows = [&](uint32_t layer) {
         DlRows r;
-        r.w0 = r.w1 = reinterpret_cast<const uint8_t*>(layer_ptr(layer, DL_WO));
+        r.w0 = r.w1 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WO));
         r.n_rows = S::HID;
         return r;
     };
     auto gu_rows = [&](uint32_t layer) {
         DlRows r;
-        r.w0 = reinterpret_cast<const uint8_t*>(layer_ptr(layer, DL_WGATE));
-        r.w1 = reinterpret_cast<const uint8_t*>(layer_ptr(layer, DL_WUP));
+        r.w0 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WGATE));
+        r.w1 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WUP));
         r.n_rows = S::MLP;
         return r;
     };
     auto down_rows = [&](uint32_t layer) {
         DlRows r;
-        r.w0 = r.w1 = reinterpret_cast<const uint8_t*>(layer_ptr(layer, DL_WDOWN));
+        r.w0 = r.w1 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WDOWN));
         r.n_rows = S::HID;
         return r;
     };
     const int span = dl_att_span(L);
     const int att_p0 = (bs * DL_WAVES + wave) * span;
+    const int att_rows = dl_att_rows(L, att_p0, span);
     // phases with fewer units than waves spread them over the blocks
     constexpr bool qkv_sp = S::QKV_ROWS / DlUnit<S::HSB, 1>::RPW < DL_NW;
     constexpr bool o_sp = S::HID / DlUnit<S::QSB, 1>::RPW < DL_NW;
     constexpr bool gu_sp = S::MLP / DlUnit<S::HSB, 2>::RPW < DL_NW;
     constexpr bool dn_sp = S::HID / DlUnit<S::MSB, 1>::RPW < DL_NW;
 
+    auto issue_bank = [&](uint32_t layer, DlAttnBank& bk) {
+        dl_attn_issue_k(bk, dl_gptr<const uint16_t>(layer_ptr(layer, DL_K_CACHE)), kvh, att_p0, att_rows);
+        if constexpr (!S::v_late)
+            dl_attn_issue_v(bk, dl_gptr<const uint16_t>(layer_ptr(layer, DL_V_CACHE)), kvh, att_p0, att_rows);
+    };
+
+    // A phase's first units are issued when the phase begins, after the phase
+    // before has computed: a CU serves its waves' loads roughly in issue order,
+    // so loads for a later phase issued any earlier would delay the current
+    // phase's data in other waves.
     for (uint32_t layer = 0; layer < a.n_layers; ++layer) {
         const bool first = layer == 0, last = layer + 1 == a.n_layers;
         const uint32_t lsite = layer << 8;  // status code of a wait that gives up: layer and phase
@@ -893,26 +957,31 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         const uint32_t e_hprev = first ? 0u : dl_epoch(seq, layer - 1, DL_E_H_DOWN);
         DlOut out;
         out.hold.kind = -1;
-        // ---- Q|K|V: RMSNorm(h) . [Wq; Wk; Wv]^T
+        // ---- Q|K|V: RMSNorm(h) . [Wq; Wk; Wv]^T.  The attention K/V rows depend
+        // on nothing computed in this launch: they are issued with the Q|K|V
+        // weights, before h is awaited, and stream during that hand-off.
+        DlUnit<S::HSB, 1> uq[S::qkv_u];
+        DlAttnBank bk;
+        dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp>(uq, qkv_rows(layer));
+        issue_bank(layer, bk);
         out.ll32 = a.qkv_ll;
         out.e_out = e_qkv;
         dl_gemv_phase<S::HSB, 1, S::qkv_u, S::qkv_r, S::qkv_p, DL_EPI_STORE, true, qkv_sp>(
-            sm, qkv_rows(layer), first ? DL_SRC_PLAIN : DL_SRC_LL32,
+            sm, uq, qkv_rows(layer), first ? DL_SRC_PLAIN : DL_SRC_LL32,
             first ? static_cast<const void*>(a.h) : static_cast<const void*>(a.h_ll), e_hprev,
-            reinterpret_cast<const float*>(layer_ptr(layer, DL_IN_NORM)), a.eps, out, a.status, lsite | DL_W_QKV);
-        // ---- attention split: the K/V rows are loaded before q|k|v is awaited
+            dl_gptr<const float>(layer_ptr(layer, DL_IN_NORM)), a.eps, out, a.status, lsite | DL_W_QKV);
+        // ---- attention split
         {
             uint64_t lp[DL_LAYER_PTRS];
 #pragma unroll
             for (int i = 0; i < DL_LAYER_PTRS; ++i) lp[i] = layer_ptr(layer, i);
-            DlAttnBank bk;
-            dl_attn_issue(bk, reinterpret_cast<const uint16_t*>(lp[DL_K_CACHE]),
-                          reinterpret_cast<const uint16_t*>(lp[DL_V_CACHE]), kvh, att_p0, L);
             dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, pos, L, e_qkv, e_part, lsite);
         }
         // ---- attention merge (blocks 0..NH-1, one q head each)
         if (blockIdx.x < S::NH) dl_merge_phase<S>(sm.at, a, blockIdx.x, e_part, e_attn, lsite);
         // ---- o_proj + residual
+        DlUnit<S::QSB, 1> uo[S::o_u];
+        dl_issue_pre<S::QSB, 1, S::o_u, S::o_p, o_sp>(uo, o_rows(layer));
         out.ll32 = a.h_ll;
         out.plain = nullptr;
         out.hold.kind = first ? DL_SRC_PLAIN : DL_SRC_LL32;
@@ -920,14 +989,18 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         out.hold.e = e_hprev;
         out.e_out = e_ho;
         dl_gemv_phase<S::QSB, 1, S::o_u, S::o_r, S::o_p, DL_EPI_RESID, false, o_sp>(
-            sm, o_rows(layer), DL_SRC_LL16, a.attn_ll, e_attn, nullptr, a.eps, out, a.status, lsite | DL_W_O);
+            sm, uo, o_rows(layer), DL_SRC_LL16, a.attn_ll, e_attn, nullptr, a.eps, out, a.status, lsite | DL_W_O);
         // ---- RMSNorm + gate|up + SwiGLU
+        DlUnit<S::HSB, 2> ug[S::gu_u];
+        dl_issue_pre<S::HSB, 2, S::gu_u, S::gu_p, gu_sp>(ug, gu_rows(layer));
         out.ll16 = a.act_ll;
         out.e_out = e_act;
         dl_gemv_phase<S::HSB, 2, S::gu_u, S::gu_r, S::gu_p, DL_EPI_SWIGLU, true, gu_sp>(
-            sm, gu_rows(layer), DL_SRC_LL32, a.h_ll, e_ho,
-            reinterpret_cast<const float*>(layer_ptr(layer, DL_POST_NORM)), a.eps, out, a.status, lsite | DL_W_GU);
+            sm, ug, gu_rows(layer), DL_SRC_LL32, a.h_ll, e_ho,
+            dl_gptr<const float>(layer_ptr(layer, DL_POST_NORM)), a.eps, out, a.status, lsite | DL_W_GU);
         // ---- down + residual (the last layer writes the caller's h)
+        DlUnit<S::MSB, 1> ud[S::dn_u];
+        dl_issue_pre<S::MSB, 1, S::dn_u, S::dn_p, dn_sp>(ud, down_rows(layer));
         out.ll32 = a.h_ll;
         out.plain = last ? a.h : nullptr;
         out.hold.kind = DL_SRC_LL32;
@@ -935,7 +1008,8 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         out.hold.e = e_ho;
         out.e_out = e_hd;
         dl_gemv_phase<S::MSB, 1, S::dn_u, S::dn_r, S::dn_p, DL_EPI_RESID, false, dn_sp>(
-            sm, down_rows(layer), DL_SRC_LL16, a.act_ll, e_act, nullptr, a.eps, out, a.status, lsite | DL_W_DOWN);
+            sm, ud, down_rows(layer), DL_SRC_LL16, a.act_ll, e_act, nullptr, a.eps, out, a.status,
+            lsite | DL_W_DOWN);
     }
     // Every block has read the launch counter before block 0 can get here: its
     // last phase consumed every block's output.
@@ -1041,6 +1115,7 @@ extern "C" int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_l
     const bool is8b = dl_is<DlQwen3_8B>(hidden, mlp, nh, nk, d);
     if (!is8b && !dl_is<DlQwen3_0_6B>(hidden, mlp, nh, nk, d)) return T2H_ERR_UNSUPPORTED;
     if (n_layers == 0) return T2H_OK;
+    if (n_layers > DL_MAX_LAYERS) return T2H_ERR_UNSUPPORTED;
     if (s_cap == 0) return T2H_ERR_SHAPE;
     if ((size_t)(s_cap + DL_ATT_SLOTS * DL_WAVES - 1) / (DL_ATT_SLOTS * DL_WAVES) > DL_ATT_POS)
         return T2H_ERR_UNSUPPORTED;  // more than 32 positions per wave

@@ -108,6 +108,8 @@ class Qwen3Decoder:
             return f"shape hidden={c.hidden} mlp={c.mlp} heads={c.heads}/{c.kv_heads} d={c.head_dim} not built"
         if self.max_positions > 8192:
             return "KV capacity above 8192 positions"
+        if self.config.layers > 64:
+            return "more than 64 layers"
         for i in range(c.layers):
             for n in ("q", "k", "v", "o", "gate", "up", "down"):
                 if self.types[f"layers.{i}.{n}"] != "q4_k":
