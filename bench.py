@@ -34,6 +34,8 @@ PROFILES = Path(__file__).resolve().parent / "profiles"
 TRAFFIC_PROFILES = {
     "decode_layers_persistent": PROFILES / "decode_layers_qwen3_8b_int4_kv4096_pmc.md",
     "gate_up_rmsnorm_swiglu_gemv": PROFILES / "gate_up_gemv_qwen3_8b_pmc.md",
+    "prefill_gate_up_gemm": PROFILES / "gemm_swiglu_q8_0_m16384_pmc.md",
+    "asr_decode_layers_0_6b": PROFILES / "decode_layers_qwen3_0_6b_int4_kv1540_pmc.md",
 }
 PROMPT_POSITIONS = 4096
 
@@ -66,19 +68,46 @@ def parse_args():
     return p.parse_args()
 
 
-def profile_kernel_target(per_op: bool) -> int:
-    """Launch sequence for `rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE`: the dominant kernel twice over all
-    layers (the persistent layers kernel at KV 4096, 2 dispatches; or, per op, the gate|up GEMV once per
-    layer, 72 dispatches), then one plain 256 MiB device copy whose traffic is known (256 MiB read + 256 MiB
-    written), so counter readings can be scaled to bytes."""
+def profile_kernel_target(per_op: bool, config: str = "decode") -> int:
+    """Launch sequence for `rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE`: the dominant kernel of the config twice,
+    then one plain 256 MiB device copy whose traffic is known (256 MiB read + 256 MiB written), so counter
+    readings can be scaled to bytes.  decode: the persistent layers kernel at KV 4096 (2 dispatches), or per
+    op the gate|up GEMV once per layer (72 dispatches); prefill: the gate|up + SwiGLU GEMM at M 16384 (2
+    dispatches); asr: the 0.6B-shape persistent layers kernel at KV 1540 (2 dispatches)."""
     import torch
 
     from torch2vk_amd import kernels
-    from torch2vk_amd.qwen3.config import QWEN3_8B
+    from torch2vk_amd.qwen3.config import QWEN3_0_6B, QWEN3_8B
     from torch2vk_amd.qwen3.model import Qwen3Decoder
     from torch2vk_amd.qwen3.weights import synthetic_weights
 
     dev = torch.device("cuda:0")
+    if config == "prefill":
+        c = QWEN3_8B
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(0)
+        gate = kernels.quantize(torch.randn(c.mlp, c.hidden, generator=gen, device=dev) * 0.02, "q8_0")
+        up = kernels.quantize(torch.randn(c.mlp, c.hidden, generator=gen, device=dev) * 0.02, "q8_0")
+        x = torch.randn(8 * 2048, c.hidden, generator=gen, device=dev).to(torch.bfloat16)
+        act = torch.empty(8 * 2048, c.mlp, dtype=torch.bfloat16, device=dev)
+        for _ in range(2):
+            kernels.gemm_swiglu(x, gate, up, "q8_0", out=act)
+        _profile_copy(dev)
+        return 0
+    if config == "asr":
+        w = synthetic_weights(QWEN3_0_6B, device=dev, seed=2)
+        dec = Qwen3Decoder(w, max_positions=1600, max_new_tokens=4, device=dev, persistent=True)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1)
+        dec.k_cache[:, :1539].normal_(generator=gen)
+        dec.v_cache[:, :1539].normal_(generator=gen)
+        dec.h.normal_()
+        dec.position.fill_(1539)
+        for _ in range(2):
+            dec.run_decode_layers()
+        dec.check_status()
+        _profile_copy(dev)
+        return 0
     w = synthetic_weights(QWEN3_8B, device=dev, seed=0)
     if per_op:
         dec = Qwen3Decoder(w, max_positions=64, max_new_tokens=4, device=dev, persistent=False)
@@ -98,12 +127,19 @@ def profile_kernel_target(per_op: bool) -> int:
         for _ in range(2):
             dec.run_decode_layers()
         dec.check_status()
+    _profile_copy(dev)
+    return 0
+
+
+def _profile_copy(dev) -> None:
+    """The calibration launch of a counter run: one plain 256 MiB device-to-device copy."""
+    import torch
+
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
     print("[bench] profile-kernel target done", file=sys.stderr, flush=True)
-    return 0
 
 
 def main() -> int:
@@ -116,7 +152,7 @@ def main() -> int:
     if args.warmup is None:
         args.warmup = 16 if args.config == "decode" else 1
     if args.profile_kernel:
-        return profile_kernel_target(args.per_op)
+        return profile_kernel_target(args.per_op, args.config)
     if args.config == "prefill":
         return bench_prefill(args)
     if args.config == "asr":
@@ -256,6 +292,18 @@ def _graph_us_per_call(calls, reps: int) -> float:
     return us
 
 
+def persistent_bytes(weights, c, kv_len: int) -> int:
+    """Algorithmic bytes of one persistent decode launch: each layer's packed weights and norms, the K/V rows
+    0 .. kv_len - 1 read and the new row written, and the residual stream in and out."""
+    b = 0
+    for i in range(c.layers):
+        b += sum(weights.packed[f"layers.{i}.{n}"].numel() for n in ("q", "k", "v", "o", "gate", "up", "down"))
+        b += sum(weights.norms[f"layers.{i}.{n}"].numel() * 4 for n in ("input_norm", "post_norm", "q_norm",
+                                                                          "k_norm"))
+    b += c.layers * (2 * kv_len * c.kv_dim * 2 + 2 * c.kv_dim * 2) + 2 * c.hidden * 4
+    return int(b)
+
+
 def kernel_timing(dec, weights, reps: int) -> dict:
     """Per-launch timing of each decode kernel class: each class's launches over all layers' weights
     captured in one HIP graph (as in the decode step, so launch gaps match it) and replayed `reps` times."""
@@ -312,12 +360,7 @@ def kernel_timing(dec, weights, reps: int) -> dict:
         # and the new row written, the residual stream in and out
         name = "decode_layers_persistent"
         us = _graph_us_per_call([dec.run_decode_layers] * 2, reps)
-        b = 0
-        for i in range(L):
-            b += sum(wb(f"layers.{i}.{n}") for n in ("q", "k", "v", "o", "gate", "up", "down"))
-            b += sum(weights.norms[f"layers.{i}.{n}"].numel() * 4 for n in ("input_norm", "post_norm", "q_norm",
-                                                                              "k_norm"))
-        b += L * (2 * kv_len * c.kv_dim * 2 + 2 * c.kv_dim * 2) + 2 * c.hidden * 4
+        b = persistent_bytes(weights, c, kv_len)
         per_launch_us[name] = round(us, 3)
         bytes_per[name] = int(b)
         gbs[name] = b / (us * 1e-6) / 1e9
@@ -528,7 +571,11 @@ def bench_prefill(args) -> int:
     print(f"[bench] prefill {per_step * 1e3:.1f} ms per 8 x 2048 tokens: {tok_s:.0f} tok/s, {tflops:.1f} TFLOP/s",
           file=sys.stderr, flush=True)
 
-    # dominant kernel: the MLP up-projection GEMM (M 16384, K 4096, N 12288), HIP events on its stream
+    # dominant kernel of the step: gate|up + SwiGLU in one GEMM (M 16384, K 4096, 2 x 12288 rows), HIP events
+    # on its stream; the standalone up-projection GEMM the config names is timed beside it
+    gu_us = _events_us(lambda: kernels.gemm_swiglu(x, layers[0]["gate"], layers[0]["up"], "q8_0", out=act),
+                       args.kernel_reps * 4)
+    gu_tflops = 2.0 * m * c.hidden * 2 * c.mlp / (gu_us * 1e-6) / 1e12
     gemm_us = _events_us(lambda: kernels.gemm(x, layers[0]["up"], "q8_0", out=up), args.kernel_reps * 4)
     gemm_tflops = 2.0 * m * c.hidden * c.mlp / (gemm_us * 1e-6) / 1e12
     fa_us = _events_us(lambda: kernels.flash_attn_prefill(qb.view(nb, tl, c.heads, c.head_dim), kc, vc, out=attn,
@@ -559,14 +606,17 @@ def bench_prefill(args) -> int:
         "achieved_tflops": round(tflops, 1),
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_q_kernel<GemmQ80> (MLP up-projection, M 16384 K 4096 N 12288)",
-            "achieved": round(gemm_tflops, 1),
+            "kernel": "gemm_q_kernel<GemmQ80, SwiGLU epilogue> (gate|up, M 16384 K 4096 N 2 x 12288)",
+            "achieved": round(gu_tflops, 1),
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(gemm_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
-            "avg_launch_us": round(gemm_us, 1),
+            "frac": round(gu_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": profiled_traffic(TRAFFIC_PROFILES["prefill_gate_up_gemm"]),
+            "traffic_source": TRAFFIC_PROFILES["prefill_gate_up_gemm"].name,
+            "avg_launch_us": round(gu_us, 1),
         },
+        "up_projection_gemm": {"kernel": "gemm_q_kernel<GemmQ80> (M 16384 K 4096 N 12288)",
+                               "avg_launch_us": round(gemm_us, 1), "tflops": round(gemm_tflops, 1)},
         "flash_attention": {"avg_launch_us": round(fa_us, 1), "tflops": round(fa_tflops, 1)},
         "cpu_baseline": cpu,
     }
@@ -686,6 +736,13 @@ def bench_asr(args) -> int:
     y = torch.empty(nb * frames, f, dtype=torch.bfloat16, device=dev)
     fc1_us = _events_us(lambda: kernels.q8_0_linear(x_ln, fc1, bias=b1, act="gelu", out=y), args.kernel_reps * 4)
     fc1_tflops = 2.0 * nb * frames * d * f / (fc1_us * 1e-6) / 1e12
+    # dominant kernel of the step: the decoder's persistent launch (all 28 layers of a token), timed at the
+    # middle of the generated span
+    dec.position.fill_(prompt_len + new_tokens // 2)
+    kv_len = prompt_len + new_tokens // 2 + 1
+    dl_us = _graph_us_per_call([dec.run_decode_layers] * 2, args.kernel_reps * 4) if dec.persistent else None
+    dl_bytes = persistent_bytes(tw, tcfg, kv_len)
+    dec.check_status()
     print(f"[bench] asr step {per_step * 1e3:.1f} ms ({frames_s:.0f} frames/s); encoder {enc_s * 1e3:.2f} ms, "
           f"{enc_tflops:.1f} TFLOP/s; fc1 {fc1_us:.1f} us {fc1_tflops:.1f} TFLOP/s; tokens {len(transcripts[0])}",
           file=sys.stderr, flush=True)
@@ -716,15 +773,20 @@ def bench_asr(args) -> int:
         "encoder_tflops": round(enc_tflops, 1),
         "mfma_utilisation": round(enc_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         "roofline": {
-            "bound": "mfma",
-            "kernel": "gemm_q_kernel<GemmQ80> (encoder fc1 + bias + GELU, M 6000 K 1024 N 4096)",
-            "achieved": round(fc1_tflops, 1),
-            "peak": MFMA_BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(fc1_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
-            "avg_launch_us": round(fc1_us, 1),
+            "bound": "hbm",
+            "kernel": f"decode_layers_kernel<DlQwen3_0_6B> (28 layers of a decoder token, KV {kv_len})",
+            "achieved": round(dl_bytes / (dl_us * 1e-6) / 1e9, 1) if dl_us else None,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dl_bytes / (dl_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if dl_us else None,
+            "traffic": profiled_traffic(TRAFFIC_PROFILES["asr_decode_layers_0_6b"]),
+            "traffic_source": TRAFFIC_PROFILES["asr_decode_layers_0_6b"].name,
+            "avg_launch_us": round(dl_us, 1) if dl_us else None,
+            "bytes_per_launch": dl_bytes,
         },
+        "encoder_fc1": {"kernel": "gemm_q_kernel<GemmQ80> (fc1 + bias + GELU, M 6000 K 1024 N 4096)",
+                        "avg_launch_us": round(fc1_us, 1), "tflops": round(fc1_tflops, 1),
+                        "mfma_frac": round(fc1_tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
