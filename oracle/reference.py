@@ -158,9 +158,13 @@ class Qwen3CpuModel:
         return x * cos + rot * sin
 
     def forward(self, tokens: torch.Tensor, start: int, layers: int | None = None,
-                embeds: torch.Tensor | None = None) -> torch.Tensor:
+                embeds: torch.Tensor | None = None, mask: torch.Tensor | None = None,
+                all_positions: bool = False) -> torch.Tensor:
         """Run T tokens at positions start..start+T-1, fill the KV cache, return last hidden [H] (post final norm).
-        ``embeds`` [T, H] replaces the embedding lookup (a prompt with injected audio features)."""
+        ``embeds`` [T, H] replaces the embedding lookup (a prompt with injected audio features).  ``mask``: an
+        additive fp32 [T, start + T] attention mask used instead of the causal one (OmniVoice's LLM pass,
+        src/models/quantized_omnivoice/dispatch/llm_forward.py:19-70 with SDPA_MASKED_F32); ``all_positions``
+        returns every position's final-normed hidden [T, H] (that pass's output, llm_forward.py:70)."""
         s = self.shape
         w = self.w
         t_len = tokens.shape[0] if embeds is None else embeds.shape[0]
@@ -181,8 +185,11 @@ class Qwen3CpuModel:
             keys = self.k_cache[i, :start + t_len].repeat_interleave(group, dim=1)
             vals = self.v_cache[i, :start + t_len].repeat_interleave(group, dim=1)
             scores = torch.einsum("thd,shd->hts", q.float(), keys.float()) / math.sqrt(s.head_dim)
-            allowed = torch.arange(start + t_len)[None, :] <= positions[:, None]
-            scores = scores.masked_fill(~allowed[None], float("-inf"))
+            if mask is None:
+                allowed = torch.arange(start + t_len)[None, :] <= positions[:, None]
+                scores = scores.masked_fill(~allowed[None], float("-inf"))
+            else:
+                scores = scores + mask.float()[None]
             probs = torch.softmax(scores, dim=-1)
             attn = torch.einsum("hts,shd->thd", probs, vals.float()).to(self.dtype).reshape(t_len, -1)
             h = h + attn @ w[p + "o"].T
@@ -190,7 +197,7 @@ class Qwen3CpuModel:
             g = x @ w[p + "gate"].T
             u = x @ w[p + "up"].T
             h = h + (torch.nn.functional.silu(g) * u) @ w[p + "down"].T
-        return self._rms(h[-1], w["norm"])
+        return self._rms(h, w["norm"]) if all_positions else self._rms(h[-1], w["norm"])
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
         return hidden @ self.w["lm_head"].T

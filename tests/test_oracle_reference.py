@@ -113,3 +113,35 @@ def test_cpu_decoder_matches_transformers_qwen3():
     for t in (5, 6):
         h = ours.forward(tokens[t:t + 1], start=t)
         torch.testing.assert_close(ours.logits(h), ref[t], rtol=1e-4, atol=1e-6)
+
+
+def test_cpu_masked_forward_matches_transformers_qwen3():
+    """The oracle's masked full-sequence pass (OmniVoice's LLM forward: an additive mask instead of causal,
+    every position's final-normed hidden) against transformers given the same 4D additive mask; and with the
+    causal mask written out additively it reproduces the oracle's own causal path exactly."""
+    shape = R.Qwen3Shape(hidden=64, layers=2, heads=4, kv_heads=2, head_dim=32, mlp=96, vocab=120, rope_theta=1e6)
+    hf = _hf_model(shape, seed=4)
+    dense = _dense_from_hf(hf, shape)
+    tokens = torch.tensor([5, 17, 99, 3, 64, 2, 110])
+    t = tokens.numel()
+    big = -1e30
+    mask = torch.zeros(t, t, dtype=torch.float64)
+    mask[:, 5:] = big                # two padded keys hidden from every query
+    mask[5:, :] = 0.0                # ... except from the padded queries themselves
+    mask[0, 3] = big                 # and one arbitrary hole
+    with torch.no_grad():
+        ref = hf.model(input_ids=tokens[None], attention_mask=mask[None, None]).last_hidden_state[0]
+    ours = R.Qwen3CpuModel(shape, dense, max_positions=32, dtype=torch.float64)
+    got = ours.forward(tokens, 0, mask=mask, all_positions=True)
+    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-6)
+    # bidirectional: a later token changes an earlier position's output (it would not under causality)
+    other = R.Qwen3CpuModel(shape, dense, max_positions=32, dtype=torch.float64)
+    changed = other.forward(torch.tensor([5, 17, 99, 3, 64, 2, 111]), 0, mask=torch.zeros(t, t, dtype=torch.float64),
+                            all_positions=True)
+    same = R.Qwen3CpuModel(shape, dense, max_positions=32, dtype=torch.float64)
+    base = same.forward(tokens, 0, mask=torch.zeros(t, t, dtype=torch.float64), all_positions=True)
+    assert (changed[0] - base[0]).abs().max() > 1e-6
+    causal = torch.triu(torch.full((t, t), big, dtype=torch.float64), diagonal=1)
+    a = R.Qwen3CpuModel(shape, dense, max_positions=32, dtype=torch.float64)
+    b = R.Qwen3CpuModel(shape, dense, max_positions=32, dtype=torch.float64)
+    torch.testing.assert_close(a.forward(tokens, 0, mask=causal), b.forward(tokens, 0), rtol=0, atol=1e-12)

@@ -311,11 +311,12 @@ class Qwen3Decoder:
         rows = q.shape[0] + k.shape[0] + v.shape[0]
         return q.as_strided((rows, q.shape[1]), (q.shape[1], 1))
 
-    def _prefill_layer(self, i: int, h: torch.Tensor, start: int) -> None:
+    def _prefill_layer(self, i: int, h: torch.Tensor, start: int, mask: torch.Tensor | None = None) -> None:
         """One layer over a chunk's fp32 residual stream h [n, hidden] at positions start.. (run_text_layer,
         src/models/optimized_qwen3/dispatch/text_layer.py): RMSNorm rows -> q|k|v GEMM -> q/k norm + RoPE +
         KV cache write -> causal flash attention over the cache -> o GEMM + residual -> RMSNorm -> gate|up
-        GEMM with SwiGLU in its epilogue -> down GEMM + residual.  GEMMs run on the matrix cores for any chunk length."""
+        GEMM with SwiGLU in its epilogue -> down GEMM + residual.  GEMMs run on the matrix cores for any chunk length.
+        ``mask`` (additive fp32 [1, n, start + n]) replaces causality in the attention."""
         c, t, p = self.config, self.types, f"layers.{i}."
         n = h.shape[0]
         x = kernels.rms_norm(h, self._n(p + "input_norm"), out=torch.empty(n, c.hidden, dtype=torch.bfloat16,
@@ -332,7 +333,10 @@ class Qwen3Decoder:
                                    theta=c.rope_theta, eps=c.rms_eps)
         keys = self.k_cache[i, :start + n].unsqueeze(0)
         vals = self.v_cache[i, :start + n].unsqueeze(0)
-        attn = kernels.flash_attn_prefill(qb.unsqueeze(0), keys, vals, causal=True, causal_offset=start)
+        if mask is None:
+            attn = kernels.flash_attn_prefill(qb.unsqueeze(0), keys, vals, causal=True, causal_offset=start)
+        else:
+            attn = kernels.flash_attn_prefill(qb.unsqueeze(0), keys, vals, causal=False, mask=mask)
         kernels.gemm(attn.view(n, c.q_dim), self._w(p + "o"), t[p + "o"], out=h, residual=h)
         x = kernels.rms_norm(h, self._n(p + "post_norm"), out=x, eps=c.rms_eps)
         if t[p + "gate"] == t[p + "up"]:
@@ -343,6 +347,23 @@ class Qwen3Decoder:
             act = kernels.swiglu(gate, up)
             del gate, up
         kernels.gemm(act, self._w(p + "down"), t[p + "down"], out=h, residual=h)
+
+    def forward_masked(self, embeds: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """OmniVoice's LLM pass (src/models/quantized_omnivoice/dispatch/llm_forward.py:19-70): every layer over
+        the whole sequence of input embeddings [T, hidden] at positions 0..T-1, attention under the additive
+        mask [T, T] (SDPA_MASKED_F32; -inf where a key is hidden) instead of causality, then the final RMSNorm
+        of every position -> fp32 [T, hidden].  The layers' K/V go to rows 0..T-1 of the KV cache.  The same
+        kernels as the chunked prefill: matrix-core GEMMs of each weight's type and masked flash attention."""
+        c = self.config
+        e = embeds.to(device=self.device, dtype=torch.float32).reshape(-1, c.hidden)
+        t_len = e.shape[0]
+        if t_len > self.max_positions:
+            raise ValueError(f"{t_len} positions exceed the KV capacity {self.max_positions}")
+        m = mask.to(device=self.device, dtype=torch.float32).reshape(1, t_len, t_len).contiguous()
+        h = e.clone()
+        for i in range(c.layers):
+            self._prefill_layer(i, h, 0, mask=m)
+        return kernels.rms_norm(h, self._n("norm"), out=torch.empty_like(h), eps=c.rms_eps)
 
     def prefill_chunked(self, prompt_ids: torch.Tensor | None = None, *, embeds: torch.Tensor | None = None,
                         start: int = 0, chunk: int = 2048) -> None:
