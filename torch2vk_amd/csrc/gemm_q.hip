@@ -34,7 +34,10 @@ constexpr int GQ_THREADS = 512;
 constexpr int GQ_BN = 256;
 constexpr int GQ_BK = 64;
 constexpr int GQ_LDS_ROW = GQ_BK + 8;  // bf16 elements per padded LDS row
-constexpr int GQ_GROUP_M = 8;
+#ifndef GQ_GROUP_M_DEF
+#define GQ_GROUP_M_DEF 8
+#endif
+constexpr int GQ_GROUP_M = GQ_GROUP_M_DEF;  // tiles per group down M (4 and 8 measured fastest)
 
 enum GemmEpilogue { GQEPI_F32 = 0, GQEPI_BF16 = 1, GQEPI_RESID = 2, GQEPI_SWIGLU = 3 };
 
