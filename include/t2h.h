@@ -285,6 +285,19 @@ int t2h_im2col(const void* x, int x_dtype, const int64_t* x_strides, uint32_t ba
                uint32_t in_h, uint32_t in_w, uint32_t kh, uint32_t kw, uint32_t stride_h, uint32_t stride_w,
                uint32_t pad_h, uint32_t pad_w, uint32_t out_h, uint32_t out_w, void* out, uint32_t out_cols,
                void* stream);
+/* conv1d taps of x [B, C, L] (fp32 or bf16, any element strides x_strides[3] = b, c, l): bf16 out
+ * [B * out_len, out_cols], row b * out_len + t, column c * K + k = x[b, c, t * stride + k * dilation - pad]
+ * (zero outside the input); columns past C * K are zero.  With a Q8_0 GEMM over [Co, C * K] weight rows
+ * (t2h_q8_0_linear) this is CONV1D_Q8_0W_F32B_F32 (src/models/quantized_omnivoice/shaders/
+ * conv1d_q8_0w_f32b_f32.py: conv_input_value, q8_0_value_prepared), stride, padding and dilation included. */
+int t2h_im2col_1d(const void* x, int x_dtype, const int64_t* x_strides, uint32_t batch, uint32_t channels,
+                  uint32_t length, uint32_t k, uint32_t stride, uint32_t pad, uint32_t dilation, uint32_t out_len,
+                  void* out, uint32_t out_cols, void* stream);
+/* Snake activation over channels-last fp32 rows [rows, C]: out = x + sin(alpha_c x)^2 / (alpha_c + eps).
+ * Replaces ADD_SCALAR + RECIPROCAL_F32 + AUDIO_DECODE_MUL_BROADCAST + SIN_F32 + POW_SCALAR_F16 + ADD
+ * (src/models/quantized_omnivoice/dispatch/audio_decode.py:151-161; eps 1e-9, add_scalar.py:43). */
+int t2h_snake(const float* x, const float* alpha, float* out, uint64_t rows, uint32_t channels, float eps,
+              void* stream);
 /* out = (x - mean) / sqrt(var + eps) * w + b per row (biased variance, two passes); x, out fp32 or bf16,
  * cols % 4 == 0, 16-B aligned.  replaces LAYER_NORM_F32W_F32B_F32
  * (src/models/quantized_qwen3_asr/shaders/layer_norm_f32w_f32b_f32.py:20-105). */

@@ -1,0 +1,95 @@
+"""GPU parity of the OmniVoice audio-decoder operators against oracle/omnivoice.py: the conv1d taps
+(bit-exact), conv1d with Q8_0 weights at the decoder's kernel sizes and dilations, the snake activation, and
+a whole residual unit (snake -> dilated conv k7 -> snake -> conv k1 -> + x)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import omnivoice as O
+from oracle import reference as R
+from tests.conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(a: np.ndarray) -> np.ndarray:
+    return R.bf16_round(np.asarray(a, np.float32)).astype(np.float64)
+
+
+@pytest.mark.parametrize("k,stride,pad,dil", [(7, 1, 3, 1), (7, 1, 27, 9), (1, 1, 0, 1), (4, 3, 2, 2)])
+def test_im2col_1d_bit_exact(device, k, stride, pad, dil):
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(k + 10 * dil)
+    b, length, c = 2, 37, 24
+    x = rng.standard_normal((b, length, c)).astype(np.float32)
+    cols = kernels.im2col_1d(torch.from_numpy(x).to(device), k, stride=stride, padding=pad, dilation=dil)
+    got = cols.float().cpu().numpy()
+    ref = O.conv1d_taps(_bf16(x).transpose(0, 2, 1), k, stride, pad, dil)
+    assert got.shape[0] == ref.shape[0] and got.shape[1] % 64 == 0
+    assert np.array_equal(got[:, :c * k], ref)
+    assert not got[:, c * k:].any()
+
+
+@pytest.mark.parametrize("c,co,k,pad,dil", [(96, 64, 7, 3, 1), (64, 64, 7, 27, 9), (128, 96, 1, 0, 1)])
+def test_conv1d_q8_0_matches_oracle(device, c, co, k, pad, dil):
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(c + co + dil)
+    b, length = 2, 50
+    x = rng.standard_normal((b, length, c)).astype(np.float32)
+    w = (rng.standard_normal((co, c * k)) * 0.05).astype(np.float32)
+    bias = rng.standard_normal(co).astype(np.float32)
+    packed = kernels.quantize(torch.from_numpy(w).to(device), "q8_0")
+    dense = oracle.dequant_q8_0(packed.cpu().numpy(), c * k)
+    y = kernels.conv1d_q8_0(torch.from_numpy(x).to(device), packed, torch.from_numpy(bias).to(device), k,
+                            padding=pad, dilation=dil)
+    ref = O.conv1d_ref(_bf16(x).transpose(0, 2, 1), dense, bias, k, 1, pad, dil).transpose(0, 2, 1)
+    got = y.cpu().numpy()
+    print(f"conv1d c={c} co={co} k={k} dil={dil}: max-abs {np.abs(got - ref).max():.3e}", flush=True)
+    # the GEMM stages dequantized weights as bf16: ~2^-9 relative per weight
+    assert_close(got, ref, max_abs=1e-2 * float(np.abs(ref).max()), min_cos=0.9999, what="conv1d")
+
+
+def test_snake_matches_oracle(device):
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((3, 41, 80)) * 3).astype(np.float32)
+    alpha = np.abs(rng.standard_normal(80)).astype(np.float32) + 0.1
+    y = kernels.snake(torch.from_numpy(x).to(device), torch.from_numpy(alpha).to(device)).cpu().numpy()
+    ref = O.snake_ref(x, alpha, channel_axis=2)
+    assert_close(y, ref, max_abs=2e-5 * float(np.abs(ref).max()), min_cos=0.9999999, what="snake")
+
+
+@pytest.mark.parametrize("dil", [1, 3, 9])
+def test_residual_unit_matches_oracle(device, dil):
+    """The decoder's residual unit: y = x + conv_k1(snake2(conv_k7,dil(snake1(x)))), lengths preserved."""
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(20 + dil)
+    b, length, c = 1, 64, 64
+    x = rng.standard_normal((b, length, c)).astype(np.float32)
+    a1, a2 = (np.abs(rng.standard_normal(c)).astype(np.float32) + 0.2 for _ in range(2))
+    w1 = (rng.standard_normal((c, c * 7)) * 0.03).astype(np.float32)
+    w2 = (rng.standard_normal((c, c)) * 0.1).astype(np.float32)
+    b1, b2 = (rng.standard_normal(c).astype(np.float32) * 0.1 for _ in range(2))
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    p1, p2 = kernels.quantize(t(w1), "q8_0"), kernels.quantize(t(w2), "q8_0")
+    xd = t(x)
+    s1 = kernels.snake(xd, t(a1))
+    h1 = kernels.conv1d_q8_0(s1, p1, t(b1), 7, padding=3 * dil, dilation=dil)
+    s2 = kernels.snake(h1, t(a2))
+    y = kernels.conv1d_q8_0(s2, p2, t(b2), 1, residual=xd).cpu().numpy()
+    d1, d2 = oracle.dequant_q8_0(p1.cpu().numpy(), c * 7), oracle.dequant_q8_0(p2.cpu().numpy(), c)
+    xr = x.transpose(0, 2, 1).astype(np.float64)
+    r1 = O.conv1d_ref(_bf16(O.snake_ref(xr, a1)), d1, b1, 7, 1, 3 * dil, dil)
+    r2 = O.conv1d_ref(_bf16(O.snake_ref(r1, a2)), d2, b2, 1)
+    ref = (xr + r2).transpose(0, 2, 1)
+    assert y.shape == ref.shape
+    print(f"residual unit dil={dil}: max-abs {np.abs(y - ref).max():.3e}", flush=True)
+    assert_close(y, ref, max_abs=2e-2 * float(np.abs(ref).max()), min_cos=0.9999, what="residual unit")

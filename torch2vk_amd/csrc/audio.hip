@@ -30,6 +30,7 @@ struct Im2colArgs {
     uint32_t out_cols;       // row length of the output (>= channels * kh * kw)
     uint32_t pad_threads;    // threads per row that zero the columns past channels * kh * kw
     uint64_t rows;           // batch * out_h * out_w
+    uint32_t dil_w;          // tap spacing along w (1: plain conv)
 };
 
 template <typename T>
@@ -72,7 +73,7 @@ __global__ __launch_bounds__(256) void im2col_kernel(const T* __restrict__ x, ui
         const int ih = (int)(oh * a.stride_h + fh) - (int)a.pad_h;
         const bool h_ok = ih >= 0 && ih < (int)a.in_h;
         for (uint32_t fw = 0; fw < a.kw; ++fw) {
-            const int iw = (int)(ow * a.stride_w + fw) - (int)a.pad_w;
+            const int iw = (int)(ow * a.stride_w + fw * a.dil_w) - (int)a.pad_w;
             uint16_t v = 0;
             if (h_ok && iw >= 0 && iw < (int)a.in_w) v = to_bf16_bits<T>(xc[(int64_t)ih * a.sh + (int64_t)iw * a.sw]);
             dst[fh * a.kw + fw] = v;
@@ -240,6 +241,7 @@ extern "C" int t2h_im2col(const void* x, int x_dtype, const int64_t* x_strides, 
     a.stride_w = stride_w;
     a.pad_h = pad_h;
     a.pad_w = pad_w;
+    a.dil_w = 1;
     a.out_h = out_h;
     a.out_w = out_w;
     a.out_cols = out_cols;
@@ -367,6 +369,86 @@ extern "C" int t2h_embedding_q8_0(const void* w, uint64_t vocab, const int64_t* 
     hipLaunchKernelGGL(embedding_q8_0_kernel, dim3(grid_for(threads)), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const uint8_t*>(w), vocab, ids, n_ids,
                        dim, out);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+// conv1d taps of x [B, C, L] (any strides): row b * out_len + t holds
+// x[b, c, t * stride + k * dilation - pad] at column c * K + k (zero outside
+// the input), the reference conv1d's operand order
+// (src/models/quantized_omnivoice/shaders/conv1d_q8_0w_f32b_f32.py, conv_input_value);
+// columns past C * K are zero.  The 2-D kernel with one row.
+extern "C" int t2h_im2col_1d(const void* x, int x_dtype, const int64_t* x_strides, uint32_t batch, uint32_t channels,
+                             uint32_t length, uint32_t k, uint32_t stride, uint32_t pad, uint32_t dilation,
+                             uint32_t out_len, void* out, uint32_t out_cols, void* stream) {
+    if (!x || !x_strides || !out) return T2H_ERR_NULL;
+    if (x_dtype != T2H_DTYPE_F32 && x_dtype != T2H_DTYPE_BF16) return T2H_ERR_DTYPE;
+    if (k == 0 || stride == 0 || dilation == 0 || channels == 0) return T2H_ERR_SHAPE;
+    if ((uint64_t)channels * k > out_cols) return T2H_ERR_SHAPE;
+    if (out_len > 0 && (uint64_t)(out_len - 1) * stride > (uint64_t)length + 2 * pad) return T2H_ERR_SHAPE;
+    if (length > 0x7fffffffu || pad > 0xffffu || (uint64_t)(k - 1) * dilation > 0x7fffffffu) return T2H_ERR_SHAPE;
+    for (int i = 0; i < 3; ++i)
+        if (x_strides[i] < 0) return T2H_ERR_ARG;
+    Im2colArgs a;
+    a.sb = x_strides[0];
+    a.sc = x_strides[1];
+    a.sh = 0;
+    a.sw = x_strides[2];
+    a.channels = channels;
+    a.in_h = 1;
+    a.in_w = length;
+    a.kh = 1;
+    a.kw = k;
+    a.stride_h = 1;
+    a.stride_w = stride;
+    a.pad_h = 0;
+    a.pad_w = pad;
+    a.dil_w = dilation;
+    a.out_h = 1;
+    a.out_w = out_len;
+    a.out_cols = out_cols;
+    a.pad_threads = (out_cols - channels * k + 7) / 8;
+    a.rows = (uint64_t)batch * out_len;
+    const uint64_t threads = a.rows * ((uint64_t)channels + a.pad_threads);
+    if (threads == 0) return T2H_OK;
+    if (threads / 256 >= 0x7fffffffu) return T2H_ERR_SHAPE;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    uint16_t* o = reinterpret_cast<uint16_t*>(out);
+    if (x_dtype == T2H_DTYPE_F32)
+        hipLaunchKernelGGL(im2col_kernel<float>, dim3(grid_for(threads)), dim3(256), 0, s,
+                           reinterpret_cast<const float*>(x), o, a);
+    else
+        hipLaunchKernelGGL(im2col_kernel<uint16_t>, dim3(grid_for(threads)), dim3(256), 0, s,
+                           reinterpret_cast<const uint16_t*>(x), o, a);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+// ----------------------------------------------------------------- snake --
+
+// y = x + sin(alpha_c x)^2 / (alpha_c + eps) per channel c of channels-last
+// rows [rows, C]: the snake activation of the audio decoder, built in the
+// reference from ADD_SCALAR (eps 1e-9), RECIPROCAL, MUL_BROADCAST, SIN and
+// POW_SCALAR (src/models/quantized_omnivoice/dispatch/audio_decode.py:151-161).
+__global__ __launch_bounds__(256) void snake_kernel(const float* __restrict__ x, const float* __restrict__ alpha,
+                                                    float* __restrict__ y, uint64_t n, uint32_t channels, float eps) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float a = alpha[i % channels];
+    const float v = x[i];
+    const float s = sinf(a * v);
+    y[i] = v + (1.0f / (a + eps)) * (s * s);
+}
+
+extern "C" int t2h_snake(const float* x, const float* alpha, float* out, uint64_t rows, uint32_t channels, float eps,
+                         void* stream) {
+    if (!x || !alpha || !out) return T2H_ERR_NULL;
+    if (channels == 0) return T2H_ERR_SHAPE;
+    const uint64_t n = rows * channels;
+    if (n == 0) return T2H_OK;
+    if (n / 256 >= 0x7fffffffu) return T2H_ERR_SHAPE;
+    hipLaunchKernelGGL(snake_kernel, dim3(grid_for(n)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), x, alpha,
+                       out, n, channels, eps);
     T2H_LAUNCH_CHECK();
     return T2H_OK;
 }

@@ -793,3 +793,68 @@ def embedding_q8_0(w: torch.Tensor, ids: torch.Tensor, dim: int, out: torch.Tens
     _check(out, "output", torch.float32)
     call("t2h_embedding_q8_0", ptr(w), int(w.shape[0]), ptr(ids), ids.numel(), dim, ptr(out), stream_handle())
     return out
+
+
+SNAKE_EPS = 1e-9  # add_scalar.py:43 of the reference's OmniVoice decoder
+
+
+def conv1d_out_len(length: int, kernel: int, stride: int = 1, padding: int = 0, dilation: int = 1) -> int:
+    return (length + 2 * padding - dilation * (kernel - 1) - 1) // stride + 1
+
+
+def im2col_1d(x: torch.Tensor, kernel: int, *, stride: int = 1, padding: int = 0, dilation: int = 1,
+              out_cols: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """conv1d taps of x [B, L, C] (channels-last, fp32 or bf16, any strides) -> bf16 [B * Lo, out_cols], column
+    c * K + k = x[b, t * stride + k * dilation - padding, c] (zero outside); columns past C * K are zero
+    (out_cols defaults to C * K rounded up to 64, the GEMM's K step)."""
+    if not isinstance(x, torch.Tensor) or x.device.type != "cuda":
+        raise ValueError("x must be a tensor on a HIP device")
+    if x.dtype not in _IN_DTYPES:
+        raise TypeError(f"x dtype {x.dtype} not in {tuple(_IN_DTYPES)}")
+    if x.dim() != 3:
+        raise ValueError(f"x must be [B, L, C], got {tuple(x.shape)}")
+    b, length, c = (int(d) for d in x.shape)
+    lo = conv1d_out_len(length, kernel, stride, padding, dilation)
+    if lo < 1:
+        raise ValueError("empty conv1d output")
+    cols = out_cols if out_cols is not None else (c * kernel + 63) // 64 * 64
+    if out is None:
+        out = torch.empty(b * lo, cols, dtype=torch.bfloat16, device=x.device)
+    _check(out, "output", torch.bfloat16)
+    if tuple(out.shape) != (b * lo, cols):
+        raise ValueError(f"output must be {(b * lo, cols)}, got {tuple(out.shape)}")
+    strides = (_lib.ctypes.c_int64 * 3)(x.stride(0), x.stride(2), x.stride(1))
+    call("t2h_im2col_1d", ptr(x), _IN_DTYPES[x.dtype], strides, b, c, length, kernel, stride, padding, dilation, lo,
+         ptr(out), cols, stream_handle())
+    return out
+
+
+def conv1d_q8_0(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, kernel: int, *, stride: int = 1,
+                padding: int = 0, dilation: int = 1, out_dtype: torch.dtype = torch.float32,
+                residual: torch.Tensor | None = None) -> torch.Tensor:
+    """CONV1D_Q8_0W_F32B_F32 on channels-last activations: x [B, L, C] -> [B, Lo, Co], W the reference's Q8_0
+    rows [Co, C * K] (column c * K + k), bias fp32 [Co]; im2col_1d then the Q8_0 GEMM with the bias (and an fp32
+    residual [B, Lo, Co]) in its epilogue."""
+    b = int(x.shape[0])
+    cols = im2col_1d(x, kernel, stride=stride, padding=padding, dilation=dilation)
+    lo = cols.shape[0] // b
+    out = torch.empty(b, lo, int(w.shape[0]), dtype=out_dtype, device=x.device)
+    q8_0_linear(cols, w, bias=bias, out=out.view(b * lo, -1), out_dtype=out_dtype,
+                residual=None if residual is None else residual.reshape(b * lo, -1))
+    return out
+
+
+def snake(x: torch.Tensor, alpha: torch.Tensor, *, eps: float = SNAKE_EPS, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x + sin(alpha x)^2 / (alpha + eps) per channel of channels-last fp32 x [..., C]; alpha fp32 [C]."""
+    _check(x, "x", torch.float32)
+    _check(alpha, "alpha", torch.float32)
+    c = int(x.shape[-1])
+    if alpha.numel() != c:
+        raise ValueError(f"alpha must have {c} elements, got {alpha.numel()}")
+    if out is None:
+        out = torch.empty_like(x)
+    _check(out, "output", torch.float32)
+    if out.shape != x.shape:
+        raise ValueError("output must have x's shape")
+    call("t2h_snake", ptr(x), ptr(alpha), ptr(out), x.numel() // c, c, float(eps), stream_handle())
+    return out
