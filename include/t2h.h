@@ -298,6 +298,15 @@ int t2h_im2col_1d(const void* x, int x_dtype, const int64_t* x_strides, uint32_t
  * (src/models/quantized_omnivoice/dispatch/audio_decode.py:151-161; eps 1e-9, add_scalar.py:43). */
 int t2h_snake(const float* x, const float* alpha, float* out, uint64_t rows, uint32_t channels, float eps,
               void* stream);
+/* Transposed conv1d with Q8_0 weights: x fp32 [B, Ci, L_in] (any element strides x_strides[3] = b, c, l),
+ * w the reference's Q8_0 rows [Ci, ceil(Co * K / 32) * 34 bytes] (element co * K + k of row ci), bias fp32
+ * [Co] or NULL; out fp32 [B, L_out, Co] contiguous, L_out = (L_in - 1) * stride - 2 pad + K.
+ * y[b, t, co] = bias[co] + sum over ci and the taps k with t + pad - k = i * stride, 0 <= i < L_in, of
+ * W[ci, co * K + k] x[b, ci, i].  Replaces CONV_TRANSPOSE1D_Q8_0W_F32B_F32
+ * (src/models/quantized_omnivoice/shaders/conv_transpose1d_q8_0w_f32b_f32.py). */
+int t2h_conv_transpose1d_q8_0(const float* x, const int64_t* x_strides, const void* w, const float* bias, float* out,
+                              uint32_t batch, uint32_t ci, uint32_t li, uint32_t co, uint32_t kh, uint32_t stride,
+                              uint32_t pad, uint32_t lo, void* stream);
 /* out = (x - mean) / sqrt(var + eps) * w + b per row (biased variance, two passes); x, out fp32 or bf16,
  * cols % 4 == 0, 16-B aligned.  replaces LAYER_NORM_F32W_F32B_F32
  * (src/models/quantized_qwen3_asr/shaders/layer_norm_f32w_f32b_f32.py:20-105). */

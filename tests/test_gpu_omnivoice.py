@@ -93,3 +93,28 @@ def test_residual_unit_matches_oracle(device, dil):
     assert y.shape == ref.shape
     print(f"residual unit dil={dil}: max-abs {np.abs(y - ref).max():.3e}", flush=True)
     assert_close(y, ref, max_abs=2e-2 * float(np.abs(ref).max()), min_cos=0.9999, what="residual unit")
+
+
+@pytest.mark.parametrize("ci,co,k,stride,pad", [(64, 32, 16, 8, 4), (96, 48, 10, 5, 3), (32, 32, 4, 2, 1),
+                                                (48, 24, 3, 1, 0)])
+def test_conv_transpose1d_q8_0_matches_oracle(device, ci, co, k, stride, pad):
+    """The reference's Q8_0 rows [Ci, Co K] read as they are, fp32 arithmetic: agreement to fp32 rounding of
+    the sums against the float64 oracle on the exactly dequantized weights."""
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(ci + k)
+    b, length = 2, 21
+    x = rng.standard_normal((b, length, ci)).astype(np.float32)
+    # rows of Co K values in whole 32-value blocks (the last one zero-padded when Co K % 32 != 0)
+    kk = co * k
+    kpad = (kk + 31) // 32 * 32
+    w = np.zeros((ci, kpad), np.float32)
+    w[:, :kk] = rng.standard_normal((ci, kk)) * 0.05
+    bias = rng.standard_normal(co).astype(np.float32)
+    packed = kernels.quantize(torch.from_numpy(w).to(device), "q8_0")
+    dense = oracle.dequant_q8_0(packed.cpu().numpy(), kpad)[:, :kk]
+    y = kernels.conv_transpose1d_q8_0(torch.from_numpy(x).to(device), packed, torch.from_numpy(bias).to(device),
+                                      co, k, stride=stride, padding=pad).cpu().numpy()
+    ref = O.conv_transpose1d_ref(x.transpose(0, 2, 1), dense, bias, k, stride, pad).transpose(0, 2, 1)
+    assert y.shape == ref.shape
+    assert_close(y, ref, max_abs=1e-5 * float(np.abs(ref).max()), min_cos=0.9999999, what="conv_transpose1d")

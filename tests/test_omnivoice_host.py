@@ -49,3 +49,17 @@ def test_snake_fixed_points_and_period():
     # x = pi / (2 alpha): the added term is its maximum 1 / (alpha + eps)
     np.testing.assert_allclose(O.snake_ref(np.pi / (2 * alpha[None, :]), alpha, eps=0.0, channel_axis=1)
                                - np.pi / (2 * alpha), 1.0 / alpha[None, :], rtol=1e-12)
+
+
+@pytest.mark.parametrize("k,stride,pad", [(16, 8, 4), (10, 5, 3), (4, 2, 1), (8, 4, 2), (3, 1, 0), (6, 3, 0)])
+def test_conv_transpose1d_ref_matches_torch(k, stride, pad):
+    rng = np.random.default_rng(k * 10 + stride)
+    b, ci, co, length = 2, 5, 4, 9
+    x = rng.standard_normal((b, ci, length))
+    w = rng.standard_normal((ci, co, k))
+    bias = rng.standard_normal(co)
+    ref = torch.nn.functional.conv_transpose1d(torch.from_numpy(x), torch.from_numpy(w), torch.from_numpy(bias),
+                                               stride=stride, padding=pad).numpy()
+    got = O.conv_transpose1d_ref(x, w.reshape(ci, co * k), bias, k, stride, pad)
+    assert got.shape == ref.shape
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)

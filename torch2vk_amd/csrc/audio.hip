@@ -452,3 +452,88 @@ extern "C" int t2h_snake(const float* x, const float* alpha, float* out, uint64_
     T2H_LAUNCH_CHECK();
     return T2H_OK;
 }
+
+// ------------------------------------------------------ conv transpose --
+
+// y[b, t, co] = bias[co] + sum_ci sum_k W[ci, co K + k] x[b, ci, i] over the
+// taps k with t + pad - k = i * stride, 0 <= i < L_in: CONV_TRANSPOSE1D_Q8_0W_F32B_F32
+// (src/models/quantized_omnivoice/shaders/conv_transpose1d_q8_0w_f32b_f32.py:
+// deconv_input_value, deconv_weight_value), reading the reference's Q8_0 rows
+// [Ci, Co K] (34-byte blocks: fp16 scale + 32 int8) as they are, in fp32.
+// One thread per output (b, t, co); consecutive threads take consecutive co,
+// so a wave shares every x value it reads.
+struct ConvTArgs {
+    const float* x;
+    int64_t sb, sc, sl;     // x strides (elements): batch, channel, position
+    const uint8_t* w;
+    const float* bias;
+    float* out;             // [B, L_out, Co] contiguous
+    uint32_t ci, li, co, kh, stride, pad, lo;
+    uint32_t row_bytes;     // Q8_0 bytes per weight row (ceil(Co K / 32) * 34)
+    uint64_t n;             // B * L_out * Co
+};
+
+__global__ __launch_bounds__(256) void conv_transpose1d_q8_0_kernel(const ConvTArgs a) {
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= a.n) return;
+    const uint32_t co = (uint32_t)(idx % a.co);
+    const uint64_t r = idx / a.co;
+    const uint32_t t = (uint32_t)(r % a.lo);
+    const uint64_t b = r / a.lo;
+    // first tap whose input position is a whole step: (t + pad - k) % stride == 0
+    const uint32_t k0 = (t + a.pad) % a.stride;
+    float acc = a.bias ? a.bias[co] : 0.0f;
+    for (uint32_t k = k0; k < a.kh; k += a.stride) {
+        const int num = (int)t + (int)a.pad - (int)k;
+        if (num < 0) break;  // k only grows
+        const uint32_t i = (uint32_t)num / a.stride;
+        if (i >= a.li) continue;
+        const uint32_t e = co * a.kh + k;          // element of every weight row
+        const uint32_t blk = e >> 5, q = e & 31u;
+        const float* xi = a.x + (int64_t)b * a.sb + (int64_t)i * a.sl;
+        const uint8_t* wb = a.w + (size_t)blk * 34;
+        for (uint32_t c = 0; c < a.ci; ++c) {
+            const uint8_t* row = wb + (size_t)c * a.row_bytes;
+            const float d = f16_bits_to_f32((uint32_t)row[0] | ((uint32_t)row[1] << 8));
+            const float wv = d * (float)(int8_t)row[2 + q];
+            acc = fmaf(wv, xi[(int64_t)c * a.sc], acc);
+        }
+    }
+    a.out[idx] = acc;
+}
+
+extern "C" int t2h_conv_transpose1d_q8_0(const float* x, const int64_t* x_strides, const void* w, const float* bias,
+                                         float* out, uint32_t batch, uint32_t ci, uint32_t li, uint32_t co,
+                                         uint32_t kh, uint32_t stride, uint32_t pad, uint32_t lo, void* stream) {
+    if (!x || !x_strides || !w || !out) return T2H_ERR_NULL;
+    if (ci == 0 || co == 0 || kh == 0 || stride == 0 || li == 0) return T2H_ERR_SHAPE;
+    // L_out of a transposed conv with no output padding
+    if ((int64_t)lo != ((int64_t)li - 1) * stride - 2 * (int64_t)pad + kh) return T2H_ERR_SHAPE;
+    if ((uint64_t)co * kh > 0x7fffffffu || pad > 0xffffu || li > 0x7fffffffu) return T2H_ERR_SHAPE;
+    if (reinterpret_cast<uintptr_t>(w) % 2 != 0) return T2H_ERR_ALIGN;
+    for (int i = 0; i < 3; ++i)
+        if (x_strides[i] < 0) return T2H_ERR_ARG;
+    ConvTArgs a;
+    a.x = x;
+    a.sb = x_strides[0];
+    a.sc = x_strides[1];
+    a.sl = x_strides[2];
+    a.w = reinterpret_cast<const uint8_t*>(w);
+    a.bias = bias;
+    a.out = out;
+    a.ci = ci;
+    a.li = li;
+    a.co = co;
+    a.kh = kh;
+    a.stride = stride;
+    a.pad = pad;
+    a.lo = lo;
+    a.row_bytes = (uint32_t)(((uint64_t)co * kh + 31) / 32 * 34);
+    a.n = (uint64_t)batch * lo * co;
+    if (a.n == 0) return T2H_OK;
+    if (a.n / 256 >= 0x7fffffffu) return T2H_ERR_SHAPE;
+    hipLaunchKernelGGL(conv_transpose1d_q8_0_kernel, dim3(grid_for(a.n)), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), a);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}

@@ -858,3 +858,28 @@ def snake(x: torch.Tensor, alpha: torch.Tensor, *, eps: float = SNAKE_EPS, out: 
         raise ValueError("output must have x's shape")
     call("t2h_snake", ptr(x), ptr(alpha), ptr(out), x.numel() // c, c, float(eps), stream_handle())
     return out
+
+
+def conv_transpose1d_q8_0(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, out_channels: int,
+                          kernel: int, *, stride: int = 1, padding: int = 0) -> torch.Tensor:
+    """CONV_TRANSPOSE1D_Q8_0W_F32B_F32 on channels-last fp32 x [B, L, Ci] -> [B, Lo, Co], Lo = (L - 1) stride -
+    2 padding + kernel; W the reference's Q8_0 rows [Ci, Co * kernel] as they are, bias fp32 [Co]."""
+    if not isinstance(x, torch.Tensor) or x.device.type != "cuda" or x.dtype != torch.float32 or x.dim() != 3:
+        raise ValueError("x must be fp32 [B, L, Ci] on a HIP device")
+    _check(w, "weight", torch.uint8, align=2)
+    b, length, ci = (int(d) for d in x.shape)
+    blocks = (out_channels * kernel + 31) // 32
+    if w.dim() != 2 or tuple(w.shape) != (ci, blocks * Q8_0_BYTES):
+        raise ValueError(f"weight must be uint8 [{ci}, {blocks * Q8_0_BYTES}], got {tuple(w.shape)}")
+    if bias is not None:
+        _check(bias, "bias", torch.float32, align=4)
+        if bias.numel() != out_channels:
+            raise ValueError(f"bias must have {out_channels} elements")
+    lo = (length - 1) * stride - 2 * padding + kernel
+    if lo < 1:
+        raise ValueError("empty output")
+    out = torch.empty(b, lo, out_channels, dtype=torch.float32, device=x.device)
+    strides = (_lib.ctypes.c_int64 * 3)(x.stride(0), x.stride(2), x.stride(1))
+    call("t2h_conv_transpose1d_q8_0", ptr(x), strides, ptr(w), ptr(bias), ptr(out), b, ci, length, out_channels,
+         kernel, stride, padding, lo, stream_handle())
+    return out
