@@ -307,6 +307,31 @@ int t2h_snake(const float* x, const float* alpha, float* out, uint64_t rows, uin
 int t2h_conv_transpose1d_q8_0(const float* x, const int64_t* x_strides, const void* w, const float* bias, float* out,
                               uint32_t batch, uint32_t ci, uint32_t li, uint32_t co, uint32_t kh, uint32_t stride,
                               uint32_t pad, uint32_t lo, void* stream);
+
+/* ----------------------------------------------- OmniVoice token loop --- */
+/* hidden fp32 [B, S, H] = sum over c < C of audio_w row (c * V + ids[b, c, s]) where audio_mask[b, s] != 0,
+ * else text_w row ids[b, 0, s]; Q8_0 rows of H values (H % 32 == 0); ids int64 [B, C, S], audio_mask uint32
+ * [B, S]; a token outside its table contributes 0.  Replaces OMNIVOICE_INPUT_EMBED_Q8_0_F32
+ * (src/models/quantized_omnivoice/shaders/omnivoice_input_embed_q8_0_f32.py). */
+int t2h_omnivoice_input_embed_q8_0(const void* text_w, uint32_t n_text, const void* audio_w, const int64_t* ids,
+                                   const uint32_t* audio_mask, float* out, uint32_t batch, uint32_t codebooks,
+                                   uint32_t seq, uint32_t hidden, uint32_t vocab, void* stream);
+/* Per (codebook c, target t) of C x T: log-softmax over codebook c's V logits of the conditional row
+ * (logits[0, S - T + t]) and the unconditional row (logits[1, t]) of fp32 logits [2, S, C * V]; guided =
+ * c + guidance (c - u); the best token other than mask_id (ties to the lowest id) and its guided
+ * log-probability minus c * layer_penalty, divided by temperature plus Gumbel noise (the reference's hash
+ * of seed, step and position) when temperature > 0, and -FLT_MAX where tokens[c T + t] != mask_id.
+ * Replaces OMNIVOICE_CFG_SCORE_F32 (src/models/quantized_omnivoice/shaders/omnivoice_cfg_score_f32.py). */
+int t2h_omnivoice_cfg_score(const float* logits, const int64_t* tokens, int64_t* cand_tokens, float* cand_scores,
+                            uint32_t seq, uint32_t codebooks, uint32_t targets, uint32_t vocab, float guidance,
+                            float layer_penalty, float temperature, uint32_t step, uint32_t seed, int64_t mask_id,
+                            void* stream);
+/* Unmask the min(unmask_count, C T) best candidates (score descending, index ascending): tokens[i] and
+ * batch_input_ids int64 [2, C, S] at [0, c, S - T + t] and [1, c, t] take cand_tokens[i].  Replaces
+ * OMNIVOICE_TOKEN_UPDATE_TOPK_F32 (src/models/quantized_omnivoice/shaders/omnivoice_token_update_topk_f32.py). */
+int t2h_omnivoice_token_update_topk(const int64_t* cand_tokens, const float* cand_scores, int64_t* tokens,
+                                    int64_t* batch_input_ids, uint32_t codebooks, uint32_t targets, uint32_t seq,
+                                    uint32_t unmask_count, void* stream);
 /* out = (x - mean) / sqrt(var + eps) * w + b per row (biased variance, two passes); x, out fp32 or bf16,
  * cols % 4 == 0, 16-B aligned.  replaces LAYER_NORM_F32W_F32B_F32
  * (src/models/quantized_qwen3_asr/shaders/layer_norm_f32w_f32b_f32.py:20-105). */

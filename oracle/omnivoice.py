@@ -9,6 +9,11 @@ path, never called by it).
   conv_transpose1d_q8_0w_f32b_f32.py: deconv_input_value / deconv_weight_value -- output t takes input i
   through tap k when t + padding - k = i * stride; weight row ci, element co * Kh + k), as a scatter over the
   inputs.  Pinned against torch.nn.functional.conv_transpose1d.
+* cfg_score_ref, token_update_topk_ref and input_embed_ref follow OMNIVOICE_CFG_SCORE_F32,
+  OMNIVOICE_TOKEN_UPDATE_TOPK_F32 and OMNIVOICE_INPUT_EMBED_Q8_0_F32 (src/models/quantized_omnivoice/shaders/
+  omnivoice_*.py), the Gumbel hash bit for bit (lowbias32 constants).  Pinned in tests/test_omnivoice_host.py:
+  the score against scipy-free log-softmax closed forms (guidance 0 = the conditional log-probability of the
+  argmax), the noise by the Gumbel mean (Euler's constant), the ranking against a stable argsort.
 * snake_ref follows the decoder's snake built from ADD_SCALAR (eps 1e-9), RECIPROCAL_F32, MUL_BROADCAST,
   SIN_F32, POW_SCALAR_F16 and ADD (src/models/quantized_omnivoice/dispatch/audio_decode.py:151-161), in
   float64 (the reference stores sin^2 in fp16; here it is kept exact).  Pinned by its fixed points
@@ -72,3 +77,89 @@ def conv_transpose1d_ref(x: np.ndarray, w: np.ndarray, bias: np.ndarray | None, 
     if bias is not None:
         y = y + np.asarray(bias, np.float64)[None, :, None]
     return y
+
+
+FLT_MAX = float(np.finfo(np.float32).max)
+
+
+def ov_hash(x: int) -> int:
+    x &= 0xFFFFFFFF
+    x ^= x >> 16
+    x = (x * 0x7FEB352D) & 0xFFFFFFFF
+    x ^= x >> 15
+    x = (x * 0x846CA68B) & 0xFFFFFFFF
+    x ^= x >> 16
+    return x
+
+
+def ov_gumbel(seed: int, step: int, flat: int) -> float:
+    x = (seed ^ ((step * 0x9E3779B9) & 0xFFFFFFFF) ^ ((flat * 0x85EBCA6B) & 0xFFFFFFFF)) & 0xFFFFFFFF
+    u = (float(ov_hash(x) & 0x00FFFFFF) + 0.5) * (1.0 / 16777216.0)
+    u = min(max(u, 1.0e-7), 1.0 - 1.0e-7)
+    return -np.log(-np.log(u))
+
+
+def _log_softmax(v: np.ndarray) -> np.ndarray:
+    m = v.max()
+    return v - m - np.log(np.exp(v - m).sum())
+
+
+def cfg_score_ref(logits: np.ndarray, tokens: np.ndarray, codebooks: int, targets: int, vocab: int, guidance: float,
+                  layer_penalty: float, temperature: float, step: int, seed: int, mask_id: int):
+    """logits [2, S, C * V] -> (candidate tokens [C * T], scores [C * T]) in float64."""
+    lg = np.asarray(logits, np.float64)
+    s_len = lg.shape[1]
+    ct = np.zeros(codebooks * targets, np.int64)
+    cs = np.zeros(codebooks * targets)
+    for c in range(codebooks):
+        for t in range(targets):
+            flat = c * targets + t
+            clp = _log_softmax(lg[0, s_len - targets + t, c * vocab:(c + 1) * vocab])
+            ulp = _log_softmax(lg[1, t, c * vocab:(c + 1) * vocab])
+            g = clp + guidance * (clp - ulp)
+            cand = g.copy()
+            if 0 <= mask_id < vocab:
+                cand[mask_id] = -np.inf
+            best = int(np.argmax(cand))              # first maximum: ties to the lowest id
+            conf = g[best] - g.max() - np.log(np.exp(g - g.max()).sum()) - c * layer_penalty
+            if temperature > 0:
+                conf = conf / temperature + ov_gumbel(seed, step, flat)
+            if tokens[flat] != mask_id:
+                conf = -FLT_MAX
+            ct[flat], cs[flat] = best, conf
+    return ct, cs
+
+
+def token_update_topk_ref(cand_tokens, cand_scores, tokens, batch_input_ids, unmask_count: int):
+    """In place on copies: the min(unmask_count, C T) best (score desc, index asc) positions take their token."""
+    tokens = np.array(tokens, copy=True)
+    ids = np.array(batch_input_ids, copy=True)
+    _, c_books, s_len = ids.shape
+    n = tokens.size
+    t_len = n // c_books
+    order = np.argsort(-np.asarray(cand_scores, np.float64), kind="stable")
+    for i in order[:min(unmask_count, n)]:
+        c, t = divmod(int(i), t_len)
+        tokens[i] = cand_tokens[i]
+        ids[0, c, s_len - t_len + t] = cand_tokens[i]
+        ids[1, c, t] = cand_tokens[i]
+    return tokens, ids
+
+
+def input_embed_ref(text_dense: np.ndarray, audio_dense: np.ndarray, ids: np.ndarray, audio_mask: np.ndarray,
+                    vocab: int) -> np.ndarray:
+    """text_dense [n_text, H], audio_dense [C * V, H] (dequantized rows) -> [B, S, H]."""
+    b, c_books, s_len = ids.shape
+    out = np.zeros((b, s_len, text_dense.shape[1]))
+    for bi in range(b):
+        for s in range(s_len):
+            if audio_mask[bi, s]:
+                for c in range(c_books):
+                    tok = int(ids[bi, c, s])
+                    if 0 <= tok < vocab:
+                        out[bi, s] += audio_dense[c * vocab + tok]
+            else:
+                tok = int(ids[bi, 0, s])
+                if 0 <= tok < text_dense.shape[0]:
+                    out[bi, s] = text_dense[tok]
+    return out

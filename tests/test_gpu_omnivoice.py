@@ -118,3 +118,60 @@ def test_conv_transpose1d_q8_0_matches_oracle(device, ci, co, k, stride, pad):
     ref = O.conv_transpose1d_ref(x.transpose(0, 2, 1), dense, bias, k, stride, pad).transpose(0, 2, 1)
     assert y.shape == ref.shape
     assert_close(y, ref, max_abs=1e-5 * float(np.abs(ref).max()), min_cos=0.9999999, what="conv_transpose1d")
+
+
+def test_input_embed_matches_oracle(device):
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(9)
+    b, c, s, h, vocab, n_text = 2, 3, 17, 64, 20, 50
+    tw = (rng.standard_normal((n_text, h)) * 0.1).astype(np.float32)
+    aw = (rng.standard_normal((c * vocab, h)) * 0.1).astype(np.float32)
+    tp, ap = kernels.quantize(torch.from_numpy(tw).to(device), "q8_0"), kernels.quantize(torch.from_numpy(aw).to(device), "q8_0")
+    ids = rng.integers(0, vocab, (b, c, s)).astype(np.int64)
+    ids[0, 1, 3] = vocab + 5                     # outside the audio table: contributes 0
+    mask = (rng.random((b, s)) < 0.6).astype(np.int32)
+    got = kernels.omnivoice_input_embed_q8_0(tp, ap, torch.from_numpy(ids).to(device), torch.from_numpy(mask).to(device),
+                                             vocab).cpu().numpy()
+    ref = O.input_embed_ref(oracle.dequant_q8_0(tp.cpu().numpy(), h), oracle.dequant_q8_0(ap.cpu().numpy(), h), ids,
+                            mask, vocab)
+    assert_close(got, ref, max_abs=1e-6 * float(np.abs(ref).max()) + 1e-7, min_cos=0.9999999, what="input embed")
+
+
+@pytest.mark.parametrize("temperature", [0.0, 5.0])
+def test_cfg_score_matches_oracle(device, temperature):
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(11)
+    c, t, s, vocab, mask_id = 8, 20, 30, 1025, 1024
+    logits = (rng.standard_normal((2, s, c * vocab)) * 3).astype(np.float32)
+    tokens = np.full(c * t, mask_id, np.int64)
+    tokens[::7] = 3                              # decided positions score -FLT_MAX
+    kw = dict(codebooks=c, targets=t, vocab=vocab, guidance=2.0, layer_penalty=0.1, temperature=temperature,
+              step=3, seed=1234, mask_id=mask_id)
+    ct, cs = kernels.omnivoice_cfg_score(torch.from_numpy(logits).to(device), torch.from_numpy(tokens).to(device), **kw)
+    rt, rs = O.cfg_score_ref(logits, tokens, c, t, vocab, 2.0, 0.1, temperature, 3, 1234, mask_id)
+    assert np.array_equal(ct.cpu().numpy(), rt)
+    got = cs.cpu().numpy().astype(np.float64)
+    open_ = tokens == mask_id
+    assert np.all(got[~open_] == -O.FLT_MAX)
+    assert np.abs(got[open_] - rs[open_]).max() <= 1e-3, np.abs(got[open_] - rs[open_]).max()
+
+
+def test_token_update_topk_matches_oracle(device):
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(13)
+    c, t, s = 8, 25, 40
+    scores = rng.standard_normal(c * t).astype(np.float32)
+    scores[[4, 9, 30]] = scores[17]              # ties go to the lower index
+    scores[::11] = -O.FLT_MAX                    # decided positions never rank
+    cand = rng.integers(0, 1024, c * t).astype(np.int64)
+    tokens = np.full(c * t, 1024, np.int64)
+    ids = rng.integers(0, 1024, (2, c, s)).astype(np.int64)
+    td, idd = torch.from_numpy(tokens).to(device), torch.from_numpy(ids).to(device)
+    kernels.omnivoice_token_update_topk(torch.from_numpy(cand).to(device), torch.from_numpy(scores).to(device), td, idd,
+                                        unmask_count=37)
+    rt, rids = O.token_update_topk_ref(cand, scores.astype(np.float64), tokens, ids, 37)
+    assert np.array_equal(td.cpu().numpy(), rt)
+    assert np.array_equal(idd.cpu().numpy(), rids)

@@ -63,3 +63,56 @@ def test_conv_transpose1d_ref_matches_torch(k, stride, pad):
     got = O.conv_transpose1d_ref(x, w.reshape(ci, co * k), bias, k, stride, pad)
     assert got.shape == ref.shape
     np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_cfg_score_ref_closed_forms():
+    rng = np.random.default_rng(7)
+    c_books, t_len, vocab, s_len = 2, 3, 11, 5
+    logits = rng.standard_normal((2, s_len, c_books * vocab))
+    mask_id = 4
+    tokens = np.full(c_books * t_len, mask_id, np.int64)
+    tokens[1] = 2                                            # an already decided position
+    ct, cs = O.cfg_score_ref(logits, tokens, c_books, t_len, vocab, 0.0, 0.25, 0.0, 0, 0, mask_id)
+    for c in range(c_books):
+        for t in range(t_len):
+            flat = c * t_len + t
+            row = logits[0, s_len - t_len + t, c * vocab:(c + 1) * vocab]
+            lp = row - np.log(np.exp(row).sum())              # guidance 0: the conditional log-probability
+            lp_no_mask = lp.copy()
+            lp_no_mask[mask_id] = -np.inf
+            assert ct[flat] == int(np.argmax(lp_no_mask))
+            want = lp_no_mask.max() - 0.25 * c
+            assert (cs[flat] == -O.FLT_MAX) if flat == 1 else np.isclose(cs[flat], want, atol=1e-12)
+    # guidance g: guided = (1 + g) c - g u, renormalised
+    g = 1.5
+    undecided = np.full(c_books * t_len, -1, np.int64)       # mask id -1: no token excluded, every position open
+    ct, cs = O.cfg_score_ref(logits, undecided, c_books, t_len, vocab, g, 0.0, 0.0, 0, 0, -1)
+    c_lp = logits[0, s_len - t_len][:vocab] - np.log(np.exp(logits[0, s_len - t_len][:vocab]).sum())
+    u_lp = logits[1, 0][:vocab] - np.log(np.exp(logits[1, 0][:vocab]).sum())
+    guided = (1 + g) * c_lp - g * u_lp
+    assert ct[0] == int(np.argmax(guided))
+    assert np.isclose(cs[0], guided.max() - np.log(np.exp(guided).sum()), atol=1e-12)
+
+
+def test_gumbel_noise_statistics():
+    draws = np.array([O.ov_gumbel(1234, 7, i) for i in range(20000)])
+    assert abs(draws.mean() - 0.5772156649) < 0.03          # the Gumbel mean is Euler's constant
+    assert abs(draws.var() - np.pi ** 2 / 6) < 0.1
+    assert O.ov_hash(0) == 0 and len({O.ov_hash(i) for i in range(5000)}) == 5000
+
+
+def test_token_update_topk_ref_matches_sorting():
+    rng = np.random.default_rng(3)
+    c_books, t_len, s_len = 3, 4, 9
+    scores = rng.standard_normal(c_books * t_len)
+    scores[5] = scores[2]                                    # a tie: the lower index ranks first
+    cand = rng.integers(0, 50, c_books * t_len)
+    tokens = np.full(c_books * t_len, 99, np.int64)
+    ids = np.full((2, c_books, s_len), -1, np.int64)
+    new_tokens, new_ids = O.token_update_topk_ref(cand, scores, tokens, ids, 5)
+    chosen = sorted(range(scores.size), key=lambda i: (-scores[i], i))[:5]
+    assert set(np.nonzero(new_tokens != 99)[0]) == set(chosen)
+    for i in chosen:
+        c, t = divmod(i, t_len)
+        assert new_ids[0, c, s_len - t_len + t] == cand[i] and new_ids[1, c, t] == cand[i]
+    assert (new_ids != -1).sum() == 10

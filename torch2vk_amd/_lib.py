@@ -80,6 +80,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "t2h_snake": (_i32, [_vp, _vp, _vp, _u64, _u32, _f32, _vp]),
     "t2h_conv_transpose1d_q8_0": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
                                          _vp]),
+    "t2h_omnivoice_input_embed_q8_0": (_i32, [_vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
+    "t2h_omnivoice_cfg_score": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _f32, _f32, _f32, _u32, _u32,
+                                       ctypes.c_int64, _vp]),
+    "t2h_omnivoice_token_update_topk": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     "t2h_qk_norm_rope_cache": (_i32, [_vp, _u64, _vp, _u64, _vp, _u64, _vp, _vp, _f32, _f32, ctypes.c_int32, _u32,
                                       _u32, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
 }

@@ -883,3 +883,56 @@ def conv_transpose1d_q8_0(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor |
     call("t2h_conv_transpose1d_q8_0", ptr(x), strides, ptr(w), ptr(bias), ptr(out), b, ci, length, out_channels,
          kernel, stride, padding, lo, stream_handle())
     return out
+
+
+def omnivoice_input_embed_q8_0(text_w: torch.Tensor, audio_w: torch.Tensor, ids: torch.Tensor,
+                               audio_mask: torch.Tensor, vocab: int) -> torch.Tensor:
+    """OMNIVOICE_INPUT_EMBED_Q8_0_F32: ids int64 [B, C, S], audio_mask uint32/int32 [B, S] -> fp32 [B, S, H]; text_w
+    Q8_0 rows [n_text, H], audio_w Q8_0 rows [C * vocab, H]."""
+    _check(text_w, "text_w", torch.uint8, align=2)
+    _check(audio_w, "audio_w", torch.uint8, align=2)
+    _check(ids, "ids", torch.int64, align=8)
+    _check(audio_mask, "audio_mask", (torch.int32, torch.uint32), align=4)
+    b, c, s = (int(d) for d in ids.shape)
+    h = int(text_w.shape[1]) // Q8_0_BYTES * 32
+    if int(audio_w.shape[1]) != int(text_w.shape[1]) or int(audio_w.shape[0]) != c * vocab:
+        raise ValueError("audio_w must be Q8_0 rows [C * vocab, H] like text_w")
+    if tuple(audio_mask.shape) != (b, s):
+        raise ValueError(f"audio_mask must be [{b}, {s}]")
+    out = torch.empty(b, s, h, dtype=torch.float32, device=ids.device)
+    call("t2h_omnivoice_input_embed_q8_0", ptr(text_w), int(text_w.shape[0]), ptr(audio_w), ptr(ids), ptr(audio_mask),
+         ptr(out), b, c, s, h, vocab, stream_handle())
+    return out
+
+
+def omnivoice_cfg_score(logits: torch.Tensor, tokens: torch.Tensor, *, codebooks: int, targets: int, vocab: int,
+                        guidance: float, layer_penalty: float, temperature: float, step: int, seed: int,
+                        mask_id: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """OMNIVOICE_CFG_SCORE_F32: fp32 logits [2, S, C * V], tokens int64 [C * T] -> (candidate tokens int64 [C * T],
+    candidate scores fp32 [C * T])."""
+    _check(logits, "logits", torch.float32)
+    _check(tokens, "tokens", torch.int64, align=8)
+    if logits.dim() != 3 or logits.shape[0] != 2 or logits.shape[2] != codebooks * vocab:
+        raise ValueError(f"logits must be [2, S, {codebooks * vocab}], got {tuple(logits.shape)}")
+    if tokens.numel() != codebooks * targets:
+        raise ValueError("tokens must hold C * T values")
+    ct = torch.empty(codebooks * targets, dtype=torch.int64, device=logits.device)
+    cs = torch.empty(codebooks * targets, dtype=torch.float32, device=logits.device)
+    call("t2h_omnivoice_cfg_score", ptr(logits), ptr(tokens), ptr(ct), ptr(cs), int(logits.shape[1]), codebooks,
+         targets, vocab, float(guidance), float(layer_penalty), float(temperature), step & 0xffffffff,
+         seed & 0xffffffff, int(mask_id), stream_handle())
+    return ct, cs
+
+
+def omnivoice_token_update_topk(cand_tokens: torch.Tensor, cand_scores: torch.Tensor, tokens: torch.Tensor,
+                                batch_input_ids: torch.Tensor, *, unmask_count: int) -> None:
+    """OMNIVOICE_TOKEN_UPDATE_TOPK_F32 in place on tokens int64 [C * T] and batch_input_ids int64 [2, C, S]."""
+    for x, n, dt in ((cand_tokens, "cand_tokens", torch.int64), (cand_scores, "cand_scores", torch.float32),
+                     (tokens, "tokens", torch.int64), (batch_input_ids, "batch_input_ids", torch.int64)):
+        _check(x, n, dt, align=4)
+    _, c, s = (int(d) for d in batch_input_ids.shape)
+    n = tokens.numel()
+    if n % c or cand_tokens.numel() != n or cand_scores.numel() != n:
+        raise ValueError("candidates and tokens must hold C * T values")
+    call("t2h_omnivoice_token_update_topk", ptr(cand_tokens), ptr(cand_scores), ptr(tokens), ptr(batch_input_ids), c,
+         n // c, s, int(unmask_count), stream_handle())
