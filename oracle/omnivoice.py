@@ -163,3 +163,31 @@ def input_embed_ref(text_dense: np.ndarray, audio_dense: np.ndarray, ids: np.nda
                 if 0 <= tok < text_dense.shape[0]:
                     out[bi, s] = text_dense[tok]
     return out
+
+
+def audio_decode_ref(cfg, dense: dict, codes: np.ndarray, round_gemm_inputs=None) -> np.ndarray:
+    """The acoustic decoder in float64 over dequantized weights (dense[name] as the GPU path uses them),
+    following run_audio_decode (src/models/quantized_omnivoice/dispatch/audio_decode.py:60-760): codebook
+    lookups and projections summed, fc2, conv1, per block snake -> conv_transpose1d -> residual units at
+    dilations 1/3/9, snake -> conv2.  ``round_gemm_inputs`` (e.g. bf16 rounding) is applied where the GPU
+    stages a GEMM's activations.  codes [C, T] -> waveform [T_out]."""
+    import math
+    rnd = round_gemm_inputs or (lambda a: a)
+    t = codes.shape[1]
+    acc = np.zeros((t, cfg.latent))
+    for c in range(cfg.codebooks):
+        e = dense[f"cb{c}"][codes[c]]
+        acc = acc + rnd(e) @ dense[f"proj{c}.w"].T + dense[f"proj{c}.b"]
+    h = rnd(acc) @ dense["fc2.w"].T + dense["fc2.b"]                     # [T, hidden]
+    x = conv1d_ref(rnd(h.T[None]), dense["conv1.w"], dense["conv1.b"], 7, 1, 3)   # [1, C, T]
+    ch = cfg.channels
+    for i, s in enumerate(cfg.strides):
+        x = snake_ref(x, dense[f"b{i}.alpha"])
+        x = conv_transpose1d_ref(x, dense[f"b{i}.convt.w"], dense[f"b{i}.convt.b"], 2 * s, s, math.ceil(s / 2))
+        for j, d in enumerate((1, 3, 9)):
+            p = f"b{i}.r{j}."
+            r = conv1d_ref(rnd(snake_ref(x, dense[p + "a1"])), dense[p + "c1.w"], dense[p + "c1.b"], 7, 1, 3 * d, d)
+            x = x + conv1d_ref(rnd(snake_ref(r, dense[p + "a2"])), dense[p + "c2.w"], dense[p + "c2.b"], 1)
+        ch //= 2
+    x = snake_ref(x, dense["final.alpha"])
+    return conv1d_ref(rnd(x), dense["conv2.w"], dense["conv2.b"], 7, 1, 3).reshape(-1)

@@ -175,3 +175,33 @@ def test_token_update_topk_matches_oracle(device):
     rt, rids = O.token_update_topk_ref(cand, scores.astype(np.float64), tokens, ids, 37)
     assert np.array_equal(td.cpu().numpy(), rt)
     assert np.array_equal(idd.cpu().numpy(), rids)
+
+
+def test_audio_decoder_matches_oracle(device):
+    """The whole acoustic decoder (2 codebooks, 2 upsampling blocks of strides 2 and 4, 6 residual units)
+    against the float64 oracle composite on the same dequantized weights, with GEMM activations and weights
+    rounded to bf16 where the GPU stages them, so only summation order separates the two."""
+    from torch2vk_amd.omnivoice.decoder import AudioDecoderConfig, OmniVoiceAudioDecoder, out_len, synthetic_dense
+
+    cfg = AudioDecoderConfig(codebooks=2, vocab=16, codebook_dim=32, latent=64, hidden=64, channels=128,
+                             strides=(2, 4))
+    dense = synthetic_dense(cfg, seed=5)
+    dec = OmniVoiceAudioDecoder(cfg, dense, device)
+    deq = {}
+    for n, a in dense.items():
+        if a.ndim == 2:
+            kp = (a.shape[1] + 31) // 32 * 32
+            deq[n] = oracle.dequant_q8_0(dec.w[n].cpu().numpy(), kp)[:, :a.shape[1]].astype(np.float64)
+            # the GEMM-run ops (linears, conv1d) stage dequantized weights as bf16 (d q rounded to nearest
+            # even); the embedding and conv_transpose1d read them in fp32
+            if not (n.startswith("cb") or n.endswith("convt.w")):
+                deq[n] = _bf16(deq[n])
+        else:
+            deq[n] = a.astype(np.float64)
+    codes = np.random.default_rng(8).integers(0, cfg.vocab, (cfg.codebooks, 10)).astype(np.int64)
+    y = dec.decode(torch.from_numpy(codes)).cpu().numpy()
+    ref = O.audio_decode_ref(cfg, deq, codes, round_gemm_inputs=_bf16)
+    assert y.shape == (out_len(cfg, 10),) == ref.shape
+    print(f"audio decoder: {y.shape[0]} samples, max-abs {np.abs(y - ref).max():.3e}, max |ref| {np.abs(ref).max():.3e}",
+          flush=True)
+    assert_close(y, ref, max_abs=1e-4 * float(np.abs(ref).max()), min_cos=0.9999999, what="waveform")
