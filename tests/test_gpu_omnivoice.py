@@ -205,3 +205,63 @@ def test_audio_decoder_matches_oracle(device):
     print(f"audio decoder: {y.shape[0]} samples, max-abs {np.abs(y - ref).max():.3e}, max |ref| {np.abs(ref).max():.3e}",
           flush=True)
     assert_close(y, ref, max_abs=1e-4 * float(np.abs(ref).max()), min_cos=0.9999999, what="waveform")
+
+
+def test_generation_loop(device):
+    """OmniVoice's loop on a 2-layer backbone: every step unmasks exactly the scheduled count, the two sequence
+    copies carry the tokens, nothing stays masked; the first step's logits match the CPU oracle's masked
+    Qwen3 pass and Q6_K head on the same embeddings."""
+    from torch2vk_amd import kernels
+    from torch2vk_amd.omnivoice.generate import OmniVoiceGenerator, unmask_schedule
+    from torch2vk_amd.qwen3.config import Qwen3Config
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+    from torch2vk_amd.qwen3.weights import matrix_shapes, synthetic_weights
+    from oracle.qwen3_check import dense_weights
+    from oracle.reference import Qwen3Shape
+
+    cfg = Qwen3Config("tiny-ov", hidden=1024, layers=2, heads=8, kv_heads=2, head_dim=128, mlp=1024, vocab=1024,
+                      eos_token_ids=(1023,))
+    w = synthetic_weights(cfg, device=device, seed=71, std=0.05, norm_std=0.1)
+    llm = Qwen3Decoder(w, max_positions=32, max_new_tokens=4)
+    c, v, mask_id, t_len, s_len = 2, 64, 63, 6, 16
+    rng = np.random.default_rng(12)
+    q = lambda a, wt: kernels.quantize(torch.from_numpy(a.astype(np.float32)).to(device), wt)  # noqa: E731
+    text_w = q(rng.standard_normal((cfg.vocab, cfg.hidden)) * 0.05, "q8_0")
+    audio_w = q(rng.standard_normal((c * v, cfg.hidden)) * 0.05, "q8_0")
+    head_w = q(rng.standard_normal((c * v, cfg.hidden)) * 0.05, "q6_k")
+    ids = np.zeros((2, c, s_len), np.int64)
+    ids[0, :, :s_len - t_len] = rng.integers(0, cfg.vocab, s_len - t_len)
+    ids[0, :, s_len - t_len:] = mask_id
+    ids[1, :, :t_len] = mask_id
+    amask = np.zeros((2, s_len), np.int32)
+    amask[0, s_len - t_len:] = 1
+    amask[1, :t_len] = 1
+    attn = np.zeros((2, s_len, s_len), np.float32)
+    attn[1, :t_len, t_len:] = -np.inf                # the unconditional targets see only themselves
+    ids_d, amask_d, attn_d = (torch.from_numpy(a).to(device) for a in (ids, amask, attn))
+    tokens = torch.full((c * t_len,), mask_id, dtype=torch.int64, device=device)
+    gen = OmniVoiceGenerator(llm, text_w, audio_w, head_w, codebooks=c, vocab=v, mask_id=mask_id)
+    # step-0 logits against the oracle on the same embeddings
+    hidden = kernels.omnivoice_input_embed_q8_0(text_w, audio_w, ids_d, amask_d, v).cpu()
+    lg0 = gen.logits(ids_d, amask_d, attn_d).cpu().numpy()
+    dense = dense_weights({k: x.cpu().numpy() for k, x in w.packed.items()}, w.types,
+                          {k: x.cpu().numpy() for k, x in w.norms.items()}, matrix_shapes(cfg))
+    shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
+                       head_dim=cfg.head_dim, mlp=cfg.mlp, vocab=cfg.vocab, rope_theta=cfg.rope_theta)
+    head = oracle.dequant_q6_k(head_w.cpu().numpy(), cfg.hidden).astype(np.float64)
+    for b in range(2):
+        hb = R.Qwen3CpuModel(shape, dense, max_positions=32).forward(None, 0, embeds=hidden[b],
+                                                                     mask=torch.from_numpy(attn[b]), all_positions=True)
+        ref = hb.double().numpy() @ head.T
+        assert_close(lg0[b], ref, max_abs=0.05 * float(np.abs(ref).max()), min_cos=0.999, what=f"logits row {b}")
+    sched = unmask_schedule(c * t_len, 4)
+    seen = []
+    gen.generate(ids_d, amask_d, attn_d, tokens, num_steps=4, guidance=2.0, layer_penalty=0.1, temperature=0.0,
+                 on_step=lambda step, k, lg: seen.append(int((tokens != mask_id).sum().item())))
+    assert seen == list(np.cumsum(sched)), (seen, sched)
+    tk = tokens.cpu().numpy()
+    assert (tk != mask_id).all() and (tk >= 0).all() and (tk < v).all()
+    out_ids = ids_d.cpu().numpy()
+    for i in range(c * t_len):
+        cb, t = divmod(i, t_len)
+        assert out_ids[0, cb, s_len - t_len + t] == tk[i] == out_ids[1, cb, t]

@@ -116,3 +116,16 @@ def test_token_update_topk_ref_matches_sorting():
         c, t = divmod(i, t_len)
         assert new_ids[0, c, s_len - t_len + t] == cand[i] and new_ids[1, c, t] == cand[i]
     assert (new_ids != -1).sum() == 10
+
+
+def test_unmask_schedule():
+    from torch2vk_amd.omnivoice.generate import time_steps, unmask_schedule
+
+    t = time_steps(0.0, 1.0, 8, 0.1)
+    assert t[0] == 0.0 and abs(float(t[-1]) - 1.0) < 1e-7 and np.all(np.diff(t) > 0)
+    assert abs(float(time_steps(0.0, 1.0, 2, 0.1)[1]) - 0.05 / 0.55) < 1e-7   # s t / (1 + (s - 1) t) at t = 1/2
+    for total, steps in ((12, 4), (4000, 32), (7, 10)):
+        sched = unmask_schedule(total, steps)
+        assert len(sched) == steps and sum(sched) == total and min(sched) >= 0
+    assert unmask_schedule(100, 4, t_shift=1.0) == [25, 25, 25, 25]           # no shift: an even split
+    assert unmask_schedule(100, 4)[0] < unmask_schedule(100, 4)[-1]           # shift 0.1: few early, many late
