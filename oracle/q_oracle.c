@@ -371,6 +371,16 @@ static float make_qx_quants16(const float* v, int* levels) {
     return scale;
 }
 
+/* The per-sub-block searches on their own, over n sub-blocks (32 values for Q4_K, 16 for Q6_K), so that tests
+ * can check which candidate each one keeps. */
+void oracle_q4_k_subblocks(const float* v, int64_t n, float* scales, float* min_offsets) {
+    for (int64_t i = 0; i < n; ++i) scales[i] = choose_subblock_scale(v + 32 * i, min_offsets + i);
+}
+
+void oracle_q6_k_subblocks(const float* v, int64_t n, float* scales, int* levels) {
+    for (int64_t i = 0; i < n; ++i) scales[i] = make_qx_quants16(v + 16 * i, levels + 16 * i);
+}
+
 /* vulkan.py:566-634: one 256-value superblock -> 210 bytes */
 static void q6_k_block(const float* values, uint8_t* out) {
     int levels[256];

@@ -54,6 +54,10 @@ def _load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = [u8p, ctypes.c_int64, ctypes.c_int64, f32p]
             fn.restype = None
+        lib.oracle_q4_k_subblocks.argtypes = [f32p, ctypes.c_int64, f32p, f32p]
+        lib.oracle_q4_k_subblocks.restype = None
+        lib.oracle_q6_k_subblocks.argtypes = [f32p, ctypes.c_int64, f32p, ctypes.POINTER(ctypes.c_int)]
+        lib.oracle_q6_k_subblocks.restype = None
         lib.oracle_f32_to_f16.argtypes = [ctypes.c_float]
         lib.oracle_f32_to_f16.restype = ctypes.c_uint16
         lib.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
@@ -105,6 +109,28 @@ def quantize_q8_0(x: np.ndarray) -> np.ndarray:
     out = np.empty((rows, padded // 32 * Q8_0_BLOCK_BYTES), dtype=np.uint8)
     _load().oracle_quantize_q8_0(_ptr(x, ctypes.c_float), rows, padded, _ptr(out, ctypes.c_uint8))
     return out
+
+
+def q4_k_subblock_search(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The Q4_K sub-block search alone (choose_subblock_scale, vulkan.py:263-329) over rows of 32 values:
+    fp32 (scale, min_offset) per row, before the superblock's 6-bit coding."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, 32)
+    scale = np.empty(x.shape[0], np.float32)
+    mins = np.empty(x.shape[0], np.float32)
+    _load().oracle_q4_k_subblocks(_ptr(x, ctypes.c_float), x.shape[0], _ptr(scale, ctypes.c_float),
+                                  _ptr(mins, ctypes.c_float))
+    return scale, mins
+
+
+def q6_k_subblock_search(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The Q6_K sub-block search alone (make_qx_quants16, vulkan.py:483-540) over rows of 16 values: the fp32
+    scale and the 6-bit levels (0..63) per row, before the superblock's int8 scale coding."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, 16)
+    scale = np.empty(x.shape[0], np.float32)
+    levels = np.empty((x.shape[0], 16), np.int32)
+    _load().oracle_q6_k_subblocks(_ptr(x, ctypes.c_float), x.shape[0], _ptr(scale, ctypes.c_float),
+                                  _ptr(levels, ctypes.c_int))
+    return scale, levels
 
 
 def _dequant(fn_name: str, w: np.ndarray, k: int, block: int, nbytes: int) -> np.ndarray:

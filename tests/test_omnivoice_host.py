@@ -51,18 +51,39 @@ def test_snake_fixed_points_and_period():
                                - np.pi / (2 * alpha), 1.0 / alpha[None, :], rtol=1e-12)
 
 
-@pytest.mark.parametrize("k,stride,pad", [(16, 8, 4), (10, 5, 3), (4, 2, 1), (8, 4, 2), (3, 1, 0), (6, 3, 0)])
-def test_conv_transpose1d_ref_matches_torch(k, stride, pad):
-    rng = np.random.default_rng(k * 10 + stride)
+@pytest.mark.parametrize("k,stride,pad,opad", [(16, 8, 4, 0), (10, 5, 3, 0), (10, 5, 3, 1), (4, 2, 1, 0), (8, 4, 2, 0),
+                                              (3, 1, 0, 0), (6, 3, 0, 0), (6, 3, 2, 1), (6, 3, 2, 2)])
+def test_conv_transpose1d_ref_matches_torch(k, stride, pad, opad):
+    rng = np.random.default_rng(k * 10 + stride + opad)
     b, ci, co, length = 2, 5, 4, 9
     x = rng.standard_normal((b, ci, length))
     w = rng.standard_normal((ci, co, k))
     bias = rng.standard_normal(co)
     ref = torch.nn.functional.conv_transpose1d(torch.from_numpy(x), torch.from_numpy(w), torch.from_numpy(bias),
-                                               stride=stride, padding=pad).numpy()
-    got = O.conv_transpose1d_ref(x, w.reshape(ci, co * k), bias, k, stride, pad)
+                                               stride=stride, padding=pad, output_padding=opad).numpy()
+    got = O.conv_transpose1d_ref(x, w.reshape(ci, co * k), bias, k, stride, pad, opad)
     assert got.shape == ref.shape
     np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_decoder_block_lengths_match_the_reference_tensors():
+    """Each upsampling block (kernel 2s, padding ceil(s/2), output padding s % 2) writes s outputs per input, so
+    the strides 8, 5, 4, 2, 3 give the reference's target_len * 8, * 40, * 160, * 320, * 960 samples
+    (src/models/quantized_omnivoice/tensors/audio_decode.py)."""
+    import math
+
+    from torch2vk_amd.omnivoice.decoder import AudioDecoderConfig, out_len
+
+    expect = {8: 8, 5: 40, 4: 160, 2: 320, 3: 960}
+    strides = (8, 5, 4, 2, 3)
+    for t in (1, 2, 7, 75, 1000):
+        length = t
+        for s in strides:
+            length = (length - 1) * s - 2 * math.ceil(s / 2) + 2 * s + s % 2
+            assert length == t * expect[s]
+        cfg = AudioDecoderConfig(codebooks=1, vocab=4, codebook_dim=8, latent=8, hidden=8, channels=64,
+                                 strides=strides)
+        assert out_len(cfg, t) == 960 * t
 
 
 def test_cfg_score_ref_closed_forms():
@@ -128,4 +149,11 @@ def test_unmask_schedule():
         sched = unmask_schedule(total, steps)
         assert len(sched) == steps and sum(sched) == total and min(sched) >= 0
     assert unmask_schedule(100, 4, t_shift=1.0) == [25, 25, 25, 25]           # no shift: an even split
+    # float32 products (the reference's promotion): these totals round differently in float64
+    # (..., 41, 125] and a 129 / 3894 pair)
+    assert unmask_schedule(221, 8) == [4, 5, 6, 8, 12, 20, 40, 126]
+    assert unmask_schedule(9752, 16)[5] == 128 and unmask_schedule(9752, 16)[-1] == 3895
+    # fewer positions than steps: the remainder runs out and later steps unmask nothing
+    sched = unmask_schedule(7, 10)
+    assert sum(sched) == 7 and sched[-1] == 0 and all(k >= 0 for k in sched)
     assert unmask_schedule(100, 4)[0] < unmask_schedule(100, 4)[-1]           # shift 0.1: few early, many late

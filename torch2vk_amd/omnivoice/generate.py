@@ -25,11 +25,12 @@ def time_steps(t_start: float, t_end: float, num_step: int, t_shift: float) -> n
 
 def unmask_schedule(total_mask: int, num_steps: int, t_shift: float = 0.1) -> list[int]:
     """Positions unmasked per step (run.py:224-234): ceil(total * dt) capped by what remains; the last step
-    takes the remainder."""
+    takes the remainder.  The product is float32, as the reference's int times a float32 grid difference is
+    under numpy 2's promotion rules; in float64 some totals round across an integer (221 over 8 steps)."""
     t = time_steps(0.0, 1.0, num_steps, t_shift)
     rem, out = total_mask, []
     for s in range(num_steps):
-        num = rem if s == num_steps - 1 else min(math.ceil(total_mask * float(t[s + 1] - t[s])), rem)
+        num = rem if s == num_steps - 1 else min(math.ceil(np.float32(total_mask) * (t[s + 1] - t[s])), rem)
         out.append(int(num))
         rem -= int(num)
     return out
@@ -62,6 +63,8 @@ class OmniVoiceGenerator:
         """Run the loop in place on ids and tokens; returns tokens [C * T]."""
         t_len = tokens.numel() // self.c
         for step, k in enumerate(unmask_schedule(tokens.numel(), num_steps, t_shift)):
+            if k <= 0:
+                continue  # nothing left to unmask: the reference skips the step (run.py:251-253)
             lg = self.logits(ids, audio_mask, attn_mask)
             ct, cs = kernels.omnivoice_cfg_score(lg, tokens, codebooks=self.c, targets=t_len, vocab=self.v,
                                                  guidance=guidance, layer_penalty=layer_penalty,
