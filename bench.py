@@ -57,10 +57,13 @@ def parse_args():
     p.add_argument("--positions", type=int, default=PROMPT_POSITIONS, help="KV positions prefilled before timing")
     p.add_argument("--kernel-reps", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-sample-steps", type=int, default=3)
+    p.add_argument("--cpu-sample-steps", type=int, default=5, help="CPU baseline runs (the median is reported)")
     p.add_argument("--no-graph", action="store_true")
     p.add_argument("--per-op", action="store_true",
                    help="one launch per op instead of the persistent layers kernel (t2h_qwen3_decode_layers)")
+    p.add_argument("--phase-trace", action="store_true",
+                   help="run the persistent decode kernel's traced instantiation at the configured KV position and "
+                        "print its per-phase timeline (markdown), no JSON line")
     p.add_argument("--profile-kernel", action="store_true",
                    help="counter-collection target: run the dominant kernel (the persistent layers kernel, or "
                         "with --per-op the gate|up GEMV over all layers) plus a 256 MiB copy (the calibration for "
@@ -131,6 +134,77 @@ def profile_kernel_target(per_op: bool, config: str = "decode") -> int:
     return 0
 
 
+def phase_trace(args) -> int:
+    """Per-phase timeline of the persistent decode kernel (its traced instantiation) at KV position
+    args.positions: for each phase of the middle layers, when blocks enter it, have its input in hand and
+    finish, relative to the previous phase's last block finishing; printed as a markdown table."""
+    import numpy as np
+    import torch
+
+    from torch2vk_amd import kernels
+    from torch2vk_amd.qwen3.config import QWEN3_0_6B, QWEN3_8B
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+    from torch2vk_amd.qwen3.weights import synthetic_weights
+
+    dev = torch.device("cuda:0")
+    cfg = QWEN3_8B if args.model == "8b" else QWEN3_0_6B
+    w = synthetic_weights(cfg, device=dev, seed=0)
+    dec = Qwen3Decoder(w, max_positions=args.positions + 64, max_new_tokens=4, device=dev, persistent=True)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    dec.k_cache[:, :args.positions].normal_(generator=gen)
+    dec.v_cache[:, :args.positions].normal_(generator=gen)
+    dec.position.fill_(args.positions)
+    trace = kernels.decode_layers_trace(cfg.layers, dev)
+    launches = []
+    for _ in range(max(3, args.kernel_reps)):
+        dec.h.normal_(generator=gen)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        dec.run_decode_layers(trace=trace)
+        end.record()
+        end.synchronize()
+        launches.append((start.elapsed_time(end) * 1e3, trace.cpu().numpy().copy()))
+    status = decode_status(dec)
+    if status:
+        print(f"[bench] persistent kernel status {status:#x}: trace invalid", file=sys.stderr)
+        return 3
+    us_launch = float(np.median([u for u, _ in launches]))
+    names = kernels.DECODE_TRACE_PHASES
+    n_blocks = [256, 256, cfg.heads, 256, 256, 256]
+    rows = []   # [layer, phase] -> begin, ready_med, ready_max, end_med, end_max, polls (us from prev phase end)
+    periods = []
+    for _, tr in launches[1:]:
+        t = tr[..., :4].astype(np.float64) * 0.01     # 100 MHz -> us
+        lo, hi = 2, cfg.layers - 1
+        periods.append((t[hi - 1, 5, :, 3].max() - t[lo - 1, 5, :, 3].max()) / (hi - lo))
+        for layer in range(lo, hi):
+            prev = t[layer - 1, 5, :, 3].max()
+            r = []
+            for ph in range(6):
+                e = t[layer, ph, :n_blocks[ph]]
+                r.append([np.median(e[:, 0]) - prev, np.median(e[:, 1]) - prev, e[:, 1].max() - prev,
+                          np.median(e[:, 3]) - prev, e[:, 3].max() - prev,
+                          float(tr[layer, ph, :n_blocks[ph], 4].mean())])
+                prev = e[:, 3].max()
+            rows.append(r)
+    m = np.mean(np.array(rows), axis=0)
+    period = float(np.mean(periods))
+    print(f"| phase | blocks | start (median) | input in hand (median / last) | end (median / last) | polls per "
+          f"wait |\n|---|---|---|---|---|---|")
+    for ph in range(6):
+        b, rm, rx, em, ex, pl = m[ph]
+        print(f"| {names[ph]} | {n_blocks[ph]} | {b:.2f} | {rm:.2f} / {rx:.2f} | {em:.2f} / {ex:.2f} | {pl:.1f} |")
+    crit = m[:, 4]
+    print(f"\nlaunch {us_launch:.1f} us ({cfg.layers} layers, KV position {args.positions}); layer period "
+          f"{period:.2f} us; sum of phase critical-path steps {crit.sum():.2f} us")
+    wait = m[:, 1] - m[:, 0]
+    after = m[:, 3] - m[:, 1]
+    print("\nper phase (median block): wait for input " + ", ".join(f"{names[i]} {wait[i]:.2f}" for i in range(6)) +
+          " us; input in hand to end " + ", ".join(f"{names[i]} {after[i]:.2f}" for i in range(6)) + " us")
+    return 0
+
+
 def _profile_copy(dev) -> None:
     """The calibration launch of a counter run: one plain 256 MiB device-to-device copy."""
     import torch
@@ -153,6 +227,8 @@ def main() -> int:
         args.warmup = 16 if args.config == "decode" else 1
     if args.profile_kernel:
         return profile_kernel_target(args.per_op, args.config)
+    if args.phase_trace:
+        return phase_trace(args)
     if args.config == "prefill":
         return bench_prefill(args)
     if args.config == "asr":
@@ -207,8 +283,21 @@ def main() -> int:
     print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/token, {tok_s:.1f} tok/s "
           f"({n_generated} tokens stored)", file=sys.stderr, flush=True)
 
+    # the persistent kernel's waits are bounded: one that gave up sets the status word and the tokens of that
+    # launch are invalid, so a run with the word set reports nothing
+    status_timed = decode_status(dec)
+    if status_timed:
+        print(f"[bench] persistent kernel status {status_timed:#x} after the timed steps: run invalid",
+              file=sys.stderr, flush=True)
+        return 3
+
     kern = kernel_timing(dec, weights, args.kernel_reps)
     print(f"[bench] kernel timing: {json.dumps(kern['per_launch_us'])}", file=sys.stderr, flush=True)
+    status_kernels = decode_status(dec)
+    if status_kernels:
+        print(f"[bench] persistent kernel status {status_kernels:#x} after the kernel timing: run invalid",
+              file=sys.stderr, flush=True)
+        return 3
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -257,9 +346,15 @@ def main() -> int:
         "qmatmul_gbs": round(kern["qmatmul_gbs"], 1),
         "kernel_us_per_token": round(kern["us_per_token"], 1),
         "cpu_baseline": cpu,
+        "status": status_timed | status_kernels,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def decode_status(dec) -> int:
+    """The persistent kernel's status word (0 = every bounded wait ended in time; always 0 for per-op launches)."""
+    return int(dec.status.item()) if dec.persistent else 0
 
 
 def _graph_us_per_call(calls, reps: int) -> float:
@@ -428,7 +523,7 @@ def cpu_baseline(cfg, weights, positions: int, steps: int) -> dict:
         hidden = model.forward(torch.tensor([s % 8]), start=positions + s)
         layer_times.append(time.perf_counter() - t0)
     lm_times = []
-    for _ in range(2):
+    for _ in range(max(5, steps)):
         t0 = time.perf_counter()
         logits = model.logits(hidden)
         int(torch.argmax(logits))
@@ -443,7 +538,7 @@ def cpu_baseline(cfg, weights, positions: int, steps: int) -> dict:
         "cores": threads,
         "kind": "port",
         "sample": f"CPU oracle decoder (torch {torch.__version__}, fp32 dense weights dequantized by the oracle): "
-                  f"1 of {c.layers} layers at KV position {positions} timed over {steps} steps (median "
+                  f"1 of {c.layers} layers at KV position {positions}, median of {steps} steps ("
                   f"{t_layer * 1e3:.1f} ms) x {c.layers} + LM head+argmax (median {t_lm * 1e3:.1f} ms)",
     }
 
@@ -650,7 +745,7 @@ def cpu_baseline_prefill(lw, c) -> dict:
     shape = Qwen3Shape(hidden=c.hidden, layers=1, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
                        mlp=c.mlp, vocab=c.vocab, rope_theta=c.rope_theta)
     times = []
-    for _ in range(3):
+    for _ in range(5):
         model = Qwen3CpuModel(shape, dense, max_positions=256)
         t0 = time.perf_counter()
         model.forward(torch.arange(256), start=0)
@@ -662,7 +757,7 @@ def cpu_baseline_prefill(lw, c) -> dict:
         "cores": threads,
         "kind": "port",
         "sample": f"CPU oracle Qwen3 forward (torch {torch.__version__}, fp32 dense weights dequantized from the "
-                  f"Q8_0 bytes) of 1 of {c.layers} layers over one 256-token chunk (median {t_layer * 1e3:.0f} ms), "
+                  f"Q8_0 bytes) of 1 of {c.layers} layers over one 256-token chunk (median of 5 runs {t_layer * 1e3:.0f} ms), "
                   f"x {c.layers}; attention at 256 rather than 2048 tokens, so this overstates the CPU rate",
     }
 

@@ -226,6 +226,18 @@ size_t t2h_qwen3_decode_layers_workspace_bytes(uint32_t hidden, uint32_t mlp, ui
 int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden, uint32_t mlp, uint32_t nh,
                             uint32_t nk, uint32_t d, uint32_t s_cap, float* h, const int32_t* cache_position, float eps,
                             float theta, void* workspace, size_t workspace_bytes, uint32_t* status, void* stream);
+/* The same launch with a phase timeline: trace (device, 8-B aligned, t2h_qwen3_decode_layers_trace_bytes()
+ * bytes) receives, per layer, phase (qkv, attention, merge, o, gate/up, down) and block (256), 8 uint64 slots:
+ * the 100 MHz real-time clock at the phase's start, when its input is in hand, after its first reduced unit
+ * (attention: its softmax), at its end, then the polls its first wave made for the input.  A separate kernel
+ * instantiation with the stamps compiled in; a diagnostic with no counterpart in the reference, which profiles
+ * its dispatches with SQTT traces instead (src/torch2vk/runtime/profile.py). */
+size_t t2h_qwen3_decode_layers_trace_bytes(uint32_t n_layers);
+int t2h_qwen3_decode_layers_traced(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden, uint32_t mlp,
+                                   uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap, float* h,
+                                   const int32_t* cache_position, float eps, float theta, void* workspace,
+                                   size_t workspace_bytes, uint32_t* status, uint64_t* trace, size_t trace_bytes,
+                                   void* stream);
 
 /* -------------------------------------------------- prefill attention --- */
 /* out = softmax(q.k^T * scale + mask) . v on the matrix cores (bf16 in, fp32
@@ -300,7 +312,9 @@ int t2h_snake(const float* x, const float* alpha, float* out, uint64_t rows, uin
               void* stream);
 /* Transposed conv1d with Q8_0 weights: x fp32 [B, Ci, L_in] (any element strides x_strides[3] = b, c, l),
  * w the reference's Q8_0 rows [Ci, ceil(Co * K / 32) * 34 bytes] (element co * K + k of row ci), bias fp32
- * [Co] or NULL; out fp32 [B, L_out, Co] contiguous, L_out = (L_in - 1) * stride - 2 pad + K.
+ * [Co] or NULL; out fp32 [B, L_out, Co] contiguous, L_out = (L_in - 1) * stride - 2 pad + K + output padding,
+ * the output padding in [0, stride) (the reference's blocks write stride * L_in outputs: kernel 2 stride, pad
+ * ceil(stride / 2), output padding stride % 2; the extra positions take the taps that reach them).
  * y[b, t, co] = bias[co] + sum over ci and the taps k with t + pad - k = i * stride, 0 <= i < L_in, of
  * W[ci, co * K + k] x[b, ci, i].  Replaces CONV_TRANSPOSE1D_Q8_0W_F32B_F32
  * (src/models/quantized_omnivoice/shaders/conv_transpose1d_q8_0w_f32b_f32.py). */

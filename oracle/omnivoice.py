@@ -61,18 +61,19 @@ def snake_ref(x: np.ndarray, alpha: np.ndarray, eps: float = 1e-9, channel_axis:
 
 
 def conv_transpose1d_ref(x: np.ndarray, w: np.ndarray, bias: np.ndarray | None, kernel: int, stride: int = 1,
-                         padding: int = 0) -> np.ndarray:
+                         padding: int = 0, output_padding: int = 0) -> np.ndarray:
     """x [B, Ci, L], w [Ci, Co * K] (row ci, element co * K + k) -> [B, Co, Lo] in float64, Lo = (L - 1) stride -
-    2 padding + K: every input i adds W[ci, co, k] x[b, ci, i] to output i * stride + k - padding."""
+    2 padding + K + output_padding: every input i adds W[ci, co, k] x[b, ci, i] to output i * stride + k - padding;
+    the output_padding positions at the end take whatever taps reach them (torch's conv_transpose1d)."""
     x = np.asarray(x, np.float64)
     b, ci, length = x.shape
     wk = np.asarray(w, np.float64).reshape(ci, -1, kernel)                 # [Ci, Co, K]
     co = wk.shape[1]
-    full = np.zeros((b, co, (length - 1) * stride + kernel))
+    full = np.zeros((b, co, (length - 1) * stride + kernel + output_padding))
     contrib = np.einsum("bci,cok->boik", x, wk)                             # [B, Co, L, K]
     for k in range(kernel):
         full[:, :, k:k + (length - 1) * stride + 1:stride] += contrib[:, :, :, k]
-    lo = (length - 1) * stride - 2 * padding + kernel
+    lo = (length - 1) * stride - 2 * padding + kernel + output_padding
     y = full[:, :, padding:padding + lo]
     if bias is not None:
         y = y + np.asarray(bias, np.float64)[None, :, None]
@@ -183,7 +184,7 @@ def audio_decode_ref(cfg, dense: dict, codes: np.ndarray, round_gemm_inputs=None
     ch = cfg.channels
     for i, s in enumerate(cfg.strides):
         x = snake_ref(x, dense[f"b{i}.alpha"])
-        x = conv_transpose1d_ref(x, dense[f"b{i}.convt.w"], dense[f"b{i}.convt.b"], 2 * s, s, math.ceil(s / 2))
+        x = conv_transpose1d_ref(x, dense[f"b{i}.convt.w"], dense[f"b{i}.convt.b"], 2 * s, s, math.ceil(s / 2), s % 2)
         for j, d in enumerate((1, 3, 9)):
             p = f"b{i}.r{j}."
             r = conv1d_ref(rnd(snake_ref(x, dense[p + "a1"])), dense[p + "c1.w"], dense[p + "c1.b"], 7, 1, 3 * d, d)

@@ -5,10 +5,12 @@ bytes the GPU runs on (dequantized by the C oracle), then replays the GPU's toke
 checks each one against the oracle's logits:
 
 * if the oracle's top-2 margin exceeds ``tie_tol``, the GPU token must equal the oracle argmax;
-* otherwise the GPU token's oracle logit must be within ``tie_tol`` of the maximum.
+* otherwise the GPU token's oracle logit must be within ``tie_tol`` of the maximum;
+* the number of steps whose GPU token differs from the oracle argmax is bounded.
 
 The exact-token rule is the reference's (token compares use equality, src/torch2vk/runtime/compare.py:119-128);
-the near-tie allowance covers bf16 activation rounding, which the fp32 oracle does not perform.
+the oracle rounds the same tensors to bf16 as the kernels (matrix-product inputs, KV cache), so the near-tie
+allowance covers only fp32 summation order and the bf16 roundings it can flip.
 """
 
 from __future__ import annotations
@@ -43,13 +45,27 @@ def dense_weights(packed: dict[str, np.ndarray], types: dict[str, str], norms: d
 
 def check_greedy_tokens(shape: Qwen3Shape, dense: dict[str, torch.Tensor], prompt: list[int], gpu_tokens: list[int],
                         *, tie_tol: float = 5e-3, kv_bf16: bool = True,
-                        prompt_embeds: torch.Tensor | None = None) -> dict:
+                        prompt_embeds: torch.Tensor | None = None, start: int = 0,
+                        kv_init: tuple[torch.Tensor, torch.Tensor] | None = None,
+                        max_mismatch: int | None = None) -> dict:
     """Teacher-forced replay of ``gpu_tokens`` on the oracle; returns stats, raises AssertionError on mismatch.
-    ``prompt_embeds`` [len(prompt), H] replaces the prompt's embedding lookup (injected audio features)."""
-    model = Qwen3CpuModel(shape, dense, max_positions=len(prompt) + len(gpu_tokens) + 1)
-    hidden = model.forward(torch.tensor(prompt), start=0, embeds=prompt_embeds)
+    ``prompt_embeds`` [len(prompt), H] replaces the prompt's embedding lookup (injected audio features).
+    ``kv_init`` (k, v) [layers, start, NK, D] fills cache positions 0..start-1 first (a prefilled KV cache); the
+    prompt then runs at positions start..  The oracle stages matrix-product inputs and the KV cache in bf16 as the
+    kernels do (``kv_bf16``), so the GPU's logits differ from it only by fp32 summation order.
+    ``max_mismatch`` bounds the steps where the GPU token is not the oracle's argmax (allowed only inside
+    ``tie_tol``); the default is one in ten steps, at least one."""
+    n_pos = start + len(prompt) + len(gpu_tokens) + 1
+    model = Qwen3CpuModel(shape, dense, max_positions=n_pos, stage_bf16=kv_bf16)
+    if kv_init is not None:
+        k0, v0 = kv_init
+        assert k0.shape[1] == start and v0.shape[1] == start
+        model.k_cache[:, :start] = k0.float()
+        model.v_cache[:, :start] = v0.float()
+    hidden = model.forward(torch.tensor(prompt), start=start, embeds=prompt_embeds)
     exact = 0
     near = 0
+    mismatch = 0
     min_margin = float("inf")
     for i, tok in enumerate(gpu_tokens):
         logits = model.logits(hidden).double().numpy()
@@ -64,9 +80,9 @@ def check_greedy_tokens(shape: Qwen3Shape, dense: dict[str, torch.Tensor], promp
             assert logits[best] - logits[tok] <= tie_tol, (
                 f"step {i}: GPU token {tok} logit {logits[tok]:.5f} vs max {logits[best]:.5f}")
             near += 1
+        mismatch += int(tok != best)
         if i + 1 < len(gpu_tokens):
-            if kv_bf16:
-                model.k_cache.copy_(model.k_cache.to(torch.bfloat16).float())
-                model.v_cache.copy_(model.v_cache.to(torch.bfloat16).float())
-            hidden = model.forward(torch.tensor([tok]), start=len(prompt) + i)
-    return {"exact": exact, "near_tie": near, "min_margin": min_margin}
+            hidden = model.forward(torch.tensor([tok]), start=start + len(prompt) + i)
+    bound = max(1, len(gpu_tokens) // 10) if max_mismatch is None else max_mismatch
+    assert mismatch <= bound, f"{mismatch} of {len(gpu_tokens)} GPU tokens are not the oracle's argmax (bound {bound})"
+    return {"exact": exact, "near_tie": near, "mismatch": mismatch, "min_margin": min_margin}

@@ -132,9 +132,14 @@ class Qwen3CpuModel:
     """
 
     def __init__(self, shape: Qwen3Shape, weights: dict[str, torch.Tensor], max_positions: int,
-                 dtype: torch.dtype = torch.float32) -> None:
+                 dtype: torch.dtype = torch.float32, stage_bf16: bool = False) -> None:
         self.shape = shape
         self.dtype = dtype
+        # stage_bf16: round every matrix-product input to bf16 and keep K/V in bf16, as the decode kernels
+        # stage them (RMSNorm output, attention output, SwiGLU output, the LM head input and the KV cache);
+        # the residual stream, q and the products stay fp32.  The reference stages the same tensors in fp16
+        # (src/torch2vk/export/dtype_policy.py:23-36).
+        self.stage_bf16 = stage_bf16
         self.w = {k: v.to(dtype) for k, v in weights.items()}
         s = shape
         self.k_cache = torch.zeros(s.layers, max_positions, s.kv_heads, s.head_dim, dtype=dtype)
@@ -148,6 +153,9 @@ class Qwen3CpuModel:
         xf = x.to(torch.float32)
         inv = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + RMS_EPS)
         return (xf * inv).to(x.dtype) * w
+
+    def _stage(self, x: torch.Tensor) -> torch.Tensor:
+        return x.to(torch.bfloat16).to(x.dtype) if self.stage_bf16 else x
 
     def _rope(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         ang = positions.to(torch.float64)[:, None] * self.inv_freq[None, :]
@@ -174,14 +182,14 @@ class Qwen3CpuModel:
         n_layers = s.layers if layers is None else layers
         for i in range(n_layers):
             p = f"layers.{i}."
-            x = self._rms(h, w[p + "input_norm"])
+            x = self._stage(self._rms(h, w[p + "input_norm"]))
             q = (x @ w[p + "q"].T).view(t_len, s.heads, s.head_dim)
             k = (x @ w[p + "k"].T).view(t_len, s.kv_heads, s.head_dim)
             v = (x @ w[p + "v"].T).view(t_len, s.kv_heads, s.head_dim)
             q = self._rope(self._rms(q, w[p + "q_norm"]), positions)
             k = self._rope(self._rms(k, w[p + "k_norm"]), positions)
-            self.k_cache[i, start:start + t_len] = k
-            self.v_cache[i, start:start + t_len] = v
+            self.k_cache[i, start:start + t_len] = self._stage(k)
+            self.v_cache[i, start:start + t_len] = self._stage(v)
             keys = self.k_cache[i, :start + t_len].repeat_interleave(group, dim=1)
             vals = self.v_cache[i, :start + t_len].repeat_interleave(group, dim=1)
             scores = torch.einsum("thd,shd->hts", q.float(), keys.float()) / math.sqrt(s.head_dim)
@@ -192,12 +200,12 @@ class Qwen3CpuModel:
                 scores = scores + mask.float()[None]
             probs = torch.softmax(scores, dim=-1)
             attn = torch.einsum("hts,shd->thd", probs, vals.float()).to(self.dtype).reshape(t_len, -1)
-            h = h + attn @ w[p + "o"].T
-            x = self._rms(h, w[p + "post_norm"])
+            h = h + self._stage(attn) @ w[p + "o"].T
+            x = self._stage(self._rms(h, w[p + "post_norm"]))
             g = x @ w[p + "gate"].T
             u = x @ w[p + "up"].T
-            h = h + (torch.nn.functional.silu(g) * u) @ w[p + "down"].T
+            h = h + self._stage(torch.nn.functional.silu(g) * u) @ w[p + "down"].T
         return self._rms(h, w["norm"]) if all_positions else self._rms(h[-1], w["norm"])
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
-        return hidden @ self.w["lm_head"].T
+        return self._stage(hidden) @ self.w["lm_head"].T

@@ -95,9 +95,9 @@ def test_residual_unit_matches_oracle(device, dil):
     assert_close(y, ref, max_abs=2e-2 * float(np.abs(ref).max()), min_cos=0.9999, what="residual unit")
 
 
-@pytest.mark.parametrize("ci,co,k,stride,pad", [(64, 32, 16, 8, 4), (96, 48, 10, 5, 3), (32, 32, 4, 2, 1),
-                                                (48, 24, 3, 1, 0)])
-def test_conv_transpose1d_q8_0_matches_oracle(device, ci, co, k, stride, pad):
+@pytest.mark.parametrize("ci,co,k,stride,pad,opad", [(64, 32, 16, 8, 4, 0), (96, 48, 10, 5, 3, 0), (32, 32, 4, 2, 1, 0),
+                                                     (48, 24, 3, 1, 0, 0), (96, 48, 10, 5, 3, 1), (64, 32, 6, 3, 2, 1)])
+def test_conv_transpose1d_q8_0_matches_oracle(device, ci, co, k, stride, pad, opad):
     """The reference's Q8_0 rows [Ci, Co K] read as they are, fp32 arithmetic: agreement to fp32 rounding of
     the sums against the float64 oracle on the exactly dequantized weights."""
     from torch2vk_amd import kernels
@@ -114,8 +114,9 @@ def test_conv_transpose1d_q8_0_matches_oracle(device, ci, co, k, stride, pad):
     packed = kernels.quantize(torch.from_numpy(w).to(device), "q8_0")
     dense = oracle.dequant_q8_0(packed.cpu().numpy(), kpad)[:, :kk]
     y = kernels.conv_transpose1d_q8_0(torch.from_numpy(x).to(device), packed, torch.from_numpy(bias).to(device),
-                                      co, k, stride=stride, padding=pad).cpu().numpy()
-    ref = O.conv_transpose1d_ref(x.transpose(0, 2, 1), dense, bias, k, stride, pad).transpose(0, 2, 1)
+                                      co, k, stride=stride, padding=pad, output_padding=opad).cpu().numpy()
+    ref = O.conv_transpose1d_ref(x.transpose(0, 2, 1), dense, bias, k, stride, pad, opad).transpose(0, 2, 1)
+    assert y.shape[1] == (length - 1) * stride - 2 * pad + k + opad
     assert y.shape == ref.shape
     assert_close(y, ref, max_abs=1e-5 * float(np.abs(ref).max()), min_cos=0.9999999, what="conv_transpose1d")
 
@@ -177,14 +178,16 @@ def test_token_update_topk_matches_oracle(device):
     assert np.array_equal(idd.cpu().numpy(), rids)
 
 
-def test_audio_decoder_matches_oracle(device):
-    """The whole acoustic decoder (2 codebooks, 2 upsampling blocks of strides 2 and 4, 6 residual units)
-    against the float64 oracle composite on the same dequantized weights, with GEMM activations and weights
-    rounded to bf16 where the GPU stages them, so only summation order separates the two."""
+@pytest.mark.parametrize("strides", [(2, 4), (8, 5, 4, 2, 3)])
+def test_audio_decoder_matches_oracle(device, strides):
+    """The whole acoustic decoder (2 codebooks, upsampling blocks of strides 2 and 4, and the reference's five
+    blocks of strides 8, 5, 4, 2, 3 with 960 samples per frame) against the float64 oracle composite on the same
+    dequantized weights, with GEMM activations and weights rounded to bf16 where the GPU stages them, so only
+    summation order separates the two."""
     from torch2vk_amd.omnivoice.decoder import AudioDecoderConfig, OmniVoiceAudioDecoder, out_len, synthetic_dense
 
-    cfg = AudioDecoderConfig(codebooks=2, vocab=16, codebook_dim=32, latent=64, hidden=64, channels=128,
-                             strides=(2, 4))
+    cfg = AudioDecoderConfig(codebooks=2, vocab=16, codebook_dim=32, latent=64, hidden=64,
+                             channels=128 if len(strides) == 2 else 512, strides=strides)
     dense = synthetic_dense(cfg, seed=5)
     dec = OmniVoiceAudioDecoder(cfg, dense, device)
     deq = {}
@@ -202,9 +205,17 @@ def test_audio_decoder_matches_oracle(device):
     y = dec.decode(torch.from_numpy(codes)).cpu().numpy()
     ref = O.audio_decode_ref(cfg, deq, codes, round_gemm_inputs=_bf16)
     assert y.shape == (out_len(cfg, 10),) == ref.shape
+    if strides == (8, 5, 4, 2, 3):
+        assert y.shape == (960 * 10,)
     print(f"audio decoder: {y.shape[0]} samples, max-abs {np.abs(y - ref).max():.3e}, max |ref| {np.abs(ref).max():.3e}",
           flush=True)
-    assert_close(y, ref, max_abs=1e-4 * float(np.abs(ref).max()), min_cos=0.9999999, what="waveform")
+    if len(strides) == 2:
+        assert_close(y, ref, max_abs=1e-4 * float(np.abs(ref).max()), min_cos=0.9999999, what="waveform")
+    else:
+        # 5 blocks and 15 residual units amplify a single flipped bf16 rounding of a staged activation: the
+        # float64 oracle itself moves by 1.9 % of its maximum (cosine 0.99983) when its staged values are
+        # perturbed by 1e-7 relative before rounding, so summation order alone gives differences of that size
+        assert_close(y, ref, max_abs=5e-2 * float(np.abs(ref).max()), min_cos=0.999, what="waveform")
 
 
 def test_generation_loop(device):

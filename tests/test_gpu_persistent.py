@@ -139,3 +139,118 @@ def test_persistent_graph_replay_equals_eager(device, setup_8b2):
     n = prompt.numel() + 17
     torch.testing.assert_close(a.k_cache[:, :n], b.k_cache[:, :n], rtol=0, atol=0)
     torch.testing.assert_close(a.v_cache[:, :n], b.v_cache[:, :n], rtol=0, atol=0)
+
+
+# ------------------------------------------------------------------------------------------------------
+# The benchmarked configurations: the 8B shape at a KV cache of 4096 positions and near the 8192 capacity
+# (17 and 32 attention rows per wave), and the full 28-layer 0.6B decoder.
+
+
+@pytest.fixture(scope="module")
+def setup_8b_long(device):
+    from torch2vk_amd.qwen3.config import QWEN3_8B
+    from torch2vk_amd.qwen3.weights import matrix_shapes, synthetic_weights
+
+    cfg = replace(QWEN3_8B, layers=2, vocab=4096, eos_token_ids=(4095,))
+    w = synthetic_weights(cfg, device=device, seed=8, std=0.02, norm_std=0.1)
+    shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
+                       head_dim=cfg.head_dim, mlp=cfg.mlp, vocab=cfg.vocab, rope_theta=cfg.rope_theta)
+    dense = dense_weights({k: v.cpu().numpy() for k, v in w.packed.items()}, w.types,
+                          {k: v.cpu().numpy() for k, v in w.norms.items()}, matrix_shapes(cfg))
+    return cfg, w, shape, dense
+
+
+@pytest.mark.parametrize("pos", [4096, 8100])
+def test_persistent_long_kv_matches_per_op(device, setup_8b_long, pos):
+    """Layer 0 of the 8B shape at cache position 4096 (the headline bench: 17 rows per attention wave) and 8100
+    (32 rows per wave, the kernel's limit) on an N(0,1) cache: q|k|v and the new K/V rows are bit-identical to
+    the per-op kernels'; the attention output differs by at most bf16 rounding of a differently ordered sum."""
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg, w, _, _ = setup_8b_long
+    print(f"persistent vs per-op, 8B shape, layer 0 at pos {pos}", flush=True)
+    a = Qwen3Decoder(w, max_positions=8192, max_new_tokens=4, persistent=True)
+    b = Qwen3Decoder(w, max_positions=8192, max_new_tokens=4, persistent=False)
+    g = torch.Generator(device=device)
+    g.manual_seed(pos)
+    kc = torch.randn(a.k_cache.shape, generator=g, device=device).to(torch.bfloat16)
+    vc = torch.randn(a.v_cache.shape, generator=g, device=device).to(torch.bfloat16)
+    h0 = torch.randn(cfg.hidden, generator=g, device=device)
+    for d in (a, b):
+        d.k_cache.copy_(kc)
+        d.v_cache.copy_(vc)
+        d.h.copy_(h0)
+        d.position.fill_(pos)
+    del kc, vc
+    a.layer_table = a.layer_table[:1].contiguous()
+    a.run_decode_layers()
+    b.run_decode_layer(0)
+    torch.cuda.synchronize()
+    a.check_status()
+    assert int(a.status.item()) == 0
+    qkv = _ws_ll32(a, WS_QKV, cfg.q_dim + 2 * cfg.kv_dim)
+    torch.testing.assert_close(qkv, torch.cat([b.q, b.k, b.v]), rtol=0, atol=0)
+    torch.testing.assert_close(a.k_cache[0], b.k_cache[0], rtol=0, atol=0)
+    torch.testing.assert_close(a.v_cache[0], b.v_cache[0], rtol=0, atol=0)
+    attn = _ws_ll16(a, _ws_attn(cfg), cfg.q_dim).float()
+    ref = b.attn.float()
+    err = (attn - ref).abs().max().item()
+    print(f"attention max-abs diff {err:.3e} (max {ref.abs().max().item():.3e})", flush=True)
+    assert err <= 2 ** -7 * ref.abs().max().item()
+    herr = (a.h - b.h).abs().max().item()
+    assert herr <= 1e-3 * b.h.abs().max().item(), herr
+
+
+def test_persistent_long_kv_decode_matches_oracle(device, setup_8b_long):
+    """Greedy decode with the persistent kernel from an N(0,1) KV cache of 4096 positions (the headline bench's
+    state): a 2-token prompt at positions 4096-4097, then 8 tokens through graph replay; every token against the
+    CPU oracle started from the same cache, and the kernel's status word stays clear."""
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg, w, shape, dense = setup_8b_long
+    start = 4096
+    dec = Qwen3Decoder(w, max_positions=start + 64, max_new_tokens=16, persistent=True)
+    dec.stop_on_eos = False
+    g = torch.Generator(device=device)
+    g.manual_seed(41)
+    dec.k_cache[:, :start].normal_(generator=g)
+    dec.v_cache[:, :start].normal_(generator=g)
+    prompt = [77, 3001]
+    print(f"persistent 8B-shape decode from KV {start}", flush=True)
+    dec.prefill(torch.tensor(prompt), start=start)
+    dec.run_steps(7, steps_per_graph=4, use_graph=True)
+    toks = dec.generated[:int(dec.length.item())].tolist()
+    dec.check_status()
+    assert int(dec.status.item()) == 0 and len(toks) == 8
+    print(f"tokens {toks}", flush=True)
+    kv = (dec.k_cache[:, :start].cpu(), dec.v_cache[:, :start].cpu())
+    stats = check_greedy_tokens(shape, dense, prompt, toks, start=start, kv_init=kv, tie_tol=2e-3)
+    print(stats, flush=True)
+
+
+def test_persistent_0_6b_full_depth_matches_oracle(device):
+    """The whole 28-layer Qwen3-0.6B decoder (vocab 151936) in the persistent kernel: a 128-token random prompt
+    fed one launch per position, then 32 greedy tokens in HIP graphs; status clear after all 160 launches and
+    every token against the CPU oracle.  This depth is where residual hold threads once polled rows owned by
+    another block and a bounded wait gave up."""
+    from torch2vk_amd.qwen3.config import QWEN3_0_6B
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+    from torch2vk_amd.qwen3.weights import matrix_shapes, synthetic_weights
+
+    cfg = QWEN3_0_6B
+    print("persistent 0.6B, 28 layers: weights", flush=True)
+    w = synthetic_weights(cfg, device=device, seed=0, std=0.02, norm_std=0.1)
+    prompt = np.random.default_rng(0).integers(0, cfg.vocab, 128).tolist()
+    dec = Qwen3Decoder(w, max_positions=256, max_new_tokens=40, persistent=True)
+    assert dec.persistent
+    dec.stop_on_eos = False
+    toks = dec.generate(torch.tensor(prompt), 32, steps_per_graph=8, use_graph=True)
+    assert int(dec.status.item()) == 0 and len(toks) == 32
+    print(f"tokens {toks}", flush=True)
+    shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
+                       head_dim=cfg.head_dim, mlp=cfg.mlp, vocab=cfg.vocab, rope_theta=cfg.rope_theta)
+    dense = dense_weights({k: v.cpu().numpy() for k, v in w.packed.items()}, w.types,
+                          {k: v.cpu().numpy() for k, v in w.norms.items()}, matrix_shapes(cfg))
+    del w, dec
+    stats = check_greedy_tokens(shape, dense, prompt, toks, tie_tol=2e-3)
+    print(stats, flush=True)

@@ -507,8 +507,10 @@ extern "C" int t2h_conv_transpose1d_q8_0(const float* x, const int64_t* x_stride
                                          uint32_t kh, uint32_t stride, uint32_t pad, uint32_t lo, void* stream) {
     if (!x || !x_strides || !w || !out) return T2H_ERR_NULL;
     if (ci == 0 || co == 0 || kh == 0 || stride == 0 || li == 0) return T2H_ERR_SHAPE;
-    // L_out of a transposed conv with no output padding
-    if ((int64_t)lo != ((int64_t)li - 1) * stride - 2 * (int64_t)pad + kh) return T2H_ERR_SHAPE;
+    // L_out of a transposed conv plus an output padding in [0, stride): the extra last positions take the taps
+    // that reach them (the reference's blocks produce stride * L_in outputs, output padding stride % 2)
+    const int64_t lo_min = ((int64_t)li - 1) * stride - 2 * (int64_t)pad + kh;
+    if ((int64_t)lo < lo_min || (int64_t)lo >= lo_min + stride) return T2H_ERR_SHAPE;
     if ((uint64_t)co * kh > 0x7fffffffu || pad > 0xffffu || li > 0x7fffffffu) return T2H_ERR_SHAPE;
     if (reinterpret_cast<uintptr_t>(w) % 2 != 0) return T2H_ERR_ALIGN;
     for (int i = 0; i < 3; ++i)

@@ -99,7 +99,23 @@ struct DlArgs {
     uint32_t* attn_ll;        // [QD] bf16 + epoch16: attention output
     uint32_t* act_ll;         // [MLP] bf16 + epoch16: SwiGLU output
     uint32_t* status;         // set non-zero when a consumer spin timed out
+    uint64_t* trace;          // phase timestamps (the traced build only): [layer][phase][block][DL_TR_SLOTS]
 };
+
+// Phase timeline of the traced instantiation: per (layer, phase, block) the
+// 100 MHz real-time clock at the phase's start, when its input is in hand,
+// after its first unit is reduced (GEMV) or its softmax (attention), at its
+// end, and the number of polls its first wave made for the input.
+enum DlTraceSlot { DL_TR_BEGIN = 0, DL_TR_READY, DL_TR_FIRST, DL_TR_END, DL_TR_POLLS, DL_TR_SLOTS = 8 };
+constexpr int DL_TR_PHASES = 6;  // qkv, attention, merge, o, gate|up, down
+
+__device__ __forceinline__ uint64_t* dl_trace_at(const DlArgs& a, uint32_t layer, int phase) {
+    return a.trace == nullptr ? nullptr
+                              : a.trace + (((size_t)layer * DL_TR_PHASES + phase) * DL_BLOCKS + blockIdx.x) * DL_TR_SLOTS;
+}
+__device__ __forceinline__ void dl_stamp(uint64_t* tr, int slot) {
+    if (tr != nullptr && threadIdx.x == 0) tr[slot] = __builtin_amdgcn_s_memrealtime();
+}
 
 // The thread index as an opaque value: per-lane offsets derived from it are
 // recomputed in every phase instead of being hoisted out of the layer loop,
@@ -162,8 +178,9 @@ constexpr uint32_t DL_STATUS_TIMEOUT = 0x80000000u;
 
 // Load N words (addr(i)) until ok(i, word) holds for all of them; bounded.
 template <int N, class Addr, class Ok>
-__device__ __forceinline__ void ll_wait(uint64_t (&w)[N], Addr addr, Ok ok, uint32_t* status, uint32_t site) {
-    for (uint32_t polls = 0;; ++polls) {
+__device__ __forceinline__ uint32_t ll_wait(uint64_t (&w)[N], Addr addr, Ok ok, uint32_t* status, uint32_t site) {
+    uint32_t polls = 0;
+    for (;; ++polls) {
 #pragma unroll
         for (int i = 0; i < N; ++i) w[i] = ll_load(addr(i));
         bool all = true;
@@ -176,6 +193,7 @@ __device__ __forceinline__ void ll_wait(uint64_t (&w)[N], Addr addr, Ok ok, uint
         }
         __builtin_amdgcn_s_sleep(1);
     }
+    return polls;
 }
 
 template <int GROUP>
@@ -312,6 +330,7 @@ struct DlHold {
     int rpw;
     bool spread;      // the phase's unit mapping (dl_unit)
     uint32_t n_rows;
+    uint64_t* tr;     // phase timeline slots (traced build), else nullptr
 };
 
 // Row of hold slot t, or n_rows when the slot's unit has no such row.  Only a
@@ -350,6 +369,7 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
     float hold = 0.0f;
     if (has_hold && hd.kind == DL_SRC_PLAIN) hold = reinterpret_cast<const float*>(hd.src)[hold_row];
     float4 hv[PT];
+    uint32_t polls = 0;
     if (src_kind == DL_SRC_PLAIN) {
         const float* x = reinterpret_cast<const float*>(src);
 #pragma unroll
@@ -357,8 +377,8 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
     } else if (src_kind == DL_SRC_LL32) {
         const uint64_t* x = reinterpret_cast<const uint64_t*>(src);
         uint64_t w[4 * PT];
-        ll_wait(w, [&](int i) { return x + elem(i / 4) + (i % 4); }, [&](int, uint64_t v) { return ll_ok32(v, e); },
-                status, site);
+        polls = ll_wait(w, [&](int i) { return x + elem(i / 4) + (i % 4); },
+                        [&](int, uint64_t v) { return ll_ok32(v, e); }, status, site);
 #pragma unroll
         for (int j = 0; j < PT; ++j)
             hv[j] = make_float4(ll_val32(w[4 * j]), ll_val32(w[4 * j + 1]), ll_val32(w[4 * j + 2]),
@@ -367,7 +387,7 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
         // 2 elements per word; word 2 PT is the residual value (threads without one re-read word 0)
         const uint64_t* x = reinterpret_cast<const uint64_t*>(src);
         uint64_t w[2 * PT + 1];
-        ll_wait(w,
+        polls = ll_wait(w,
                 [&](int i) {
                     return i < 2 * PT ? x + elem(i / 2) / 2 + (i % 2) : (hold_ll_wait ? hold_ll : x + elem(0) / 2);
                 },
@@ -383,6 +403,7 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
                                 bf16_bits_to_f32((uint32_t)(w[2 * j + 1] >> 32) & 0xffffu));
         if (hold_ll_wait) hold = ll_val32(w[2 * PT]);
     }
+    if (hd.tr != nullptr && tid == 0) hd.tr[DL_TR_POLLS] = polls;
     if (has_hold) hd.lds[tid] = hold;
 #pragma unroll
     for (int j = 0; j < PT; ++j)
@@ -470,6 +491,7 @@ struct DlOut {
     float* plain;        // RESID on the last layer: the caller's h (no epoch)
     DlHold hold;         // RESID: where the old h comes from (staged in LDS with x)
     uint32_t e_out;      // epoch written
+    uint64_t* tr;        // phase timeline slots (traced build), else nullptr
 };
 
 //   STORE: y[row] = dot;  RESID: y[row] = h_old[row] + dot;  SWIGLU: y[row] = bf16(silu(g) * u)
@@ -536,9 +558,11 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
     hd.rpw = RPW;
     hd.spread = SPREAD;
     hd.n_rows = rows.n_rows;
+    hd.tr = out.tr;
     if (EPI != DL_EPI_RESID) hd.kind = -1;
     dl_stage_x<NSB * 256, RMSNORM>(sm.g.xp, sm.g.xsum, sm.g.red, src_kind, x_src, e_x, norm_w, eps, hd, status,
                                    site);
+    dl_stamp(out.tr, DL_TR_READY);
     if (!active) return;
 #pragma unroll
     for (int i = PRE; i < R; ++i) dl_issue_unit(u[i], rows, dl_unit<SPREAD>(wave, i));
@@ -548,6 +572,7 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
         __builtin_amdgcn_sched_barrier(0);
         float res[NG][RPW];
         dl_dot_unit(u[i], sm.g.xp, sm.g.xsum, lc, res);
+        if (i == 0) dl_stamp(out.tr, DL_TR_FIRST);
         dl_store_unit<NG, RPW, EPI>(out, dl_unit<SPREAD>(wave, i), rows.n_rows, res,
                                     &sm.g.hold[(wave * UPW + i) * RPW]);
         __builtin_amdgcn_sched_barrier(0);
@@ -622,7 +647,7 @@ __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w,
 template <class S>
 __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP>& sm, const DlArgs& a,
                                               const uint64_t* lp, int kvh, int bs, int pos, int L, uint32_t e_qkv,
-                                              uint32_t e_part, uint32_t site) {
+                                              uint32_t e_part, uint32_t site, uint64_t* tr) {
     constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int span = dl_att_span(L);
@@ -650,7 +675,9 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
     if (wave < GROUP) {
         const int hq = kvh * GROUP + wave;
         uint64_t w[2];
-        ll_wait(w, [&](int i) { return q + hq * DL_D + lane + 64 * i; }, ok, a.status, site | DL_W_ATTN_Q);
+        const uint32_t polls =
+            ll_wait(w, [&](int i) { return q + hq * DL_D + lane + 64 * i; }, ok, a.status, site | DL_W_ATTN_Q);
+        if (tr != nullptr && tid == 0) tr[DL_TR_POLLS] = polls;
         float r0, r1;
         dl_norm_rope(ll_val32(w[0]), ll_val32(w[1]), q_norm, q_norm != nullptr, a.eps, cs, sn, rope, r0, r1);
         const float scale = 1.0f / sqrtf((float)DL_D);
@@ -674,6 +701,7 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
         reinterpret_cast<uint32_t*>(vc + off)[lane] = vnew;
     }
     __syncthreads();
+    dl_stamp(tr, DL_TR_READY);
     // V_LATE: V is needed only after the scores, issued behind every wait of the phase
     if constexpr (S::v_late) dl_attn_issue_v(bk, vc, kvh, p0, rows);
 
@@ -752,6 +780,7 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    dl_stamp(tr, DL_TR_FIRST);
     float o0[GROUP], o1[GROUP];
 #pragma unroll
     for (int gg = 0; gg < GROUP; ++gg) o0[gg] = o1[gg] = 0.0f;
@@ -819,19 +848,21 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
 // Head hq = blockIdx.x (< NH): merge the DL_ATT_SLOTS block partials of its kv head.
 template <class S>
 __device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP>& sm, const DlArgs& a, int hq, uint32_t e_part,
-                                               uint32_t e_attn, uint32_t site) {
+                                               uint32_t e_attn, uint32_t site, uint64_t* tr) {
     constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kvh = hq / GROUP, gg = hq % GROUP;
     constexpr int PER_WAVE = DL_ATT_SLOTS / DL_WAVES;  // 4 partials per wave
     __syncthreads();  // every wave is done with the previous phase's LDS
     uint64_t w[4 * PER_WAVE];
-    ll_wait(w, [&](int i) {
+    const uint32_t polls = ll_wait(w, [&](int i) {
                 const int bs = wave * PER_WAVE + i / 4, k = i % 4;
                 const uint64_t* pg = a.part_ll + (((size_t)kvh * DL_ATT_SLOTS + bs) * GROUP + gg) * (2 + DL_D);
                 return k < 2 ? pg + k : pg + 2 + 2 * lane + (k - 2);
             },
             [&](int, uint64_t v) { return ll_ok32(v, e_part); }, a.status, site | DL_W_MERGE);
+    if (tr != nullptr && tid == 0) tr[DL_TR_POLLS] = polls;
+    dl_stamp(tr, DL_TR_READY);
     float2 ml[PER_WAVE], ov[PER_WAVE];
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
@@ -876,7 +907,7 @@ __device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP>& sm, const Dl
 
 // ------------------------------------------------------------- the kernel ----
 
-template <class S>
+template <class S, bool TRACE>
 __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs a) {
     __shared__ __align__(16) DlShared<S> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -957,6 +988,10 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         const uint32_t e_hprev = first ? 0u : dl_epoch(seq, layer - 1, DL_E_H_DOWN);
         DlOut out;
         out.hold.kind = -1;
+        // phase timeline slots of this block (the traced instantiation only)
+        auto trp = [&](int phase) -> uint64_t* { return TRACE ? dl_trace_at(a, layer, phase) : nullptr; };
+        out.tr = trp(0);
+        dl_stamp(out.tr, DL_TR_BEGIN);
         // ---- Q|K|V: RMSNorm(h) . [Wq; Wk; Wv]^T.  The attention K/V rows depend
         // on nothing computed in this launch: they are issued with the Q|K|V
         // weights, before h is awaited, and stream during that hand-off.
@@ -970,16 +1005,27 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
             sm, uq, qkv_rows(layer), first ? DL_SRC_PLAIN : DL_SRC_LL32,
             first ? static_cast<const void*>(a.h) : static_cast<const void*>(a.h_ll), e_hprev,
             dl_gptr<const float>(layer_ptr(layer, DL_IN_NORM)), a.eps, out, a.status, lsite | DL_W_QKV);
+        dl_stamp(out.tr, DL_TR_END);
         // ---- attention split
         {
+            uint64_t* tr = trp(1);
+            dl_stamp(tr, DL_TR_BEGIN);
             uint64_t lp[DL_LAYER_PTRS];
 #pragma unroll
             for (int i = 0; i < DL_LAYER_PTRS; ++i) lp[i] = layer_ptr(layer, i);
-            dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, pos, L, e_qkv, e_part, lsite);
+            dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, pos, L, e_qkv, e_part, lsite, tr);
+            dl_stamp(tr, DL_TR_END);
         }
         // ---- attention merge (blocks 0..NH-1, one q head each)
-        if (blockIdx.x < S::NH) dl_merge_phase<S>(sm.at, a, blockIdx.x, e_part, e_attn, lsite);
+        if (blockIdx.x < S::NH) {
+            uint64_t* tr = trp(2);
+            dl_stamp(tr, DL_TR_BEGIN);
+            dl_merge_phase<S>(sm.at, a, blockIdx.x, e_part, e_attn, lsite, tr);
+            dl_stamp(tr, DL_TR_END);
+        }
         // ---- o_proj + residual
+        out.tr = trp(3);
+        dl_stamp(out.tr, DL_TR_BEGIN);
         DlUnit<S::QSB, 1> uo[S::o_u];
         dl_issue_pre<S::QSB, 1, S::o_u, S::o_p, o_sp>(uo, o_rows(layer));
         out.ll32 = a.h_ll;
@@ -990,7 +1036,10 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         out.e_out = e_ho;
         dl_gemv_phase<S::QSB, 1, S::o_u, S::o_r, S::o_p, DL_EPI_RESID, false, o_sp>(
             sm, uo, o_rows(layer), DL_SRC_LL16, a.attn_ll, e_attn, nullptr, a.eps, out, a.status, lsite | DL_W_O);
+        dl_stamp(out.tr, DL_TR_END);
         // ---- RMSNorm + gate|up + SwiGLU
+        out.tr = trp(4);
+        dl_stamp(out.tr, DL_TR_BEGIN);
         DlUnit<S::HSB, 2> ug[S::gu_u];
         dl_issue_pre<S::HSB, 2, S::gu_u, S::gu_p, gu_sp>(ug, gu_rows(layer));
         out.ll16 = a.act_ll;
@@ -998,7 +1047,10 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         dl_gemv_phase<S::HSB, 2, S::gu_u, S::gu_r, S::gu_p, DL_EPI_SWIGLU, true, gu_sp>(
             sm, ug, gu_rows(layer), DL_SRC_LL32, a.h_ll, e_ho,
             dl_gptr<const float>(layer_ptr(layer, DL_POST_NORM)), a.eps, out, a.status, lsite | DL_W_GU);
+        dl_stamp(out.tr, DL_TR_END);
         // ---- down + residual (the last layer writes the caller's h)
+        out.tr = trp(5);
+        dl_stamp(out.tr, DL_TR_BEGIN);
         DlUnit<S::MSB, 1> ud[S::dn_u];
         dl_issue_pre<S::MSB, 1, S::dn_u, S::dn_p, dn_sp>(ud, down_rows(layer));
         out.ll32 = a.h_ll;
@@ -1010,6 +1062,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         dl_gemv_phase<S::MSB, 1, S::dn_u, S::dn_r, S::dn_p, DL_EPI_RESID, false, dn_sp>(
             sm, ud, down_rows(layer), DL_SRC_LL16, a.act_ll, e_act, nullptr, a.eps, out, a.status,
             lsite | DL_W_DOWN);
+        dl_stamp(out.tr, DL_TR_END);
     }
     // Every block has read the launch counter before block 0 can get here: its
     // last phase consumed every block's output.
@@ -1052,7 +1105,8 @@ static bool dl_grid_fits() {
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_layers_kernel<S>, DL_THREADS, 0) != hipSuccess) {
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_layers_kernel<S, false>, DL_THREADS, 0) !=
+            hipSuccess) {
         fits = 0;
         return false;
     }
@@ -1069,7 +1123,7 @@ static bool dl_is(uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk, uint3
 template <class S>
 static int dl_launch(const uint64_t* layer_table, uint32_t n_layers, uint32_t s_cap, float* h,
                      const int32_t* cache_position, float eps, float theta, void* workspace, size_t workspace_bytes,
-                     uint32_t* status, void* stream) {
+                     uint32_t* status, uint64_t* trace, void* stream) {
     const DlLayout l = dl_layout<S>();
     if (workspace_bytes < l.total) return T2H_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return T2H_ERR_ALIGN;
@@ -1090,8 +1144,13 @@ static int dl_launch(const uint64_t* layer_table, uint32_t n_layers, uint32_t s_
     a.h_ll = reinterpret_cast<uint64_t*>(ws + l.h);
     a.part_ll = reinterpret_cast<uint64_t*>(ws + l.part);
     a.status = status;
-    hipLaunchKernelGGL(decode_layers_kernel<S>, dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
-                       reinterpret_cast<hipStream_t>(stream), a);
+    a.trace = trace;
+    if (trace == nullptr)
+        hipLaunchKernelGGL((decode_layers_kernel<S, false>), dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
+                           reinterpret_cast<hipStream_t>(stream), a);
+    else
+        hipLaunchKernelGGL((decode_layers_kernel<S, true>), dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
+                           reinterpret_cast<hipStream_t>(stream), a);
     T2H_LAUNCH_CHECK();
     return T2H_OK;
 }
@@ -1107,10 +1166,10 @@ extern "C" size_t t2h_qwen3_decode_layers_workspace_bytes(uint32_t hidden, uint3
     return 0;
 }
 
-extern "C" int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden, uint32_t mlp,
-                                       uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap, float* h,
-                                       const int32_t* cache_position, float eps, float theta, void* workspace,
-                                       size_t workspace_bytes, uint32_t* status, void* stream) {
+static int dl_entry(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden, uint32_t mlp, uint32_t nh,
+                    uint32_t nk, uint32_t d, uint32_t s_cap, float* h, const int32_t* cache_position, float eps,
+                    float theta, void* workspace, size_t workspace_bytes, uint32_t* status, uint64_t* trace,
+                    void* stream) {
     if (!layer_table || !h || !cache_position || !workspace || !status) return T2H_ERR_NULL;
     const bool is8b = dl_is<DlQwen3_8B>(hidden, mlp, nh, nk, d);
     if (!is8b && !dl_is<DlQwen3_0_6B>(hidden, mlp, nh, nk, d)) return T2H_ERR_UNSUPPORTED;
@@ -1120,7 +1179,31 @@ extern "C" int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_l
     if ((size_t)(s_cap + DL_ATT_SLOTS * DL_WAVES - 1) / (DL_ATT_SLOTS * DL_WAVES) > DL_ATT_POS)
         return T2H_ERR_UNSUPPORTED;  // more than 32 positions per wave
     return is8b ? dl_launch<DlQwen3_8B>(layer_table, n_layers, s_cap, h, cache_position, eps, theta, workspace,
-                                        workspace_bytes, status, stream)
+                                        workspace_bytes, status, trace, stream)
                 : dl_launch<DlQwen3_0_6B>(layer_table, n_layers, s_cap, h, cache_position, eps, theta, workspace,
-                                          workspace_bytes, status, stream);
+                                          workspace_bytes, status, trace, stream);
+}
+
+extern "C" int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden, uint32_t mlp,
+                                       uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap, float* h,
+                                       const int32_t* cache_position, float eps, float theta, void* workspace,
+                                       size_t workspace_bytes, uint32_t* status, void* stream) {
+    return dl_entry(layer_table, n_layers, hidden, mlp, nh, nk, d, s_cap, h, cache_position, eps, theta, workspace,
+                    workspace_bytes, status, nullptr, stream);
+}
+
+extern "C" size_t t2h_qwen3_decode_layers_trace_bytes(uint32_t n_layers) {
+    return (size_t)n_layers * DL_TR_PHASES * DL_BLOCKS * DL_TR_SLOTS * sizeof(uint64_t);
+}
+
+extern "C" int t2h_qwen3_decode_layers_traced(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden,
+                                              uint32_t mlp, uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap,
+                                              float* h, const int32_t* cache_position, float eps, float theta,
+                                              void* workspace, size_t workspace_bytes, uint32_t* status,
+                                              uint64_t* trace, size_t trace_bytes, void* stream) {
+    if (!trace) return T2H_ERR_NULL;
+    if (trace_bytes < t2h_qwen3_decode_layers_trace_bytes(n_layers)) return T2H_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(trace) % 8 != 0) return T2H_ERR_ALIGN;
+    return dl_entry(layer_table, n_layers, hidden, mlp, nh, nk, d, s_cap, h, cache_position, eps, theta, workspace,
+                    workspace_bytes, status, trace, stream);
 }

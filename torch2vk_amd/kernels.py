@@ -527,8 +527,9 @@ def decode_layer_table(packed: dict[str, torch.Tensor], norms: dict[str, torch.T
 
 def decode_layers(table: torch.Tensor, h: torch.Tensor, cache_position: torch.Tensor, workspace: torch.Tensor,
                   status: torch.Tensor, *, hidden: int, mlp: int, nh: int, nk: int, d: int, s_cap: int,
-                  eps: float = RMS_EPS, theta: float = 1.0e6) -> None:
-    """All decoder layers of one token in one persistent launch (h updated in place)."""
+                  eps: float = RMS_EPS, theta: float = 1.0e6, trace: torch.Tensor | None = None) -> None:
+    """All decoder layers of one token in one persistent launch (h updated in place).  ``trace`` (uint64
+    [layers, 6, 256, 8], see decode_layers_trace) runs the instantiation that records the phase timeline."""
     _check(table, "layer_table", torch.int64, align=8)
     _check(h, "h", torch.float32)
     _check(cache_position, "cache_position", torch.int32, align=4)
@@ -536,8 +537,26 @@ def decode_layers(table: torch.Tensor, h: torch.Tensor, cache_position: torch.Te
     _check(status, "status", torch.int32, align=4)
     if table.dim() != 2 or table.shape[1] != 13:
         raise ValueError(f"layer_table must be int64 [layers, 13], got {tuple(table.shape)}")
-    call("t2h_qwen3_decode_layers", ptr(table), int(table.shape[0]), hidden, mlp, nh, nk, d, s_cap, ptr(h),
-         ptr(cache_position), eps, theta, ptr(workspace), workspace.numel(), ptr(status), stream_handle())
+    args = (ptr(table), int(table.shape[0]), hidden, mlp, nh, nk, d, s_cap, ptr(h), ptr(cache_position), eps, theta,
+            ptr(workspace), workspace.numel(), ptr(status))
+    if trace is None:
+        call("t2h_qwen3_decode_layers", *args, stream_handle())
+    else:
+        _check(trace, "trace", torch.int64, align=8)
+        call("t2h_qwen3_decode_layers_traced", *args, ptr(trace), trace.numel() * 8, stream_handle())
+
+
+DECODE_TRACE_PHASES = ("qkv", "attention", "merge", "o", "gate_up", "down")
+DECODE_TRACE_SLOTS = ("begin", "ready", "first", "end", "polls")
+
+
+def decode_layers_trace(layers: int, device) -> torch.Tensor:
+    """Buffer for the persistent kernel's phase timeline: int64 [layers, 6 phases, 256 blocks, 8 slots]; slots
+    0-3 are 100 MHz clock stamps (DECODE_TRACE_SLOTS), slot 4 a poll count."""
+    shape = (layers, len(DECODE_TRACE_PHASES), 256, 8)
+    if int(_lib.lib().t2h_qwen3_decode_layers_trace_bytes(layers)) != 8 * layers * 6 * 256 * 8:
+        raise RuntimeError("libt2h's trace layout differs from this wrapper's")
+    return torch.zeros(shape, dtype=torch.int64, device=device)
 
 
 # ------------------------------------------------------ prefill attention --
@@ -861,9 +880,10 @@ def snake(x: torch.Tensor, alpha: torch.Tensor, *, eps: float = SNAKE_EPS, out: 
 
 
 def conv_transpose1d_q8_0(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, out_channels: int,
-                          kernel: int, *, stride: int = 1, padding: int = 0) -> torch.Tensor:
+                          kernel: int, *, stride: int = 1, padding: int = 0, output_padding: int = 0) -> torch.Tensor:
     """CONV_TRANSPOSE1D_Q8_0W_F32B_F32 on channels-last fp32 x [B, L, Ci] -> [B, Lo, Co], Lo = (L - 1) stride -
-    2 padding + kernel; W the reference's Q8_0 rows [Ci, Co * kernel] as they are, bias fp32 [Co]."""
+    2 padding + kernel + output_padding (0 <= output_padding < stride); W the reference's Q8_0 rows
+    [Ci, Co * kernel] as they are, bias fp32 [Co]."""
     if not isinstance(x, torch.Tensor) or x.device.type != "cuda" or x.dtype != torch.float32 or x.dim() != 3:
         raise ValueError("x must be fp32 [B, L, Ci] on a HIP device")
     _check(w, "weight", torch.uint8, align=2)
@@ -875,7 +895,9 @@ def conv_transpose1d_q8_0(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor |
         _check(bias, "bias", torch.float32, align=4)
         if bias.numel() != out_channels:
             raise ValueError(f"bias must have {out_channels} elements")
-    lo = (length - 1) * stride - 2 * padding + kernel
+    if not 0 <= output_padding < stride:
+        raise ValueError(f"output_padding must be in [0, stride), got {output_padding}")
+    lo = (length - 1) * stride - 2 * padding + kernel + output_padding
     if lo < 1:
         raise ValueError("empty output")
     out = torch.empty(b, lo, out_channels, dtype=torch.float32, device=x.device)

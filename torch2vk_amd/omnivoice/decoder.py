@@ -4,7 +4,7 @@
     per codebook c: EMBEDDING_Q8_0 -> LINEAR_BIAS (project_out), summed      (lines 66-141)
     LINEAR_BIAS fc2                                                          (line 145)
     CONV1D conv1 (k 7, pad 3)                                                (line 149)
-    per block (stride s): snake -> CONV_TRANSPOSE1D (k 2s, pad ceil(s/2))
+    per block (stride s): snake -> CONV_TRANSPOSE1D (k 2s, pad ceil(s/2), s outputs per input)
                           -> 3 residual units (dilation 1, 3, 9):
                              x + conv_k1(snake(conv_k7,dil(snake(x))))       (lines 151-740)
     snake -> CONV1D conv2 (k 7, pad 3, one output channel)                   (lines 741-755)
@@ -38,8 +38,11 @@ class AudioDecoderConfig:
 
 
 def out_len(cfg: AudioDecoderConfig, t: int) -> int:
+    """Waveform samples for t codec frames: each block's transposed conv (kernel 2s, padding ceil(s/2), output
+    padding s % 2) writes s outputs per input, as the reference's tensors are sized (target_len * 8, * 40, * 160,
+    * 320, * 960 for strides 8, 5, 4, 2, 3: src/models/quantized_omnivoice/tensors/audio_decode.py)."""
     for s in cfg.strides:
-        t = (t - 1) * s - 2 * math.ceil(s / 2) + 2 * s
+        t = (t - 1) * s - 2 * math.ceil(s / 2) + 2 * s + s % 2
     return t
 
 
@@ -123,7 +126,7 @@ class OmniVoiceAudioDecoder:
         for i, s in enumerate(cfg.strides):
             x = kernels.snake(x, w[f"b{i}.alpha"])
             x = kernels.conv_transpose1d_q8_0(x, w[f"b{i}.convt.w"], w[f"b{i}.convt.b"], ch // 2, 2 * s, stride=s,
-                                              padding=math.ceil(s / 2))
+                                              padding=math.ceil(s / 2), output_padding=s % 2)
             for j, d in enumerate(DILATIONS):
                 x = self._unit(x, f"b{i}.r{j}.", d)
             ch //= 2

@@ -217,13 +217,14 @@ class Qwen3Decoder:
                             stop_on_eos=self.stop_on_eos, token_index_ptr=self.length,
                             advance=self.position if advance else None)
 
-    def run_decode_layers(self) -> None:
-        """Every layer at the device-resident position: one persistent launch, or one launch per op."""
+    def run_decode_layers(self, trace: torch.Tensor | None = None) -> None:
+        """Every layer at the device-resident position: one persistent launch, or one launch per op.
+        ``trace`` (kernels.decode_layers_trace) records the persistent launch's phase timeline."""
         if self.persistent:
             c = self.config
             kernels.decode_layers(self.layer_table, self.h, self.position, self.layers_ws, self.status,
                                   hidden=c.hidden, mlp=c.mlp, nh=c.heads, nk=c.kv_heads, d=c.head_dim,
-                                  s_cap=self.max_positions, eps=c.rms_eps, theta=c.rope_theta)
+                                  s_cap=self.max_positions, eps=c.rms_eps, theta=c.rope_theta, trace=trace)
         else:
             for i in range(self.config.layers):
                 self.run_decode_layer(i)
