@@ -226,6 +226,18 @@ size_t t2h_qwen3_decode_layers_workspace_bytes(uint32_t hidden, uint32_t mlp, ui
 int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden, uint32_t mlp, uint32_t nh,
                             uint32_t nk, uint32_t d, uint32_t s_cap, float* h, const int32_t* cache_position, float eps,
                             float theta, void* workspace, size_t workspace_bytes, uint32_t* status, void* stream);
+/* t2h_qwen3_decode_layers without a workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid allocation).  No counterpart in the
+ * reference.  The workspace is a file-scope device array of 1.5 MiB per GPU (held until the process ends, zero at
+ * load), large enough for both built shapes; a shape whose workspace would exceed it returns T2H_ERR_WORKSPACE.
+ * The first call on a GPU looks up that GPU's copy of the array (hipGetSymbolAddress, no allocation).  Every call
+ * on one GPU shares the array and its launch counter: calls that overlap in time on one GPU race, and no call may
+ * overlap a launch of t2h_qwen3_decode_layers on the same GPU that uses this array as its workspace.  Results are
+ * bit-identical to t2h_qwen3_decode_layers on the same inputs. */
+int t2h_qwen3_decode_layers_noalloc(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden, uint32_t mlp,
+                                    uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap, float* h,
+                                    const int32_t* cache_position, float eps, float theta, uint32_t* status,
+                                    void* stream);
 /* The same launch with a phase timeline: trace (device, 8-B aligned, t2h_qwen3_decode_layers_trace_bytes()
  * bytes) receives, per layer, phase (qkv, attention, merge, o, gate/up, down) and block (256), 8 uint64 slots:
  * the 100 MHz real-time clock at the phase's start, when its input is in hand, after its first reduced unit

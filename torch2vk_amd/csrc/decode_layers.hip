@@ -43,6 +43,9 @@
 // line.  Weights and the KV cache rows read here are not written in the same
 // launch (except the new row, which its owner substitutes), so they use
 // ordinary loads.
+#include <atomic>
+#include <mutex>
+
 #include "q4k_device.h"
 
 
@@ -1072,6 +1075,40 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
 
 static size_t dl_align(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// ------------------------------------------- allocation-free entry point ----
+
+// Workspace of t2h_qwen3_decode_layers_noalloc: one per GPU, held until the
+// process ends, zero at load (a zero launch counter and no valid epoch).  Large
+// enough for every built shape's layout (8B: 1.16 MiB, 0.6B: 0.6 MiB).
+constexpr size_t DL_SCRATCH_BYTES = (size_t)3 << 19;  // 1.5 MiB
+static __device__ __align__(256) uint8_t scratch[DL_SCRATCH_BYTES];
+constexpr int DL_MAX_DEVICES = 64;
+static std::atomic<void*> dl_scratch_ptr[DL_MAX_DEVICES];
+static std::mutex dl_scratch_mu;
+
+// The device address of the current GPU's copy of `scratch`, looked up on the
+// first call on that GPU (hipGetSymbolAddress, with the GPU current) and kept:
+// in host code the array's name is not a device address.
+static int dl_scratch(void** out) {
+    int dev = 0;
+    const hipError_t ge = hipGetDevice(&dev);
+    if (ge != hipSuccess) return T2H_ERR_HIP_BASE + (int)ge;
+    if (dev < 0 || dev >= DL_MAX_DEVICES) return T2H_ERR_UNSUPPORTED;
+    void* p = dl_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(dl_scratch_mu);
+        p = dl_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return T2H_ERR_HIP_BASE + (int)e;
+            if (p == nullptr) return T2H_ERR_NULL;
+            dl_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return T2H_OK;
+}
+
 struct DlLayout {
     size_t ctl, qkv, attn, act, h, part, total;
 };
@@ -1190,6 +1227,20 @@ extern "C" int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_l
                                        size_t workspace_bytes, uint32_t* status, void* stream) {
     return dl_entry(layer_table, n_layers, hidden, mlp, nh, nk, d, s_cap, h, cache_position, eps, theta, workspace,
                     workspace_bytes, status, nullptr, stream);
+}
+
+extern "C" int t2h_qwen3_decode_layers_noalloc(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden,
+                                               uint32_t mlp, uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap,
+                                               float* h, const int32_t* cache_position, float eps, float theta,
+                                               uint32_t* status, void* stream) {
+    const size_t need = t2h_qwen3_decode_layers_workspace_bytes(hidden, mlp, nh, nk, d);
+    if (need == 0) return T2H_ERR_UNSUPPORTED;
+    if (need > DL_SCRATCH_BYTES) return T2H_ERR_WORKSPACE;  // a shape whose workspace the array cannot hold
+    void* ws = nullptr;
+    const int rc = dl_scratch(&ws);
+    if (rc != T2H_OK) return rc;
+    return dl_entry(layer_table, n_layers, hidden, mlp, nh, nk, d, s_cap, h, cache_position, eps, theta, ws,
+                    DL_SCRATCH_BYTES, status, nullptr, stream);
 }
 
 extern "C" size_t t2h_qwen3_decode_layers_trace_bytes(uint32_t n_layers) {

@@ -546,6 +546,21 @@ def decode_layers(table: torch.Tensor, h: torch.Tensor, cache_position: torch.Te
         call("t2h_qwen3_decode_layers_traced", *args, ptr(trace), trace.numel() * 8, stream_handle())
 
 
+def decode_layers_noalloc(table: torch.Tensor, h: torch.Tensor, cache_position: torch.Tensor, status: torch.Tensor,
+                          *, hidden: int, mlp: int, nh: int, nk: int, d: int, s_cap: int, eps: float = RMS_EPS,
+                          theta: float = 1.0e6) -> None:
+    """decode_layers with the library's own per-GPU workspace (t2h_qwen3_decode_layers_noalloc): no device memory is
+    allocated, by the library or here.  Calls on one GPU must not overlap."""
+    _check(table, "layer_table", torch.int64, align=8)
+    _check(h, "h", torch.float32)
+    _check(cache_position, "cache_position", torch.int32, align=4)
+    _check(status, "status", torch.int32, align=4)
+    if table.dim() != 2 or table.shape[1] != 13:
+        raise ValueError(f"layer_table must be int64 [layers, 13], got {tuple(table.shape)}")
+    call("t2h_qwen3_decode_layers_noalloc", ptr(table), int(table.shape[0]), hidden, mlp, nh, nk, d, s_cap, ptr(h),
+         ptr(cache_position), eps, theta, ptr(status), stream_handle())
+
+
 DECODE_TRACE_PHASES = ("qkv", "attention", "merge", "o", "gate_up", "down")
 DECODE_TRACE_SLOTS = ("begin", "ready", "first", "end", "polls")
 
