@@ -114,6 +114,13 @@ int t2h_q6k_rmsnorm_matvec(const float* h, const float* norm_w, float eps, const
 int t2h_q8_0_matvec(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
                     uint32_t k, uint32_t n, void* stream);
 
+/* 1 when t2h_q4k_matvec / t2h_q6k_matvec / t2h_q8_0_matvec (wtype T2H_WTYPE_*) are built for rows of k
+ * values and n output rows, else 0 (those calls would return T2H_ERR_UNSUPPORTED or T2H_ERR_SHAPE).
+ * The reference's matvec shaders take any K and N; a caller routes the other shapes to the GEMM.
+ * serves the kernel choice of make_linear_nobias_q4_k_m_variant
+ * (src/torch2vk/export/shaders/linear_nobias_quantized.py:47-80). */
+int t2h_matvec_supported(int wtype, uint32_t k, uint32_t n);
+
 /* Q6_K LM head + per-block argmax, as t2h_q4k_lm_head_argmax_partial.
  * replaces LM_HEAD_Q6_K_ARGMAX_PARTIAL_F16 (src/torch2vk/export/shaders/lm_head_q6_k_argmax_partial_f16.py:24-209). */
 int t2h_q6k_lm_head_argmax_partial(const void* x, const float* norm_w, float eps, const void* w, uint32_t k,

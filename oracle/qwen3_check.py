@@ -86,3 +86,15 @@ def check_greedy_tokens(shape: Qwen3Shape, dense: dict[str, torch.Tensor], promp
     bound = max(1, len(gpu_tokens) // 10) if max_mismatch is None else max_mismatch
     assert mismatch <= bound, f"{mismatch} of {len(gpu_tokens)} GPU tokens are not the oracle's argmax (bound {bound})"
     return {"exact": exact, "near_tie": near, "mismatch": mismatch, "min_margin": min_margin}
+
+
+def oracle_step_logits(shape: Qwen3Shape, dense: dict[str, torch.Tensor], k_cache: torch.Tensor,
+                       v_cache: torch.Tensor, token: int, position: int, *, stage_bf16: bool = True) -> np.ndarray:
+    """The oracle's logits for ``token`` at ``position`` over a given KV history (rows 0..position-1 of every
+    layer, [layers, position, NK, D], e.g. the GPU's own bf16 cache): one decode step, so a GPU step's logits can
+    be held to a stated tolerance without the drift of a teacher-forced replay."""
+    model = Qwen3CpuModel(shape, dense, max_positions=position + 1, stage_bf16=stage_bf16)
+    model.k_cache[:, :position] = k_cache.float()
+    model.v_cache[:, :position] = v_cache.float()
+    hidden = model.forward(torch.tensor([token]), start=position)
+    return model.logits(hidden).double().numpy()

@@ -47,6 +47,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "t2h_q6k_matvec": (_i32, [_vp, _vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp]),
     "t2h_q6k_rmsnorm_matvec": (_i32, [_vp, _vp, _f32, _vp, _vp, _i32, _u32, _u32, _vp]),
     "t2h_q8_0_matvec": (_i32, [_vp, _vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp]),
+    "t2h_matvec_supported": (_i32, [_i32, _u32, _u32]),
     "t2h_q8_0_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp]),
     "t2h_q4k_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp]),
     "t2h_q6k_lm_head_argmax_partial": (_i32, [_vp, _vp, _f32, _vp, _u32, _u32, _vp, _vp, _u32, _vp]),

@@ -527,6 +527,15 @@ static int fill_parts(Q4GemvArgs& a, uint32_t n_parts, const void* const* w, voi
     return T2H_OK;
 }
 
+namespace t2h {
+// The plain and residual GEMV is built for K and N: a supported superblock
+// count and N a multiple of the rows one unit covers.
+bool q4k_matvec_shape_built(uint32_t k, uint32_t n) {
+    if (validate_q4(k) != T2H_OK || n == 0) return false;
+    return n % q4_geometry(k / 256, Q4EPI_F32).rpw == 0;
+}
+}  // namespace t2h
+
 extern "C" int t2h_q4k_matvec(const void* x, const void* w, void* y, int out_dtype, const float* residual,
                               uint32_t m, uint32_t k, uint32_t n, void* stream) {
     if (!x || !w || !y) return T2H_ERR_NULL;

@@ -487,6 +487,20 @@ static int qx_matvec(const void* x, const float* norm_w, float eps, const void* 
 
 using namespace t2h;
 
+namespace t2h {
+bool q4k_matvec_shape_built(uint32_t k, uint32_t n);
+}
+
+extern "C" int t2h_matvec_supported(int wtype, uint32_t k, uint32_t n) {
+    QxGeom g;
+    switch (wtype) {
+        case T2H_WTYPE_Q4_K: return q4k_matvec_shape_built(k, n) ? 1 : 0;
+        case T2H_WTYPE_Q6_K: return n > 0 && qx_geometry<Q6KFormat>(k, g) == T2H_OK && n % g.rpw == 0 ? 1 : 0;
+        case T2H_WTYPE_Q8_0: return n > 0 && qx_geometry<Q80Format>(k, g) == T2H_OK && n % g.rpw == 0 ? 1 : 0;
+        default: return 0;
+    }
+}
+
 extern "C" int t2h_q6k_matvec(const void* x, const void* w, void* y, int out_dtype, const float* residual,
                               uint32_t m, uint32_t k, uint32_t n, void* stream) {
     return qx_matvec<Q6KFormat>(x, nullptr, 0.0f, w, y, out_dtype, residual, m, k, n, stream);

@@ -314,6 +314,33 @@ def gemm_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, wtype
     return out
 
 
+GEMV_MAX_ROWS = 8  # rows handled by the decode GEMVs; more go to the matrix-core GEMM
+
+
+def matvec_supported(wtype: str, k: int, n: int) -> bool:
+    """Whether the decode GEMV of ``wtype`` is built for rows of k values and n output rows."""
+    return bool(_lib.lib().t2h_matvec_supported(WTYPES[wtype], k, n))
+
+
+def quantized_linear(x: torch.Tensor, w: torch.Tensor, wtype: str, *, out: torch.Tensor | None = None,
+                     out_dtype: torch.dtype = torch.float32, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """y[M, N] = x[M, K] . deq(W)^T (+ residual) with the kernel the reference would pick: the weight's GGUF type
+    selects the family (run_quantized_linear, src/torch2vk/runtime/quantized_dispatch.py:15-35) and M <= 8 rows
+    run the decode GEMV (one launch per row, the weights streamed per row), more the matrix-core GEMM
+    (make_linear_nobias_q4_k_m_variant, src/torch2vk/export/shaders/linear_nobias_quantized.py:47-80).
+    Shapes the GEMVs are not built for (matvec_supported) run on the GEMM at any M."""
+    if wtype not in ("q4_k", "q6_k", "q8_0"):
+        raise ValueError(f"quantized_linear handles q4_k, q6_k and q8_0 weights, got {wtype!r}")
+    k = int(x.shape[-1])
+    m = x.numel() // k if k else 0
+    n = int(w.shape[0])
+    if m <= GEMV_MAX_ROWS and matvec_supported(wtype, k, n):
+        if wtype == "q4_k":
+            return q4k_matvec(x, w, out=out, out_dtype=out_dtype, residual=residual)
+        return qx_matvec(x, w, wtype, out=out, out_dtype=out_dtype, residual=residual)
+    return gemm(x, w, wtype, out=out, out_dtype=out_dtype, residual=residual)
+
+
 def qk_norm_rope_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out: torch.Tensor,
                        k_cache: torch.Tensor, v_cache: torch.Tensor, start: int, *,
                        q_norm_weight: torch.Tensor | None = None, k_norm_weight: torch.Tensor | None = None,

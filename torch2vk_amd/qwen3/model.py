@@ -194,12 +194,9 @@ class Qwen3Decoder:
                                    self.act, eps=self.config.rms_eps)
 
     def _linear_residual(self, x: torch.Tensor, name: str) -> None:
-        """h += x . deq(W)^T with the GEMV of W's type (_linear_q4_or_q6,
-        src/models/optimized_qwen3/dispatch/decode_layer.py:22-58)."""
-        if self.types[name] == "q4_k":
-            kernels.q4k_matvec(x, self._w(name), out=self.h, residual=self.h)
-        else:
-            kernels.qx_matvec(x, self._w(name), self.types[name], out=self.h, residual=self.h)
+        """h += x . deq(W)^T with the kernel of W's type (_linear_q4_or_q6,
+        src/models/optimized_qwen3/dispatch/decode_layer.py:22-58; one row, so a GEMV)."""
+        kernels.quantized_linear(x, self._w(name), self.types[name], out=self.h, residual=self.h)
 
     def _lm_head(self) -> None:
         kernels.lm_head_argmax_partial(self.h, self._w("lm_head"), self.types["lm_head"], self.partial_scores,
@@ -324,10 +321,11 @@ class Qwen3Decoder:
                                                                            device=self.device), eps=c.rms_eps)
         fused = self._fused_qkv(i)
         if fused is not None:
-            qkv = kernels.gemm(x, fused, t[p + "q"], out_dtype=torch.float32)
+            qkv = kernels.quantized_linear(x, fused, t[p + "q"], out_dtype=torch.float32)
             q, k, v = qkv[:, :c.q_dim], qkv[:, c.q_dim:c.q_dim + c.kv_dim], qkv[:, c.q_dim + c.kv_dim:]
         else:
-            q, k, v = (kernels.gemm(x, self._w(p + nm), t[p + nm], out_dtype=torch.float32) for nm in ("q", "k", "v"))
+            q, k, v = (kernels.quantized_linear(x, self._w(p + nm), t[p + nm], out_dtype=torch.float32)
+                       for nm in ("q", "k", "v"))
         qb = torch.empty(n, c.heads, c.head_dim, dtype=torch.bfloat16, device=self.device)
         kernels.qk_norm_rope_cache(q, k, v, qb, self.k_cache[i], self.v_cache[i], start,
                                    q_norm_weight=self._n(p + "q_norm"), k_norm_weight=self._n(p + "k_norm"),
@@ -338,16 +336,16 @@ class Qwen3Decoder:
             attn = kernels.flash_attn_prefill(qb.unsqueeze(0), keys, vals, causal=True, causal_offset=start)
         else:
             attn = kernels.flash_attn_prefill(qb.unsqueeze(0), keys, vals, causal=False, mask=mask)
-        kernels.gemm(attn.view(n, c.q_dim), self._w(p + "o"), t[p + "o"], out=h, residual=h)
+        kernels.quantized_linear(attn.view(n, c.q_dim), self._w(p + "o"), t[p + "o"], out=h, residual=h)
         x = kernels.rms_norm(h, self._n(p + "post_norm"), out=x, eps=c.rms_eps)
-        if t[p + "gate"] == t[p + "up"]:
+        if t[p + "gate"] == t[p + "up"] and n > kernels.GEMV_MAX_ROWS:
             act = kernels.gemm_swiglu(x, self._w(p + "gate"), self._w(p + "up"), t[p + "gate"])
         else:
-            gate = kernels.gemm(x, self._w(p + "gate"), t[p + "gate"], out_dtype=torch.float32)
-            up = kernels.gemm(x, self._w(p + "up"), t[p + "up"], out_dtype=torch.float32)
+            gate = kernels.quantized_linear(x, self._w(p + "gate"), t[p + "gate"], out_dtype=torch.float32)
+            up = kernels.quantized_linear(x, self._w(p + "up"), t[p + "up"], out_dtype=torch.float32)
             act = kernels.swiglu(gate, up)
             del gate, up
-        kernels.gemm(act, self._w(p + "down"), t[p + "down"], out=h, residual=h)
+        kernels.quantized_linear(act, self._w(p + "down"), t[p + "down"], out=h, residual=h)
 
     def forward_masked(self, embeds: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
         """OmniVoice's LLM pass (src/models/quantized_omnivoice/dispatch/llm_forward.py:19-70): every layer over
