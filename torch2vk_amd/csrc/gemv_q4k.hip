@@ -101,7 +101,8 @@ __global__ __launch_bounds__(WPB * 64) void q4k_gemv_kernel(const Q4GemvArgs a) 
     // with unit i+NSTAGE as soon as unit i has been reduced.  Every wave runs
     // the same number of units; units past the end are clamped to the last one
     // and their results dropped, so the load stream has no divergent branches.
-    constexpr int NSTAGE = UPW > 0 ? UPW : ((NG * NIT == 1) ? 4 : 2);
+    // (gate|up rows of 3 steps per unit hold 72 VGPRs of weights per stage: one stage, so nothing spills)
+    constexpr int NSTAGE = UPW > 0 ? UPW : ((NG * NIT == 1) ? 4 : (NG * NIT >= 6 ? 1 : 2));
     struct Stage {
         uint4 hdr[NG][NIT];
         uint4 q0[NG][NIT];
@@ -213,9 +214,15 @@ __global__ __launch_bounds__(WPB * 64) void q4k_gemv_kernel(const Q4GemvArgs a) 
 #pragma unroll
     for (int s = 1; s < NSTAGE; ++s)
         if ((uint32_t)s < n_iter) issue(clamp_unit(wrow + s * total_wrows), st[s]);
-    XSlice16 xs[NIT];
+    // A lane's x slices (34 VGPRs per step) stay in registers for the whole launch when they fit beside the
+    // weight ring; otherwise (3 steps per unit, or gate|up rings of 2 steps) each unit re-reads them from LDS,
+    // which keeps the kernel within 256 VGPRs without scratch.
+    constexpr bool XREG = NIT * 34 + NSTAGE * NG * NIT * 12 <= 160;
+    XSlice16 xs[XREG ? NIT : 1];
+    if constexpr (XREG) {
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) load_xslice16(xp, xsum, sbi[it], g, xs[it]);
+        for (int it = 0; it < NIT; ++it) load_xslice16(xp, xsum, sbi[it], g, xs[it]);
+    }
     const Q4LaneConsts lc = q4k_lane_consts(g);
 
     float best_score = -3.4028234663852886e38f;
@@ -243,24 +250,33 @@ __global__ __launch_bounds__(WPB * 64) void q4k_gemv_kernel(const Q4GemvArgs a) 
 
     auto consume = [&](uint32_t i, uint32_t u, const Stage& st) {
         const bool live = u < a.n_units;
+        float acc[NG][RPW];
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) acc[gi][r] = 0.0f;
+        }
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            XSlice16 xl;
+            if constexpr (!XREG) load_xslice16(xp, xsum, sbi[it], g, xl);
+            const XSlice16& x = XREG ? xs[XREG ? it : 0] : xl;
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) {
+                const float c = q4k_lane_dot(st.hdr[gi][it], st.q0[gi][it], st.q1[gi][it], x, lc);
+                if constexpr (RPW == 1) {
+                    acc[gi][0] += c;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < RPW; ++r) acc[gi][r] += (rloc[it] == r) ? c : 0.0f;
+                }
+            }
+        }
         float res[NG][RPW];
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
-            float acc[RPW];
 #pragma unroll
-            for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-#pragma unroll
-            for (int it = 0; it < NIT; ++it) {
-                const float c = q4k_lane_dot(st.hdr[gi][it], st.q0[gi][it], st.q1[gi][it], xs[it], lc);
-                if constexpr (RPW == 1) {
-                    acc[0] += c;
-                } else {
-#pragma unroll
-                    for (int r = 0; r < RPW; ++r) acc[r] += (rloc[it] == r) ? c : 0.0f;
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < RPW; ++r) res[gi][r] = wave_sum(acc[r]);
+            for (int r = 0; r < RPW; ++r) res[gi][r] = wave_sum(acc[gi][r]);
         }
         const uint32_t row0 = u * RPW;
         if (!live) return;
@@ -387,13 +403,13 @@ static Q4Geometry q4_geometry(uint32_t nsb, int epi) {
 // Row lengths with straight-line kernels for 1..4 units per wave (the decode
 // shapes of Qwen3-0.6B and -8B); every other launch runs the ring loop.
 static bool q4_straight_line(uint32_t nsb, int epi) {
-    return epi != Q4EPI_ARGMAX && (nsb == 4 || nsb == 16 || nsb == 48);
+    return epi != Q4EPI_ARGMAX && (nsb == 4 || nsb == 16 || (nsb == 48 && epi != Q4EPI_SWIGLU));
 }
 
 template <int NSB, int KS, int WPB, int PRO, int EPI>
 static void launch_upw(uint32_t upw, dim3 grid, const Q4GemvArgs& a, hipStream_t s) {
     const dim3 block(WPB * 64);
-    if constexpr (EPI != Q4EPI_ARGMAX && (NSB == 4 || NSB == 16 || NSB == 48)) {
+    if constexpr (EPI != Q4EPI_ARGMAX && (NSB == 4 || NSB == 16 || (NSB == 48 && EPI != Q4EPI_SWIGLU))) {
         switch (upw) {
             case 1: hipLaunchKernelGGL((q4k_gemv_kernel<NSB, KS, WPB, PRO, EPI, 1>), grid, block, 0, s, a); return;
             case 2: hipLaunchKernelGGL((q4k_gemv_kernel<NSB, KS, WPB, PRO, EPI, 2>), grid, block, 0, s, a); return;
