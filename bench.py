@@ -172,7 +172,7 @@ def phase_trace(args) -> int:
     us_launch = float(np.median([u for u, _ in launches]))
     names = kernels.DECODE_TRACE_PHASES
     n_blocks = [256, 256, cfg.heads, 256, 256, 256]
-    rows = []   # [layer, phase] -> begin, ready_med, ready_max, end_med, end_max, polls (us from prev phase end)
+    rows = []   # [layer, phase] -> begin, ready_med, ready_max, end_med, end_max, polls, first_med (us from prev end)
     periods = []
     for _, tr in launches[1:]:
         t = tr[..., :4].astype(np.float64) * 0.01     # 100 MHz -> us
@@ -185,19 +185,29 @@ def phase_trace(args) -> int:
                 e = t[layer, ph, :n_blocks[ph]]
                 r.append([np.median(e[:, 0]) - prev, np.median(e[:, 1]) - prev, e[:, 1].max() - prev,
                           np.median(e[:, 3]) - prev, e[:, 3].max() - prev,
-                          float(tr[layer, ph, :n_blocks[ph], 4].mean())])
+                          float(tr[layer, ph, :n_blocks[ph], 4].mean()), np.median(e[:, 2]) - prev])
                 prev = e[:, 3].max()
             rows.append(r)
     m = np.mean(np.array(rows), axis=0)
     period = float(np.mean(periods))
-    print(f"| phase | blocks | start (median) | input in hand (median / last) | end (median / last) | polls per "
-          f"wait |\n|---|---|---|---|---|---|")
+    print(f"| phase | blocks | start (median) | input in hand (median / last) | first unit or softmax (median) | "
+          f"end (median / last) | polls per wait |\n|---|---|---|---|---|---|---|")
     for ph in range(6):
-        b, rm, rx, em, ex, pl = m[ph]
-        print(f"| {names[ph]} | {n_blocks[ph]} | {b:.2f} | {rm:.2f} / {rx:.2f} | {em:.2f} / {ex:.2f} | {pl:.1f} |")
+        b, rm, rx, em, ex, pl, fm = m[ph]
+        print(f"| {names[ph]} | {n_blocks[ph]} | {b:.2f} | {rm:.2f} / {rx:.2f} | {fm:.2f} | {em:.2f} / {ex:.2f} | "
+              f"{pl:.1f} |")
     crit = m[:, 4]
     print(f"\nlaunch {us_launch:.1f} us ({cfg.layers} layers, KV position {args.positions}); layer period "
           f"{period:.2f} us; sum of phase critical-path steps {crit.sum():.2f} us")
+    att = []
+    for _, tr in launches[1:]:
+        t = tr.astype(np.float64) * 0.01
+        for layer in range(2, cfg.layers - 1):
+            e = t[layer, 1]
+            att.append([np.median(e[:, k] - e[:, 1]) for k in (5, 2, 6, 7, 3)])
+    a5 = np.mean(np.array(att), axis=0)
+    print(f"\nattention, median block, from input in hand: scores {a5[0]:.2f}, softmax {a5[1]:.2f}, P.V {a5[2]:.2f}, "
+          f"waves merged {a5[3]:.2f}, end {a5[4]:.2f} us")
     wait = m[:, 1] - m[:, 0]
     after = m[:, 3] - m[:, 1]
     print("\nper phase (median block): wait for input " + ", ".join(f"{names[i]} {wait[i]:.2f}" for i in range(6)) +

@@ -82,8 +82,10 @@ def test_persistent_layer_matches_per_op(device, setup_8b2, pos):
     assert (attn - ref).abs().max().item() <= 2 ** -7 * ref.abs().max().item()
     torch.testing.assert_close(a.k_cache[0], b.k_cache[0], rtol=0, atol=0)
     torch.testing.assert_close(a.v_cache[0], b.v_cache[0], rtol=0, atol=0)
+    # both attention outputs are within half a bf16 step of the fp64 value; where the two fp32 sums round
+    # to neighbouring bf16 values, o_proj and the MLP carry that step into h
     herr = (a.h - b.h).abs().max().item()
-    assert herr <= 1e-3 * b.h.abs().max().item(), herr
+    assert herr <= 3e-3 * b.h.abs().max().item(), herr
 
 
 def test_persistent_prefill_close_to_per_op(device, setup_8b2):
@@ -197,8 +199,10 @@ def test_persistent_long_kv_matches_per_op(device, setup_8b_long, pos):
     err = (attn - ref).abs().max().item()
     print(f"attention max-abs diff {err:.3e} (max {ref.abs().max().item():.3e})", flush=True)
     assert err <= 2 ** -7 * ref.abs().max().item()
+    # as in test_persistent_layer_matches_per_op: neighbouring bf16 roundings of the attention output carried
+    # through o_proj and the MLP
     herr = (a.h - b.h).abs().max().item()
-    assert herr <= 1e-3 * b.h.abs().max().item(), herr
+    assert herr <= 3e-3 * b.h.abs().max().item(), herr
 
 
 def test_persistent_long_kv_decode_matches_oracle(device, setup_8b_long):
@@ -247,10 +251,31 @@ def test_persistent_0_6b_full_depth_matches_oracle(device):
     toks = dec.generate(torch.tensor(prompt), 32, steps_per_graph=8, use_graph=True)
     assert int(dec.status.item()) == 0 and len(toks) == 32
     print(f"tokens {toks}", flush=True)
+    # one more step's logits (RMSNorm -> bf16 -> LM-head GEMV over the persistent launch's h) against the
+    # oracle's for the same token, position and KV history
+    from oracle.qwen3_check import oracle_step_logits
+    from tests.conftest import cosine
+    from torch2vk_amd import kernels
+
+    pos, tok = int(dec.position.item()), int(dec.next_token.item())
+    kv = (dec.k_cache[:, :pos].cpu(), dec.v_cache[:, :pos].cpu())
+    dec.run_decode_embed()
+    dec.run_decode_layers()
+    x = kernels.rms_norm(dec.h.view(1, -1), w.norms["norm"],
+                         out=torch.empty(1, cfg.hidden, dtype=torch.bfloat16, device=device))
+    got = kernels.quantized_linear(x, w.packed["lm_head"], w.types["lm_head"]).view(-1).cpu().numpy()
+    assert int(dec.status.item()) == 0
     shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
                        head_dim=cfg.head_dim, mlp=cfg.mlp, vocab=cfg.vocab, rope_theta=cfg.rope_theta)
     dense = dense_weights({k: v.cpu().numpy() for k, v in w.packed.items()}, w.types,
                           {k: v.cpu().numpy() for k, v in w.norms.items()}, matrix_shapes(cfg))
     del w, dec
-    stats = check_greedy_tokens(shape, dense, prompt, toks, tie_tol=2e-3)
+    ref = oracle_step_logits(shape, dense, *kv, tok, pos)
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    err = float(np.abs(got - ref).max())
+    print(f"step logits at pos {pos}: max-abs {err:.4f} (rms {rms:.3f}), cos {cosine(got, ref):.6f}", flush=True)
+    # the per-step tolerance of test_gpu_model.py (3e-2 of the logits' rms; measured 1.5e-2 at 28 layers)
+    assert err <= 3e-2 * rms and cosine(got, ref) >= 0.9999
+    # near ties: two logits each within that tolerance
+    stats = check_greedy_tokens(shape, dense, prompt, toks, tie_tol_rms=6e-2)
     print(stats, flush=True)

@@ -79,10 +79,10 @@ def test_chunked_prefill_decode_matches_oracle(device, policy, chunk):
     dec.stop_on_eos = False
     toks = dec.generate(torch.tensor(prompt), 10, steps_per_graph=4, prefill_chunk=chunk)
     print(f"chunked prefill {policy} chunk={chunk}: {toks}", flush=True)
-    # near-tie allowance of two logits each within the per-step tolerance (3e-2 of the logit rms ~ 1.6, see
+    # near-tie allowance of two logits each within the per-step tolerance (3e-2 of the logit rms, see
     # test_step_logits_within_tolerance): chunks of <= 8 tokens run on the GEMVs, whose tokens at a 0.023 margin
     # step equal the token-by-token prefill's but not the oracle's teacher-forced replay
-    print(check_greedy_tokens(shape, dense, prompt, toks, tie_tol=0.1))
+    print(check_greedy_tokens(shape, dense, prompt, toks, tie_tol_rms=6e-2))
 
 
 def test_chunked_prefill_cache_matches_token_prefill(device):

@@ -109,7 +109,12 @@ struct DlArgs {
 // 100 MHz real-time clock at the phase's start, when its input is in hand,
 // after its first unit is reduced (GEMV) or its softmax (attention), at its
 // end, and the number of polls its first wave made for the input.
-enum DlTraceSlot { DL_TR_BEGIN = 0, DL_TR_READY, DL_TR_FIRST, DL_TR_END, DL_TR_POLLS, DL_TR_SLOTS = 8 };
+// Attention only: after the scores (DL_TR_A_SCORES), after P.V (DL_TR_A_PV) and after the waves' partials
+// are merged in LDS (DL_TR_A_MERGED), each as seen by wave 0.
+enum DlTraceSlot {
+    DL_TR_BEGIN = 0, DL_TR_READY, DL_TR_FIRST, DL_TR_END, DL_TR_POLLS, DL_TR_A_SCORES, DL_TR_A_PV, DL_TR_A_MERGED,
+    DL_TR_SLOTS = 8
+};
 constexpr int DL_TR_PHASES = 6;  // qkv, attention, merge, o, gate|up, down
 
 __device__ __forceinline__ uint64_t* dl_trace_at(const DlArgs& a, uint32_t layer, int phase) {
@@ -199,13 +204,18 @@ __device__ __forceinline__ uint32_t ll_wait(uint64_t (&w)[N], Addr addr, Ok ok, 
     return polls;
 }
 
+typedef __bf16 dl_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float dl_f32x4_t __attribute__((ext_vector_type(4)));
+
 template <int GROUP>
 struct DlAttnLds {
-    float qs[GROUP][4][36];                // q heads x 4 quarters x (32 dims + pad)
-    float ps[DL_WAVES][DL_ATT_POS][GROUP]; // exp(score - m) per wave, position and q head
+    // the block's q heads, normalised, rotated and scaled, as bf16 hi + lo parts (q = hi + lo to 2^-17)
+    uint16_t qhi[GROUP][DL_D];
+    uint16_t qlo[GROUP][DL_D];
     float wml[DL_WAVES][GROUP][2];
     float2 wo[DL_WAVES][GROUP][64];
-    uint16_t knew[DL_D];
+    uint16_t knew[DL_D];                   // the new position's K and V rows (bf16), for the wave holding it
+    uint16_t vnew[DL_D];
 };
 
 constexpr int dl_max3(int a, int b, int c) { return a > b ? (a > c ? a : c) : (b > c ? b : c); }
@@ -585,11 +595,21 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
 
 // --------------------------------------------------------- attention phase ----
 
-// K and V rows of one wave's positions, loaded ahead of the scores.
+// K and V rows of one wave's 32 positions, loaded ahead of the scores.
+// K is the A operand of v_mfma_f32_16x16x32_bf16 (lane l: row l % 16 of a
+// 16-position tile, dims 32 c + 8 (l / 16) .. + 7 of chunk c); tile t row r is
+// position 8 (r / 4) + 4 t + r % 4, so that a lane's 8 scores come out as the
+// positions 8 (l / 16) .. + 7.  V: lane l holds dims 8 (l % 16) .. + 7 of those
+// same positions, for P.V on the VALU.
 struct DlAttnBank {
-    uint4 kr[2][4];            // rows p_k and 16 + p_k: dims part*32 .. +31
-    uint32_t vr[DL_ATT_POS];   // dims 2 lane, 2 lane + 1 of each position
+    uint4 kr[2][4];
+    uint4 vr[8];
 };
+
+__device__ __forceinline__ int dl_att_kpos(int lane, int t) {
+    const int r = lane & 15;
+    return 8 * (r >> 2) + 4 * t + (r & 3);
+}
 
 __device__ __forceinline__ int dl_att_span(int L) {
     // positions per wave: the kv head's L positions over its DL_ATT_SLOTS * DL_WAVES waves
@@ -607,23 +627,39 @@ __device__ __forceinline__ int dl_att_rows(int L, int p0, int span) {
 // that P = 0 times V stays 0.
 __device__ __forceinline__ void dl_attn_issue_k(DlAttnBank& bk, const uint16_t* kc, int kvh, int p0, int rows) {
     const int lane = dl_tid() & 63;
-    const int p_k = lane >> 2, part = lane & 3;
+    const int kg = lane >> 4;
     const size_t stride = (size_t)8 * DL_D;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const bool in = 16 * r + p_k < rows;
-        const uint16_t* krow = kc + (size_t)(in ? p0 + 16 * r + p_k : 0) * stride + (size_t)kvh * DL_D + part * 32;
+    for (int t = 0; t < 2; ++t) {
+        const int p = dl_att_kpos(lane, t);
+        const bool in = p < rows;
+        const uint16_t* row = kc + (size_t)(in ? p0 + p : 0) * stride + (size_t)kvh * DL_D + 8 * kg;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) bk.kr[r][i] = in ? load_u4(krow + 8 * i) : make_uint4(0u, 0u, 0u, 0u);
+        for (int c = 0; c < 4; ++c) bk.kr[t][c] = in ? load_u4(row + 32 * c) : make_uint4(0u, 0u, 0u, 0u);
     }
 }
 
 __device__ __forceinline__ void dl_attn_issue_v(DlAttnBank& bk, const uint16_t* vc, int kvh, int p0, int rows) {
     const int lane = dl_tid() & 63;
+    const int part = lane & 15, pg = lane >> 4;
     const size_t stride = (size_t)8 * DL_D;
-    const uint32_t* vrow = reinterpret_cast<const uint32_t*>(vc + (size_t)p0 * stride + (size_t)kvh * DL_D) + lane;
 #pragma unroll
-    for (int i = 0; i < DL_ATT_POS; ++i) bk.vr[i] = i < rows ? vrow[(size_t)i * stride / 2] : 0u;
+    for (int j = 0; j < 8; ++j) {
+        const bool in = 8 * pg + j < rows;
+        const uint16_t* row = vc + (size_t)(in ? p0 + 8 * pg + j : 0) * stride + (size_t)kvh * DL_D + part * 8;
+        bk.vr[j] = in ? load_u4(row) : make_uint4(0u, 0u, 0u, 0u);
+    }
+}
+
+// Reduce-scatter across the wave's rows: lanes with lane bit 4 or 5 (MASK 16 or 32) clear keep the lower
+// half of the N values, the others the upper half, each adding its partner's partial of the half it keeps.
+template <int MASK, int N>
+__device__ __forceinline__ void dl_rs_x(const float (&in)[N], float (&out)[N / 2], bool upper) {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+        const float lo = in[i], hi = in[N / 2 + i];
+        out[i] = (upper ? hi : lo) + __shfl_xor(upper ? lo : hi, MASK, 64);
+    }
 }
 
 __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w, bool has_w, float eps, float cs,
@@ -684,8 +720,12 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
         float r0, r1;
         dl_norm_rope(ll_val32(w[0]), ll_val32(w[1]), q_norm, q_norm != nullptr, a.eps, cs, sn, rope, r0, r1);
         const float scale = 1.0f / sqrtf((float)DL_D);
-        sm.qs[wave][lane >> 5][lane & 31] = r0 * scale;
-        sm.qs[wave][2 + (lane >> 5)][lane & 31] = r1 * scale;
+        const float q0 = r0 * scale, q1 = r1 * scale;
+        const uint32_t h0 = f32_to_bf16_bits(q0), h1 = f32_to_bf16_bits(q1);
+        sm.qhi[wave][lane] = (uint16_t)h0;
+        sm.qhi[wave][lane + 64] = (uint16_t)h1;
+        sm.qlo[wave][lane] = (uint16_t)f32_to_bf16_bits(q0 - bf16_bits_to_f32(h0));
+        sm.qlo[wave][lane + 64] = (uint16_t)f32_to_bf16_bits(q1 - bf16_bits_to_f32(h1));
     }
     uint32_t vnew = 0;
     if (has_new) {
@@ -698,6 +738,7 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
         sm.knew[lane] = kb0;
         sm.knew[lane + 64] = kb1;
         vnew = pack_bf16x2(ll_val32(w[2]), ll_val32(w[3]));
+        reinterpret_cast<uint32_t*>(sm.vnew)[lane] = vnew;
         const size_t off = (size_t)pos * 8 * DL_D + (size_t)kvh * DL_D;
         kc[off + lane] = kb0;
         kc[off + lane + 64] = kb1;
@@ -708,119 +749,110 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
     // V_LATE: V is needed only after the scores, issued behind every wait of the phase
     if constexpr (S::v_late) dl_attn_issue_v(bk, vc, kvh, p0, rows);
 
-    const int p_k = lane >> 2, part = lane & 3;
-    float mg[GROUP], lg[GROUP];
+    // Scores S[position][head] = K . q^T on the matrix cores: two 16-position
+    // tiles, 4 chunks of 32 dims, q as bf16 hi + lo (columns >= GROUP are 0).
+    // Lane l then holds head l % 16 at positions 8 (l / 16) + 4 t + i.
+    constexpr int NV = GROUP * 8;
+    const int kg = lane >> 4, n = lane & 15;
+    const int pg = kg, part = n;  // the P.V view of the same lane
+    dl_bf16x8_t qh[4], ql[4];
 #pragma unroll
-    for (int gg = 0; gg < GROUP; ++gg) {
-        mg[gg] = -INFINITY;
-        lg[gg] = 0.0f;
-    }
-    float s[2][GROUP];
-    uint4 kr[2][4];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kr[r][i] = bk.kr[r][i];
-        if (has_new && 16 * r + p_k == rnew) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) kr[r][i] = *reinterpret_cast<const uint4*>(&sm.knew[part * 32 + 8 * i]);
+    for (int c = 0; c < 4; ++c) {
+        uint4 h = make_uint4(0u, 0u, 0u, 0u), lo = h;
+        if (n < GROUP) {
+            h = *reinterpret_cast<const uint4*>(&sm.qhi[n][32 * c + 8 * kg]);
+            lo = *reinterpret_cast<const uint4*>(&sm.qlo[n][32 * c + 8 * kg]);
         }
-#pragma unroll
-        for (int gg = 0; gg < GROUP; ++gg) s[r][gg] = 0.0f;
+        qh[c] = __builtin_bit_cast(dl_bf16x8_t, h);
+        ql[c] = __builtin_bit_cast(dl_bf16x8_t, lo);
     }
-    // each q fragment read from LDS once and used for both K rows; the
-    // scheduling fence keeps the q reads of one quarter from being hoisted
-    // ahead of the previous one's products
+    // the new position's row: read from LDS into registers first and selected as a value (a select between
+    // two loads would be merged into one generic load through a selected pointer, re-reading the cache row)
+    uint4 knr[4] = {}, vnr = {};
+    if (has_new) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        __builtin_amdgcn_sched_barrier(0);
-        float kf[2][8];
+        for (int c = 0; c < 4; ++c) knr[c] = *reinterpret_cast<const uint4*>(&sm.knew[32 * c + 8 * kg]);
+        vnr = *reinterpret_cast<const uint4*>(&sm.vnew[part * 8]);
+    }
+    dl_f32x4_t acc[2];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const uint4 kk = kr[r][i];
-            kf[r][0] = bf16_bits_to_f32(kk.x & 0xffffu); kf[r][1] = bf16_bits_to_f32(kk.x >> 16);
-            kf[r][2] = bf16_bits_to_f32(kk.y & 0xffffu); kf[r][3] = bf16_bits_to_f32(kk.y >> 16);
-            kf[r][4] = bf16_bits_to_f32(kk.z & 0xffffu); kf[r][5] = bf16_bits_to_f32(kk.z >> 16);
-            kf[r][6] = bf16_bits_to_f32(kk.w & 0xffffu); kf[r][7] = bf16_bits_to_f32(kk.w >> 16);
-        }
+    for (int t = 0; t < 2; ++t) {
+        const bool sub = has_new && dl_att_kpos(lane, t) == rnew;
+        acc[t] = dl_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int gg = 0; gg < GROUP; ++gg) {
-            const float4 qa = *reinterpret_cast<const float4*>(&sm.qs[gg][part][8 * i]);
-            const float4 qb = *reinterpret_cast<const float4*>(&sm.qs[gg][part][8 * i + 4]);
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                float t = s[r][gg];
-                t = fmaf(qa.x, kf[r][0], t); t = fmaf(qa.y, kf[r][1], t);
-                t = fmaf(qa.z, kf[r][2], t); t = fmaf(qa.w, kf[r][3], t);
-                t = fmaf(qb.x, kf[r][4], t); t = fmaf(qb.y, kf[r][5], t);
-                t = fmaf(qb.z, kf[r][6], t); t = fmaf(qb.w, kf[r][7], t);
-                s[r][gg] = t;
-            }
+        for (int c = 0; c < 4; ++c) {
+            const uint4 kk = sub ? knr[c] : bk.kr[t][c];
+            const dl_bf16x8_t ka = __builtin_bit_cast(dl_bf16x8_t, kk);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qh[c], acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, ql[c], acc[t], 0, 0, 0);
         }
     }
+    if (tr != nullptr) dl_stamp(tr, DL_TR_A_SCORES);
+    // softmax of head n over the wave's positions (the 4 lanes n, 16 + n, 32 + n, 48 + n)
+    float sc[8];
+    bool valid[8];
+    float m = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-#pragma unroll
-        for (int gg = 0; gg < GROUP; ++gg) {
-            s[r][gg] += dpp_f32<0xB1>(s[r][gg]);
-            s[r][gg] += dpp_f32<0x4E>(s[r][gg]);
-        }
+    for (int j = 0; j < 8; ++j) {
+        sc[j] = acc[j >> 2][j & 3];
+        valid[j] = 8 * kg + j < rows;
+        m = fmaxf(m, valid[j] ? sc[j] : -INFINITY);
     }
-    // softmax statistics over this wave's rows (both halves)
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    float e[8];
+    float l = 0.0f;
 #pragma unroll
-    for (int gg = 0; gg < GROUP; ++gg) {
-        const bool v0 = p_k < rows, v1 = 16 + p_k < rows;
-        const float a0 = v0 ? s[0][gg] : -INFINITY, a1 = v1 ? s[1][gg] : -INFINITY;
-        const float m = wave_max(fmaxf(a0, a1));
-        const float e0 = v0 ? expf(a0 - m) : 0.0f, e1 = v1 ? expf(a1 - m) : 0.0f;
-        mg[gg] = m;
-        lg[gg] = wave_sum(part == 0 ? e0 + e1 : 0.0f);
-        if (part == 0) {
-            sm.ps[wave][p_k][gg] = e0;
-            sm.ps[wave][16 + p_k][gg] = e1;
-        }
+    for (int j = 0; j < 8; ++j) {
+        e[j] = valid[j] ? expf(sc[j] - m) : 0.0f;
+        l += e[j];
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
     dl_stamp(tr, DL_TR_FIRST);
-    float o0[GROUP], o1[GROUP];
+    // P of every head at the row's 8 positions, from lanes 0 .. GROUP-1 of the row (row_newbcast)
+    float p[NV];
 #pragma unroll
-    for (int gg = 0; gg < GROUP; ++gg) o0[gg] = o1[gg] = 0.0f;
-    // P.V over the wave's positions (p >= rows carry p = 0).  Fully unrolled so
-    // the V registers are indexed statically; the scheduling fence every 8
-    // positions keeps the P reads from all being hoisted at once.
-#pragma unroll
-    for (int p = 0; p < DL_ATT_POS; ++p) {
-        if (p % 8 == 0) __builtin_amdgcn_sched_barrier(0);
-        const uint32_t vv = (has_new && p == rnew) ? vnew : bk.vr[p];
-        const float v0 = bf16_bits_to_f32(vv & 0xffffu), v1 = bf16_bits_to_f32(vv >> 16);
-        float pr[GROUP];
+    for (int j = 0; j < 8; ++j) {
+        p[0 * 8 + j] = dpp_f32<0x150>(e[j]);
+        p[1 * 8 + j] = dpp_f32<0x151>(e[j]);
         if constexpr (GROUP == 4) {
-            const float4 t = *reinterpret_cast<const float4*>(&sm.ps[wave][p][0]);
-            pr[0] = t.x; pr[1] = t.y; pr[2] = t.z; pr[3] = t.w;
-        } else if constexpr (GROUP == 2) {
-            const float2 t = *reinterpret_cast<const float2*>(&sm.ps[wave][p][0]);
-            pr[0] = t.x; pr[1] = t.y;
-        } else {
-#pragma unroll
-            for (int gg = 0; gg < GROUP; ++gg) pr[gg] = sm.ps[wave][p][gg];
-        }
-#pragma unroll
-        for (int gg = 0; gg < GROUP; ++gg) {
-            o0[gg] = fmaf(pr[gg], v0, o0[gg]);
-            o1[gg] = fmaf(pr[gg], v1, o1[gg]);
+            p[2 * 8 + j] = dpp_f32<0x152>(e[j]);
+            p[3 * 8 + j] = dpp_f32<0x153>(e[j]);
         }
     }
+    // P.V over the row's positions (dims 8 part .. + 7), then summed over the 4 rows (scattered)
+    float o[NV];
 #pragma unroll
-    for (int gg = 0; gg < GROUP; ++gg) {
-        sm.wo[wave][gg][lane] = make_float2(o0[gg], o1[gg]);
-        if (lane == 0) {
-            sm.wml[wave][gg][0] = mg[gg];
-            sm.wml[wave][gg][1] = lg[gg];
-        }
+    for (int i = 0; i < NV; ++i) o[i] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint4 vv = (has_new && rnew == 8 * pg + j) ? vnr : bk.vr[j];
+        const float vf[8] = {bf16_bits_to_f32(vv.x & 0xffffu), bf16_bits_to_f32(vv.x >> 16),
+                             bf16_bits_to_f32(vv.y & 0xffffu), bf16_bits_to_f32(vv.y >> 16),
+                             bf16_bits_to_f32(vv.z & 0xffffu), bf16_bits_to_f32(vv.z >> 16),
+                             bf16_bits_to_f32(vv.w & 0xffffu), bf16_bits_to_f32(vv.w >> 16)};
+#pragma unroll
+        for (int gg = 0; gg < GROUP; ++gg)
+#pragma unroll
+            for (int d = 0; d < 8; ++d) o[gg * 8 + d] = fmaf(p[gg * 8 + j], vf[d], o[gg * 8 + d]);
+    }
+    float o1[NV / 2], of[NV / 4];
+    dl_rs_x<32>(o, o1, pg >> 1);
+    dl_rs_x<16>(o1, of, pg & 1);
+    if (tr != nullptr) dl_stamp(tr, DL_TR_A_PV);
+    // the lane holds head og, dims 8 part + od .. + NV/4 - 1
+    const int obase = (pg >> 1) * (NV / 2) + (pg & 1) * (NV / 4);
+    const int og = obase / 8, od = obase % 8;
+    float* wo = reinterpret_cast<float*>(&sm.wo[wave][og][0]) + part * 8 + od;
+#pragma unroll
+    for (int i = 0; i < NV / 4; ++i) wo[i] = of[i];
+    if (kg == 0 && n < GROUP) {
+        sm.wml[wave][n][0] = m;
+        sm.wml[wave][n][1] = l;
     }
     __syncthreads();
+    if (tr != nullptr) dl_stamp(tr, DL_TR_A_MERGED);
     // block partial: [kvh][bs][g] = (M, l, o[128])
     uint64_t* pb = a.part_ll + (((size_t)kvh * DL_ATT_SLOTS + bs) * GROUP) * (2 + DL_D);
     for (int idx = tid; idx < GROUP * 64; idx += DL_THREADS) {
