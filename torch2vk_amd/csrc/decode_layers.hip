@@ -75,6 +75,26 @@ constexpr uint32_t DL_SPIN_LIMIT = 1u << DL_SPIN_LOG2;
 #ifndef DL_PRE_DOWN
 #define DL_PRE_DOWN 1
 #endif   // polls before a consumer gives up (~16 ms)
+// Units of the next phase issued early, so that the weight stream runs on across a phase boundary: o_proj units
+// once the attention phase has its q (they stream during the attention arithmetic and the merge); gate|up,
+// down and the next layer's Q|K|V units (with its attention K/V rows) right after the phase before has issued
+// its last unit.  A phase's input wait then queues behind fewer loads of its own.
+#ifndef DL_O_EARLY
+#define DL_O_EARLY 2
+#endif
+#ifndef DL_GU_EARLY
+#define DL_GU_EARLY 0
+#endif
+#ifndef DL_DN_EARLY
+#define DL_DN_EARLY 0
+#endif
+#ifndef DL_QKV_EARLY
+#define DL_QKV_EARLY 0
+#endif
+
+struct DlNoHook {
+    __device__ void operator()() const {}
+};
 
 // Per-layer pointer table (device memory, DL_LAYER_PTRS uint64 per layer).
 // DL_WQ points at the q, k and v rows stacked contiguously (q_dim + 2 kv_dim
@@ -553,10 +573,12 @@ __device__ __forceinline__ void dl_issue_pre(DlUnit<NSB, NG> (&u)[UPW], const Dl
 // keep each refill after the reduction that frees its registers.
 // SPREAD: fewer units than waves (dl_unit); a wave without a unit issues and
 // stores nothing.
-template <int NSB, int NG, int UPW, int R, int PRE, int EPI, bool RMSNORM, bool SPREAD, class SH>
+template <int NSB, int NG, int UPW, int R, int PRE, int EPI, bool RMSNORM, bool SPREAD, class SH,
+          class Hook = DlNoHook>
 __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW], const DlRows& rows, int src_kind,
                                               const void* x_src, uint32_t e_x, const float* norm_w, float eps,
-                                              const DlOut& out, uint32_t* status, uint32_t site) {
+                                              const DlOut& out, uint32_t* status, uint32_t site,
+                                              Hook after_issue = Hook()) {
     static_assert(PRE >= 0 && PRE <= R && R >= 1 && R <= UPW, "ring size");
     constexpr int RPW = DlUnit<NSB, NG>::RPW;
     static_assert(EPI != DL_EPI_RESID || UPW * RPW <= DL_HOLD, "residual rows per wave");
@@ -576,9 +598,15 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
     dl_stage_x<NSB * 256, RMSNORM>(sm.g.xp, sm.g.xsum, sm.g.red, src_kind, x_src, e_x, norm_w, eps, hd, status,
                                    site);
     dl_stamp(out.tr, DL_TR_READY);
-    if (!active) return;
+    // after_issue: the caller's early loads for the next phase, right behind this phase's last unit (every
+    // wave calls it once, with or without units)
+    if (!active) {
+        after_issue();
+        return;
+    }
 #pragma unroll
     for (int i = PRE; i < R; ++i) dl_issue_unit(u[i], rows, dl_unit<SPREAD>(wave, i));
+    if constexpr (R >= UPW) after_issue();
     const Q4LaneConsts lc = q4k_lane_consts(dl_tid() & 3);
 #pragma unroll
     for (int i = 0; i < UPW; ++i) {
@@ -590,6 +618,7 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
                                     &sm.g.hold[(wave * UPW + i) * RPW]);
         __builtin_amdgcn_sched_barrier(0);
         if (i + R < UPW) dl_issue_unit(u[i + R], rows, dl_unit<SPREAD>(wave, i + R));
+        if (i + R == UPW - 1) after_issue();
     }
 }
 
@@ -683,10 +712,11 @@ __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w,
 
 // Block (kv head kvh, slot bs): wave w covers positions [p0, p0 + span) of the
 // first L; the block's (max, sum, output) per q head goes to part[kvh][bs].
-template <class S>
+template <class S, class Hook = DlNoHook>
 __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP>& sm, const DlArgs& a,
                                               const uint64_t* lp, int kvh, int bs, int pos, int L, uint32_t e_qkv,
-                                              uint32_t e_part, uint32_t site, uint64_t* tr) {
+                                              uint32_t e_part, uint32_t site, uint64_t* tr,
+                                              Hook after_ready = Hook()) {
     constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int span = dl_att_span(L);
@@ -748,6 +778,7 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
     dl_stamp(tr, DL_TR_READY);
     // V_LATE: V is needed only after the scores, issued behind every wait of the phase
     if constexpr (S::v_late) dl_attn_issue_v(bk, vc, kvh, p0, rows);
+    after_ready();
 
     // Scores S[position][head] = K . q^T on the matrix cores: two 16-position
     // tiles, 4 chunks of 32 dims, q as bf16 hi + lo (columns >= GROUP are 0).
@@ -1014,6 +1045,12 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
     // before has computed: a CU serves its waves' loads roughly in issue order,
     // so loads for a later phase issued any earlier would delay the current
     // phase's data in other waves.
+    DlUnit<S::HSB, 1> uq[S::qkv_u];
+    DlAttnBank bk;
+    if constexpr (DL_QKV_EARLY) {
+        dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp>(uq, qkv_rows(0));
+        issue_bank(0, bk);
+    }
     for (uint32_t layer = 0; layer < a.n_layers; ++layer) {
         const bool first = layer == 0, last = layer + 1 == a.n_layers;
         const uint32_t lsite = layer << 8;  // status code of a wait that gives up: layer and phase
@@ -1029,11 +1066,12 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         dl_stamp(out.tr, DL_TR_BEGIN);
         // ---- Q|K|V: RMSNorm(h) . [Wq; Wk; Wv]^T.  The attention K/V rows depend
         // on nothing computed in this launch: they are issued with the Q|K|V
-        // weights, before h is awaited, and stream during that hand-off.
-        DlUnit<S::HSB, 1> uq[S::qkv_u];
-        DlAttnBank bk;
-        dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp>(uq, qkv_rows(layer));
-        issue_bank(layer, bk);
+        // weights, before h is awaited (with DL_QKV_EARLY, during the layer
+        // before's down_proj), and stream during that hand-off.
+        if constexpr (!DL_QKV_EARLY) {
+            dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp>(uq, qkv_rows(layer));
+            issue_bank(layer, bk);
+        }
         out.ll32 = a.qkv_ll;
         out.e_out = e_qkv;
         dl_gemv_phase<S::HSB, 1, S::qkv_u, S::qkv_r, S::qkv_p, DL_EPI_STORE, true, qkv_sp>(
@@ -1042,13 +1080,18 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
             dl_gptr<const float>(layer_ptr(layer, DL_IN_NORM)), a.eps, out, a.status, lsite | DL_W_QKV);
         dl_stamp(out.tr, DL_TR_END);
         // ---- attention split
+        constexpr int o_early = DL_O_EARLY < S::o_r ? DL_O_EARLY : S::o_r;
+        constexpr int o_pre = o_early > 0 ? o_early : S::o_p;
+        DlUnit<S::QSB, 1> uo[S::o_u];
         {
             uint64_t* tr = trp(1);
             dl_stamp(tr, DL_TR_BEGIN);
             uint64_t lp[DL_LAYER_PTRS];
 #pragma unroll
             for (int i = 0; i < DL_LAYER_PTRS; ++i) lp[i] = layer_ptr(layer, i);
-            dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, pos, L, e_qkv, e_part, lsite, tr);
+            dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, pos, L, e_qkv, e_part, lsite, tr, [&] {
+                if constexpr (o_early > 0) dl_issue_pre<S::QSB, 1, S::o_u, o_early, o_sp>(uo, o_rows(layer));
+            });
             dl_stamp(tr, DL_TR_END);
         }
         // ---- attention merge (blocks 0..NH-1, one q head each)
@@ -1061,42 +1104,57 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         // ---- o_proj + residual
         out.tr = trp(3);
         dl_stamp(out.tr, DL_TR_BEGIN);
-        DlUnit<S::QSB, 1> uo[S::o_u];
-        dl_issue_pre<S::QSB, 1, S::o_u, S::o_p, o_sp>(uo, o_rows(layer));
+        if constexpr (o_early == 0) dl_issue_pre<S::QSB, 1, S::o_u, S::o_p, o_sp>(uo, o_rows(layer));
         out.ll32 = a.h_ll;
         out.plain = nullptr;
         out.hold.kind = first ? DL_SRC_PLAIN : DL_SRC_LL32;
         out.hold.src = first ? static_cast<const void*>(a.h) : static_cast<const void*>(a.h_ll);
         out.hold.e = e_hprev;
         out.e_out = e_ho;
-        dl_gemv_phase<S::QSB, 1, S::o_u, S::o_r, S::o_p, DL_EPI_RESID, false, o_sp>(
-            sm, uo, o_rows(layer), DL_SRC_LL16, a.attn_ll, e_attn, nullptr, a.eps, out, a.status, lsite | DL_W_O);
+        constexpr int gu_early = DL_GU_EARLY < S::gu_r ? DL_GU_EARLY : S::gu_r;
+        constexpr int gu_pre = gu_early > 0 ? gu_early : S::gu_p;
+        DlUnit<S::HSB, 2> ug[S::gu_u];
+        dl_gemv_phase<S::QSB, 1, S::o_u, S::o_r, o_pre, DL_EPI_RESID, false, o_sp>(
+            sm, uo, o_rows(layer), DL_SRC_LL16, a.attn_ll, e_attn, nullptr, a.eps, out, a.status, lsite | DL_W_O,
+            [&] {
+                if constexpr (gu_early > 0) dl_issue_pre<S::HSB, 2, S::gu_u, gu_early, gu_sp>(ug, gu_rows(layer));
+            });
         dl_stamp(out.tr, DL_TR_END);
         // ---- RMSNorm + gate|up + SwiGLU
         out.tr = trp(4);
         dl_stamp(out.tr, DL_TR_BEGIN);
-        DlUnit<S::HSB, 2> ug[S::gu_u];
-        dl_issue_pre<S::HSB, 2, S::gu_u, S::gu_p, gu_sp>(ug, gu_rows(layer));
+        if constexpr (gu_early == 0) dl_issue_pre<S::HSB, 2, S::gu_u, S::gu_p, gu_sp>(ug, gu_rows(layer));
         out.ll16 = a.act_ll;
         out.e_out = e_act;
-        dl_gemv_phase<S::HSB, 2, S::gu_u, S::gu_r, S::gu_p, DL_EPI_SWIGLU, true, gu_sp>(
+        constexpr int dn_early = DL_DN_EARLY < S::dn_r ? DL_DN_EARLY : S::dn_r;
+        constexpr int dn_pre = dn_early > 0 ? dn_early : S::dn_p;
+        DlUnit<S::MSB, 1> ud[S::dn_u];
+        dl_gemv_phase<S::HSB, 2, S::gu_u, S::gu_r, gu_pre, DL_EPI_SWIGLU, true, gu_sp>(
             sm, ug, gu_rows(layer), DL_SRC_LL32, a.h_ll, e_ho,
-            dl_gptr<const float>(layer_ptr(layer, DL_POST_NORM)), a.eps, out, a.status, lsite | DL_W_GU);
+            dl_gptr<const float>(layer_ptr(layer, DL_POST_NORM)), a.eps, out, a.status, lsite | DL_W_GU, [&] {
+                if constexpr (dn_early > 0) dl_issue_pre<S::MSB, 1, S::dn_u, dn_early, dn_sp>(ud, down_rows(layer));
+            });
         dl_stamp(out.tr, DL_TR_END);
         // ---- down + residual (the last layer writes the caller's h)
         out.tr = trp(5);
         dl_stamp(out.tr, DL_TR_BEGIN);
-        DlUnit<S::MSB, 1> ud[S::dn_u];
-        dl_issue_pre<S::MSB, 1, S::dn_u, S::dn_p, dn_sp>(ud, down_rows(layer));
+        if constexpr (dn_early == 0) dl_issue_pre<S::MSB, 1, S::dn_u, S::dn_p, dn_sp>(ud, down_rows(layer));
         out.ll32 = a.h_ll;
         out.plain = last ? a.h : nullptr;
         out.hold.kind = DL_SRC_LL32;
         out.hold.src = a.h_ll;
         out.hold.e = e_ho;
         out.e_out = e_hd;
-        dl_gemv_phase<S::MSB, 1, S::dn_u, S::dn_r, S::dn_p, DL_EPI_RESID, false, dn_sp>(
+        dl_gemv_phase<S::MSB, 1, S::dn_u, S::dn_r, dn_pre, DL_EPI_RESID, false, dn_sp>(
             sm, ud, down_rows(layer), DL_SRC_LL16, a.act_ll, e_act, nullptr, a.eps, out, a.status,
-            lsite | DL_W_DOWN);
+            lsite | DL_W_DOWN, [&] {
+                if constexpr (DL_QKV_EARLY) {
+                    if (!last) {
+                        dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp>(uq, qkv_rows(layer + 1));
+                        issue_bank(layer + 1, bk);
+                    }
+                }
+            });
         dl_stamp(out.tr, DL_TR_END);
     }
     // Every block has read the launch counter before block 0 can get here: its
