@@ -76,7 +76,7 @@ def profile_kernel_target(per_op: bool, config: str = "decode") -> int:
     then one plain 256 MiB device copy whose traffic is known (256 MiB read + 256 MiB written), so counter
     readings can be scaled to bytes.  decode: the persistent layers kernel at KV 4096 (2 dispatches), or per
     op the gate|up GEMV once per layer (72 dispatches); prefill: the gate|up + SwiGLU GEMM at M 16384 (2
-    dispatches); asr: the 0.6B-shape persistent layers kernel at KV 1540 (2 dispatches)."""
+    dispatches) and causal flash attention over 8 x 2048 tokens (2 dispatches); asr: the 0.6B-shape persistent layers kernel at KV 1540 (2 dispatches)."""
     import torch
 
     from torch2vk_amd import kernels
@@ -95,6 +95,13 @@ def profile_kernel_target(per_op: bool, config: str = "decode") -> int:
         act = torch.empty(8 * 2048, c.mlp, dtype=torch.bfloat16, device=dev)
         for _ in range(2):
             kernels.gemm_swiglu(x, gate, up, "q8_0", out=act)
+        # and causal flash attention over the same 8 x 2048 tokens (32 q heads over 8 kv heads, D 128)
+        q = torch.randn(8, 2048, c.heads, c.head_dim, generator=gen, device=dev).to(torch.bfloat16)
+        k = torch.randn(8, 2048, c.kv_heads, c.head_dim, generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn(8, 2048, c.kv_heads, c.head_dim, generator=gen, device=dev).to(torch.bfloat16)
+        o = torch.empty_like(q)
+        for _ in range(2):
+            kernels.flash_attn_prefill(q, k, v, out=o, causal=True)
         _profile_copy(dev)
         return 0
     if config == "asr":

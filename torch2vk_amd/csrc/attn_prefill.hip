@@ -50,7 +50,7 @@ constexpr int FA_WAVES = 4;
 constexpr int FA_THREADS = FA_WAVES * 64;
 constexpr int FA_BM = 32 * FA_WAVES;  // queries per block
 constexpr int FA_BN = 64;             // keys per tile
-constexpr int FA_VROW = FA_BN + 8;    // LDS V^T row length (bf16)
+constexpr int FA_VROW = FA_BN;        // LDS V^T row length (bf16): 128 B, one pass over the 32 banks
 constexpr float FA_LOG2E = 1.4426950408889634f;
 constexpr float FA_RESCALE = 8.0f;    // log2 headroom of the lazily updated running max
 
@@ -69,6 +69,7 @@ struct FaArgs {
     size_t m_sb, m_st;
     uint32_t nh;
     uint32_t group;  // q heads per kv head
+    uint32_t batch;
     uint32_t t_len;
     uint32_t s_len;
     int32_t causal_offset;
@@ -77,6 +78,34 @@ struct FaArgs {
 
 __device__ __forceinline__ fa_bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return __builtin_bit_cast(fa_bf16x8_t, make_uint4(a, b, c, d));
+}
+
+// V^T row d keeps its 16 groups of 4 keys (8 B, two banks) in the order g ^ fa_vswz(d): the 16 rows written
+// by 16 consecutive lanes (d = 4 dg + r, dg consecutive) and the 16 rows read by 16 consecutive lanes (d
+// consecutive) then fall on 16 distinct bank pairs.
+__device__ __forceinline__ int fa_vswz(int d) { return ((d >> 2) ^ ((d & 3) << 2)) & 15; }
+
+// Block -> (query block, batch, head).  Blocks go round-robin to the 8 XCDs; when the (batch, kv head) groups
+// split evenly over them, each XCD takes whole groups, so a group's K/V rows stay in one L2.  Within that
+// order (or over the whole grid otherwise) the query blocks with the most keys start first.
+__device__ __forceinline__ void fa_block(const FaArgs& a, int nqb, int& qb, int& b, int& h) {
+    const int L = blockIdx.x;
+    const int nk = (int)(a.nh / a.group);
+    const int groups = (int)a.batch * nk;
+    if (groups % 8 == 0) {
+        const int x = L % 8, j = L / 8;
+        const int per_qb = groups / 8 * (int)a.group;  // blocks of one query block on one XCD
+        qb = nqb - 1 - j / per_qb;
+        const int r = j % per_qb;
+        const int grp = x + 8 * (r / (int)a.group);
+        b = grp / nk;
+        h = (grp % nk) * (int)a.group + r % (int)a.group;
+    } else {
+        const int bh = (int)a.batch * (int)a.nh;
+        qb = nqb - 1 - L / bh;
+        b = (L % bh) / (int)a.nh;
+        h = (L % bh) % (int)a.nh;
+    }
 }
 
 // Keys [lo, hi) of the segment holding token q: the last i with cu[i] <= q.
@@ -109,7 +138,7 @@ __device__ __forceinline__ int2 fa_key_range(const FaArgs& a, int q) {
 }
 
 template <int D, bool CAUSAL, bool MASK, bool SEG>
-__global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) {
+__global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void fa_prefill_kernel(const FaArgs a) {
     constexpr int KROW = D + 8;                                // LDS K row length (bf16)
     constexpr int DS = D / 16;                                 // k-steps of S^T
     constexpr int DB = D / 32;                                 // 32-dim blocks of O^T
@@ -123,10 +152,10 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int half = lane >> 5;
-    const int h = blockIdx.y % a.nh;
-    const int b = blockIdx.y / a.nh;
+    int qb, b, h;
+    fa_block(a, ((int)a.t_len + FA_BM - 1) / FA_BM, qb, b, h);
     const int kvh = h / a.group;
-    const int q0 = blockIdx.x * FA_BM;
+    const int q0 = qb * FA_BM;
     const int qi = q0 + 32 * wave + (lane & 31);  // this lane's query
     const bool q_valid = qi < (int)a.t_len;
     const int qc = q_valid ? qi : (int)a.t_len - 1;
@@ -194,11 +223,12 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
                                         __builtin_amdgcn_perm(r[3].y, r[2].y, 0x05040100u));
             const uint2 d3 = make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, 0x07060302u),
                                         __builtin_amdgcn_perm(r[3].y, r[2].y, 0x07060302u));
-            uint16_t* dst = &vts[buf][(4 * dg) * FA_VROW + 4 * kg];
-            *reinterpret_cast<uint2*>(dst) = d0;
-            *reinterpret_cast<uint2*>(dst + FA_VROW) = d1;
-            *reinterpret_cast<uint2*>(dst + 2 * FA_VROW) = d2;
-            *reinterpret_cast<uint2*>(dst + 3 * FA_VROW) = d3;
+            const uint2 dv[4] = {d0, d1, d2, d3};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int d = 4 * dg + r;
+                *reinterpret_cast<uint2*>(&vts[buf][d * FA_VROW + ((kg ^ fa_vswz(d)) << 2)]) = dv[r];
+            }
         }
     };
 
@@ -316,11 +346,14 @@ __global__ __launch_bounds__(FA_THREADS) void fa_prefill_kernel(const FaArgs a) 
             for (int stp = 0; stp < 2; ++stp) {
                 const fa_bf16x8_t pf =
                     as_bf16x8(pk[kb][4 * stp], pk[kb][4 * stp + 1], pk[kb][4 * stp + 2], pk[kb][4 * stp + 3]);
-                const uint16_t* vcol = &vts[buf][(lane & 31) * FA_VROW + 32 * kb + 16 * stp + 4 * half];
+                // key groups 8 kb + 4 stp + half and + 2, at their swizzled places in row d
+                const int g1 = 8 * kb + 4 * stp + half;
 #pragma unroll
                 for (int db = 0; db < DB; ++db) {
-                    const uint2 va = *reinterpret_cast<const uint2*>(vcol + 32 * db * FA_VROW);
-                    const uint2 vb = *reinterpret_cast<const uint2*>(vcol + 32 * db * FA_VROW + 8);
+                    const int d = 32 * db + (lane & 31);
+                    const uint16_t* vrow = &vts[buf][d * FA_VROW];
+                    const uint2 va = *reinterpret_cast<const uint2*>(vrow + ((g1 ^ fa_vswz(d)) << 2));
+                    const uint2 vb = *reinterpret_cast<const uint2*>(vrow + (((g1 + 2) ^ fa_vswz(d)) << 2));
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(va.x, va.y, vb.x, vb.y), pf, o[db],
                                                                    0, 0, 0);
                 }
@@ -375,7 +408,9 @@ static int fa_prefill(const void* q, const void* k, const void* v, void* out, co
     if (nh == 0 || nk == 0 || nh % nk != 0) return T2H_ERR_SHAPE;
     if (batch == 0 || t_len == 0) return T2H_OK;
     if (s_len == 0) return T2H_ERR_SHAPE;
-    if ((size_t)batch * nh > 65535u || t_len > 0x7fffffffu - FA_BM || s_len > 0x7fffffffu) return T2H_ERR_SHAPE;
+    if ((size_t)batch * nh * ((t_len + FA_BM - 1) / FA_BM) > 0x7fffffffu || t_len > 0x7fffffffu - FA_BM ||
+        s_len > 0x7fffffffu)
+        return T2H_ERR_SHAPE;
     const int n_strides = mask ? 14 : 12;
     for (int i = 0; i < n_strides; ++i)
         if (strides[i] < 0) return T2H_ERR_ARG;
@@ -414,12 +449,13 @@ static int fa_prefill(const void* q, const void* k, const void* v, void* out, co
     }
     a.nh = nh;
     a.group = nh / nk;
+    a.batch = batch;
     a.t_len = t_len;
     a.s_len = s_len;
     a.causal_offset = causal_offset;
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf((float)d);
     a.scale_log2 = sc * FA_LOG2E;
-    const dim3 grid((t_len + FA_BM - 1) / FA_BM, batch * nh);
+    const dim3 grid((uint32_t)((t_len + FA_BM - 1) / FA_BM * batch * nh));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (d == 128) fa_launch<128>(causal != 0, mask != nullptr, cu != nullptr, grid, a, s);
     else fa_launch<64>(causal != 0, mask != nullptr, cu != nullptr, grid, a, s);
