@@ -86,18 +86,19 @@ __device__ __forceinline__ fa_bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_
 __device__ __forceinline__ int fa_vswz(int d) { return ((d >> 2) ^ ((d & 3) << 2)) & 15; }
 
 // Block -> (query block, batch, head).  Blocks go round-robin to the 8 XCDs; when the (batch, kv head) groups
-// split evenly over them, each XCD takes whole groups, so a group's K/V rows stay in one L2.  Within that
-// order (or over the whole grid otherwise) the query blocks with the most keys start first.
+// split evenly over them, each XCD takes whole groups one after another (a group's K/V rows then stay in that
+// XCD's L2 while its blocks run), and within a group the query blocks with the most keys start first; else
+// the longest query blocks start first over the whole grid.
 __device__ __forceinline__ void fa_block(const FaArgs& a, int nqb, int& qb, int& b, int& h) {
     const int L = blockIdx.x;
     const int nk = (int)(a.nh / a.group);
     const int groups = (int)a.batch * nk;
     if (groups % 8 == 0) {
         const int x = L % 8, j = L / 8;
-        const int per_qb = groups / 8 * (int)a.group;  // blocks of one query block on one XCD
-        qb = nqb - 1 - j / per_qb;
-        const int r = j % per_qb;
-        const int grp = x + 8 * (r / (int)a.group);
+        const int per_grp = nqb * (int)a.group;  // blocks of one (batch, kv head) group
+        const int grp = x + 8 * (j / per_grp);
+        const int r = j % per_grp;
+        qb = nqb - 1 - r / (int)a.group;
         b = grp / nk;
         h = (grp % nk) * (int)a.group + r % (int)a.group;
     } else {
