@@ -276,6 +276,22 @@ int t2h_qwen3_decode_layers_traced(const uint64_t* layer_table, uint32_t n_layer
 int t2h_flash_attn_prefill(const void* q, const void* k, const void* v, void* out, const float* mask, uint32_t batch,
                            uint32_t nh, uint32_t nk, uint32_t t_len, uint32_t s_len, uint32_t d,
                            const int64_t* strides, int causal, int32_t causal_offset, float scale, void* stream);
+/* Class of every block of 128 queries x 64 keys of an additive fp32 mask [mask_batch][t_len][s_len] (element
+ * strides m_sb, m_st; keys contiguous): 1 if every entry is <= -FLT_MAX/2 (all masked), 2 if every entry is 0,
+ * else 0; tiles uint8 [mask_batch][ceil(t_len/128)][ceil(s_len/64)].
+ * replaces FA_MASK_OPT_F16 (src/models/optimized_qwen3/shaders/fa_mask_opt_f16.py:20-60; its rule, on this
+ * kernel's block shape). */
+int t2h_fa_mask_tiles(const float* mask, uint32_t mask_batch, uint32_t t_len, uint32_t s_len, int64_t m_sb,
+                      int64_t m_st, uint8_t* tiles, void* stream);
+/* t2h_flash_attn_prefill with the mask's tile classes (t2h_fa_mask_tiles over the same mask; one row of tiles
+ * for every batch when strides[12] is 0): all-masked tiles are skipped, all-zero tiles are not read.  The
+ * result equals t2h_flash_attn_prefill's, except that a query whose every key is masked gets zeros.
+ * replaces LLAMA_FLASH_ATTN_F32_F16_F16 driven with its mask-opt buffer
+ * (src/models/optimized_qwen3/run.py:406,437). */
+int t2h_flash_attn_prefill_tiles(const void* q, const void* k, const void* v, void* out, const float* mask,
+                                 const uint8_t* mask_tiles, uint32_t batch, uint32_t nh, uint32_t nk, uint32_t t_len,
+                                 uint32_t s_len, uint32_t d, const int64_t* strides, int causal, int32_t causal_offset,
+                                 float scale, void* stream);
 /* Self-attention within segments: token t attends to the keys of its own segment [cu[i], cu[i+1]),
  * cu_seqlens int32 [n_seg + 1] on the device, ascending, cu[0] = 0, cu[n_seg] = t_len (a token outside
  * [cu[0], cu[n_seg]) gets zeros).  Same tensors and strides[0..11] as t2h_flash_attn_prefill with

@@ -114,3 +114,64 @@ def test_fully_masked_rows_are_zero(device):
     assert np.all(got[0, :10] == 0.0)
     ref = _ref(q[:, 10:], k, v, causal_offset=0)
     assert_close(got[:, 10:], ref, max_abs=2e-2, min_cos=0.999, what="offset -10")
+
+
+def _classes_ref(mask: np.ndarray) -> np.ndarray:
+    """FA_MASK_OPT_F16's rule on 128-query x 64-key blocks: 1 all <= -FLT_MAX/2, 2 all zero, else 0."""
+    b, t, s = mask.shape
+    out = np.zeros((b, -(-t // 128), -(-s // 64)), np.uint8)
+    lim = np.float32(1.7014117e38)
+    for bi in range(b):
+        for qb in range(out.shape[1]):
+            for kt in range(out.shape[2]):
+                blk = mask[bi, 128 * qb:128 * qb + 128, 64 * kt:64 * kt + 64]
+                if blk.max() <= -lim:
+                    out[bi, qb, kt] = 1
+                elif blk.min() == 0 and blk.max() == 0:
+                    out[bi, qb, kt] = 2
+    return out
+
+
+def _tile_mask(t: int, s: int, rng) -> np.ndarray:
+    """Padded keys, a bidirectional block, an all-masked hole and scattered -FLT_MAX / finite entries."""
+    m = np.zeros((t, s), np.float32)
+    m[:, s - 70:] = -np.inf                    # padded keys: two whole tiles and a partial one
+    m[128:256, 64:192] = -np.inf               # a hole of two whole tiles in the second query block
+    m[:128, 192:256] = -np.finfo(np.float32).max
+    m[300:, :64] = rng.standard_normal((t - 300, 64)).astype(np.float32)  # mixed
+    m[5, 10] = -1.0                            # one entry makes a zero tile mixed
+    return m
+
+
+def test_mask_tile_classes(device):
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(1)
+    t, s = 330, 450
+    mask = np.stack([_tile_mask(t, s, rng), np.zeros((t, s), np.float32)])
+    mask[1, :, 200:] = -np.inf
+    tiles = kernels.fa_mask_tiles(torch.from_numpy(mask).to(device)).cpu().numpy()
+    want = _classes_ref(mask)
+    np.testing.assert_array_equal(tiles, want)
+    assert {0, 1, 2} <= set(np.unique(want).tolist())
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_mask_tiles_give_the_same_result(device, shared):
+    """With the tile classes, all-masked tiles are skipped and all-zero tiles not read: bit-identical to reading
+    every mask entry whenever each query sees some key (the reference's FA_MASK_OPT_F16 + flash attention)."""
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(2)
+    b, t, s, nh, nk, d = 2, 330, 450, 8, 2, 128
+    q, k, v = _qkv(rng, b, t, s, nh, nk, d)
+    one = _tile_mask(t, s, rng)
+    mask = one[None] if shared else np.stack([one, _tile_mask(t, s, rng)])
+    mt = torch.from_numpy(mask).to(device)
+    qt, kt, vt = _dev(q, device), _dev(k, device), _dev(v, device)
+    with_tiles = kernels.flash_attn_prefill(qt, kt, vt, causal=False, mask=mt)
+    every_entry = kernels.flash_attn_prefill(qt, kt, vt, causal=False, mask=mt, mask_tiles=False)
+    assert torch.equal(with_tiles, every_entry)
+    ref = _ref(q, k, v, mask=mask)
+    assert_close(with_tiles.float().cpu().numpy(), ref, max_abs=2 ** -7 * max(1.0, np.abs(ref).max()),
+                 min_cos=0.9999, what="tiled mask attention")

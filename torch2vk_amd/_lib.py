@@ -67,6 +67,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                               _vp, _sz, _vp, _vp, _sz, _vp]),
     "t2h_flash_attn_prefill": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _i32,
                                       ctypes.c_int32, _f32, _vp]),
+    "t2h_flash_attn_prefill_tiles": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp,
+                                            _i32, ctypes.c_int32, _f32, _vp]),
+    "t2h_fa_mask_tiles": (_i32, [_vp, _u32, _u32, _u32, ctypes.c_int64, ctypes.c_int64, _vp, _vp]),
     "t2h_embedding_q4_k": (_i32, [_vp, _u64, _vp, _u32, _u32, _vp, _vp]),
     "t2h_rms_norm": (_i32, [_vp, _i32, _vp, _vp, _i32, _u32, _u32, _f32, _vp]),
     "t2h_swiglu": (_i32, [_vp, _vp, _i32, _vp, _u64, _vp]),

@@ -74,7 +74,15 @@ struct FaArgs {
     uint32_t s_len;
     int32_t causal_offset;
     float scale_log2;  // softmax scale * log2(e)
+    const uint8_t* tiles;  // MASK: class of each (query block, key tile) of the mask, or null
+    size_t tiles_sb;       // batch stride of tiles (0: one mask for every batch)
+    uint32_t n_tiles;      // key tiles per query block row of tiles
 };
+
+// Mask tile classes (the reference's FA_MASK_OPT_F16: all masked / all zero / mixed), per block of FA_BM
+// queries x FA_BN keys.  A value at or below -FA_MASKED masks its key.
+enum FaTile { FA_TILE_MIXED = 0, FA_TILE_MASKED = 1, FA_TILE_ZERO = 2 };
+constexpr float FA_MASKED = 1.7014117e38f;  // FLT_MAX / 2
 
 __device__ __forceinline__ fa_bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return __builtin_bit_cast(fa_bf16x8_t, make_uint4(a, b, c, d));
@@ -169,8 +177,16 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
     const int2 rq = fa_key_range<CAUSAL, SEG>(a, qc);
     const int blk_lo = fa_key_range<CAUSAL, SEG>(a, q0).x;
     const int blk_hi = fa_key_range<CAUSAL, SEG>(a, q_last).y;
-    const int t_first = blk_lo / FA_BN;
-    const int t_end = blk_hi > blk_lo ? (blk_hi + FA_BN - 1) / FA_BN : t_first;
+    int t_first = blk_lo / FA_BN;
+    int t_end = blk_hi > blk_lo ? (blk_hi + FA_BN - 1) / FA_BN : t_first;
+    if constexpr (MASK) {
+        // all-masked tiles at either end of the block's row of the mask are not visited at all
+        if (a.tiles != nullptr) {
+            const uint8_t* tr = a.tiles + (size_t)b * a.tiles_sb + (size_t)qb * a.n_tiles;
+            while (t_first < t_end && tr[t_first] == FA_TILE_MASKED) ++t_first;
+            while (t_end > t_first && tr[t_end - 1] == FA_TILE_MASKED) --t_end;
+        }
+    }
     const int wave_lo_max = __builtin_amdgcn_readlane(rq.x, 31);
     const int wave_hi_min = __builtin_amdgcn_readlane(rq.y, 0);
 
@@ -249,11 +265,18 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 
     const float* mrow = nullptr;
     if constexpr (MASK) mrow = a.mask + (size_t)b * a.m_sb + (size_t)qc * a.m_st;
+    // tile classes of this block's row of the mask (the range was already narrowed before the first load)
+    const uint8_t* trow = nullptr;
+    if constexpr (MASK) {
+        if (a.tiles != nullptr) trow = a.tiles + (size_t)b * a.tiles_sb + (size_t)qb * a.n_tiles;
+    }
 
     for (int t = t_first; t < t_end; ++t) {
         const int buf = (t - t_first) & 1;
         const int t0 = t * FA_BN;
         if (t + 1 < t_end) load_tile(t0 + FA_BN);
+        const int cls = trow != nullptr ? (int)trow[t] : FA_TILE_MIXED;  // block-uniform
+        if (cls != FA_TILE_MASKED) {
 
         // S^T for two 32-key blocks
         fa_f32x16_t s[2];
@@ -275,12 +298,15 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
         const bool edge = t0 < wave_lo_max || t0 + FA_BN > wave_hi_min;
         float mt = -INFINITY;  // tile max of this query, log2 units
         if constexpr (MASK) {
+            // an all-zero tile adds nothing: fmaf(0, log2 e, x) is x, so the mask is not read
+            const bool zero = cls == FA_TILE_ZERO;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int key = t0 + 32 * kb + 8 * (e >> 2) + 4 * half + (e & 3);
-                    float x = fmaf(mrow[min(key, s_len - 1)], FA_LOG2E, s[kb][e] * a.scale_log2);
+                    const float mv = zero ? 0.0f : mrow[min(key, s_len - 1)];
+                    float x = fmaf(mv, FA_LOG2E, s[kb][e] * a.scale_log2);
                     x = key >= rq.x && key < rq.y ? x : -INFINITY;
                     s[kb][e] = x;
                     mt = fmaxf(mt, x);
@@ -360,6 +386,7 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
                 }
             }
         }
+        }  // cls != FA_TILE_MASKED: an all-masked tile contributes nothing and is skipped
         // the other buffer was last read in iteration t - 1, before the barrier that ended it
         if (t + 1 < t_end) store_tile(buf ^ 1);
         __syncthreads();
@@ -382,6 +409,40 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
     }
 }
 
+// One block per (key tile, query block, mask batch): min and max of the mask over the block's FA_BM x FA_BN
+// entries inside [t_len) x [s_len), then the class (FA_MASK_OPT_F16's rule).
+__global__ __launch_bounds__(256) void fa_mask_tiles_kernel(const float* mask, size_t m_sb, size_t m_st,
+                                                            uint32_t t_len, uint32_t s_len, uint32_t nqb,
+                                                            uint32_t n_tiles, uint8_t* tiles) {
+    const uint32_t tile = blockIdx.x, qb = blockIdx.y, b = blockIdx.z;
+    float mn = FA_MASKED, mx = -FA_MASKED;
+    for (uint32_t i = threadIdx.x; i < (uint32_t)(FA_BM * FA_BN); i += 256) {
+        const uint32_t row = qb * FA_BM + i / FA_BN, col = tile * FA_BN + i % FA_BN;
+        if (row < t_len && col < s_len) {
+            const float v = mask[(size_t)b * m_sb + (size_t)row * m_st + col];
+            mn = fminf(mn, v);
+            mx = fmaxf(mx, v);
+        }
+    }
+    mn = -wave_max(-mn);
+    mx = wave_max(mx);
+    __shared__ float rmn[4], rmx[4];
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        rmn[wave] = mn;
+        rmx[wave] = mx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) {
+            mn = fminf(mn, rmn[w]);
+            mx = fmaxf(mx, rmx[w]);
+        }
+        const uint8_t cls = mx <= -FA_MASKED ? FA_TILE_MASKED : (mn == 0.0f && mx == 0.0f ? FA_TILE_ZERO : FA_TILE_MIXED);
+        tiles[((size_t)b * nqb + qb) * n_tiles + tile] = cls;
+    }
+}
+
 template <int D>
 static void fa_launch(bool causal, bool mask, bool seg, dim3 grid, const FaArgs& a, hipStream_t s) {
     const dim3 block(FA_THREADS);
@@ -401,9 +462,9 @@ static void fa_launch(bool causal, bool mask, bool seg, dim3 grid, const FaArgs&
 using namespace t2h;
 
 static int fa_prefill(const void* q, const void* k, const void* v, void* out, const float* mask,
-                      const int32_t* cu, uint32_t n_seg, uint32_t batch, uint32_t nh, uint32_t nk, uint32_t t_len,
-                      uint32_t s_len, uint32_t d, const int64_t* strides, int causal, int32_t causal_offset,
-                      float scale, void* stream) {
+                      const uint8_t* tiles, const int32_t* cu, uint32_t n_seg, uint32_t batch, uint32_t nh,
+                      uint32_t nk, uint32_t t_len, uint32_t s_len, uint32_t d, const int64_t* strides, int causal,
+                      int32_t causal_offset, float scale, void* stream) {
     if (!q || !k || !v || !out || !strides) return T2H_ERR_NULL;
     if (d != 64 && d != 128) return T2H_ERR_UNSUPPORTED;
     if (nh == 0 || nk == 0 || nh % nk != 0) return T2H_ERR_SHAPE;
@@ -447,6 +508,9 @@ static int fa_prefill(const void* q, const void* k, const void* v, void* out, co
     if (mask) {
         a.m_sb = (size_t)strides[12];
         a.m_st = (size_t)strides[13];
+        a.tiles = tiles;
+        a.n_tiles = (s_len + FA_BN - 1) / FA_BN;
+        a.tiles_sb = a.m_sb == 0 ? 0 : (size_t)((t_len + FA_BM - 1) / FA_BM) * a.n_tiles;
     }
     a.nh = nh;
     a.group = nh / nk;
@@ -468,8 +532,32 @@ extern "C" int t2h_flash_attn_prefill(const void* q, const void* k, const void* 
                                       uint32_t batch, uint32_t nh, uint32_t nk, uint32_t t_len, uint32_t s_len,
                                       uint32_t d, const int64_t* strides, int causal, int32_t causal_offset,
                                       float scale, void* stream) {
-    return fa_prefill(q, k, v, out, mask, nullptr, 0, batch, nh, nk, t_len, s_len, d, strides, causal,
+    return fa_prefill(q, k, v, out, mask, nullptr, nullptr, 0, batch, nh, nk, t_len, s_len, d, strides, causal,
                       causal_offset, scale, stream);
+}
+
+extern "C" int t2h_flash_attn_prefill_tiles(const void* q, const void* k, const void* v, void* out,
+                                            const float* mask, const uint8_t* mask_tiles, uint32_t batch,
+                                            uint32_t nh, uint32_t nk, uint32_t t_len, uint32_t s_len, uint32_t d,
+                                            const int64_t* strides, int causal, int32_t causal_offset, float scale,
+                                            void* stream) {
+    if (!mask || !mask_tiles) return T2H_ERR_NULL;
+    return fa_prefill(q, k, v, out, mask, mask_tiles, nullptr, 0, batch, nh, nk, t_len, s_len, d, strides, causal,
+                      causal_offset, scale, stream);
+}
+
+extern "C" int t2h_fa_mask_tiles(const float* mask, uint32_t mask_batch, uint32_t t_len, uint32_t s_len,
+                                 int64_t m_sb, int64_t m_st, uint8_t* tiles, void* stream) {
+    if (!mask || !tiles) return T2H_ERR_NULL;
+    if (m_sb < 0 || m_st < 0) return T2H_ERR_ARG;
+    if (mask_batch == 0 || t_len == 0 || s_len == 0) return T2H_OK;
+    const uint32_t nqb = (t_len + FA_BM - 1) / FA_BM, n_tiles = (s_len + FA_BN - 1) / FA_BN;
+    if (mask_batch > 65535u || nqb > 65535u) return T2H_ERR_SHAPE;
+    hipLaunchKernelGGL(fa_mask_tiles_kernel, dim3(n_tiles, nqb, mask_batch), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), mask, (size_t)m_sb, (size_t)m_st, t_len, s_len, nqb,
+                       n_tiles, tiles);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
 }
 
 extern "C" int t2h_flash_attn_segments(const void* q, const void* k, const void* v, void* out,
@@ -478,6 +566,6 @@ extern "C" int t2h_flash_attn_segments(const void* q, const void* k, const void*
                                        void* stream) {
     if (!cu_seqlens) return T2H_ERR_NULL;
     if (n_seg == 0 || n_seg > 0x7fffffffu) return T2H_ERR_SHAPE;
-    return fa_prefill(q, k, v, out, nullptr, cu_seqlens, n_seg, batch, nh, nk, t_len, t_len, d, strides, 0, 0,
-                      scale, stream);
+    return fa_prefill(q, k, v, out, nullptr, nullptr, cu_seqlens, n_seg, batch, nh, nk, t_len, t_len, d, strides, 0,
+                      0, scale, stream);
 }

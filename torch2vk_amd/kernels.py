@@ -616,12 +616,34 @@ def _check_strided(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
         raise ValueError(f"{name} needs a contiguous last dimension")
 
 
+FA_BLOCK_QUERIES = 128  # queries per flash-attention block (a row of mask tiles)
+FA_TILE_KEYS = 64       # keys per flash-attention tile
+
+
+def fa_mask_tiles(mask: torch.Tensor) -> torch.Tensor:
+    """uint8 [B, ceil(T/128), ceil(S/64)] class of each 128 x 64 block of an additive fp32 mask [B, T, S]:
+    1 all masked (every entry <= -FLT_MAX/2), 2 all zero, 0 mixed (the reference's FA_MASK_OPT_F16 rule).  A mask
+    used by several attention calls (every layer of one pass) is classified once."""
+    _check_strided(mask, "mask", torch.float32)
+    if mask.dim() != 3:
+        raise ValueError(f"mask must be rank 3 [B, T, S], got {tuple(mask.shape)}")
+    b, t_len, s_len = mask.shape
+    tiles = torch.empty(b, -(-t_len // FA_BLOCK_QUERIES), -(-s_len // FA_TILE_KEYS), dtype=torch.uint8,
+                        device=mask.device)
+    call("t2h_fa_mask_tiles", ptr(mask), b, t_len, s_len, mask.stride(0), mask.stride(1), ptr(tiles),
+         stream_handle())
+    return tiles
+
+
 def flash_attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None, *,
                        causal: bool = True, causal_offset: int = 0, mask: torch.Tensor | None = None,
-                       scale: float | None = None) -> torch.Tensor:
+                       scale: float | None = None, mask_tiles: torch.Tensor | bool | None = None) -> torch.Tensor:
     """softmax(q k^T * scale + mask) v; q/out [B, T, NH, D], k/v [B, S, NK, D], bf16, any (batch, token, head)
     strides with D contiguous -- token-major tensors as they are, head-major ones as ``x.transpose(1, 2)``.
-    ``mask``: additive fp32 [B or 1, T, S] (S contiguous).  Causal: query t sees keys <= t + causal_offset."""
+    ``mask``: additive fp32 [B or 1, T, S] (S contiguous).  Causal: query t sees keys <= t + causal_offset.
+    ``mask_tiles``: the mask's fa_mask_tiles (computed here when None; False reads every mask entry): all-masked
+    tiles are skipped and all-zero tiles not read -- the same result, except that a query whose every key is
+    masked gets zeros."""
     for t, name in ((q, "q"), (k, "k"), (v, "v")):
         _check_strided(t, name, torch.bfloat16)
         if t.dim() != 4:
@@ -645,6 +667,15 @@ def flash_attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: t
     strides = (_lib.ctypes.c_int64 * 14)(q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1),
                                          k.stride(2), v.stride(0), v.stride(1), v.stride(2), out.stride(0),
                                          out.stride(1), out.stride(2), m_sb, m_st)
+    if mask is not None and mask_tiles is not False:
+        tiles = fa_mask_tiles(mask) if mask_tiles is None or mask_tiles is True else mask_tiles
+        want = (mask.shape[0], -(-t_len // FA_BLOCK_QUERIES), -(-s_len // FA_TILE_KEYS))
+        _check(tiles, "mask_tiles", torch.uint8, align=1)
+        if tuple(tiles.shape) != want:
+            raise ValueError(f"mask_tiles must be {want} (fa_mask_tiles of the mask), got {tuple(tiles.shape)}")
+        call("t2h_flash_attn_prefill_tiles", ptr(q), ptr(k), ptr(v), ptr(out), ptr(mask), ptr(tiles), b, nh, nk,
+             t_len, s_len, d, strides, 1 if causal else 0, int(causal_offset), float(scale or 0.0), stream_handle())
+        return out
     call("t2h_flash_attn_prefill", ptr(q), ptr(k), ptr(v), ptr(out), ptr(mask), b, nh, nk, t_len, s_len, d,
          strides, 1 if causal else 0, int(causal_offset), float(scale or 0.0), stream_handle())
     return out

@@ -309,12 +309,14 @@ class Qwen3Decoder:
         rows = q.shape[0] + k.shape[0] + v.shape[0]
         return q.as_strided((rows, q.shape[1]), (q.shape[1], 1))
 
-    def _prefill_layer(self, i: int, h: torch.Tensor, start: int, mask: torch.Tensor | None = None) -> None:
+    def _prefill_layer(self, i: int, h: torch.Tensor, start: int, mask: torch.Tensor | None = None,
+                       mask_tiles: torch.Tensor | None = None) -> None:
         """One layer over a chunk's fp32 residual stream h [n, hidden] at positions start.. (run_text_layer,
         src/models/optimized_qwen3/dispatch/text_layer.py): RMSNorm rows -> q|k|v GEMM -> q/k norm + RoPE +
         KV cache write -> causal flash attention over the cache -> o GEMM + residual -> RMSNorm -> gate|up
         GEMM with SwiGLU in its epilogue -> down GEMM + residual.  GEMMs run on the matrix cores for any chunk length.
-        ``mask`` (additive fp32 [1, n, start + n]) replaces causality in the attention."""
+        ``mask`` (additive fp32 [1, n, start + n]) replaces causality in the attention; ``mask_tiles`` are its
+        tile classes (kernels.fa_mask_tiles), computed once for every layer of a pass."""
         c, t, p = self.config, self.types, f"layers.{i}."
         n = h.shape[0]
         x = kernels.rms_norm(h, self._n(p + "input_norm"), out=torch.empty(n, c.hidden, dtype=torch.bfloat16,
@@ -335,7 +337,8 @@ class Qwen3Decoder:
         if mask is None:
             attn = kernels.flash_attn_prefill(qb.unsqueeze(0), keys, vals, causal=True, causal_offset=start)
         else:
-            attn = kernels.flash_attn_prefill(qb.unsqueeze(0), keys, vals, causal=False, mask=mask)
+            attn = kernels.flash_attn_prefill(qb.unsqueeze(0), keys, vals, causal=False, mask=mask,
+                                              mask_tiles=mask_tiles)
         kernels.quantized_linear(attn.view(n, c.q_dim), self._w(p + "o"), t[p + "o"], out=h, residual=h)
         x = kernels.rms_norm(h, self._n(p + "post_norm"), out=x, eps=c.rms_eps)
         if t[p + "gate"] == t[p + "up"] and n > kernels.GEMV_MAX_ROWS:
@@ -360,8 +363,9 @@ class Qwen3Decoder:
             raise ValueError(f"{t_len} positions exceed the KV capacity {self.max_positions}")
         m = mask.to(device=self.device, dtype=torch.float32).reshape(1, t_len, t_len).contiguous()
         h = e.clone()
+        tiles = kernels.fa_mask_tiles(m)  # FA_MASK_OPT_F16 once per pass (src/models/optimized_qwen3/run.py:406)
         for i in range(c.layers):
-            self._prefill_layer(i, h, 0, mask=m)
+            self._prefill_layer(i, h, 0, mask=m, mask_tiles=tiles)
         return kernels.rms_norm(h, self._n("norm"), out=torch.empty_like(h), eps=c.rms_eps)
 
     def prefill_chunked(self, prompt_ids: torch.Tensor | None = None, *, embeds: torch.Tensor | None = None,
