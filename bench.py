@@ -43,10 +43,12 @@ PROMPT_POSITIONS = 4096
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--config", choices=("decode", "prefill", "asr"), default="decode",
-                   help="decode: BASELINE configs[2], the headline (default); prefill: configs[3], 8 x 2048 tokens "
-                        "through the 36-layer 8B shape with Q8_0 weights; asr: configs[4], the 24-layer encoder over "
-                        "4 x 1500 frames then a 0.6B-shape int4 decoder for 64 tokens per utterance")
+    p.add_argument("--config", choices=("decode", "prefill", "asr", "linear"), default="decode",
+                   help="decode: BASELINE configs[2], the headline (default; with --model 0.6b, configs[1]: a "
+                        "128-token prompt through the chunked prefill, then 128 greedy tokens); prefill: configs[3], "
+                        "8 x 2048 tokens through the 36-layer 8B shape with Q8_0 weights; asr: configs[4], the "
+                        "24-layer encoder over 4 x 1500 frames then a 0.6B-shape int4 decoder for 64 tokens per "
+                        "utterance; linear: configs[0], one Q4_K linear x[1,1024] . W[3072,1024]^T")
     p.add_argument("--steps", type=int, default=None, help="timed steps (default 256 decode tokens, 5 prefill or "
                                                            "asr passes)")
     p.add_argument("--warmup", type=int, default=None, help="untimed steps (default 16 decode, 1 prefill/asr)")
@@ -250,6 +252,10 @@ def main() -> int:
         return bench_prefill(args)
     if args.config == "asr":
         return bench_asr(args)
+    if args.config == "linear":
+        return bench_linear(args)
+    if args.model == "0.6b":
+        return bench_c2(args)
     import torch
 
     from torch2vk_amd import kernels
@@ -558,6 +564,215 @@ def cpu_baseline(cfg, weights, positions: int, steps: int) -> dict:
                   f"1 of {c.layers} layers at KV position {positions}, median of {steps} steps ("
                   f"{t_layer * 1e3:.1f} ms) x {c.layers} + LM head+argmax (median {t_lm * 1e3:.1f} ms)",
     }
+
+
+# ------------------------------------------------------------------ C1 linear --
+
+LINEAR_COPIES = 256  # distinct weight copies streamed for GB/s: 453 MB, past the 256 MB MALL
+
+
+def bench_linear(args) -> int:
+    """y = x . deq(W)^T with x bf16 [1, 1024] ~ N(0, 1) and W fp32 [3072, 1024] ~ N(0, 0.02)
+    quantized to Q4_K (seed 0).  Latency: one call on a hot weight, calls replayed back to back in a HIP graph.
+    Bandwidth: one call on each of LINEAR_COPIES distinct weight copies in a graph (every copy cold), GB/s of
+    the algorithmic bytes.  CPU: torch F.linear on the oracle-dequantized fp32 weight, median of 7 runs."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from torch2vk_amd import kernels
+
+    if not torch.cuda.is_available():
+        print("no HIP device", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    n, k = 3072, 1024
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    x = torch.randn(1, k, generator=gen, device=dev).to(torch.bfloat16)
+    w = kernels.quantize(torch.randn(n, k, generator=gen, device=dev) * 0.02, "q4_k")
+    y = torch.empty(1, n, device=dev)
+    kernels.q4k_matvec(x, w, out=y)
+    torch.cuda.synchronize()
+    w_deq = oracle.dequant_q4_k(w.cpu().numpy(), k)
+    ref = x.float().cpu().numpy().astype(np.float64) @ w_deq.astype(np.float64).T
+    err = float(np.abs(y.cpu().numpy() - ref).max() / np.abs(ref).max())
+    reps = max(args.steps, 20)
+    hot_us = _graph_us_per_call([lambda: kernels.q4k_matvec(x, w, out=y)] * 64, reps)
+    eager_us = _events_us(lambda: kernels.q4k_matvec(x, w, out=y), 64 * reps)
+    copies = [w.clone() for _ in range(LINEAR_COPIES)]
+    ys = [torch.empty(1, n, device=dev) for _ in range(LINEAR_COPIES)]
+    calls = [(lambda wc=wc, yc=yc: kernels.q4k_matvec(x, wc, out=yc)) for wc, yc in zip(copies, ys)]
+    cold_us = _graph_us_per_call(calls, reps)
+    call_bytes = w.numel() + k * 2 + n * 4
+    gbs = call_bytes / (cold_us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = len(os.sched_getaffinity(0))
+        torch.set_num_threads(threads)
+        xc = x.float().cpu()
+        wc = torch.from_numpy(w_deq)
+        runs = []
+        for _ in range(7):
+            t0 = time.perf_counter()
+            for _ in range(200):
+                torch.nn.functional.linear(xc, wc)
+            runs.append((time.perf_counter() - t0) / 200)
+        cpu = {"value": round(statistics.median(runs) * 1e6, 2), "unit": "us/call", "cores": threads, "kind": "port",
+               "sample": f"torch {torch.__version__} F.linear on the oracle-dequantized fp32 W, median of 7 runs of "
+                         f"200 calls"}
+    line = {
+        "metric": "Q4_K linear x[1,1024] . W[3072,1024]^T latency (BASELINE configs[0])",
+        "value": round(hot_us, 3),
+        "unit": "us/call",
+        "n_gpus": 1,
+        "steps": reps,
+        "warmup": 1,
+        "ms_per_step": round(hot_us * 64 / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seed 0: x ~ N(0,1) bf16, W ~ N(0,0.02) quantized to Q4_K on the GPU)",
+        "config": {"workload": "one Q4_K GEMV, x bf16 [1,1024], W [3072,1024] (1 769 472 B packed), fp32 out; "
+                               "a step = 64 calls replayed in a HIP graph on the hot weight",
+                   "batch": 1},
+        "eager_us_per_call": round(eager_us, 3),
+        "max_rel_error_vs_oracle": err,
+        "roofline": {"bound": "hbm", "kernel": "q4k_gemv_kernel (K 1024)", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": call_bytes, "avg_launch_us": round(cold_us, 3),
+                     "note": f"one call on each of {LINEAR_COPIES} distinct weight copies per replay (cold weights)"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+# --------------------------------------------------------------- C2 0.6B decode --
+
+C2_PROMPT = 128
+C2_TOKENS = 128
+
+
+def bench_c2(args) -> int:
+    """the 28-layer Qwen3-0.6B shape, a prompt of 128 random token ids through the chunked
+    matrix-core prefill, then 128 greedy tokens (HIP graphs of 8 decode steps).  value = the 128 tokens over
+    the time from the prompt's arrival to the last token; the decode-only rate is reported beside it."""
+    import torch
+
+    from torch2vk_amd.qwen3.config import QWEN3_0_6B
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+    from torch2vk_amd.qwen3.weights import synthetic_weights
+
+    if not torch.cuda.is_available():
+        print("no HIP device", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    cfg = QWEN3_0_6B
+    weights = synthetic_weights(cfg, device=dev, seed=0, policy=args.policy)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    prompt = torch.randint(0, cfg.vocab, (C2_PROMPT,), generator=gen, device=dev)
+    dec = Qwen3Decoder(weights, max_positions=C2_PROMPT + C2_TOKENS + 16, max_new_tokens=C2_TOKENS + 8, device=dev)
+    dec.stop_on_eos = False
+    spg = args.steps_per_graph
+    runs = []
+    for r in range(1 + max(1, args.kernel_reps)):   # the first pass warms the graphs and is not counted
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dec.prefill_chunked(prompt)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        dec.run_steps(C2_TOKENS - 1, steps_per_graph=spg, use_graph=not args.no_graph)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        status = decode_status(dec)
+        if status:
+            print(f"[bench] persistent kernel status {status:#x}: run invalid", file=sys.stderr, flush=True)
+            return 3
+        if r:
+            runs.append((t1 - t0, t2 - t1))
+        print(f"[bench] pass {r}: prefill {1e3 * (t1 - t0):.2f} ms, {C2_TOKENS - 1} steps {1e3 * (t2 - t1):.2f} ms",
+              file=sys.stderr, flush=True)
+    pre = statistics.median(u for u, _ in runs)
+    steps_s = statistics.median(v for _, v in runs)
+    total = pre + steps_s
+    tokens = [int(t) for t in dec.generated[:C2_TOKENS].tolist()]
+    assert len(tokens) == C2_TOKENS and min(tokens) >= 0
+    kern = kernel_timing(dec, weights, args.kernel_reps)
+    dom = kern["dominant"]
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_c2(cfg, weights, prompt.cpu(), args.cpu_sample_steps)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+    line = {
+        "metric": "Qwen3-0.6B-shape int4 decode tok/s @bs1, 128-token prompt + 128 tokens (BASELINE configs[1])",
+        "value": round(C2_TOKENS / total, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": C2_TOKENS,
+        "warmup": 1,
+        "ms_per_step": round(1e3 * total / C2_TOKENS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        # the reference's one published number: Qwen3-0.6B Q4_K_M greedy decode at 7.4 ms/token (~135 tok/s) on
+        # its Radeon 890M (docs/torch2vk-introduction.md:676); comparable for the Q4_K_M policy only
+        "vs_baseline": round((C2_TOKENS / total) / 135.0, 3) if args.policy == "q4_k_m" else None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights quantized on the GPU, "
+                + ("Q4_K uniform int4" if args.policy == "uniform" else "Q4_K_M (Q4_K + Q6_K)") + "; random prompt ids)",
+        "config": {"workload": f"qwen3-0.6b-shape greedy decode, batch 1: {C2_PROMPT}-token prompt through the "
+                               f"chunked prefill, then {C2_TOKENS} tokens (HIP graphs of {spg} steps, "
+                               + ("persistent layers kernel" if dec.persistent else "one launch per op") + ")",
+                   "batch": 1, "prompt": C2_PROMPT, "new_tokens": C2_TOKENS},
+        "prefill_ms": round(pre * 1e3, 3),
+        "decode_tok_s": round((C2_TOKENS - 1) / steps_s, 2),
+        "roofline": {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(dom["gbs"], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": dom["bytes"], "avg_launch_us": round(dom["us"], 3)},
+        "qmatmul_gbs": round(kern["qmatmul_gbs"], 1),
+        "cpu_baseline": cpu,
+        "status": 0,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline_c2(cfg, weights, prompt, runs: int) -> dict:
+    """The CPU oracle's whole 0.6B decoder (torch, fp32 weights dequantized by the oracle): the 128-token
+    prompt, then the median of ``runs`` single-token decode steps after it."""
+    import torch
+
+    import oracle
+    from oracle.reference import Qwen3CpuModel, Qwen3Shape
+    from torch2vk_amd.qwen3.weights import matrix_shapes
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    c = cfg
+    shapes = matrix_shapes(c)
+    dense = {name: torch.from_numpy(getattr(oracle, f"dequant_{weights.types[name]}")(
+        weights.packed[name].cpu().numpy(), shapes[name][1])) for name in weights.packed}
+    dense.update({name: t.cpu() for name, t in weights.norms.items()})
+    shape = Qwen3Shape(hidden=c.hidden, layers=c.layers, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
+                       mlp=c.mlp, vocab=c.vocab, rope_theta=c.rope_theta)
+    model = Qwen3CpuModel(shape, dense, max_positions=len(prompt) + runs + 2)
+    t0 = time.perf_counter()
+    hidden = model.forward(prompt.long(), start=0)
+    t_prompt = time.perf_counter() - t0
+    tok = int(torch.argmax(model.logits(hidden)))
+    times = []
+    for s in range(runs):
+        t0 = time.perf_counter()
+        hidden = model.forward(torch.tensor([tok]), start=len(prompt) + s)
+        tok = int(torch.argmax(model.logits(hidden)))
+        times.append(time.perf_counter() - t0)
+    t_tok = statistics.median(times)
+    return {"value": round(1.0 / t_tok, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"CPU oracle decoder (torch {torch.__version__}, all 28 layers, fp32 weights dequantized by the "
+                      f"oracle): {len(prompt)}-token prompt in {t_prompt:.2f} s, then the median of {runs} decode "
+                      f"steps ({t_tok * 1e3:.1f} ms)"}
 
 
 # ----------------------------------------------------------------- prefill --
