@@ -331,7 +331,7 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
                 for (int e = 0; e < 16; ++e) mt = fmaxf(mt, s[kb][e]);
             mt *= a.scale_log2;
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 32, T2H_WAVE));
+        mt = xor_max<32>(mt);
         // The running max moves only when the tile's max exceeds it by more than
         // FA_RESCALE (log2 units): P then stays below 2^FA_RESCALE, and the O
         // rescale is skipped on the tiles where no lane of the wave needs it.
@@ -392,7 +392,7 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
         __syncthreads();
     }
 
-    const float l = l_part + __shfl_xor(l_part, 32, T2H_WAVE);
+    const float l = xor_sum<32>(l_part);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     if (q_valid) {
         uint16_t* orow = a.out + (size_t)b * a.o_sb + (size_t)qi * a.o_st + (size_t)h * a.o_sh;

@@ -84,6 +84,49 @@ __device__ __forceinline__ float dpp_f32(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
 }
 
+// Exchange between lanes l and l ^ MASK (MASK 16 or 32) on v_permlane16_swap /
+// v_permlane32_swap: VALU instructions, where __shfl_xor is an LDS-crossbar
+// permute (ds_bpermute).  With operands (a, b), a lane with bit MASK clear gets
+// (its a, the partner's a) and a lane with it set (the partner's b, its b).
+template <int MASK>
+__device__ __forceinline__ void lane_swap(float a, float b, float& r0, float& r1) {
+    static_assert(MASK == 16 || MASK == 32, "swap across 16 or 32 lanes");
+    const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+    if constexpr (MASK == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(ua, ub, false, false);
+        r0 = __uint_as_float(r[0]);
+        r1 = __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(ua, ub, false, false);
+        r0 = __uint_as_float(r[0]);
+        r1 = __uint_as_float(r[1]);
+    }
+}
+
+// x[l] + x[l ^ MASK] and max(x[l], x[l ^ MASK]) in every lane: the same values
+// as x + __shfl_xor(x, MASK) (addition and max commute).
+template <int MASK>
+__device__ __forceinline__ float xor_sum(float x) {
+    float r0, r1;
+    lane_swap<MASK>(x, x, r0, r1);
+    return r0 + r1;
+}
+template <int MASK>
+__device__ __forceinline__ float xor_max(float x) {
+    float r0, r1;
+    lane_swap<MASK>(x, x, r0, r1);
+    return fmaxf(r0, r1);
+}
+
+// Reduce-scatter of a pair across lanes l and l ^ MASK: the lane with bit MASK
+// clear gets lo + the partner's lo, the other hi + the partner's hi.
+template <int MASK>
+__device__ __forceinline__ float xor_reduce_scatter(float lo, float hi) {
+    float r0, r1;
+    lane_swap<MASK>(lo, hi, r0, r1);
+    return r0 + r1;
+}
+
 // Sum over the 64 lanes of a wave; every lane gets the total.  Butterfly
 // within each 16-lane row with DPP (xor 1, xor 2, half-row mirror, row
 // mirror), then the four row totals are read out as scalars.

@@ -241,12 +241,9 @@ struct DlAttnLds {
 constexpr int dl_max3(int a, int b, int c) { return a > b ? (a > c ? a : c) : (b > c ? b : c); }
 
 // Model shape (8 kv heads of 128) and, per GEMV phase, the units per wave, the
-// ring depth and the units issued before the input is awaited.  V_LATE: the
-// attention V rows are issued once q|k|v has arrived instead of with the K
-// rows before the Q|K|V phase (measured faster for the 0.6B shape, slower for
-// the 8B one).
+// ring depth and the units issued before the input is awaited.
 template <int HSB_, int MSB_, int NH_, int QKV_U, int QKV_R, int QKV_P, int O_U, int O_R, int O_P, int GU_U,
-          int GU_R, int GU_P, int DN_U, int DN_R, int DN_P, bool V_LATE>
+          int GU_R, int GU_P, int DN_U, int DN_R, int DN_P>
 struct DlShape {
     static constexpr int HSB = HSB_;             // hidden / 256 (superblocks)
     static constexpr int MSB = MSB_;             // MLP / 256
@@ -259,7 +256,6 @@ struct DlShape {
     static constexpr int KMAX = dl_max3(HID, MLP, QD);
     static constexpr int qkv_u = QKV_U, qkv_r = QKV_R, qkv_p = QKV_P, o_u = O_U, o_r = O_R, o_p = O_P;
     static constexpr int gu_u = GU_U, gu_r = GU_R, gu_p = GU_P, dn_u = DN_U, dn_r = DN_R, dn_p = DN_P;
-    static constexpr bool v_late = V_LATE;
     static_assert(NH % NK == 0 && NH / NK <= 4, "GQA group of 1..4 q heads");
 };
 #ifndef DL_R_QKV
@@ -275,8 +271,8 @@ struct DlShape {
 #define DL_R_DOWN 2
 #endif
 using DlQwen3_8B = DlShape<16, 48, 32, 3, DL_R_QKV, DL_PRE_QKV, 2, DL_R_O, DL_PRE_O, 6, DL_R_GU, DL_PRE_GU, 2, DL_R_DOWN,
-                           DL_PRE_DOWN, false>;
-using DlQwen3_0_6B = DlShape<4, 12, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, true>;
+                           DL_PRE_DOWN>;
+using DlQwen3_0_6B = DlShape<4, 12, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1>;
 
 constexpr int DL_HOLD = 4;  // residual rows a wave owns in one phase, at most
 
@@ -683,12 +679,9 @@ __device__ __forceinline__ void dl_attn_issue_v(DlAttnBank& bk, const uint16_t* 
 // Reduce-scatter across the wave's rows: lanes with lane bit 4 or 5 (MASK 16 or 32) clear keep the lower
 // half of the N values, the others the upper half, each adding its partner's partial of the half it keeps.
 template <int MASK, int N>
-__device__ __forceinline__ void dl_rs_x(const float (&in)[N], float (&out)[N / 2], bool upper) {
+__device__ __forceinline__ void dl_rs_x(const float (&in)[N], float (&out)[N / 2]) {
 #pragma unroll
-    for (int i = 0; i < N / 2; ++i) {
-        const float lo = in[i], hi = in[N / 2 + i];
-        out[i] = (upper ? hi : lo) + __shfl_xor(upper ? lo : hi, MASK, 64);
-    }
+    for (int i = 0; i < N / 2; ++i) out[i] = xor_reduce_scatter<MASK>(in[i], in[N / 2 + i]);
 }
 
 __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w, bool has_w, float eps, float cs,
@@ -776,8 +769,6 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
     }
     __syncthreads();
     dl_stamp(tr, DL_TR_READY);
-    // V_LATE: V is needed only after the scores, issued behind every wait of the phase
-    if constexpr (S::v_late) dl_attn_issue_v(bk, vc, kvh, p0, rows);
     after_ready();
 
     // Scores S[position][head] = K . q^T on the matrix cores: two 16-position
@@ -829,8 +820,8 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
         valid[j] = 8 * kg + j < rows;
         m = fmaxf(m, valid[j] ? sc[j] : -INFINITY);
     }
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    m = xor_max<16>(m);
+    m = xor_max<32>(m);
     float e[8];
     float l = 0.0f;
 #pragma unroll
@@ -838,8 +829,8 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
         e[j] = valid[j] ? expf(sc[j] - m) : 0.0f;
         l += e[j];
     }
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l = xor_sum<16>(l);
+    l = xor_sum<32>(l);
     dl_stamp(tr, DL_TR_FIRST);
     // P of every head at the row's 8 positions, from lanes 0 .. GROUP-1 of the row (row_newbcast)
     float p[NV];
@@ -869,8 +860,8 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
             for (int d = 0; d < 8; ++d) o[gg * 8 + d] = fmaf(p[gg * 8 + j], vf[d], o[gg * 8 + d]);
     }
     float o1[NV / 2], of[NV / 4];
-    dl_rs_x<32>(o, o1, pg >> 1);
-    dl_rs_x<16>(o1, of, pg & 1);
+    dl_rs_x<32>(o, o1);
+    dl_rs_x<16>(o1, of);
     if (tr != nullptr) dl_stamp(tr, DL_TR_A_PV);
     // the lane holds head og, dims 8 part + od .. + NV/4 - 1
     const int obase = (pg >> 1) * (NV / 2) + (pg & 1) * (NV / 4);
@@ -1037,8 +1028,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
 
     auto issue_bank = [&](uint32_t layer, DlAttnBank& bk) {
         dl_attn_issue_k(bk, dl_gptr<const uint16_t>(layer_ptr(layer, DL_K_CACHE)), kvh, att_p0, att_rows);
-        if constexpr (!S::v_late)
-            dl_attn_issue_v(bk, dl_gptr<const uint16_t>(layer_ptr(layer, DL_V_CACHE)), kvh, att_p0, att_rows);
+        dl_attn_issue_v(bk, dl_gptr<const uint16_t>(layer_ptr(layer, DL_V_CACHE)), kvh, att_p0, att_rows);
     };
 
     // A phase's first units are issued when the phase begins, after the phase

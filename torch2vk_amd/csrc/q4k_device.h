@@ -49,7 +49,7 @@ __device__ __forceinline__ void stage_x4(uint32_t* xp, float* xsum, int k, float
     float s = (v0 + v1) + (v2 + v3);
     s += dpp_f32<0xB1>(s);  // quad_perm [1,0,3,2]: lane ^ 1
     s += dpp_f32<0x4E>(s);  // quad_perm [2,3,0,1]: lane ^ 2
-    s += __shfl_xor(s, 4, T2H_WAVE);
+    s += dpp_f32<0x141>(s);  // row_half_mirror: a lane of the other quad of the 8, which holds that quad's sum
     if (((k >> 2) & 7) == 0) xsum[k >> 5] = s;
 }
 
