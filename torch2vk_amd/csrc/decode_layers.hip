@@ -742,7 +742,9 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
         if (tr != nullptr && tid == 0) tr[DL_TR_POLLS] = polls;
         float r0, r1;
         dl_norm_rope(ll_val32(w[0]), ll_val32(w[1]), q_norm, q_norm != nullptr, a.eps, cs, sn, rope, r0, r1);
-        const float scale = 1.0f / sqrtf((float)DL_D);
+        // scores in base-2 units (log2(e) / sqrt(D) folded into q): the softmax and every combine of partials
+        // below are exp2 of differences, one v_exp_f32 each
+        const float scale = 1.4426950408889634f / sqrtf((float)DL_D);
         const float q0 = r0 * scale, q1 = r1 * scale;
         const uint32_t h0 = f32_to_bf16_bits(q0), h1 = f32_to_bf16_bits(q1);
         sm.qhi[wave][lane] = (uint16_t)h0;
@@ -826,7 +828,7 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
     float l = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        e[j] = valid[j] ? expf(sc[j] - m) : 0.0f;
+        e[j] = valid[j] ? __builtin_amdgcn_exp2f(sc[j] - m) : 0.0f;
         l += e[j];
     }
     l = xor_sum<16>(l);
@@ -886,7 +888,7 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
 #pragma unroll
         for (int w = 0; w < DL_WAVES; ++w) {
             const float m = sm.wml[w][gg][0];
-            const float f = m == -INFINITY ? 0.0f : expf(m - M);
+            const float f = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
             l = fmaf(f, sm.wml[w][gg][1], l);
             const float2 ov = sm.wo[w][gg][dl];
             r0 = fmaf(f, ov.x, r0);
@@ -932,7 +934,7 @@ __device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP>& sm, const Dl
     float l = 0.0f, r0 = 0.0f, r1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
-        const float f = ml[i].x == -INFINITY ? 0.0f : expf(ml[i].x - M);
+        const float f = ml[i].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml[i].x - M);
         l = fmaf(f, ml[i].y, l);
         r0 = fmaf(f, ov[i].x, r0);
         r1 = fmaf(f, ov[i].y, r1);
@@ -951,7 +953,7 @@ __device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP>& sm, const Dl
 #pragma unroll
         for (int w = 0; w < DL_WAVES; ++w) {
             const float m = sm.wml[w][0][0];
-            const float f = m == -INFINITY ? 0.0f : expf(m - Mt);
+            const float f = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - Mt);
             lt = fmaf(f, sm.wml[w][0][1], lt);
             const float2 o = sm.wo[w][0][lane];
             a0 = fmaf(f, o.x, a0);
