@@ -127,6 +127,16 @@ __device__ __forceinline__ float xor_reduce_scatter(float lo, float hi) {
     return r0 + r1;
 }
 
+// ds_read_b64_tr_b16 (gfx950), 8 bytes per lane from LDS, transposed within each
+// 16-lane group: with row(L) the four 16-bit elements at lane L's address, lane i
+// receives element j of its result = row(4 j + i / 4)[i % 4], j = 0..3.
+typedef short t2h_v4i16 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16_b64(const uint16_t* lds) {
+    const t2h_v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (t2h_v4i16 __attribute__((address_space(3)))*)(lds));
+    return __builtin_bit_cast(uint2, r);
+}
+
 // Sum over the 64 lanes of a wave; every lane gets the total.  Butterfly
 // within each 16-lane row with DPP (xor 1, xor 2, half-row mirror, row
 // mirror), then the four row totals are read out as scalars.

@@ -227,13 +227,22 @@ __device__ __forceinline__ uint32_t ll_wait(uint64_t (&w)[N], Addr addr, Ok ok, 
 typedef __bf16 dl_bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float dl_f32x4_t __attribute__((ext_vector_type(4)));
 
-template <int GROUP>
+// V rows staged for the matrix-core P.V: [position][dims], padded to 272 B so that the transposing reads of
+// 16 rows at one column spread over the banks
+constexpr int DL_VROW = DL_D + 8;
+
+template <int GROUP, bool PV_MFMA>
 struct DlAttnLds {
+    // each wave's V rows, read back transposed (ds_read_b64_tr_b16) as the B operand of P.V (matrix-core P.V)
+    alignas(16) uint16_t vst[PV_MFMA ? DL_WAVES : 1][DL_ATT_POS * DL_VROW];
     // the block's q heads, normalised, rotated and scaled, as bf16 hi + lo parts (q = hi + lo to 2^-17)
     uint16_t qhi[GROUP][DL_D];
     uint16_t qlo[GROUP][DL_D];
     float wml[DL_WAVES][GROUP][2];
-    float2 wo[DL_WAVES][GROUP][64];
+    // each wave's P.V: [dim][head] (heads 0 .. GROUP-1 of 4) from the matrix cores, or [head][dim pair] as
+    // float2 from the VALU
+    float4 wo[DL_WAVES][DL_D];
+    float2 mo[DL_WAVES][64];               // the merge: each wave's combine of its partials
     uint16_t knew[DL_D];                   // the new position's K and V rows (bf16), for the wave holding it
     uint16_t vnew[DL_D];
 };
@@ -243,7 +252,7 @@ constexpr int dl_max3(int a, int b, int c) { return a > b ? (a > c ? a : c) : (b
 // Model shape (8 kv heads of 128) and, per GEMV phase, the units per wave, the
 // ring depth and the units issued before the input is awaited.
 template <int HSB_, int MSB_, int NH_, int QKV_U, int QKV_R, int QKV_P, int O_U, int O_R, int O_P, int GU_U,
-          int GU_R, int GU_P, int DN_U, int DN_R, int DN_P>
+          int GU_R, int GU_P, int DN_U, int DN_R, int DN_P, bool PV_MFMA>
 struct DlShape {
     static constexpr int HSB = HSB_;             // hidden / 256 (superblocks)
     static constexpr int MSB = MSB_;             // MLP / 256
@@ -256,6 +265,10 @@ struct DlShape {
     static constexpr int KMAX = dl_max3(HID, MLP, QD);
     static constexpr int qkv_u = QKV_U, qkv_r = QKV_R, qkv_p = QKV_P, o_u = O_U, o_r = O_R, o_p = O_P;
     static constexpr int gu_u = GU_U, gu_r = GU_R, gu_p = GU_P, dn_u = DN_U, dn_r = DN_R, dn_p = DN_P;
+    // attention P.V on the matrix cores (V transposed through LDS) or on the VALU (P broadcast by DPP):
+    // measured faster for the 8B shape (4 q heads, 17 positions per wave at 4096) and slower for the 0.6B
+    // one (2 q heads, 7 positions per wave at 1540)
+    static constexpr bool pv_mfma = PV_MFMA;
     static_assert(NH % NK == 0 && NH / NK <= 4, "GQA group of 1..4 q heads");
 };
 #ifndef DL_R_QKV
@@ -271,8 +284,8 @@ struct DlShape {
 #define DL_R_DOWN 2
 #endif
 using DlQwen3_8B = DlShape<16, 48, 32, 3, DL_R_QKV, DL_PRE_QKV, 2, DL_R_O, DL_PRE_O, 6, DL_R_GU, DL_PRE_GU, 2, DL_R_DOWN,
-                           DL_PRE_DOWN>;
-using DlQwen3_0_6B = DlShape<4, 12, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1>;
+                           DL_PRE_DOWN, true>;
+using DlQwen3_0_6B = DlShape<4, 12, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, false>;
 
 constexpr int DL_HOLD = 4;  // residual rows a wave owns in one phase, at most
 
@@ -284,7 +297,7 @@ union DlShared {
         float red[DL_WAVES];
         float hold[DL_WAVES * DL_HOLD];  // residual epilogue: the old h of the block's rows [wave][row]
     } g;
-    DlAttnLds<S::GROUP> at;
+    DlAttnLds<S::GROUP, S::pv_mfma> at;
 };
 
 // ------------------------------------------------------------ GEMV phase ----
@@ -676,14 +689,6 @@ __device__ __forceinline__ void dl_attn_issue_v(DlAttnBank& bk, const uint16_t* 
     }
 }
 
-// Reduce-scatter across the wave's rows: lanes with lane bit 4 or 5 (MASK 16 or 32) clear keep the lower
-// half of the N values, the others the upper half, each adding its partner's partial of the half it keeps.
-template <int MASK, int N>
-__device__ __forceinline__ void dl_rs_x(const float (&in)[N], float (&out)[N / 2]) {
-#pragma unroll
-    for (int i = 0; i < N / 2; ++i) out[i] = xor_reduce_scatter<MASK>(in[i], in[N / 2 + i]);
-}
-
 __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w, bool has_w, float eps, float cs,
                                              float sn, bool rope, float& r0, float& r1) {
     const int lane = dl_tid() & 63;
@@ -706,7 +711,7 @@ __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w,
 // Block (kv head kvh, slot bs): wave w covers positions [p0, p0 + span) of the
 // first L; the block's (max, sum, output) per q head goes to part[kvh][bs].
 template <class S, class Hook = DlNoHook>
-__device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP>& sm, const DlArgs& a,
+__device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP, S::pv_mfma>& sm, const DlArgs& a,
                                               const uint64_t* lp, int kvh, int bs, int pos, int L, uint32_t e_qkv,
                                               uint32_t e_part, uint32_t site, uint64_t* tr,
                                               Hook after_ready = Hook()) {
@@ -776,7 +781,6 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
     // Scores S[position][head] = K . q^T on the matrix cores: two 16-position
     // tiles, 4 chunks of 32 dims, q as bf16 hi + lo (columns >= GROUP are 0).
     // Lane l then holds head l % 16 at positions 8 (l / 16) + 4 t + i.
-    constexpr int NV = GROUP * 8;
     const int kg = lane >> 4, n = lane & 15;
     const int pg = kg, part = n;  // the P.V view of the same lane
     dl_bf16x8_t qh[4], ql[4];
@@ -834,43 +838,91 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
     l = xor_sum<16>(l);
     l = xor_sum<32>(l);
     dl_stamp(tr, DL_TR_FIRST);
-    // P of every head at the row's 8 positions, from lanes 0 .. GROUP-1 of the row (row_newbcast)
-    float p[NV];
+    if constexpr (S::pv_mfma) {
+        // P.V on the matrix cores: O[head][dim] = P[head][position] . V[position][dim].  P is the A operand as the
+        // scores left it (lane l: head l % 16 at positions 8 (l / 16) + j), as bf16 hi + lo; V goes through LDS:
+        // the wave's rows are stored [position][dims] and read back transposed, lane 4 j + q of row group g
+        // addressing row 8 g + j (+ 4), dims 16 T + 4 q, so that lane i of the group receives dim 16 T + i of
+        // positions 8 g + 0..7, the B operand of dim tile T.
+        uint16_t* vs = sm.vst[wave];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        p[0 * 8 + j] = dpp_f32<0x150>(e[j]);
-        p[1 * 8 + j] = dpp_f32<0x151>(e[j]);
-        if constexpr (GROUP == 4) {
-            p[2 * 8 + j] = dpp_f32<0x152>(e[j]);
-            p[3 * 8 + j] = dpp_f32<0x153>(e[j]);
+        for (int j = 0; j < 8; ++j) {
+            const uint4 vv = (has_new && rnew == 8 * pg + j) ? vnr : bk.vr[j];
+            *reinterpret_cast<uint4*>(vs + (8 * pg + j) * DL_VROW + part * 8) = vv;
         }
+        uint4 ph4, pl4;
+        {
+            uint32_t hb[8], lb[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                hb[j] = f32_to_bf16_bits(e[j]);
+                lb[j] = f32_to_bf16_bits(e[j] - bf16_bits_to_f32(hb[j]));
+            }
+            ph4 = make_uint4(hb[0] | hb[1] << 16, hb[2] | hb[3] << 16, hb[4] | hb[5] << 16, hb[6] | hb[7] << 16);
+            pl4 = make_uint4(lb[0] | lb[1] << 16, lb[2] | lb[3] << 16, lb[4] | lb[5] << 16, lb[6] | lb[7] << 16);
+        }
+        const dl_bf16x8_t pa_hi = __builtin_bit_cast(dl_bf16x8_t, ph4), pa_lo = __builtin_bit_cast(dl_bf16x8_t, pl4);
+        const uint16_t* vt = vs + (8 * kg + (n >> 2)) * DL_VROW + 4 * (n & 3);
+        dl_f32x4_t ov[DL_D / 16];
+#pragma unroll
+        for (int t = 0; t < DL_D / 16; ++t) {
+            const uint2 b0 = lds_read_tr16_b64(vt + 16 * t);
+            const uint2 b1 = lds_read_tr16_b64(vt + 4 * DL_VROW + 16 * t);
+            const dl_bf16x8_t vb = __builtin_bit_cast(dl_bf16x8_t, make_uint4(b0.x, b0.y, b1.x, b1.y));
+            ov[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_hi, vb, dl_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            ov[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, vb, ov[t], 0, 0, 0);
+        }
+        if (tr != nullptr) dl_stamp(tr, DL_TR_A_PV);
+        // lanes 0..15 hold heads 0..3 of dims 16 T + lane
+        if (lane < 16) {
+#pragma unroll
+            for (int t = 0; t < DL_D / 16; ++t)
+                sm.wo[wave][16 * t + lane] = make_float4(ov[t][0], ov[t][1], ov[t][2], ov[t][3]);
+        }
+    } else {
+        // P of every head at the row's 8 positions, from lanes 0 .. GROUP-1 of the row (row_newbcast)
+        constexpr int NV = GROUP * 8;
+        float p[NV];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            p[0 * 8 + j] = dpp_f32<0x150>(e[j]);
+            p[1 * 8 + j] = dpp_f32<0x151>(e[j]);
+            if constexpr (GROUP == 4) {
+                p[2 * 8 + j] = dpp_f32<0x152>(e[j]);
+                p[3 * 8 + j] = dpp_f32<0x153>(e[j]);
+            }
+        }
+        // P.V over the row's positions (dims 8 part .. + 7), then summed over the 4 rows (scattered)
+        float o[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) o[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint4 vv = (has_new && rnew == 8 * pg + j) ? vnr : bk.vr[j];
+            const float vf[8] = {bf16_bits_to_f32(vv.x & 0xffffu), bf16_bits_to_f32(vv.x >> 16),
+                                 bf16_bits_to_f32(vv.y & 0xffffu), bf16_bits_to_f32(vv.y >> 16),
+                                 bf16_bits_to_f32(vv.z & 0xffffu), bf16_bits_to_f32(vv.z >> 16),
+                                 bf16_bits_to_f32(vv.w & 0xffffu), bf16_bits_to_f32(vv.w >> 16)};
+#pragma unroll
+            for (int gg = 0; gg < GROUP; ++gg)
+#pragma unroll
+                for (int d = 0; d < 8; ++d) o[gg * 8 + d] = fmaf(p[gg * 8 + j], vf[d], o[gg * 8 + d]);
+        }
+        // reduce-scatter over the 4 rows: lanes with bit 5 (then 4) clear keep the lower half, each adding its
+        // partner's partial of that half
+        float o1[NV / 2], of[NV / 4];
+#pragma unroll
+        for (int i = 0; i < NV / 2; ++i) o1[i] = xor_reduce_scatter<32>(o[i], o[NV / 2 + i]);
+#pragma unroll
+        for (int i = 0; i < NV / 4; ++i) of[i] = xor_reduce_scatter<16>(o1[i], o1[NV / 4 + i]);
+        if (tr != nullptr) dl_stamp(tr, DL_TR_A_PV);
+        // the lane holds head og, dims 8 part + od .. + NV/4 - 1
+        const int obase = (pg >> 1) * (NV / 2) + (pg & 1) * (NV / 4);
+        const int og = obase / 8, od = obase % 8;
+        float* wo = reinterpret_cast<float*>(&sm.wo[wave][0]) + og * DL_D + part * 8 + od;
+#pragma unroll
+        for (int i = 0; i < NV / 4; ++i) wo[i] = of[i];
     }
-    // P.V over the row's positions (dims 8 part .. + 7), then summed over the 4 rows (scattered)
-    float o[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) o[i] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint4 vv = (has_new && rnew == 8 * pg + j) ? vnr : bk.vr[j];
-        const float vf[8] = {bf16_bits_to_f32(vv.x & 0xffffu), bf16_bits_to_f32(vv.x >> 16),
-                             bf16_bits_to_f32(vv.y & 0xffffu), bf16_bits_to_f32(vv.y >> 16),
-                             bf16_bits_to_f32(vv.z & 0xffffu), bf16_bits_to_f32(vv.z >> 16),
-                             bf16_bits_to_f32(vv.w & 0xffffu), bf16_bits_to_f32(vv.w >> 16)};
-#pragma unroll
-        for (int gg = 0; gg < GROUP; ++gg)
-#pragma unroll
-            for (int d = 0; d < 8; ++d) o[gg * 8 + d] = fmaf(p[gg * 8 + j], vf[d], o[gg * 8 + d]);
-    }
-    float o1[NV / 2], of[NV / 4];
-    dl_rs_x<32>(o, o1);
-    dl_rs_x<16>(o1, of);
-    if (tr != nullptr) dl_stamp(tr, DL_TR_A_PV);
-    // the lane holds head og, dims 8 part + od .. + NV/4 - 1
-    const int obase = (pg >> 1) * (NV / 2) + (pg & 1) * (NV / 4);
-    const int og = obase / 8, od = obase % 8;
-    float* wo = reinterpret_cast<float*>(&sm.wo[wave][og][0]) + part * 8 + od;
-#pragma unroll
-    for (int i = 0; i < NV / 4; ++i) wo[i] = of[i];
     if (kg == 0 && n < GROUP) {
         sm.wml[wave][n][0] = m;
         sm.wml[wave][n][1] = l;
@@ -890,7 +942,12 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
             const float m = sm.wml[w][gg][0];
             const float f = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
             l = fmaf(f, sm.wml[w][gg][1], l);
-            const float2 ov = sm.wo[w][gg][dl];
+            float2 ov;
+            if constexpr (S::pv_mfma)
+                ov = make_float2(reinterpret_cast<const float*>(&sm.wo[w][2 * dl])[gg],
+                                 reinterpret_cast<const float*>(&sm.wo[w][2 * dl + 1])[gg]);
+            else
+                ov = reinterpret_cast<const float2*>(reinterpret_cast<const float*>(&sm.wo[w][0]) + gg * DL_D)[dl];
             r0 = fmaf(f, ov.x, r0);
             r1 = fmaf(f, ov.y, r1);
         }
@@ -906,8 +963,8 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
 
 // Head hq = blockIdx.x (< NH): merge the DL_ATT_SLOTS block partials of its kv head.
 template <class S>
-__device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP>& sm, const DlArgs& a, int hq, uint32_t e_part,
-                                               uint32_t e_attn, uint32_t site, uint64_t* tr) {
+__device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP, S::pv_mfma>& sm, const DlArgs& a, int hq,
+                                               uint32_t e_part, uint32_t e_attn, uint32_t site, uint64_t* tr) {
     constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kvh = hq / GROUP, gg = hq % GROUP;
@@ -939,7 +996,7 @@ __device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP>& sm, const Dl
         r0 = fmaf(f, ov[i].x, r0);
         r1 = fmaf(f, ov[i].y, r1);
     }
-    sm.wo[wave][0][lane] = make_float2(r0, r1);
+    sm.mo[wave][lane] = make_float2(r0, r1);
     if (lane == 0) {
         sm.wml[wave][0][0] = M;
         sm.wml[wave][0][1] = l;
@@ -955,7 +1012,7 @@ __device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP>& sm, const Dl
             const float m = sm.wml[w][0][0];
             const float f = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - Mt);
             lt = fmaf(f, sm.wml[w][0][1], lt);
-            const float2 o = sm.wo[w][0][lane];
+            const float2 o = sm.mo[w][lane];
             a0 = fmaf(f, o.x, a0);
             a1 = fmaf(f, o.y, a1);
         }
