@@ -451,6 +451,7 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
     for (int j = 0; j < PT; ++j)
         if (!valid(j)) hv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if constexpr (RMSNORM) {
+        // (loading the norm weights before the input wait instead measured slower for both shapes)
         float4 wv[PT];
 #pragma unroll
         for (int j = 0; j < PT; ++j) wv[j] = *reinterpret_cast<const float4*>(norm_w + elem(j));
@@ -689,15 +690,16 @@ __device__ __forceinline__ void dl_attn_issue_v(DlAttnBank& bk, const uint16_t* 
     }
 }
 
-__device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w, bool has_w, float eps, float cs,
+// Per-head RMSNorm (weights w0, w1 of the lane's dims lane and lane + 64, loaded by the caller before its
+// input wait) and rotate-half RoPE.
+__device__ __forceinline__ void dl_norm_rope(float x0, float x1, float w0, float w1, bool has_w, float eps, float cs,
                                              float sn, bool rope, float& r0, float& r1) {
-    const int lane = dl_tid() & 63;
     float n0 = x0, n1 = x1;
     if (has_w) {
         const float ss = wave_sum(x0 * x0 + x1 * x1);
         const float inv = 1.0f / sqrtf(ss / (float)DL_D + eps);
-        n0 = x0 * inv * w[lane];
-        n1 = x1 * inv * w[lane + 64];
+        n0 = x0 * inv * w0;
+        n1 = x1 * inv * w1;
     }
     if (rope) {
         r0 = n0 * cs - n1 * sn;
@@ -712,9 +714,9 @@ __device__ __forceinline__ void dl_norm_rope(float x0, float x1, const float* w,
 // first L; the block's (max, sum, output) per q head goes to part[kvh][bs].
 template <class S, class Hook = DlNoHook>
 __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP, S::pv_mfma>& sm, const DlArgs& a,
-                                              const uint64_t* lp, int kvh, int bs, int pos, int L, uint32_t e_qkv,
-                                              uint32_t e_part, uint32_t site, uint64_t* tr,
-                                              Hook after_ready = Hook()) {
+                                              const uint64_t* lp, int kvh, int bs, int pos, int L, float cs,
+                                              float sn, uint32_t e_qkv, uint32_t e_part, uint32_t site,
+                                              uint64_t* tr, Hook after_ready = Hook()) {
     constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int span = dl_att_span(L);
@@ -732,21 +734,27 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
     const uint64_t* kn = a.qkv_ll + S::QD;
     const uint64_t* vn = a.qkv_ll + S::QD + S::KVD;
     auto ok = [&](int, uint64_t v) { return ll_ok32(v, e_qkv); };
+    // the q / k norm weights of the lane's dims, in flight before the waits below
+    const bool q_wave = wave < GROUP;
+    float qw0 = 1.0f, qw1 = 1.0f, kw0 = 1.0f, kw1 = 1.0f;
+    if (q_wave && q_norm != nullptr) {
+        qw0 = q_norm[lane];
+        qw1 = q_norm[lane + 64];
+    }
+    if (has_new && k_norm != nullptr) {
+        kw0 = k_norm[lane];
+        kw1 = k_norm[lane + 64];
+    }
     __syncthreads();  // every wave is done with the previous phase's LDS
 
-    float cs = 1.0f, sn = 0.0f;
-    if (rope && (wave < GROUP || has_new)) {
-        const float inv_freq = exp2f(-(2.0f * (float)lane / (float)DL_D) * log2f(a.theta));
-        sincosf((float)pos * inv_freq, &sn, &cs);
-    }
-    if (wave < GROUP) {
+    if (q_wave) {
         const int hq = kvh * GROUP + wave;
         uint64_t w[2];
         const uint32_t polls =
             ll_wait(w, [&](int i) { return q + hq * DL_D + lane + 64 * i; }, ok, a.status, site | DL_W_ATTN_Q);
         if (tr != nullptr && tid == 0) tr[DL_TR_POLLS] = polls;
         float r0, r1;
-        dl_norm_rope(ll_val32(w[0]), ll_val32(w[1]), q_norm, q_norm != nullptr, a.eps, cs, sn, rope, r0, r1);
+        dl_norm_rope(ll_val32(w[0]), ll_val32(w[1]), qw0, qw1, q_norm != nullptr, a.eps, cs, sn, rope, r0, r1);
         // scores in base-2 units (log2(e) / sqrt(D) folded into q): the softmax and every combine of partials
         // below are exp2 of differences, one v_exp_f32 each
         const float scale = 1.4426950408889634f / sqrtf((float)DL_D);
@@ -763,7 +771,7 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
         ll_wait(w, [&](int i) { return i < 2 ? kn + kvh * DL_D + lane + 64 * i : vn + kvh * DL_D + 2 * lane + (i - 2); },
                 ok, a.status, site | DL_W_ATTN_KV);
         float k0, k1;
-        dl_norm_rope(ll_val32(w[0]), ll_val32(w[1]), k_norm, k_norm != nullptr, a.eps, cs, sn, rope, k0, k1);
+        dl_norm_rope(ll_val32(w[0]), ll_val32(w[1]), kw0, kw1, k_norm != nullptr, a.eps, cs, sn, rope, k0, k1);
         const uint16_t kb0 = (uint16_t)f32_to_bf16_bits(k0), kb1 = (uint16_t)f32_to_bf16_bits(k1);
         sm.knew[lane] = kb0;
         sm.knew[lane + 64] = kb1;
@@ -1036,6 +1044,13 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
     const int pos = __builtin_amdgcn_readfirstlane(
         __hip_atomic_load(const_cast<int32_t*>(a.pos_ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     const int L = pos + 1 < (int)a.s_cap ? pos + 1 : (int)a.s_cap;
+    // RoPE at `pos` for the rotation pair (lane, lane + 64) of a head: the same in every layer of the launch
+    float rope_cs = 1.0f, rope_sn = 0.0f;
+    if (a.theta > 0.0f) {
+        const int lane = threadIdx.x & 63;
+        const float inv_freq = exp2f(-(2.0f * (float)lane / (float)DL_D) * log2f(a.theta));
+        sincosf((float)pos * inv_freq, &rope_sn, &rope_cs);
+    }
     const int kvh = blockIdx.x % 8, bs = blockIdx.x / 8;
 
     // The layer table is copied into LDS once.  Read from memory, each layer's
@@ -1138,7 +1153,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
             uint64_t lp[DL_LAYER_PTRS];
 #pragma unroll
             for (int i = 0; i < DL_LAYER_PTRS; ++i) lp[i] = layer_ptr(layer, i);
-            dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, pos, L, e_qkv, e_part, lsite, tr, [&] {
+            dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, pos, L, rope_cs, rope_sn, e_qkv, e_part, lsite, tr, [&] {
                 if constexpr (o_early > 0) dl_issue_pre<S::QSB, 1, S::o_u, o_early, o_sp>(uo, o_rows(layer));
             });
             dl_stamp(tr, DL_TR_END);
