@@ -34,6 +34,12 @@ constexpr int GQ_THREADS = 512;
 constexpr int GQ_BN = 256;
 constexpr int GQ_BK = 64;
 constexpr int GQ_LDS_ROW = GQ_BK + 8;  // bf16 elements per padded LDS row
+// Stage kt + 1's LDS stores spread over stage kt's four 16-deep MFMA steps (A in the first two, the weight
+// dequantisation in the third), so that the VALU work runs while the matrix cores are busy instead of
+// after them.
+#ifndef GQ_SPLIT_STORE
+#define GQ_SPLIT_STORE 1
+#endif
 #ifndef GQ_GROUP_M_DEF
 #define GQ_GROUP_M_DEF 8
 #endif
@@ -305,6 +311,19 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
         }
         store_w<F>(rw, lds_b[s], kt * GQ_BK);
     };
+    // part p (0..3) of store_stage: A chunks in parts 0 and 1, the weights in part 2
+    auto store_part = [&](int p, uint32_t kt, int s) {
+        if (p < 2) {
+#pragma unroll
+            for (int i = p * (ACH / 2); i < (p + 1) * (ACH / 2); ++i) {
+                const uint32_t c = t + GQ_THREADS * i;
+                *reinterpret_cast<uint4*>(&lds_a[s][(c >> 3) * GQ_LDS_ROW + (c & 7) * 8]) = ra[i];
+            }
+        } else if (p == 2) {
+            store_w<F>(rw, lds_b[s], kt * GQ_BK);
+        }
+    };
+    static_assert(ACH % 2 == 0, "A chunks split over two steps");
 
     f32x16_t acc[MI][2];
 #pragma unroll
@@ -324,8 +343,8 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
 
     const int frag_row = lane & 31;
     const int frag_k = (lane >> 5) * 8;
-    for (uint32_t kt = 0; kt < KT; ++kt) {
-        const int s = kt & 1;
+    // the 16-deep MFMA steps of stage kt from LDS buffer s; part p of the next stage's LDS stores after step p
+    auto mma_stage = [&](uint32_t kt, int s, bool store_next) {
         const uint16_t* sa = lds_a[s] + (wm * 32 * MI + frag_row) * GQ_LDS_ROW + frag_k;
         const uint16_t* sb = lds_b[s] + (wn * 64 + frag_row) * GQ_LDS_ROW + frag_k;
 #pragma unroll
@@ -342,11 +361,20 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            if (GQ_SPLIT_STORE && store_next) store_part(kk / 16, kt + 1, s ^ 1);
         }
-        if (kt + 1 < KT) store_stage(kt + 1, s ^ 1);
-        if (kt + 2 < KT) load_stage(kt + 2);
+    };
+    // Every stage but the last stores the next one, so the loop body has no branch around the stores and the
+    // scheduler can place the dequantisation between the matrix instructions; the load two stages ahead is
+    // clamped to the last stage (a re-read that nothing uses) for the same reason.
+    for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
+        const int s = kt & 1;
+        mma_stage(kt, s, true);
+        if (!GQ_SPLIT_STORE) store_stage(kt + 1, s ^ 1);
+        load_stage(kt + 2 < KT ? kt + 2 : KT - 1);
         __syncthreads();
     }
+    mma_stage(KT - 1, (KT - 1) & 1, false);
 
     // epilogue: lane holds column (lane % 32) of each 32x32 tile, rows 8(e/4) + 4(lane/32) + e%4
     const uint32_t col_base = n0 + wn * 64 + (lane & 31);
