@@ -95,6 +95,7 @@ struct GemmQ80 {
     static constexpr int BLOCK_VALUES = 32;
     static constexpr int BLOCK_BYTES = 34;
     static constexpr int ALIGN = 2;
+    static constexpr int STORE_STEP = 2;  // MFMA step after which the next stage's A is stored (measured)
     struct Raw {
         uint4 q0, q1;
         uint32_t d;
@@ -142,6 +143,7 @@ struct GemmQ4K {
     static constexpr int BLOCK_VALUES = 256;
     static constexpr int BLOCK_BYTES = 144;
     static constexpr int ALIGN = 16;
+    static constexpr int STORE_STEP = 0;
     struct Raw {
         uint4 hdr, q0, q1;
     };
@@ -204,6 +206,7 @@ struct GemmQ6K {
     static constexpr int BLOCK_VALUES = 256;
     static constexpr int BLOCK_BYTES = 210;
     static constexpr int ALIGN = 2;
+    static constexpr int STORE_STEP = 0;
     struct Raw {
         uint4 ql0, ql1, qh0, qh1;
         uint32_t sc, d;
@@ -311,19 +314,20 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
         }
         store_w<F>(rw, lds_b[s], kt * GQ_BK);
     };
-    // part p (0..3) of store_stage: A chunks in parts 0 and 1, the weights in part 2
+    // part p (0..3) of store_stage: A chunks after MFMA step F::STORE_STEP, the weights after the next (the
+    // later the step, the longer the global loads issued at the end of the stage before have to land)
     auto store_part = [&](int p, uint32_t kt, int s) {
-        if (p < 2) {
+        if (p == F::STORE_STEP) {
 #pragma unroll
-            for (int i = p * (ACH / 2); i < (p + 1) * (ACH / 2); ++i) {
+            for (int i = 0; i < ACH; ++i) {
                 const uint32_t c = t + GQ_THREADS * i;
                 *reinterpret_cast<uint4*>(&lds_a[s][(c >> 3) * GQ_LDS_ROW + (c & 7) * 8]) = ra[i];
             }
-        } else if (p == 2) {
+        } else if (p == F::STORE_STEP + 1) {
             store_w<F>(rw, lds_b[s], kt * GQ_BK);
         }
     };
-    static_assert(ACH % 2 == 0, "A chunks split over two steps");
+    static_assert(F::STORE_STEP >= 0 && F::STORE_STEP + 1 < GQ_BK / 16, "store steps within the stage");
 
     f32x16_t acc[MI][2];
 #pragma unroll
