@@ -393,9 +393,11 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
             for (int e = 0; e < 16; ++e) {
                 const uint32_t row = row_base + i * 32 + (e >> 2) * 8 + (e & 3);
                 if (row < a.m) {
+                    // silu(g) = g / (1 + e^-g) on v_exp_f32 and v_rcp_f32 (e^-g overflowing to inf gives 0)
                     const float g = acc[i][0][e];
+                    const float sg = g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
                     reinterpret_cast<uint16_t*>(a.c)[(size_t)row * a.n_ff + f] =
-                        (uint16_t)f32_to_bf16_bits(g / (1.0f + expf(-g)) * acc[i][1][e]);
+                        (uint16_t)f32_to_bf16_bits(sg * acc[i][1][e]);
                 }
             }
         }
