@@ -869,11 +869,10 @@ def bench_prefill(args) -> int:
     def layer_pass(lw) -> None:
         kernels.rms_norm(h, lw["input_norm"], out=x)
         kernels.gemm(x, lw["qkv"], "q8_0", out=qkv)
-        for b in range(nb):
-            r = slice(b * tl, (b + 1) * tl)
-            kernels.qk_norm_rope_cache(qkv[r, :c.q_dim], qkv[r, c.q_dim:c.q_dim + c.kv_dim],
-                                       qkv[r, c.q_dim + c.kv_dim:], qb[r], kc[b], vc[b], 0,
-                                       q_norm_weight=lw["q_norm"], k_norm_weight=lw["k_norm"], theta=c.rope_theta)
+        # the 8 sequences' q/k norm + RoPE + KV writes in one launch, each into its own cache
+        kernels.qk_norm_rope_cache(qkv[:, :c.q_dim], qkv[:, c.q_dim:c.q_dim + c.kv_dim], qkv[:, c.q_dim + c.kv_dim:],
+                                   qb, kc, vc, 0, q_norm_weight=lw["q_norm"], k_norm_weight=lw["k_norm"],
+                                   theta=c.rope_theta)
         kernels.flash_attn_prefill(qb.view(nb, tl, c.heads, c.head_dim), kc, vc, out=attn, causal=True)
         kernels.gemm(attn.view(m, c.q_dim), lw["o"], "q8_0", out=h, residual=h)
         kernels.rms_norm(h, lw["post_norm"], out=x)

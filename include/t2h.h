@@ -308,6 +308,14 @@ int t2h_qk_norm_rope_cache(const float* q, uint64_t q_row, const float* k, uint6
                            uint64_t v_row, const float* q_norm_w, const float* k_norm_w, float eps, float theta,
                            int32_t start, uint32_t n, uint32_t nh, uint32_t nk, uint32_t d, void* q_out,
                            void* k_cache, void* v_cache, uint32_t s_cap, void* stream);
+/* The same prologue for n_seq sequences of n tokens each, in one launch (a batched prefill): q, k, v and q_out
+ * have n_seq * n rows (sequence s at rows s n ..), each sequence's tokens are at positions start + t, and the
+ * caches hold n_seq consecutive [s_cap, nk, 128] caches, one per sequence.  n_seq = 1 is
+ * t2h_qk_norm_rope_cache.  Replaces the same shaders, run per sequence of a batch. */
+int t2h_qk_norm_rope_cache_seqs(const float* q, uint64_t q_row, const float* k, uint64_t k_row, const float* v,
+                                uint64_t v_row, const float* q_norm_w, const float* k_norm_w, float eps, float theta,
+                                int32_t start, uint32_t n, uint32_t n_seq, uint32_t nh, uint32_t nk, uint32_t d,
+                                void* q_out, void* k_cache, void* v_cache, uint32_t s_cap, void* stream);
 int t2h_flash_attn_segments(const void* q, const void* k, const void* v, void* out, const int32_t* cu_seqlens,
                             uint32_t n_seg, uint32_t batch, uint32_t nh, uint32_t nk, uint32_t t_len, uint32_t d,
                             const int64_t* strides, float scale, void* stream);

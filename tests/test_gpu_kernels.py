@@ -335,3 +335,20 @@ def test_rms_norm_and_swiglu(device):
     u = rng.standard_normal(4096).astype(np.float32)
     s = kernels.swiglu(torch.from_numpy(g).to(device), torch.from_numpy(u).to(device)).float().cpu().numpy()
     assert_close(s, R.silu_mul(g, u), max_abs=2e-2, min_cos=0.9999, what="swiglu")
+
+
+@pytest.mark.parametrize("h,out_bf16", [(1024, False), (4096, True), (5120, True), (8192, False), (3000, True)])
+def test_rms_norm_row_widths(device, h, out_bf16):
+    """fp32 rows of 1024 .. 8192 values in whole KiB-elements take the register-resident kernel (one read of
+    the row, vector loads and stores), other widths the scalar one; both against the oracle's RMSNorm."""
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(h)
+    x = (rng.standard_normal((37, h)) * 4).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(h)).astype(np.float32)
+    out = torch.empty(37, h, dtype=torch.bfloat16 if out_bf16 else torch.float32, device=device)
+    got = kernels.rms_norm(torch.from_numpy(x).to(device), torch.from_numpy(w).to(device), out=out).float().cpu()
+    ref = R.rms_norm(x, w)
+    # fp32 rounding of the sum of squares (~1e-6 relative), then the bf16 rounding of the output (2^-9)
+    tol = (2.0 ** -8 if out_bf16 else 1e-5) * float(np.abs(ref).max())
+    assert_close(got.numpy(), ref, max_abs=tol, min_cos=0.99999, what=f"rmsnorm h={h}")

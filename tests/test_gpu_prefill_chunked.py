@@ -55,6 +55,33 @@ def test_chunk_prologue_matches_decode_prologue_and_oracle(device):
         assert torch.equal(vd[start + t], vc[start + t]), t
 
 
+@pytest.mark.parametrize("nh,nk", [(8, 2), (32, 8)])
+def test_chunk_prologue_batched_equals_per_sequence(device, nh, nk):
+    """n_seq sequences in one launch (q|k|v rows sequence after sequence, one cache per sequence) write the
+    same bits as one call per sequence."""
+    from torch2vk_amd import kernels
+
+    n_seq, n, d, start, s_cap, theta = 3, 37, 128, 100, 256, 1e6
+    rng = np.random.default_rng(nh)
+    qkv = torch.from_numpy(rng.standard_normal((n_seq * n, (nh + 2 * nk) * d)).astype(np.float32)).to(device)
+    qw = torch.from_numpy((1 + 0.1 * rng.standard_normal(d)).astype(np.float32)).to(device)
+    kw = torch.from_numpy((1 + 0.1 * rng.standard_normal(d)).astype(np.float32)).to(device)
+    q, k, v = qkv[:, :nh * d], qkv[:, nh * d:(nh + nk) * d], qkv[:, (nh + nk) * d:]
+    kc = torch.zeros(n_seq, s_cap, nk, d, dtype=torch.bfloat16, device=device)
+    vc = torch.zeros_like(kc)
+    qb = torch.empty(n_seq * n, nh, d, dtype=torch.bfloat16, device=device)
+    kernels.qk_norm_rope_cache(q, k, v, qb, kc, vc, start, q_norm_weight=qw, k_norm_weight=kw, theta=theta)
+    kc1, vc1 = torch.zeros_like(kc), torch.zeros_like(kc)
+    qb1 = torch.empty_like(qb)
+    for sq in range(n_seq):
+        r = slice(sq * n, (sq + 1) * n)
+        kernels.qk_norm_rope_cache(q[r], k[r], v[r], qb1[r], kc1[sq], vc1[sq], start, q_norm_weight=qw,
+                                   k_norm_weight=kw, theta=theta)
+    assert torch.equal(qb, qb1)
+    assert torch.equal(kc, kc1) and torch.equal(vc, vc1)
+    assert not kc[:, :start].any() and not kc[:, start + n:].any()
+
+
 def _setup(cfg, device, seed, std, policy):
     from torch2vk_amd.qwen3.weights import matrix_shapes, synthetic_weights
 

@@ -95,6 +95,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "t2h_omnivoice_token_update_topk": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     "t2h_qk_norm_rope_cache": (_i32, [_vp, _u64, _vp, _u64, _vp, _u64, _vp, _vp, _f32, _f32, ctypes.c_int32, _u32,
                                       _u32, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
+    "t2h_qk_norm_rope_cache_seqs": (_i32, [_vp, _u64, _vp, _u64, _vp, _u64, _vp, _vp, _f32, _f32, ctypes.c_int32,
+                                           _u32, _u32, _u32, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
 }
 
 

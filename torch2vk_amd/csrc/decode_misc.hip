@@ -6,6 +6,8 @@
 //   QWEN3_TOKEN_STORE_EOS_F32            src/models/optimized_qwen3/shaders/qwen3_token_store_eos_f32.py:21-140
 //   RMS_NORM_MUL_F16_F32                 src/models/optimized_qwen3/shaders/rms_norm_mul_f16_f32.py:22-115
 //   SWIGLU_F16                           src/models/optimized_qwen3/shaders/swiglu_f16.py:20-81
+#include <type_traits>
+
 #include "common.h"
 
 namespace t2h {
@@ -195,6 +197,43 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const void* __restrict__ 
     }
 }
 
+// RMSNorm of fp32 rows of NCH * 1024 values: each thread keeps its NCH float4 of the row in registers, so the
+// row is read from memory once, with 16-byte loads, and written with 8- (bf16) or 16-byte (fp32) stores.
+template <int NCH, bool OBF16>
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                            void* __restrict__ outv, uint32_t h, float eps) {
+    __shared__ float red[4];
+    const uint64_t base = (uint64_t)blockIdx.x * h;
+    const float4* xr = reinterpret_cast<const float4*>(x + base);
+    float4 v[NCH];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        v[c] = xr[c * 256 + threadIdx.x];
+        ss = fmaf(v[c].x, v[c].x, ss);
+        ss = fmaf(v[c].y, v[c].y, ss);
+        ss = fmaf(v[c].z, v[c].z, ss);
+        ss = fmaf(v[c].w, v[c].w, ss);
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = red[0] + red[1] + red[2] + red[3];
+    const float inv = 1.0f / sqrtf(total / (float)h + eps);
+    const float4* wr = reinterpret_cast<const float4*>(w);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t i4 = c * 256 + threadIdx.x;
+        const float4 wv = wr[i4];
+        const float4 y = make_float4(v[c].x * inv * wv.x, v[c].y * inv * wv.y, v[c].z * inv * wv.z,
+                                     v[c].w * inv * wv.w);
+        if constexpr (OBF16)
+            reinterpret_cast<uint2*>(outv)[base / 4 + i4] = make_uint2(pack_bf16x2(y.x, y.y), pack_bf16x2(y.z, y.w));
+        else
+            reinterpret_cast<float4*>(outv)[base / 4 + i4] = y;
+    }
+}
+
 template <bool GBF16>
 __global__ void swiglu_kernel(const void* __restrict__ gate, const void* __restrict__ up,
                               uint16_t* __restrict__ out, uint64_t n) {
@@ -269,6 +308,32 @@ extern "C" int t2h_rms_norm(const void* x, int x_dtype, const float* w, void* ou
     hipStream_t s = (hipStream_t)stream;
     const bool xb = x_dtype == T2H_DTYPE_BF16, ob = out_dtype == T2H_DTYPE_BF16;
     if ((!xb && x_dtype != T2H_DTYPE_F32) || (!ob && out_dtype != T2H_DTYPE_F32)) return T2H_ERR_DTYPE;
+    // fp32 rows of 1024..8192 values in whole KiB-elements, 16-byte aligned: the register-resident kernel
+    const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                           reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    if (!xb && aligned && h % 1024 == 0 && h <= 8192) {
+        const uint32_t nch = h / 1024;
+        auto go = [&](auto nc) {
+            constexpr int NC = decltype(nc)::value;
+            const float* xf = static_cast<const float*>(x);
+            if (ob)
+                hipLaunchKernelGGL((rms_norm_rows_kernel<NC, true>), dim3(rows), dim3(256), 0, s, xf, w, out, h, eps);
+            else
+                hipLaunchKernelGGL((rms_norm_rows_kernel<NC, false>), dim3(rows), dim3(256), 0, s, xf, w, out, h, eps);
+        };
+        switch (nch) {
+            case 1: go(std::integral_constant<int, 1>{}); break;
+            case 2: go(std::integral_constant<int, 2>{}); break;
+            case 3: go(std::integral_constant<int, 3>{}); break;
+            case 4: go(std::integral_constant<int, 4>{}); break;
+            case 5: go(std::integral_constant<int, 5>{}); break;
+            case 6: go(std::integral_constant<int, 6>{}); break;
+            case 7: go(std::integral_constant<int, 7>{}); break;
+            default: go(std::integral_constant<int, 8>{}); break;
+        }
+        T2H_LAUNCH_CHECK();
+        return T2H_OK;
+    }
     if (xb && ob) hipLaunchKernelGGL((rms_norm_kernel<true, true>), dim3(rows), dim3(256), 0, s, x, w, out, h, eps);
     else if (xb) hipLaunchKernelGGL((rms_norm_kernel<true, false>), dim3(rows), dim3(256), 0, s, x, w, out, h, eps);
     else if (ob) hipLaunchKernelGGL((rms_norm_kernel<false, true>), dim3(rows), dim3(256), 0, s, x, w, out, h, eps);

@@ -347,7 +347,10 @@ def qk_norm_rope_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out:
                        theta: float = 1e6, eps: float = RMS_EPS) -> torch.Tensor:
     """Prefill chunk prologue: q/k per-head RMSNorm + RoPE at positions start.., q -> q_out bf16 [n, nh, 128],
     k/v -> bf16 rows of one layer's cache [s_cap, nk, 128].  q, k, v fp32 [n, heads * 128] with unit column
-    stride (row views of one wider buffer are fine)."""
+    stride (row views of one wider buffer are fine).
+
+    With caches of shape [n_seq, s_cap, nk, 128], the rows of q, k, v and q_out are n_seq sequences of
+    n / n_seq tokens each, every one at positions start.. of its own cache, in one launch."""
     n = int(q.shape[0])
     for t, name in ((q, "q"), (k, "k"), (v, "v")):
         _check_strided(t, name, torch.float32)
@@ -359,10 +362,20 @@ def qk_norm_rope_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out:
     _check(q_out, "q_out", torch.bfloat16)
     if q_out.numel() != n * nh * 128:
         raise ValueError(f"q_out must hold [{n}, {nh}, 128]")
+    if k_cache.dim() == 4:
+        n_seq = int(k_cache.shape[0])
+        if n_seq == 0 or n % n_seq:
+            raise ValueError(f"{n} rows do not split into {n_seq} sequences")
+    else:
+        n_seq = 1
     for t, name in ((k_cache, "k_cache"), (v_cache, "v_cache")):
         _check(t, name, torch.bfloat16)
-        if t.dim() != 3 or t.shape[1] != nk or t.shape[2] != 128:
-            raise ValueError(f"{name} must be bf16 [s_cap, {nk}, 128], got {tuple(t.shape)}")
+        if t.dim() != k_cache.dim() or t.dim() not in (3, 4) or t.shape[-2] != nk or t.shape[-1] != 128 or \
+                (t.dim() == 4 and t.shape[0] != n_seq):
+            raise ValueError(f"{name} must be bf16 [s_cap, {nk}, 128] or [n_seq, s_cap, {nk}, 128], "
+                             f"got {tuple(t.shape)}")
+    if v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache and v_cache must have the same shape")
     if (q_norm_weight is None) != (k_norm_weight is None):
         raise ValueError("pass both q and k norm weights or neither")
     for t, name in ((q_norm_weight, "q_norm_weight"), (k_norm_weight, "k_norm_weight")):
@@ -370,12 +383,17 @@ def qk_norm_rope_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out:
             _check(t, name, torch.float32, align=4)
             if t.numel() != 128:
                 raise ValueError(f"{name} must have 128 elements")
-    s_cap = int(k_cache.shape[0])
-    if start < 0 or start + n > s_cap:
-        raise ValueError(f"positions {start}..{start + n - 1} exceed the cache capacity {s_cap}")
-    call("t2h_qk_norm_rope_cache", ptr(q), q.stride(0), ptr(k), k.stride(0), ptr(v), v.stride(0), ptr(q_norm_weight),
-         ptr(k_norm_weight), eps, theta, int(start), n, nh, nk, 128, ptr(q_out), ptr(k_cache), ptr(v_cache), s_cap,
-         stream_handle())
+    s_cap = int(k_cache.shape[-3])
+    per_seq = n // n_seq
+    if start < 0 or start + per_seq > s_cap:
+        raise ValueError(f"positions {start}..{start + per_seq - 1} exceed the cache capacity {s_cap}")
+    head = (ptr(q), q.stride(0), ptr(k), k.stride(0), ptr(v), v.stride(0), ptr(q_norm_weight), ptr(k_norm_weight),
+            eps, theta, int(start), per_seq)
+    tail = (nh, nk, 128, ptr(q_out), ptr(k_cache), ptr(v_cache), s_cap, stream_handle())
+    if k_cache.dim() == 3:
+        call("t2h_qk_norm_rope_cache", *head, *tail)
+    else:
+        call("t2h_qk_norm_rope_cache_seqs", *head, n_seq, *tail)
     return q_out
 
 
