@@ -48,11 +48,13 @@ def _ws_ll16(dec, offset, n):
     return dec.layers_ws[offset:offset + 4 * n].view(torch.int16).view(n, 2)[:, 0].contiguous().view(torch.bfloat16)
 
 
-@pytest.mark.parametrize("pos", [0, 5, 300])
+@pytest.mark.parametrize("pos", [0, 5, 255, 256, 300])
 def test_persistent_layer_matches_per_op(device, setup_8b2, pos):
     """One layer at one position on random caches: the Q|K|V projections are bit-identical to the
     per-op GEMV (same lane mapping and reduction order); the attention output differs at most by
-    bf16 rounding of a differently ordered fp32 sum; h by what that rounding does downstream."""
+    bf16 rounding of a differently ordered fp32 sum; h by what that rounding does downstream.
+    Positions 0, 5 and 255 (up to 256 keys) take the one-block-per-kv-head attention without a merge
+    phase; 256 and 300 spread the keys over 32 blocks per kv head and merge."""
     from torch2vk_amd.qwen3.model import Qwen3Decoder
 
     cfg, w, _ = setup_8b2

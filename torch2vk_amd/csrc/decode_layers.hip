@@ -710,18 +710,17 @@ __device__ __forceinline__ void dl_norm_rope(float x0, float x1, float w0, float
     }
 }
 
-// Block (kv head kvh, slot bs): wave w covers positions [p0, p0 + span) of the
-// first L; the block's (max, sum, output) per q head goes to part[kvh][bs].
+// Block (kv head kvh, slot bs): the wave covers positions [p0, p0 + rows).  The
+// block's (max, sum, output) per q head goes to part[kvh][bs]; with `direct` (the
+// block covers every position of its kv head) the normalised output goes to the
+// attention output words instead, with epoch e_out either way.
 template <class S, class Hook = DlNoHook>
 __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP, S::pv_mfma>& sm, const DlArgs& a,
-                                              const uint64_t* lp, int kvh, int bs, int pos, int L, float cs,
-                                              float sn, uint32_t e_qkv, uint32_t e_part, uint32_t site,
-                                              uint64_t* tr, Hook after_ready = Hook()) {
+                                              const uint64_t* lp, int kvh, int bs, int p0, int rows, bool direct,
+                                              int pos, float cs, float sn, uint32_t e_qkv, uint32_t e_out,
+                                              uint32_t site, uint64_t* tr, Hook after_ready = Hook()) {
     constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int span = dl_att_span(L);
-    const int p0 = (bs * DL_WAVES + wave) * span;
-    const int rows = dl_att_rows(L, p0, span);
     const int s_cap = (int)a.s_cap;
     const bool has_new = pos < s_cap && pos >= p0 && pos < p0 + rows;
     const int rnew = pos - p0;
@@ -959,12 +958,18 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
             r0 = fmaf(f, ov.x, r0);
             r1 = fmaf(f, ov.y, r1);
         }
+        if (direct) {
+            const float inv = 1.0f / l;
+            ll_store(reinterpret_cast<uint64_t*>(a.attn_ll) + ((kvh * GROUP + gg) * DL_D) / 2 + dl,
+                     ll_pack16x2(r0 * inv, r1 * inv, e_out));
+            continue;
+        }
         uint64_t* pg = pb + gg * (2 + DL_D);
-        ll_put32(pg + 2 + 2 * dl, r0, e_part);
-        ll_put32(pg + 3 + 2 * dl, r1, e_part);
+        ll_put32(pg + 2 + 2 * dl, r0, e_out);
+        ll_put32(pg + 3 + 2 * dl, r1, e_out);
         if (dl == 0) {
-            ll_put32(pg, M, e_part);
-            ll_put32(pg + 1, l, e_part);
+            ll_put32(pg, M, e_out);
+            ll_put32(pg + 1, l, e_out);
         }
     }
 }
@@ -1091,9 +1096,14 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         r.n_rows = S::HID;
         return r;
     };
-    const int span = dl_att_span(L);
-    const int att_p0 = (bs * DL_WAVES + wave) * span;
-    const int att_rows = dl_att_rows(L, att_p0, span);
+    // Up to DL_WAVES * DL_ATT_POS positions, block bs = 0 of each kv head covers them all (32 per wave) and
+    // writes the normalised output itself: no partials, no merge phase and no hand-off into it.  Longer, the
+    // kv head's positions are spread over its DL_ATT_SLOTS blocks and merged per q head.
+    const bool att_direct = L <= DL_WAVES * DL_ATT_POS;
+    const bool att_block = !att_direct || bs == 0;
+    const int span = att_direct ? DL_ATT_POS : dl_att_span(L);
+    const int att_p0 = att_direct ? wave * DL_ATT_POS : (bs * DL_WAVES + wave) * span;
+    const int att_rows = att_block ? dl_att_rows(L, att_p0, span) : 0;
     // phases with fewer units than waves spread them over the blocks
     constexpr bool qkv_sp = S::QKV_ROWS / DlUnit<S::HSB, 1>::RPW < DL_NW;
     constexpr bool o_sp = S::HID / DlUnit<S::QSB, 1>::RPW < DL_NW;
@@ -1153,13 +1163,19 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
             uint64_t lp[DL_LAYER_PTRS];
 #pragma unroll
             for (int i = 0; i < DL_LAYER_PTRS; ++i) lp[i] = layer_ptr(layer, i);
-            dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, pos, L, rope_cs, rope_sn, e_qkv, e_part, lsite, tr, [&] {
-                if constexpr (o_early > 0) dl_issue_pre<S::QSB, 1, S::o_u, o_early, o_sp>(uo, o_rows(layer));
-            });
+            if (att_block) {
+                dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, att_p0, att_rows, att_direct, pos, rope_cs, rope_sn,
+                                 e_qkv, att_direct ? e_attn : e_part, lsite, tr, [&] {
+                                     if constexpr (o_early > 0)
+                                         dl_issue_pre<S::QSB, 1, S::o_u, o_early, o_sp>(uo, o_rows(layer));
+                                 });
+            } else if constexpr (o_early > 0) {
+                dl_issue_pre<S::QSB, 1, S::o_u, o_early, o_sp>(uo, o_rows(layer));
+            }
             dl_stamp(tr, DL_TR_END);
         }
         // ---- attention merge (blocks 0..NH-1, one q head each)
-        if (blockIdx.x < S::NH) {
+        if (!att_direct && blockIdx.x < S::NH) {
             uint64_t* tr = trp(2);
             dl_stamp(tr, DL_TR_BEGIN);
             dl_merge_phase<S>(sm.at, a, blockIdx.x, e_part, e_attn, lsite, tr);
