@@ -147,7 +147,7 @@ __device__ __forceinline__ int2 fa_key_range(const FaArgs& a, int q) {
 }
 
 template <int D, bool CAUSAL, bool MASK, bool SEG>
-__global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void fa_prefill_kernel(const FaArgs a) {
+__global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(MASK ? 1 : 2))) void fa_prefill_kernel(const FaArgs a) {
     constexpr int KROW = D + 8;                                // LDS K row length (bf16)
     constexpr int DS = D / 16;                                 // k-steps of S^T
     constexpr int DB = D / 32;                                 // 32-dim blocks of O^T

@@ -95,7 +95,8 @@ struct GemmQ80 {
     static constexpr int BLOCK_VALUES = 32;
     static constexpr int BLOCK_BYTES = 34;
     static constexpr int ALIGN = 2;
-    static constexpr int STORE_STEP = 2;  // MFMA step after which the next stage's A is stored (measured)
+    // MFMA step after which the next stage's A is stored, at 128- and at 256-row tiles (measured)
+    static constexpr int STORE_STEP = 2, STORE_STEP_256 = 2;
     struct Raw {
         uint4 q0, q1;
         uint32_t d;
@@ -143,7 +144,7 @@ struct GemmQ4K {
     static constexpr int BLOCK_VALUES = 256;
     static constexpr int BLOCK_BYTES = 144;
     static constexpr int ALIGN = 16;
-    static constexpr int STORE_STEP = 0;
+    static constexpr int STORE_STEP = 0, STORE_STEP_256 = 0;
     struct Raw {
         uint4 hdr, q0, q1;
     };
@@ -206,7 +207,7 @@ struct GemmQ6K {
     static constexpr int BLOCK_VALUES = 256;
     static constexpr int BLOCK_BYTES = 210;
     static constexpr int ALIGN = 2;
-    static constexpr int STORE_STEP = 0;
+    static constexpr int STORE_STEP = 0, STORE_STEP_256 = 1;  // at 256 rows, 0 spills registers
     struct Raw {
         uint4 ql0, ql1, qh0, qh1;
         uint32_t sc, d;
@@ -314,20 +315,21 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
         }
         store_w<F>(rw, lds_b[s], kt * GQ_BK);
     };
-    // part p (0..3) of store_stage: A chunks after MFMA step F::STORE_STEP, the weights after the next (the
-    // later the step, the longer the global loads issued at the end of the stage before have to land)
+    // part p (0..3) of store_stage: A chunks after MFMA step SS, the weights after the next (the later the
+    // step, the longer the global loads issued at the end of the stage before have to land)
+    constexpr int SS = MI == 4 ? F::STORE_STEP_256 : F::STORE_STEP;
     auto store_part = [&](int p, uint32_t kt, int s) {
-        if (p == F::STORE_STEP) {
+        if (p == SS) {
 #pragma unroll
             for (int i = 0; i < ACH; ++i) {
                 const uint32_t c = t + GQ_THREADS * i;
                 *reinterpret_cast<uint4*>(&lds_a[s][(c >> 3) * GQ_LDS_ROW + (c & 7) * 8]) = ra[i];
             }
-        } else if (p == F::STORE_STEP + 1) {
+        } else if (p == SS + 1) {
             store_w<F>(rw, lds_b[s], kt * GQ_BK);
         }
     };
-    static_assert(F::STORE_STEP >= 0 && F::STORE_STEP + 1 < GQ_BK / 16, "store steps within the stage");
+    static_assert(SS >= 0 && SS + 1 < GQ_BK / 16, "store steps within the stage");
 
     f32x16_t acc[MI][2];
 #pragma unroll
