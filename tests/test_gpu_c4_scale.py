@@ -111,3 +111,33 @@ def test_flash_attention_causal_8x2048(device):
         for tq in rows:
             ref = R.attention_ref(qc[bi, tq:tq + 1], kc[bi, :tq + 1], vc[bi, :tq + 1])
             assert_close(oc[bi, tq:tq + 1], ref, max_abs=2e-2, min_cos=0.999, what=f"sequence {bi} query {tq}")
+
+
+@pytest.mark.parametrize("wtype", ["q4_k", "q6_k"])
+def test_gemm_k_quants_256_row_tiles(device, wtype):
+    """Q4_K and Q6_K weights on the 256 x 256-tile kernel (M 4096 x N 16384: 1024 tiles, the first grid that
+    takes it), whose stage loop stores the next stage at a per-format MFMA step; sampled whole rows and columns
+    against x . bf16(deq W)^T in fp64."""
+    from torch2vk_amd import kernels
+
+    m, k, n = 4096, 1024, 16384
+    print(f"gemm {wtype} M={m} K={k} N={n} (1024 tiles of 256 x 256)", flush=True)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(6)
+    x = torch.randn(m, k, generator=gen, device=device).to(torch.bfloat16)
+    w = kernels.quantize(torch.randn(n, k, generator=gen, device=device).mul_(0.02), wtype)
+    y = kernels.gemm(x, w, wtype, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(7)
+    rows = np.unique(np.concatenate([[0, 255, 256, 2047, 2048, m - 1], rng.integers(0, m, 26)]))
+    cols = np.unique(np.concatenate([[0, 255, 256, 8191, 8192, n - 1], rng.integers(0, n, 58)]))
+    got_r = y[torch.from_numpy(rows).to(device)].cpu().numpy()
+    got_c = y[:, torch.from_numpy(cols).to(device)].cpu().numpy()
+    del y
+    wd = R.bf16_round(getattr(oracle, f"dequant_{wtype}")(w.cpu().numpy(), k)).astype(np.float64)
+    xall = x.float().cpu().numpy().astype(np.float64)
+    ref_r = xall[rows] @ wd.T
+    ref_c = xall @ wd[cols].T
+    scale = max(np.abs(ref_r).max(), np.abs(ref_c).max())
+    assert_close(got_r, ref_r, max_abs=1e-5 * scale + 1e-6, min_cos=0.999999, what="sampled rows")
+    assert_close(got_c, ref_c, max_abs=1e-5 * scale + 1e-6, min_cos=0.999999, what="sampled columns")
