@@ -215,12 +215,14 @@ int t2h_attn_decode(const float* q, const float* k_new, const float* v_new, cons
  * with no grid barrier (no host sync, graph-capturable).  Calls on one
  * workspace must not overlap in time.
  * Built for the Qwen3-8B shape (hidden 4096, mlp 12288, 32/8 heads) and the Qwen3-0.6B shape (hidden
- * 1024, mlp 3072, 16/8 heads), d 128, uniform Q4_K weights, bf16 KV caches [s_cap, 8, 128] with
- * s_cap <= 8192, n_layers <= 64 (otherwise T2H_ERR_UNSUPPORTED; so is a GPU that cannot hold 256 blocks).
- * layer_table: device int64 [n_layers][13] pointers in the order
+ * 1024, mlp 3072, 16/8 heads), d 128, Q4_K weights with v and down each Q4_K or Q6_K per layer (the uniform
+ * and Q4_K_M policies), bf16 KV caches [s_cap, 8, 128] with s_cap <= 8192, n_layers <= 64 (otherwise
+ * T2H_ERR_UNSUPPORTED; so is a GPU that cannot hold 256 blocks).
+ * layer_table: device int64 [n_layers][14]: pointers in the order
  *   wq, wk, wv, wo, w_gate, w_up, w_down, input_norm, post_norm, q_norm, k_norm, k_cache, v_cache,
- * where wq..wv must be one allocation of q_dim + 2 kv_dim stacked rows (wk = wq + q_dim rows, wv = wk +
- * kv_dim rows).
+ * then the layer's weight types: bit 0 set = wv is Q6_K, bit 1 set = w_down is Q6_K.  wq and wk must be one
+ * allocation of q_dim + kv_dim stacked rows (wk = wq + q_dim rows); a Q4_K wv must continue it (wv = wk +
+ * kv_dim rows), a Q6_K wv is an allocation of its own.
  * workspace: t2h_qwen3_decode_layers_workspace_bytes() bytes, 256-B aligned,
  * zero-filled once before its first use (it holds a launch counter that later
  * calls advance).  *status (device) is set to 0x80000000 | layer << 8 | phase

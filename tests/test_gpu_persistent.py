@@ -234,18 +234,19 @@ def test_persistent_long_kv_decode_matches_oracle(device, setup_8b_long):
     print(stats, flush=True)
 
 
-def test_persistent_0_6b_full_depth_matches_oracle(device):
+@pytest.mark.parametrize("policy", ["uniform", "q4_k_m"])
+def test_persistent_0_6b_full_depth_matches_oracle(device, policy):
     """The whole 28-layer Qwen3-0.6B decoder (vocab 151936) in the persistent kernel: a 128-token random prompt
     fed one launch per position, then 32 greedy tokens in HIP graphs; status clear after all 160 launches and
     every token against the CPU oracle.  This depth is where residual hold threads once polled rows owned by
-    another block and a bounded wait gave up."""
+    another block and a bounded wait gave up.  Q4_K_M: 14 of the 28 layers have Q6_K v and down rows."""
     from torch2vk_amd.qwen3.config import QWEN3_0_6B
     from torch2vk_amd.qwen3.model import Qwen3Decoder
     from torch2vk_amd.qwen3.weights import matrix_shapes, synthetic_weights
 
     cfg = QWEN3_0_6B
-    print("persistent 0.6B, 28 layers: weights", flush=True)
-    w = synthetic_weights(cfg, device=device, seed=0, std=0.02, norm_std=0.1)
+    print(f"persistent 0.6B, 28 layers, {policy}: weights", flush=True)
+    w = synthetic_weights(cfg, device=device, seed=0, std=0.02, norm_std=0.1, policy=policy)
     prompt = np.random.default_rng(0).integers(0, cfg.vocab, 128).tolist()
     dec = Qwen3Decoder(w, max_positions=256, max_new_tokens=40, persistent=True)
     assert dec.persistent
@@ -281,3 +282,95 @@ def test_persistent_0_6b_full_depth_matches_oracle(device):
     # near ties: two logits each within that tolerance
     stats = check_greedy_tokens(shape, dense, prompt, toks, tie_tol_rms=6e-2)
     print(stats, flush=True)
+
+
+# ------------------------------------------------------------------------------------------------------
+# The Q4_K_M policy on the persistent kernel: with 2 layers, layer 1 is a more-bits layer (Q6_K v and down
+# rows) and layer 0 is all Q4_K.
+
+
+@pytest.fixture(scope="module", params=["8b", "0.6b"])
+def setup_km(device, request):
+    from torch2vk_amd.qwen3.config import QWEN3_0_6B, QWEN3_8B
+    from torch2vk_amd.qwen3.weights import synthetic_weights
+
+    base = QWEN3_8B if request.param == "8b" else QWEN3_0_6B
+    cfg = replace(base, layers=2, vocab=4096, eos_token_ids=(4095,))
+    w = synthetic_weights(cfg, device=device, seed=9, std=0.02, norm_std=0.1, policy="q4_k_m")
+    assert (w.types["layers.0.v"], w.types["layers.0.down"]) == ("q4_k", "q4_k")
+    assert (w.types["layers.1.v"], w.types["layers.1.down"]) == ("q6_k", "q6_k")
+    shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
+                       head_dim=cfg.head_dim, mlp=cfg.mlp, vocab=cfg.vocab, rope_theta=cfg.rope_theta)
+    return cfg, w, shape
+
+
+@pytest.mark.parametrize("layer,pos", [(1, 5), (1, 300), (0, 300)])
+def test_persistent_q4_k_m_layer_matches_per_op(device, setup_km, layer, pos):
+    """One Q4_K_M layer at one position: the q and k rows are bit-identical to the per-op Q4_K GEMV; a Q6_K
+    v (layer 1) agrees with the per-op Q6_K GEMV to fp32 rounding (the persistent kernel runs x as fp16 with
+    the offset 1056, the per-op kernel as bf16 with 160: both exact products of the same bf16 x); the
+    attention output and h then as in test_persistent_layer_matches_per_op, through a Q6_K down at layer 1."""
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg, w, _ = setup_km
+    print(f"persistent vs per-op, Q4_K_M layer {layer} at pos {pos}", flush=True)
+    a = Qwen3Decoder(w, max_positions=512, max_new_tokens=4, persistent=True)
+    b = Qwen3Decoder(w, max_positions=512, max_new_tokens=4, persistent=False)
+    assert a.persistent and not b.persistent
+    assert int(a.layer_table[1, 13]) == 3 and int(a.layer_table[0, 13]) == 0
+    g = torch.Generator(device=device)
+    g.manual_seed(11 + pos + layer)
+    kc = torch.randn(a.k_cache.shape, generator=g, device=device).to(torch.bfloat16)
+    vc = torch.randn(a.v_cache.shape, generator=g, device=device).to(torch.bfloat16)
+    h0 = torch.randn(cfg.hidden, generator=g, device=device)
+    for d in (a, b):
+        d.k_cache.copy_(kc)
+        d.v_cache.copy_(vc)
+        d.h.copy_(h0)
+        d.position.fill_(pos)
+    a.layer_table = a.layer_table[layer:layer + 1].contiguous()
+    a.run_decode_layers()
+    b.run_decode_layer(layer)
+    torch.cuda.synchronize()
+    a.check_status()
+    qkv = _ws_ll32(a, WS_QKV, cfg.q_dim + 2 * cfg.kv_dim)
+    qk = cfg.q_dim + cfg.kv_dim
+    torch.testing.assert_close(qkv[:qk], torch.cat([b.q, b.k]), rtol=0, atol=0)
+    torch.testing.assert_close(a.k_cache[layer], b.k_cache[layer], rtol=0, atol=0)
+    vmax = b.v.abs().max().item()
+    if layer == 1:
+        verr = (qkv[qk:] - b.v).abs().max().item()
+        print(f"Q6_K v max-abs diff {verr:.3e} (max {vmax:.3e})", flush=True)
+        assert verr <= 1e-5 * vmax
+        # the new V row: one bf16 rounding of values that agree to ~1e-5, so at most one bf16 step apart
+        vr_a, vr_b = a.v_cache[layer, pos].float(), b.v_cache[layer, pos].float()
+        assert ((vr_a - vr_b).abs() <= 2 ** -7 * vr_b.abs() + 1e-30).all()
+    else:
+        torch.testing.assert_close(qkv[qk:], b.v, rtol=0, atol=0)
+        torch.testing.assert_close(a.v_cache[layer], b.v_cache[layer], rtol=0, atol=0)
+    attn = _ws_ll16(a, _ws_attn(cfg), cfg.q_dim).float()
+    ref = b.attn.float()
+    assert (attn - ref).abs().max().item() <= 2 ** -7 * ref.abs().max().item()
+    herr = (a.h - b.h).abs().max().item()
+    print(f"h max-abs diff {herr:.3e} (max {b.h.abs().max().item():.3e})", flush=True)
+    assert herr <= 3e-3 * b.h.abs().max().item(), herr
+
+
+def test_persistent_q4_k_m_decode_matches_oracle(device, setup_km):
+    """Greedy decode with the persistent kernel on Q4_K_M weights (a Q4_K layer and a Q6_K v/down layer):
+    prompt and 10 tokens through graph replay, every token against the CPU oracle."""
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+    from torch2vk_amd.qwen3.weights import matrix_shapes
+
+    cfg, w, shape = setup_km
+    dense = dense_weights({k: v.cpu().numpy() for k, v in w.packed.items()}, w.types,
+                          {k: v.cpu().numpy() for k, v in w.norms.items()}, matrix_shapes(cfg))
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab, 5).tolist()
+    dec = Qwen3Decoder(w, max_positions=128, max_new_tokens=16, persistent=True)
+    assert dec.persistent
+    dec.stop_on_eos = False
+    toks = dec.generate(torch.tensor(prompt), 10, steps_per_graph=4, use_graph=True)
+    dec.check_status()
+    print(f"persistent Q4_K_M {cfg.name}-shape decode: {toks}", flush=True)
+    tie = 2e-3 if cfg.hidden == 4096 else 5e-3
+    print(check_greedy_tokens(shape, dense, prompt, toks, tie_tol=tie))

@@ -45,6 +45,7 @@
 // ordinary loads.
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "q4k_device.h"
 
@@ -75,36 +76,29 @@ constexpr uint32_t DL_SPIN_LIMIT = 1u << DL_SPIN_LOG2;
 #ifndef DL_PRE_DOWN
 #define DL_PRE_DOWN 1
 #endif   // polls before a consumer gives up (~16 ms)
-// Units of the next phase issued early, so that the weight stream runs on across a phase boundary: o_proj units
-// once the attention phase has its q (they stream during the attention arithmetic and the merge); gate|up,
-// down and the next layer's Q|K|V units (with its attention K/V rows) right after the phase before has issued
-// its last unit.  A phase's input wait then queues behind fewer loads of its own.
+// o_proj units issued once the attention phase has its q, so that they stream during the attention
+// arithmetic and the merge (0: when the o_proj phase begins, like every other phase's units).
 #ifndef DL_O_EARLY
 #define DL_O_EARLY 2
-#endif
-#ifndef DL_GU_EARLY
-#define DL_GU_EARLY 0
-#endif
-#ifndef DL_DN_EARLY
-#define DL_DN_EARLY 0
-#endif
-#ifndef DL_QKV_EARLY
-#define DL_QKV_EARLY 0
 #endif
 
 struct DlNoHook {
     __device__ void operator()() const {}
 };
 
-// Per-layer pointer table (device memory, DL_LAYER_PTRS uint64 per layer).
-// DL_WQ points at the q, k and v rows stacked contiguously (q_dim + 2 kv_dim
-// rows); DL_WK and DL_WV must point inside it at rows q_dim and q_dim + kv_dim
-// (checked by the host).
+// Per-layer table (device memory, DL_LAYER_PTRS uint64 per layer): the
+// pointers, then the layer's weight types (DL_WTYPES bits).  DL_WQ points at
+// the q and k rows stacked contiguously (q_dim + kv_dim rows), followed by the
+// v rows when v is Q4_K too; DL_WK must point at row q_dim of it, and so must
+// DL_WV at row q_dim + kv_dim when v is Q4_K (checked by the host).  A Q6_K v
+// (DL_WT_V_Q6) or down (DL_WT_DOWN_Q6) is an allocation of its own: the
+// Q4_K_M policy's more-bits layers.
 enum DlLayerPtr {
     DL_WQ = 0, DL_WK, DL_WV, DL_WO, DL_WGATE, DL_WUP, DL_WDOWN,
-    DL_IN_NORM, DL_POST_NORM, DL_Q_NORM, DL_K_NORM, DL_K_CACHE, DL_V_CACHE,
+    DL_IN_NORM, DL_POST_NORM, DL_Q_NORM, DL_K_NORM, DL_K_CACHE, DL_V_CACHE, DL_WTYPES,
     DL_LAYER_PTRS
 };
+enum DlWeightTypes : uint32_t { DL_WT_V_Q6 = 1u, DL_WT_DOWN_Q6 = 2u };
 constexpr uint32_t DL_MAX_LAYERS = 64;  // layers per launch (the table is held in LDS)
 
 struct DlArgs {
@@ -294,6 +288,7 @@ union DlShared {
     struct {
         uint32_t xp[xp_words(S::KMAX)];
         float xsum[S::KMAX / 32];
+        float xsum16[S::KMAX / 16];  // sums of 16 values: the Q6_K units' scale groups
         float red[DL_WAVES];
         float hold[DL_WAVES * DL_HOLD];  // residual epilogue: the old h of the block's rows [wave][row]
     } g;
@@ -303,9 +298,16 @@ union DlShared {
 // ------------------------------------------------------------ GEMV phase ----
 
 // Weights of one unit, K = NSB*256: RPW consecutive rows of each of NG row
-// groups, streamed in NIT steps of 16 superblocks; per step a lane holds the
-// header and the two 16-B nibble chunks of superblock (step * 16 + lane / 4) of
-// the unit (row = that / NSB).  RPW = 1 for rows of 16, 32, 48 superblocks.
+// groups, streamed in NIT steps of 16 superblocks; per step a lane holds a
+// quarter of superblock (step * 16 + lane / 4) of the unit (row = that / NSB).
+// RPW = 1 for rows of 16, 32, 48 superblocks.
+//   Q4_K: the header and the lane's two 16-B nibble chunks (hdr, q0, q1).
+//   Q6_K: piece lane % 4 (half h = piece / 2, values l0 = 16 (piece % 2) ..
+//         l0 + 15 of each of the half's 4 parts of 32): the 16-B ql chunks of
+//         parts 0|2 and 1|3 (hdr, q0), the 16-B qh chunk (q1), the half's 8
+//         int8 scales (sc) and d (d).
+// The fields a format does not use are never touched, so they take no
+// registers.
 template <int NSB, int NG>
 struct DlUnit {
     static constexpr int RPW = 16 / cgcd(NSB, 16);
@@ -313,7 +315,14 @@ struct DlUnit {
     uint4 hdr[NG][NIT];
     uint4 q0[NG][NIT];
     uint4 q1[NG][NIT];
+    uint2 sc[NG][NIT];
+    uint32_t d[NG][NIT];
 };
+
+// Unit formats of a GEMV phase: every unit Q4_K; Q4_K with the rows from
+// DlRows::n_rows4 on in Q6_K (each wave's last unit slot may be one of those);
+// every unit Q6_K.
+enum DlFmt { DL_FMT_Q4 = 0, DL_FMT_Q4_TAIL6 = 1, DL_FMT_Q6 = 2 };
 
 // Unit i of wave `wave` of this block.  Block-major when every wave has a unit;
 // SPREAD (fewer units than waves): across the blocks first, so that every CU
@@ -327,12 +336,17 @@ __device__ __forceinline__ uint32_t dl_unit(uint32_t wave, uint32_t i) {
 struct DlRows {
     const uint8_t* w0;  // rows of the matrix (QKV: q, k and v rows stacked in one allocation)
     const uint8_t* w1;  // NG == 2: the second matrix (up)
-    uint32_t n_rows;
+    uint32_t n_rows;    // output rows of the phase
+    uint32_t n_rows4;   // DL_FMT_Q4_TAIL6: rows 0 .. n_rows4 - 1 are w0's (Q4_K), the rest w6's rows (Q6_K)
+    const uint8_t* w6;
 };
 
-template <int NSB, int NG>
-__device__ __forceinline__ void dl_issue_unit(DlUnit<NSB, NG>& u, const DlRows& r, uint32_t unit) {
-    constexpr int ROW_BYTES = NSB * 144;
+// Issue unit `unit` of a matrix of n_rows rows (Q4_K, or Q6_K with Q6).
+template <bool Q6, int NSB, int NG>
+__device__ __forceinline__ void dl_issue_unit(DlUnit<NSB, NG>& u, const uint8_t* w0, const uint8_t* w1,
+                                              uint32_t n_rows, uint32_t unit) {
+    constexpr int BLK = Q6 ? 210 : 144;
+    constexpr int ROW_BYTES = NSB * BLK;
     constexpr int RPW = DlUnit<NSB, NG>::RPW;
     const int lane = dl_tid() & 63;
     const int sbo = lane >> 2;
@@ -343,12 +357,21 @@ __device__ __forceinline__ void dl_issue_unit(DlUnit<NSB, NG>& u, const DlRows& 
         for (int it = 0; it < DlUnit<NSB, NG>::NIT; ++it) {
             const int sbu = it * 16 + sbo;  // superblock of the unit
             uint32_t row = unit * RPW + (RPW == 1 ? 0 : sbu / NSB);
-            row = row < r.n_rows ? row : r.n_rows - 1;
-            const uint8_t* p = (gi == 0 ? r.w0 : r.w1) + (size_t)row * ROW_BYTES +
-                               (size_t)(RPW == 1 ? sbu : sbu % NSB) * 144;
-            u.hdr[gi][it] = load_u4(p);
-            u.q0[gi][it] = load_u4(p + 16 + g * 32);
-            u.q1[gi][it] = load_u4(p + 32 + g * 32);
+            row = row < n_rows ? row : n_rows - 1;
+            const uint8_t* p = (gi == 0 ? w0 : w1) + (size_t)row * ROW_BYTES + (size_t)(RPW == 1 ? sbu : sbu % NSB) * BLK;
+            if constexpr (Q6) {
+                // superblocks are 210 B, so only 2-byte aligned: the hardware's unaligned access
+                const int h = g >> 1, l0 = (g & 1) * 16;
+                u.hdr[gi][it] = load_u4_ua(p + 64 * h + l0);
+                u.q0[gi][it] = load_u4_ua(p + 64 * h + 32 + l0);
+                u.q1[gi][it] = load_u4_ua(p + 128 + 32 * h + l0);
+                u.sc[gi][it] = load_u2_ua(p + 192 + 8 * h);
+                u.d[gi][it] = load_u16(p + 208);
+            } else {
+                u.hdr[gi][it] = load_u4(p);
+                u.q0[gi][it] = load_u4(p + 16 + g * 32);
+                u.q1[gi][it] = load_u4(p + 32 + g * 32);
+            }
         }
     }
 }
@@ -390,7 +413,8 @@ __device__ __forceinline__ uint32_t dl_hold_row(const DlHold& hd, int t) {
 // x = bf16(h * rsqrt(mean(h^2) + eps) * w); otherwise x = bf16(src).  The
 // residual values of the block's rows (hd) are awaited with the same loads.
 template <int K, bool RMSNORM>
-__device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red, int src_kind, const void* src,
+__device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* xsum16, float* red, int src_kind,
+                                           const void* src,
                                            uint32_t e, const float* norm_w, float eps, const DlHold& hd,
                                            uint32_t* status, uint32_t site) {
     // PT float4 per thread; when K does not fill the block, the threads past
@@ -475,7 +499,7 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
             if (!valid(j)) continue;
             const int k = (j * DL_THREADS + tid) * 4;
             stage_x4(xp, xsum, k, bf16_round(hv[j].x * inv * wv[j].x), bf16_round(hv[j].y * inv * wv[j].y),
-                     bf16_round(hv[j].z * inv * wv[j].z), bf16_round(hv[j].w * inv * wv[j].w));
+                     bf16_round(hv[j].z * inv * wv[j].z), bf16_round(hv[j].w * inv * wv[j].w), xsum16);
         }
     } else {
 #pragma unroll
@@ -483,7 +507,7 @@ __device__ __forceinline__ void dl_stage_x(uint32_t* xp, float* xsum, float* red
             if (!valid(j)) continue;
             const int k = (j * DL_THREADS + tid) * 4;
             stage_x4(xp, xsum, k, bf16_round(hv[j].x), bf16_round(hv[j].y), bf16_round(hv[j].z),
-                     bf16_round(hv[j].w));
+                     bf16_round(hv[j].w), xsum16);
         }
     }
     __syncthreads();
@@ -510,6 +534,86 @@ __device__ __forceinline__ void dl_dot_unit(const DlUnit<NSB, NG>& u, const uint
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
             const float c = q4k_lane_dot(u.hdr[gi][it], u.q0[gi][it], u.q1[gi][it], xs, lc);
+            if constexpr (RPW == 1) {
+                acc[gi][0] = it == 0 ? c : acc[gi][0] + c;
+            } else {
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const float v = sbu / NSB == r ? c : 0.0f;
+                    acc[gi][r] = it == 0 ? v : acc[gi][r] + v;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) res[gi][r] = wave_sum(acc[gi][r]);
+}
+
+// The same for a Q6_K unit.  A lane's piece is 16 values of each of 4 parts
+// (values 32 p + l0 .. + 15 of half h): each run is 8 pair words of the staged
+// x.  Codes q (6 bits) become fp16 1024 + q with one and-or, so
+//   sum x (q - 32) = sum x (1024 + q) - 1056 sum x,
+// the second sum from the staged 16-value sums.
+// Q6_K: value(128h + 32p + l) = d * sc[8h + 2p + l/16] * (q - 32),
+//   q = (ql[64h + 32(p&1) + l] >> 4(p>>1) & 15) | ((qh[32h + l] >> 2p) & 3) << 4.
+template <int NSB, int NG>
+__device__ __forceinline__ void dl_dot_unit6(const DlUnit<NSB, NG>& u, const uint32_t* xp, const float* xsum16,
+                                             float (&res)[NG][DlUnit<NSB, NG>::RPW]) {
+    constexpr int NIT = DlUnit<NSB, NG>::NIT;
+    constexpr int RPW = DlUnit<NSB, NG>::RPW;
+    constexpr uint32_t B = 0x64006400u, LO = 0x000f000fu, HI = 0x00300030u;
+    const int lane = dl_tid() & 63;
+    const int sbo = lane >> 2;
+    const int g = lane & 3;
+    const int h = g >> 1, l0 = (g & 1) * 16, sh = (g & 1) * 8;
+    float acc[NG][RPW];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int sbu = it * 16 + sbo;
+        const int e0 = (RPW == 1 ? sbu : sbu % NSB) * 256 + 128 * h + l0;  // first value of part 0
+        uint32_t x[4][8];
+        float xs[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t* xw = xp + xp_word(e0 + 32 * p);
+            const uint4 a = *reinterpret_cast<const uint4*>(xw);
+            const uint4 b = *reinterpret_cast<const uint4*>(xw + 4);
+            x[p][0] = a.x; x[p][1] = a.y; x[p][2] = a.z; x[p][3] = a.w;
+            x[p][4] = b.x; x[p][5] = b.y; x[p][6] = b.z; x[p][7] = b.w;
+            xs[p] = xsum16[(e0 + 32 * p) >> 4];
+        }
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+            const uint4 qa = u.hdr[gi][it], qb = u.q0[gi][it], qc = u.q1[gi][it];
+            const uint32_t ql0[4] = {qa.x, qa.y, qa.z, qa.w};
+            const uint32_t ql1[4] = {qb.x, qb.y, qb.z, qb.w};
+            const uint32_t qh[4] = {qc.x, qc.y, qc.z, qc.w};
+            float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t w0 = ql0[c], w1 = ql1[c], hq = qh[c];
+                s0 = dot2_f16((w0 & LO) | ((hq << 4) & HI) | B, x[0][2 * c], s0);
+                s0 = dot2_f16(((w0 >> 8) & LO) | ((hq >> 4) & HI) | B, x[0][2 * c + 1], s0);
+                s1 = dot2_f16((w1 & LO) | ((hq << 2) & HI) | B, x[1][2 * c], s1);
+                s1 = dot2_f16(((w1 >> 8) & LO) | ((hq >> 6) & HI) | B, x[1][2 * c + 1], s1);
+                s2 = dot2_f16(((w0 >> 4) & LO) | (hq & HI) | B, x[2][2 * c], s2);
+                s2 = dot2_f16(((w0 >> 12) & LO) | ((hq >> 8) & HI) | B, x[2][2 * c + 1], s2);
+                s3 = dot2_f16(((w1 >> 4) & LO) | ((hq >> 2) & HI) | B, x[3][2 * c], s3);
+                s3 = dot2_f16(((w1 >> 12) & LO) | ((hq >> 10) & HI) | B, x[3][2 * c + 1], s3);
+            }
+            // int8 scales sc[8h + 2p + l0 / 16]: byte (l0 / 16) and 2 + (l0 / 16) of each dword
+            const uint2 scw = u.sc[gi][it];
+            const float sc0 = (float)(int8_t)((scw.x >> sh) & 0xffu);
+            const float sc1 = (float)(int8_t)((scw.x >> (16 + sh)) & 0xffu);
+            const float sc2 = (float)(int8_t)((scw.y >> sh) & 0xffu);
+            const float sc3 = (float)(int8_t)((scw.y >> (16 + sh)) & 0xffu);
+            float t = sc0 * fmaf(-1056.0f, xs[0], s0);
+            t = fmaf(sc1, fmaf(-1056.0f, xs[1], s1), t);
+            t = fmaf(sc2, fmaf(-1056.0f, xs[2], s2), t);
+            t = fmaf(sc3, fmaf(-1056.0f, xs[3], s3), t);
+            const float c = f16_bits_to_f32(u.d[gi][it] & 0xffffu) * t;
             if constexpr (RPW == 1) {
                 acc[gi][0] = it == 0 ? c : acc[gi][0] + c;
             } else {
@@ -562,15 +666,36 @@ __device__ __forceinline__ void dl_store_unit(const DlOut& o, uint32_t unit, uin
     }
 }
 
+// Issue unit slot i of the wave (unit dl_unit<SPREAD>(wave, i)) in the phase's
+// format.  DL_FMT_Q4_TAIL6: units from n_rows4 / RPW on are Q6_K units of w6;
+// only the last slot can hold one (units grow with the slot), so the others
+// are Q4_K at compile time.
+template <int FMT, int UPW, bool SPREAD, int NSB, int NG>
+__device__ __forceinline__ void dl_issue_slot(DlUnit<NSB, NG>& u, const DlRows& r, int wave, int i) {
+    constexpr int RPW = DlUnit<NSB, NG>::RPW;
+    const uint32_t unit = dl_unit<SPREAD>(wave, i);
+    if constexpr (FMT == DL_FMT_Q6) {
+        dl_issue_unit<true>(u, r.w0, r.w1, r.n_rows, unit);
+    } else if constexpr (FMT == DL_FMT_Q4_TAIL6) {
+        const uint32_t units4 = r.n_rows4 / RPW;
+        if (i == UPW - 1 && unit >= units4)
+            dl_issue_unit<true>(u, r.w6, r.w6, r.n_rows - r.n_rows4, unit - units4);
+        else
+            dl_issue_unit<false>(u, r.w0, r.w1, r.n_rows4, unit);
+    } else {
+        dl_issue_unit<false>(u, r.w0, r.w1, r.n_rows, unit);
+    }
+}
+
 // The first PRE units of a GEMV phase.  SPREAD phases: waves without a unit
 // issue nothing.
-template <int NSB, int NG, int UPW, int PRE, bool SPREAD>
+template <int NSB, int NG, int UPW, int PRE, bool SPREAD, int FMT = DL_FMT_Q4>
 __device__ __forceinline__ void dl_issue_pre(DlUnit<NSB, NG> (&u)[UPW], const DlRows& rows) {
     constexpr int RPW = DlUnit<NSB, NG>::RPW;
     const int wave = __builtin_amdgcn_readfirstlane(dl_tid() >> 6);
     if (SPREAD && dl_unit<SPREAD>(wave, 0) >= (rows.n_rows + RPW - 1) / RPW) return;
 #pragma unroll
-    for (int i = 0; i < PRE; ++i) dl_issue_unit(u[i], rows, dl_unit<SPREAD>(wave, i));
+    for (int i = 0; i < PRE; ++i) dl_issue_slot<FMT, UPW, SPREAD>(u[i], rows, wave, i);
 }
 
 // One GEMV phase over the wave's UPW units (rows wrow + i * DL_NW), streamed
@@ -582,9 +707,9 @@ __device__ __forceinline__ void dl_issue_pre(DlUnit<NSB, NG> (&u)[UPW], const Dl
 // is unrolled, so the ring is static registers, and the scheduling fences
 // keep each refill after the reduction that frees its registers.
 // SPREAD: fewer units than waves (dl_unit); a wave without a unit issues and
-// stores nothing.
-template <int NSB, int NG, int UPW, int R, int PRE, int EPI, bool RMSNORM, bool SPREAD, class SH,
-          class Hook = DlNoHook>
+// stores nothing.  FMT: the units' weight formats (DlFmt).
+template <int NSB, int NG, int UPW, int R, int PRE, int EPI, bool RMSNORM, bool SPREAD, int FMT = DL_FMT_Q4,
+          class SH, class Hook = DlNoHook>
 __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW], const DlRows& rows, int src_kind,
                                               const void* x_src, uint32_t e_x, const float* norm_w, float eps,
                                               const DlOut& out, uint32_t* status, uint32_t site,
@@ -605,8 +730,8 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
     hd.n_rows = rows.n_rows;
     hd.tr = out.tr;
     if (EPI != DL_EPI_RESID) hd.kind = -1;
-    dl_stage_x<NSB * 256, RMSNORM>(sm.g.xp, sm.g.xsum, sm.g.red, src_kind, x_src, e_x, norm_w, eps, hd, status,
-                                   site);
+    dl_stage_x<NSB * 256, RMSNORM>(sm.g.xp, sm.g.xsum, FMT == DL_FMT_Q4 ? nullptr : sm.g.xsum16, sm.g.red, src_kind,
+                                   x_src, e_x, norm_w, eps, hd, status, site);
     dl_stamp(out.tr, DL_TR_READY);
     // after_issue: the caller's early loads for the next phase, right behind this phase's last unit (every
     // wave calls it once, with or without units)
@@ -615,19 +740,28 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
         return;
     }
 #pragma unroll
-    for (int i = PRE; i < R; ++i) dl_issue_unit(u[i], rows, dl_unit<SPREAD>(wave, i));
+    for (int i = PRE; i < R; ++i) dl_issue_slot<FMT, UPW, SPREAD>(u[i], rows, wave, i);
     if constexpr (R >= UPW) after_issue();
     const Q4LaneConsts lc = q4k_lane_consts(dl_tid() & 3);
 #pragma unroll
     for (int i = 0; i < UPW; ++i) {
         __builtin_amdgcn_sched_barrier(0);
         float res[NG][RPW];
-        dl_dot_unit(u[i], sm.g.xp, sm.g.xsum, lc, res);
+        const uint32_t unit = dl_unit<SPREAD>(wave, i);
+        if constexpr (FMT == DL_FMT_Q6) {
+            dl_dot_unit6(u[i], sm.g.xp, sm.g.xsum16, res);
+        } else if constexpr (FMT == DL_FMT_Q4_TAIL6) {
+            if (i == UPW - 1 && unit >= rows.n_rows4 / RPW)
+                dl_dot_unit6(u[i], sm.g.xp, sm.g.xsum16, res);
+            else
+                dl_dot_unit(u[i], sm.g.xp, sm.g.xsum, lc, res);
+        } else {
+            dl_dot_unit(u[i], sm.g.xp, sm.g.xsum, lc, res);
+        }
         if (i == 0) dl_stamp(out.tr, DL_TR_FIRST);
-        dl_store_unit<NG, RPW, EPI>(out, dl_unit<SPREAD>(wave, i), rows.n_rows, res,
-                                    &sm.g.hold[(wave * UPW + i) * RPW]);
+        dl_store_unit<NG, RPW, EPI>(out, unit, rows.n_rows, res, &sm.g.hold[(wave * UPW + i) * RPW]);
         __builtin_amdgcn_sched_barrier(0);
-        if (i + R < UPW) dl_issue_unit(u[i + R], rows, dl_unit<SPREAD>(wave, i + R));
+        if (i + R < UPW) dl_issue_slot<FMT, UPW, SPREAD>(u[i + R], rows, wave, i + R);
         if (i + R == UPW - 1) after_issue();
     }
 }
@@ -1071,31 +1205,19 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
         return (uint64_t)hi << 32 | lo;
     };
-    auto qkv_rows = [&](uint32_t layer) {
+    auto make_rows = [&](uint32_t layer, int f0, int f1, uint32_t n_rows) {
         DlRows r;
-        r.w0 = r.w1 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WQ));  // q | k | v rows, contiguous
-        r.n_rows = S::QKV_ROWS;
+        r.w0 = dl_gptr<const uint8_t>(layer_ptr(layer, f0));
+        r.w1 = dl_gptr<const uint8_t>(layer_ptr(layer, f1));
+        r.n_rows = r.n_rows4 = n_rows;
+        r.w6 = nullptr;
         return r;
     };
-    auto o_rows = [&](uint32_t layer) {
-        DlRows r;
-        r.w0 = r.w1 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WO));
-        r.n_rows = S::HID;
-        return r;
-    };
-    auto gu_rows = [&](uint32_t layer) {
-        DlRows r;
-        r.w0 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WGATE));
-        r.w1 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WUP));
-        r.n_rows = S::MLP;
-        return r;
-    };
-    auto down_rows = [&](uint32_t layer) {
-        DlRows r;
-        r.w0 = r.w1 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WDOWN));
-        r.n_rows = S::HID;
-        return r;
-    };
+    // q | k | v rows, contiguous (q | k only when v is Q6_K: the DL_FMT_Q4_TAIL6 phase sets n_rows4 and w6)
+    auto qkv_rows = [&](uint32_t layer) { return make_rows(layer, DL_WQ, DL_WQ, S::QKV_ROWS); };
+    auto o_rows = [&](uint32_t layer) { return make_rows(layer, DL_WO, DL_WO, S::HID); };
+    auto gu_rows = [&](uint32_t layer) { return make_rows(layer, DL_WGATE, DL_WUP, S::MLP); };
+    auto down_rows = [&](uint32_t layer) { return make_rows(layer, DL_WDOWN, DL_WDOWN, S::HID); };
     // Up to DL_WAVES * DL_ATT_POS positions, block bs = 0 of each kv head covers them all (32 per wave) and
     // writes the normalised output itself: no partials, no merge phase and no hand-off into it.  Longer, the
     // kv head's positions are spread over its DL_ATT_SLOTS blocks and merged per q head.
@@ -1118,13 +1240,10 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
     // A phase's first units are issued when the phase begins, after the phase
     // before has computed: a CU serves its waves' loads roughly in issue order,
     // so loads for a later phase issued any earlier would delay the current
-    // phase's data in other waves.
+    // phase's data in other waves (measured for gate|up, down and the next
+    // layer's Q|K|V; only o_proj's units go early, see DL_O_EARLY).
     DlUnit<S::HSB, 1> uq[S::qkv_u];
     DlAttnBank bk;
-    if constexpr (DL_QKV_EARLY) {
-        dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp>(uq, qkv_rows(0));
-        issue_bank(0, bk);
-    }
     for (uint32_t layer = 0; layer < a.n_layers; ++layer) {
         const bool first = layer == 0, last = layer + 1 == a.n_layers;
         const uint32_t lsite = layer << 8;  // status code of a wait that gives up: layer and phase
@@ -1132,6 +1251,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         const uint32_t e_attn = dl_epoch(seq, layer, DL_E_ATTN), e_ho = dl_epoch(seq, layer, DL_E_H_O);
         const uint32_t e_act = dl_epoch(seq, layer, DL_E_ACT), e_hd = dl_epoch(seq, layer, DL_E_H_DOWN);
         const uint32_t e_hprev = first ? 0u : dl_epoch(seq, layer - 1, DL_E_H_DOWN);
+        const uint32_t wtypes = (uint32_t)layer_ptr(layer, DL_WTYPES);  // wave-uniform
         DlOut out;
         out.hold.kind = -1;
         // phase timeline slots of this block (the traced instantiation only)
@@ -1140,18 +1260,31 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         dl_stamp(out.tr, DL_TR_BEGIN);
         // ---- Q|K|V: RMSNorm(h) . [Wq; Wk; Wv]^T.  The attention K/V rows depend
         // on nothing computed in this launch: they are issued with the Q|K|V
-        // weights, before h is awaited (with DL_QKV_EARLY, during the layer
-        // before's down_proj), and stream during that hand-off.
-        if constexpr (!DL_QKV_EARLY) {
-            dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp>(uq, qkv_rows(layer));
-            issue_bank(layer, bk);
-        }
+        // weights, before h is awaited, and stream during that hand-off.  A Q6_K
+        // v: the q and k rows are Q4_K units and the v rows the Q6_K units that
+        // follow them in the same unit numbering (each wave's last slot).
         out.ll32 = a.qkv_ll;
         out.e_out = e_qkv;
-        dl_gemv_phase<S::HSB, 1, S::qkv_u, S::qkv_r, S::qkv_p, DL_EPI_STORE, true, qkv_sp>(
-            sm, uq, qkv_rows(layer), first ? DL_SRC_PLAIN : DL_SRC_LL32,
-            first ? static_cast<const void*>(a.h) : static_cast<const void*>(a.h_ll), e_hprev,
-            dl_gptr<const float>(layer_ptr(layer, DL_IN_NORM)), a.eps, out, a.status, lsite | DL_W_QKV);
+        const bool v6 = wtypes & DL_WT_V_Q6;
+        DlRows qrows = qkv_rows(layer);
+        if (v6) {
+            qrows.n_rows4 = S::QD + S::KVD;
+            qrows.w6 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WV));
+            dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp, DL_FMT_Q4_TAIL6>(uq, qrows);
+        } else {
+            dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp, DL_FMT_Q4>(uq, qrows);
+        }
+        issue_bank(layer, bk);
+        auto qkv_phase = [&](auto fmt) {
+            dl_gemv_phase<S::HSB, 1, S::qkv_u, S::qkv_r, S::qkv_p, DL_EPI_STORE, true, qkv_sp, decltype(fmt)::value>(
+                sm, uq, qrows, first ? DL_SRC_PLAIN : DL_SRC_LL32,
+                first ? static_cast<const void*>(a.h) : static_cast<const void*>(a.h_ll), e_hprev,
+                dl_gptr<const float>(layer_ptr(layer, DL_IN_NORM)), a.eps, out, a.status, lsite | DL_W_QKV);
+        };
+        if (v6)
+            qkv_phase(std::integral_constant<int, DL_FMT_Q4_TAIL6>());
+        else
+            qkv_phase(std::integral_constant<int, DL_FMT_Q4>());
         dl_stamp(out.tr, DL_TR_END);
         // ---- attention split
         constexpr int o_early = DL_O_EARLY < S::o_r ? DL_O_EARLY : S::o_r;
@@ -1160,6 +1293,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         {
             uint64_t* tr = trp(1);
             dl_stamp(tr, DL_TR_BEGIN);
+            // only the fields the attention phase reads (each is two scalar registers)
             uint64_t lp[DL_LAYER_PTRS];
 #pragma unroll
             for (int i = 0; i < DL_LAYER_PTRS; ++i) lp[i] = layer_ptr(layer, i);
@@ -1191,50 +1325,41 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         out.hold.src = first ? static_cast<const void*>(a.h) : static_cast<const void*>(a.h_ll);
         out.hold.e = e_hprev;
         out.e_out = e_ho;
-        constexpr int gu_early = DL_GU_EARLY < S::gu_r ? DL_GU_EARLY : S::gu_r;
-        constexpr int gu_pre = gu_early > 0 ? gu_early : S::gu_p;
-        DlUnit<S::HSB, 2> ug[S::gu_u];
         dl_gemv_phase<S::QSB, 1, S::o_u, S::o_r, o_pre, DL_EPI_RESID, false, o_sp>(
-            sm, uo, o_rows(layer), DL_SRC_LL16, a.attn_ll, e_attn, nullptr, a.eps, out, a.status, lsite | DL_W_O,
-            [&] {
-                if constexpr (gu_early > 0) dl_issue_pre<S::HSB, 2, S::gu_u, gu_early, gu_sp>(ug, gu_rows(layer));
-            });
+            sm, uo, o_rows(layer), DL_SRC_LL16, a.attn_ll, e_attn, nullptr, a.eps, out, a.status, lsite | DL_W_O);
         dl_stamp(out.tr, DL_TR_END);
         // ---- RMSNorm + gate|up + SwiGLU
         out.tr = trp(4);
         dl_stamp(out.tr, DL_TR_BEGIN);
-        if constexpr (gu_early == 0) dl_issue_pre<S::HSB, 2, S::gu_u, S::gu_p, gu_sp>(ug, gu_rows(layer));
+        DlUnit<S::HSB, 2> ug[S::gu_u];
+        dl_issue_pre<S::HSB, 2, S::gu_u, S::gu_p, gu_sp>(ug, gu_rows(layer));
         out.ll16 = a.act_ll;
         out.e_out = e_act;
-        constexpr int dn_early = DL_DN_EARLY < S::dn_r ? DL_DN_EARLY : S::dn_r;
-        constexpr int dn_pre = dn_early > 0 ? dn_early : S::dn_p;
-        DlUnit<S::MSB, 1> ud[S::dn_u];
-        dl_gemv_phase<S::HSB, 2, S::gu_u, S::gu_r, gu_pre, DL_EPI_SWIGLU, true, gu_sp>(
-            sm, ug, gu_rows(layer), DL_SRC_LL32, a.h_ll, e_ho,
-            dl_gptr<const float>(layer_ptr(layer, DL_POST_NORM)), a.eps, out, a.status, lsite | DL_W_GU, [&] {
-                if constexpr (dn_early > 0) dl_issue_pre<S::MSB, 1, S::dn_u, dn_early, dn_sp>(ud, down_rows(layer));
-            });
+        dl_gemv_phase<S::HSB, 2, S::gu_u, S::gu_r, S::gu_p, DL_EPI_SWIGLU, true, gu_sp>(
+            sm, ug, gu_rows(layer), DL_SRC_LL32, a.h_ll, e_ho, dl_gptr<const float>(layer_ptr(layer, DL_POST_NORM)),
+            a.eps, out, a.status, lsite | DL_W_GU);
         dl_stamp(out.tr, DL_TR_END);
-        // ---- down + residual (the last layer writes the caller's h)
+        // ---- down + residual (the last layer writes the caller's h); Q4_K or Q6_K rows
         out.tr = trp(5);
         dl_stamp(out.tr, DL_TR_BEGIN);
-        if constexpr (dn_early == 0) dl_issue_pre<S::MSB, 1, S::dn_u, S::dn_p, dn_sp>(ud, down_rows(layer));
         out.ll32 = a.h_ll;
         out.plain = last ? a.h : nullptr;
         out.hold.kind = DL_SRC_LL32;
         out.hold.src = a.h_ll;
         out.hold.e = e_ho;
         out.e_out = e_hd;
-        dl_gemv_phase<S::MSB, 1, S::dn_u, S::dn_r, dn_pre, DL_EPI_RESID, false, dn_sp>(
-            sm, ud, down_rows(layer), DL_SRC_LL16, a.act_ll, e_act, nullptr, a.eps, out, a.status,
-            lsite | DL_W_DOWN, [&] {
-                if constexpr (DL_QKV_EARLY) {
-                    if (!last) {
-                        dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp>(uq, qkv_rows(layer + 1));
-                        issue_bank(layer + 1, bk);
-                    }
-                }
-            });
+        auto down_phase = [&](auto fmt) {
+            constexpr int FMT = decltype(fmt)::value;
+            DlUnit<S::MSB, 1> ud[S::dn_u];
+            dl_issue_pre<S::MSB, 1, S::dn_u, S::dn_p, dn_sp, FMT>(ud, down_rows(layer));
+            dl_gemv_phase<S::MSB, 1, S::dn_u, S::dn_r, S::dn_p, DL_EPI_RESID, false, dn_sp, FMT>(
+                sm, ud, down_rows(layer), DL_SRC_LL16, a.act_ll, e_act, nullptr, a.eps, out, a.status,
+                lsite | DL_W_DOWN);
+        };
+        if (wtypes & DL_WT_DOWN_Q6)
+            down_phase(std::integral_constant<int, DL_FMT_Q6>());
+        else
+            down_phase(std::integral_constant<int, DL_FMT_Q4>());
         dl_stamp(out.tr, DL_TR_END);
     }
     // Every block has read the launch counter before block 0 can get here: its

@@ -40,15 +40,18 @@ __device__ __forceinline__ int xp_word(int k) { return (k >> 1) + ((k >> 6) << 2
 
 // Stage 4 consecutive x values (already bf16-exact) at element k: one fp16
 // pair word (e0,e2) and one (e1,e3), and, through the 8 threads that hold one
-// 32-value sub-block, that sub-block's sum.  All 8 threads of a sub-block call
+// 32-value sub-block, that sub-block's sum (and, with xsum16, the sum of each
+// 16 values, for Q6_K's scale groups).  All 8 threads of a sub-block call
 // this together.
-__device__ __forceinline__ void stage_x4(uint32_t* xp, float* xsum, int k, float v0, float v1, float v2, float v3) {
+__device__ __forceinline__ void stage_x4(uint32_t* xp, float* xsum, int k, float v0, float v1, float v2, float v3,
+                                         float* xsum16 = nullptr) {
     const uint32_t a = f32_to_f16_bits(v0) | (f32_to_f16_bits(v2) << 16);
     const uint32_t b = f32_to_f16_bits(v1) | (f32_to_f16_bits(v3) << 16);
     *reinterpret_cast<uint2*>(&xp[xp_word(k)]) = make_uint2(a, b);
     float s = (v0 + v1) + (v2 + v3);
     s += dpp_f32<0xB1>(s);  // quad_perm [1,0,3,2]: lane ^ 1
     s += dpp_f32<0x4E>(s);  // quad_perm [2,3,0,1]: lane ^ 2
+    if (xsum16 != nullptr && ((k >> 2) & 3) == 0) xsum16[k >> 4] = s;  // the quad's 16 values
     s += dpp_f32<0x141>(s);  // row_half_mirror: a lane of the other quad of the 8, which holds that quad's sum
     if (((k >> 2) & 7) == 0) xsum[k >> 5] = s;
 }

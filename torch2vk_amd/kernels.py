@@ -553,19 +553,36 @@ def decode_layers_workspace(hidden: int, mlp: int, nh: int, nk: int, d: int, dev
     return torch.zeros(n, dtype=torch.uint8, device=device) if n else None
 
 
+DECODE_LAYER_TABLE_COLUMNS = 14
+DL_WT_V_Q6, DL_WT_DOWN_Q6 = 1, 2  # bits of the table's weight-types column
+
+
 def decode_layer_table(packed: dict[str, torch.Tensor], norms: dict[str, torch.Tensor], layers: int,
-                       k_cache: torch.Tensor, v_cache: torch.Tensor) -> torch.Tensor:
-    """Device int64 [layers, 13] pointer table (q, k, v, o, gate, up, down, norms, caches) for
-    :func:`decode_layers`; q, k and v must be consecutive rows of one allocation."""
+                       k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       types: dict[str, str] | None = None) -> torch.Tensor:
+    """Device int64 [layers, 14] table for :func:`decode_layers`: the q, k, v, o, gate, up, down, norm and cache
+    pointers, then the layer's weight types (bit 0: v is Q6_K, bit 1: down is Q6_K).  ``types`` (GGUF type per
+    weight name; None = all Q4_K): q, k, o, gate and up must be Q4_K, v and down Q4_K or Q6_K (the Q4_K_M
+    policy).  q and k must be consecutive rows of one allocation, followed by v's rows when v is Q4_K."""
     rows = []
     for i in range(layers):
         p = f"layers.{i}."
+        t = {n: (types[p + n] if types is not None else "q4_k") for n in ("q", "k", "v", "o", "gate", "up", "down")}
+        for n in ("q", "k", "o", "gate", "up"):
+            if t[n] != "q4_k":
+                raise ValueError(f"layer {i}: {n} must be Q4_K, got {t[n]}")
+        for n in ("v", "down"):
+            if t[n] not in ("q4_k", "q6_k"):
+                raise ValueError(f"layer {i}: {n} must be Q4_K or Q6_K, got {t[n]}")
         q, k, v = packed[p + "q"], packed[p + "k"], packed[p + "v"]
-        if k.data_ptr() != q.data_ptr() + q.numel() or v.data_ptr() != k.data_ptr() + k.numel():
-            raise ValueError(f"layer {i}: q, k and v rows must be stacked in one allocation")
+        if k.data_ptr() != q.data_ptr() + q.numel():
+            raise ValueError(f"layer {i}: q and k rows must be stacked in one allocation")
+        if t["v"] == "q4_k" and v.data_ptr() != k.data_ptr() + k.numel():
+            raise ValueError(f"layer {i}: a Q4_K v must follow k's rows in the same allocation")
         ptrs = [packed[p + n].data_ptr() for n in ("q", "k", "v", "o", "gate", "up", "down")]
         ptrs += [norms[p + n].data_ptr() for n in ("input_norm", "post_norm", "q_norm", "k_norm")]
         ptrs += [k_cache[i].data_ptr(), v_cache[i].data_ptr()]
+        ptrs.append((DL_WT_V_Q6 if t["v"] == "q6_k" else 0) | (DL_WT_DOWN_Q6 if t["down"] == "q6_k" else 0))
         rows.append(ptrs)
     return torch.tensor(rows, dtype=torch.int64).to(k_cache.device)
 
@@ -580,8 +597,8 @@ def decode_layers(table: torch.Tensor, h: torch.Tensor, cache_position: torch.Te
     _check(cache_position, "cache_position", torch.int32, align=4)
     _check(workspace, "workspace", torch.uint8, align=256)
     _check(status, "status", torch.int32, align=4)
-    if table.dim() != 2 or table.shape[1] != 13:
-        raise ValueError(f"layer_table must be int64 [layers, 13], got {tuple(table.shape)}")
+    if table.dim() != 2 or table.shape[1] != DECODE_LAYER_TABLE_COLUMNS:
+        raise ValueError(f"layer_table must be int64 [layers, {DECODE_LAYER_TABLE_COLUMNS}], got {tuple(table.shape)}")
     args = (ptr(table), int(table.shape[0]), hidden, mlp, nh, nk, d, s_cap, ptr(h), ptr(cache_position), eps, theta,
             ptr(workspace), workspace.numel(), ptr(status))
     if trace is None:
@@ -600,8 +617,8 @@ def decode_layers_noalloc(table: torch.Tensor, h: torch.Tensor, cache_position: 
     _check(h, "h", torch.float32)
     _check(cache_position, "cache_position", torch.int32, align=4)
     _check(status, "status", torch.int32, align=4)
-    if table.dim() != 2 or table.shape[1] != 13:
-        raise ValueError(f"layer_table must be int64 [layers, 13], got {tuple(table.shape)}")
+    if table.dim() != 2 or table.shape[1] != DECODE_LAYER_TABLE_COLUMNS:
+        raise ValueError(f"layer_table must be int64 [layers, {DECODE_LAYER_TABLE_COLUMNS}], got {tuple(table.shape)}")
     call("t2h_qwen3_decode_layers_noalloc", ptr(table), int(table.shape[0]), hidden, mlp, nh, nk, d, s_cap, ptr(h),
          ptr(cache_position), eps, theta, ptr(status), stream_handle())
 

@@ -55,8 +55,9 @@ def _check_types(c: Qwen3Config, types: dict[str, str]) -> None:
 
 class Qwen3Decoder:
     """Greedy decoder over libt2h.  ``persistent`` selects how a token's layers run: one persistent launch
-    for all of them (t2h_qwen3_decode_layers: the 8B shape with uniform Q4_K weights), or one launch per
-    op (run_decode_layer, every shape and weight mix).  None (the default) picks the persistent kernel when it
+    for all of them (t2h_qwen3_decode_layers: the 8B and 0.6B shapes with Q4_K weights, v and down Q4_K or
+    Q6_K as the uniform and Q4_K_M policies give them), or one launch per op (run_decode_layer, every shape and
+    weight mix).  None (the default) picks the persistent kernel when it
     applies: on MI355X it saves the launch and ramp of ~250 kernels per token."""
 
     def __init__(self, weights: Qwen3Weights, *, max_positions: int, max_new_tokens: int, device=None,
@@ -97,7 +98,7 @@ class Qwen3Decoder:
             if why is None:
                 self.layers_ws = kernels.decode_layers_workspace(c.hidden, c.mlp, c.heads, c.kv_heads, c.head_dim, dev)
                 self.layer_table = kernels.decode_layer_table(weights.packed, weights.norms, c.layers, self.k_cache,
-                                                              self.v_cache)
+                                                              self.v_cache, self.types)
                 self.persistent = True
             elif persistent:
                 raise NotImplementedError(f"persistent decode kernel: {why}")
@@ -111,12 +112,16 @@ class Qwen3Decoder:
         if self.config.layers > 64:
             return "more than 64 layers"
         for i in range(c.layers):
-            for n in ("q", "k", "v", "o", "gate", "up", "down"):
-                if self.types[f"layers.{i}.{n}"] != "q4_k":
-                    return "weights other than uniform Q4_K"
+            t = {n: self.types[f"layers.{i}.{n}"] for n in ("q", "k", "v", "o", "gate", "up", "down")}
+            if any(t[n] != "q4_k" for n in ("q", "k", "o", "gate", "up")):
+                return "q, k, o, gate or up weights other than Q4_K"
+            if any(t[n] not in ("q4_k", "q6_k") for n in ("v", "down")):
+                return "v or down weights other than Q4_K or Q6_K"
             q, k, v = (self.weights.packed[f"layers.{i}.{n}"] for n in ("q", "k", "v"))
-            if k.data_ptr() != q.data_ptr() + q.numel() or v.data_ptr() != k.data_ptr() + k.numel():
-                return "q, k and v rows are not stacked in one allocation"
+            if k.data_ptr() != q.data_ptr() + q.numel():
+                return "q and k rows are not stacked in one allocation"
+            if t["v"] == "q4_k" and v.data_ptr() != k.data_ptr() + k.numel():
+                return "a Q4_K v does not follow k's rows in the same allocation"
         return None
 
     def check_status(self) -> None:

@@ -77,13 +77,16 @@ def synthetic_weights(config: Qwen3Config, *, device, seed: int = 0, std: float 
 
 
 def stack_qkv(w: Qwen3Weights) -> None:
-    """Keep each layer's q, k and v rows in one allocation (q, k, v become views of it) when they share a
-    GGUF type: the persistent decode kernel streams them as one 6144-row matrix.  Rows are quantized
-    independently, so the bytes are unchanged."""
+    """Keep each layer's q and k rows, and v's when it has their GGUF type, in one allocation (they become
+    views of it): the persistent decode kernel streams them as one matrix (6144 rows at the 8B shape), and
+    a Q6_K v (Q4_K_M more-bits layers) as its own.  Rows are quantized independently, so the bytes are
+    unchanged."""
     for i in range(w.config.layers):
         names = [f"layers.{i}.{n}" for n in ("q", "k", "v")]
-        if len({w.types[n] for n in names}) != 1:
+        if w.types[names[0]] != w.types[names[1]]:
             continue
+        if w.types[names[2]] != w.types[names[0]]:
+            names = names[:2]
         parts = [w.packed[n] for n in names]
         fused = torch.cat(parts, dim=0)
         begin = 0
