@@ -152,6 +152,20 @@ int t2h_q4k_gemm(const void* x, const void* w, void* y, int out_dtype, const flo
  * text_layer.py; src/models/optimized_qwen3/shaders/swiglu_f32.py). */
 int t2h_gemm_swiglu(int wtype, const void* x, const void* w_gate, const void* w_up, void* y, uint32_t m, uint32_t k,
                     uint32_t n_ff, void* stream);
+/* Split-K form of the prefill GEMMs above, for grids too small to fill the GPU (a few hundred rows, as in a
+ * short prompt or a 512-token prefill chunk): K is cut into `splits` equal parts of whole 64-wide stages, each
+ * part's fp32 products go to partials (t2h_gemm_splitk_bytes(m, n, splits, swiglu) bytes, 16-B aligned),
+ * then a second kernel sums the parts in order and applies the epilogue: bias,
+ * act, and fp32 (+ residual, which may alias y) or bf16 output.  w_up non-null selects the SwiGLU form (w the
+ * gate rows, n = n_ff features, y bf16 [m, n_ff]; no bias, act or residual).  wtype Q8_0 / Q4_K / Q6_K;
+ * w_k as t2h_q8_0_linear (= k for the K types and for SwiGLU); 1 <= splits <= min(k / 64, 64).  The results
+ * equal the one-pass GEMM's up to the order of the fp32 sum.  No counterpart of its own in the reference: it
+ * is the same LINEAR_NOBIAS_*_F32 / LLAMA_MATMUL_*_F32 products (see the entries above), scheduled for small
+ * M. */
+size_t t2h_gemm_splitk_bytes(uint32_t m, uint32_t n, uint32_t splits, int swiglu);
+int t2h_gemm_splitk(int wtype, const void* x, const void* w, const void* w_up, const float* bias, int act, void* y,
+                    int out_dtype, const float* residual, uint32_t m, uint32_t k, uint32_t n, uint32_t w_k,
+                    uint32_t splits, void* partials, size_t partials_bytes, void* stream);
 /* replaces LLAMA_MATMUL_Q6_K_F32_{M,L} (src/models/optimized_qwen3/shaders/llama_matmul_q6_k_f32.py:27-141):
  * the Q6_K v/down weights of the Q4_K_M more-bits layers; k % 256 == 0, W 2-byte aligned. */
 int t2h_q6k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,

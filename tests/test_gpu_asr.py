@@ -36,11 +36,15 @@ LINEAR_CASES = [
 ]
 
 
+@pytest.mark.parametrize("splits", [1, None], ids=["one_pass", "auto_split"])
 @pytest.mark.parametrize("m,kx,kw,n,bias,act,out", LINEAR_CASES)
-def test_q8_0_linear_matches_oracle(device, m, kx, kw, n, bias, act, out):
+def test_q8_0_linear_matches_oracle(device, m, kx, kw, n, bias, act, out, splits):
+    """splits 1: the one-pass kernel; None: the wrapper's choice (small grids split K, the bias, GELU and
+    residual then applied in the reduction)."""
     from torch2vk_amd import kernels
 
-    print(f"q8_0_linear M={m} Kx={kx} Kw={kw} N={n} bias={bias} act={act} out={out}", flush=True)
+    print(f"q8_0_linear M={m} Kx={kx} Kw={kw} N={n} bias={bias} act={act} out={out} "
+          f"splits={kernels.gemm_splits(m, n, kx) if splits is None else 1}", flush=True)
     rng = np.random.default_rng(m + kx + n)
     w = (rng.standard_normal((n, kw)) * 0.03).astype(np.float32)
     packed = oracle.quantize_q8_0(w)
@@ -56,14 +60,14 @@ def test_q8_0_linear_matches_oracle(device, m, kx, kw, n, bias, act, out):
     wt = torch.from_numpy(packed).to(device)
     bt = torch.from_numpy(b).to(device) if b is not None else None
     dt = torch.bfloat16 if out == "bf16" else torch.float32
-    got = kernels.q8_0_linear(xt, wt, bias=bt, act=act, out_dtype=dt).float().cpu().numpy()
+    got = kernels.q8_0_linear(xt, wt, bias=bt, act=act, out_dtype=dt, splits=splits).float().cpu().numpy()
     scale = np.abs(ref).max()
     tol = 8e-3 * scale if out == "bf16" else 1e-5 * scale + 1e-5
     assert_close(got, ref, max_abs=tol, min_cos=0.99999, what="q8_0_linear")
     if out == "f32" and act is None:
         res = rng.standard_normal((m, n)).astype(np.float32)
         rt = torch.from_numpy(res).to(device)
-        kernels.q8_0_linear(xt, wt, bias=bt, out=rt, residual=rt)
+        kernels.q8_0_linear(xt, wt, bias=bt, out=rt, residual=rt, splits=splits)
         assert_close(rt.cpu().numpy(), ref + res, max_abs=1e-5 * scale + 1e-5, min_cos=0.99999, what="residual")
 
 

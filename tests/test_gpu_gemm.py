@@ -32,15 +32,18 @@ CASES = [("q8_0", 256, 256, 256), ("q8_0", 300, 1024, 520), ("q8_0", 17, 2048, 1
          ("q6_k", 256, 256, 256), ("q6_k", 300, 1024, 520), ("q6_k", 17, 4096, 1024), ("q6_k", 700, 3072, 384)]
 
 
+@pytest.mark.parametrize("splits", [1, None], ids=["one_pass", "auto_split"])
 @pytest.mark.parametrize("wtype,m,k,n", CASES)
-def test_gemm_matches_oracle(device, wtype, m, k, n):
+def test_gemm_matches_oracle(device, wtype, m, k, n, splits):
+    """splits 1: the one-pass kernel; None: the wrapper's choice (small grids split K: t2h_gemm_splitk)."""
     from torch2vk_amd import kernels
 
-    print(f"gemm {wtype} M={m} K={k} N={n}", flush=True)
+    print(f"gemm {wtype} M={m} K={k} N={n} splits={kernels.gemm_splits(m, n, k) if splits is None else 1}",
+          flush=True)
     rng, packed, wd, x = _problem(wtype, m, k, n, m + k + n)
     xt = torch.from_numpy(x).to(device).to(torch.bfloat16)
     wt = torch.from_numpy(packed).to(device)
-    got = kernels.gemm(xt, wt, wtype, out_dtype=torch.float32).cpu().numpy()
+    got = kernels.gemm(xt, wt, wtype, out_dtype=torch.float32, splits=splits).cpu().numpy()
     # the weight tile is dequantised to bf16: against x . bf16(deq W)^T only fp32 accumulation differs,
     # which pins the tile layout and the dequantisation exactly
     ref_tile = x.astype(np.float64) @ R.bf16_round(wd.astype(np.float32)).astype(np.float64).T
@@ -50,11 +53,11 @@ def test_gemm_matches_oracle(device, wtype, m, k, n):
     ref = x.astype(np.float64) @ wd.astype(np.float64).T
     assert_close(got, ref, max_abs=1e-2 * np.abs(ref).max(), min_cos=0.9999, what="vs fp64 oracle")
     # bf16 output and the residual epilogue (in place)
-    got16 = kernels.gemm(xt, wt, wtype).float().cpu().numpy()
+    got16 = kernels.gemm(xt, wt, wtype, splits=splits).float().cpu().numpy()
     assert_close(got16, ref_tile, max_abs=1e-2 * scale, min_cos=0.9999, what="bf16 out")
     res = rng.standard_normal((m, n)).astype(np.float32)
     rt = torch.from_numpy(res).to(device)
-    kernels.gemm(xt, wt, wtype, out=rt, residual=rt)
+    kernels.gemm(xt, wt, wtype, out=rt, residual=rt, splits=splits)
     assert_close(rt.cpu().numpy(), ref_tile + res, max_abs=1e-5 * scale + 1e-5, min_cos=0.999999, what="residual")
 
 
@@ -70,9 +73,10 @@ def test_gemm_rejects_bad_shapes(device):
     assert st == 2
 
 
+@pytest.mark.parametrize("splits", [1, None], ids=["one_pass", "auto_split"])
 @pytest.mark.parametrize("wtype,m,k,n", [("q8_0", 300, 1024, 520), ("q4_k", 17, 2048, 1024), ("q8_0", 700, 512, 96),
                                          ("q6_k", 260, 1024, 384), ("q4_k", 1030, 4096, 768)])
-def test_gemm_swiglu_matches_oracle(device, wtype, m, k, n):
+def test_gemm_swiglu_matches_oracle(device, wtype, m, k, n, splits):
     """Gate and up products with SwiGLU in the epilogue, against silu(x Wg^T) * (x Wu^T) on the bf16 tiles."""
     from torch2vk_amd import kernels
 
@@ -86,6 +90,61 @@ def test_gemm_swiglu_matches_oracle(device, wtype, m, k, n):
     u = xd @ R.bf16_round(wud.astype(np.float32)).astype(np.float64).T
     ref = g / (1.0 + np.exp(-g)) * u
     xt = torch.from_numpy(x).to(device).to(torch.bfloat16)
-    got = kernels.gemm_swiglu(xt, torch.from_numpy(pg).to(device), torch.from_numpy(pu).to(device), wtype)
+    got = kernels.gemm_swiglu(xt, torch.from_numpy(pg).to(device), torch.from_numpy(pu).to(device), wtype,
+                              splits=splits)
     assert_close(got.float().cpu().numpy(), ref, max_abs=8e-3 * np.abs(ref).max() + 1e-6, min_cos=0.9999,
                  what="gemm_swiglu")
+
+
+@pytest.mark.parametrize("wtype,m,k,n,splits", [("q8_0", 128, 2048, 1024, 16), ("q4_k", 100, 3072, 1024, 5),
+                                                ("q6_k", 37, 1024, 4096, 3), ("q8_0", 512, 1024, 4096, 4),
+                                                ("q4_k", 483, 3072, 1024, 16)])
+def test_gemm_splitk_equals_one_pass(device, wtype, m, k, n, splits):
+    """Split-K (parts of uneven stage counts included) against the one-pass kernel on the same inputs: the same
+    products summed in another fp32 order, so within fp32 rounding of the sum; the residual epilogue in place,
+    the bf16 output, and the SwiGLU form (gate | up products reduced, then silu(g) u)."""
+    from torch2vk_amd import kernels
+
+    print(f"split-K {wtype} M={m} K={k} N={n} splits={splits}", flush=True)
+    g = torch.Generator(device=device)
+    g.manual_seed(m + n + splits)
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    w = kernels.quantize(torch.randn(n, k, generator=g, device=device) * 0.02, wtype)
+    one = kernels.gemm(x, w, wtype, out_dtype=torch.float32, splits=1)
+    got = kernels.gemm(x, w, wtype, out_dtype=torch.float32, splits=splits)
+    scale = one.abs().max().item()
+    assert (got - one).abs().max().item() <= 1e-5 * scale
+    res = torch.randn(m, n, generator=g, device=device)
+    r1, r2 = res.clone(), res.clone()
+    kernels.gemm(x, w, wtype, out=r1, residual=r1, splits=1)
+    kernels.gemm(x, w, wtype, out=r2, residual=r2, splits=splits)
+    assert (r1 - r2).abs().max().item() <= 1e-5 * (scale + res.abs().max().item())
+    b1 = kernels.gemm(x, w, wtype, splits=1).float()
+    b2 = kernels.gemm(x, w, wtype, splits=splits).float()
+    # bf16 roundings of fp32 values within 1e-5 of the scale: one bf16 step apart, or that absolute error
+    assert ((b1 - b2).abs() <= 2 ** -7 * b1.abs() + 2e-5 * scale).all()
+    wu = kernels.quantize(torch.randn(n, k, generator=g, device=device) * 0.02, wtype)
+    s1 = kernels.gemm_swiglu(x, w, wu, wtype, splits=1).float()
+    s2 = kernels.gemm_swiglu(x, w, wu, wtype, splits=splits).float()
+    assert ((s1 - s2).abs() <= 2 ** -7 * s1.abs() + 1e-4 * s1.abs().max()).all()
+    torch.cuda.synchronize()
+
+
+def test_gemm_splitk_rejects_bad_arguments(device):
+    from torch2vk_amd import _lib
+
+    lib = _lib.lib()
+    x = torch.zeros(4, 256, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(64, 256 // 32 * 34, dtype=torch.uint8, device=device)
+    y = torch.empty(4, 64, dtype=torch.float32, device=device)
+    need = int(lib.t2h_gemm_splitk_bytes(4, 64, 2, 0))
+    assert need == 2 * 4 * 64 * 4
+    assert int(lib.t2h_gemm_splitk_bytes(4, 100, 2, 1)) == 2 * 4 * 256 * 4  # gate | up rows in whole tiles
+    part = torch.empty(need // 4, dtype=torch.float32, device=device)
+    args = lambda splits, nbytes: (8, x.data_ptr(), w.data_ptr(), None, None, 0, y.data_ptr(), 0, None, 4, 256, 64,
+                                   256, splits, part.data_ptr(), nbytes, None)
+    assert lib.t2h_gemm_splitk(*args(2, need - 4)) == 6     # workspace too small
+    assert lib.t2h_gemm_splitk(*args(5, need * 4)) == 5     # more parts than 64-wide stages (4)
+    assert lib.t2h_gemm_splitk(*args(0, need)) == 5
+    assert lib.t2h_gemm_splitk(*args(2, need)) == 0
+    torch.cuda.synchronize()

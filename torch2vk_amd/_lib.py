@@ -85,6 +85,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "t2h_embedding_q8_0": (_i32, [_vp, _u64, _vp, _u32, _u32, _vp, _vp]),
     "t2h_q6k_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp]),
     "t2h_gemm_swiglu": (_i32, [_i32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "t2h_gemm_splitk_bytes": (_sz, [_u32, _u32, _u32, _i32]),
+    "t2h_gemm_splitk": (_i32, [_i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _sz,
+                               _vp]),
     "t2h_im2col_1d": (_i32, [_vp, _i32, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _u32, _vp]),
     "t2h_snake": (_i32, [_vp, _vp, _vp, _u64, _u32, _f32, _vp]),
     "t2h_conv_transpose1d_q8_0": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32,

@@ -45,7 +45,8 @@ constexpr int GQ_LDS_ROW = GQ_BK + 8;  // bf16 elements per padded LDS row
 #endif
 constexpr int GQ_GROUP_M = GQ_GROUP_M_DEF;  // tiles per group down M (4 and 8 measured fastest)
 
-enum GemmEpilogue { GQEPI_F32 = 0, GQEPI_BF16 = 1, GQEPI_RESID = 2, GQEPI_SWIGLU = 3 };
+// GQEPI_GATED_F32: the SwiGLU form's gate | up tile columns written as fp32 products (split-K partials).
+enum GemmEpilogue { GQEPI_F32 = 0, GQEPI_BF16 = 1, GQEPI_RESID = 2, GQEPI_SWIGLU = 3, GQEPI_GATED_F32 = 4 };
 
 enum GemmAct { GQACT_NONE = 0, GQACT_GELU = 1 };
 
@@ -62,6 +63,8 @@ struct GemmArgs {
     uint32_t tiles_m, tiles_n;
     const uint8_t* w_up;   // GQEPI_SWIGLU: up rows (w holds the gate rows)
     uint32_t n_ff;         // GQEPI_SWIGLU: features; n = 2 n_ff
+    uint32_t split_stages; // split-K: 64-wide K stages per split (blockIdx.y), split s writing its fp32
+                           // products to c + s m n; 0: the whole K range in one pass
 };
 
 // Packed row of B-tile row r (0..255) of the tile at n0.  Plain: weight row
@@ -293,11 +296,16 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
     const int wn = wave & 3;   // 0..3: cols wn * 64
 
     // A stage load: GQ_BM rows x 64 bf16 in 16-B chunks, ACH per thread
-    const uint32_t KT = a.k / GQ_BK;
+    // this block's K stages: [kt0, kt0 + KT) (all of K, or split blockIdx.y's part of it)
+    uint32_t kt0 = 0, KT = a.k / GQ_BK;
+    if (a.split_stages != 0) {
+        kt0 = blockIdx.y * a.split_stages;
+        KT = min(KT - kt0, a.split_stages);
+    }
     uint4 ra[ACH];
     typename F::Raw rw;
     auto load_stage = [&](uint32_t kt) {
-        const uint32_t k0 = kt * GQ_BK;
+        const uint32_t k0 = (kt0 + kt) * GQ_BK;
 #pragma unroll
         for (int i = 0; i < ACH; ++i) {
             const uint32_t c = t + GQ_THREADS * i;
@@ -305,7 +313,7 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
             row = row < a.m ? row : a.m - 1;
             ra[i] = load_u4(a.a + (size_t)row * a.k + k0 + (c & 7) * 8);
         }
-        F::template load<EPI == GQEPI_SWIGLU>(a, n0, k0, rw);
+        F::template load<EPI == GQEPI_SWIGLU || EPI == GQEPI_GATED_F32>(a, n0, k0, rw);
     };
     auto store_stage = [&](uint32_t kt, int s) {
 #pragma unroll
@@ -313,7 +321,7 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
             const uint32_t c = t + GQ_THREADS * i;
             *reinterpret_cast<uint4*>(&lds_a[s][(c >> 3) * GQ_LDS_ROW + (c & 7) * 8]) = ra[i];
         }
-        store_w<F>(rw, lds_b[s], kt * GQ_BK);
+        store_w<F>(rw, lds_b[s], (kt0 + kt) * GQ_BK);
     };
     // part p (0..3) of store_stage: A chunks after MFMA step SS, the weights after the next (the later the
     // step, the longer the global loads issued at the end of the stage before have to land)
@@ -326,7 +334,7 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
                 *reinterpret_cast<uint4*>(&lds_a[s][(c >> 3) * GQ_LDS_ROW + (c & 7) * 8]) = ra[i];
             }
         } else if (p == SS + 1) {
-            store_w<F>(rw, lds_b[s], kt * GQ_BK);
+            store_w<F>(rw, lds_b[s], (kt0 + kt) * GQ_BK);
         }
     };
     static_assert(SS >= 0 && SS + 1 < GQ_BK / 16, "store steps within the stage");
@@ -418,8 +426,9 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
                     const size_t idx = (size_t)row * a.n + col;
                     float v = acc[i][j][e] + bj;
                     if (a.act == GQACT_GELU) v = gelu_erf(v);
-                    if constexpr (EPI == GQEPI_F32) {
-                        reinterpret_cast<float*>(a.c)[idx] = v;
+                    if constexpr (EPI == GQEPI_F32 || EPI == GQEPI_GATED_F32) {
+                        // split s of a split-K launch: its own m x n slice
+                        reinterpret_cast<float*>(a.c)[(size_t)blockIdx.y * a.m * a.n + idx] = v;
                     } else if constexpr (EPI == GQEPI_BF16) {
                         reinterpret_cast<uint16_t*>(a.c)[idx] = (uint16_t)f32_to_bf16_bits(v);
                     } else {
@@ -545,6 +554,137 @@ static int gemm_swiglu_launch(const void* x, const void* w_gate, const void* w_u
     gemm_q_dispatch<F, GQEPI_SWIGLU>(a, reinterpret_cast<hipStream_t>(stream));
     T2H_LAUNCH_CHECK();
     return T2H_OK;
+}
+
+// ---------------------------------------------------------------- split-K ----
+
+// out = epilogue(sum over the splits of partial[s]) in split order.  Plain: y[row][col] from partial column
+// col, + bias, GELU, then fp32 (+ residual) or bf16.  SwiGLU (n_ff > 0): feature f's gate and up products are
+// the tile-interleaved columns the gated kernel writes (per 256-column tile: 4 groups of 32 gate then 32 up
+// columns, 128 features; partial rows are whole tiles, n_cols a multiple of 256).
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ partial, uint32_t splits,
+                                                                 uint32_t m, uint32_t n_cols, uint32_t n_out,
+                                                                 uint32_t n_ff, const float* bias, int act,
+                                                                 void* y, int out_dtype, const float* residual) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)m * n_out) return;
+    const uint32_t row = (uint32_t)(i / n_out), col = (uint32_t)(i % n_out);
+    const size_t slice = (size_t)m * n_cols;
+    if (n_ff != 0) {
+        const uint32_t gc = (col / 128) * 256 + ((col % 128) / 32) * 64 + col % 32;
+        const float* pg = partial + (size_t)row * n_cols + gc;
+        float g = 0.0f, u = 0.0f;
+        for (uint32_t s = 0; s < splits; ++s) {
+            g += pg[s * slice];
+            u += pg[s * slice + 32];
+        }
+        const float sg = g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
+        reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)f32_to_bf16_bits(sg * u);
+        return;
+    }
+    const float* p = partial + (size_t)row * n_cols + col;
+    float v = 0.0f;
+    for (uint32_t s = 0; s < splits; ++s) v += p[s * slice];
+    v += bias != nullptr ? bias[col] : 0.0f;
+    if (act == GQACT_GELU) v = gelu_erf(v);
+    if (residual != nullptr)
+        reinterpret_cast<float*>(y)[i] = residual[i] + v;
+    else if (out_dtype == T2H_DTYPE_F32)
+        reinterpret_cast<float*>(y)[i] = v;
+    else
+        reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)f32_to_bf16_bits(v);
+}
+
+// Partial products of `splits` parts of K, then the reduction.  Gated: w_up != nullptr, n = n_ff features.
+template <class F>
+static int gemm_splitk_launch(const void* x, const void* w, const void* w_up, const float* bias, int act, void* y,
+                              int out_dtype, const float* residual, uint32_t m, uint32_t k, uint32_t n, uint32_t w_k,
+                              uint32_t splits, void* partials, size_t partials_bytes, void* stream) {
+    if (!x || !w || !y || !partials) return T2H_ERR_NULL;
+    const bool gated = w_up != nullptr;
+    if (k == 0 || k % GQ_BK != 0) return T2H_ERR_SHAPE;
+    if (w_k == 0 || w_k > k || w_k % F::BLOCK_VALUES != 0) return T2H_ERR_SHAPE;
+    if ((F::BLOCK_VALUES == 256 || gated) && w_k != k) return T2H_ERR_SHAPE;
+    if (act != GQACT_NONE && act != GQACT_GELU) return T2H_ERR_ARG;
+    if (gated && (bias || act != GQACT_NONE || residual || out_dtype != T2H_DTYPE_BF16)) return T2H_ERR_ARG;
+    if (residual && out_dtype != T2H_DTYPE_F32) return T2H_ERR_DTYPE;
+    if (out_dtype != T2H_DTYPE_F32 && out_dtype != T2H_DTYPE_BF16) return T2H_ERR_DTYPE;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) return T2H_ERR_ALIGN;
+    if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(w_up)) & (F::ALIGN - 1)) != 0)
+        return T2H_ERR_ALIGN;
+    if ((reinterpret_cast<uintptr_t>(partials) & 15) != 0) return T2H_ERR_ALIGN;
+    const uint32_t stages = k / GQ_BK;
+    if (splits == 0 || splits > stages || splits > 64) return T2H_ERR_ARG;
+    if (m == 0 || n == 0) return T2H_OK;
+    if (n > 0x3fffffffu || (uint64_t)m * n > 0x7fffffffu) return T2H_ERR_SHAPE;
+    // gated: whole 256-column tiles of gate | up groups, so that every feature's up column exists
+    const uint32_t n_cols = gated ? (2 * n + GQ_BN - 1) / GQ_BN * GQ_BN : n;
+    if (partials_bytes < t2h_gemm_splitk_bytes(m, n, splits, gated ? 1 : 0)) return T2H_ERR_WORKSPACE;
+    GemmArgs a = {};
+    a.a = reinterpret_cast<const uint16_t*>(x);
+    a.w = reinterpret_cast<const uint8_t*>(w);
+    a.w_up = reinterpret_cast<const uint8_t*>(w_up);
+    a.c = partials;
+    a.m = m;
+    a.n = n_cols;
+    a.n_ff = gated ? n : 0;
+    a.k = k;
+    a.w_blocks = w_k / F::BLOCK_VALUES;
+    a.row_bytes = a.w_blocks * F::BLOCK_BYTES;
+    // every split takes the same number of stages, so none is empty
+    const uint32_t per = (stages + splits - 1) / splits;
+    a.split_stages = per;
+    const uint32_t used = (stages + per - 1) / per;
+    a.tiles_n = (n_cols + GQ_BN - 1) / GQ_BN;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    // 128-row tiles as in gemm_q_dispatch, and for up to 128 rows (a 256-row tile would compute half of it for
+    // nothing)
+    if ((m + 255) / 256 * a.tiles_n < 1024) {
+        a.tiles_m = (m + 127) / 128;
+        if (gated)
+            hipLaunchKernelGGL((gemm_q_kernel<F, GQEPI_GATED_F32, 2>), dim3(a.tiles_m * a.tiles_n, used), dim3(512),
+                               0, s, a);
+        else
+            hipLaunchKernelGGL((gemm_q_kernel<F, GQEPI_F32, 2>), dim3(a.tiles_m * a.tiles_n, used), dim3(512), 0, s,
+                               a);
+    } else {
+        a.tiles_m = (m + 255) / 256;
+        if (gated)
+            hipLaunchKernelGGL((gemm_q_kernel<F, GQEPI_GATED_F32, 4>), dim3(a.tiles_m * a.tiles_n, used), dim3(512),
+                               0, s, a);
+        else
+            hipLaunchKernelGGL((gemm_q_kernel<F, GQEPI_F32, 4>), dim3(a.tiles_m * a.tiles_n, used), dim3(512), 0, s,
+                               a);
+    }
+    T2H_LAUNCH_CHECK();
+    const size_t outs = (size_t)m * n;
+    hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<const float*>(partials), used, m, n_cols, n, a.n_ff, bias, act, y, out_dtype,
+                       residual);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+extern "C" size_t t2h_gemm_splitk_bytes(uint32_t m, uint32_t n, uint32_t splits, int swiglu) {
+    const size_t n_cols = swiglu ? ((size_t)2 * n + GQ_BN - 1) / GQ_BN * GQ_BN : n;
+    return (size_t)splits * m * n_cols * sizeof(float);
+}
+
+extern "C" int t2h_gemm_splitk(int wtype, const void* x, const void* w, const void* w_up, const float* bias, int act,
+                               void* y, int out_dtype, const float* residual, uint32_t m, uint32_t k, uint32_t n,
+                               uint32_t w_k, uint32_t splits, void* partials, size_t partials_bytes, void* stream) {
+    switch (wtype) {
+        case T2H_WTYPE_Q8_0:
+            return gemm_splitk_launch<GemmQ80>(x, w, w_up, bias, act, y, out_dtype, residual, m, k, n, w_k, splits,
+                                               partials, partials_bytes, stream);
+        case T2H_WTYPE_Q4_K:
+            return gemm_splitk_launch<GemmQ4K>(x, w, w_up, bias, act, y, out_dtype, residual, m, k, n, w_k, splits,
+                                               partials, partials_bytes, stream);
+        case T2H_WTYPE_Q6_K:
+            return gemm_splitk_launch<GemmQ6K>(x, w, w_up, bias, act, y, out_dtype, residual, m, k, n, w_k, splits,
+                                               partials, partials_bytes, stream);
+        default: return T2H_ERR_DTYPE;
+    }
 }
 
 extern "C" int t2h_gemm_swiglu(int wtype, const void* x, const void* w_gate, const void* w_up, void* y, uint32_t m,

@@ -265,10 +265,36 @@ def lm_head_argmax_partial(x: torch.Tensor, w: torch.Tensor, wtype: str, partial
          ptr(partial_tokens), g, stream_handle())
 
 
+GEMM_FILL_BLOCKS = 128  # grids below this many tiles split K (t2h_gemm_splitk)
+
+
+def gemm_splits(m: int, n_cols: int, k: int) -> int:
+    """K parts for a prefill GEMM of m rows and n_cols tile columns (1 = the one-pass GEMM): when the
+    one-pass grid has fewer than GEMM_FILL_BLOCKS tiles, enough parts that the split grid (128-row tiles)
+    reaches ~256 blocks, each part at least 2 stages of 64, at most 16 parts."""
+    tiles_n = -(-n_cols // 256)
+    tiles_256 = -(-m // 256) * tiles_n
+    tiles = -(-m // 128) * tiles_n if (tiles_256 < 1024 and m > 128) else tiles_256
+    if tiles >= GEMM_FILL_BLOCKS:
+        return 1
+    split_tiles = -(-m // 128) * tiles_n
+    return max(1, min(k // 128, -(-256 // split_tiles), 16))
+
+
+def _gemm_splitk(wtype: str, x: torch.Tensor, w: torch.Tensor, w_up: torch.Tensor | None, out: torch.Tensor,
+                 m: int, k: int, n: int, w_k: int, splits: int, *, bias: torch.Tensor | None = None, act: int = 0,
+                 residual: torch.Tensor | None = None) -> None:
+    nbytes = int(_lib.lib().t2h_gemm_splitk_bytes(m, n, splits, 1 if w_up is not None else 0))
+    partials = torch.empty(nbytes // 4, dtype=torch.float32, device=x.device)
+    call("t2h_gemm_splitk", WTYPES[wtype], ptr(x), ptr(w), ptr(w_up), ptr(bias), act, ptr(out),
+         _OUT_DTYPES[out.dtype], ptr(residual), m, k, n, w_k, splits, ptr(partials), nbytes, stream_handle())
+
+
 def gemm(x: torch.Tensor, w: torch.Tensor, wtype: str, *, out: torch.Tensor | None = None,
-         out_dtype: torch.dtype = torch.bfloat16, residual: torch.Tensor | None = None) -> torch.Tensor:
+         out_dtype: torch.dtype = torch.bfloat16, residual: torch.Tensor | None = None,
+         splits: int | None = None) -> torch.Tensor:
     """Prefill GEMM on the matrix cores: y[M, N] = x[M, K] . deq(W)^T (+ residual); x bf16, W Q8_0, Q4_K or
-    Q6_K."""
+    Q6_K.  ``splits``: K parts (t2h_gemm_splitk; None = gemm_splits' choice, 1 = one pass)."""
     if wtype not in ("q8_0", "q4_k", "q6_k"):
         raise ValueError(f"gemm handles q8_0, q4_k and q6_k weights, got {wtype!r}")
     _check(x, "x", torch.bfloat16)
@@ -286,15 +312,20 @@ def gemm(x: torch.Tensor, w: torch.Tensor, wtype: str, *, out: torch.Tensor | No
         _check(residual, "residual", torch.float32, align=4)
         if residual.numel() != m * n or out.dtype != torch.float32:
             raise ValueError("residual must be fp32 with the output's shape; output must be fp32")
+    splits = gemm_splits(m, n, k) if splits is None else splits
+    if splits > 1:
+        _gemm_splitk(wtype, x, w, None, out, m, k, n, k, splits, residual=residual)
+        return out
     name = {"q8_0": "t2h_q8_0_gemm", "q4_k": "t2h_q4k_gemm", "q6_k": "t2h_q6k_gemm"}[wtype]
     call(name, ptr(x), ptr(w), ptr(out), _OUT_DTYPES[out.dtype], ptr(residual), m, k, n, stream_handle())
     return out
 
 
 def gemm_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, wtype: str, *,
-                out: torch.Tensor | None = None) -> torch.Tensor:
+                out: torch.Tensor | None = None, splits: int | None = None) -> torch.Tensor:
     """bf16 [M, F] = silu(x . deq(W_gate)^T) * (x . deq(W_up)^T) in one matrix-core launch (the prefill MLP's
-    gate and up GEMMs with SwiGLU in the epilogue); x bf16 [M, K], both weights [F, K] of type ``wtype``."""
+    gate and up GEMMs with SwiGLU in the epilogue); x bf16 [M, K], both weights [F, K] of type ``wtype``.
+    ``splits`` as for :func:`gemm` (split-K: the products, then SwiGLU in the reduction)."""
     if wtype not in ("q8_0", "q4_k", "q6_k"):
         raise ValueError(f"gemm_swiglu handles q8_0, q4_k and q6_k weights, got {wtype!r}")
     _check(x, "x", torch.bfloat16)
@@ -310,6 +341,10 @@ def gemm_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, wtype
     _check(out, "output", torch.bfloat16, align=2)
     if out.numel() != m * n:
         raise ValueError(f"output has {out.numel()} elements, expected {m * n}")
+    splits = gemm_splits(m, 2 * n, k) if splits is None else splits
+    if splits > 1:
+        _gemm_splitk(wtype, x, w_gate, w_up, out, m, k, n, k, splits)
+        return out
     call("t2h_gemm_swiglu", WTYPES[wtype], ptr(x), ptr(w_gate), ptr(w_up), ptr(out), m, k, n, stream_handle())
     return out
 
@@ -402,7 +437,7 @@ ACTS = {None: 0, "none": 0, "gelu": 1}
 
 def q8_0_linear(x: torch.Tensor, w: torch.Tensor, *, bias: torch.Tensor | None = None, act: str | None = None,
                 out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
-                residual: torch.Tensor | None = None) -> torch.Tensor:
+                residual: torch.Tensor | None = None, splits: int | None = None) -> torch.Tensor:
     """y[M, N] = act(x[M, K] . deq(W)^T + bias) (+ residual) on the matrix cores (LINEAR_BIAS_Q8_0W_F32B_F32).
     x bf16 with K % 64 == 0; W Q8_0 rows of w_k = 32 * blocks <= K values (x's columns past w_k must be
     finite: they multiply zeros); bias fp32 [N]; act None or "gelu" (exact erf)."""
@@ -435,6 +470,10 @@ def q8_0_linear(x: torch.Tensor, w: torch.Tensor, *, bias: torch.Tensor | None =
         _check(residual, "residual", torch.float32, align=4)
         if residual.numel() != m * n or out.dtype != torch.float32:
             raise ValueError("residual must be fp32 with the output's shape; output must be fp32")
+    splits = gemm_splits(m, n, k) if splits is None else splits
+    if splits > 1:
+        _gemm_splitk("q8_0", x, w, None, out, m, k, n, w_k, splits, bias=bias, act=ACTS[act], residual=residual)
+        return out
     call("t2h_q8_0_linear", ptr(x), ptr(w), ptr(bias), ACTS[act], ptr(out), _OUT_DTYPES[out.dtype], ptr(residual),
          m, k, n, w_k, stream_handle())
     return out
