@@ -35,7 +35,7 @@ TRAFFIC_PROFILES = {
     "decode_layers_persistent": PROFILES / "decode_layers_qwen3_8b_int4_kv4096_pmc.md",
     "gate_up_rmsnorm_swiglu_gemv": PROFILES / "gate_up_gemv_qwen3_8b_pmc.md",
     "prefill_gate_up_gemm": PROFILES / "gemm_swiglu_q8_0_m16384_pmc.md",
-    "asr_decode_layers_0_6b": PROFILES / "decode_layers_qwen3_0_6b_int4_kv1540_pmc.md",
+    "asr_decode_layers_0_6b": PROFILES / "decode_layers_qwen3_0_6b_x4_int4_kv1540_pmc.md",
 }
 PROMPT_POSITIONS = 4096
 
@@ -78,7 +78,8 @@ def profile_kernel_target(per_op: bool, config: str = "decode") -> int:
     then one plain 256 MiB device copy whose traffic is known (256 MiB read + 256 MiB written), so counter
     readings can be scaled to bytes.  decode: the persistent layers kernel at KV 4096 (2 dispatches), or per
     op the gate|up GEMV once per layer (72 dispatches); prefill: the gate|up + SwiGLU GEMM at M 16384 (2
-    dispatches) and causal flash attention over 8 x 2048 tokens (2 dispatches); asr: the 0.6B-shape persistent layers kernel at KV 1540 (2 dispatches)."""
+    dispatches) and causal flash attention over 8 x 2048 tokens (2 dispatches); asr: the 0.6B-shape persistent layers
+    kernel for 4 sequences at KV 1540 each (2 dispatches)."""
     import torch
 
     from torch2vk_amd import kernels
@@ -107,17 +108,22 @@ def profile_kernel_target(per_op: bool, config: str = "decode") -> int:
         _profile_copy(dev)
         return 0
     if config == "asr":
+        from torch2vk_amd.qwen3.model import Qwen3DecoderGroup
+
         w = synthetic_weights(QWEN3_0_6B, device=dev, seed=2)
-        dec = Qwen3Decoder(w, max_positions=1600, max_new_tokens=4, device=dev, persistent=True)
+        decs = [Qwen3Decoder(w, max_positions=1600, max_new_tokens=4, device=dev, persistent=True) for _ in range(4)]
         gen = torch.Generator(device=dev)
         gen.manual_seed(1)
-        dec.k_cache[:, :1539].normal_(generator=gen)
-        dec.v_cache[:, :1539].normal_(generator=gen)
-        dec.h.normal_()
-        dec.position.fill_(1539)
+        for dec in decs:
+            dec.k_cache[:, :1539].normal_(generator=gen)
+            dec.v_cache[:, :1539].normal_(generator=gen)
+            dec.h.normal_()
+            dec.position.fill_(1539)
+        group = Qwen3DecoderGroup(decs)
         for _ in range(2):
-            dec.run_decode_layers()
-        dec.check_status()
+            group.run_decode_layers()
+        for dec in decs:
+            dec.check_status()
         _profile_copy(dev)
         return 0
     w = synthetic_weights(QWEN3_8B, device=dev, seed=0)
@@ -410,15 +416,16 @@ def _graph_us_per_call(calls, reps: int) -> float:
     return us
 
 
-def persistent_bytes(weights, c, kv_len: int) -> int:
-    """Algorithmic bytes of one persistent decode launch: each layer's packed weights and norms, the K/V rows
-    0 .. kv_len - 1 read and the new row written, and the residual stream in and out."""
+def persistent_bytes(weights, c, kv_len: int, n_seq: int = 1) -> int:
+    """Algorithmic bytes of one persistent decode launch: each layer's packed weights and norms (once, however
+    many sequences share them), and per sequence the K/V rows 0 .. kv_len - 1 read and the new row written,
+    and the residual stream in and out."""
     b = 0
     for i in range(c.layers):
         b += sum(weights.packed[f"layers.{i}.{n}"].numel() for n in ("q", "k", "v", "o", "gate", "up", "down"))
         b += sum(weights.norms[f"layers.{i}.{n}"].numel() * 4 for n in ("input_norm", "post_norm", "q_norm",
                                                                           "k_norm"))
-    b += c.layers * (2 * kv_len * c.kv_dim * 2 + 2 * c.kv_dim * 2) + 2 * c.hidden * 4
+    b += n_seq * (c.layers * (2 * kv_len * c.kv_dim * 2 + 2 * c.kv_dim * 2) + 2 * c.hidden * 4)
     return int(b)
 
 
@@ -1006,7 +1013,7 @@ def bench_asr(args) -> int:
 
     from torch2vk_amd import kernels
     from torch2vk_amd.qwen3.config import QWEN3_0_6B
-    from torch2vk_amd.qwen3.model import Qwen3Decoder
+    from torch2vk_amd.qwen3.model import Qwen3Decoder, Qwen3DecoderGroup
     from torch2vk_amd.qwen3.weights import synthetic_weights
     from torch2vk_amd.qwen3_asr.config import ASR_C5_ENCODER
     from torch2vk_amd.qwen3_asr.encoder import (Qwen3AudioEncoder, quantize_audio_weights, run_audio_inject,
@@ -1027,8 +1034,13 @@ def bench_asr(args) -> int:
     tw = synthetic_weights(tcfg, device=dev, seed=2)
     prefix, suffix = [151644, 8948, 198, 151669], [151670, 151645, 198]
     prompt_len = len(prefix) + frames + len(suffix)
-    dec = Qwen3Decoder(tw, max_positions=prompt_len + new_tokens + 16, max_new_tokens=new_tokens + 8, device=dev)
-    dec.stop_on_eos = False
+    # one decoder (KV cache) per utterance; their decode steps run together, all 4 sequences' layers in one
+    # persistent launch
+    decs = [Qwen3Decoder(tw, max_positions=prompt_len + new_tokens + 16, max_new_tokens=new_tokens + 8, device=dev)
+            for _ in range(nb)]
+    for dec in decs:
+        dec.stop_on_eos = False
+    group = Qwen3DecoderGroup(decs)
     ids = torch.tensor(prefix + [ecfg_audio_id()] * frames + suffix, device=dev)
     audio_pos = torch.arange(len(prefix), len(prefix) + frames, device=dev)
     h = torch.empty_like(feats_in)
@@ -1044,10 +1056,11 @@ def bench_asr(args) -> int:
     def step() -> None:
         feats = encode()
         transcripts.clear()
-        for b in range(nb):
+        for b, dec in enumerate(decs):
             emb = dec.embed_tokens(ids)
             run_audio_inject(emb, audio_pos, feats[b * frames:(b + 1) * frames])
-            transcripts.append(dec.generate_from_embeds(emb, new_tokens, prefill_chunk=2048))
+            dec.prefill_chunked(embeds=emb, chunk=2048)
+        transcripts.extend(group.finish(new_tokens))
 
     per_step = _timed_steps(step, args.warmup, args.steps)
     frames_s = nb * frames / per_step
@@ -1062,13 +1075,17 @@ def bench_asr(args) -> int:
     y = torch.empty(nb * frames, f, dtype=torch.bfloat16, device=dev)
     fc1_us = _events_us(lambda: kernels.q8_0_linear(x_ln, fc1, bias=b1, act="gelu", out=y), args.kernel_reps * 4)
     fc1_tflops = 2.0 * nb * frames * d * f / (fc1_us * 1e-6) / 1e12
-    # dominant kernel of the step: the decoder's persistent launch (all 28 layers of a token), timed at the
-    # middle of the generated span
-    dec.position.fill_(prompt_len + new_tokens // 2)
+    # dominant kernel of the step: the 4 decoders' persistent launch (all 28 layers of a token of each
+    # utterance), timed at the middle of the generated span; its bytes are the shared weights once and each
+    # sequence's KV rows (the 4 groups of blocks read the same weights, which L2 and the MALL serve after the
+    # first: the counters measure 1.04x these bytes)
+    for dec in decs:
+        dec.position.fill_(prompt_len + new_tokens // 2)
     kv_len = prompt_len + new_tokens // 2 + 1
-    dl_us = _graph_us_per_call([dec.run_decode_layers] * 2, args.kernel_reps * 4) if dec.persistent else None
-    dl_bytes = persistent_bytes(tw, tcfg, kv_len)
-    dec.check_status()
+    dl_us = _graph_us_per_call([group.run_decode_layers] * 2, args.kernel_reps * 4)
+    dl_bytes = persistent_bytes(tw, tcfg, kv_len, n_seq=nb)
+    for dec in decs:
+        dec.check_status()
     print(f"[bench] asr step {per_step * 1e3:.1f} ms ({frames_s:.0f} frames/s); encoder {enc_s * 1e3:.2f} ms, "
           f"{enc_tflops:.1f} TFLOP/s; fc1 {fc1_us:.1f} us {fc1_tflops:.1f} TFLOP/s; tokens {len(transcripts[0])}",
           file=sys.stderr, flush=True)
@@ -1091,8 +1108,9 @@ def bench_asr(args) -> int:
         "config": {
             "workload": "4 utterances x 1500 frames: encoder (24 layers, hidden 1024, 16 heads, FFN 4096, "
                         "attention within each utterance) + ln_post/proj1/proj2, then per utterance the audio "
-                        "states injected into a 1507-position prompt, chunked prefill and 64 greedy tokens "
-                        "(Qwen3-0.6B shape, uniform Q4_K, HIP graphs of 8 steps)",
+                        "states injected into a 1507-position prompt and chunked prefill, and 64 greedy tokens of "
+                        "the 4 utterances decoded together (Qwen3-0.6B shape, uniform Q4_K, one persistent launch "
+                        "for the 4 sequences' layers per step, HIP graphs of 8 steps)",
             "batch": nb, "frames": frames, "decoder_tokens": new_tokens,
         },
         "encoder_ms": round(enc_s * 1e3, 3),
@@ -1100,7 +1118,8 @@ def bench_asr(args) -> int:
         "mfma_utilisation": round(enc_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": f"decode_layers_kernel<DlQwen3_0_6B> (28 layers of a decoder token, KV {kv_len})",
+            "kernel": f"decode_layers_kernel<DlQwen3_0_6B_x4> (28 layers of a decoder token of each of the "
+                      f"4 utterances, KV {kv_len})",
             "achieved": round(dl_bytes / (dl_us * 1e-6) / 1e9, 1) if dl_us else None,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -261,6 +261,19 @@ int t2h_qwen3_decode_layers_noalloc(const uint64_t* layer_table, uint32_t n_laye
                                     uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap, float* h,
                                     const int32_t* cache_position, float eps, float theta, uint32_t* status,
                                     void* stream);
+/* n_seq independent decode sequences in one launch, each with its own layer table (its own KV caches; the
+ * weights may be shared), h, *cache_position, workspace (t2h_qwen3_decode_layers_workspace_bytes(), distinct per
+ * sequence) and *status, as t2h_qwen3_decode_layers; all share n_layers, the shape, s_cap, eps and theta.  The
+ * host arrays hold n_seq device pointers each.  n_seq = 1 is t2h_qwen3_decode_layers; n_seq = 4 is built for
+ * the Qwen3-0.6B shape with s_cap <= 2048: the 256 blocks split into 4 groups of 64, one per sequence, each
+ * streaming its own copy of the weights (at this shape the hand-offs, not HBM, bound a launch, so four
+ * sequences take little longer than one).  No counterpart in the reference, which decodes one sequence at a
+ * time (run_decode_layer, src/models/optimized_qwen3/dispatch/decode_layer.py:60-136, per sequence). */
+int t2h_qwen3_decode_layers_seqs(uint32_t n_seq, const uint64_t* const* layer_tables, uint32_t n_layers,
+                                 uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap,
+                                 float* const* hs, const int32_t* const* cache_positions, float eps, float theta,
+                                 void* const* workspaces, size_t workspace_bytes, uint32_t* const* statuses,
+                                 void* stream);
 /* The same launch with a phase timeline: trace (device, 8-B aligned, t2h_qwen3_decode_layers_trace_bytes()
  * bytes) receives, per layer, phase (qkv, attention, merge, o, gate/up, down) and block (256), 8 uint64 slots:
  * the 100 MHz real-time clock at the phase's start, when its input is in hand, after its first reduced unit

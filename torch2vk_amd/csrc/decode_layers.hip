@@ -246,8 +246,11 @@ constexpr int dl_max3(int a, int b, int c) { return a > b ? (a > c ? a : c) : (b
 // Model shape (8 kv heads of 128) and, per GEMV phase, the units per wave, the
 // ring depth and the units issued before the input is awaited.
 template <int HSB_, int MSB_, int NH_, int QKV_U, int QKV_R, int QKV_P, int O_U, int O_R, int O_P, int GU_U,
-          int GU_R, int GU_P, int DN_U, int DN_R, int DN_P, bool PV_MFMA>
+          int GU_R, int GU_P, int DN_U, int DN_R, int DN_P, bool PV_MFMA, int NB_ = DL_BLOCKS>
 struct DlShape {
+    // blocks per sequence: the launch's 256 blocks run 256 / NB sequences side by side
+    static constexpr int NB = NB_, NSEQ = DL_BLOCKS / NB_, NW = NB_ * DL_WAVES, ATT_SLOTS = NB_ / 8;
+    static_assert(NB == DL_BLOCKS || NB == 64, "one sequence, or four of 64 blocks");
     static constexpr int HSB = HSB_;             // hidden / 256 (superblocks)
     static constexpr int MSB = MSB_;             // MLP / 256
     static constexpr int NH = NH_;               // q heads
@@ -280,11 +283,15 @@ struct DlShape {
 using DlQwen3_8B = DlShape<16, 48, 32, 3, DL_R_QKV, DL_PRE_QKV, 2, DL_R_O, DL_PRE_O, 6, DL_R_GU, DL_PRE_GU, 2, DL_R_DOWN,
                            DL_PRE_DOWN, true>;
 using DlQwen3_0_6B = DlShape<4, 12, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, false>;
+// four 0.6B sequences of 64 blocks each: every phase's units over 512 waves (Q|K|V 2 per wave, o 1, gate|up 2,
+// down spread), attention over 8 blocks per kv head
+using DlQwen3_0_6B_x4 = DlShape<4, 12, 16, 2, 2, 1, 1, 1, 1, 2, 2, 1, 1, 1, 1, false, 64>;
 
 constexpr int DL_HOLD = 4;  // residual rows a wave owns in one phase, at most
 
 template <class S>
 union DlShared {
+    static constexpr int NB = S::NB;
     struct {
         uint32_t xp[xp_words(S::KMAX)];
         float xsum[S::KMAX / 32];
@@ -324,12 +331,15 @@ struct DlUnit {
 // every unit Q6_K.
 enum DlFmt { DL_FMT_Q4 = 0, DL_FMT_Q4_TAIL6 = 1, DL_FMT_Q6 = 2 };
 
-// Unit i of wave `wave` of this block.  Block-major when every wave has a unit;
-// SPREAD (fewer units than waves): across the blocks first, so that every CU
-// streams a share.
-template <bool SPREAD>
+// Unit i of wave `wave` of this block, among the NB blocks of its sequence
+// (blockIdx.x % NB: one sequence, or one of 256 / NB).  Block-major when every
+// wave has a unit; SPREAD (fewer units than waves): across the blocks first, so
+// that every CU streams a share.
+template <bool SPREAD, int NB>
 __device__ __forceinline__ uint32_t dl_unit(uint32_t wave, uint32_t i) {
-    return SPREAD ? wave * DL_BLOCKS + blockIdx.x + i * DL_NW : blockIdx.x * DL_WAVES + wave + i * DL_NW;
+    constexpr uint32_t NW = NB * DL_WAVES;
+    const uint32_t lb = blockIdx.x % NB;
+    return SPREAD ? wave * NB + lb + i * NW : lb * DL_WAVES + wave + i * NW;
 }
 
 // Row pointers of a GEMV phase: NG == 2 reads row `row` of w0 and w1.
@@ -394,6 +404,7 @@ struct DlHold {
     int upw;
     int rpw;
     bool spread;      // the phase's unit mapping (dl_unit)
+    int nb;           // blocks per sequence (dl_unit's NB: 256 or 64)
     uint32_t n_rows;
     uint64_t* tr;     // phase timeline slots (traced build), else nullptr
 };
@@ -404,7 +415,8 @@ struct DlHold {
 // race with its owner's overwrite and wait for an epoch that is already gone).
 __device__ __forceinline__ uint32_t dl_hold_row(const DlHold& hd, int t) {
     const uint32_t w = (uint32_t)(t / (hd.upw * hd.rpw)), i = (uint32_t)((t / hd.rpw) % hd.upw);
-    const uint32_t unit = hd.spread ? dl_unit<true>(w, i) : dl_unit<false>(w, i);
+    const uint32_t unit = hd.nb == 64 ? (hd.spread ? dl_unit<true, 64>(w, i) : dl_unit<false, 64>(w, i))
+                                      : (hd.spread ? dl_unit<true, 256>(w, i) : dl_unit<false, 256>(w, i));
     const uint32_t row = unit * (uint32_t)hd.rpw + (uint32_t)(t % hd.rpw);
     return row < hd.n_rows ? row : hd.n_rows;
 }
@@ -670,10 +682,10 @@ __device__ __forceinline__ void dl_store_unit(const DlOut& o, uint32_t unit, uin
 // format.  DL_FMT_Q4_TAIL6: units from n_rows4 / RPW on are Q6_K units of w6;
 // only the last slot can hold one (units grow with the slot), so the others
 // are Q4_K at compile time.
-template <int FMT, int UPW, bool SPREAD, int NSB, int NG>
+template <int FMT, int UPW, bool SPREAD, int NB, int NSB, int NG>
 __device__ __forceinline__ void dl_issue_slot(DlUnit<NSB, NG>& u, const DlRows& r, int wave, int i) {
     constexpr int RPW = DlUnit<NSB, NG>::RPW;
-    const uint32_t unit = dl_unit<SPREAD>(wave, i);
+    const uint32_t unit = dl_unit<SPREAD, NB>(wave, i);
     if constexpr (FMT == DL_FMT_Q6) {
         dl_issue_unit<true>(u, r.w0, r.w1, r.n_rows, unit);
     } else if constexpr (FMT == DL_FMT_Q4_TAIL6) {
@@ -689,13 +701,13 @@ __device__ __forceinline__ void dl_issue_slot(DlUnit<NSB, NG>& u, const DlRows& 
 
 // The first PRE units of a GEMV phase.  SPREAD phases: waves without a unit
 // issue nothing.
-template <int NSB, int NG, int UPW, int PRE, bool SPREAD, int FMT = DL_FMT_Q4>
+template <int NSB, int NG, int UPW, int PRE, bool SPREAD, int NB, int FMT = DL_FMT_Q4>
 __device__ __forceinline__ void dl_issue_pre(DlUnit<NSB, NG> (&u)[UPW], const DlRows& rows) {
     constexpr int RPW = DlUnit<NSB, NG>::RPW;
     const int wave = __builtin_amdgcn_readfirstlane(dl_tid() >> 6);
-    if (SPREAD && dl_unit<SPREAD>(wave, 0) >= (rows.n_rows + RPW - 1) / RPW) return;
+    if (SPREAD && dl_unit<SPREAD, NB>(wave, 0) >= (rows.n_rows + RPW - 1) / RPW) return;
 #pragma unroll
-    for (int i = 0; i < PRE; ++i) dl_issue_slot<FMT, UPW, SPREAD>(u[i], rows, wave, i);
+    for (int i = 0; i < PRE; ++i) dl_issue_slot<FMT, UPW, SPREAD, NB>(u[i], rows, wave, i);
 }
 
 // One GEMV phase over the wave's UPW units (rows wrow + i * DL_NW), streamed
@@ -709,7 +721,7 @@ __device__ __forceinline__ void dl_issue_pre(DlUnit<NSB, NG> (&u)[UPW], const Dl
 // SPREAD: fewer units than waves (dl_unit); a wave without a unit issues and
 // stores nothing.  FMT: the units' weight formats (DlFmt).
 template <int NSB, int NG, int UPW, int R, int PRE, int EPI, bool RMSNORM, bool SPREAD, int FMT = DL_FMT_Q4,
-          class SH, class Hook = DlNoHook>
+          class SH, class Hook = DlNoHook, int NB = SH::NB>
 __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW], const DlRows& rows, int src_kind,
                                               const void* x_src, uint32_t e_x, const float* norm_w, float eps,
                                               const DlOut& out, uint32_t* status, uint32_t site,
@@ -720,13 +732,14 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
     static_assert(!SPREAD || UPW == 1, "spread phases have one unit per wave");
     const int wave = __builtin_amdgcn_readfirstlane(dl_tid() >> 6);
     const uint32_t n_units = (rows.n_rows + RPW - 1) / RPW;
-    const bool active = !SPREAD || dl_unit<SPREAD>(wave, 0) < n_units;  // wave-uniform
+    const bool active = !SPREAD || dl_unit<SPREAD, NB>(wave, 0) < n_units;  // wave-uniform
     __syncthreads();  // every wave is done with the previous phase's LDS
     DlHold hd = out.hold;
     hd.lds = sm.g.hold;
     hd.upw = UPW;
     hd.rpw = RPW;
     hd.spread = SPREAD;
+    hd.nb = NB;
     hd.n_rows = rows.n_rows;
     hd.tr = out.tr;
     if (EPI != DL_EPI_RESID) hd.kind = -1;
@@ -740,14 +753,14 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
         return;
     }
 #pragma unroll
-    for (int i = PRE; i < R; ++i) dl_issue_slot<FMT, UPW, SPREAD>(u[i], rows, wave, i);
+    for (int i = PRE; i < R; ++i) dl_issue_slot<FMT, UPW, SPREAD, NB>(u[i], rows, wave, i);
     if constexpr (R >= UPW) after_issue();
     const Q4LaneConsts lc = q4k_lane_consts(dl_tid() & 3);
 #pragma unroll
     for (int i = 0; i < UPW; ++i) {
         __builtin_amdgcn_sched_barrier(0);
         float res[NG][RPW];
-        const uint32_t unit = dl_unit<SPREAD>(wave, i);
+        const uint32_t unit = dl_unit<SPREAD, NB>(wave, i);
         if constexpr (FMT == DL_FMT_Q6) {
             dl_dot_unit6(u[i], sm.g.xp, sm.g.xsum16, res);
         } else if constexpr (FMT == DL_FMT_Q4_TAIL6) {
@@ -761,7 +774,7 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
         if (i == 0) dl_stamp(out.tr, DL_TR_FIRST);
         dl_store_unit<NG, RPW, EPI>(out, unit, rows.n_rows, res, &sm.g.hold[(wave * UPW + i) * RPW]);
         __builtin_amdgcn_sched_barrier(0);
-        if (i + R < UPW) dl_issue_slot<FMT, UPW, SPREAD>(u[i + R], rows, wave, i + R);
+        if (i + R < UPW) dl_issue_slot<FMT, UPW, SPREAD, NB>(u[i + R], rows, wave, i + R);
         if (i + R == UPW - 1) after_issue();
     }
 }
@@ -784,9 +797,10 @@ __device__ __forceinline__ int dl_att_kpos(int lane, int t) {
     return 8 * (r >> 2) + 4 * t + (r & 3);
 }
 
+template <int SLOTS>
 __device__ __forceinline__ int dl_att_span(int L) {
-    // positions per wave: the kv head's L positions over its DL_ATT_SLOTS * DL_WAVES waves
-    return (L + DL_ATT_SLOTS * DL_WAVES - 1) / (DL_ATT_SLOTS * DL_WAVES);
+    // positions per wave: the kv head's L positions over its SLOTS * DL_WAVES waves
+    return (L + SLOTS * DL_WAVES - 1) / (SLOTS * DL_WAVES);
 }
 
 // Positions of the wave's span it covers: rows = clamp(L - p0, 0, span).
@@ -1071,7 +1085,7 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
     __syncthreads();
     if (tr != nullptr) dl_stamp(tr, DL_TR_A_MERGED);
     // block partial: [kvh][bs][g] = (M, l, o[128])
-    uint64_t* pb = a.part_ll + (((size_t)kvh * DL_ATT_SLOTS + bs) * GROUP) * (2 + DL_D);
+    uint64_t* pb = a.part_ll + (((size_t)kvh * S::ATT_SLOTS + bs) * GROUP) * (2 + DL_D);
     for (int idx = tid; idx < GROUP * 64; idx += DL_THREADS) {
         const int gg = idx >> 6, dl = idx & 63;
         float M = -INFINITY;
@@ -1108,19 +1122,19 @@ __device__ __forceinline__ void dl_attn_phase(DlAttnBank& bk, DlAttnLds<S::GROUP
     }
 }
 
-// Head hq = blockIdx.x (< NH): merge the DL_ATT_SLOTS block partials of its kv head.
+// Head hq (< NH): merge the S::ATT_SLOTS block partials of its kv head.
 template <class S>
 __device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP, S::pv_mfma>& sm, const DlArgs& a, int hq,
                                                uint32_t e_part, uint32_t e_attn, uint32_t site, uint64_t* tr) {
     constexpr int GROUP = S::GROUP;
     const int tid = dl_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kvh = hq / GROUP, gg = hq % GROUP;
-    constexpr int PER_WAVE = DL_ATT_SLOTS / DL_WAVES;  // 4 partials per wave
+    constexpr int PER_WAVE = S::ATT_SLOTS / DL_WAVES;  // partials per wave: 4 (1 with 64 blocks per sequence)
     __syncthreads();  // every wave is done with the previous phase's LDS
     uint64_t w[4 * PER_WAVE];
     const uint32_t polls = ll_wait(w, [&](int i) {
                 const int bs = wave * PER_WAVE + i / 4, k = i % 4;
-                const uint64_t* pg = a.part_ll + (((size_t)kvh * DL_ATT_SLOTS + bs) * GROUP + gg) * (2 + DL_D);
+                const uint64_t* pg = a.part_ll + (((size_t)kvh * S::ATT_SLOTS + bs) * GROUP + gg) * (2 + DL_D);
                 return k < 2 ? pg + k : pg + 2 + 2 * lane + (k - 2);
             },
             [&](int, uint64_t v) { return ll_ok32(v, e_part); }, a.status, site | DL_W_MERGE);
@@ -1170,10 +1184,19 @@ __device__ __forceinline__ void dl_merge_phase(DlAttnLds<S::GROUP, S::pv_mfma>& 
 
 // ------------------------------------------------------------- the kernel ----
 
+// The arguments of the 256 / NB sequences one launch runs (block b serves sequence b / NB).
+template <int NSEQ>
+struct DlArgsSet {
+    DlArgs s[NSEQ];
+};
+
 template <class S, bool TRACE>
-__global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs a) {
+__global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgsSet<S::NSEQ> as) {
     __shared__ __align__(16) DlShared<S> sm;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // this block's sequence and its place among that sequence's NB blocks
+    const int lb = blockIdx.x % S::NB;
+    const DlArgs& a = as.s[blockIdx.x / S::NB];
     // The launch counter (written by block 0 of the previous launch) and the
     // position (written by the token-store kernel) are read with agent-scope
     // atomic loads: a plain scalar load can return a stale copy on another XCD,
@@ -1190,7 +1213,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         const float inv_freq = exp2f(-(2.0f * (float)lane / (float)DL_D) * log2f(a.theta));
         sincosf((float)pos * inv_freq, &rope_sn, &rope_cs);
     }
-    const int kvh = blockIdx.x % 8, bs = blockIdx.x / 8;
+    const int kvh = lb % 8, bs = lb / 8;
 
     // The layer table is copied into LDS once.  Read from memory, each layer's
     // pointers would be a scalar-cache miss per launch, and a scalar load
@@ -1220,17 +1243,23 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
     auto down_rows = [&](uint32_t layer) { return make_rows(layer, DL_WDOWN, DL_WDOWN, S::HID); };
     // Up to DL_WAVES * DL_ATT_POS positions, block bs = 0 of each kv head covers them all (32 per wave) and
     // writes the normalised output itself: no partials, no merge phase and no hand-off into it.  Longer, the
-    // kv head's positions are spread over its DL_ATT_SLOTS blocks and merged per q head.
+    // kv head's positions are spread over its S::ATT_SLOTS blocks and merged per q head.
     const bool att_direct = L <= DL_WAVES * DL_ATT_POS;
     const bool att_block = !att_direct || bs == 0;
-    const int span = att_direct ? DL_ATT_POS : dl_att_span(L);
+    const int span = att_direct ? DL_ATT_POS : dl_att_span<S::ATT_SLOTS>(L);
     const int att_p0 = att_direct ? wave * DL_ATT_POS : (bs * DL_WAVES + wave) * span;
     const int att_rows = att_block ? dl_att_rows(L, att_p0, span) : 0;
     // phases with fewer units than waves spread them over the blocks
-    constexpr bool qkv_sp = S::QKV_ROWS / DlUnit<S::HSB, 1>::RPW < DL_NW;
-    constexpr bool o_sp = S::HID / DlUnit<S::QSB, 1>::RPW < DL_NW;
-    constexpr bool gu_sp = S::MLP / DlUnit<S::HSB, 2>::RPW < DL_NW;
-    constexpr bool dn_sp = S::HID / DlUnit<S::MSB, 1>::RPW < DL_NW;
+    constexpr int NB = S::NB;
+    constexpr bool qkv_sp = S::QKV_ROWS / DlUnit<S::HSB, 1>::RPW < S::NW;
+    constexpr bool o_sp = S::HID / DlUnit<S::QSB, 1>::RPW < S::NW;
+    constexpr bool gu_sp = S::MLP / DlUnit<S::HSB, 2>::RPW < S::NW;
+    constexpr bool dn_sp = S::HID / DlUnit<S::MSB, 1>::RPW < S::NW;
+    static_assert((S::QKV_ROWS / DlUnit<S::HSB, 1>::RPW + S::NW - 1) / S::NW <= S::qkv_u &&
+                      (S::HID / DlUnit<S::QSB, 1>::RPW + S::NW - 1) / S::NW <= S::o_u &&
+                      (S::MLP / DlUnit<S::HSB, 2>::RPW + S::NW - 1) / S::NW <= S::gu_u &&
+                      (S::HID / DlUnit<S::MSB, 1>::RPW + S::NW - 1) / S::NW <= S::dn_u,
+                  "units per wave cover every unit");
 
     auto issue_bank = [&](uint32_t layer, DlAttnBank& bk) {
         dl_attn_issue_k(bk, dl_gptr<const uint16_t>(layer_ptr(layer, DL_K_CACHE)), kvh, att_p0, att_rows);
@@ -1270,9 +1299,9 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         if (v6) {
             qrows.n_rows4 = S::QD + S::KVD;
             qrows.w6 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WV));
-            dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp, DL_FMT_Q4_TAIL6>(uq, qrows);
+            dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp, NB, DL_FMT_Q4_TAIL6>(uq, qrows);
         } else {
-            dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp, DL_FMT_Q4>(uq, qrows);
+            dl_issue_pre<S::HSB, 1, S::qkv_u, S::qkv_p, qkv_sp, NB, DL_FMT_Q4>(uq, qrows);
         }
         issue_bank(layer, bk);
         auto qkv_phase = [&](auto fmt) {
@@ -1301,24 +1330,24 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
                 dl_attn_phase<S>(bk, sm.at, a, lp, kvh, bs, att_p0, att_rows, att_direct, pos, rope_cs, rope_sn,
                                  e_qkv, att_direct ? e_attn : e_part, lsite, tr, [&] {
                                      if constexpr (o_early > 0)
-                                         dl_issue_pre<S::QSB, 1, S::o_u, o_early, o_sp>(uo, o_rows(layer));
+                                         dl_issue_pre<S::QSB, 1, S::o_u, o_early, o_sp, NB>(uo, o_rows(layer));
                                  });
             } else if constexpr (o_early > 0) {
-                dl_issue_pre<S::QSB, 1, S::o_u, o_early, o_sp>(uo, o_rows(layer));
+                dl_issue_pre<S::QSB, 1, S::o_u, o_early, o_sp, NB>(uo, o_rows(layer));
             }
             dl_stamp(tr, DL_TR_END);
         }
         // ---- attention merge (blocks 0..NH-1, one q head each)
-        if (!att_direct && blockIdx.x < S::NH) {
+        if (!att_direct && lb < S::NH) {
             uint64_t* tr = trp(2);
             dl_stamp(tr, DL_TR_BEGIN);
-            dl_merge_phase<S>(sm.at, a, blockIdx.x, e_part, e_attn, lsite, tr);
+            dl_merge_phase<S>(sm.at, a, lb, e_part, e_attn, lsite, tr);
             dl_stamp(tr, DL_TR_END);
         }
         // ---- o_proj + residual
         out.tr = trp(3);
         dl_stamp(out.tr, DL_TR_BEGIN);
-        if constexpr (o_early == 0) dl_issue_pre<S::QSB, 1, S::o_u, S::o_p, o_sp>(uo, o_rows(layer));
+        if constexpr (o_early == 0) dl_issue_pre<S::QSB, 1, S::o_u, S::o_p, o_sp, NB>(uo, o_rows(layer));
         out.ll32 = a.h_ll;
         out.plain = nullptr;
         out.hold.kind = first ? DL_SRC_PLAIN : DL_SRC_LL32;
@@ -1332,7 +1361,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         out.tr = trp(4);
         dl_stamp(out.tr, DL_TR_BEGIN);
         DlUnit<S::HSB, 2> ug[S::gu_u];
-        dl_issue_pre<S::HSB, 2, S::gu_u, S::gu_p, gu_sp>(ug, gu_rows(layer));
+        dl_issue_pre<S::HSB, 2, S::gu_u, S::gu_p, gu_sp, NB>(ug, gu_rows(layer));
         out.ll16 = a.act_ll;
         out.e_out = e_act;
         dl_gemv_phase<S::HSB, 2, S::gu_u, S::gu_r, S::gu_p, DL_EPI_SWIGLU, true, gu_sp>(
@@ -1351,7 +1380,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
         auto down_phase = [&](auto fmt) {
             constexpr int FMT = decltype(fmt)::value;
             DlUnit<S::MSB, 1> ud[S::dn_u];
-            dl_issue_pre<S::MSB, 1, S::dn_u, S::dn_p, dn_sp, FMT>(ud, down_rows(layer));
+            dl_issue_pre<S::MSB, 1, S::dn_u, S::dn_p, dn_sp, NB, FMT>(ud, down_rows(layer));
             dl_gemv_phase<S::MSB, 1, S::dn_u, S::dn_r, S::dn_p, DL_EPI_RESID, false, dn_sp, FMT>(
                 sm, ud, down_rows(layer), DL_SRC_LL16, a.act_ll, e_act, nullptr, a.eps, out, a.status,
                 lsite | DL_W_DOWN);
@@ -1362,9 +1391,9 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgs 
             down_phase(std::integral_constant<int, DL_FMT_Q4>());
         dl_stamp(out.tr, DL_TR_END);
     }
-    // Every block has read the launch counter before block 0 can get here: its
-    // last phase consumed every block's output.
-    if (blockIdx.x == 0 && threadIdx.x == 0)
+    // Every block of the sequence has read the launch counter before its block 0
+    // can get here: its last phase consumed every block's output.
+    if (lb == 0 && threadIdx.x == 0)
         __hip_atomic_store(a.ctl, seq + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -1452,16 +1481,15 @@ static bool dl_is(uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk, uint3
            d == (uint32_t)DL_D;
 }
 
+// One sequence's arguments over its workspace (laid out by dl_layout).
 template <class S>
-static int dl_launch(const uint64_t* layer_table, uint32_t n_layers, uint32_t s_cap, float* h,
-                     const int32_t* cache_position, float eps, float theta, void* workspace, size_t workspace_bytes,
-                     uint32_t* status, uint64_t* trace, void* stream) {
+static int dl_args(DlArgs& a, const uint64_t* layer_table, uint32_t n_layers, uint32_t s_cap, float* h,
+                   const int32_t* cache_position, float eps, float theta, void* workspace, size_t workspace_bytes,
+                   uint32_t* status, uint64_t* trace) {
     const DlLayout l = dl_layout<S>();
     if (workspace_bytes < l.total) return T2H_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return T2H_ERR_ALIGN;
-    if (!dl_grid_fits<S>()) return T2H_ERR_UNSUPPORTED;
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-    DlArgs a;
     a.layers = layer_table;
     a.n_layers = n_layers;
     a.h = h;
@@ -1477,12 +1505,46 @@ static int dl_launch(const uint64_t* layer_table, uint32_t n_layers, uint32_t s_
     a.part_ll = reinterpret_cast<uint64_t*>(ws + l.part);
     a.status = status;
     a.trace = trace;
+    return T2H_OK;
+}
+
+template <class S>
+static int dl_launch(const uint64_t* layer_table, uint32_t n_layers, uint32_t s_cap, float* h,
+                     const int32_t* cache_position, float eps, float theta, void* workspace, size_t workspace_bytes,
+                     uint32_t* status, uint64_t* trace, void* stream) {
+    static_assert(S::NSEQ == 1, "one sequence");
+    DlArgsSet<1> as;
+    const int rc = dl_args<S>(as.s[0], layer_table, n_layers, s_cap, h, cache_position, eps, theta, workspace,
+                              workspace_bytes, status, trace);
+    if (rc != T2H_OK) return rc;
+    if (!dl_grid_fits<S>()) return T2H_ERR_UNSUPPORTED;
     if (trace == nullptr)
         hipLaunchKernelGGL((decode_layers_kernel<S, false>), dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
-                           reinterpret_cast<hipStream_t>(stream), a);
+                           reinterpret_cast<hipStream_t>(stream), as);
     else
         hipLaunchKernelGGL((decode_layers_kernel<S, true>), dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
-                           reinterpret_cast<hipStream_t>(stream), a);
+                           reinterpret_cast<hipStream_t>(stream), as);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+// S::NSEQ sequences side by side, sequence i on blocks [i NB, (i + 1) NB).
+template <class S>
+static int dl_launch_seqs(const uint64_t* const* layer_tables, uint32_t n_layers, uint32_t s_cap, float* const* hs,
+                          const int32_t* const* cache_positions, float eps, float theta, void* const* workspaces,
+                          size_t workspace_bytes, uint32_t* const* statuses, void* stream) {
+    DlArgsSet<S::NSEQ> as;
+    for (int i = 0; i < S::NSEQ; ++i) {
+        if (!layer_tables[i] || !hs[i] || !cache_positions[i] || !workspaces[i] || !statuses[i]) return T2H_ERR_NULL;
+        const int rc = dl_args<S>(as.s[i], layer_tables[i], n_layers, s_cap, hs[i], cache_positions[i], eps, theta,
+                                  workspaces[i], workspace_bytes, statuses[i], nullptr);
+        if (rc != T2H_OK) return rc;
+        for (int j = 0; j < i; ++j)
+            if (workspaces[j] == workspaces[i]) return T2H_ERR_ARG;  // each sequence needs its own workspace
+    }
+    if (!dl_grid_fits<S>()) return T2H_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((decode_layers_kernel<S, false>), dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
+                       reinterpret_cast<hipStream_t>(stream), as);
     T2H_LAUNCH_CHECK();
     return T2H_OK;
 }
@@ -1552,4 +1614,25 @@ extern "C" int t2h_qwen3_decode_layers_traced(const uint64_t* layer_table, uint3
     if (reinterpret_cast<uintptr_t>(trace) % 8 != 0) return T2H_ERR_ALIGN;
     return dl_entry(layer_table, n_layers, hidden, mlp, nh, nk, d, s_cap, h, cache_position, eps, theta, workspace,
                     workspace_bytes, status, trace, stream);
+}
+
+extern "C" int t2h_qwen3_decode_layers_seqs(uint32_t n_seq, const uint64_t* const* layer_tables, uint32_t n_layers,
+                                            uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk, uint32_t d,
+                                            uint32_t s_cap, float* const* hs, const int32_t* const* cache_positions,
+                                            float eps, float theta, void* const* workspaces, size_t workspace_bytes,
+                                            uint32_t* const* statuses, void* stream) {
+    if (!layer_tables || !hs || !cache_positions || !workspaces || !statuses) return T2H_ERR_NULL;
+    if (n_seq == 1)
+        return t2h_qwen3_decode_layers(layer_tables[0], n_layers, hidden, mlp, nh, nk, d, s_cap, hs[0],
+                                       cache_positions[0], eps, theta, workspaces[0], workspace_bytes, statuses[0],
+                                       stream);
+    if (n_seq != (uint32_t)DlQwen3_0_6B_x4::NSEQ || !dl_is<DlQwen3_0_6B_x4>(hidden, mlp, nh, nk, d))
+        return T2H_ERR_UNSUPPORTED;
+    if (n_layers == 0) return T2H_OK;
+    if (n_layers > DL_MAX_LAYERS) return T2H_ERR_UNSUPPORTED;
+    if (s_cap == 0) return T2H_ERR_SHAPE;
+    constexpr uint32_t waves = DlQwen3_0_6B_x4::ATT_SLOTS * DL_WAVES;
+    if ((size_t)(s_cap + waves - 1) / waves > DL_ATT_POS) return T2H_ERR_UNSUPPORTED;  // over 32 positions a wave
+    return dl_launch_seqs<DlQwen3_0_6B_x4>(layer_tables, n_layers, s_cap, hs, cache_positions, eps, theta, workspaces,
+                                            workspace_bytes, statuses, stream);
 }

@@ -8,6 +8,8 @@ computes on the CPU: there is no fallback path.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from torch2vk_amd import _lib
@@ -660,6 +662,36 @@ def decode_layers_noalloc(table: torch.Tensor, h: torch.Tensor, cache_position: 
         raise ValueError(f"layer_table must be int64 [layers, {DECODE_LAYER_TABLE_COLUMNS}], got {tuple(table.shape)}")
     call("t2h_qwen3_decode_layers_noalloc", ptr(table), int(table.shape[0]), hidden, mlp, nh, nk, d, s_cap, ptr(h),
          ptr(cache_position), eps, theta, ptr(status), stream_handle())
+
+
+DECODE_SEQS = (1, 4)  # sequences one persistent launch can run (4: the Qwen3-0.6B shape, s_cap <= 2048)
+
+
+def decode_layers_seqs(tables: list[torch.Tensor], hs: list[torch.Tensor], cache_positions: list[torch.Tensor],
+                       workspaces: list[torch.Tensor], statuses: list[torch.Tensor], *, hidden: int, mlp: int,
+                       nh: int, nk: int, d: int, s_cap: int, eps: float = RMS_EPS, theta: float = 1.0e6) -> None:
+    """decode_layers for len(tables) sequences in one persistent launch (t2h_qwen3_decode_layers_seqs): each
+    sequence its own table (its KV caches), h, position, workspace and status."""
+    n = len(tables)
+    if n not in DECODE_SEQS or not (len(hs) == len(cache_positions) == len(workspaces) == len(statuses) == n):
+        raise ValueError(f"decode_layers_seqs runs {DECODE_SEQS} sequences with one of each argument per sequence")
+    for i in range(n):
+        _check(tables[i], "layer_table", torch.int64, align=8)
+        _check(hs[i], "h", torch.float32)
+        _check(cache_positions[i], "cache_position", torch.int32, align=4)
+        _check(workspaces[i], "workspace", torch.uint8, align=256)
+        _check(statuses[i], "status", torch.int32, align=4)
+        if tables[i].dim() != 2 or tables[i].shape != tables[0].shape or tables[i].shape[1] != DECODE_LAYER_TABLE_COLUMNS:
+            raise ValueError("layer tables must all be int64 [layers, 14]")
+        if workspaces[i].numel() != workspaces[0].numel():
+            raise ValueError("workspaces must all have the same size")
+    if len({w.data_ptr() for w in workspaces}) != n:
+        raise ValueError("every sequence needs its own workspace")
+    arr = lambda ts: (ctypes.c_void_p * n)(*[t.data_ptr() for t in ts])  # noqa: E731
+    t_arr, h_arr, p_arr, w_arr, s_arr = arr(tables), arr(hs), arr(cache_positions), arr(workspaces), arr(statuses)
+    call("t2h_qwen3_decode_layers_seqs", n, ctypes.addressof(t_arr), int(tables[0].shape[0]), hidden, mlp, nh, nk, d,
+         s_cap, ctypes.addressof(h_arr), ctypes.addressof(p_arr), eps, theta, ctypes.addressof(w_arr),
+         workspaces[0].numel(), ctypes.addressof(s_arr), stream_handle())
 
 
 DECODE_TRACE_PHASES = ("qkv", "attention", "merge", "o", "gate_up", "down")

@@ -241,6 +241,10 @@ class Qwen3Decoder:
         """One full greedy step: forward, select + store the token, advance the position."""
         self.run_decode_embed()
         self.run_decode_layers()
+        self.run_step_tail()
+
+    def run_step_tail(self) -> None:
+        """The end of a decode step after the layers: LM head, select + store the token, advance the position."""
         self._lm_head()
         kernels.token_select_store(self.partial_scores, self.partial_tokens, self.eos, self.next_token, self.done,
                                    self.generated, self.length, self.stopped, stop_on_eos=self.stop_on_eos,
@@ -458,3 +462,80 @@ class Qwen3Decoder:
         else:
             self.prefill_embeds(embeds)
         return self._finish(max_new_tokens, steps_per_graph, use_graph)
+
+
+class Qwen3DecoderGroup:
+    """Several persistent decoders (each with its own KV cache, position and tokens; typically one set of
+    weights) stepped together: one persistent launch runs every sequence's layers
+    (t2h_qwen3_decode_layers_seqs), then each sequence's embedding, LM head and token store run as usual.
+    Built for 4 sequences of the Qwen3-0.6B shape, as in the Qwen3-ASR job's utterances."""
+
+    def __init__(self, decoders: list[Qwen3Decoder]) -> None:
+        if len(decoders) not in kernels.DECODE_SEQS:
+            raise ValueError(f"a group runs {kernels.DECODE_SEQS} sequences, got {len(decoders)}")
+        d0 = decoders[0]
+        for d in decoders:
+            if not d.persistent:
+                raise ValueError("every decoder of a group must run the persistent kernel")
+            if d.config != d0.config or d.max_positions != d0.max_positions or d.device != d0.device:
+                raise ValueError("a group's decoders must share the shape, KV capacity and device")
+        self.decoders = decoders
+        self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+
+    def run_decode_layers(self) -> None:
+        ds, c = self.decoders, self.decoders[0].config
+        kernels.decode_layers_seqs([d.layer_table for d in ds], [d.h for d in ds], [d.position for d in ds],
+                                   [d.layers_ws for d in ds], [d.status for d in ds], hidden=c.hidden, mlp=c.mlp,
+                                   nh=c.heads, nk=c.kv_heads, d=c.head_dim, s_cap=ds[0].max_positions,
+                                   eps=c.rms_eps, theta=c.rope_theta)
+
+    def decode_step(self) -> None:
+        for d in self.decoders:
+            d.run_decode_embed()
+        self.run_decode_layers()
+        for d in self.decoders:
+            d.run_step_tail()
+
+    def graph(self, steps: int) -> torch.cuda.CUDAGraph:
+        """A graph of ``steps`` consecutive group decode steps (captured once per step count)."""
+        if steps not in self._graphs:
+            saved = [d._save_state() for d in self.decoders]
+            dev = self.decoders[0].device
+            side = torch.cuda.Stream(device=dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                self.decode_step()  # warm-up launch outside capture
+            torch.cuda.current_stream(dev).wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(steps):
+                    self.decode_step()
+            for d, st in zip(self.decoders, saved):
+                d._restore_state(st)
+            self._graphs[steps] = g
+        return self._graphs[steps]
+
+    def run_steps(self, n: int, steps_per_graph: int = 8, use_graph: bool = True) -> None:
+        if not use_graph:
+            for _ in range(n):
+                self.decode_step()
+            return
+        full, rest = divmod(n, steps_per_graph)
+        if full:
+            g = self.graph(steps_per_graph)
+            for _ in range(full):
+                g.replay()
+        for _ in range(rest):
+            self.decode_step()
+
+    def finish(self, max_new_tokens: int, steps_per_graph: int = 8, use_graph: bool = True) -> list[list[int]]:
+        """After every decoder's prefill (which stored its first token): the remaining tokens of all of them
+        together; each sequence's generated ids."""
+        for d in self.decoders:
+            d._check_budget(int(d.position.item()), max_new_tokens)
+        self.run_steps(max_new_tokens - 1, steps_per_graph=steps_per_graph, use_graph=use_graph)
+        out = []
+        for d in self.decoders:
+            d.check_status()
+            out.append(d.generated[:int(d.length.item())].tolist())
+        return out
