@@ -1034,13 +1034,13 @@ def bench_asr(args) -> int:
     tw = synthetic_weights(tcfg, device=dev, seed=2)
     prefix, suffix = [151644, 8948, 198, 151669], [151670, 151645, 198]
     prompt_len = len(prefix) + frames + len(suffix)
-    # one decoder (KV cache) per utterance; their decode steps run together, all 4 sequences' layers in one
-    # persistent launch
-    decs = [Qwen3Decoder(tw, max_positions=prompt_len + new_tokens + 16, max_new_tokens=new_tokens + 8, device=dev)
-            for _ in range(nb)]
+    # one decoder (KV cache) per utterance: their prompts prefill as one batch and their decode steps run
+    # together, all 4 sequences' layers in one persistent launch
+    group = Qwen3DecoderGroup.create(tw, nb, max_positions=prompt_len + new_tokens + 16,
+                                     max_new_tokens=new_tokens + 8, device=dev)
+    decs = group.decoders
     for dec in decs:
         dec.stop_on_eos = False
-    group = Qwen3DecoderGroup(decs)
     ids = torch.tensor(prefix + [ecfg_audio_id()] * frames + suffix, device=dev)
     audio_pos = torch.arange(len(prefix), len(prefix) + frames, device=dev)
     h = torch.empty_like(feats_in)
@@ -1056,10 +1056,12 @@ def bench_asr(args) -> int:
     def step() -> None:
         feats = encode()
         transcripts.clear()
+        embs = []
         for b, dec in enumerate(decs):
             emb = dec.embed_tokens(ids)
             run_audio_inject(emb, audio_pos, feats[b * frames:(b + 1) * frames])
-            dec.prefill_chunked(embeds=emb, chunk=2048)
+            embs.append(emb)
+        group.prefill_chunked(embs, chunk=2048)
         transcripts.extend(group.finish(new_tokens))
 
     per_step = _timed_steps(step, args.warmup, args.steps)
@@ -1108,9 +1110,9 @@ def bench_asr(args) -> int:
         "config": {
             "workload": "4 utterances x 1500 frames: encoder (24 layers, hidden 1024, 16 heads, FFN 4096, "
                         "attention within each utterance) + ln_post/proj1/proj2, then per utterance the audio "
-                        "states injected into a 1507-position prompt and chunked prefill, and 64 greedy tokens of "
-                        "the 4 utterances decoded together (Qwen3-0.6B shape, uniform Q4_K, one persistent launch "
-                        "for the 4 sequences' layers per step, HIP graphs of 8 steps)",
+                        "states injected into a 1507-position prompt, the 4 prompts prefilled as one batch, and 64 "
+                        "greedy tokens of the 4 utterances decoded together (Qwen3-0.6B shape, uniform Q4_K, one "
+                        "persistent launch for the 4 sequences' layers per step, HIP graphs of 8 steps)",
             "batch": nb, "frames": frames, "decoder_tokens": new_tokens,
         },
         "encoder_ms": round(enc_s * 1e3, 3),

@@ -128,3 +128,37 @@ def test_group_rejects_bad_arguments(device, small_06b):
     with pytest.raises(RuntimeError):
         kernels.decode_layers_seqs([d.layer_table for d in ds], [d.h for d in ds], [d.position for d in ds],
                                    [d.layers_ws for d in ds], [d.status for d in ds], **{**args, "s_cap": 4096})
+
+
+def test_group_batched_prefill_matches_each_prefill(device, small_06b):
+    """Four equal-length prompts of input embeddings prefilled as one batch (Qwen3DecoderGroup.create's
+    layer-major caches) against each decoder's own chunked prefill, chunks of 64 over 150 positions: the same
+    products, summed in another order where the single prefill's small GEMMs split K, so the caches and the
+    last hidden state agree to bf16 rounding; the first tokens and 6 more of group decode against the oracle."""
+    from torch2vk_amd.qwen3.model import Qwen3DecoderGroup
+
+    cfg, w, shape, dense = small_06b
+    group = Qwen3DecoderGroup.create(w, 4, max_positions=256, max_new_tokens=24, device=device)
+    for d in group.decoders:
+        d.stop_on_eos = False
+    single = _decoders(w, 4, 256)
+    rng = np.random.default_rng(9)
+    prompts = [rng.integers(0, cfg.vocab, 150).tolist() for _ in range(4)]
+    embs = [group.decoders[0].embed_tokens(torch.tensor(p, device=device)) for p in prompts]
+    group.prefill_chunked(embs, chunk=64)
+    for d, e in zip(single, embs):
+        d.prefill_chunked(embeds=e, chunk=64)
+    torch.cuda.synchronize()
+    for a, b in zip(group.decoders, single):
+        for ca, cb in ((a.k_cache[:, :150], b.k_cache[:, :150]), (a.v_cache[:, :150], b.v_cache[:, :150])):
+            # layer 0 sees the same inputs: its rows agree to one bf16 rounding of a reordered fp32 sum
+            d0 = (ca[0].float() - cb[0].float()).abs()
+            assert (d0 <= 2 ** -7 * cb[0].float().abs() + 1e-3).all(), d0.max().item()
+            # layer 1 inherits layer 0's bf16-level differences through attention, o_proj and the MLP
+            d1 = (ca[1].float() - cb[1].float()).abs().max().item()
+            assert d1 <= 1e-2 * cb[1].float().abs().max().item(), d1
+        assert int(a.position.item()) == int(b.position.item()) == 150
+    toks = group.finish(7, steps_per_graph=4, use_graph=True)
+    for p, tk in zip(prompts, toks):
+        assert len(tk) == 7
+        print(check_greedy_tokens(shape, dense, p, tk, tie_tol=5e-3), flush=True)

@@ -61,7 +61,8 @@ class Qwen3Decoder:
     applies: on MI355X it saves the launch and ramp of ~250 kernels per token."""
 
     def __init__(self, weights: Qwen3Weights, *, max_positions: int, max_new_tokens: int, device=None,
-                 persistent: bool | None = None) -> None:
+                 persistent: bool | None = None,
+                 kv_cache: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
         c = weights.config
         self.config: Qwen3Config = c
         self.weights = weights
@@ -71,8 +72,18 @@ class Qwen3Decoder:
         self.device = dev
         self.max_positions = max_positions
         bf, f32 = torch.bfloat16, torch.float32
-        self.k_cache = torch.zeros(c.layers, max_positions, c.kv_heads, c.head_dim, dtype=bf, device=dev)
-        self.v_cache = torch.zeros_like(self.k_cache)
+        if kv_cache is None:
+            self.k_cache = torch.zeros(c.layers, max_positions, c.kv_heads, c.head_dim, dtype=bf, device=dev)
+            self.v_cache = torch.zeros_like(self.k_cache)
+        else:
+            # caller-owned bf16 [layers, max_positions, kv_heads, head_dim] views, each layer's rows contiguous
+            # (a Qwen3DecoderGroup's layer-major caches)
+            want = (c.layers, max_positions, c.kv_heads, c.head_dim)
+            for t in kv_cache:
+                if (tuple(t.shape) != want or t.dtype != bf or t.device != dev or not t[0].is_contiguous()
+                        or t.stride(1) != c.kv_heads * c.head_dim):
+                    raise ValueError(f"kv_cache tensors must be bf16 {want} on {dev} with contiguous layers")
+            self.k_cache, self.v_cache = kv_cache
         self.h = torch.zeros(c.hidden, dtype=f32, device=dev)
         self.q = torch.zeros(c.q_dim, dtype=f32, device=dev)
         self.k = torch.zeros(c.kv_dim, dtype=f32, device=dev)
@@ -468,7 +479,23 @@ class Qwen3DecoderGroup:
     """Several persistent decoders (each with its own KV cache, position and tokens; typically one set of
     weights) stepped together: one persistent launch runs every sequence's layers
     (t2h_qwen3_decode_layers_seqs), then each sequence's embedding, LM head and token store run as usual.
-    Built for 4 sequences of the Qwen3-0.6B shape, as in the Qwen3-ASR job's utterances."""
+    Built for 4 sequences of the Qwen3-0.6B shape, as in the Qwen3-ASR job's utterances.  A group made by
+    ``create`` keeps its sequences' caches layer-major ([layers, n_seq, positions, kv heads, dim]), so equal-
+    length prompts can also be prefilled as one batch (``prefill_chunked``)."""
+
+    @classmethod
+    def create(cls, weights: Qwen3Weights, n_seq: int, *, max_positions: int, max_new_tokens: int,
+               device=None) -> "Qwen3DecoderGroup":
+        c = weights.config
+        dev = torch.device(device) if device is not None else weights.packed["embed"].device
+        shape = (c.layers, n_seq, max_positions, c.kv_heads, c.head_dim)
+        k = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+        v = torch.zeros_like(k)
+        decs = [Qwen3Decoder(weights, max_positions=max_positions, max_new_tokens=max_new_tokens, device=dev,
+                             persistent=True, kv_cache=(k[:, b], v[:, b])) for b in range(n_seq)]
+        group = cls(decs)
+        group.k_cache, group.v_cache = k, v
+        return group
 
     def __init__(self, decoders: list[Qwen3Decoder]) -> None:
         if len(decoders) not in kernels.DECODE_SEQS:
@@ -481,6 +508,80 @@ class Qwen3DecoderGroup:
                 raise ValueError("a group's decoders must share the shape, KV capacity and device")
         self.decoders = decoders
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self.k_cache: torch.Tensor | None = None  # layer-major caches of a group made by create()
+        self.v_cache: torch.Tensor | None = None
+
+    def _prefill_layer(self, i: int, h: torch.Tensor, n_seq: int, start: int) -> None:
+        """Qwen3Decoder._prefill_layer for n_seq sequences of n tokens each (h [n_seq n, hidden], sequence-major
+        rows) at positions start..: the GEMMs and norms over all rows at once, the q/k prologue into every
+        sequence's cache in one launch, and causal flash attention over the batch of caches."""
+        d0 = self.decoders[0]
+        c, t, p = d0.config, d0.types, f"layers.{i}."
+        rows = h.shape[0]
+        n = rows // n_seq
+        x = kernels.rms_norm(h, d0._n(p + "input_norm"),
+                             out=torch.empty(rows, c.hidden, dtype=torch.bfloat16, device=d0.device), eps=c.rms_eps)
+        fused = d0._fused_qkv(i)
+        if fused is not None:
+            qkv = kernels.quantized_linear(x, fused, t[p + "q"], out_dtype=torch.float32)
+            q, k, v = qkv[:, :c.q_dim], qkv[:, c.q_dim:c.q_dim + c.kv_dim], qkv[:, c.q_dim + c.kv_dim:]
+        else:
+            q, k, v = (kernels.quantized_linear(x, d0._w(p + nm), t[p + nm], out_dtype=torch.float32)
+                       for nm in ("q", "k", "v"))
+        qb = torch.empty(rows, c.heads, c.head_dim, dtype=torch.bfloat16, device=d0.device)
+        kernels.qk_norm_rope_cache(q, k, v, qb, self.k_cache[i], self.v_cache[i], start,
+                                   q_norm_weight=d0._n(p + "q_norm"), k_norm_weight=d0._n(p + "k_norm"),
+                                   theta=c.rope_theta, eps=c.rms_eps)
+        keys = self.k_cache[i, :, :start + n]
+        vals = self.v_cache[i, :, :start + n]
+        attn = kernels.flash_attn_prefill(qb.view(n_seq, n, c.heads, c.head_dim), keys, vals, causal=True,
+                                          causal_offset=start)
+        kernels.quantized_linear(attn.view(rows, c.q_dim), d0._w(p + "o"), t[p + "o"], out=h, residual=h)
+        x = kernels.rms_norm(h, d0._n(p + "post_norm"), out=x, eps=c.rms_eps)
+        if t[p + "gate"] == t[p + "up"]:
+            act = kernels.gemm_swiglu(x, d0._w(p + "gate"), d0._w(p + "up"), t[p + "gate"])
+        else:
+            gate = kernels.quantized_linear(x, d0._w(p + "gate"), t[p + "gate"], out_dtype=torch.float32)
+            up = kernels.quantized_linear(x, d0._w(p + "up"), t[p + "up"], out_dtype=torch.float32)
+            act = kernels.swiglu(gate, up)
+            del gate, up
+        kernels.quantized_linear(act, d0._w(p + "down"), t[p + "down"], out=h, residual=h)
+
+    def prefill_chunked(self, embeds: list[torch.Tensor], *, start: int = 0, chunk: int = 2048) -> None:
+        """Every sequence's prompt of input embeddings (fp32 [T, hidden], the same T for all) through the
+        matrix-core prefill as one batch, ``chunk`` positions at a time; then, per sequence, the last token's
+        final norm, LM head and greedy select, and the first generated token stored (as
+        Qwen3Decoder.prefill_chunked, which a group of one equals)."""
+        if self.k_cache is None:
+            raise ValueError("batched prefill needs a group made by Qwen3DecoderGroup.create")
+        ds, c = self.decoders, self.decoders[0].config
+        if len(embeds) != len(ds):
+            raise ValueError(f"one prompt per sequence: {len(ds)}, got {len(embeds)}")
+        e = [x.reshape(-1, c.hidden) for x in embeds]
+        total = e[0].shape[0]
+        if total == 0 or any(x.shape[0] != total for x in e):
+            raise ValueError("the prompts must be non-empty and of one length")
+        if any(x.dtype != torch.float32 or x.device != ds[0].device for x in e):
+            raise ValueError("embeds must be fp32 on the decoders' device")
+        if start + total > ds[0].max_positions:
+            raise ValueError("prompt exceeds the KV cache capacity")
+        if chunk <= 0:
+            raise ValueError("chunk must be positive")
+        n_seq = len(ds)
+        stacked = torch.stack(e)  # [n_seq, T, hidden]
+        for d in ds:
+            d.reset(position=start)
+        for c0 in range(0, total, chunk):
+            n = min(chunk, total - c0)
+            h = stacked[:, c0:c0 + n].reshape(n_seq * n, c.hidden).clone()
+            for i in range(c.layers):
+                self._prefill_layer(i, h, n_seq, start + c0)
+        last = h.view(n_seq, -1, c.hidden)[:, -1]
+        for b, d in enumerate(ds):
+            d.h.copy_(last[b])
+            d.position.fill_(start + total - 1)
+            d.run_lm_head_select()
+            d.run_token_store(advance=True)
 
     def run_decode_layers(self) -> None:
         ds, c = self.decoders, self.decoders[0].config
