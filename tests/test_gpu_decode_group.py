@@ -162,3 +162,29 @@ def test_group_batched_prefill_matches_each_prefill(device, small_06b):
     for p, tk in zip(prompts, toks):
         assert len(tk) == 7
         print(check_greedy_tokens(shape, dense, p, tk, tie_tol=5e-3), flush=True)
+
+
+def test_group_q4_k_m_equals_one_launch_each(device):
+    """Q4_K_M weights (layer 1 of 2 with Q6_K v and down rows) in the 4-sequence launch: at 64 blocks per
+    sequence a Q6_K v lands in each wave's second Q|K|V slot and the Q6_K down units spread over the blocks;
+    short prompts keep every position under 256 keys, so tokens, h and caches equal the single launches'."""
+    from torch2vk_amd.qwen3.config import QWEN3_0_6B
+    from torch2vk_amd.qwen3.model import Qwen3DecoderGroup
+    from torch2vk_amd.qwen3.weights import synthetic_weights
+
+    cfg = replace(QWEN3_0_6B, layers=2, vocab=4096, eos_token_ids=(4095,))
+    w = synthetic_weights(cfg, device=device, seed=21, std=0.02, norm_std=0.1, policy="q4_k_m")
+    assert (w.types["layers.1.v"], w.types["layers.1.down"]) == ("q6_k", "q6_k")
+    rng = np.random.default_rng(8)
+    prompts = [rng.integers(0, cfg.vocab, n).tolist() for n in (6, 3, 10, 8)]
+    single = _decoders(w, 4, 128)
+    ref = [d.generate(torch.tensor(p), 10, steps_per_graph=4, use_graph=True) for d, p in zip(single, prompts)]
+    group = _decoders(w, 4, 128)
+    for d, p in zip(group, prompts):
+        d.prefill(torch.tensor(p))
+    got = Qwen3DecoderGroup(group).finish(10, steps_per_graph=4, use_graph=True)
+    print(f"group {got}\nsingle {ref}", flush=True)
+    assert got == ref
+    for a, b in zip(group, single):
+        torch.testing.assert_close(a.h, b.h, rtol=0, atol=0)
+        torch.testing.assert_close(a.v_cache, b.v_cache, rtol=0, atol=0)

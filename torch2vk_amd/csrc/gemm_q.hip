@@ -503,59 +503,6 @@ static int gemm_q_launch(const void* x, const void* w, const float* bias, int ac
     return T2H_OK;
 }
 
-}  // namespace t2h
-
-using namespace t2h;
-
-extern "C" int t2h_q8_0_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
-                             uint32_t k, uint32_t n, void* stream) {
-    return gemm_q_launch<GemmQ80>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
-}
-
-extern "C" int t2h_q4k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
-                            uint32_t k, uint32_t n, void* stream) {
-    return gemm_q_launch<GemmQ4K>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
-}
-
-extern "C" int t2h_q8_0_linear(const void* x, const void* w, const float* bias, int act, void* y, int out_dtype,
-                               const float* residual, uint32_t m, uint32_t k, uint32_t n, uint32_t w_k,
-                               void* stream) {
-    return gemm_q_launch<GemmQ80>(x, w, bias, act, y, out_dtype, residual, m, k, n, w_k, stream);
-}
-
-extern "C" int t2h_q6k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
-                            uint32_t k, uint32_t n, void* stream) {
-    return gemm_q_launch<GemmQ6K>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
-}
-
-// y[m, n_ff] = bf16(silu(x . deq(W_gate)^T) * (x . deq(W_up)^T)): the prefill MLP's gate and up products
-// in one launch, SwiGLU applied in the epilogue (no fp32 gate/up intermediates).
-template <class F>
-static int gemm_swiglu_launch(const void* x, const void* w_gate, const void* w_up, void* y, uint32_t m, uint32_t k,
-                              uint32_t n_ff, void* stream) {
-    if (!x || !w_gate || !w_up || !y) return T2H_ERR_NULL;
-    if (k == 0 || k % GQ_BK != 0 || k % F::BLOCK_VALUES != 0) return T2H_ERR_SHAPE;
-    if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) return T2H_ERR_ALIGN;
-    if (((reinterpret_cast<uintptr_t>(w_gate) | reinterpret_cast<uintptr_t>(w_up)) & (F::ALIGN - 1)) != 0)
-        return T2H_ERR_ALIGN;
-    if (n_ff > 0x3fffffffu) return T2H_ERR_SHAPE;
-    if (m == 0 || n_ff == 0) return T2H_OK;
-    GemmArgs a = {};
-    a.a = reinterpret_cast<const uint16_t*>(x);
-    a.w = reinterpret_cast<const uint8_t*>(w_gate);
-    a.w_up = reinterpret_cast<const uint8_t*>(w_up);
-    a.c = y;
-    a.m = m;
-    a.k = k;
-    a.n_ff = n_ff;
-    a.n = 2 * n_ff;
-    a.w_blocks = k / F::BLOCK_VALUES;
-    a.row_bytes = a.w_blocks * F::BLOCK_BYTES;
-    gemm_q_dispatch<F, GQEPI_SWIGLU>(a, reinterpret_cast<hipStream_t>(stream));
-    T2H_LAUNCH_CHECK();
-    return T2H_OK;
-}
-
 // ---------------------------------------------------------------- split-K ----
 
 // out = epilogue(sum over the splits of partial[s]) in split order.  Plain: y[row][col] from partial column
@@ -661,6 +608,59 @@ static int gemm_splitk_launch(const void* x, const void* w, const void* w_up, co
     hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s,
                        reinterpret_cast<const float*>(partials), used, m, n_cols, n, a.n_ff, bias, act, y, out_dtype,
                        residual);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+}  // namespace t2h
+
+using namespace t2h;
+
+extern "C" int t2h_q8_0_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                             uint32_t k, uint32_t n, void* stream) {
+    return gemm_q_launch<GemmQ80>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
+}
+
+extern "C" int t2h_q4k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                            uint32_t k, uint32_t n, void* stream) {
+    return gemm_q_launch<GemmQ4K>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
+}
+
+extern "C" int t2h_q8_0_linear(const void* x, const void* w, const float* bias, int act, void* y, int out_dtype,
+                               const float* residual, uint32_t m, uint32_t k, uint32_t n, uint32_t w_k,
+                               void* stream) {
+    return gemm_q_launch<GemmQ80>(x, w, bias, act, y, out_dtype, residual, m, k, n, w_k, stream);
+}
+
+extern "C" int t2h_q6k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                            uint32_t k, uint32_t n, void* stream) {
+    return gemm_q_launch<GemmQ6K>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
+}
+
+// y[m, n_ff] = bf16(silu(x . deq(W_gate)^T) * (x . deq(W_up)^T)): the prefill MLP's gate and up products
+// in one launch, SwiGLU applied in the epilogue (no fp32 gate/up intermediates).
+template <class F>
+static int gemm_swiglu_launch(const void* x, const void* w_gate, const void* w_up, void* y, uint32_t m, uint32_t k,
+                              uint32_t n_ff, void* stream) {
+    if (!x || !w_gate || !w_up || !y) return T2H_ERR_NULL;
+    if (k == 0 || k % GQ_BK != 0 || k % F::BLOCK_VALUES != 0) return T2H_ERR_SHAPE;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) != 0) return T2H_ERR_ALIGN;
+    if (((reinterpret_cast<uintptr_t>(w_gate) | reinterpret_cast<uintptr_t>(w_up)) & (F::ALIGN - 1)) != 0)
+        return T2H_ERR_ALIGN;
+    if (n_ff > 0x3fffffffu) return T2H_ERR_SHAPE;
+    if (m == 0 || n_ff == 0) return T2H_OK;
+    GemmArgs a = {};
+    a.a = reinterpret_cast<const uint16_t*>(x);
+    a.w = reinterpret_cast<const uint8_t*>(w_gate);
+    a.w_up = reinterpret_cast<const uint8_t*>(w_up);
+    a.c = y;
+    a.m = m;
+    a.k = k;
+    a.n_ff = n_ff;
+    a.n = 2 * n_ff;
+    a.w_blocks = k / F::BLOCK_VALUES;
+    a.row_bytes = a.w_blocks * F::BLOCK_BYTES;
+    gemm_q_dispatch<F, GQEPI_SWIGLU>(a, reinterpret_cast<hipStream_t>(stream));
     T2H_LAUNCH_CHECK();
     return T2H_OK;
 }
