@@ -419,21 +419,35 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
         const float bj = a.bias != nullptr && col < a.n ? a.bias[col] : 0.0f;
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
+            // the tile's 16 residual values first, then its 16 results, then the 16 stores, each in registers
+            // of their own: element by element, the loads (which may alias the output) and the stores
+            // serialised on the memory round trip
+            float rv[16];
+            if constexpr (EPI == GQEPI_RESID) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t row = row_base + i * 32 + (e >> 2) * 8 + (e & 3);
+                    rv[e] = row < a.m && col < a.n ? a.residual[(size_t)row * a.n + col] : 0.0f;
+                }
+            }
+            float ov[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                float v = acc[i][j][e] + bj;
+                if (a.act == GQACT_GELU) v = gelu_erf(v);
+                ov[e] = EPI == GQEPI_RESID ? rv[e] + v : v;
+            }
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const uint32_t row = row_base + i * 32 + (e >> 2) * 8 + (e & 3);
                 if (row < a.m && col < a.n) {
                     const size_t idx = (size_t)row * a.n + col;
-                    float v = acc[i][j][e] + bj;
-                    if (a.act == GQACT_GELU) v = gelu_erf(v);
-                    if constexpr (EPI == GQEPI_F32 || EPI == GQEPI_GATED_F32) {
-                        // split s of a split-K launch: its own m x n slice
-                        reinterpret_cast<float*>(a.c)[(size_t)blockIdx.y * a.m * a.n + idx] = v;
-                    } else if constexpr (EPI == GQEPI_BF16) {
-                        reinterpret_cast<uint16_t*>(a.c)[idx] = (uint16_t)f32_to_bf16_bits(v);
-                    } else {
-                        reinterpret_cast<float*>(a.c)[idx] = a.residual[idx] + v;
-                    }
+                    if constexpr (EPI == GQEPI_BF16)
+                        reinterpret_cast<uint16_t*>(a.c)[idx] = (uint16_t)f32_to_bf16_bits(ov[e]);
+                    else if constexpr (EPI == GQEPI_RESID)
+                        reinterpret_cast<float*>(a.c)[idx] = ov[e];
+                    else  // fp32 products; split s of a split-K launch writes its own m x n slice
+                        reinterpret_cast<float*>(a.c)[(size_t)blockIdx.y * a.m * a.n + idx] = ov[e];
                 }
             }
         }
