@@ -93,6 +93,16 @@ int t2h_q4k_lm_head_argmax_partial(const void* x, const float* norm_w, float eps
                                    uint32_t n, float* partial_scores, uint32_t* partial_tokens,
                                    uint32_t num_partials, void* stream);
 
+/* t2h_q4k_lm_head_argmax_partial with the final RMSNorm fused, for n_seq (1..4) sequences that decode
+ * together: the head's rows are read once, and sequence i's fp32 residual stream h[i] gives its own
+ * num_partials (score, token) pairs in partial_scores[i] / partial_tokens[i], bit-identical to the
+ * single-sequence call.  k is 1024 or 4096 (other k: T2H_ERR_UNSUPPORTED).
+ * replaces one LM_HEAD_Q6_K_ARGMAX_PARTIAL_F16 dispatch per sequence (src/models/optimized_qwen3/run.py:116-122,
+ * _run_lm_head_select, called once per decode step at run.py:162) for the sequences of a batched decode. */
+int t2h_q4k_lm_head_argmax_partial_seqs(uint32_t n_seq, const float* const* h, const float* norm_w, float eps,
+                                        const void* w, uint32_t k, uint32_t n, float* const* partial_scores,
+                                        uint32_t* const* partial_tokens, uint32_t num_partials, void* stream);
+
 /* Q6_K GEMV: y[m, n] = x[m, k] . deq(W)^T (+ residual), x bf16, k % 256 == 0,
  * k <= 12288 (longer rows: T2H_ERR_UNSUPPORTED).
  * replaces LINEAR_NOBIAS_Q6_K_MATVEC_F32 (src/models/quantized_qwen3/shaders/linear_nobias_q6_k_matvec_f32.py:20-193)

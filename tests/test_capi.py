@@ -73,6 +73,15 @@ def test_argument_validation_returns_status(lib):
     assert lib.t2h_q8_0_matvec(None, fake, fake, 0, None, 1, 1024, 16, None) == 1
     assert lib.t2h_q6k_rmsnorm_matvec(fake, None, 1e-6, fake, fake, 0, 1024, 16, None) == 1
     assert lib.t2h_q6k_lm_head_argmax_partial(fake, None, 1e-6, fake, 4096, 100, fake, fake, 0, None) == 5
+    # the LM head of several sequences: sequence count, built k, row multiple, partial count, null arrays
+    arr = (ctypes.c_void_p * 4)(fake, fake, fake, fake)
+    pa = ctypes.addressof(arr)
+    assert lib.t2h_q4k_lm_head_argmax_partial_seqs(0, pa, fake, 1e-6, fake, 1024, 64, pa, pa, 8, None) == 5
+    assert lib.t2h_q4k_lm_head_argmax_partial_seqs(5, pa, fake, 1e-6, fake, 1024, 64, pa, pa, 8, None) == 5
+    assert lib.t2h_q4k_lm_head_argmax_partial_seqs(2, pa, fake, 1e-6, fake, 2048, 64, pa, pa, 8, None) == 4
+    assert lib.t2h_q4k_lm_head_argmax_partial_seqs(2, pa, fake, 1e-6, fake, 1024, 66, pa, pa, 8, None) == 2
+    assert lib.t2h_q4k_lm_head_argmax_partial_seqs(2, pa, fake, 1e-6, fake, 1024, 64, pa, pa, 0, None) == 5
+    assert lib.t2h_q4k_lm_head_argmax_partial_seqs(2, None, fake, 1e-6, fake, 1024, 64, pa, pa, 8, None) == 1
 
 
 def test_python_wrappers_reject_host_tensors():

@@ -146,6 +146,42 @@ def test_q4k_rmsnorm_swiglu(device, k, n):
     assert_close(out.float().cpu().numpy(), ref, max_abs=2e-2 * np.abs(ref).max(), min_cos=0.9995, what="swiglu")
 
 
+
+@pytest.mark.parametrize("k,n,g", [(1024, 5000, 64), (1024, 151936, 512), (4096, 20000, 96)])
+def test_lm_head_seqs_equals_each_sequence(device, k, n, g):
+    """The LM head of 1..4 sequences in one launch: every sequence's partial (score, token) pairs are
+    bit-identical to its own single-sequence launch, including a tie between two equal rows (the lower id)."""
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(k + n)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w[n // 2 + 1] = w[n // 2]  # equal rows: equal scores, the lower token wins
+    wt = torch.from_numpy(oracle.quantize_q4_k(w)).to(device)
+    nw = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)).to(device)
+    hs = [torch.from_numpy((rng.standard_normal(k) * (1 + i)).astype(np.float32)).to(device) for i in range(4)]
+    for n_seq in (1, 2, 3, 4):
+        ps = [torch.full((g,), 7.0, dtype=torch.float32, device=device) for _ in range(n_seq)]
+        pt = [torch.full((g,), 7, dtype=torch.int32, device=device) for _ in range(n_seq)]
+        kernels.q4k_lm_head_argmax_partial_seqs(hs[:n_seq], wt, ps, pt, norm_weight=nw)
+        for i in range(n_seq):
+            rs = torch.empty(g, dtype=torch.float32, device=device)
+            rt = torch.empty(g, dtype=torch.int32, device=device)
+            kernels.q4k_lm_head_argmax_partial(hs[i], wt, rs, rt, norm_weight=nw)
+            assert torch.equal(ps[i].view(torch.int32), rs.view(torch.int32)), (n_seq, i)
+            assert torch.equal(pt[i], rt), (n_seq, i)
+    # the tie: a sequence whose best row is one of the equal pair picks the lower id
+    wd = oracle.dequant_q4_k(wt.cpu().numpy(), k)
+    htie = torch.from_numpy((wd[n // 2] / np.linalg.norm(wd[n // 2]) * np.sqrt(k)).astype(np.float32)).to(device)
+    ones = torch.ones(k, dtype=torch.float32, device=device)
+    ps = [torch.empty(g, dtype=torch.float32, device=device) for _ in range(2)]
+    pt = [torch.empty(g, dtype=torch.int32, device=device) for _ in range(2)]
+    kernels.q4k_lm_head_argmax_partial_seqs([htie, hs[1]], wt, ps, pt, norm_weight=ones)
+    eos = torch.tensor([n - 1], dtype=torch.int64, device=device)
+    nxt = torch.empty(1, 1, dtype=torch.int64, device=device)
+    done = torch.empty(1, dtype=torch.int32, device=device)
+    kernels.token_select(ps[0], pt[0], eos, nxt, done)
+    assert int(nxt.item()) == n // 2
+
 @pytest.mark.parametrize("norm", [False, True])
 def test_lm_head_argmax_and_select(device, norm):
     """Fused LM-head GEMV + argmax: the index must equal the argmax of the GPU's own logits (bit-exact

@@ -43,6 +43,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "t2h_q4k_matvec_multi": (_i32, [_vp, _vp, _f32, _u32, _vp, _vp, _vp, _u32, _i32, _vp]),
     "t2h_q4k_rmsnorm_swiglu_matvec": (_i32, [_vp, _vp, _f32, _vp, _vp, _vp, _u32, _u32, _vp]),
     "t2h_q4k_lm_head_argmax_partial": (_i32, [_vp, _vp, _f32, _vp, _u32, _u32, _vp, _vp, _u32, _vp]),
+    "t2h_q4k_lm_head_argmax_partial_seqs": (_i32, [_u32, _vp, _vp, _f32, _vp, _u32, _u32, _vp, _vp, _u32,
+                                                    _vp]),
     "t2h_set_gemv_max_blocks": (_i32, [_u32, _u32]),
     "t2h_q6k_matvec": (_i32, [_vp, _vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp]),
     "t2h_q6k_rmsnorm_matvec": (_i32, [_vp, _vp, _f32, _vp, _vp, _i32, _u32, _u32, _vp]),

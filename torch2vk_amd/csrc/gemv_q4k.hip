@@ -665,3 +665,232 @@ extern "C" int t2h_q4k_lm_head_argmax_partial(const void* x, const float* norm_w
     return q4k_launch(norm_w ? Q4PRO_RMSNORM : Q4PRO_BF16, Q4EPI_ARGMAX, a, nsb, 0, num_partials,
                       reinterpret_cast<hipStream_t>(stream));
 }
+
+// ----------------------------------------------- LM head of several sequences --
+//
+// The LM head + per-block argmax of up to Q4_HEAD_SEQS sequences that decode
+// together (one step of a decoder group): the head's rows are streamed once and
+// dotted with every sequence's normed x, each sequence keeping its own argmax.
+// Per sequence the result is bit-identical to t2h_q4k_lm_head_argmax_partial
+// with the RMSNorm prologue: the same x staging (block of 8 waves, the same
+// sum-of-squares order), the same lane dots, the same units per block, and row
+// sums over the 64 / RPW lanes that hold a row, which is what wave_sum gives for
+// the single-sequence kernel's per-row masked sums (every other lane adds an
+// exact zero).
+namespace t2h {
+
+constexpr int Q4_HEAD_SEQS = 4;
+
+struct Q4HeadSeqsArgs {
+    const float* h[Q4_HEAD_SEQS];  // fp32 residual streams [K]
+    const float* norm_w;           // fp32 [K], the final RMSNorm weight
+    const uint8_t* w;              // Q4_K rows [N, K]
+    float* scores[Q4_HEAD_SEQS];   // [gridDim.x] each
+    uint32_t* tokens[Q4_HEAD_SEQS];
+    uint32_t n_units;
+    uint32_t units_per_wave;
+    float eps;
+};
+
+// Sum over the 16 lanes of a DPP row (every lane of the row gets it), in
+// wave_sum's order.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    return v;
+}
+
+template <int NSB, int NX>
+__global__ __launch_bounds__(512) void q4k_lm_head_seqs_kernel(const Q4HeadSeqsArgs a) {
+    constexpr int K = NSB * 256;
+    constexpr int WPB = 8;
+    constexpr int NT = WPB * 64;
+    constexpr int RPW = 16 / cgcd(NSB, 16);
+    constexpr int ROW_BYTES = NSB * 144;
+    constexpr int NSTAGE = 4;
+    static_assert(NSB == 4 || NSB == 16, "rows of 4 or 16 superblocks: one 16-superblock step per unit");
+    static_assert(NX >= 1 && NX <= Q4_HEAD_SEQS, "1..4 sequences");
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int sbo = lane >> 2;
+    const int g = lane & 3;
+    const int rloc = sbo / NSB;  // row of the unit this lane's superblock belongs to (lanes 64/RPW per row)
+    const int sbi = sbo % NSB;
+
+    struct Stage {
+        uint4 hdr, q0, q1;
+    };
+    auto issue = [&](uint32_t unit, Stage& st) {
+        const uint8_t* base = a.w + (size_t)(unit * RPW + (uint32_t)rloc) * ROW_BYTES + (size_t)sbi * 144;
+        st.hdr = load_u4(base);
+        st.q0 = load_u4(base + 16 + g * 32);
+        st.q1 = load_u4(base + 32 + g * 32);
+    };
+    const uint32_t wrow = blockIdx.x * WPB + wave;
+    const uint32_t total_wrows = gridDim.x * WPB;
+    const uint32_t last_unit = a.n_units - 1;
+    auto clamp_unit = [&](uint32_t u) { return u < a.n_units ? u : last_unit; };
+    const uint32_t n_iter = a.units_per_wave;
+    Stage st[NSTAGE];
+
+    // x of every sequence: RMSNorm (bf16-rounded) staged in LDS as fp16 pair words
+    __shared__ __align__(16) uint32_t xp[NX][xp_words(K)];
+    __shared__ float xsum[NX][K / 32];
+    __shared__ float red[NX][WPB];
+    constexpr int PT = (K + 4 * NT - 1) / (4 * NT);
+    float4 hv[NX][PT], wv[PT];
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+        const int k = (j * NT + (int)threadIdx.x) * 4;
+        const bool in = K % (4 * NT) == 0 || k < K;
+        wv[j] = in ? *reinterpret_cast<const float4*>(a.norm_w + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int x = 0; x < NX; ++x)
+            hv[x][j] = in ? *reinterpret_cast<const float4*>(a.h[x] + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    issue(clamp_unit(wrow), st[0]);
+#pragma unroll
+    for (int x = 0; x < NX; ++x) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            ss = fmaf(hv[x][j].x, hv[x][j].x, ss);
+            ss = fmaf(hv[x][j].y, hv[x][j].y, ss);
+            ss = fmaf(hv[x][j].z, hv[x][j].z, ss);
+            ss = fmaf(hv[x][j].w, hv[x][j].w, ss);
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[x][wave] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int x = 0; x < NX; ++x) {
+        float total = 0.0f;
+#pragma unroll
+        for (int i = 0; i < WPB; ++i) total += red[x][i];
+        const float inv = 1.0f / sqrtf(total / (float)K + a.eps);
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            const int k = (j * NT + (int)threadIdx.x) * 4;
+            if (K % (4 * NT) == 0 || k < K)
+                stage_x4(xp[x], xsum[x], k, bf16_round(hv[x][j].x * inv * wv[j].x),
+                         bf16_round(hv[x][j].y * inv * wv[j].y), bf16_round(hv[x][j].z * inv * wv[j].z),
+                         bf16_round(hv[x][j].w * inv * wv[j].w));
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 1; s < NSTAGE; ++s)
+        if ((uint32_t)s < n_iter) issue(clamp_unit(wrow + s * total_wrows), st[s]);
+    XSlice16 xs[NX];
+#pragma unroll
+    for (int x = 0; x < NX; ++x) load_xslice16(xp[x], xsum[x], sbi, g, xs[x]);
+    const Q4LaneConsts lc = q4k_lane_consts(g);
+
+    // each lane keeps the best (score, token) of the rows its 64 / RPW-lane group covers
+    float best_score[NX];
+    uint32_t best_token[NX];
+#pragma unroll
+    for (int x = 0; x < NX; ++x) {
+        best_score[x] = -3.4028234663852886e38f;
+        best_token[x] = 0xffffffffu;
+    }
+    auto consume = [&](uint32_t u, const Stage& s) {
+        const uint32_t row = u * RPW + (uint32_t)rloc;
+#pragma unroll
+        for (int x = 0; x < NX; ++x) {
+            const float c = q4k_lane_dot(s.hdr, s.q0, s.q1, xs[x], lc);
+            const float r = RPW == 4 ? row16_sum(c) : wave_sum(c);
+            if (u < a.n_units && better_pair(r, row, best_score[x], best_token[x])) {
+                best_score[x] = r;
+                best_token[x] = row;
+            }
+        }
+    };
+    for (uint32_t i = 0; i < n_iter; i += NSTAGE) {
+#pragma unroll
+        for (int s = 0; s < NSTAGE; ++s) {
+            const uint32_t ui = i + s;
+            if (ui >= n_iter) break;  // wave-uniform
+            consume(wrow + ui * total_wrows, st[s]);
+            if (ui + NSTAGE < n_iter) issue(clamp_unit(wrow + (ui + NSTAGE) * total_wrows), st[s]);
+        }
+    }
+
+    __shared__ float bs[NX][WPB];
+    __shared__ uint32_t bt[NX][WPB];
+#pragma unroll
+    for (int x = 0; x < NX; ++x) {
+        float sc = best_score[x];
+        uint32_t tk = best_token[x];
+        wave_argmax(sc, tk);
+        if (lane == 0) {
+            bs[x][wave] = sc;
+            bt[x][wave] = tk;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < (unsigned)NX) {
+        const int x = threadIdx.x;
+        float sc = bs[x][0];
+        uint32_t tk = bt[x][0];
+        for (int i = 1; i < WPB; ++i) {
+            if (better_pair(bs[x][i], bt[x][i], sc, tk)) {
+                sc = bs[x][i];
+                tk = bt[x][i];
+            }
+        }
+        a.scores[x][blockIdx.x] = sc;
+        a.tokens[x][blockIdx.x] = tk;
+    }
+}
+
+template <int NSB>
+static hipError_t launch_head_seqs(uint32_t nx, dim3 grid, const Q4HeadSeqsArgs& a, hipStream_t s) {
+    switch (nx) {
+        case 1: hipLaunchKernelGGL((q4k_lm_head_seqs_kernel<NSB, 1>), grid, dim3(512), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((q4k_lm_head_seqs_kernel<NSB, 2>), grid, dim3(512), 0, s, a); break;
+        case 3: hipLaunchKernelGGL((q4k_lm_head_seqs_kernel<NSB, 3>), grid, dim3(512), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((q4k_lm_head_seqs_kernel<NSB, 4>), grid, dim3(512), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace t2h
+
+extern "C" int t2h_q4k_lm_head_argmax_partial_seqs(uint32_t n_seq, const float* const* h, const float* norm_w,
+                                                   float eps, const void* w, uint32_t k, uint32_t n,
+                                                   float* const* partial_scores, uint32_t* const* partial_tokens,
+                                                   uint32_t num_partials, void* stream) {
+    if (!h || !norm_w || !w || !partial_scores || !partial_tokens) return T2H_ERR_NULL;
+    if (n_seq == 0 || n_seq > (uint32_t)Q4_HEAD_SEQS) return T2H_ERR_ARG;
+    if (k != 1024 && k != 4096) return T2H_ERR_UNSUPPORTED;
+    const uint32_t nsb = k / 256;
+    const Q4Geometry geo = q4_geometry(nsb, Q4EPI_ARGMAX);
+    if (n == 0 || n % geo.rpw) return T2H_ERR_SHAPE;
+    if (num_partials == 0) return T2H_ERR_ARG;
+    if (reinterpret_cast<uintptr_t>(norm_w) % 16) return T2H_ERR_ALIGN;
+    Q4HeadSeqsArgs a = {};
+    for (uint32_t i = 0; i < n_seq; ++i) {
+        if (!h[i] || !partial_scores[i] || !partial_tokens[i]) return T2H_ERR_NULL;
+        if (reinterpret_cast<uintptr_t>(h[i]) % 16) return T2H_ERR_ALIGN;  // float4 loads
+        a.h[i] = h[i];
+        a.scores[i] = partial_scores[i];
+        a.tokens[i] = partial_tokens[i];
+    }
+    a.norm_w = norm_w;
+    a.w = static_cast<const uint8_t*>(w);
+    a.eps = eps;
+    a.n_units = n / geo.rpw;
+    // the single-sequence launch's geometry: num_partials blocks of 8 waves, the same units per wave
+    a.units_per_wave = units_per_wave_for(a.n_units, num_partials, geo);
+    if (blocks_for(a.n_units, a.units_per_wave, geo) > num_partials) return T2H_ERR_ARG;
+    const dim3 grid(num_partials);
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const hipError_t e = nsb == 4 ? launch_head_seqs<4>(n_seq, grid, a, s) : launch_head_seqs<16>(n_seq, grid, a, s);
+    return e == hipSuccess ? T2H_OK : T2H_ERR_HIP_BASE + (int)e;
+}

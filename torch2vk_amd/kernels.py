@@ -185,6 +185,34 @@ def q4k_lm_head_argmax_partial(x: torch.Tensor, w: torch.Tensor, partial_scores:
          ptr(partial_tokens), g, stream_handle())
 
 
+def q4k_lm_head_argmax_partial_seqs(hs: list[torch.Tensor], w: torch.Tensor, partial_scores: list[torch.Tensor],
+                                    partial_tokens: list[torch.Tensor], *, norm_weight: torch.Tensor,
+                                    eps: float = RMS_EPS) -> None:
+    """q4k_lm_head_argmax_partial (final RMSNorm fused) for 1..4 sequences in one launch: the head is read
+    once; sequence i's partials land in partial_scores[i] / partial_tokens[i], bit-identical to its own
+    call (t2h_q4k_lm_head_argmax_partial_seqs)."""
+    n_seq = len(hs)
+    if not 1 <= n_seq <= LM_HEAD_SEQS_MAX or len(partial_scores) != n_seq or len(partial_tokens) != n_seq:
+        raise ValueError(f"1..{LM_HEAD_SEQS_MAX} sequences with one partial pair each")
+    _check(norm_weight, "norm_weight", torch.float32)
+    k = int(hs[0].numel())
+    for h in hs:
+        _check(h, "h", torch.float32)
+        if h.numel() != k:
+            raise ValueError("every h must have the same length")
+    n = _check_q4(w, "weight", None, k)
+    g = int(partial_scores[0].numel())
+    for sc, tk in zip(partial_scores, partial_tokens):
+        _check(sc, "partial_scores", torch.float32, align=4)
+        _check(tk, "partial_tokens", torch.int32, align=4)
+        if sc.numel() != g or tk.numel() != g or g == 0:
+            raise ValueError("partial_scores and partial_tokens must all have the same non-zero length")
+    arr = lambda ts: (ctypes.c_void_p * n_seq)(*[t.data_ptr() for t in ts])  # noqa: E731
+    h_arr, s_arr, t_arr = arr(hs), arr(partial_scores), arr(partial_tokens)
+    call("t2h_q4k_lm_head_argmax_partial_seqs", n_seq, ctypes.addressof(h_arr), ptr(norm_weight), eps, ptr(w), k,
+         n, ctypes.addressof(s_arr), ctypes.addressof(t_arr), g, stream_handle())
+
+
 _BLOCK = {"q4_k": (256, Q4_K_BYTES), "q6_k": (256, Q6_K_BYTES), "q8_0": (32, Q8_0_BYTES)}
 
 
@@ -665,6 +693,7 @@ def decode_layers_noalloc(table: torch.Tensor, h: torch.Tensor, cache_position: 
 
 
 DECODE_SEQS = (1, 4)  # sequences one persistent launch can run (4: the Qwen3-0.6B shape, s_cap <= 2048)
+LM_HEAD_SEQS_MAX = 4  # sequences of one t2h_q4k_lm_head_argmax_partial_seqs launch
 
 
 def decode_layers_seqs(tables: list[torch.Tensor], hs: list[torch.Tensor], cache_positions: list[torch.Tensor],

@@ -257,6 +257,10 @@ class Qwen3Decoder:
     def run_step_tail(self) -> None:
         """The end of a decode step after the layers: LM head, select + store the token, advance the position."""
         self._lm_head()
+        self._select_store()
+
+    def _select_store(self) -> None:
+        """Reduce the LM head's partials to the greedy token, store it, advance the position."""
         kernels.token_select_store(self.partial_scores, self.partial_tokens, self.eos, self.next_token, self.done,
                                    self.generated, self.length, self.stopped, stop_on_eos=self.stop_on_eos,
                                    advance=self.position)
@@ -590,12 +594,28 @@ class Qwen3DecoderGroup:
                                    nh=c.heads, nk=c.kv_heads, d=c.head_dim, s_cap=ds[0].max_positions,
                                    eps=c.rms_eps, theta=c.rope_theta)
 
+    def run_lm_heads(self) -> None:
+        """Every sequence's final norm + LM head + per-block argmax: one launch that reads a Q4_K head once for
+        all of them (bit-identical to each sequence's own), else one launch per sequence."""
+        ds = self.decoders
+        d0 = ds[0]
+        shared = all(d._w("lm_head").data_ptr() == d0._w("lm_head").data_ptr()
+                     and d._n("norm").data_ptr() == d0._n("norm").data_ptr() for d in ds)
+        if shared and d0.types["lm_head"] == "q4_k" and d0.config.hidden in (1024, 4096):
+            kernels.q4k_lm_head_argmax_partial_seqs([d.h for d in ds], d0._w("lm_head"),
+                                                    [d.partial_scores for d in ds], [d.partial_tokens for d in ds],
+                                                    norm_weight=d0._n("norm"), eps=d0.config.rms_eps)
+        else:
+            for d in ds:
+                d._lm_head()
+
     def decode_step(self) -> None:
         for d in self.decoders:
             d.run_decode_embed()
         self.run_decode_layers()
+        self.run_lm_heads()
         for d in self.decoders:
-            d.run_step_tail()
+            d._select_store()
 
     def graph(self, steps: int) -> torch.cuda.CUDAGraph:
         """A graph of ``steps`` consecutive group decode steps (captured once per step count)."""
