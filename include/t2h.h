@@ -210,6 +210,17 @@ int t2h_token_select_store(const float* scores, const uint32_t* tokens, uint32_t
                            uint32_t n_eos, int64_t* next_token, uint32_t* done, int64_t* generated, uint32_t gen_cap,
                            uint32_t* length, uint32_t* stopped, uint32_t stop_on_eos, int32_t* advance, void* stream);
 
+/* t2h_token_select_store for n_seq (1..4) sequences that decode together, in one launch: sequence i's
+ * partials, token, flags, generated ids, counters and (nullable) advance counter are element i of each
+ * pointer array; done[i] and advance[i] may be null; g, eos, gen_cap and stop_on_eos are shared.  Each
+ * sequence's result equals its own t2h_token_select_store call.
+ * replaces one QWEN3_TOKEN_SELECT_REDUCE_F32 + QWEN3_TOKEN_STORE_EOS_F32 pair per sequence
+ * (src/models/optimized_qwen3/run.py:123-139 and the token store of its decode loop) for a batched decode. */
+int t2h_token_select_store_seqs(uint32_t n_seq, const float* const* scores, const uint32_t* const* tokens, uint32_t g,
+                                const int64_t* eos, uint32_t n_eos, int64_t* const* next_token, uint32_t* const* done,
+                                int64_t* const* generated, uint32_t gen_cap, uint32_t* const* length,
+                                uint32_t* const* stopped, uint32_t stop_on_eos, int32_t* const* advance, void* stream);
+
 /* ------------------------------------------------- decode attention ---- */
 /* Split-K flash decoding over a bf16 token-major cache [s_cap, nk, d] (d = 128).
  * q [nh, d], k_new/v_new [nk, d] fp32 projections.  With q_norm_w/k_norm_w,
@@ -363,6 +374,11 @@ int t2h_flash_attn_segments(const void* q, const void* k, const void* v, void* o
 /* replaces EMBEDDING_Q4_K_F32 (src/models/quantized_qwen3/shaders/embedding_q4_k_f32.py:62-121); out fp32 [n_ids, dim] */
 int t2h_embedding_q4_k(const void* w, uint64_t vocab, const int64_t* ids, uint32_t n_ids, uint32_t dim, float* out,
                        void* stream);
+/* One token of each of n_seq (1..4) sequences: out[i] (fp32 [dim], 16-byte aligned) = row ids[i][0] of the
+ * Q4_K embedding, as t2h_embedding_q4_k.  replaces one EMBEDDING_Q4_K_F32 dispatch per sequence
+ * (src/models/quantized_qwen3/shaders/embedding_q4_k_f32.py:62-121, run_decode_embed) for a batched decode. */
+int t2h_embedding_q4_k_seqs(uint32_t n_seq, const void* w, uint64_t vocab, const int64_t* const* ids, uint32_t dim,
+                            float* const* out, void* stream);
 /* replaces RMS_NORM_MUL_F16_F32 / RMS_NORM_MUL_F32 (src/models/optimized_qwen3/shaders/rms_norm_mul_f16_f32.py:22-115) */
 int t2h_rms_norm(const void* x, int x_dtype, const float* w, void* out, int out_dtype, uint32_t rows, uint32_t h,
                  float eps, void* stream);

@@ -82,6 +82,12 @@ def test_argument_validation_returns_status(lib):
     assert lib.t2h_q4k_lm_head_argmax_partial_seqs(2, pa, fake, 1e-6, fake, 1024, 66, pa, pa, 8, None) == 2
     assert lib.t2h_q4k_lm_head_argmax_partial_seqs(2, pa, fake, 1e-6, fake, 1024, 64, pa, pa, 0, None) == 5
     assert lib.t2h_q4k_lm_head_argmax_partial_seqs(2, None, fake, 1e-6, fake, 1024, 64, pa, pa, 8, None) == 1
+    assert lib.t2h_embedding_q4_k_seqs(0, fake, 10, pa, 1024, pa, None) == 5
+    assert lib.t2h_embedding_q4_k_seqs(2, fake, 10, pa, 1000, pa, None) == 2
+    assert lib.t2h_embedding_q4_k_seqs(2, None, 10, pa, 1024, pa, None) == 1
+    assert lib.t2h_token_select_store_seqs(5, pa, pa, 8, fake, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 5
+    assert lib.t2h_token_select_store_seqs(2, pa, pa, 0, fake, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 2
+    assert lib.t2h_token_select_store_seqs(2, pa, pa, 8, None, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 1
 
 
 def test_python_wrappers_reject_host_tensors():

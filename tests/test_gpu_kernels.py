@@ -182,6 +182,50 @@ def test_lm_head_seqs_equals_each_sequence(device, k, n, g):
     kernels.token_select(ps[0], pt[0], eos, nxt, done)
     assert int(nxt.item()) == n // 2
 
+
+def test_select_store_and_embedding_seqs_equal_each_sequence(device):
+    """The batched select + store and the batched embedding of 4 sequences equal each sequence's own launch,
+    with the sequences in different states: one stopped, one at its generated capacity, one selecting EOS."""
+    from torch2vk_amd import kernels
+
+    rng = np.random.default_rng(5)
+    g, cap, n = 96, 6, 4
+    eos = torch.tensor([17, 23], dtype=torch.int64, device=device)
+
+    def state(i):
+        sc = torch.from_numpy(rng.standard_normal(g).astype(np.float32)).to(device)
+        tk = torch.from_numpy(rng.integers(0, 1000, g).astype(np.int32)).to(device)
+        if i == 2:
+            tk[int(sc.argmax())] = 23  # this sequence selects an EOS id
+        gen = torch.full((cap,), -1, dtype=torch.int64, device=device)
+        length = torch.tensor([cap if i == 1 else i], dtype=torch.int32, device=device)
+        stopped = torch.tensor([1 if i == 3 else 0], dtype=torch.int32, device=device)
+        return [sc, tk, torch.zeros(1, 1, dtype=torch.int64, device=device), torch.zeros(1, dtype=torch.int32,
+                device=device), gen, length, stopped, torch.tensor([100 + i], dtype=torch.int32, device=device)]
+
+    states = [state(i) for i in range(n)]
+    mine = [[t.clone() for t in st] for st in states]
+    for st in states:
+        kernels.token_select_store(st[0], st[1], eos, st[2], st[3], st[4], st[5], st[6], stop_on_eos=True,
+                                   advance=st[7])
+    kernels.token_select_store_seqs([m[0] for m in mine], [m[1] for m in mine], eos, [m[2] for m in mine],
+                                    [m[3] for m in mine], [m[4] for m in mine], [m[5] for m in mine],
+                                    [m[6] for m in mine], stop_on_eos=True, advance=[m[7] for m in mine])
+    for i in range(n):
+        for a, b in zip(states[i], mine[i]):
+            assert torch.equal(a, b), i
+    assert int(states[2][3].item()) == 1 and int(states[2][6].item()) == 1  # EOS flagged and stopped
+    assert int(states[1][5].item()) == cap  # at capacity: nothing appended
+
+    dim, vocab = 1024, 300
+    w = torch.from_numpy(oracle.quantize_q4_k((rng.standard_normal((vocab, dim)) * 0.05).astype(np.float32)))
+    w = w.to(device)
+    ids = [torch.tensor([t], dtype=torch.int64, device=device) for t in (0, 299, 17, 17)]
+    outs = [torch.full((dim,), 9.0, dtype=torch.float32, device=device) for _ in ids]
+    kernels.embedding_q4_k_seqs(w, ids, dim, outs)
+    for t, o in zip(ids, outs):
+        assert torch.equal(o, kernels.embedding_q4_k(w, t, dim)[0])
+
 @pytest.mark.parametrize("norm", [False, True])
 def test_lm_head_argmax_and_select(device, norm):
     """Fused LM-head GEMV + argmax: the index must equal the argmax of the GPU's own logits (bit-exact

@@ -56,6 +56,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "t2h_token_select": (_i32, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp]),
     "t2h_token_store": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _u32, _vp, _u32, _vp, _vp]),
     "t2h_token_select_store": (_i32, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _u32, _vp, _vp, _u32, _vp, _vp]),
+    "t2h_token_select_store_seqs": (_i32, [_u32, _vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp, _u32, _vp, _vp, _u32,
+                                            _vp, _vp]),
     "t2h_attn_decode_workspace_bytes": (_sz, [_u32, _u32, _u32, _u32]),
     "t2h_attn_decode": (_i32, [_vp, _vp, _vp, _vp, _vp, _f32, _f32, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp,
                               _vp, _sz, _vp]),
@@ -75,6 +77,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                             _i32, ctypes.c_int32, _f32, _vp]),
     "t2h_fa_mask_tiles": (_i32, [_vp, _u32, _u32, _u32, ctypes.c_int64, ctypes.c_int64, _vp, _vp]),
     "t2h_embedding_q4_k": (_i32, [_vp, _u64, _vp, _u32, _u32, _vp, _vp]),
+    "t2h_embedding_q4_k_seqs": (_i32, [_u32, _vp, _u64, _vp, _u32, _vp, _vp]),
     "t2h_rms_norm": (_i32, [_vp, _i32, _vp, _vp, _i32, _u32, _u32, _f32, _vp]),
     "t2h_swiglu": (_i32, [_vp, _vp, _i32, _vp, _u64, _vp]),
     "t2h_q8_0_linear": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _u32, _u32, _u32, _u32, _vp]),

@@ -15,11 +15,8 @@ namespace t2h {
 // One block per token: dequantise the token's Q4_K embedding row into fp32.
 // Thread t handles nibble group (t & 3) of superblock (t >> 2): one 16-B
 // header and 32 B of nibbles -> 64 values, written as 16 float4 stores.
-__global__ __launch_bounds__(256) void embedding_q4_k_kernel(const uint8_t* __restrict__ w,
-                                                             const int64_t* __restrict__ ids, uint32_t dim,
-                                                             uint64_t vocab, float* __restrict__ out) {
-    const uint32_t t = blockIdx.x;
-    int64_t id = ids[t];
+__device__ __forceinline__ void embed_q4_k_row(const uint8_t* __restrict__ w, int64_t id, uint32_t dim, uint64_t vocab,
+                                               float* __restrict__ out_row) {
     if (id < 0 || (uint64_t)id >= vocab) id = 0;  // the host validates host-side ids; device ids are clamped
     const uint32_t nsb = dim / 256;
     const uint8_t* row = w + (uint64_t)id * nsb * 144;
@@ -46,7 +43,7 @@ __global__ __launch_bounds__(256) void embedding_q4_k_kernel(const uint8_t* __re
             }
         }
         const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        float* o = out + (uint64_t)t * dim + sb * 256 + 64 * g;
+        float* o = out_row + sb * 256 + 64 * g;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const float a = d * (float)sc[h];
@@ -64,6 +61,25 @@ __global__ __launch_bounds__(256) void embedding_q4_k_kernel(const uint8_t* __re
             }
         }
     }
+}
+
+__global__ __launch_bounds__(256) void embedding_q4_k_kernel(const uint8_t* __restrict__ w,
+                                                             const int64_t* __restrict__ ids, uint32_t dim,
+                                                             uint64_t vocab, float* __restrict__ out) {
+    embed_q4_k_row(w, ids[blockIdx.x], dim, vocab, out + (uint64_t)blockIdx.x * dim);
+}
+
+// One decode step's embedding for several sequences (a decoder group): block b embeds sequence b's next
+// token into its own hidden row.
+constexpr int SEQS_MAX = 4;
+struct EmbedSeqsArgs {
+    const int64_t* ids[SEQS_MAX];
+    float* out[SEQS_MAX];
+};
+
+__global__ __launch_bounds__(256) void embedding_q4_k_seqs_kernel(const uint8_t* __restrict__ w, uint32_t dim,
+                                                                  uint64_t vocab, const EmbedSeqsArgs a) {
+    embed_q4_k_row(w, a.ids[blockIdx.x][0], dim, vocab, a.out[blockIdx.x]);
 }
 
 // Reduce G (score, token) partials to one greedy token; flag EOS.
@@ -125,7 +141,7 @@ __global__ void token_store_kernel(const int64_t* __restrict__ next_token, const
 
 // Greedy select fused with the token store: one launch per decode step for
 // both QWEN3_TOKEN_SELECT_REDUCE_F32 and QWEN3_TOKEN_STORE_EOS_F32.
-__global__ __launch_bounds__(1024) void token_select_store_kernel(
+__device__ __forceinline__ void token_select_store_block(
     const float* __restrict__ scores, const uint32_t* __restrict__ tokens, uint32_t g,
     const int64_t* __restrict__ eos, uint32_t n_eos, int64_t* __restrict__ next_token, uint32_t* __restrict__ done,
     int64_t* __restrict__ generated, uint32_t gen_cap, uint32_t* __restrict__ length, uint32_t* __restrict__ stopped,
@@ -168,6 +184,37 @@ __global__ __launch_bounds__(1024) void token_select_store_kernel(
             if (stop_on_eos && is_done) stopped[0] = 1u;
         }
     }
+}
+
+__global__ __launch_bounds__(1024) void token_select_store_kernel(
+    const float* __restrict__ scores, const uint32_t* __restrict__ tokens, uint32_t g,
+    const int64_t* __restrict__ eos, uint32_t n_eos, int64_t* __restrict__ next_token, uint32_t* __restrict__ done,
+    int64_t* __restrict__ generated, uint32_t gen_cap, uint32_t* __restrict__ length, uint32_t* __restrict__ stopped,
+    uint32_t stop_on_eos, int32_t* __restrict__ advance) {
+    token_select_store_block(scores, tokens, g, eos, n_eos, next_token, done, generated, gen_cap, length, stopped,
+                             stop_on_eos, advance);
+}
+
+// The select + store of several sequences (a decoder group's step): block b runs sequence b's, exactly as
+// its own token_select_store_kernel launch would.
+struct SelectStoreSeqsArgs {
+    const float* scores[SEQS_MAX];
+    const uint32_t* tokens[SEQS_MAX];
+    int64_t* next_token[SEQS_MAX];
+    uint32_t* done[SEQS_MAX];
+    int64_t* generated[SEQS_MAX];
+    uint32_t* length[SEQS_MAX];
+    uint32_t* stopped[SEQS_MAX];
+    int32_t* advance[SEQS_MAX];
+};
+
+__global__ __launch_bounds__(1024) void token_select_store_seqs_kernel(uint32_t g, const int64_t* __restrict__ eos,
+                                                                       uint32_t n_eos, uint32_t gen_cap,
+                                                                       uint32_t stop_on_eos,
+                                                                       const SelectStoreSeqsArgs a) {
+    const uint32_t b = blockIdx.x;
+    token_select_store_block(a.scores[b], a.tokens[b], g, eos, n_eos, a.next_token[b], a.done[b], a.generated[b],
+                             gen_cap, a.length[b], a.stopped[b], stop_on_eos, a.advance[b]);
 }
 
 // rows x H RMSNorm; x and out are fp32 or bf16, weight fp32.
@@ -285,6 +332,53 @@ extern "C" int t2h_token_select_store(const float* scores, const uint32_t* token
     if (g == 0) return T2H_ERR_SHAPE;
     hipLaunchKernelGGL(token_select_store_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, scores, tokens, g, eos,
                        n_eos, next_token, done, generated, gen_cap, length, stopped, stop_on_eos, advance);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+extern "C" int t2h_embedding_q4_k_seqs(uint32_t n_seq, const void* w, uint64_t vocab, const int64_t* const* ids,
+                                       uint32_t dim, float* const* out, void* stream) {
+    if (!w || !ids || !out) return T2H_ERR_NULL;
+    if (n_seq == 0 || n_seq > (uint32_t)SEQS_MAX) return T2H_ERR_ARG;
+    if (dim == 0 || dim % 256 != 0 || vocab == 0) return T2H_ERR_SHAPE;
+    EmbedSeqsArgs a = {};
+    for (uint32_t i = 0; i < n_seq; ++i) {
+        if (!ids[i] || !out[i]) return T2H_ERR_NULL;
+        if (reinterpret_cast<uintptr_t>(out[i]) % 16) return T2H_ERR_ALIGN;  // float4 stores
+        a.ids[i] = ids[i];
+        a.out[i] = out[i];
+    }
+    hipLaunchKernelGGL(embedding_q4_k_seqs_kernel, dim3(n_seq), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)w, dim, vocab, a);
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
+extern "C" int t2h_token_select_store_seqs(uint32_t n_seq, const float* const* scores, const uint32_t* const* tokens,
+                                           uint32_t g, const int64_t* eos, uint32_t n_eos, int64_t* const* next_token,
+                                           uint32_t* const* done, int64_t* const* generated, uint32_t gen_cap,
+                                           uint32_t* const* length, uint32_t* const* stopped, uint32_t stop_on_eos,
+                                           int32_t* const* advance, void* stream) {
+    if (!scores || !tokens || !next_token || !done || !generated || !length || !stopped || !advance)
+        return T2H_ERR_NULL;
+    if (n_seq == 0 || n_seq > (uint32_t)SEQS_MAX) return T2H_ERR_ARG;
+    if (n_eos && !eos) return T2H_ERR_NULL;
+    if (g == 0) return T2H_ERR_SHAPE;
+    SelectStoreSeqsArgs a = {};
+    for (uint32_t i = 0; i < n_seq; ++i) {
+        if (!scores[i] || !tokens[i] || !next_token[i] || !generated[i] || !length[i] || !stopped[i])
+            return T2H_ERR_NULL;
+        a.scores[i] = scores[i];
+        a.tokens[i] = tokens[i];
+        a.next_token[i] = next_token[i];
+        a.done[i] = done[i];          // may be null, as in t2h_token_select_store
+        a.generated[i] = generated[i];
+        a.length[i] = length[i];
+        a.stopped[i] = stopped[i];
+        a.advance[i] = advance[i];    // may be null
+    }
+    hipLaunchKernelGGL(token_select_store_seqs_kernel, dim3(n_seq), dim3(1024), 0, (hipStream_t)stream, g, eos, n_eos,
+                       gen_cap, stop_on_eos, a);
     T2H_LAUNCH_CHECK();
     return T2H_OK;
 }

@@ -563,6 +563,43 @@ def token_select_store(partial_scores: torch.Tensor, partial_tokens: torch.Tenso
          int(stop_on_eos), ptr(advance), stream_handle())
 
 
+
+def _tensor_ptrs(ts: list[torch.Tensor | None]):
+    """A ctypes array of the tensors' device addresses (null for None), kept alive by the caller."""
+    return (ctypes.c_void_p * len(ts))(*[None if t is None else t.data_ptr() for t in ts])
+
+
+def token_select_store_seqs(partial_scores: list[torch.Tensor], partial_tokens: list[torch.Tensor],
+                            eos_ids: torch.Tensor, next_tokens: list[torch.Tensor], dones: list[torch.Tensor],
+                            generated: list[torch.Tensor], lengths: list[torch.Tensor], stopped: list[torch.Tensor],
+                            *, stop_on_eos: bool = True, advance: list[torch.Tensor] | None = None) -> None:
+    """token_select_store of 1..4 sequences in one launch (t2h_token_select_store_seqs); argument i of every
+    list belongs to sequence i, and each sequence's result equals its own call."""
+    n = len(partial_scores)
+    lists = (partial_tokens, next_tokens, dones, generated, lengths, stopped) + ((advance,) if advance else ())
+    if not 1 <= n <= LM_HEAD_SEQS_MAX or any(len(x) != n for x in lists):
+        raise ValueError(f"1..{LM_HEAD_SEQS_MAX} sequences with one of each argument per sequence")
+    g, cap = partial_scores[0].numel(), generated[0].numel()
+    _check(eos_ids, "eos_token_ids", torch.int64, align=8)
+    for i in range(n):
+        _check(partial_scores[i], "scores", torch.float32, align=4)
+        _check(partial_tokens[i], "tokens", torch.int32, align=4)
+        _check(next_tokens[i], "next_token", torch.int64, align=8)
+        _check(dones[i], "done", torch.int32, align=4)
+        _check(generated[i], "generated_tokens", torch.int64, align=8)
+        _check(lengths[i], "generated_length", torch.int32, align=4)
+        _check(stopped[i], "stopped", torch.int32, align=4)
+        if advance:
+            _check(advance[i], "advance", torch.int32, align=4)
+        if partial_scores[i].numel() != g or partial_tokens[i].numel() != g or generated[i].numel() != cap:
+            raise ValueError("every sequence needs the same partial count and generated capacity")
+    arrs = [_tensor_ptrs(x) for x in (partial_scores, partial_tokens, next_tokens, dones, generated, lengths, stopped,
+                                    advance if advance else [None] * n)]
+    sc, tk, nt, dn, gen, ln, st, adv = (ctypes.addressof(a) for a in arrs)
+    call("t2h_token_select_store_seqs", n, sc, tk, g, ptr(eos_ids), eos_ids.numel(), nt, dn, gen, cap, ln, st,
+         int(stop_on_eos), adv, stream_handle())
+
+
 # ------------------------------------------------------ decode attention --
 
 
@@ -868,6 +905,25 @@ def embedding_q4_k(w: torch.Tensor, ids: torch.Tensor, dim: int, out: torch.Tens
     _check(out, "output", torch.float32, align=4)
     call("t2h_embedding_q4_k", ptr(w), int(w.shape[0]), ptr(ids), ids.numel(), dim, ptr(out), stream_handle())
     return out
+
+
+def embedding_q4_k_seqs(w: torch.Tensor, ids: list[torch.Tensor], dim: int, outs: list[torch.Tensor]) -> None:
+    """One token of each of 1..4 sequences (ids[i][0]) embedded into outs[i] (fp32 [dim]) in one launch
+    (t2h_embedding_q4_k_seqs)."""
+    n = len(ids)
+    if not 1 <= n <= LM_HEAD_SEQS_MAX or len(outs) != n:
+        raise ValueError(f"1..{LM_HEAD_SEQS_MAX} sequences with one id tensor and one output each")
+    _check(w, "weight", torch.uint8, align=1)
+    if w.shape[1] != q4_k_row_bytes(dim):
+        raise ValueError("embedding weight width does not match dim")
+    for i in range(n):
+        _check(ids[i], "indices", torch.int64, align=8)
+        _check(outs[i], "output", torch.float32, align=16)
+        if ids[i].numel() < 1 or outs[i].numel() != dim:
+            raise ValueError("each sequence needs one id and a [dim] output")
+    id_arr, out_arr = _tensor_ptrs(ids), _tensor_ptrs(outs)
+    call("t2h_embedding_q4_k_seqs", n, ptr(w), int(w.shape[0]), ctypes.addressof(id_arr), dim,
+         ctypes.addressof(out_arr), stream_handle())
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,

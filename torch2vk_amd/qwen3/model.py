@@ -609,13 +609,38 @@ class Qwen3DecoderGroup:
             for d in ds:
                 d._lm_head()
 
+    def run_decode_embeds(self) -> None:
+        """Every sequence's next token into its residual stream: one launch for a shared Q4_K embedding, else
+        one per sequence."""
+        ds = self.decoders
+        d0 = ds[0]
+        if d0.types["embed"] == "q4_k" and all(d._w("embed").data_ptr() == d0._w("embed").data_ptr() for d in ds):
+            kernels.embedding_q4_k_seqs(d0._w("embed"), [d.next_token.view(-1) for d in ds], d0.config.hidden,
+                                        [d.h for d in ds])
+        else:
+            for d in ds:
+                d.run_decode_embed()
+
+    def run_select_stores(self) -> None:
+        """Every sequence's greedy select + token store + position advance: one launch when the sequences
+        share the EOS policy and the generated capacity, else one per sequence."""
+        ds = self.decoders
+        d0 = ds[0]
+        if all(d.stop_on_eos == d0.stop_on_eos and d.generated.numel() == d0.generated.numel() for d in ds):
+            kernels.token_select_store_seqs([d.partial_scores for d in ds], [d.partial_tokens for d in ds], d0.eos,
+                                            [d.next_token for d in ds], [d.done for d in ds],
+                                            [d.generated for d in ds], [d.length for d in ds],
+                                            [d.stopped for d in ds], stop_on_eos=d0.stop_on_eos,
+                                            advance=[d.position for d in ds])
+        else:
+            for d in ds:
+                d._select_store()
+
     def decode_step(self) -> None:
-        for d in self.decoders:
-            d.run_decode_embed()
+        self.run_decode_embeds()
         self.run_decode_layers()
         self.run_lm_heads()
-        for d in self.decoders:
-            d._select_store()
+        self.run_select_stores()
 
     def graph(self, steps: int) -> torch.cuda.CUDAGraph:
         """A graph of ``steps`` consecutive group decode steps (captured once per step count)."""
