@@ -689,6 +689,7 @@ struct Q4HeadSeqsArgs {
     uint32_t* tokens[Q4_HEAD_SEQS];
     uint32_t n_units;
     uint32_t units_per_wave;
+    uint32_t n_partials;  // slots per sequence; those past the grid get the empty pair
     float eps;
 };
 
@@ -845,6 +846,10 @@ __global__ __launch_bounds__(512) void q4k_lm_head_seqs_kernel(const Q4HeadSeqsA
         }
         a.scores[x][blockIdx.x] = sc;
         a.tokens[x][blockIdx.x] = tk;
+        for (uint32_t slot = gridDim.x + blockIdx.x; slot < a.n_partials; slot += gridDim.x) {
+            a.scores[x][slot] = -3.4028234663852886e38f;  // no row: loses to every row's (score, token)
+            a.tokens[x][slot] = 0xffffffffu;
+        }
     }
 }
 
@@ -886,10 +891,22 @@ extern "C" int t2h_q4k_lm_head_argmax_partial_seqs(uint32_t n_seq, const float* 
     a.w = static_cast<const uint8_t*>(w);
     a.eps = eps;
     a.n_units = n / geo.rpw;
-    // the single-sequence launch's geometry: num_partials blocks of 8 waves, the same units per wave
-    a.units_per_wave = units_per_wave_for(a.n_units, num_partials, geo);
-    if (blocks_for(a.n_units, a.units_per_wave, geo) > num_partials) return T2H_ERR_ARG;
-    const dim3 grid(num_partials);
+    a.n_partials = num_partials;
+    // One sequence: the single-sequence launch's geometry (num_partials blocks of 8 waves, its partials
+    // bit for bit).  Several: above 128 VGPRs a CU holds one block of 8 waves, so the grid is one block per
+    // CU (a second round of blocks would wait for the first); the unused slots get the empty pair, and the
+    // selected (score, token) is the same, the order of better_pair being total.
+    uint32_t blocks = num_partials;
+    if (n_seq > 1) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            return T2H_ERR_HIP_BASE + (int)hipErrorInvalidDevice;
+        blocks = num_partials < (uint32_t)cus ? num_partials : (uint32_t)cus;
+    }
+    a.units_per_wave = units_per_wave_for(a.n_units, blocks, geo);
+    if (blocks_for(a.n_units, a.units_per_wave, geo) > blocks) return T2H_ERR_ARG;
+    const dim3 grid(blocks);
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const hipError_t e = nsb == 4 ? launch_head_seqs<4>(n_seq, grid, a, s) : launch_head_seqs<16>(n_seq, grid, a, s);
     return e == hipSuccess ? T2H_OK : T2H_ERR_HIP_BASE + (int)e;
