@@ -183,3 +183,29 @@ def test_forward_masked_matches_oracle(device, policy):
     assert_close(got, ref, max_abs=0.05 * float(np.abs(ref).max()), min_cos=0.999, what="final hidden")
     for row in (0, 19, 20, 37, 44):
         assert_close(got[row], ref[row], max_abs=0.05 * float(np.abs(ref).max()), min_cos=0.999, what=f"row {row}")
+
+
+def test_graphed_prefill_equals_eager_prefill(device):
+    """prefill_graphed replays one captured prefill: three prompts of one length, with eager decode steps
+    between the replays, each give prefill_chunked's KV cache, token and counters bit for bit."""
+    from torch2vk_amd.qwen3.config import Qwen3Config
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+
+    cfg = Qwen3Config("tiny-p", hidden=1024, layers=3, heads=8, kv_heads=2, head_dim=128, mlp=1024, vocab=1024,
+                      eos_token_ids=(1023,))
+    w, _, _ = _setup(cfg, device, seed=61, std=0.05, policy="uniform")
+    a = Qwen3Decoder(w, max_positions=80, max_new_tokens=8)
+    b = Qwen3Decoder(w, max_positions=80, max_new_tokens=8)
+    a.stop_on_eos = b.stop_on_eos = False
+    rng = np.random.default_rng(7)
+    for rep in range(3):
+        prompt = torch.tensor(rng.integers(0, cfg.vocab, 50).tolist(), device=device)
+        a.prefill_chunked(prompt, chunk=20)
+        b.prefill_graphed(prompt, chunk=20)
+        torch.cuda.synchronize()
+        for name in ("k_cache", "v_cache", "next_token", "position", "length", "generated", "h"):
+            assert torch.equal(getattr(a, name), getattr(b, name)), (rep, name)
+        a.run_steps(3, use_graph=False)
+        b.run_steps(3, use_graph=False)
+        assert torch.equal(a.generated, b.generated), rep
+    assert len(b._prefill_graphs) == 1

@@ -102,6 +102,7 @@ class Qwen3Decoder:
         self.eos = torch.tensor(c.eos_token_ids, dtype=torch.int64, device=dev)
         self.stop_on_eos = True
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self._prefill_graphs: dict[tuple[int, int, int], tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
         self.persistent = False
         self.status = torch.zeros(1, dtype=torch.int32, device=dev)
         if persistent is not False:
@@ -431,6 +432,31 @@ class Qwen3Decoder:
         self.position.fill_(start + total - 1)
         self.run_lm_head_select()
         self.run_token_store(advance=True)
+
+    def prefill_graphed(self, prompt_ids: torch.Tensor, *, start: int = 0, chunk: int = 2048) -> None:
+        """prefill_chunked of a token-id prompt replayed from a HIP graph: the first call for a (length, start,
+        chunk) captures the whole prefill (every layer's launches, the LM head and the token store) reading the
+        ids from a buffer of the decoder's; later calls copy the ids into that buffer and replay.  Results are
+        prefill_chunked's bit for bit; a short prompt's prefill is bound by launch overhead, which the graph
+        removes."""
+        ids = prompt_ids.to(device=self.device, dtype=torch.int64).view(-1)
+        if ids.numel() == 0:
+            raise ValueError("empty prompt")
+        key = (ids.numel(), start, chunk)
+        if key not in self._prefill_graphs:
+            buf = ids.clone()
+            side = torch.cuda.Stream(device=self.device)
+            side.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(side):
+                self.prefill_chunked(buf, start=start, chunk=chunk)  # warm-up launch outside capture
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.prefill_chunked(buf, start=start, chunk=chunk)
+            self._prefill_graphs[key] = (g, buf)
+        g, buf = self._prefill_graphs[key]
+        buf.copy_(ids)
+        g.replay()
 
     def prefill_embeds(self, embeds: torch.Tensor, start: int = 0) -> None:
         """Feed a prompt given as fp32 input embeddings [T, hidden] -- a Qwen3-ASR prompt after the audio
