@@ -100,6 +100,16 @@ def audio_tower_cpu(w: dict[str, torch.Tensor], cfg, padded_feature: np.ndarray,
     h = h + torch.from_numpy(np.asarray(position_embedding, np.float32))
     h = h.reshape(-1, h.shape[-1])[torch.from_numpy(np.asarray(compact_index, np.int64))]
     mask = None if attention_mask is None else torch.from_numpy(np.asarray(attention_mask, np.float32))[0, 0]
+    h = encoder_layers_cpu(w, cfg, h, mask=mask, cu_seqlens=cu_seqlens)
+    return encoder_head_cpu(w, cfg, h)
+
+
+def encoder_layers_cpu(w: dict[str, torch.Tensor], cfg, h: torch.Tensor, *, mask: torch.Tensor | None = None,
+                       cu_seqlens=None) -> torch.Tensor:
+    """Every pre-LN encoder layer over the fp32 residual stream h [T, d_model] (``_run_audio_layer``,
+    pytorch_modules.py:484-526): attention under the additive ``mask`` [T, T] when given, else window by
+    window over ``cu_seqlens``."""
+    p = PREFIX
     hd = cfg.d_model // cfg.heads
     scale = 1.0 / math.sqrt(hd)
     for i in range(cfg.layers):
@@ -125,6 +135,12 @@ def audio_tower_cpu(w: dict[str, torch.Tensor], cfg, padded_feature: np.ndarray,
                          eps=cfg.eps)
         y = gelu(y @ w[lp + "fc1.weight"].T + w[lp + "fc1.bias"])
         h = res + y @ w[lp + "fc2.weight"].T + w[lp + "fc2.bias"]
+    return h
+
+
+def encoder_head_cpu(w: dict[str, torch.Tensor], cfg, h: torch.Tensor) -> torch.Tensor:
+    """ln_post -> proj1 + GELU -> proj2 (pytorch_modules.py:476-481): fp32 [T, output_dim]."""
+    p = PREFIX
     y = F.layer_norm(h, (cfg.d_model,), w[p + "ln_post.weight"], w[p + "ln_post.bias"], eps=cfg.eps)
     y = gelu(y @ w[p + "proj1.weight"].T + w[p + "proj1.bias"])
     return y @ w[p + "proj2.weight"].T + w[p + "proj2.bias"]

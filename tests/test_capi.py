@@ -85,6 +85,12 @@ def test_argument_validation_returns_status(lib):
     assert lib.t2h_embedding_q4_k_seqs(0, fake, 10, pa, 1024, pa, None) == 5
     assert lib.t2h_embedding_q4_k_seqs(2, fake, 10, pa, 1000, pa, None) == 2
     assert lib.t2h_embedding_q4_k_seqs(2, None, 10, pa, 1024, pa, None) == 1
+    # weights read with 16-byte loads: a misaligned weight pointer is refused
+    odd = ctypes.c_void_p(0x1001)
+    assert lib.t2h_q4k_lm_head_argmax_partial_seqs(2, pa, fake, 1e-6, odd, 1024, 64, pa, pa, 8, None) == 7
+    assert lib.t2h_embedding_q4_k_seqs(2, odd, 10, pa, 1024, pa, None) == 7
+    assert lib.t2h_embedding_q4_k(odd, 10, fake, 1, 1024, fake, None) == 7
+    assert lib.t2h_embedding_q4_k(fake, 10, fake, 1, 1024, odd, None) == 7
     assert lib.t2h_token_select_store_seqs(5, pa, pa, 8, fake, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 5
     assert lib.t2h_token_select_store_seqs(2, pa, pa, 0, fake, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 2
     assert lib.t2h_token_select_store_seqs(2, pa, pa, 8, None, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 1

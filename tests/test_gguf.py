@@ -213,7 +213,7 @@ def test_export_load_decode_matches_oracle(device, tmp_path):
     greedy decode on the GPU equals the CPU oracle decoder's tokens."""
     from safetensors.torch import save_file
 
-    from oracle.qwen3_check import check_greedy_tokens, dense_weights
+    from oracle.qwen3_check import check_greedy_tokens, decoder_step_logits, dense_weights
     from oracle.reference import Qwen3Shape
     from torch2vk_amd.qwen3.model import Qwen3Decoder
     from torch2vk_amd.qwen3.weights import matrix_shapes
@@ -234,10 +234,12 @@ def test_export_load_decode_matches_oracle(device, tmp_path):
     assert gguf.export_q4_k_m_gguf(model_dir=tmp_path / "ck", output=out, config=policy) == out  # kept
     w = gguf.load_qwen3_gguf(out, cfg, device=device)
     dec = Qwen3Decoder(w, max_positions=64, max_new_tokens=8)
+    dec.stop_on_eos = False
     prompt = [5, 17, 200, 3]
     tokens = dec.generate(torch.tensor(prompt, dtype=torch.int64, device=device), 8)
     dense = dense_weights({k: v.cpu().numpy() for k, v in w.packed.items()}, w.types,
                           {k: v.cpu().numpy() for k, v in w.norms.items()}, matrix_shapes(cfg))
     shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
                        head_dim=cfg.head_dim, mlp=cfg.mlp, vocab=cfg.vocab, rope_theta=cfg.rope_theta)
-    check_greedy_tokens(shape, dense, prompt, tokens)
+    print(check_greedy_tokens(shape, dense, prompt, tokens, kv_history=(dec.k_cache, dec.v_cache),
+                              gpu_logits=decoder_step_logits(dec), label="gguf"))

@@ -284,7 +284,7 @@ def test_audio_injected_decode_matches_oracle(device):
     """Encoder features injected at the audio placeholder positions of the prompt embeddings, then greedy
     decode (Q8_0 token embedding as under the Qwen3-ASR policy): tokens equal the oracle decoder's given the
     same injected embeddings."""
-    from oracle.qwen3_check import check_greedy_tokens, dense_weights
+    from oracle.qwen3_check import check_greedy_tokens, decoder_step_logits, dense_weights
     from oracle.reference import Qwen3Shape
     from torch2vk_amd.qwen3.config import Qwen3Config
     from torch2vk_amd.qwen3.model import Qwen3Decoder
@@ -313,4 +313,6 @@ def test_audio_injected_decode_matches_oracle(device):
                           {k: v.cpu().numpy() for k, v in w.norms.items()}, matrix_shapes(tcfg))
     shape = Qwen3Shape(hidden=tcfg.hidden, layers=tcfg.layers, heads=tcfg.heads, kv_heads=tcfg.kv_heads,
                        head_dim=tcfg.head_dim, mlp=tcfg.mlp, vocab=tcfg.vocab, rope_theta=tcfg.rope_theta)
-    print(check_greedy_tokens(shape, dense, prompt, toks, prompt_embeds=embeds.cpu()))
+    print(check_greedy_tokens(shape, dense, prompt, toks, prompt_embeds=embeds.cpu(),
+                              kv_history=(dec.k_cache, dec.v_cache), gpu_logits=decoder_step_logits(dec),
+                              label="asr inject"))

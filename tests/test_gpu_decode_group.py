@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.qwen3_check import check_greedy_tokens, dense_weights
+from oracle.qwen3_check import check_greedy_tokens, decoder_step_logits, dense_weights
 from oracle.reference import Qwen3Shape
 
 pytestmark = pytest.mark.gpu
@@ -104,7 +104,8 @@ def test_group_long_kv_matches_oracle(device, small_06b):
         assert len(toks) == 7
         kv = (d.k_cache[:, :st].cpu(), d.v_cache[:, :st].cpu())
         print(f"start {st}: {toks}", flush=True)
-        print(check_greedy_tokens(shape, dense, p, toks, start=st, kv_init=kv, tie_tol=5e-3), flush=True)
+        print(check_greedy_tokens(shape, dense, p, toks, start=st, kv_init=kv, kv_history=(d.k_cache, d.v_cache),
+                                  gpu_logits=decoder_step_logits(d), label=f"group from KV {st}"), flush=True)
 
 
 def test_group_rejects_bad_arguments(device, small_06b):
@@ -146,6 +147,7 @@ def test_group_batched_prefill_matches_each_prefill(device, small_06b):
     prompts = [rng.integers(0, cfg.vocab, 150).tolist() for _ in range(4)]
     embs = [group.decoders[0].embed_tokens(torch.tensor(p, device=device)) for p in prompts]
     group.prefill_chunked(embs, chunk=64)
+    prefill_h = [d.h.clone() for d in group.decoders]  # step 0's tokens come from these rows
     for d, e in zip(single, embs):
         d.prefill_chunked(embeds=e, chunk=64)
     torch.cuda.synchronize()
@@ -159,9 +161,11 @@ def test_group_batched_prefill_matches_each_prefill(device, small_06b):
             assert d1 <= 1e-2 * cb[1].float().abs().max().item(), d1
         assert int(a.position.item()) == int(b.position.item()) == 150
     toks = group.finish(7, steps_per_graph=4, use_graph=True)
-    for p, tk in zip(prompts, toks):
+    for b, (d, p, tk) in enumerate(zip(group.decoders, prompts, toks)):
         assert len(tk) == 7
-        print(check_greedy_tokens(shape, dense, p, tk, tie_tol=5e-3), flush=True)
+        print(check_greedy_tokens(shape, dense, p, tk, kv_history=(d.k_cache, d.v_cache),
+                                  gpu_logits=decoder_step_logits(d, prefill_h[b]), label=f"batched prefill {b}"),
+              flush=True)
 
 
 def test_group_q4_k_m_equals_one_launch_each(device):

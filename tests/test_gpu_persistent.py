@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.qwen3_check import check_greedy_tokens, dense_weights
+from oracle.qwen3_check import check_greedy_tokens, decoder_step_logits, dense_weights
 from oracle.reference import Qwen3Shape
 
 pytestmark = pytest.mark.gpu
@@ -123,9 +123,8 @@ def test_persistent_decode_matches_oracle(device, setup_8b2):
     dec.stop_on_eos = False
     toks = dec.generate(torch.tensor(prompt), 10, steps_per_graph=4, use_graph=True)
     print(f"persistent {cfg.name}-shape decode: {toks}", flush=True)
-    # near-tie tolerance: bf16 activation rounding moves the 0.6B shape's smaller logits by a few 1e-3
-    tie = 2e-3 if cfg.hidden == 4096 else 5e-3
-    print(check_greedy_tokens(shape, dense, prompt, toks, tie_tol=tie))
+    print(check_greedy_tokens(shape, dense, prompt, toks, kv_history=(dec.k_cache, dec.v_cache),
+                              gpu_logits=decoder_step_logits(dec), label=f"persistent {cfg.name}"))
 
 
 def test_persistent_graph_replay_equals_eager(device, setup_8b2):
@@ -230,7 +229,9 @@ def test_persistent_long_kv_decode_matches_oracle(device, setup_8b_long):
     assert int(dec.status.item()) == 0 and len(toks) == 8
     print(f"tokens {toks}", flush=True)
     kv = (dec.k_cache[:, :start].cpu(), dec.v_cache[:, :start].cpu())
-    stats = check_greedy_tokens(shape, dense, prompt, toks, start=start, kv_init=kv, tie_tol=2e-3)
+    stats = check_greedy_tokens(shape, dense, prompt, toks, start=start, kv_init=kv,
+                                kv_history=(dec.k_cache, dec.v_cache), gpu_logits=decoder_step_logits(dec),
+                                label="persistent 8B from KV 4096")
     print(stats, flush=True)
 
 
@@ -256,31 +257,24 @@ def test_persistent_0_6b_full_depth_matches_oracle(device, policy):
     print(f"tokens {toks}", flush=True)
     # one more step's logits (RMSNorm -> bf16 -> LM-head GEMV over the persistent launch's h) against the
     # oracle's for the same token, position and KV history
-    from oracle.qwen3_check import oracle_step_logits
+    from oracle.qwen3_check import STEP_TOL_RMS, oracle_step_logits
     from tests.conftest import cosine
-    from torch2vk_amd import kernels
 
     pos, tok = int(dec.position.item()), int(dec.next_token.item())
-    kv = (dec.k_cache[:, :pos].cpu(), dec.v_cache[:, :pos].cpu())
-    dec.run_decode_embed()
-    dec.run_decode_layers()
-    x = kernels.rms_norm(dec.h.view(1, -1), w.norms["norm"],
-                         out=torch.empty(1, cfg.hidden, dtype=torch.bfloat16, device=device))
-    got = kernels.quantized_linear(x, w.packed["lm_head"], w.types["lm_head"]).view(-1).cpu().numpy()
+    got = dec.step_logits(pos, token=tok).cpu().numpy()
     assert int(dec.status.item()) == 0
     shape = Qwen3Shape(hidden=cfg.hidden, layers=cfg.layers, heads=cfg.heads, kv_heads=cfg.kv_heads,
                        head_dim=cfg.head_dim, mlp=cfg.mlp, vocab=cfg.vocab, rope_theta=cfg.rope_theta)
     dense = dense_weights({k: v.cpu().numpy() for k, v in w.packed.items()}, w.types,
                           {k: v.cpu().numpy() for k, v in w.norms.items()}, matrix_shapes(cfg))
-    del w, dec
-    ref = oracle_step_logits(shape, dense, *kv, tok, pos)
+    ref = oracle_step_logits(shape, dense, dec.k_cache[:, :pos].cpu(), dec.v_cache[:, :pos].cpu(), tok, pos)
     rms = float(np.sqrt(np.mean(ref * ref)))
     err = float(np.abs(got - ref).max())
     print(f"step logits at pos {pos}: max-abs {err:.4f} (rms {rms:.3f}), cos {cosine(got, ref):.6f}", flush=True)
-    # the per-step tolerance of test_gpu_model.py (3e-2 of the logits' rms; measured 1.5e-2 at 28 layers)
-    assert err <= 3e-2 * rms and cosine(got, ref) >= 0.9999
-    # near ties: two logits each within that tolerance
-    stats = check_greedy_tokens(shape, dense, prompt, toks, tie_tol_rms=6e-2)
+    # the per-step tolerance (3e-2 of the logits' rms; measured 1.5e-2 at 28 layers)
+    assert err <= STEP_TOL_RMS * rms and cosine(got, ref) >= 0.9999
+    stats = check_greedy_tokens(shape, dense, prompt, toks, kv_history=(dec.k_cache, dec.v_cache),
+                                gpu_logits=decoder_step_logits(dec), label=f"0.6B 28 layers {policy}")
     print(stats, flush=True)
 
 
@@ -372,5 +366,5 @@ def test_persistent_q4_k_m_decode_matches_oracle(device, setup_km):
     toks = dec.generate(torch.tensor(prompt), 10, steps_per_graph=4, use_graph=True)
     dec.check_status()
     print(f"persistent Q4_K_M {cfg.name}-shape decode: {toks}", flush=True)
-    tie = 2e-3 if cfg.hidden == 4096 else 5e-3
-    print(check_greedy_tokens(shape, dense, prompt, toks, tie_tol=tie))
+    print(check_greedy_tokens(shape, dense, prompt, toks, kv_history=(dec.k_cache, dec.v_cache),
+                              gpu_logits=decoder_step_logits(dec), label=f"persistent Q4_K_M {cfg.name}"))

@@ -1,6 +1,6 @@
 """GPU parity of the chunked matrix-core prefill: the chunk prologue kernel against the decode prologue
 (bit-exact cache rows) and the numpy oracle, and whole prompts prefilled in chunks against the CPU oracle
-decoder (greedy tokens, near-tie aware) and against the token-by-token prefill's KV cache."""
+decoder (greedy tokens, exact) and against the token-by-token prefill's KV cache."""
 
 from __future__ import annotations
 
@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import reference as R
-from oracle.qwen3_check import check_greedy_tokens, dense_weights
+from oracle.qwen3_check import check_greedy_tokens, decoder_step_logits, dense_weights
 from oracle.reference import Qwen3Shape
 from tests.conftest import assert_close
 
@@ -104,12 +104,14 @@ def test_chunked_prefill_decode_matches_oracle(device, policy, chunk):
     prompt = np.random.default_rng(2).integers(0, cfg.vocab, 37).tolist()
     dec = Qwen3Decoder(w, max_positions=96, max_new_tokens=16)
     dec.stop_on_eos = False
-    toks = dec.generate(torch.tensor(prompt), 10, steps_per_graph=4, prefill_chunk=chunk)
+    dec.prefill_chunked(torch.tensor(prompt), chunk=chunk)
+    prefill_h = dec.h.clone()  # the first token is selected from this row
+    dec.run_steps(9, steps_per_graph=4)
+    toks = dec.generated[:int(dec.length.item())].tolist()
     print(f"chunked prefill {policy} chunk={chunk}: {toks}", flush=True)
-    # near-tie allowance of two logits each within the per-step tolerance (3e-2 of the logit rms, see
-    # test_step_logits_within_tolerance): chunks of <= 8 tokens run on the GEMVs, whose tokens at a 0.023 margin
-    # step equal the token-by-token prefill's but not the oracle's teacher-forced replay
-    print(check_greedy_tokens(shape, dense, prompt, toks, tie_tol_rms=6e-2))
+    assert len(toks) == 10
+    print(check_greedy_tokens(shape, dense, prompt, toks, kv_history=(dec.k_cache, dec.v_cache),
+                              gpu_logits=decoder_step_logits(dec, prefill_h), label=f"chunked {policy} {chunk}"))
 
 
 def test_chunked_prefill_cache_matches_token_prefill(device):

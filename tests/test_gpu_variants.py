@@ -243,8 +243,8 @@ def test_run_decode_layer_matches_fused_path(device):
 def test_variant_decode_matches_oracle(device, policy, cfg_kw):
     """Greedy decode where every layer runs as run_decode_layer(rt, i, cache_position=pos) and the embedding
     as EMBEDDING_Q4_K_F32 (Q4_K_M: the Q6_K v rows through LINEAR_NOBIAS_Q4_QK_Q6_V_MATVEC_F32 and Q6_K o/down
-    through the Q6_K add variant) -- the oracle's tokens, near-tie aware."""
-    from oracle.qwen3_check import check_greedy_tokens
+    through the Q6_K add variant) -- the oracle's tokens."""
+    from oracle.qwen3_check import check_greedy_tokens, decoder_step_logits
     from torch2vk_amd import variants as V
     from torch2vk_amd.qwen3.dispatch import bind_model_tensors, run_decode_layer
     from torch2vk_amd.qwen3.model import Qwen3Decoder
@@ -277,4 +277,5 @@ def test_variant_decode_matches_oracle(device, policy, cfg_kw):
     if policy == "q4_k_m":
         assert {"linear_nobias_q4_qk_q6_v_matvec_f32", "linear_nobias_q6_k_matvec_add_f32"} <= used
     print(f"variant decode {policy}: {toks}", flush=True)
-    print(check_greedy_tokens(shape, dense, prompt, toks))
+    print(check_greedy_tokens(shape, dense, prompt, toks, kv_history=(dec.k_cache, dec.v_cache),
+                              gpu_logits=decoder_step_logits(dec), label=f"variants {policy}"))

@@ -305,6 +305,8 @@ extern "C" int t2h_embedding_q4_k(const void* w, uint64_t vocab, const int64_t* 
                                   float* out, void* stream) {
     if (!w || !ids || !out) return T2H_ERR_NULL;
     if (dim == 0 || dim % 256 != 0 || vocab == 0) return T2H_ERR_SHAPE;
+    // 16-B superblock loads and float4 stores
+    if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(out) % 16) return T2H_ERR_ALIGN;
     if (n_ids == 0) return T2H_OK;
     hipLaunchKernelGGL(embedding_q4_k_kernel, dim3(n_ids), dim3(256), 0, (hipStream_t)stream,
                        (const uint8_t*)w, ids, dim, vocab, out);
@@ -341,6 +343,7 @@ extern "C" int t2h_embedding_q4_k_seqs(uint32_t n_seq, const void* w, uint64_t v
     if (!w || !ids || !out) return T2H_ERR_NULL;
     if (n_seq == 0 || n_seq > (uint32_t)SEQS_MAX) return T2H_ERR_ARG;
     if (dim == 0 || dim % 256 != 0 || vocab == 0) return T2H_ERR_SHAPE;
+    if (reinterpret_cast<uintptr_t>(w) % 16) return T2H_ERR_ALIGN;  // 16-B superblock loads
     EmbedSeqsArgs a = {};
     for (uint32_t i = 0; i < n_seq; ++i) {
         if (!ids[i] || !out[i]) return T2H_ERR_NULL;

@@ -879,6 +879,7 @@ extern "C" int t2h_q4k_lm_head_argmax_partial_seqs(uint32_t n_seq, const float* 
     if (n == 0 || n % geo.rpw) return T2H_ERR_SHAPE;
     if (num_partials == 0) return T2H_ERR_ARG;
     if (reinterpret_cast<uintptr_t>(norm_w) % 16) return T2H_ERR_ALIGN;
+    if (reinterpret_cast<uintptr_t>(w) % 16) return T2H_ERR_ALIGN;  // 16-B superblock loads
     Q4HeadSeqsArgs a = {};
     for (uint32_t i = 0; i < n_seq; ++i) {
         if (!h[i] || !partial_scores[i] || !partial_tokens[i]) return T2H_ERR_NULL;

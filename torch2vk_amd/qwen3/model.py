@@ -60,6 +60,8 @@ class Qwen3Decoder:
     weight mix).  None (the default) picks the persistent kernel when it
     applies: on MI355X it saves the launch and ramp of ~250 kernels per token."""
 
+    PREFILL_GRAPHS = 4  # captured prefill graphs kept (prefill_graphed)
+
     def __init__(self, weights: Qwen3Weights, *, max_positions: int, max_new_tokens: int, device=None,
                  persistent: bool | None = None,
                  kv_cache: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
@@ -102,7 +104,7 @@ class Qwen3Decoder:
         self.eos = torch.tensor(c.eos_token_ids, dtype=torch.int64, device=dev)
         self.stop_on_eos = True
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
-        self._prefill_graphs: dict[tuple[int, int, int], tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+        self._prefill_graphs: dict[tuple[int, int, int, bool], tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
         self.persistent = False
         self.status = torch.zeros(1, dtype=torch.int32, device=dev)
         if persistent is not False:
@@ -236,6 +238,42 @@ class Qwen3Decoder:
         kernels.token_store(self.next_token, self.done, self.generated, self.length, self.stopped,
                             stop_on_eos=self.stop_on_eos, token_index_ptr=self.length,
                             advance=self.position if advance else None)
+
+    def logits(self, h: torch.Tensor | None = None) -> torch.Tensor:
+        """fp32 [vocab] logits of one residual-stream row (default: the decoder's own h): final RMSNorm -> bf16 ->
+        LM-head GEMV of the head's type.  A decode step's fused LM head + argmax never writes these; they are
+        for checking a step's token against its scores."""
+        c = self.config
+        h = self.h if h is None else h
+        x = kernels.rms_norm(h.reshape(1, c.hidden), self._n("norm"),
+                             out=torch.empty(1, c.hidden, dtype=torch.bfloat16, device=self.device), eps=c.rms_eps)
+        return kernels.quantized_linear(x, self._w("lm_head"), self.types["lm_head"]).view(-1)
+
+    def step_logits(self, position: int, *, token: int | None = None,
+                    embed: torch.Tensor | None = None) -> torch.Tensor:
+        """fp32 [vocab] logits of the decode step at ``position`` over the cache rows 0..position-1 as they stand,
+        its input the embedding of ``token`` or the fp32 row ``embed``: the same layer launches as a decode step,
+        then ``logits``.  The decoder's position, token, residual stream and the cache rows at ``position`` are
+        restored afterwards, so a finished generation can be re-examined step by step."""
+        if (token is None) == (embed is None):
+            raise ValueError("pass token or embed")
+        if not 0 <= position < self.max_positions:
+            raise ValueError(f"position {position} outside the KV capacity {self.max_positions}")
+        saved = [t.clone() for t in (self.position, self.next_token, self.h, self.k_cache[:, position],
+                                     self.v_cache[:, position])]
+        self.position.fill_(position)
+        if embed is None:
+            self.next_token.fill_(int(token))
+            self.run_decode_embed()
+        else:
+            self.h.copy_(embed.reshape(-1))
+        self.run_decode_layers()
+        out = self.logits()
+        self.check_status()
+        for dst, src in zip((self.position, self.next_token, self.h, self.k_cache[:, position],
+                             self.v_cache[:, position]), saved):
+            dst.copy_(src)
+        return out
 
     def run_decode_layers(self, trace: torch.Tensor | None = None) -> None:
         """Every layer at the device-resident position: one persistent launch, or one launch per op.
@@ -435,15 +473,22 @@ class Qwen3Decoder:
 
     def prefill_graphed(self, prompt_ids: torch.Tensor, *, start: int = 0, chunk: int = 2048) -> None:
         """prefill_chunked of a token-id prompt replayed from a HIP graph: the first call for a (length, start,
-        chunk) captures the whole prefill (every layer's launches, the LM head and the token store) reading the
-        ids from a buffer of the decoder's; later calls copy the ids into that buffer and replay.  Results are
-        prefill_chunked's bit for bit; a short prompt's prefill is bound by launch overhead, which the graph
-        removes."""
+        chunk, stop_on_eos) captures the whole prefill (every layer's launches, the LM head and the token store)
+        reading the ids from a buffer of the decoder's; later calls copy the ids into that buffer and replay.
+        Results are prefill_chunked's bit for bit; a short prompt's prefill is bound by launch overhead, which the
+        graph removes.  Each captured graph keeps a memory pool holding every intermediate of one whole prefill
+        (about the GEMM activations of one chunk), so at most PREFILL_GRAPHS of them are kept, least recently
+        used first out; ``clear_prefill_graphs`` drops them all."""
         ids = prompt_ids.to(device=self.device, dtype=torch.int64).view(-1)
         if ids.numel() == 0:
             raise ValueError("empty prompt")
-        key = (ids.numel(), start, chunk)
-        if key not in self._prefill_graphs:
+        # stop_on_eos is read on the host when the token store is launched, so the capture freezes it
+        key = (ids.numel(), start, chunk, bool(self.stop_on_eos))
+        if key in self._prefill_graphs:
+            self._prefill_graphs[key] = self._prefill_graphs.pop(key)  # most recently used last
+        else:
+            while len(self._prefill_graphs) >= self.PREFILL_GRAPHS:
+                self._prefill_graphs.pop(next(iter(self._prefill_graphs)))
             buf = ids.clone()
             side = torch.cuda.Stream(device=self.device)
             side.wait_stream(torch.cuda.current_stream(self.device))
@@ -457,6 +502,10 @@ class Qwen3Decoder:
         g, buf = self._prefill_graphs[key]
         buf.copy_(ids)
         g.replay()
+
+    def clear_prefill_graphs(self) -> None:
+        """Drop every captured prefill graph and its memory pool."""
+        self._prefill_graphs.clear()
 
     def prefill_embeds(self, embeds: torch.Tensor, start: int = 0) -> None:
         """Feed a prompt given as fp32 input embeddings [T, hidden] -- a Qwen3-ASR prompt after the audio
@@ -574,7 +623,7 @@ class Qwen3DecoderGroup:
                                           causal_offset=start)
         kernels.quantized_linear(attn.view(rows, c.q_dim), d0._w(p + "o"), t[p + "o"], out=h, residual=h)
         x = kernels.rms_norm(h, d0._n(p + "post_norm"), out=x, eps=c.rms_eps)
-        if t[p + "gate"] == t[p + "up"]:
+        if t[p + "gate"] == t[p + "up"] and rows > kernels.GEMV_MAX_ROWS:
             act = kernels.gemm_swiglu(x, d0._w(p + "gate"), d0._w(p + "up"), t[p + "gate"])
         else:
             gate = kernels.quantized_linear(x, d0._w(p + "gate"), t[p + "gate"], out_dtype=torch.float32)
