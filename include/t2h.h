@@ -466,6 +466,42 @@ int t2h_index_copy_rows(void* dst, uint64_t dst_rows, uint32_t row_bytes, const 
 int t2h_embedding_q8_0(const void* w, uint64_t vocab, const int64_t* ids, uint32_t n_ids, uint32_t dim, float* out,
                        void* stream);
 
+/* ------------------------------------ the reference's unfused operators --- */
+/* cos / sin fp32 [B, T, D] of positions start + t (start from *start_position_ptr when it is not NULL, else
+ * start_position): inv_freq(d) = theta^(-2 (d mod D/2) / D), values times attention_scaling.  The factors the
+ * fused kernels compute in registers (rope.h), bit for bit.  replaces ROPE_TABLE_F32
+ * (src/torch2vk/runtime/rope_table.py:32-122). */
+int t2h_rope_table(float* cos_out, float* sin_out, uint32_t b, uint32_t t, uint32_t d, float theta,
+                   uint32_t start_position, const int32_t* start_position_ptr, float attention_scaling, void* stream);
+/* Per-head RMSNorm over D = 128 (weight fp32 [D], eps) then rotate-half RoPE from a table:
+ * out[d] = n[d] cos[d] - n[d + 64] sin[d], out[d + 64] = n[d + 64] cos[d + 64] + n[d] sin[d + 64], per row
+ * (b, t, g) of x [B, T, G, D] (fp32 or bf16) with the table row (b, t) of cos / sin fp32 [B, T, D]; out fp32 or
+ * bf16 [B, T, G, D], or [B, G, T, D] with transpose_out.  replaces RMS_NORM_ROPE_TRANSPOSE_F16
+ * (src/models/optimized_qwen3/shaders/rms_norm_rope_transpose_f16.py:22-145) and RMS_NORM_ROPE_TOKEN_F32 /
+ * _TO_F16 (src/models/optimized_qwen3/shaders/rms_norm_rope_token_f32.py:22-99). */
+int t2h_rms_norm_rope(const void* x, int x_dtype, const float* weight, const float* cos_table,
+                      const float* sin_table, void* out, int out_dtype, uint32_t b, uint32_t t, uint32_t g, uint32_t d,
+                      int transpose_out, float eps, void* stream);
+/* Rows src [B, T, H, D] (fp32 or bf16) into n_caches (1..3) token-major bf16 caches [B, s_caps[c], H, D] at
+ * positions[t] (int64 [T]; a position outside a cache writes nothing there).  replaces
+ * TOKEN_MAJOR_KV_CACHE_WRITE_F16_PAIR / _TRIPLE and TOKEN_MAJOR_VALUE_CACHE_WRITE_F32_TO_F16_PAIR / _TRIPLE
+ * (src/models/optimized_qwen3/shaders/token_major_kv_cache_write_f16_pair.py:20-103). */
+int t2h_kv_cache_write(const void* src, int src_dtype, const int64_t* positions, uint32_t n_caches,
+                       void* const* caches, const uint32_t* s_caps, uint32_t b, uint32_t t, uint32_t h, uint32_t d,
+                       void* stream);
+/* The best (score, token) of each chunk of 1024 of g partials (ties to the lower token id): chunk_scores /
+ * chunk_tokens [ceil(g / 1024)].  replaces QWEN3_TOKEN_SELECT_REDUCE_CHUNKS_F32
+ * (src/torch2vk/export/shaders/qwen3_token_select_reduce_f32.py:22-120). */
+int t2h_token_select_chunks(const float* scores, const uint32_t* tokens, uint32_t g, float* chunk_scores,
+                            uint32_t* chunk_tokens, void* stream);
+/* out = x + y over n elements of dtype (fp32, or bf16 with an fp32 sum rounded once); out may alias x or y.
+ * replaces ADD_F32_PREFILL (src/models/optimized_qwen3/shaders/add_f32_prefill.py:20-60) and ADD_F32_36
+ * (src/models/optimized_qwen3/shaders/add_f32_36.py:22-80). */
+int t2h_add(const void* x, const void* y, void* out, int dtype, uint64_t n, void* stream);
+/* out [B, 1, H] (fp32 or bf16) = row S - 1 of each batch of x fp32 [B, S, H].  replaces
+ * SLICE_LAST_TOKEN_F32_TO_F16 (src/models/optimized_qwen3/shaders/slice_last_token_f32_to_f16.py:19-60). */
+int t2h_slice_last_token(const float* x, void* out, int out_dtype, uint32_t b, uint32_t s, uint32_t h, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -91,6 +91,23 @@ def test_argument_validation_returns_status(lib):
     assert lib.t2h_embedding_q4_k_seqs(2, odd, 10, pa, 1024, pa, None) == 7
     assert lib.t2h_embedding_q4_k(odd, 10, fake, 1, 1024, fake, None) == 7
     assert lib.t2h_embedding_q4_k(fake, 10, fake, 1, 1024, odd, None) == 7
+    # the unfused operators: null pointers, dtype codes, head_dim, cache count, alignment
+    assert lib.t2h_rope_table(None, fake, 1, 4, 128, 1e6, 0, None, 1.0, None) == 1
+    assert lib.t2h_rope_table(fake, fake, 1, 4, 127, 1e6, 0, None, 1.0, None) == 2
+    assert lib.t2h_rope_table(fake, fake, 1, 4, 128, 0.0, 0, None, 1.0, None) == 2
+    assert lib.t2h_rms_norm_rope(fake, 0, fake, fake, fake, fake, 0, 1, 4, 2, 64, 0, 1e-6, None) == 4
+    assert lib.t2h_rms_norm_rope(fake, 7, fake, fake, fake, fake, 0, 1, 4, 2, 128, 0, 1e-6, None) == 3
+    assert lib.t2h_rms_norm_rope(fake, 0, None, fake, fake, fake, 0, 1, 4, 2, 128, 0, 1e-6, None) == 1
+    caps = (ctypes.c_uint32 * 4)(8, 8, 8, 8)
+    cp = ctypes.addressof(caps)
+    assert lib.t2h_kv_cache_write(fake, 1, fake, 0, pa, cp, 1, 2, 2, 128, None) == 5
+    assert lib.t2h_kv_cache_write(fake, 1, fake, 4, pa, cp, 1, 2, 2, 128, None) == 5
+    assert lib.t2h_kv_cache_write(ctypes.c_void_p(0x1002), 1, fake, 2, pa, cp, 1, 2, 2, 128, None) == 7
+    assert lib.t2h_kv_cache_write(fake, 2, fake, 2, pa, cp, 1, 2, 2, 128, None) == 3
+    assert lib.t2h_token_select_chunks(fake, fake, 0, fake, fake, None) == 2
+    assert lib.t2h_token_select_chunks(None, fake, 8, fake, fake, None) == 1
+    assert lib.t2h_add(fake, fake, fake, 5, 16, None) == 3
+    assert lib.t2h_slice_last_token(fake, fake, 0, 1, 0, 16, None) == 2
     assert lib.t2h_token_select_store_seqs(5, pa, pa, 8, fake, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 5
     assert lib.t2h_token_select_store_seqs(2, pa, pa, 0, fake, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 2
     assert lib.t2h_token_select_store_seqs(2, pa, pa, 8, None, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 1

@@ -203,7 +203,7 @@ def _model(device, policy, cfg_kw, seed):
 def test_run_decode_layer_matches_fused_path(device):
     """One step of every layer through the named variants equals the decoder's fused per-op step (RMSNorm in
     the GEMV prologues, SwiGLU in the gate|up epilogue) to bf16 rounding of the activations; KV rows match."""
-    from torch2vk_amd.qwen3.dispatch import bind_model_tensors, run_decode_layer
+    from torch2vk_amd.qwen3.dispatch import bind_model_tensors, run_decode_layer, run_decode_rope
     from torch2vk_amd.qwen3.model import Qwen3Decoder
     from torch2vk_amd.runtime import RuntimeSession
 
@@ -222,15 +222,21 @@ def test_run_decode_layer_matches_fused_path(device):
     dec.v_cache.copy_(vc0)
     rt = RuntimeSession(device, record=True)
     bind_model_tensors(dec)
+    run_decode_rope(rt, cache_position=pos, rope_theta=cfg.rope_theta)
     for i in range(cfg.layers):
         run_decode_layer(rt, i, cache_position=pos)
     names = [r.shader for r in rt.records]
-    assert names[:8] == ["rms_norm_mul_f16_f32", "linear_nobias_q4_k_qkv_matvec_f32",
-                         "sdpa_decode_qk_norm_rope_cache_write_f32", "linear_nobias_q4_k_matvec_add_f32",
-                         "rms_norm_mul_f16_f32", "linear_nobias_q4_k_qk_matvec_f32", "swiglu_f16",
-                         "linear_nobias_q4_k_matvec_add_f32"] and len(names) == 8 * cfg.layers
+    # the reference's sequence (decode_layer.py:60-128) after the step's RoPE table
+    assert names[:11] == ["rope_table_f32", "rms_norm_mul_f16_f32", "linear_nobias_q4_k_qkv_matvec_f32",
+                          "rms_norm_rope_transpose_f16", "rms_norm_rope_transpose_f16",
+                          "sdpa_decode_cache_write_f32", "linear_nobias_q4_k_matvec_add_f32",
+                          "rms_norm_mul_f16_f32", "linear_nobias_q4_k_qk_matvec_f32", "swiglu_f16",
+                          "linear_nobias_q4_k_matvec_add_f32"] and len(names) == 1 + 10 * cfg.layers
     scale = float(h_fused.abs().max())
     assert_close(dec.h.cpu().numpy(), h_fused.cpu().numpy(), max_abs=1e-2 * scale, min_cos=0.9999, what="h")
+    # layer 0's new K row: the table-driven q/k norm + RoPE and the fused attention prologue share their
+    # arithmetic (rope.h), and the RMSNorm + q|k|v GEMVs read the same bf16 input, so the row is bit-identical
+    assert torch.equal(dec.k_cache[0, pos], kc_fused[0, pos])
     assert_close(dec.k_cache[:, pos].float().cpu().numpy(), kc_fused[:, pos].float().cpu().numpy(),
                  max_abs=3e-2, min_cos=0.9999, what="k row")
     assert torch.equal(dec.k_cache[:, :pos], kc_fused[:, :pos])
@@ -246,7 +252,7 @@ def test_variant_decode_matches_oracle(device, policy, cfg_kw):
     through the Q6_K add variant) -- the oracle's tokens."""
     from oracle.qwen3_check import check_greedy_tokens, decoder_step_logits
     from torch2vk_amd import variants as V
-    from torch2vk_amd.qwen3.dispatch import bind_model_tensors, run_decode_layer
+    from torch2vk_amd.qwen3.dispatch import bind_model_tensors, run_decode_layer, run_decode_rope
     from torch2vk_amd.qwen3.model import Qwen3Decoder
     from torch2vk_amd.runtime import RuntimeSession
 
@@ -266,6 +272,7 @@ def test_variant_decode_matches_oracle(device, policy, cfg_kw):
                                  output=dec.h.view(1, 1, cfg.hidden))
         else:
             dec.run_decode_embed()
+        run_decode_rope(rt, cache_position=step, rope_theta=cfg.rope_theta)
         for i in range(cfg.layers):
             run_decode_layer(rt, i, cache_position=step)
         dec.run_lm_head_select()

@@ -98,7 +98,17 @@ def test_reference_variant_names():
               "linear_nobias_q6_k_matvec_add_f32", "linear_nobias_q8_0_matvec_f32", "linear_nobias_q4_k_qkv_matvec_f32",
               "linear_nobias_q4_k_qk_matvec_f32", "linear_nobias_q4_qk_q6_v_matvec_f32", "linear_nobias_q4_k_f32",
               "linear_nobias_q8_0_f32", "rms_norm_mul_f16_f32", "swiglu_f16", "embedding_q4_k_f32",
-              "sdpa_decode_cache_write_f32"):
+              "sdpa_decode_cache_write_f32",
+              # the rest of the decode step and the prefill (src/models/optimized_qwen3/dispatch/*.py, run.py)
+              "lm_head_q6_k_argmax_partial_f16", "qwen3_token_select_reduce_chunks_f32",
+              "qwen3_token_select_reduce_f32", "qwen3_token_store_eos_f32", "qwen3_token_store_eos",
+              "qwen3_token_store", "rms_norm_rope_transpose_f16", "rope_table_f32", "rms_norm_rope_token_f32",
+              "rms_norm_rope_token_f32_to_f16", "llama_flash_attn_f32_f16_f16", "fa_mask_opt_f16",
+              "llama_matmul_q4_k_f32_m", "llama_matmul_q4_k_f32_l", "llama_matmul_q6_k_f32_m",
+              "llama_matmul_q6_k_f32_l", "embedding_q4_k_act_f32", "embedding_q8_0_f32", "rms_norm_mul_f32",
+              "add_f32_prefill", "add_f32_36", "slice_last_token_f32_to_f16", "swiglu_f32",
+              "token_major_kv_cache_write_f16_pair", "token_major_kv_cache_write_f16_triple",
+              "token_major_value_cache_write_f32_to_f16_pair", "token_major_value_cache_write_f32_to_f16_triple"):
         assert n in names, n
     # the variant the rows select, as make_linear_nobias_q4_k_m_variant does
     assert V.linear_nobias_quantized_variant(1, Q4_K_WORDS) is V.LINEAR_NOBIAS_Q4_K_MATVEC_F32
@@ -138,3 +148,42 @@ def test_matvec_shape_query():
     assert not kernels.matvec_supported("q6_k", 16384, 64)      # longer rows than the register-resident x
     assert kernels.matvec_supported("q8_0", 512, 80) and not kernels.matvec_supported("q8_0", 256, 8)
     assert not kernels.matvec_supported("q4_k", 1000, 64)       # not a whole number of superblocks
+
+
+def test_named_dispatch_functions_exist_and_need_bound_tensors():
+    """The reference's dispatch function names (src/models/optimized_qwen3/dispatch/*.py) are all here, and each
+    refuses to run before bind_model_tensors / bind_prefill_tensors."""
+    import torch2vk_amd.qwen3.dispatch as D
+
+    for name in ("run_decode_embed", "run_decode_layer", "run_decode_norm", "run_prefill_full_embed",
+                 "run_prefill_tail_embed", "run_prefill_full_layer", "run_prefill_tail_layer",
+                 "run_prefill_tail_last_layer_tail", "run_prefill_full_mask_opt", "run_prefill_tail_mask_opt",
+                 "run_text_norm", "run_lm_head_select", "run_token_store", "run_decode_step", "run_prefill"):
+        assert callable(getattr(D, name)), name
+    D._MODEL = None
+    rt = RuntimeSession("cpu")
+    with pytest.raises(RuntimeError, match="bind_model_tensors"):
+        D.run_decode_embed(rt)
+    with pytest.raises(RuntimeError, match="bind_model_tensors"):
+        D.run_prefill_tail_layer(rt, 0)
+
+
+def test_float_push_input():
+    """ROPE_TABLE_F32's theta is a float push input: a number is taken, a tensor or a string is refused before
+    the launch; start_position stays an unsigned input."""
+    from torch2vk_amd import variants as V
+
+    log = []
+    probe = ShaderVariant("probe_rope", "test", ShaderContract(
+        "Probe", "probe_rope", V.ROPE_TABLE_F32.contract.fields, V.ROPE_TABLE_F32.contract.push_inputs),
+        lambda rt, t, sym, push: log.append(dict(push)))
+    rt = RuntimeSession("cpu")
+    cos, sin = torch.zeros(1, 3, 128), torch.zeros(1, 3, 128)
+    probe(rt, cos=cos, sin=sin, theta=1e6, start_position=7)
+    assert log == [{"theta": 1e6, "start_position": 7}]
+    with pytest.raises(TypeError, match="theta"):
+        probe(rt, cos=cos, sin=sin, theta="1e6", start_position=7)
+    with pytest.raises(TypeError, match="start_position"):
+        probe(rt, cos=cos, sin=sin, theta=1e6, start_position=-1)
+    with pytest.raises(ValueError, match="kind"):
+        PushConstantInput("x", "float64")

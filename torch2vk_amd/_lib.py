@@ -107,6 +107,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                       _u32, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
     "t2h_qk_norm_rope_cache_seqs": (_i32, [_vp, _u64, _vp, _u64, _vp, _u64, _vp, _vp, _f32, _f32, ctypes.c_int32,
                                            _u32, _u32, _u32, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
+    "t2h_rope_table": (_i32, [_vp, _vp, _u32, _u32, _u32, _f32, _u32, _vp, _f32, _vp]),
+    "t2h_rms_norm_rope": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _i32, _u32, _u32, _u32, _u32, _i32, _f32, _vp]),
+    "t2h_kv_cache_write": (_i32, [_vp, _i32, _vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "t2h_token_select_chunks": (_i32, [_vp, _vp, _u32, _vp, _vp, _vp]),
+    "t2h_add": (_i32, [_vp, _vp, _vp, _i32, _u64, _vp]),
+    "t2h_slice_last_token": (_i32, [_vp, _vp, _i32, _u32, _u32, _u32, _vp]),
 }
 
 

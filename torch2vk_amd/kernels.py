@@ -21,6 +21,9 @@ Q8_0_BYTES = 34
 RMS_EPS = 1e-6
 
 _OUT_DTYPES = {torch.float32: T2H_DTYPE_F32, torch.bfloat16: T2H_DTYPE_BF16}
+# the reference's uint32 buffers (token ids of the LM head's partials, done / length / stopped flags), or
+# int32 ones of the same bits
+_TOKEN_DTYPES = (torch.int32, torch.uint32)
 WTYPES = {"q4_k": _lib.T2H_WTYPE_Q4_K, "q6_k": _lib.T2H_WTYPE_Q6_K, "q8_0": _lib.T2H_WTYPE_Q8_0}
 
 
@@ -177,7 +180,7 @@ def q4k_lm_head_argmax_partial(x: torch.Tensor, w: torch.Tensor, partial_scores:
     k = int(x.numel())
     n = _check_q4(w, "weight", None, k)
     _check(partial_scores, "partial_scores", torch.float32, align=4)
-    _check(partial_tokens, "partial_tokens", torch.int32, align=4)
+    _check(partial_tokens, "partial_tokens", _TOKEN_DTYPES, align=4)
     g = int(partial_scores.numel())
     if partial_tokens.numel() != g or g == 0:
         raise ValueError("partial_scores and partial_tokens must have the same non-zero length")
@@ -204,7 +207,7 @@ def q4k_lm_head_argmax_partial_seqs(hs: list[torch.Tensor], w: torch.Tensor, par
     g = int(partial_scores[0].numel())
     for sc, tk in zip(partial_scores, partial_tokens):
         _check(sc, "partial_scores", torch.float32, align=4)
-        _check(tk, "partial_tokens", torch.int32, align=4)
+        _check(tk, "partial_tokens", _TOKEN_DTYPES, align=4)
         if sc.numel() != g or tk.numel() != g or g == 0:
             raise ValueError("partial_scores and partial_tokens must all have the same non-zero length")
     arr = lambda ts: (ctypes.c_void_p * n_seq)(*[t.data_ptr() for t in ts])  # noqa: E731
@@ -287,7 +290,7 @@ def lm_head_argmax_partial(x: torch.Tensor, w: torch.Tensor, wtype: str, partial
     k = int(x.numel())
     n = _check_packed(w, "weight", "q6_k", k)
     _check(partial_scores, "partial_scores", torch.float32, align=4)
-    _check(partial_tokens, "partial_tokens", torch.int32, align=4)
+    _check(partial_tokens, "partial_tokens", _TOKEN_DTYPES, align=4)
     g = int(partial_scores.numel())
     if partial_tokens.numel() != g or g == 0:
         raise ValueError("partial_scores and partial_tokens must have the same non-zero length")
@@ -520,10 +523,10 @@ def set_gemv_max_blocks(max_blocks: int, max_blocks_norm: int = 0) -> None:
 def token_select(partial_scores: torch.Tensor, partial_tokens: torch.Tensor, eos_ids: torch.Tensor,
                  next_token: torch.Tensor, done: torch.Tensor) -> None:
     _check(partial_scores, "scores", torch.float32, align=4)
-    _check(partial_tokens, "tokens", torch.int32, align=4)
+    _check(partial_tokens, "tokens", _TOKEN_DTYPES, align=4)
     _check(eos_ids, "eos_token_ids", torch.int64, align=8)
     _check(next_token, "next_token", torch.int64, align=8)
-    _check(done, "done", torch.int32, align=4)
+    _check(done, "done", _TOKEN_DTYPES, align=4)
     call("t2h_token_select", ptr(partial_scores), ptr(partial_tokens), partial_scores.numel(), ptr(eos_ids),
          eos_ids.numel(), ptr(next_token), ptr(done), stream_handle())
 
@@ -532,10 +535,10 @@ def token_store(next_token: torch.Tensor, done: torch.Tensor, generated: torch.T
                 stopped: torch.Tensor, *, stop_on_eos: bool = True, token_index: int = 0,
                 token_index_ptr: torch.Tensor | None = None, advance: torch.Tensor | None = None) -> None:
     _check(next_token, "next_token", torch.int64, align=8)
-    _check(done, "done", torch.int32, align=4)
+    _check(done, "done", _TOKEN_DTYPES, align=4)
     _check(generated, "generated_tokens", torch.int64, align=8)
-    _check(length, "generated_length", torch.int32, align=4)
-    _check(stopped, "stopped", torch.int32, align=4)
+    _check(length, "generated_length", _TOKEN_DTYPES, align=4)
+    _check(stopped, "stopped", _TOKEN_DTYPES, align=4)
     if token_index_ptr is not None:
         _check(token_index_ptr, "token_index", torch.int32, align=4)
     if advance is not None:
@@ -549,13 +552,13 @@ def token_select_store(partial_scores: torch.Tensor, partial_tokens: torch.Tenso
                        stopped: torch.Tensor, *, stop_on_eos: bool = True, advance: torch.Tensor | None = None) -> None:
     """token_select + token_store (index from the device length counter) in one launch."""
     _check(partial_scores, "scores", torch.float32, align=4)
-    _check(partial_tokens, "tokens", torch.int32, align=4)
+    _check(partial_tokens, "tokens", _TOKEN_DTYPES, align=4)
     _check(eos_ids, "eos_token_ids", torch.int64, align=8)
     _check(next_token, "next_token", torch.int64, align=8)
-    _check(done, "done", torch.int32, align=4)
+    _check(done, "done", _TOKEN_DTYPES, align=4)
     _check(generated, "generated_tokens", torch.int64, align=8)
-    _check(length, "generated_length", torch.int32, align=4)
-    _check(stopped, "stopped", torch.int32, align=4)
+    _check(length, "generated_length", _TOKEN_DTYPES, align=4)
+    _check(stopped, "stopped", _TOKEN_DTYPES, align=4)
     if advance is not None:
         _check(advance, "advance", torch.int32, align=4)
     call("t2h_token_select_store", ptr(partial_scores), ptr(partial_tokens), partial_scores.numel(), ptr(eos_ids),
@@ -583,12 +586,12 @@ def token_select_store_seqs(partial_scores: list[torch.Tensor], partial_tokens: 
     _check(eos_ids, "eos_token_ids", torch.int64, align=8)
     for i in range(n):
         _check(partial_scores[i], "scores", torch.float32, align=4)
-        _check(partial_tokens[i], "tokens", torch.int32, align=4)
+        _check(partial_tokens[i], "tokens", _TOKEN_DTYPES, align=4)
         _check(next_tokens[i], "next_token", torch.int64, align=8)
-        _check(dones[i], "done", torch.int32, align=4)
+        _check(dones[i], "done", _TOKEN_DTYPES, align=4)
         _check(generated[i], "generated_tokens", torch.int64, align=8)
-        _check(lengths[i], "generated_length", torch.int32, align=4)
-        _check(stopped[i], "stopped", torch.int32, align=4)
+        _check(lengths[i], "generated_length", _TOKEN_DTYPES, align=4)
+        _check(stopped[i], "stopped", _TOKEN_DTYPES, align=4)
         if advance:
             _check(advance[i], "advance", torch.int32, align=4)
         if partial_scores[i].numel() != g or partial_tokens[i].numel() != g or generated[i].numel() != cap:
@@ -792,7 +795,7 @@ FA_BLOCK_QUERIES = 128  # queries per flash-attention block (a row of mask tiles
 FA_TILE_KEYS = 64       # keys per flash-attention tile
 
 
-def fa_mask_tiles(mask: torch.Tensor) -> torch.Tensor:
+def fa_mask_tiles(mask: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """uint8 [B, ceil(T/128), ceil(S/64)] class of each 128 x 64 block of an additive fp32 mask [B, T, S]:
     1 all masked (every entry <= -FLT_MAX/2), 2 all zero, 0 mixed (the reference's FA_MASK_OPT_F16 rule).  A mask
     used by several attention calls (every layer of one pass) is classified once."""
@@ -800,8 +803,11 @@ def fa_mask_tiles(mask: torch.Tensor) -> torch.Tensor:
     if mask.dim() != 3:
         raise ValueError(f"mask must be rank 3 [B, T, S], got {tuple(mask.shape)}")
     b, t_len, s_len = mask.shape
-    tiles = torch.empty(b, -(-t_len // FA_BLOCK_QUERIES), -(-s_len // FA_TILE_KEYS), dtype=torch.uint8,
-                        device=mask.device)
+    want = (b, -(-t_len // FA_BLOCK_QUERIES), -(-s_len // FA_TILE_KEYS))
+    tiles = torch.empty(want, dtype=torch.uint8, device=mask.device) if out is None else out
+    _check(tiles, "mask_tiles", torch.uint8, align=1)
+    if tuple(tiles.shape) != want:
+        raise ValueError(f"mask_tiles must be {want}, got {tuple(tiles.shape)}")
     call("t2h_fa_mask_tiles", ptr(mask), b, t_len, s_len, mask.stride(0), mask.stride(1), ptr(tiles),
          stream_handle())
     return tiles
@@ -896,13 +902,13 @@ def flash_attn_segments(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_se
 
 
 def embedding_q4_k(w: torch.Tensor, ids: torch.Tensor, dim: int, out: torch.Tensor | None = None) -> torch.Tensor:
-    _check(w, "weight", torch.uint8, align=1)
+    _check(w, "weight", torch.uint8)  # 16-byte superblock loads
     _check(ids, "indices", torch.int64, align=8)
     if w.shape[1] != q4_k_row_bytes(dim):
         raise ValueError("embedding weight width does not match dim")
     if out is None:
         out = torch.empty(ids.numel(), dim, dtype=torch.float32, device=w.device)
-    _check(out, "output", torch.float32, align=4)
+    _check(out, "output", torch.float32)  # float4 stores
     call("t2h_embedding_q4_k", ptr(w), int(w.shape[0]), ptr(ids), ids.numel(), dim, ptr(out), stream_handle())
     return out
 
@@ -1222,3 +1228,119 @@ def omnivoice_token_update_topk(cand_tokens: torch.Tensor, cand_scores: torch.Te
         raise ValueError("candidates and tokens must hold C * T values")
     call("t2h_omnivoice_token_update_topk", ptr(cand_tokens), ptr(cand_scores), ptr(tokens), ptr(batch_input_ids), c,
          n // c, s, int(unmask_count), stream_handle())
+
+
+# ----------------------------------------------- the reference's unfused operators --
+
+def rope_table(cos: torch.Tensor, sin: torch.Tensor, start_position: int | torch.Tensor, *, theta: float,
+               attention_scaling: float = 1.0) -> None:
+    """cos / sin fp32 [B, T, D] of positions start_position + t (ROPE_TABLE_F32); ``start_position`` an int or a
+    one-element int32 device tensor (read at run time, so a captured graph replays it)."""
+    _check(cos, "cos", torch.float32, align=4)
+    _check(sin, "sin", torch.float32, align=4)
+    if cos.dim() != 3 or sin.shape != cos.shape:
+        raise ValueError(f"cos and sin must be fp32 [B, T, D] of one shape, got {tuple(cos.shape)} {tuple(sin.shape)}")
+    b, t_len, d = (int(x) for x in cos.shape)
+    if isinstance(start_position, torch.Tensor):
+        _check(start_position, "start_position", torch.int32, align=4)
+        if start_position.numel() != 1:
+            raise ValueError("start_position must have one element")
+        start, start_ptr = 0, ptr(start_position)
+    else:
+        if int(start_position) < 0:
+            raise ValueError("start_position must be non-negative")
+        start, start_ptr = int(start_position), None
+    call("t2h_rope_table", ptr(cos), ptr(sin), b, t_len, d, float(theta), start, start_ptr, float(attention_scaling),
+         stream_handle())
+
+
+def rms_norm_rope(x: torch.Tensor, weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, out: torch.Tensor, *,
+                  transpose_out: bool, eps: float = RMS_EPS) -> torch.Tensor:
+    """Per-head RMSNorm (D = 128) + RoPE from a table: x [B, T, G, D] fp32 / bf16, cos / sin fp32 [B, T, D] ->
+    out [B, T, G, D], or [B, G, T, D] when ``transpose_out`` (RMS_NORM_ROPE_TRANSPOSE_F16,
+    RMS_NORM_ROPE_TOKEN_F32)."""
+    _check(x, "x", tuple(_OUT_DTYPES), align=4)
+    _check(weight, "weight", torch.float32, align=4)
+    _check(out, "output", tuple(_OUT_DTYPES), align=4)
+    if x.dim() != 4:
+        raise ValueError(f"x must be [B, T, G, D], got {tuple(x.shape)}")
+    b, t_len, g, d = (int(v) for v in x.shape)
+    for tab, name in ((cos, "cos"), (sin, "sin")):
+        _check(tab, name, torch.float32, align=4)
+        if tuple(tab.shape) != (b, t_len, d):
+            raise ValueError(f"{name} must be [{b}, {t_len}, {d}], got {tuple(tab.shape)}")
+    if weight.numel() != d:
+        raise ValueError(f"weight must have {d} elements")
+    want = (b, g, t_len, d) if transpose_out else (b, t_len, g, d)
+    if tuple(out.shape) != want:
+        raise ValueError(f"output must be {want}, got {tuple(out.shape)}")
+    call("t2h_rms_norm_rope", ptr(x), _OUT_DTYPES[x.dtype], ptr(weight), ptr(cos), ptr(sin), ptr(out),
+         _OUT_DTYPES[out.dtype], b, t_len, g, d, int(transpose_out), float(eps), stream_handle())
+    return out
+
+
+def kv_cache_write(src: torch.Tensor, positions: torch.Tensor, caches: list[torch.Tensor]) -> None:
+    """src [B, T, H, D] (fp32 or bf16) into each bf16 cache [B, S_c, H, D] at positions int64 [T]
+    (TOKEN_MAJOR_KV_CACHE_WRITE_F16_PAIR / _TRIPLE, TOKEN_MAJOR_VALUE_CACHE_WRITE_F32_TO_F16_PAIR / _TRIPLE)."""
+    _check(src, "src", tuple(_OUT_DTYPES), align=4 if src.dtype == torch.bfloat16 else 8)
+    _check(positions, "cache_position", torch.int64, align=8)
+    if src.dim() != 4:
+        raise ValueError(f"src must be [B, T, H, D], got {tuple(src.shape)}")
+    b, t_len, h, d = (int(v) for v in src.shape)
+    if positions.numel() != t_len:
+        raise ValueError(f"cache_position must have {t_len} entries")
+    if not 1 <= len(caches) <= 3:
+        raise ValueError("one to three caches")
+    for i, c in enumerate(caches):
+        _check(c, f"cache_{i}", torch.bfloat16, align=4)
+        if c.dim() != 4 or c.shape[0] != b or c.shape[2] != h or c.shape[3] != d:
+            raise ValueError(f"cache_{i} must be bf16 [{b}, S, {h}, {d}], got {tuple(c.shape)}")
+    arr = (ctypes.c_void_p * len(caches))(*[c.data_ptr() for c in caches])
+    caps = (ctypes.c_uint32 * len(caches))(*[int(c.shape[1]) for c in caches])
+    call("t2h_kv_cache_write", ptr(src), _OUT_DTYPES[src.dtype], ptr(positions), len(caches), ctypes.addressof(arr),
+         ctypes.addressof(caps), b, t_len, h, d, stream_handle())
+
+
+def token_select_chunks(scores: torch.Tensor, tokens: torch.Tensor, chunk_scores: torch.Tensor,
+                        chunk_tokens: torch.Tensor) -> None:
+    """The best (score, token) of each chunk of 1024 partials (QWEN3_TOKEN_SELECT_REDUCE_CHUNKS_F32)."""
+    _check(scores, "scores", torch.float32, align=4)
+    _check(tokens, "tokens", _TOKEN_DTYPES, align=4)
+    _check(chunk_scores, "chunk_scores", torch.float32, align=4)
+    _check(chunk_tokens, "chunk_tokens", _TOKEN_DTYPES, align=4)
+    g = int(scores.numel())
+    if tokens.numel() != g or g == 0:
+        raise ValueError("scores and tokens must have the same non-zero length")
+    c = -(-g // 1024)
+    if chunk_scores.numel() != c or chunk_tokens.numel() != c:
+        raise ValueError(f"{g} partials make {c} chunks")
+    call("t2h_token_select_chunks", ptr(scores), ptr(tokens), g, ptr(chunk_scores), ptr(chunk_tokens),
+         stream_handle())
+
+
+def add(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out = x + y elementwise, fp32 or bf16 (ADD_F32_PREFILL, ADD_F32_36); out may be x or y."""
+    _check(x, "x", tuple(_OUT_DTYPES), align=2)
+    _check(y, "y", x.dtype, align=2)
+    if y.shape != x.shape:
+        raise ValueError("x and y must have the same shape")
+    if out is None:
+        out = torch.empty_like(x)
+    _check(out, "output", x.dtype, align=2)
+    if out.shape != x.shape:
+        raise ValueError("output must have the shape of x")
+    call("t2h_add", ptr(x), ptr(y), ptr(out), _OUT_DTYPES[x.dtype], x.numel(), stream_handle())
+    return out
+
+
+def slice_last_token(x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out [B, 1, H] = x[:, -1] of fp32 x [B, S, H] (SLICE_LAST_TOKEN_F32_TO_F16)."""
+    _check(x, "x", torch.float32, align=4)
+    _check(out, "output", tuple(_OUT_DTYPES), align=2)
+    if x.dim() != 3:
+        raise ValueError(f"x must be [B, S, H], got {tuple(x.shape)}")
+    b, s_len, h = (int(v) for v in x.shape)
+    if tuple(out.shape) != (b, 1, h):
+        raise ValueError(f"output must be [{b}, 1, {h}], got {tuple(out.shape)}")
+    call("t2h_slice_last_token", ptr(x), ptr(out), _OUT_DTYPES[out.dtype], b, s_len, h, stream_handle())
+    return out

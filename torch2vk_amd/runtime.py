@@ -119,9 +119,16 @@ class TensorFieldSpec:
 
 @dataclass(frozen=True)
 class PushConstantInput:
-    """A dynamic scalar passed by name at the call (the reference's PushConstantInput, shader.py:94-99): a Python
-    int or a one-element int32 device tensor, so a captured graph can replay it with new values."""
+    """A dynamic scalar passed by name at the call (the reference's PushConstantInput, shader.py:94-99).  An
+    unsigned input (``kind`` "uint32", the default) is a Python int or a one-element int32 device tensor, so a
+    captured graph can replay it with new values; a "float32" input (ROPE_TABLE_F32's theta) is a Python
+    number."""
     name: str
+    kind: str = "uint32"
+
+    def __post_init__(self) -> None:
+        if self.kind not in ("uint32", "float32"):
+            raise ValueError(f"push input {self.name!r}: kind must be uint32 or float32, got {self.kind!r}")
 
 
 @dataclass(frozen=True)
@@ -223,6 +230,11 @@ class RuntimeSession:
         push: dict[str, object] = {}
         for p in contract.push_inputs:
             v = arguments[p.name]
+            if p.kind == "float32":
+                if isinstance(v, bool) or not isinstance(v, (int, float)):
+                    raise TypeError(f"{variant.name}.{p.name} must be a number, got {type(v).__name__}")
+                push[p.name] = float(v)
+                continue
             if isinstance(v, torch.Tensor):
                 if v.dtype != torch.int32 or v.numel() != 1 or v.device != self.device:
                     raise TypeError(f"{variant.name}.{p.name} must be an int or a one-element int32 device tensor")

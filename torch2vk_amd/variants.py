@@ -280,3 +280,254 @@ def make_sdpa_decode_qk_norm_rope_variant(theta: float, eps: float = kernels.RMS
 
 # Qwen3's RoPE base (config rope_theta 1e6)
 SDPA_DECODE_QK_NORM_ROPE_CACHE_WRITE_F32 = make_sdpa_decode_qk_norm_rope_variant(1.0e6)
+
+
+# ---------------------------------------------------------------- RoPE table, q/k norm + RoPE --
+
+U32 = ("uint32", "int32")  # the reference's uint32 buffers; int32 ones of the same bits are taken too
+
+
+def _rope_table_launch(rt: RuntimeSession, t, sym, push) -> None:
+    kernels.rope_table(t["cos"], t["sin"], push["start_position"], theta=push["theta"])
+
+
+# src/torch2vk/runtime/rope_table.py:32-122: cos / sin of positions start_position + t.  fp32 tables (the
+# reference's are fp16): with them the unfused decode and prefill give the fused kernels' q and k bits.
+ROPE_TABLE_F32 = _variant(
+    "rope_table_f32", "RopeTableF32Program",
+    [_f("cos", IOKind.OUTPUT, F32, ("B", "T", "D")), _f("sin", IOKind.OUTPUT, F32, ("B", "T", "D"))],
+    _rope_table_launch, (PushConstantInput("theta", "float32"), PushConstantInput("start_position")))
+
+
+def _norm_rope_launch(transpose: bool):
+    def launch(rt: RuntimeSession, t, sym, push) -> None:
+        kernels.rms_norm_rope(t["x"], t["weight"], t["cos"], t["sin"], t["output"], transpose_out=transpose)
+    return launch
+
+
+def _norm_rope(name: str, class_name: str, x_dtype, transpose: bool) -> ShaderVariant:
+    out_shape = ("B", "G", "T", "D") if transpose else ("B", "T", "G", "D")
+    return _variant(name, class_name, [
+        _f("x", IOKind.INPUT, x_dtype, ("B", "T", "G", "D")), _f("weight", IOKind.INPUT, F32, ("D",)),
+        _f("cos", IOKind.INPUT, F32, ("B", "T", "D")), _f("sin", IOKind.INPUT, F32, ("B", "T", "D")),
+        _f("output", IOKind.OUTPUT, OUT, out_shape)], _norm_rope_launch(transpose))
+
+
+# src/models/optimized_qwen3/shaders/rms_norm_rope_transpose_f16.py:22-145 (decode q and k, [B, G, T, D] out)
+RMS_NORM_ROPE_TRANSPOSE_F16 = _norm_rope("rms_norm_rope_transpose_f16",
+                                         "OptimizedQwen3RmsNormRopeTransposeF16Program", OUT, True)
+# src/models/optimized_qwen3/shaders/rms_norm_rope_token_f32.py:22-99 (prefill q, token-major out)
+RMS_NORM_ROPE_TOKEN_F32 = _norm_rope("rms_norm_rope_token_f32", "OptimizedQwen3RmsNormRopeTokenF32Program", F32,
+                                     False)
+# src/models/optimized_qwen3/shaders/rms_norm_rope_token_f32_to_f16.py (prefill k, into the cache write)
+RMS_NORM_ROPE_TOKEN_F32_TO_F16 = _norm_rope("rms_norm_rope_token_f32_to_f16",
+                                            "OptimizedQwen3RmsNormRopeTokenF32ToF16Program", F32, False)
+
+
+# ------------------------------------------------------------------ LM head + greedy select --
+
+def _lm_head(name: str, class_name: str, layout: str) -> ShaderVariant:
+    fields = [_f("x", IOKind.INPUT, ACT, (1, 1, "K")), _weight("weight", "N", layout),
+              _f("partial_scores", IOKind.OUTPUT, F32, ("G",)), _f("partial_tokens", IOKind.OUTPUT, U32, ("G",))]
+
+    def launch(rt: RuntimeSession, t, sym, push) -> None:
+        kernels.lm_head_argmax_partial(t["x"].view(-1), _bytes(t["weight"]), _LAYOUT_WTYPE[layout],
+                                       t["partial_scores"], t["partial_tokens"])
+
+    return _variant(name, class_name, fields, launch)
+
+
+# src/torch2vk/export/shaders/lm_head_q6_k_argmax_partial_f16.py:24-209: per partial slot the best (score, row)
+# of the rows it covers, ties to the lower row; logits are never written.  G is any slot count.
+LM_HEAD_Q6_K_ARGMAX_PARTIAL_F16 = _lm_head("lm_head_q6_k_argmax_partial_f16", "LmHeadQ6KArgmaxPartialF16Program",
+                                           Q6_K_HALFWORDS)
+# The same over a Q4_K head (the uniform-int4 configurations; the reference's Q4_K_M policy always makes the
+# head Q6_K, so it has no Q4_K counterpart).
+LM_HEAD_Q4_K_ARGMAX_PARTIAL_F16 = _lm_head("lm_head_q4_k_argmax_partial_f16", "LmHeadQ4KArgmaxPartialF16Program",
+                                           Q4_K_WORDS)
+
+
+def _select_chunks_launch(rt: RuntimeSession, t, sym, push) -> None:
+    kernels.token_select_chunks(t["scores"], t["tokens"], t["chunk_scores"], t["chunk_tokens"])
+
+
+# src/torch2vk/export/shaders/qwen3_token_select_reduce_f32.py:22-120: the best pair of each 1024 partials
+QWEN3_TOKEN_SELECT_REDUCE_CHUNKS_F32 = _variant(
+    "qwen3_token_select_reduce_chunks_f32", "Qwen3TokenSelectReduceChunksF32Program",
+    [_f("scores", IOKind.INPUT, F32, ("G",)), _f("tokens", IOKind.INPUT, U32, ("G",)),
+     _f("chunk_scores", IOKind.OUTPUT, F32, (ceil_div("G", 1024),)),
+     _f("chunk_tokens", IOKind.OUTPUT, U32, (ceil_div("G", 1024),))], _select_chunks_launch)
+
+
+def _select_launch(rt: RuntimeSession, t, sym, push) -> None:
+    kernels.token_select(t["partial_scores"], t["partial_tokens"], t["eos_token_ids"], t["next_token"], t["done"])
+
+
+# src/torch2vk/export/shaders/qwen3_token_select_reduce_f32.py:123-241: the greedy token (ties to the lowest id)
+# and done = it is one of the EOS ids
+QWEN3_TOKEN_SELECT_REDUCE_F32 = _variant(
+    "qwen3_token_select_reduce_f32", "Qwen3TokenSelectReduceF32Program",
+    [_f("partial_scores", IOKind.INPUT, F32, ("G",)), _f("partial_tokens", IOKind.INPUT, U32, ("G",)),
+     _f("eos_token_ids", IOKind.INPUT, "int64", ("E",)), _f("next_token", IOKind.OUTPUT, "int64", (1, 1)),
+     _f("done", IOKind.OUTPUT, U32, (1,))], _select_launch)
+
+
+def _token_store_launch(stop_on_eos: bool):
+    def launch(rt: RuntimeSession, t, sym, push) -> None:
+        idx = push["token_index"]
+        kernels.token_store(t["next_token"], t["done"], t["generated_tokens"].view(-1), t["generated_length"],
+                            t["stopped"], stop_on_eos=stop_on_eos,
+                            token_index=0 if isinstance(idx, torch.Tensor) else int(idx),
+                            token_index_ptr=idx if isinstance(idx, torch.Tensor) else None)
+    return launch
+
+
+def make_qwen3_token_store_variant(name: str, class_name: str, stop_on_eos: bool) -> ShaderVariant:
+    """generated_tokens[token_index] = next_token and generated_length = token_index + 1 unless stopped; with
+    ``stop_on_eos`` a selected EOS (done) also sets stopped (src/torch2vk/export/shaders/qwen3_token_store.py)."""
+    return _variant(name, class_name, [
+        _f("next_token", IOKind.INPUT, "int64", (1, 1)), _f("done", IOKind.INPUT, U32, (1,)),
+        _f("generated_tokens", IOKind.INOUT, "int64", (1, "G")), _f("generated_length", IOKind.INOUT, U32, (1,)),
+        _f("stopped", IOKind.INOUT, U32, (1,))], _token_store_launch(stop_on_eos), (PushConstantInput("token_index"),))
+
+
+# src/torch2vk/export/shaders/qwen3_token_store.py:19 and :124; src/models/optimized_qwen3/shaders/
+# qwen3_token_store_eos_f32.py (stop_on_eos pushed as 1)
+QWEN3_TOKEN_STORE = make_qwen3_token_store_variant("qwen3_token_store", "Qwen3TokenStoreProgram", False)
+QWEN3_TOKEN_STORE_EOS = make_qwen3_token_store_variant("qwen3_token_store_eos", "Qwen3TokenStoreEosProgram", True)
+QWEN3_TOKEN_STORE_EOS_F32 = make_qwen3_token_store_variant("qwen3_token_store_eos_f32",
+                                                           "Qwen3TokenStoreEosF32Program", True)
+
+
+def _embed_q8_launch(rt: RuntimeSession, t, sym, push) -> None:
+    kernels.embedding_q8_0(_bytes(t["weight"]), t["indices"].view(-1), sym["H"], out=t["output"].view(-1, sym["H"]))
+
+
+# src/models/quantized_qwen3_asr/shaders/embedding_q8_0_f32.py:25-97 (the Qwen3-ASR policy's token embedding)
+EMBEDDING_Q8_0_F32 = _variant(
+    "embedding_q8_0_f32", "EmbeddingQ8_0Program",
+    [_weight("weight", "V", Q8_0_HALFWORDS, "H"), _f("indices", IOKind.INPUT, "int64", ("B", "T")),
+     _f("output", IOKind.OUTPUT, F32, ("B", "T", "H"))], _embed_q8_launch)
+
+# src/models/optimized_qwen3/shaders/embedding_q4_k_act_f32.py:21-60 (the prefill chunks' embedding)
+EMBEDDING_Q4_K_ACT_F32 = _variant(
+    "embedding_q4_k_act_f32", "OptimizedQwen3EmbeddingQ4KActF32Program",
+    [_weight("weight", "V", Q4_K_WORDS, "H"), _f("indices", IOKind.INPUT, "int64", ("I0", "I1")),
+     _f("output", IOKind.OUTPUT, F32, ("I0", "I1", "H"))],
+    lambda rt, t, sym, push: kernels.embedding_q4_k(_bytes(t["weight"]), t["indices"].view(-1), sym["H"],
+                                                    out=t["output"].view(-1, sym["H"])))
+
+
+# ------------------------------------------------------------------------- prefill operators --
+
+# src/models/optimized_qwen3/shaders/rms_norm_mul_f32.py:22-40 (fp32 rows in; bf16 out for the GEMMs)
+RMS_NORM_MUL_F32 = _variant(
+    "rms_norm_mul_f32", "OptimizedQwen3RmsNormMulF32Program",
+    [_f("x", IOKind.INPUT, F32, ("B", "T", "H")), _f("weight", IOKind.INPUT, F32, ("H",)),
+     _f("output", IOKind.OUTPUT, OUT, ("B", "T", "H"))], _rms_launch)
+
+
+def _llama_matmul(name: str, class_name: str, layout: str) -> ShaderVariant:
+    """The prefill GEMM of a K-quant weight (src/models/optimized_qwen3/shaders/llama_matmul_q4_k_f32.py:32-141):
+    the _M and _L names are the reference's tile sizes for <= 320 and more tokens; here both run the matrix-core
+    GEMM, which picks its own tiles (and splits K for small grids)."""
+    fields = [_weight("weight", "N", layout), _f("x", IOKind.INPUT, ACT, ("X0", "X1", "K")),
+              _f("output", IOKind.OUTPUT, OUT, ("X0", "X1", "N"))]
+
+    def launch(rt: RuntimeSession, t, sym, push) -> None:
+        kernels.gemm(t["x"], _bytes(t["weight"]), _LAYOUT_WTYPE[layout], out=t["output"])
+
+    return _variant(name, class_name, fields, launch)
+
+
+LLAMA_MATMUL_Q4_K_F32_M = _llama_matmul("llama_matmul_q4_k_f32_m", "LlamaMatmulQ4KF32Program", Q4_K_WORDS)
+LLAMA_MATMUL_Q4_K_F32_L = _llama_matmul("llama_matmul_q4_k_f32_l", "LlamaMatmulQ4KF32Program", Q4_K_WORDS)
+LLAMA_MATMUL_Q6_K_F32_M = _llama_matmul("llama_matmul_q6_k_f32_m", "LlamaMatmulQ6KF32Program", Q6_K_HALFWORDS)
+LLAMA_MATMUL_Q6_K_F32_L = _llama_matmul("llama_matmul_q6_k_f32_l", "LlamaMatmulQ6KF32Program", Q6_K_HALFWORDS)
+
+
+def _add_launch(rt: RuntimeSession, t, sym, push) -> None:
+    kernels.add(t["x"], t["y"], out=t["output"])
+
+
+# src/models/optimized_qwen3/shaders/add_f32_prefill.py:20-60 (the prefill residual adds)
+ADD_F32_PREFILL = _variant(
+    "add_f32_prefill", "AddF32PrefillProgram",
+    [_f("x", IOKind.INPUT, F32, (1, "T", "H")), _f("y", IOKind.INPUT, F32, (1, "T", "H")),
+     _f("output", IOKind.OUTPUT, F32, (1, "T", "H"))], _add_launch)
+# src/models/optimized_qwen3/shaders/add_f32_36.py:22-80 (the last prefill layer's residual add on the last token;
+# the reference adds in fp16, here fp32 or bf16)
+ADD_F32_36 = _variant(
+    "add_f32_36", "ExportAddF32Program",
+    [_f("x", IOKind.INPUT, OUT, (1, "T", "H")), _f("y", IOKind.INPUT, OUT, (1, "T", "H")),
+     _f("output", IOKind.OUTPUT, OUT, (1, "T", "H"))], _add_launch)
+
+# src/models/optimized_qwen3/shaders/slice_last_token_f32_to_f16.py:19-60 (fp32 or bf16 out; the decoder keeps the
+# residual stream in fp32)
+SLICE_LAST_TOKEN_F32_TO_F16 = _variant(
+    "slice_last_token_f32_to_f16", "SliceLastTokenF32ToF16Program",
+    [_f("x", IOKind.INPUT, F32, ("B", "S", "H")), _f("output", IOKind.OUTPUT, OUT, ("B", 1, "H"))],
+    lambda rt, t, sym, push: kernels.slice_last_token(t["x"], t["output"]))
+
+# src/models/optimized_qwen3/shaders/swiglu_f32.py:20-60 (fp32 gate / up; bf16 out, the down GEMM's input)
+SWIGLU_F32 = _variant(
+    "swiglu_f32", "SwigluF32Program",
+    [_f("gate", IOKind.INPUT, F32, ("B", "T", "H")), _f("up", IOKind.INPUT, F32, ("B", "T", "H")),
+     _f("output", IOKind.OUTPUT, ACT, ("B", "T", "H"))], _swiglu_launch)
+
+
+def _kv_write(name: str, class_name: str, src_dtype, n_caches: int) -> ShaderVariant:
+    names = ("cache_a", "cache_b", "cache_c")[:n_caches]
+    fields = [_f(n, IOKind.INOUT, ACT, ("B", f"S{n[-1].upper()}", "H", "D")) for n in names]
+    fields += [_f("cache_position", IOKind.INPUT, "int64", ("T",)),
+               _f("src", IOKind.INPUT, src_dtype, ("B", "T", "H", "D"))]
+
+    def launch(rt: RuntimeSession, t, sym, push) -> None:
+        kernels.kv_cache_write(t["src"], t["cache_position"], [t[n] for n in names])
+
+    return _variant(name, class_name, fields, launch)
+
+
+# src/models/optimized_qwen3/shaders/token_major_kv_cache_write_f16_pair.py:20-103 and the _triple / value forms:
+# rows src[b, t] to cache row cache_position[t] of every cache (bf16 caches; the reference's are fp16)
+TOKEN_MAJOR_KV_CACHE_WRITE_F16_PAIR = _kv_write("token_major_kv_cache_write_f16_pair",
+                                                "OptimizedQwen3TokenMajorKvCacheWriteF16PairProgram", ACT, 2)
+TOKEN_MAJOR_KV_CACHE_WRITE_F16_TRIPLE = _kv_write("token_major_kv_cache_write_f16_triple",
+                                                  "OptimizedQwen3TokenMajorKvCacheWriteF16TripleProgram", ACT, 3)
+TOKEN_MAJOR_VALUE_CACHE_WRITE_F32_TO_F16_PAIR = _kv_write(
+    "token_major_value_cache_write_f32_to_f16_pair", "OptimizedQwen3TokenMajorValueCacheWriteF32ToF16PairProgram",
+    F32, 2)
+TOKEN_MAJOR_VALUE_CACHE_WRITE_F32_TO_F16_TRIPLE = _kv_write(
+    "token_major_value_cache_write_f32_to_f16_triple",
+    "OptimizedQwen3TokenMajorValueCacheWriteF32ToF16TripleProgram", F32, 3)
+
+# tile classes of a [T, S] additive mask: uint8 [1, ceil(T / 128), ceil(S / 64)] (the reference packs them into
+# uint32 [W, R]); 1 all masked, 2 all zero, 0 mixed
+_MASK_OPT = ("uint8", (1, ceil_div("T", kernels.FA_BLOCK_QUERIES), ceil_div("S", kernels.FA_TILE_KEYS)))
+
+
+def _mask_opt_launch(rt: RuntimeSession, t, sym, push) -> None:
+    kernels.fa_mask_tiles(t["mask"].unsqueeze(0), out=t["output"])
+
+
+# src/models/optimized_qwen3/shaders/fa_mask_opt_f16.py:22-60 (fp32 additive mask here; the reference's is fp16)
+FA_MASK_OPT_F16 = _variant(
+    "fa_mask_opt_f16", "OptimizedQwen3FaMaskOptF16Program",
+    [_f("mask", IOKind.INPUT, F32, ("T", "S")), _f("output", IOKind.OUTPUT, *_MASK_OPT)], _mask_opt_launch)
+
+
+def _flash_launch(rt: RuntimeSession, t, sym, push) -> None:
+    kernels.flash_attn_prefill(t["q"], t["k"], t["v"], out=t["output"], causal=False, mask=t["mask"].unsqueeze(0),
+                               mask_tiles=t["mask_opt"])
+
+
+# src/models/optimized_qwen3/shaders/llama_flash_attn_f32_f16_f16.py:35-175: softmax(q k^T / sqrt(D) + mask) v
+# over token-major q [B, T, NH, D] and caches [B, S, NK, D], GQA; mask_opt's all-masked tiles are skipped and
+# all-zero ones not read.  The reference binds q as its "sink" but its mask_n_head_log2 push (NH) leaves sinks off,
+# so the field is checked and not read.
+LLAMA_FLASH_ATTN_F32_F16_F16 = _variant(
+    "llama_flash_attn_f32_f16_f16", "LlamaFlashAttnF32F16F16Program",
+    [_f("q", IOKind.INPUT, ACT, ("B", "T", "NH", "D")), _f("k", IOKind.INPUT, ACT, ("B", "S", "NK", "D")),
+     _f("v", IOKind.INPUT, ACT, ("B", "S", "NK", "D")), _f("mask", IOKind.INPUT, F32, ("T", "S")),
+     _f("sink", IOKind.INPUT, OUT, ("B", "T", "NH", "D")), _f("output", IOKind.OUTPUT, ACT, ("B", "T", "NH", "D")),
+     _f("mask_opt", IOKind.INPUT, *_MASK_OPT)], _flash_launch)
