@@ -172,7 +172,14 @@ def audio_decode_ref(cfg, dense: dict, codes: np.ndarray, round_gemm_inputs=None
     lookups and projections summed, fc2, conv1, per block snake -> conv_transpose1d -> residual units at
     dilations 1/3/9, snake -> conv2.  ``round_gemm_inputs`` (e.g. bf16 rounding) is applied where the GPU
     stages a GEMM's activations.  codes [C, T] -> waveform [T_out]."""
-    import math
+    x = audio_decode_front_ref(cfg, dense, codes, round_gemm_inputs)
+    for i in range(len(cfg.strides)):
+        x = audio_decode_block_ref(cfg, dense, x, i, round_gemm_inputs)
+    return audio_decode_final_ref(dense, x, round_gemm_inputs)
+
+
+def audio_decode_front_ref(cfg, dense: dict, codes: np.ndarray, round_gemm_inputs=None) -> np.ndarray:
+    """Codebook lookups + projections summed, fc2, conv1 (audio_decode.py:66-149): [1, channels, T]."""
     rnd = round_gemm_inputs or (lambda a: a)
     t = codes.shape[1]
     acc = np.zeros((t, cfg.latent))
@@ -180,15 +187,36 @@ def audio_decode_ref(cfg, dense: dict, codes: np.ndarray, round_gemm_inputs=None
         e = dense[f"cb{c}"][codes[c]]
         acc = acc + rnd(e) @ dense[f"proj{c}.w"].T + dense[f"proj{c}.b"]
     h = rnd(acc) @ dense["fc2.w"].T + dense["fc2.b"]                     # [T, hidden]
-    x = conv1d_ref(rnd(h.T[None]), dense["conv1.w"], dense["conv1.b"], 7, 1, 3)   # [1, C, T]
-    ch = cfg.channels
-    for i, s in enumerate(cfg.strides):
-        x = snake_ref(x, dense[f"b{i}.alpha"])
-        x = conv_transpose1d_ref(x, dense[f"b{i}.convt.w"], dense[f"b{i}.convt.b"], 2 * s, s, math.ceil(s / 2), s % 2)
-        for j, d in enumerate((1, 3, 9)):
-            p = f"b{i}.r{j}."
-            r = conv1d_ref(rnd(snake_ref(x, dense[p + "a1"])), dense[p + "c1.w"], dense[p + "c1.b"], 7, 1, 3 * d, d)
-            x = x + conv1d_ref(rnd(snake_ref(r, dense[p + "a2"])), dense[p + "c2.w"], dense[p + "c2.b"], 1)
-        ch //= 2
-    x = snake_ref(x, dense["final.alpha"])
+    return conv1d_ref(rnd(h.T[None]), dense["conv1.w"], dense["conv1.b"], 7, 1, 3)   # [1, C, T]
+
+
+def audio_decode_block_ref(cfg, dense: dict, x: np.ndarray, i: int, round_gemm_inputs=None) -> np.ndarray:
+    """Upsampling block i (audio_decode.py:151-740): snake -> conv_transpose1d -> residual units at dilations
+    1, 3, 9.  x [1, C, T] -> [1, C / 2, T']."""
+    x = audio_decode_upsample_ref(cfg, dense, x, i)
+    for j, d in enumerate((1, 3, 9)):
+        x = audio_decode_unit_ref(dense, x, f"b{i}.r{j}.", d, round_gemm_inputs)
+    return x
+
+
+def audio_decode_upsample_ref(cfg, dense: dict, x: np.ndarray, i: int) -> np.ndarray:
+    """snake -> conv_transpose1d of block i (kernel 2s, stride s, padding ceil(s/2), output padding s % 2)."""
+    import math
+    s = cfg.strides[i]
+    x = snake_ref(np.asarray(x, np.float64), dense[f"b{i}.alpha"])
+    return conv_transpose1d_ref(x, dense[f"b{i}.convt.w"], dense[f"b{i}.convt.b"], 2 * s, s, math.ceil(s / 2), s % 2)
+
+
+def audio_decode_unit_ref(dense: dict, x: np.ndarray, p: str, d: int, round_gemm_inputs=None) -> np.ndarray:
+    """One residual unit: x + conv_k1(snake(conv_k7,dilation d(snake(x))))."""
+    rnd = round_gemm_inputs or (lambda a: a)
+    x = np.asarray(x, np.float64)
+    r = conv1d_ref(rnd(snake_ref(x, dense[p + "a1"])), dense[p + "c1.w"], dense[p + "c1.b"], 7, 1, 3 * d, d)
+    return x + conv1d_ref(rnd(snake_ref(r, dense[p + "a2"])), dense[p + "c2.w"], dense[p + "c2.b"], 1)
+
+
+def audio_decode_final_ref(dense: dict, x: np.ndarray, round_gemm_inputs=None) -> np.ndarray:
+    """snake -> conv2 (audio_decode.py:741-755): the waveform [T_out]."""
+    rnd = round_gemm_inputs or (lambda a: a)
+    x = snake_ref(np.asarray(x, np.float64), dense["final.alpha"])
     return conv1d_ref(rnd(x), dense["conv2.w"], dense["conv2.b"], 7, 1, 3).reshape(-1)

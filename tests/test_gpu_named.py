@@ -237,3 +237,31 @@ def test_named_prefill_and_decode_match_oracle(device, policy, prompt_len, chunk
                                 gpu_logits=decoder_step_logits(dec, prefill_h), label=f"named {policy}")
     print(stats, flush=True)
     assert math.isfinite(stats["min_margin"])
+
+
+def test_exported_whole_prompt_names_match_oracle(device):
+    """The exported path's run_embed_tokens, run_text_layer per layer and the final norm of every position
+    (src/models/quantized_qwen3/export.py:254-315) over a 45-token prompt bound as one chunk, against the CPU
+    oracle's causal pass over all positions (bf16 activations into the GEMMs and attention bound the error)."""
+    from torch2vk_amd.qwen3 import dispatch as D
+    from torch2vk_amd.qwen3.model import Qwen3Decoder
+    from torch2vk_amd.runtime import RuntimeSession
+
+    cfg, w, dense, shape = _model(device, "uniform", 73)
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab, 45).tolist()
+    dec = Qwen3Decoder(w, max_positions=64, max_new_tokens=4, persistent=False)
+    rt = RuntimeSession(device, record=True)
+    D.bind_model_tensors(dec)
+    D.bind_prefill_tensors(torch.tensor(prompt), chunk=len(prompt))
+    D.run_embed_tokens(rt)
+    for i in range(cfg.layers):
+        D.run_text_layer(rt, i, rope_theta=cfg.rope_theta)
+    out = torch.zeros(1, len(prompt), cfg.hidden, device=device)
+    D.run_text_norm_all(rt, out)
+    torch.cuda.synchronize()
+    ref = R.Qwen3CpuModel(shape, dense, max_positions=64).forward(torch.tensor(prompt), 0, all_positions=True).numpy()
+    got = out[0].cpu().numpy()
+    print(f"exported names: max-abs {np.abs(got - ref).max():.3e} of max {np.abs(ref).max():.3e}", flush=True)
+    assert_close(got, ref, max_abs=0.05 * float(np.abs(ref).max()), min_cos=0.999, what="normed hidden")
+    names = [r.shader for r in rt.records]
+    assert names[0] == "embedding_q4_k_act_f32" and names[-1] == "rms_norm_mul_f32"

@@ -115,6 +115,42 @@ def test_cfg_score_ref_closed_forms():
     assert np.isclose(cs[0], guided.max() - np.log(np.exp(guided).sum()), atol=1e-12)
 
 
+def _lowbias32_inverse(x: int) -> int:
+    """The inverse of the lowbias32 integer hash (x ^= x >> 16; x *= 0x7feb352d; x ^= x >> 15;
+    x *= 0x846ca68b; x ^= x >> 16), derived step by step: an odd multiplier is undone by its inverse mod 2^32,
+    and x ^= x >> k by folding the shifted copies back in until they vanish."""
+    def unxorshift(v: int, k: int) -> int:
+        out, shifted = v, v >> k
+        while shifted:
+            out ^= shifted
+            shifted >>= k
+        return out & 0xFFFFFFFF
+    x = unxorshift(x & 0xFFFFFFFF, 16)
+    x = (x * pow(0x846CA68B, -1, 1 << 32)) & 0xFFFFFFFF
+    x = unxorshift(x, 15)
+    x = (x * pow(0x7FEB352D, -1, 1 << 32)) & 0xFFFFFFFF
+    return unxorshift(x, 16)
+
+
+def test_gumbel_hash_is_lowbias32():
+    """The noise hash is the published lowbias32 mixer: composing it with the mixer's inverse is the identity,
+    which a changed multiplier or shift in the oracle breaks; the inverse multipliers are the published ones."""
+    assert pow(0x7FEB352D, -1, 1 << 32) == 0x1D69E2A5 and pow(0x846CA68B, -1, 1 << 32) == 0x43021123
+    rng = np.random.default_rng(0)
+    xs = list(range(4096)) + [int(v) for v in rng.integers(0, 1 << 32, 20000, dtype=np.uint64)] + [0xFFFFFFFF]
+    for x in xs:
+        assert _lowbias32_inverse(O.ov_hash(x)) == x, hex(x)
+    # a planted mistake (one multiplier bit, one shift) is caught by the same composition
+    def wrong(x: int, mult: int, shift: int) -> int:
+        x ^= x >> 16
+        x = (x * mult) & 0xFFFFFFFF
+        x ^= x >> shift
+        x = (x * 0x846CA68B) & 0xFFFFFFFF
+        return x ^ (x >> 16)
+    assert any(_lowbias32_inverse(wrong(x, 0x7FEB352F, 15)) != x for x in range(64))
+    assert any(_lowbias32_inverse(wrong(x, 0x7FEB352D, 14)) != x for x in range(64))
+
+
 def test_gumbel_noise_statistics():
     draws = np.array([O.ov_gumbel(1234, 7, i) for i in range(20000)])
     assert abs(draws.mean() - 0.5772156649) < 0.03          # the Gumbel mean is Euler's constant

@@ -108,8 +108,10 @@ class OmniVoiceAudioDecoder:
         r = kernels.snake(r, w[p + "a2"])
         return kernels.conv1d_q8_0(r, w[p + "c2.w"], w[p + "c2.b"], 1, residual=x)
 
-    def decode(self, codes: torch.Tensor) -> torch.Tensor:
-        """codes int64 [C, T] -> waveform fp32 [out_len(T)]."""
+    def decode(self, codes: torch.Tensor, stages: list | None = None) -> torch.Tensor:
+        """codes int64 [C, T] -> waveform fp32 [out_len(T)].  ``stages``: a list that receives the fp32
+        channels-last activation [T, C] after conv1, after each block's transposed conv and after each of its
+        residual units."""
         cfg, w = self.cfg, self.w
         codes = codes.to(device=self.device, dtype=torch.int64)
         t = int(codes.shape[1])
@@ -122,13 +124,19 @@ class OmniVoiceAudioDecoder:
         h = kernels.q8_0_linear(kernels.im2col_1d(acc.view(1, t, -1), 1), w["fc2.w"], bias=w["fc2.b"],
                                 out_dtype=torch.float32)
         x = kernels.conv1d_q8_0(h.view(1, t, -1), w["conv1.w"], w["conv1.b"], 7, padding=3)
+        if stages is not None:
+            stages.append(x)
         ch = cfg.channels
         for i, s in enumerate(cfg.strides):
             x = kernels.snake(x, w[f"b{i}.alpha"])
             x = kernels.conv_transpose1d_q8_0(x, w[f"b{i}.convt.w"], w[f"b{i}.convt.b"], ch // 2, 2 * s, stride=s,
                                               padding=math.ceil(s / 2), output_padding=s % 2)
+            if stages is not None:
+                stages.append(x)
             for j, d in enumerate(DILATIONS):
                 x = self._unit(x, f"b{i}.r{j}.", d)
+                if stages is not None:
+                    stages.append(x)
             ch //= 2
         x = kernels.snake(x, w["final.alpha"])
         return kernels.conv1d_q8_0(x, w["conv2.w"], w["conv2.b"], 7, padding=3).view(-1)

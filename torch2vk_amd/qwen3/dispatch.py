@@ -627,3 +627,40 @@ def run_prefill(rt: RuntimeSession, *, rope_theta: float) -> int:
     run_lm_head_select(rt, x=m.text_norm.mul_1)
     run_token_store(rt, token_index=0)
     return int(m.next_token.view(-1)[0].item())
+
+
+# ------------------------------------------------------- the exported (un-optimized) prefill names --
+# src/models/quantized_qwen3/export.py:254-315 exports the same modules as three functions over the whole prompt
+# (no chunking): embed_tokens, one decoder layer, the final norm of every position.  Here they run the
+# optimized path's kernels over a prompt bound as one chunk (bind_prefill_tensors(prompt_ids, chunk=len)).
+
+def _whole_prompt() -> PrefillChunk:
+    m = model_tensors()
+    if m.prefill_full is not None:
+        raise RuntimeError("the exported prefill runs the whole prompt as one chunk: bind_prefill_tensors(prompt_ids, "
+                           "chunk=len(prompt_ids))")
+    return _chunk("tail")
+
+
+def run_embed_tokens(rt: RuntimeSession) -> None:
+    """Every prompt token's embedding row (src/models/quantized_qwen3/dispatch/embed_tokens.py:11-16)."""
+    _run_embed_tokens_with_tensors(rt, _whole_prompt().embed)
+
+
+def run_text_layer(rt: RuntimeSession, layer_idx: int, *, rope_theta: float = 1.0e6) -> None:
+    """One decoder layer over the whole prompt at positions 0.. with causal attention
+    (src/models/quantized_qwen3/dispatch/text_layer.py:33-106); the first layer also fills the prompt's RoPE
+    table and mask tiles."""
+    ch = _whole_prompt()
+    if layer_idx == 0:
+        V.ROPE_TABLE_F32(rt, start_position=ch.start, theta=rope_theta, cos=ch.rope.cos, sin=ch.rope.sin)
+        V.FA_MASK_OPT_F16(rt, mask=ch.causal_mask, output=ch.mask_opt)
+    _run_text_layer_with_tensors(rt, ch.layers[layer_idx], ch)
+
+
+def run_text_norm_all(rt: RuntimeSession, output: torch.Tensor) -> None:
+    """The exported run_text_norm (src/models/quantized_qwen3/dispatch/text_norm.py:11-16): the final RMSNorm of
+    every prompt position, fp32 or bf16 [1, T, H] into ``output``."""
+    ch = _whole_prompt()
+    m = model_tensors()
+    V.RMS_NORM_MUL_F32(rt, x=ch.embed.embedding, weight=m.text_norm.p_weight, output=output)
