@@ -686,6 +686,7 @@ def bench_c2(args) -> int:
     dec.stop_on_eos = False
     spg = args.steps_per_graph
     runs = []
+    first_prefill = None
     for r in range(1 + max(1, args.kernel_reps)):   # the first pass warms the graphs and is not counted
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -701,6 +702,8 @@ def bench_c2(args) -> int:
             return 3
         if r:
             runs.append((t1 - t0, t2 - t1))
+        else:
+            first_prefill = t1 - t0  # warm-up launch, capture and first replay of this prompt length
         print(f"[bench] pass {r}: prefill {1e3 * (t1 - t0):.2f} ms, {C2_TOKENS - 1} steps {1e3 * (t2 - t1):.2f} ms",
               file=sys.stderr, flush=True)
     pre = statistics.median(u for u, _ in runs)
@@ -708,6 +711,15 @@ def bench_c2(args) -> int:
     total = pre + steps_s
     tokens = [int(t) for t in dec.generated[:C2_TOKENS].tolist()]
     assert len(tokens) == C2_TOKENS and min(tokens) >= 0
+    # the same prefill eager (no graph): what a prompt of a length not seen before costs after its first call
+    eager = []
+    for _ in range(max(3, args.kernel_reps)):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dec.prefill_chunked(prompt)
+        torch.cuda.synchronize()
+        eager.append(time.perf_counter() - t0)
+    pre_eager = statistics.median(eager)
     kern = kernel_timing(dec, weights, args.kernel_reps)
     dom = kern["dominant"]
     cpu = None
@@ -731,10 +743,14 @@ def bench_c2(args) -> int:
         "data": "synthetic (seeded N(0,0.02) weights quantized on the GPU, "
                 + ("Q4_K uniform int4" if args.policy == "uniform" else "Q4_K_M (Q4_K + Q6_K)") + "; random prompt ids)",
         "config": {"workload": f"qwen3-0.6b-shape greedy decode, batch 1: {C2_PROMPT}-token prompt through the "
-                               f"chunked prefill (one HIP graph), then {C2_TOKENS} tokens (HIP graphs of {spg} steps, "
+                               f"chunked prefill (one HIP graph, captured in the untimed first pass for this prompt "
+                               f"length), then {C2_TOKENS} tokens (HIP graphs of {spg} steps, "
                                + ("persistent layers kernel" if dec.persistent else "one launch per op") + ")",
                    "batch": 1, "prompt": C2_PROMPT, "new_tokens": C2_TOKENS},
         "prefill_ms": round(pre * 1e3, 3),
+        "prefill_first_call_ms": round(first_prefill * 1e3, 3),
+        "prefill_eager_ms": round(pre_eager * 1e3, 3),
+        "value_eager_prefill": round(C2_TOKENS / (pre_eager + steps_s), 2),
         "decode_tok_s": round((C2_TOKENS - 1) / steps_s, 2),
         "roofline": {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(dom["gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
