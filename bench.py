@@ -77,8 +77,9 @@ def profile_kernel_target(per_op: bool, config: str = "decode") -> int:
     """Launch sequence for `rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE`: the dominant kernel of the config twice,
     then one plain 256 MiB device copy whose traffic is known (256 MiB read + 256 MiB written), so counter
     readings can be scaled to bytes.  decode: the persistent layers kernel at KV 4096 (2 dispatches), or per
-    op the gate|up GEMV once per layer (72 dispatches); prefill: the gate|up + SwiGLU GEMM at M 16384 (2
-    dispatches) and causal flash attention over 8 x 2048 tokens (2 dispatches); asr: the 0.6B-shape persistent layers
+    op the gate|up GEMV once per layer (72 dispatches); prefill: the gate|up + SwiGLU GEMM at M 16384 (5
+    times its 2 weight dequantisations then the bf16-weight GEMM; then twice dequantising every tile in the
+    loop) and causal flash attention over 8 x 2048 tokens (2 dispatches); asr: the 0.6B-shape persistent layers
     kernel for 4 sequences at KV 1540 each (2 dispatches)."""
     import torch
 
@@ -96,8 +97,18 @@ def profile_kernel_target(per_op: bool, config: str = "decode") -> int:
         up = kernels.quantize(torch.randn(c.mlp, c.hidden, generator=gen, device=dev) * 0.02, "q8_0")
         x = torch.randn(8 * 2048, c.hidden, generator=gen, device=dev).to(torch.bfloat16)
         act = torch.empty(8 * 2048, c.mlp, dtype=torch.bfloat16, device=dev)
-        for _ in range(2):
+        # the step's form: each weight dequantised once to bf16, then the bf16 tile loop (2 + 1 dispatches;
+        # five times, so that a kernel trace averages over warm launches) ...
+        for _ in range(5):
             kernels.gemm_swiglu(x, gate, up, "q8_0", out=act)
+        # ... and the same GEMM dequantising every tile in its loop
+        saved = kernels.DEQUANT_FIRST_ROWS
+        kernels.DEQUANT_FIRST_ROWS = 0
+        try:
+            for _ in range(2):
+                kernels.gemm_swiglu(x, gate, up, "q8_0", out=act)
+        finally:
+            kernels.DEQUANT_FIRST_ROWS = saved
         # and causal flash attention over the same 8 x 2048 tokens (32 q heads over 8 kv heads, D 128)
         q = torch.randn(8, 2048, c.heads, c.head_dim, generator=gen, device=dev).to(torch.bfloat16)
         k = torch.randn(8, 2048, c.kv_heads, c.head_dim, generator=gen, device=dev).to(torch.bfloat16)
@@ -186,21 +197,31 @@ def phase_trace(args) -> int:
         return 3
     us_launch = float(np.median([u for u, _ in launches]))
     names = kernels.DECODE_TRACE_PHASES
-    n_blocks = [256, 256, cfg.heads, 256, 256, 256]
+    # the blocks that ran each phase: those that stamped its input in hand (the buffer starts zeroed; the
+    # merge runs on as many blocks as there are q heads and not at all up to 256 positions, where the
+    # attention runs on one block per kv head)
+    ran = launches[-1][1][:, :, :, 1] != 0                       # [layers, phases, blocks]
+    n_blocks = [int(ran[2, ph].sum()) for ph in range(6)]
     rows = []   # [layer, phase] -> begin, ready_med, ready_max, end_med, end_max, polls, first_med (us from prev end)
     periods = []
     for _, tr in launches[1:]:
         t = tr[..., :4].astype(np.float64) * 0.01     # 100 MHz -> us
         lo, hi = 2, cfg.layers - 1
-        periods.append((t[hi - 1, 5, :, 3].max() - t[lo - 1, 5, :, 3].max()) / (hi - lo))
+        down = ran[2, 5]
+        periods.append((t[hi - 1, 5, down, 3].max() - t[lo - 1, 5, down, 3].max()) / (hi - lo))
         for layer in range(lo, hi):
-            prev = t[layer - 1, 5, :, 3].max()
+            prev = t[layer - 1, 5, down, 3].max()
             r = []
             for ph in range(6):
-                e = t[layer, ph, :n_blocks[ph]]
+                sel = ran[layer, ph]
+                if not sel.any():
+                    r.append([np.nan] * 7)
+                    continue
+                e = t[layer, ph, sel]
                 r.append([np.median(e[:, 0]) - prev, np.median(e[:, 1]) - prev, e[:, 1].max() - prev,
                           np.median(e[:, 3]) - prev, e[:, 3].max() - prev,
-                          float(tr[layer, ph, :n_blocks[ph], 4].mean()), np.median(e[:, 2]) - prev])
+                          float(tr[layer, ph, sel, 4].mean()),
+                          np.median(e[e[:, 2] > 0, 2]) - prev if (e[:, 2] > 0).any() else np.nan])
                 prev = e[:, 3].max()
             rows.append(r)
     m = np.mean(np.array(rows), axis=0)
@@ -213,12 +234,12 @@ def phase_trace(args) -> int:
               f"{pl:.1f} |")
     crit = m[:, 4]
     print(f"\nlaunch {us_launch:.1f} us ({cfg.layers} layers, KV position {args.positions}); layer period "
-          f"{period:.2f} us; sum of phase critical-path steps {crit.sum():.2f} us")
+          f"{period:.2f} us; sum of phase critical-path steps {np.nansum(crit):.2f} us")
     att = []
     for _, tr in launches[1:]:
         t = tr.astype(np.float64) * 0.01
         for layer in range(2, cfg.layers - 1):
-            e = t[layer, 1]
+            e = t[layer, 1, ran[layer, 1]]
             att.append([np.median(e[:, k] - e[:, 1]) for k in (5, 2, 6, 7, 3)])
     a5 = np.mean(np.array(att), axis=0)
     print(f"\nattention, median block, from input in hand: scores {a5[0]:.2f}, softmax {a5[1]:.2f}, P.V {a5[2]:.2f}, "
@@ -922,12 +943,31 @@ def bench_prefill(args) -> int:
           file=sys.stderr, flush=True)
 
     # dominant kernel of the step: gate|up + SwiGLU in one GEMM (M 16384, K 4096, 2 x 12288 rows), HIP events
-    # on its stream; the standalone up-projection GEMM the config names is timed beside it
-    gu_us = _events_us(lambda: kernels.gemm_swiglu(x, layers[0]["gate"], layers[0]["up"], "q8_0", out=act),
-                       args.kernel_reps * 4)
+    # on its stream.  At these M the step dequantises each Q8_0 weight once to bf16 (kernels.DEQUANT_FIRST_ROWS)
+    # and runs the tile loop on bf16 rows: the GEMM launch alone is the roofline kernel, the dequantisations
+    # are timed beside it, and so is the same GEMM dequantising every tile in the loop (the split of the two).
+    # The standalone up-projection GEMM the config names is timed the same ways.
+    reps = args.kernel_reps * 4
+    gate_b = kernels.dequantize_bf16(layers[0]["gate"], "q8_0", c.hidden)
+    up_b = kernels.dequantize_bf16(layers[0]["up"], "q8_0", c.hidden)
+    deq_us = _events_us(lambda: kernels.dequantize_bf16(layers[0]["up"], "q8_0", c.hidden, out=up_b), reps)
+    gu_us = _events_us(lambda: kernels.gemm_swiglu(x, gate_b, up_b, "bf16", out=act), reps)
     gu_tflops = 2.0 * m * c.hidden * 2 * c.mlp / (gu_us * 1e-6) / 1e12
-    gemm_us = _events_us(lambda: kernels.gemm(x, layers[0]["up"], "q8_0", out=up), args.kernel_reps * 4)
-    gemm_tflops = 2.0 * m * c.hidden * c.mlp / (gemm_us * 1e-6) / 1e12
+    gu_step_us = _events_us(lambda: kernels.gemm_swiglu(x, layers[0]["gate"], layers[0]["up"], "q8_0", out=act),
+                            reps)
+    gemm_us = _events_us(lambda: kernels.gemm(x, up_b, "bf16", out=up), reps)
+    gemm_step_us = _events_us(lambda: kernels.gemm(x, layers[0]["up"], "q8_0", out=up), reps)
+    saved = kernels.DEQUANT_FIRST_ROWS
+    kernels.DEQUANT_FIRST_ROWS = 0
+    try:
+        gu_tile_us = _events_us(lambda: kernels.gemm_swiglu(x, layers[0]["gate"], layers[0]["up"], "q8_0", out=act),
+                                reps)
+        gemm_tile_us = _events_us(lambda: kernels.gemm(x, layers[0]["up"], "q8_0", out=up), reps)
+    finally:
+        kernels.DEQUANT_FIRST_ROWS = saved
+    del gate_b, up_b
+    up_flop = 2.0 * m * c.hidden * c.mlp
+    gemm_tflops = up_flop / (gemm_step_us * 1e-6) / 1e12
     fa_us = _events_us(lambda: kernels.flash_attn_prefill(qb.view(nb, tl, c.heads, c.head_dim), kc, vc, out=attn,
                                                           causal=True), args.kernel_reps * 4)
     fa_tflops = 4.0 * c.heads * c.head_dim * (tl * (tl + 1) / 2) * nb / (fa_us * 1e-6) / 1e12
@@ -948,15 +988,17 @@ def bench_prefill(args) -> int:
         "config": {
             "workload": "Qwen3-8B-shape prefill of 8 sequences x 2048 tokens: Q8_0 embedding, 36 layers (RMSNorm, "
                         "q|k|v GEMM, q/k norm + RoPE + KV write, causal flash attention, o GEMM + residual, "
-                        "RMSNorm, gate|up GEMM with SwiGLU in its epilogue, down GEMM + residual), final norm + Q4_K LM head + "
-                        "greedy select of each sequence's first token",
+                        "RMSNorm, gate|up GEMM with SwiGLU in its epilogue, down GEMM + residual; every GEMM "
+                        "dequantises its Q8_0 weight to a bf16 scratch inside the step, then runs the bf16 tile "
+                        "loop), final norm + Q4_K LM head + greedy select of each sequence's first token",
             "batch": nb, "seq_len": tl, "weights": "q8_0",
         },
         "mfma_utilisation": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         "achieved_tflops": round(tflops, 1),
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_q_kernel<GemmQ80, SwiGLU epilogue> (gate|up, M 16384 K 4096 N 2 x 12288)",
+            "kernel": "gemm_q_kernel<GemmBF16, SwiGLU epilogue> (gate|up over the Q8_0 weights dequantised to "
+                      "bf16 once, M 16384 K 4096 N 2 x 12288)",
             "achieved": round(gu_tflops, 1),
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
@@ -965,8 +1007,15 @@ def bench_prefill(args) -> int:
             "traffic_source": TRAFFIC_PROFILES["prefill_gate_up_gemm"].name,
             "avg_launch_us": round(gu_us, 1),
         },
-        "up_projection_gemm": {"kernel": "gemm_q_kernel<GemmQ80> (M 16384 K 4096 N 12288)",
-                               "avg_launch_us": round(gemm_us, 1), "tflops": round(gemm_tflops, 1)},
+        "gate_up": {"with_dequant_us": round(gu_step_us, 1), "dequant_us_per_matrix": round(deq_us, 1),
+                    "in_loop_dequant_us": round(gu_tile_us, 1),
+                    "note": "with_dequant: the step's call (2 dequantisations + the bf16 GEMM); in_loop_dequant: "
+                            "gemm_q_kernel<GemmQ80> dequantising every tile"},
+        "up_projection_gemm": {"kernel": "t2h_dequantize_bf16 + gemm_q_kernel<GemmBF16> (M 16384 K 4096 N 12288, "
+                                         "fp32 out)",
+                               "avg_launch_us": round(gemm_step_us, 1), "tflops": round(gemm_tflops, 1),
+                               "gemm_alone_us": round(gemm_us, 1), "in_loop_dequant_us": round(gemm_tile_us, 1),
+                               "in_loop_dequant_tflops": round(up_flop / (gemm_tile_us * 1e-6) / 1e12, 1)},
         "flash_attention": {"avg_launch_us": round(fa_us, 1), "tflops": round(fa_tflops, 1)},
         "cpu_baseline": cpu,
     }

@@ -42,7 +42,8 @@ enum {
 };
 
 enum { T2H_DTYPE_F32 = 0, T2H_DTYPE_BF16 = 1 };
-enum { T2H_WTYPE_Q4_K = 12, T2H_WTYPE_Q6_K = 14, T2H_WTYPE_Q8_0 = 8 }; /* GGUF type ids, gguf.py:19-53 */
+enum { T2H_WTYPE_Q4_K = 12, T2H_WTYPE_Q6_K = 14, T2H_WTYPE_Q8_0 = 8, T2H_WTYPE_BF16 = 30 }; /* GGUF type ids,
+                                                                                          gguf.py:19-53 */
 
 int t2h_abi_version(void);
 const char* t2h_status_string(int status);
@@ -157,8 +158,8 @@ int t2h_q4k_gemm(const void* x, const void* w, void* y, int out_dtype, const flo
                  uint32_t k, uint32_t n, void* stream);
 /* y bf16 [m, n_ff] = silu(x . deq(W_gate)^T) * (x . deq(W_up)^T): the prefill MLP's gate and up GEMMs and
  * the SwiGLU in one launch (each wave's tile columns pair 32 gate rows with the 32 up rows of the same
- * features).  wtype T2H_WTYPE_Q8_0 / Q4_K / Q6_K, both weights [n_ff, k]; k % 64 == 0 (% 256 for the K
- * types).  replaces LLAMA_MATMUL_Q4_K_F32_{M,L} x 2 + SWIGLU_F32 (src/models/optimized_qwen3/dispatch/
+ * features).  wtype T2H_WTYPE_Q8_0 / Q4_K / Q6_K / BF16, both weights [n_ff, k]; k % 64 == 0 (% 256 for the
+ * K types).  replaces LLAMA_MATMUL_Q4_K_F32_{M,L} x 2 + SWIGLU_F32 (src/models/optimized_qwen3/dispatch/
  * text_layer.py; src/models/optimized_qwen3/shaders/swiglu_f32.py). */
 int t2h_gemm_swiglu(int wtype, const void* x, const void* w_gate, const void* w_up, void* y, uint32_t m, uint32_t k,
                     uint32_t n_ff, void* stream);
@@ -167,7 +168,7 @@ int t2h_gemm_swiglu(int wtype, const void* x, const void* w_gate, const void* w_
  * part's fp32 products go to partials (t2h_gemm_splitk_bytes(m, n, splits, swiglu) bytes, 16-B aligned),
  * then a second kernel sums the parts in order and applies the epilogue: bias,
  * act, and fp32 (+ residual, which may alias y) or bf16 output.  w_up non-null selects the SwiGLU form (w the
- * gate rows, n = n_ff features, y bf16 [m, n_ff]; no bias, act or residual).  wtype Q8_0 / Q4_K / Q6_K;
+ * gate rows, n = n_ff features, y bf16 [m, n_ff]; no bias, act or residual).  wtype Q8_0 / Q4_K / Q6_K / BF16;
  * w_k as t2h_q8_0_linear (= k for the K types and for SwiGLU); 1 <= splits <= min(k / 64, 64).  The results
  * equal the one-pass GEMM's up to the order of the fp32 sum.  No counterpart of its own in the reference: it
  * is the same LINEAR_NOBIAS_*_F32 / LLAMA_MATMUL_*_F32 products (see the entries above), scheduled for small
@@ -176,6 +177,19 @@ size_t t2h_gemm_splitk_bytes(uint32_t m, uint32_t n, uint32_t splits, int swiglu
 int t2h_gemm_splitk(int wtype, const void* x, const void* w, const void* w_up, const float* bias, int act, void* y,
                     int out_dtype, const float* residual, uint32_t m, uint32_t k, uint32_t n, uint32_t w_k,
                     uint32_t splits, void* partials, size_t partials_bytes, void* stream);
+/* The same GEMM over bf16 weight rows (GGUF BF16, 16-byte aligned): the tiles are copied into LDS instead of
+ * dequantised.  Any m and n; k % 64 == 0.  replaces LINEAR_NOBIAS_BF16W_F32
+ * (src/models/exported_qwen3_asr/shaders/linear_nobias_bf16w_f32.py, whose activations are fp16 where these are
+ * bf16), and runs the prefill GEMMs over weights dequantised once by t2h_dequantize_bf16. */
+int t2h_bf16_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
+                  uint32_t k, uint32_t n, void* stream);
+/* out bf16 [rows, k] (16-byte aligned) = the bf16 values the GEMMs above dequantise W's rows to in LDS (wtype
+ * Q8_0 / Q4_K / Q6_K; k % 64 == 0, % 256 for the K types), so that t2h_bf16_gemm / t2h_gemm_swiglu(BF16) over
+ * out give bit-identical results to the quantized GEMM on W.  For large prefills, where the quantized GEMM
+ * would dequantise every weight tile once per 256 rows of x: dequantised once here, each tile is only copied.
+ * No reference counterpart (the reference dequantises inside every GEMM workgroup,
+ * src/models/quantized_qwen3/shaders/linear_nobias_q8_0_f32.py:24-209). */
+int t2h_dequantize_bf16(int wtype, const void* w, uint32_t rows, uint32_t k, void* out, void* stream);
 /* replaces LLAMA_MATMUL_Q6_K_F32_{M,L} (src/models/optimized_qwen3/shaders/llama_matmul_q6_k_f32.py:27-141):
  * the Q6_K v/down weights of the Q4_K_M more-bits layers; k % 256 == 0, W 2-byte aligned. */
 int t2h_q6k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,

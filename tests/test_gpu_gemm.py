@@ -148,3 +148,82 @@ def test_gemm_splitk_rejects_bad_arguments(device):
     assert lib.t2h_gemm_splitk(*args(0, need)) == 5
     assert lib.t2h_gemm_splitk(*args(2, need)) == 0
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("wtype,m,k,n", [("q8_0", 300, 1024, 520), ("q8_0", 1024, 4096, 768), ("q4_k", 300, 1024, 520),
+                                         ("q4_k", 17, 2048, 1024), ("q6_k", 700, 3072, 384)])
+def test_dequantize_bf16_gemm_equals_quantized_gemm(device, wtype, m, k, n):
+    """Weights dequantised once (t2h_dequantize_bf16) hold the very bf16 values the quantized GEMM builds in its
+    LDS tiles: the bf16-weight GEMM (t2h_bf16_gemm, and the SwiGLU form) over them is bit-identical to the
+    quantized GEMM, one pass and split-K; and the dequantised rows are the oracle's dequantisation rounded to
+    bf16 (bit-equal for Q8_0, whose fp32 values d * q are exact; within one bf16 step for the K types, whose
+    fp32 products may round before the bf16 rounding in a different order)."""
+    from torch2vk_amd import kernels
+
+    rng, packed, wd, x = _problem(wtype, m, k, n, 31)
+    w = torch.from_numpy(packed).to(device)
+    wb = kernels.dequantize_bf16(w, wtype, k)
+    ref_b = torch.from_numpy(wd).to(torch.bfloat16)
+    if wtype == "q8_0":
+        assert torch.equal(wb.cpu().view(torch.int16), ref_b.view(torch.int16))
+    else:
+        diff = (wb.cpu().float() - ref_b.float()).abs()
+        assert (diff <= 2 ** -7 * ref_b.float().abs()).all()
+    xt = torch.from_numpy(x).to(device).to(torch.bfloat16)
+    for splits in (1, None):
+        yq = kernels.gemm(xt, w, wtype, out_dtype=torch.float32, splits=splits)
+        yb = kernels.gemm(xt, wb, "bf16", out_dtype=torch.float32, splits=splits)
+        torch.testing.assert_close(yb, yq, rtol=0, atol=0)
+    n_ff = n // 2
+    g, u = w[:n_ff].contiguous(), w[n_ff:2 * n_ff].contiguous()
+    gb, ub = wb[:n_ff].contiguous(), wb[n_ff:2 * n_ff].contiguous()
+    for splits in (1, None):
+        aq = kernels.gemm_swiglu(xt, g, u, wtype, splits=splits)
+        ab = kernels.gemm_swiglu(xt, gb, ub, "bf16", splits=splits)
+        torch.testing.assert_close(ab, aq, rtol=0, atol=0)
+
+
+def test_bf16_gemm_matches_fp32_reference(device):
+    """bf16 weights straight from a model (no quantization), ragged M, N and the K tail of a 64-wide stage
+    boundary: against the fp32 product of the same bf16 operands."""
+    from torch2vk_amd import kernels
+
+    g = torch.Generator(device=device)
+    g.manual_seed(5)
+    m, k, n = 333, 1088, 700
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g, device=device) * 0.05).to(torch.bfloat16)
+    y = kernels.gemm(x, w, "bf16", out_dtype=torch.float32, splits=1)
+    ref = x.float() @ w.float().t()
+    err = (y - ref).abs().max().item()
+    assert err <= 1e-4 * ref.abs().max().item(), err
+
+
+@pytest.mark.parametrize("wtype,m,k,n", [("q8_0", 4000, 256, 16384), ("q4_k", 4096, 512, 16200)])
+def test_bf16_gemm_large_grid_equals_quantized_gemm(device, wtype, m, k, n):
+    """The prefill's grid size (>= 1024 tiles of 256 x 256, the 256-row tile loop), ragged M (4000) and N
+    (16200): bf16 weights dequantised once give the quantized GEMM's bits in the plain, bf16, residual and SwiGLU
+    epilogues."""
+    from torch2vk_amd import kernels
+
+    g = torch.Generator(device=device)
+    g.manual_seed(9)
+    w = kernels.quantize(torch.randn(n, k, generator=g, device=device) * 0.02, wtype)
+    wb = kernels.dequantize_bf16(w, wtype, k)
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    yq = kernels.gemm(x, w, wtype, out_dtype=torch.float32, splits=1)
+    yb = kernels.gemm(x, wb, "bf16", out_dtype=torch.float32, splits=1)
+    torch.testing.assert_close(yb, yq, rtol=0, atol=0)
+    yq16 = kernels.gemm(x, w, wtype, out_dtype=torch.bfloat16, splits=1)
+    yb16 = kernels.gemm(x, wb, "bf16", out_dtype=torch.bfloat16, splits=1)
+    torch.testing.assert_close(yb16, yq16, rtol=0, atol=0)
+    r = torch.randn(m, n, generator=g, device=device)
+    rq, rb = r.clone(), r.clone()
+    kernels.gemm(x, w, wtype, out=rq, residual=rq, splits=1)
+    kernels.gemm(x, wb, "bf16", out=rb, residual=rb, splits=1)
+    torch.testing.assert_close(rb, rq, rtol=0, atol=0)
+    del yq, yb, yq16, yb16, r, rq, rb
+    n_ff = n // 2
+    aq = kernels.gemm_swiglu(x, w[:n_ff].contiguous(), w[n_ff:2 * n_ff].contiguous(), wtype, splits=1)
+    ab = kernels.gemm_swiglu(x, wb[:n_ff].contiguous(), wb[n_ff:2 * n_ff].contiguous(), "bf16", splits=1)
+    torch.testing.assert_close(ab, aq, rtol=0, atol=0)

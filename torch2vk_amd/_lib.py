@@ -23,6 +23,7 @@ T2H_DTYPE_BF16 = 1
 T2H_WTYPE_Q4_K = 12
 T2H_WTYPE_Q6_K = 14
 T2H_WTYPE_Q8_0 = 8
+T2H_WTYPE_BF16 = 30
 
 _vp = ctypes.c_void_p
 _u32 = ctypes.c_uint32
@@ -91,6 +92,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "t2h_index_copy_rows": (_i32, [_vp, _u64, _u32, _vp, _u32, _vp, _vp]),
     "t2h_embedding_q8_0": (_i32, [_vp, _u64, _vp, _u32, _u32, _vp, _vp]),
     "t2h_q6k_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp]),
+    "t2h_bf16_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp]),
+    "t2h_dequantize_bf16": (_i32, [_i32, _vp, _u32, _u32, _vp, _vp]),
     "t2h_gemm_swiglu": (_i32, [_i32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "t2h_gemm_splitk_bytes": (_sz, [_u32, _u32, _u32, _i32]),
     "t2h_gemm_splitk": (_i32, [_i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _sz,

@@ -258,6 +258,37 @@ struct GemmQ6K {
     }
 };
 
+// bf16 rows (GGUF BF16): no dequantisation, the stage's 64 values of a row copied as they are; thread t
+// copies half (t & 1) of row t >> 1.  Weights a prefill pass dequantised once (t2h_dequantize_bf16), or a
+// model kept in bf16.
+struct GemmBF16 {
+    static constexpr int BLOCK_VALUES = 64;
+    static constexpr int BLOCK_BYTES = 128;
+    static constexpr int ALIGN = 16;
+    static constexpr int STORE_STEP = 0, STORE_STEP_256 = 0;
+    struct Raw {
+        uint4 v[4];
+        bool inside;  // false: a stage past the row's end, stored as zeros
+    };
+    template <bool GATED>
+    __device__ static __forceinline__ void load(const GemmArgs& a, uint32_t n0, uint32_t k0, Raw& r) {
+        const uint32_t t = threadIdx.x;
+        const uint32_t blk = k0 / 64;
+        r.inside = blk < a.w_blocks;
+        const uint8_t* p = gemm_w_row<GATED>(a, n0, t >> 1) + (size_t)(r.inside ? blk : a.w_blocks - 1) * 128 +
+                           (t & 1) * 64;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.v[i] = load_u4(p + 16 * i);
+    }
+    __device__ static __forceinline__ void store(const Raw& r, uint16_t* lds_b) {
+        const uint32_t t = threadIdx.x;
+        uint16_t* dst = lds_b + (t >> 1) * GQ_LDS_ROW + (t & 1) * 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<uint4*>(dst + 8 * i) = r.inside ? r.v[i] : make_uint4(0u, 0u, 0u, 0u);
+    }
+};
+
 template <class F>
 __device__ __forceinline__ void store_w(const typename F::Raw& r, uint16_t* lds_b, uint32_t k0) {
     if constexpr (F::BLOCK_VALUES == 256) {
@@ -267,7 +298,61 @@ __device__ __forceinline__ void store_w(const typename F::Raw& r, uint16_t* lds_
     }
 }
 
+// ------------------------------------------------------ dequantise once ----
+
+// out[rows, k] bf16 = the values gemm_q_kernel dequantises into its LDS tiles: the same load and store code
+// into the same padded LDS rows, then copied out, so a GEMM over `out` (GemmBF16) multiplies bit-identical
+// operands.  Block (row tile r0 = 256 blockIdx.x, stage blockIdx.y).
+template <class F>
+__global__ __launch_bounds__(GQ_THREADS) void gemm_dequant_bf16_kernel(const GemmArgs a, uint16_t* __restrict__ out) {
+    __shared__ __align__(16) uint16_t lds_b[GQ_BN * GQ_LDS_ROW];
+    const uint32_t n0 = blockIdx.x * GQ_BN, k0 = blockIdx.y * GQ_BK;
+    typename F::Raw rw;
+    F::template load<false>(a, n0, k0, rw);
+    store_w<F>(rw, lds_b, k0);
+    __syncthreads();
+    const uint32_t t = threadIdx.x;
+    const uint32_t row = n0 + (t >> 1);
+    if (row >= a.n) return;
+    const uint16_t* src = lds_b + (t >> 1) * GQ_LDS_ROW + (t & 1) * 32;
+    uint16_t* dst = out + (size_t)row * a.k + k0 + (t & 1) * 32;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(dst + 8 * i) = *reinterpret_cast<const uint4*>(src + 8 * i);
+}
+
+template <class F>
+static int gemm_dequant_launch(const void* w, uint32_t rows, uint32_t k, void* out, void* stream) {
+    if (!w || !out) return T2H_ERR_NULL;
+    if (k == 0 || k % GQ_BK != 0 || k % F::BLOCK_VALUES != 0) return T2H_ERR_SHAPE;
+    if ((reinterpret_cast<uintptr_t>(w) & (F::ALIGN - 1)) != 0) return T2H_ERR_ALIGN;
+    if ((reinterpret_cast<uintptr_t>(out) & 15) != 0) return T2H_ERR_ALIGN;
+    if (rows == 0) return T2H_OK;
+    GemmArgs a = {};
+    a.w = reinterpret_cast<const uint8_t*>(w);
+    a.n = rows;
+    a.k = k;
+    a.w_blocks = k / F::BLOCK_VALUES;
+    a.row_bytes = a.w_blocks * F::BLOCK_BYTES;
+    hipLaunchKernelGGL(gemm_dequant_bf16_kernel<F>, dim3((rows + GQ_BN - 1) / GQ_BN, k / GQ_BK), dim3(GQ_THREADS), 0,
+                       reinterpret_cast<hipStream_t>(stream), a, reinterpret_cast<uint16_t*>(out));
+    T2H_LAUNCH_CHECK();
+    return T2H_OK;
+}
+
 // ---------------------------------------------------------------- kernel --
+
+// The block's tile: XCD-contiguous runs of blockIdx (blocks are dealt to the 8 XCDs round-robin), then groups
+// of GQ_GROUP_M tiles down M.
+__device__ __forceinline__ void gemm_tile_of(const GemmArgs& a, uint32_t& tile_m, uint32_t& tile_n) {
+    const uint32_t total = a.tiles_m * a.tiles_n;
+    uint32_t pid = blockIdx.x;
+    if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;
+    const uint32_t per_group = GQ_GROUP_M * a.tiles_n;
+    const uint32_t first_m = (pid / per_group) * GQ_GROUP_M;
+    const uint32_t gsize = min(a.tiles_m - first_m, (uint32_t)GQ_GROUP_M);
+    tile_m = first_m + (pid % per_group) % gsize;
+    tile_n = (pid % per_group) / gsize;
+}
 
 // MI = 32-row MFMA tiles per wave down M: 4 gives 256 x 256 block tiles, 2
 // gives 128 x 256 for problems with few 256-row tiles.
@@ -278,15 +363,8 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
     __shared__ __align__(16) uint16_t lds_a[2][GQ_BM * GQ_LDS_ROW];
     __shared__ __align__(16) uint16_t lds_b[2][GQ_BN * GQ_LDS_ROW];
 
-    // tile index: XCD-contiguous runs, then groups of GQ_GROUP_M tiles down M
-    const uint32_t total = a.tiles_m * a.tiles_n;
-    uint32_t pid = blockIdx.x;
-    if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;
-    const uint32_t per_group = GQ_GROUP_M * a.tiles_n;
-    const uint32_t first_m = (pid / per_group) * GQ_GROUP_M;
-    const uint32_t gsize = min(a.tiles_m - first_m, (uint32_t)GQ_GROUP_M);
-    const uint32_t tile_m = first_m + (pid % per_group) % gsize;
-    const uint32_t tile_n = (pid % per_group) / gsize;
+    uint32_t tile_m, tile_n;
+    gemm_tile_of(a, tile_m, tile_n);
     const uint32_t m0 = tile_m * GQ_BM, n0 = tile_n * GQ_BN;
 
     const uint32_t t = threadIdx.x;
@@ -646,6 +724,20 @@ extern "C" int t2h_q8_0_linear(const void* x, const void* w, const float* bias, 
     return gemm_q_launch<GemmQ80>(x, w, bias, act, y, out_dtype, residual, m, k, n, w_k, stream);
 }
 
+extern "C" int t2h_bf16_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual,
+                             uint32_t m, uint32_t k, uint32_t n, void* stream) {
+    return gemm_q_launch<GemmBF16>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
+}
+
+extern "C" int t2h_dequantize_bf16(int wtype, const void* w, uint32_t rows, uint32_t k, void* out, void* stream) {
+    switch (wtype) {
+        case T2H_WTYPE_Q8_0: return gemm_dequant_launch<GemmQ80>(w, rows, k, out, stream);
+        case T2H_WTYPE_Q4_K: return gemm_dequant_launch<GemmQ4K>(w, rows, k, out, stream);
+        case T2H_WTYPE_Q6_K: return gemm_dequant_launch<GemmQ6K>(w, rows, k, out, stream);
+        default: return T2H_ERR_DTYPE;
+    }
+}
+
 extern "C" int t2h_q6k_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
                             uint32_t k, uint32_t n, void* stream) {
     return gemm_q_launch<GemmQ6K>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
@@ -697,6 +789,9 @@ extern "C" int t2h_gemm_splitk(int wtype, const void* x, const void* w, const vo
         case T2H_WTYPE_Q6_K:
             return gemm_splitk_launch<GemmQ6K>(x, w, w_up, bias, act, y, out_dtype, residual, m, k, n, w_k, splits,
                                                partials, partials_bytes, stream);
+        case T2H_WTYPE_BF16:
+            return gemm_splitk_launch<GemmBF16>(x, w, w_up, bias, act, y, out_dtype, residual, m, k, n, w_k, splits,
+                                                partials, partials_bytes, stream);
         default: return T2H_ERR_DTYPE;
     }
 }
@@ -707,6 +802,7 @@ extern "C" int t2h_gemm_swiglu(int wtype, const void* x, const void* w_gate, con
         case T2H_WTYPE_Q8_0: return gemm_swiglu_launch<GemmQ80>(x, w_gate, w_up, y, m, k, n_ff, stream);
         case T2H_WTYPE_Q4_K: return gemm_swiglu_launch<GemmQ4K>(x, w_gate, w_up, y, m, k, n_ff, stream);
         case T2H_WTYPE_Q6_K: return gemm_swiglu_launch<GemmQ6K>(x, w_gate, w_up, y, m, k, n_ff, stream);
+        case T2H_WTYPE_BF16: return gemm_swiglu_launch<GemmBF16>(x, w_gate, w_up, y, m, k, n_ff, stream);
         default: return T2H_ERR_DTYPE;
     }
 }
