@@ -33,9 +33,12 @@
 //   * O^T += V^T . P^T: the accumulator registers of S^T, scaled, exponentiated
 //     and packed to bf16, are already the B operand of the second product when
 //     its 16 k-slots are assigned to the keys each lane holds; the A operand
-//     reads V^T from LDS with the same key order.  V is transposed on its way
-//     into LDS: each thread loads a 4 keys x 4 dims block and swaps halves with
-//     v_perm_b32.
+//     reads V^T from LDS with the same key order.  V goes into LDS as it is in
+//     memory, [key][dim], and the transposing LDS read (ds_read_b64_tr_b16)
+//     hands each lane one dim of 4 consecutive keys.
+//   * Tile loads: every full tile's K and V rows are at fixed per-thread
+//     offsets from a wave-uniform tile base; only the last, partial tile clamps
+//     its keys to the sequence.
 // Operand layout of v_mfma_f32_32x32x16_bf16: lane l supplies row (l % 32) of
 // A and column (l % 32) of B, 8 consecutive k each, k = 8 (l / 32) + j; its 16
 // results are C[8(i/4) + 4(l/32) + i%4][l % 32].
@@ -50,7 +53,7 @@ constexpr int FA_WAVES = 4;
 constexpr int FA_THREADS = FA_WAVES * 64;
 constexpr int FA_BM = 32 * FA_WAVES;  // queries per block
 constexpr int FA_BN = 64;             // keys per tile
-constexpr int FA_VROW = FA_BN;        // LDS V^T row length (bf16): 128 B, one pass over the 32 banks
+
 constexpr float FA_LOG2E = 1.4426950408889634f;
 constexpr float FA_RESCALE = 8.0f;    // log2 headroom of the lazily updated running max
 
@@ -87,11 +90,6 @@ constexpr float FA_MASKED = 1.7014117e38f;  // FLT_MAX / 2
 __device__ __forceinline__ fa_bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return __builtin_bit_cast(fa_bf16x8_t, make_uint4(a, b, c, d));
 }
-
-// V^T row d keeps its 16 groups of 4 keys (8 B, two banks) in the order g ^ fa_vswz(d): the 16 rows written
-// by 16 consecutive lanes (d = 4 dg + r, dg consecutive) and the 16 rows read by 16 consecutive lanes (d
-// consecutive) then fall on 16 distinct bank pairs.
-__device__ __forceinline__ int fa_vswz(int d) { return ((d >> 2) ^ ((d & 3) << 2)) & 15; }
 
 // Block -> (query block, batch, head).  Blocks go round-robin to the 8 XCDs; when the (batch, kv head) groups
 // split evenly over them, each XCD takes whole groups one after another (a group's K/V rows then stay in that
@@ -149,13 +147,16 @@ __device__ __forceinline__ int2 fa_key_range(const FaArgs& a, int q) {
 template <int D, bool CAUSAL, bool MASK, bool SEG>
 __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(MASK ? 1 : 2))) void fa_prefill_kernel(const FaArgs a) {
     constexpr int KROW = D + 8;                                // LDS K row length (bf16)
+    // LDS V row length: 2 VROW = 64 (mod 256) bytes, so the 4 rows x 64 B that each half-wave of a
+    // transposing read addresses fall on distinct banks (D + 16 measured 25 % bank conflicts)
+    constexpr int VROW = D + 32;
     constexpr int DS = D / 16;                                 // k-steps of S^T
     constexpr int DB = D / 32;                                 // 32-dim blocks of O^T
-    constexpr int KCH = FA_BN * D / 8 / FA_THREADS;            // 16-B K chunks per thread
-    constexpr int VBL = (FA_BN / 4) * (D / 4) / FA_THREADS;    // 4x4 V blocks per thread
-    static_assert(KCH >= 1 && VBL >= 1, "tile too small for the block");
+    constexpr int CPR = D / 8;                                 // 16-B chunks per K or V row
+    constexpr int KCH = FA_BN * CPR / FA_THREADS;              // chunks of each per thread
+    static_assert(KCH >= 1 && FA_THREADS % CPR == 0, "tile too small for the block");
     __shared__ __align__(16) uint16_t ks[2][FA_BN * KROW];
-    __shared__ __align__(16) uint16_t vts[2][D * FA_VROW];
+    __shared__ __align__(16) uint16_t vs[2][FA_BN * VROW];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -198,56 +199,52 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(MASK
 
     const uint16_t* kb_ptr = a.k + (size_t)b * a.k_sb + (size_t)kvh * a.k_sh;
     const uint16_t* vb_ptr = a.v + (size_t)b * a.v_sb + (size_t)kvh * a.v_sh;
-    uint4 kreg[KCH];
-    uint2 vreg[VBL][4];
+    // chunk i of this thread: key row tid / CPR + i FA_THREADS / CPR of the tile, 8 dims at 8 (tid % CPR)
+    const int ch_key = tid / CPR, ch_col = (tid % CPR) * 8;
+    uint32_t koff[KCH], voff[KCH];  // element offsets from a full tile's first key row
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+        koff[i] = (uint32_t)((ch_key + i * (FA_THREADS / CPR)) * a.k_st + ch_col);
+        voff[i] = (uint32_t)((ch_key + i * (FA_THREADS / CPR)) * a.v_st + ch_col);
+    }
+    uint4 kreg[KCH], vreg[KCH];
     auto load_tile = [&](int t0) {
+        if (t0 + FA_BN <= s_len) {
+            const uint16_t* kt = kb_ptr + (size_t)t0 * a.k_st;  // wave-uniform
+            const uint16_t* vt = vb_ptr + (size_t)t0 * a.v_st;
 #pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            const int c = tid + FA_THREADS * i;
-            const int key = min(t0 + c / (D / 8), s_len - 1);
-            kreg[i] = load_u4(kb_ptr + (size_t)key * a.k_st + (c % (D / 8)) * 8);
-        }
+            for (int i = 0; i < KCH; ++i) {
+                kreg[i] = load_u4(kt + koff[i]);
+                // V rows are 8-B aligned: two 8-B halves
+                const uint2 lo = *reinterpret_cast<const uint2*>(vt + voff[i]);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vt + voff[i] + 4);
+                vreg[i] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            }
+        } else {
+            // the sequence's last, partial tile: keys past the end read the last key again (never used)
 #pragma unroll
-        for (int i = 0; i < VBL; ++i) {
-            const int bi = tid + FA_THREADS * i;
-            const int dg = bi % (D / 4);
-            const int kg = bi / (D / 4);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = min(t0 + 4 * kg + r, s_len - 1);
-                vreg[i][r] = *reinterpret_cast<const uint2*>(vb_ptr + (size_t)key * a.v_st + 4 * dg);
+            for (int i = 0; i < KCH; ++i) {
+                const int key = min(t0 + ch_key + i * (FA_THREADS / CPR), s_len - 1);
+                kreg[i] = load_u4(kb_ptr + (size_t)key * a.k_st + ch_col);
+                const uint16_t* vr = vb_ptr + (size_t)key * a.v_st + ch_col;
+                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 4);
+                vreg[i] = make_uint4(lo.x, lo.y, hi.x, hi.y);
             }
         }
     };
     auto store_tile = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
-            const int c = tid + FA_THREADS * i;
-            *reinterpret_cast<uint4*>(&ks[buf][(c / (D / 8)) * KROW + (c % (D / 8)) * 8]) = kreg[i];
-        }
-#pragma unroll
-        for (int i = 0; i < VBL; ++i) {
-            const int bi = tid + FA_THREADS * i;
-            const int dg = bi % (D / 4);
-            const int kg = bi / (D / 4);
-            const uint2* r = vreg[i];
-            // rows of 4 keys x (d0 d1 | d2 d3) -> columns of 4 dims x (k0 k1 | k2 k3)
-            const uint2 d0 = make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, 0x05040100u),
-                                        __builtin_amdgcn_perm(r[3].x, r[2].x, 0x05040100u));
-            const uint2 d1 = make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, 0x07060302u),
-                                        __builtin_amdgcn_perm(r[3].x, r[2].x, 0x07060302u));
-            const uint2 d2 = make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, 0x05040100u),
-                                        __builtin_amdgcn_perm(r[3].y, r[2].y, 0x05040100u));
-            const uint2 d3 = make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, 0x07060302u),
-                                        __builtin_amdgcn_perm(r[3].y, r[2].y, 0x07060302u));
-            const uint2 dv[4] = {d0, d1, d2, d3};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int d = 4 * dg + r;
-                *reinterpret_cast<uint2*>(&vts[buf][d * FA_VROW + ((kg ^ fa_vswz(d)) << 2)]) = dv[r];
-            }
+            const int key = ch_key + i * (FA_THREADS / CPR);
+            *reinterpret_cast<uint4*>(&ks[buf][key * KROW + ch_col]) = kreg[i];
+            *reinterpret_cast<uint4*>(&vs[buf][key * VROW + ch_col]) = vreg[i];
         }
     };
+    // transposing V^T reads: lane 4 j + c of each 16-lane group addresses key row j of a 4-row block at dims
+    // 4 c .. 4 c + 3 of the group's 16 dims, and receives one dim of the 4 keys
+    const int n16 = lane & 15;
+    const int v_lane = (4 * half + (n16 >> 2)) * VROW + 16 * ((lane >> 4) & 1) + 4 * (n16 & 3);
 
     fa_f32x16_t o[DB];
 #pragma unroll
@@ -373,14 +370,12 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(MASK
             for (int stp = 0; stp < 2; ++stp) {
                 const fa_bf16x8_t pf =
                     as_bf16x8(pk[kb][4 * stp], pk[kb][4 * stp + 1], pk[kb][4 * stp + 2], pk[kb][4 * stp + 3]);
-                // key groups 8 kb + 4 stp + half and + 2, at their swizzled places in row d
-                const int g1 = 8 * kb + 4 * stp + half;
+                // dims 32 db + lane % 32 of keys 32 kb + 16 stp + 4 half + 0..3 and + 8
+                const uint16_t* vt = &vs[buf][v_lane + (32 * kb + 16 * stp) * VROW];
 #pragma unroll
                 for (int db = 0; db < DB; ++db) {
-                    const int d = 32 * db + (lane & 31);
-                    const uint16_t* vrow = &vts[buf][d * FA_VROW];
-                    const uint2 va = *reinterpret_cast<const uint2*>(vrow + ((g1 ^ fa_vswz(d)) << 2));
-                    const uint2 vb = *reinterpret_cast<const uint2*>(vrow + (((g1 + 2) ^ fa_vswz(d)) << 2));
+                    const uint2 va = lds_read_tr16_b64(vt + 32 * db);
+                    const uint2 vb = lds_read_tr16_b64(vt + 8 * VROW + 32 * db);
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(va.x, va.y, vb.x, vb.y), pf, o[db],
                                                                    0, 0, 0);
                 }
@@ -485,6 +480,9 @@ static int fa_prefill(const void* q, const void* k, const void* v, void* out, co
         if (strides[i] % 8 != 0) return T2H_ERR_ALIGN;
     for (int i = 6; i < 12; ++i)
         if (strides[i] % 4 != 0) return T2H_ERR_ALIGN;
+    // a tile's key rows are addressed by 32-bit element offsets from its first row
+    if ((uint64_t)FA_BN * (uint64_t)(strides[4] > strides[7] ? strides[4] : strides[7]) + d > 0xffffffffu)
+        return T2H_ERR_SHAPE;
     FaArgs a = {};
     a.q = reinterpret_cast<const uint16_t*>(q);
     a.k = reinterpret_cast<const uint16_t*>(k);
