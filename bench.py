@@ -172,35 +172,46 @@ def phase_trace(args) -> int:
     from torch2vk_amd.qwen3.model import Qwen3Decoder
     from torch2vk_amd.qwen3.weights import synthetic_weights
 
+    from torch2vk_amd.qwen3.model import Qwen3DecoderGroup
+
     dev = torch.device("cuda:0")
-    cfg = QWEN3_8B if args.model == "8b" else QWEN3_0_6B
+    # --config asr: the C5 decoder's launch, four 0.6B sequences side by side (64 blocks each); the table is
+    # sequence 0's blocks
+    n_seq = 4 if args.config == "asr" else 1
+    cfg = QWEN3_8B if args.model == "8b" and n_seq == 1 else QWEN3_0_6B
     w = synthetic_weights(cfg, device=dev, seed=0)
-    dec = Qwen3Decoder(w, max_positions=args.positions + 64, max_new_tokens=4, device=dev, persistent=True)
+    decs = [Qwen3Decoder(w, max_positions=args.positions + 64, max_new_tokens=4, device=dev, persistent=True)
+            for _ in range(n_seq)]
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
-    dec.k_cache[:, :args.positions].normal_(generator=gen)
-    dec.v_cache[:, :args.positions].normal_(generator=gen)
-    dec.position.fill_(args.positions)
+    for dec in decs:
+        dec.k_cache[:, :args.positions].normal_(generator=gen)
+        dec.v_cache[:, :args.positions].normal_(generator=gen)
+        dec.position.fill_(args.positions)
+    runner = decs[0] if n_seq == 1 else Qwen3DecoderGroup(decs)
     trace = kernels.decode_layers_trace(cfg.layers, dev)
     launches = []
     for _ in range(max(3, args.kernel_reps)):
-        dec.h.normal_(generator=gen)
+        for dec in decs:
+            dec.h.normal_(generator=gen)
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-        dec.run_decode_layers(trace=trace)
+        runner.run_decode_layers(trace=trace)
         end.record()
         end.synchronize()
         launches.append((start.elapsed_time(end) * 1e3, trace.cpu().numpy().copy()))
-    status = decode_status(dec)
-    if status:
-        print(f"[bench] persistent kernel status {status:#x}: trace invalid", file=sys.stderr)
-        return 3
+    for dec in decs:
+        status = decode_status(dec)
+        if status:
+            print(f"[bench] persistent kernel status {status:#x}: trace invalid", file=sys.stderr)
+            return 3
     us_launch = float(np.median([u for u, _ in launches]))
     names = kernels.DECODE_TRACE_PHASES
     # the blocks that ran each phase: those that stamped its input in hand (the buffer starts zeroed; the
     # merge runs on as many blocks as there are q heads and not at all up to 256 positions, where the
     # attention runs on one block per kv head)
     ran = launches[-1][1][:, :, :, 1] != 0                       # [layers, phases, blocks]
+    ran[:, :, 256 // n_seq:] = False                             # sequence 0's blocks
     n_blocks = [int(ran[2, ph].sum()) for ph in range(6)]
     rows = []   # [layer, phase] -> begin, ready_med, ready_max, end_med, end_max, polls, first_med (us from prev end)
     periods = []
@@ -233,7 +244,8 @@ def phase_trace(args) -> int:
         print(f"| {names[ph]} | {n_blocks[ph]} | {b:.2f} | {rm:.2f} / {rx:.2f} | {fm:.2f} | {em:.2f} / {ex:.2f} | "
               f"{pl:.1f} |")
     crit = m[:, 4]
-    print(f"\nlaunch {us_launch:.1f} us ({cfg.layers} layers, KV position {args.positions}); layer period "
+    print(f"\nlaunch {us_launch:.1f} us ({cfg.layers} layers, {n_seq} sequence(s), KV position {args.positions}); "
+          f"layer period "
           f"{period:.2f} us; sum of phase critical-path steps {np.nansum(crit):.2f} us")
     att = []
     for _, tr in launches[1:]:

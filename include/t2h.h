@@ -321,6 +321,13 @@ int t2h_qwen3_decode_layers_traced(const uint64_t* layer_table, uint32_t n_layer
                                    const int32_t* cache_position, float eps, float theta, void* workspace,
                                    size_t workspace_bytes, uint32_t* status, uint64_t* trace, size_t trace_bytes,
                                    void* stream);
+/* t2h_qwen3_decode_layers_seqs with the same timeline: one trace buffer for the launch, indexed by the grid's
+ * block, so with n_seq = 4 sequence i's stamps are blocks 64 i .. 64 i + 63. */
+int t2h_qwen3_decode_layers_seqs_traced(uint32_t n_seq, const uint64_t* const* layer_tables, uint32_t n_layers,
+                                        uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk, uint32_t d,
+                                        uint32_t s_cap, float* const* hs, const int32_t* const* cache_positions,
+                                        float eps, float theta, void* const* workspaces, size_t workspace_bytes,
+                                        uint32_t* const* statuses, uint64_t* trace, size_t trace_bytes, void* stream);
 
 /* -------------------------------------------------- prefill attention --- */
 /* out = softmax(q.k^T * scale + mask) . v on the matrix cores (bf16 in, fp32

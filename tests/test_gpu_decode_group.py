@@ -192,3 +192,37 @@ def test_group_q4_k_m_equals_one_launch_each(device):
     for a, b in zip(group, single):
         torch.testing.assert_close(a.h, b.h, rtol=0, atol=0)
         torch.testing.assert_close(a.v_cache, b.v_cache, rtol=0, atol=0)
+
+
+def test_group_traced_launch_equals_untraced(device, small_06b):
+    """The timeline instantiation of the 4-sequence launch (t2h_qwen3_decode_layers_seqs_traced) computes the same
+    bits as the plain one and stamps every sequence's 64 blocks in every phase it runs."""
+    from torch2vk_amd import kernels
+    from torch2vk_amd.qwen3.model import Qwen3DecoderGroup
+
+    cfg, w, _, _ = small_06b
+    a, b = _decoders(w, 4, 512), _decoders(w, 4, 512)
+    g = torch.Generator(device=device)
+    g.manual_seed(21)
+    for i, (da, db) in enumerate(zip(a, b)):
+        kc = torch.randn(da.k_cache.shape, generator=g, device=device).to(torch.bfloat16)
+        vc = torch.randn(da.v_cache.shape, generator=g, device=device).to(torch.bfloat16)
+        h0 = torch.randn(cfg.hidden, generator=g, device=device)
+        for d in (da, db):
+            d.k_cache.copy_(kc)
+            d.v_cache.copy_(vc)
+            d.h.copy_(h0)
+            d.position.fill_(100 + 100 * i)  # one sequence past 256 keys: the merge phase runs
+    trace = kernels.decode_layers_trace(cfg.layers, device)
+    Qwen3DecoderGroup(a).run_decode_layers(trace=trace)
+    Qwen3DecoderGroup(b).run_decode_layers()
+    torch.cuda.synchronize()
+    for da, db in zip(a, b):
+        da.check_status()
+        db.check_status()
+        torch.testing.assert_close(da.h, db.h, rtol=0, atol=0)
+        torch.testing.assert_close(da.k_cache, db.k_cache, rtol=0, atol=0)
+    tr = trace.cpu()
+    for ph in (0, 3, 4, 5):  # qkv, o, gate|up, down: every block of every sequence
+        assert (tr[:, ph, :, 3] != 0).all(), ph
+    assert (tr[:, 2, 192:192 + cfg.heads, 3] != 0).all()  # sequence 3 (400 positions) merged its q heads

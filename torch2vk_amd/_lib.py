@@ -70,6 +70,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "t2h_qwen3_decode_layers_seqs": (_i32, [_u32, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp, _f32,
                                              _f32, _vp, _sz, _vp, _vp]),
     "t2h_qwen3_decode_layers_trace_bytes": (_sz, [_u32]),
+    "t2h_qwen3_decode_layers_seqs_traced": (_i32, [_u32, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp,
+                                                   _f32, _f32, _vp, _sz, _vp, _vp, _sz, _vp]),
     "t2h_qwen3_decode_layers_traced": (_i32, [_vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp, _f32, _f32,
                                               _vp, _sz, _vp, _vp, _sz, _vp]),
     "t2h_flash_attn_prefill": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _i32,

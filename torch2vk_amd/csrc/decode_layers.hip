@@ -1529,22 +1529,28 @@ static int dl_launch(const uint64_t* layer_table, uint32_t n_layers, uint32_t s_
 }
 
 // S::NSEQ sequences side by side, sequence i on blocks [i NB, (i + 1) NB).
+// trace: one timeline buffer for the launch (t2h_qwen3_decode_layers_trace_bytes), indexed by the grid's block,
+// so sequence i's stamps are blocks [i NB, (i + 1) NB); null for the untraced instantiation.
 template <class S>
 static int dl_launch_seqs(const uint64_t* const* layer_tables, uint32_t n_layers, uint32_t s_cap, float* const* hs,
                           const int32_t* const* cache_positions, float eps, float theta, void* const* workspaces,
-                          size_t workspace_bytes, uint32_t* const* statuses, void* stream) {
+                          size_t workspace_bytes, uint32_t* const* statuses, uint64_t* trace, void* stream) {
     DlArgsSet<S::NSEQ> as;
     for (int i = 0; i < S::NSEQ; ++i) {
         if (!layer_tables[i] || !hs[i] || !cache_positions[i] || !workspaces[i] || !statuses[i]) return T2H_ERR_NULL;
         const int rc = dl_args<S>(as.s[i], layer_tables[i], n_layers, s_cap, hs[i], cache_positions[i], eps, theta,
-                                  workspaces[i], workspace_bytes, statuses[i], nullptr);
+                                  workspaces[i], workspace_bytes, statuses[i], trace);
         if (rc != T2H_OK) return rc;
         for (int j = 0; j < i; ++j)
             if (workspaces[j] == workspaces[i]) return T2H_ERR_ARG;  // each sequence needs its own workspace
     }
     if (!dl_grid_fits<S>()) return T2H_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((decode_layers_kernel<S, false>), dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
-                       reinterpret_cast<hipStream_t>(stream), as);
+    if (trace == nullptr)
+        hipLaunchKernelGGL((decode_layers_kernel<S, false>), dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
+                           reinterpret_cast<hipStream_t>(stream), as);
+    else
+        hipLaunchKernelGGL((decode_layers_kernel<S, true>), dim3(DL_BLOCKS), dim3(DL_THREADS), 0,
+                           reinterpret_cast<hipStream_t>(stream), as);
     T2H_LAUNCH_CHECK();
     return T2H_OK;
 }
@@ -1616,16 +1622,14 @@ extern "C" int t2h_qwen3_decode_layers_traced(const uint64_t* layer_table, uint3
                     workspace_bytes, status, trace, stream);
 }
 
-extern "C" int t2h_qwen3_decode_layers_seqs(uint32_t n_seq, const uint64_t* const* layer_tables, uint32_t n_layers,
-                                            uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk, uint32_t d,
-                                            uint32_t s_cap, float* const* hs, const int32_t* const* cache_positions,
-                                            float eps, float theta, void* const* workspaces, size_t workspace_bytes,
-                                            uint32_t* const* statuses, void* stream) {
+static int dl_entry_seqs(uint32_t n_seq, const uint64_t* const* layer_tables, uint32_t n_layers, uint32_t hidden,
+                         uint32_t mlp, uint32_t nh, uint32_t nk, uint32_t d, uint32_t s_cap, float* const* hs,
+                         const int32_t* const* cache_positions, float eps, float theta, void* const* workspaces,
+                         size_t workspace_bytes, uint32_t* const* statuses, uint64_t* trace, void* stream) {
     if (!layer_tables || !hs || !cache_positions || !workspaces || !statuses) return T2H_ERR_NULL;
     if (n_seq == 1)
-        return t2h_qwen3_decode_layers(layer_tables[0], n_layers, hidden, mlp, nh, nk, d, s_cap, hs[0],
-                                       cache_positions[0], eps, theta, workspaces[0], workspace_bytes, statuses[0],
-                                       stream);
+        return dl_entry(layer_tables[0], n_layers, hidden, mlp, nh, nk, d, s_cap, hs[0], cache_positions[0], eps,
+                        theta, workspaces[0], workspace_bytes, statuses[0], trace, stream);
     if (n_seq != (uint32_t)DlQwen3_0_6B_x4::NSEQ || !dl_is<DlQwen3_0_6B_x4>(hidden, mlp, nh, nk, d))
         return T2H_ERR_UNSUPPORTED;
     if (n_layers == 0) return T2H_OK;
@@ -1634,5 +1638,28 @@ extern "C" int t2h_qwen3_decode_layers_seqs(uint32_t n_seq, const uint64_t* cons
     constexpr uint32_t waves = DlQwen3_0_6B_x4::ATT_SLOTS * DL_WAVES;
     if ((size_t)(s_cap + waves - 1) / waves > DL_ATT_POS) return T2H_ERR_UNSUPPORTED;  // over 32 positions a wave
     return dl_launch_seqs<DlQwen3_0_6B_x4>(layer_tables, n_layers, s_cap, hs, cache_positions, eps, theta, workspaces,
-                                            workspace_bytes, statuses, stream);
+                                            workspace_bytes, statuses, trace, stream);
+}
+
+extern "C" int t2h_qwen3_decode_layers_seqs(uint32_t n_seq, const uint64_t* const* layer_tables, uint32_t n_layers,
+                                            uint32_t hidden, uint32_t mlp, uint32_t nh, uint32_t nk, uint32_t d,
+                                            uint32_t s_cap, float* const* hs, const int32_t* const* cache_positions,
+                                            float eps, float theta, void* const* workspaces, size_t workspace_bytes,
+                                            uint32_t* const* statuses, void* stream) {
+    return dl_entry_seqs(n_seq, layer_tables, n_layers, hidden, mlp, nh, nk, d, s_cap, hs, cache_positions, eps, theta,
+                         workspaces, workspace_bytes, statuses, nullptr, stream);
+}
+
+extern "C" int t2h_qwen3_decode_layers_seqs_traced(uint32_t n_seq, const uint64_t* const* layer_tables,
+                                                   uint32_t n_layers, uint32_t hidden, uint32_t mlp, uint32_t nh,
+                                                   uint32_t nk, uint32_t d, uint32_t s_cap, float* const* hs,
+                                                   const int32_t* const* cache_positions, float eps, float theta,
+                                                   void* const* workspaces, size_t workspace_bytes,
+                                                   uint32_t* const* statuses, uint64_t* trace, size_t trace_bytes,
+                                                   void* stream) {
+    if (!trace) return T2H_ERR_NULL;
+    if (trace_bytes < t2h_qwen3_decode_layers_trace_bytes(n_layers)) return T2H_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(trace) % 8 != 0) return T2H_ERR_ALIGN;
+    return dl_entry_seqs(n_seq, layer_tables, n_layers, hidden, mlp, nh, nk, d, s_cap, hs, cache_positions, eps, theta,
+                         workspaces, workspace_bytes, statuses, trace, stream);
 }

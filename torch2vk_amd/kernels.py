@@ -776,9 +776,11 @@ LM_HEAD_SEQS_MAX = 4  # sequences of one t2h_q4k_lm_head_argmax_partial_seqs lau
 
 def decode_layers_seqs(tables: list[torch.Tensor], hs: list[torch.Tensor], cache_positions: list[torch.Tensor],
                        workspaces: list[torch.Tensor], statuses: list[torch.Tensor], *, hidden: int, mlp: int,
-                       nh: int, nk: int, d: int, s_cap: int, eps: float = RMS_EPS, theta: float = 1.0e6) -> None:
+                       nh: int, nk: int, d: int, s_cap: int, eps: float = RMS_EPS, theta: float = 1.0e6,
+                       trace: torch.Tensor | None = None) -> None:
     """decode_layers for len(tables) sequences in one persistent launch (t2h_qwen3_decode_layers_seqs): each
-    sequence its own table (its KV caches), h, position, workspace and status."""
+    sequence its own table (its KV caches), h, position, workspace and status.  ``trace`` (decode_layers_trace)
+    records the launch's phase timeline, sequence i in blocks 256 i / n .. 256 (i + 1) / n - 1."""
     n = len(tables)
     if n not in DECODE_SEQS or not (len(hs) == len(cache_positions) == len(workspaces) == len(statuses) == n):
         raise ValueError(f"decode_layers_seqs runs {DECODE_SEQS} sequences with one of each argument per sequence")
@@ -796,9 +798,14 @@ def decode_layers_seqs(tables: list[torch.Tensor], hs: list[torch.Tensor], cache
         raise ValueError("every sequence needs its own workspace")
     arr = lambda ts: (ctypes.c_void_p * n)(*[t.data_ptr() for t in ts])  # noqa: E731
     t_arr, h_arr, p_arr, w_arr, s_arr = arr(tables), arr(hs), arr(cache_positions), arr(workspaces), arr(statuses)
-    call("t2h_qwen3_decode_layers_seqs", n, ctypes.addressof(t_arr), int(tables[0].shape[0]), hidden, mlp, nh, nk, d,
-         s_cap, ctypes.addressof(h_arr), ctypes.addressof(p_arr), eps, theta, ctypes.addressof(w_arr),
-         workspaces[0].numel(), ctypes.addressof(s_arr), stream_handle())
+    args = (n, ctypes.addressof(t_arr), int(tables[0].shape[0]), hidden, mlp, nh, nk, d, s_cap,
+            ctypes.addressof(h_arr), ctypes.addressof(p_arr), eps, theta, ctypes.addressof(w_arr),
+            workspaces[0].numel(), ctypes.addressof(s_arr))
+    if trace is None:
+        call("t2h_qwen3_decode_layers_seqs", *args, stream_handle())
+    else:
+        _check(trace, "trace", torch.int64, align=8)
+        call("t2h_qwen3_decode_layers_seqs_traced", *args, ptr(trace), trace.numel() * 8, stream_handle())
 
 
 DECODE_TRACE_PHASES = ("qkv", "attention", "merge", "o", "gate_up", "down")

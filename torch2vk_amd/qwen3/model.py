@@ -668,12 +668,14 @@ class Qwen3DecoderGroup:
             d.run_lm_head_select()
             d.run_token_store(advance=True)
 
-    def run_decode_layers(self) -> None:
+    def run_decode_layers(self, trace: torch.Tensor | None = None) -> None:
+        """Every sequence's layers in one persistent launch; ``trace`` (kernels.decode_layers_trace) records its
+        phase timeline."""
         ds, c = self.decoders, self.decoders[0].config
         kernels.decode_layers_seqs([d.layer_table for d in ds], [d.h for d in ds], [d.position for d in ds],
                                    [d.layers_ws for d in ds], [d.status for d in ds], hidden=c.hidden, mlp=c.mlp,
                                    nh=c.heads, nk=c.kv_heads, d=c.head_dim, s_cap=ds[0].max_positions,
-                                   eps=c.rms_eps, theta=c.rope_theta)
+                                   eps=c.rms_eps, theta=c.rope_theta, trace=trace)
 
     def run_lm_heads(self) -> None:
         """Every sequence's final norm + LM head + per-block argmax: one launch that reads a Q4_K head once for
