@@ -111,6 +111,26 @@ def test_argument_validation_returns_status(lib):
     assert lib.t2h_token_select_store_seqs(5, pa, pa, 8, fake, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 5
     assert lib.t2h_token_select_store_seqs(2, pa, pa, 0, fake, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 2
     assert lib.t2h_token_select_store_seqs(2, pa, pa, 8, None, 1, pa, pa, pa, 4, pa, pa, 1, pa, None) == 1
+    # bf16-weight GEMM and the dequantise-once kernel: nulls, K rule, 16-byte operands, weight type codes
+    assert lib.t2h_bf16_gemm(None, fake, fake, 0, None, 4, 128, 16, None) == 1
+    assert lib.t2h_bf16_gemm(fake, fake, fake, 0, None, 4, 100, 16, None) == 2
+    assert lib.t2h_bf16_gemm(odd, fake, fake, 0, None, 4, 128, 16, None) == 7
+    assert lib.t2h_bf16_gemm(fake, odd, fake, 0, None, 4, 128, 16, None) == 7
+    assert lib.t2h_bf16_gemm(fake, fake, fake, 9, None, 4, 128, 16, None) == 3
+    assert lib.t2h_dequantize_bf16(99, fake, 4, 256, fake, None) == 3
+    assert lib.t2h_dequantize_bf16(8, None, 4, 256, fake, None) == 1
+    assert lib.t2h_dequantize_bf16(12, fake, 4, 320, fake, None) == 2   # Q4_K: K % 256
+    assert lib.t2h_dequantize_bf16(8, fake, 4, 96, fake, None) == 2     # K % 64
+    assert lib.t2h_dequantize_bf16(8, fake, 4, 256, odd, None) == 7
+    assert lib.t2h_gemm_swiglu(30, fake, fake, fake, fake, 4, 100, 16, None) == 2
+    assert lib.t2h_gemm_swiglu(30, fake, odd, fake, fake, 4, 128, 16, None) == 7
+    # the traced multi-sequence decode launch checks its timeline buffer before anything else
+    assert lib.t2h_qwen3_decode_layers_seqs_traced(4, pa, 28, 1024, 3072, 16, 8, 128, 512, pa, pa, 1e-6, 1e6, pa,
+                                                   1 << 20, pa, None, 1 << 20, None) == 1
+    assert lib.t2h_qwen3_decode_layers_seqs_traced(4, pa, 28, 1024, 3072, 16, 8, 128, 512, pa, pa, 1e-6, 1e6, pa,
+                                                   1 << 20, pa, fake, 64, None) == 6
+    assert lib.t2h_qwen3_decode_layers_seqs_traced(4, pa, 28, 1024, 3072, 16, 8, 128, 512, pa, pa, 1e-6, 1e6, pa,
+                                                   1 << 20, pa, ctypes.c_void_p(0x1004), 1 << 24, None) == 7
 
 
 def test_python_wrappers_reject_host_tensors():
