@@ -183,6 +183,12 @@ int t2h_gemm_splitk(int wtype, const void* x, const void* w, const void* w_up, c
  * bf16), and runs the prefill GEMMs over weights dequantised once by t2h_dequantize_bf16. */
 int t2h_bf16_gemm(const void* x, const void* w, void* y, int out_dtype, const float* residual, uint32_t m,
                   uint32_t k, uint32_t n, void* stream);
+/* t2h_q8_0_linear's epilogues (bias, GELU, residual) over bf16 weight rows [n, k]: the encoder linears at
+ * large M over weights dequantised once (t2h_dequantize_bf16), bit-identical to t2h_q8_0_linear on the packed
+ * rows when they hold k values.  replaces LINEAR_BIAS_BF16W_BF16B_F32
+ * (src/models/exported_qwen3_asr/shaders/linear_bias_bf16w_bf16b_f32.py, bf16 bias there, fp32 here). */
+int t2h_bf16_linear(const void* x, const void* w, const float* bias, int act, void* y, int out_dtype,
+                    const float* residual, uint32_t m, uint32_t k, uint32_t n, void* stream);
 /* out bf16 [rows, k] (16-byte aligned) = the bf16 values the GEMMs above dequantise W's rows to in LDS (wtype
  * Q8_0 / Q4_K / Q6_K; k % 64 == 0, % 256 for the K types), so that t2h_bf16_gemm / t2h_gemm_swiglu(BF16) over
  * out give bit-identical results to the quantized GEMM on W.  For large prefills, where the quantized GEMM

@@ -227,3 +227,35 @@ def test_bf16_gemm_large_grid_equals_quantized_gemm(device, wtype, m, k, n):
     aq = kernels.gemm_swiglu(x, w[:n_ff].contiguous(), w[n_ff:2 * n_ff].contiguous(), wtype, splits=1)
     ab = kernels.gemm_swiglu(x, wb[:n_ff].contiguous(), wb[n_ff:2 * n_ff].contiguous(), "bf16", splits=1)
     torch.testing.assert_close(ab, aq, rtol=0, atol=0)
+
+
+def test_q8_0_linear_dequantise_once_equals_in_loop(device):
+    """The encoder's linears at M >= 4096 (bias + GELU, and fp32 residual) over Q8_0 weights dequantised once
+    (t2h_bf16_linear) give the in-loop GEMM's bits; weights shorter than x's rows (w_k < K) keep the in-loop
+    path."""
+    from torch2vk_amd import kernels
+
+    g = torch.Generator(device=device)
+    g.manual_seed(13)
+    m, k, n = 4500, 1024, 1536
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    w = kernels.quantize(torch.randn(n, k, generator=g, device=device) * 0.03, "q8_0")
+    bias = torch.randn(n, generator=g, device=device)
+    saved = kernels.DEQUANT_FIRST_ROWS
+    try:
+        kernels.DEQUANT_FIRST_ROWS = 0
+        ref = kernels.q8_0_linear(x, w, bias=bias, act="gelu")
+        r0 = torch.randn(m, n, generator=g, device=device)
+        ref_res = kernels.q8_0_linear(x, w, bias=bias, out=r0.clone(), out_dtype=torch.float32, residual=None)
+        ref_res2 = r0.clone()
+        kernels.q8_0_linear(x, w, out=ref_res2, out_dtype=torch.float32, residual=ref_res2)
+        kernels.DEQUANT_FIRST_ROWS = 4096
+        got = kernels.q8_0_linear(x, w, bias=bias, act="gelu")
+        got_res = kernels.q8_0_linear(x, w, bias=bias, out=r0.clone(), out_dtype=torch.float32, residual=None)
+        got_res2 = r0.clone()
+        kernels.q8_0_linear(x, w, out=got_res2, out_dtype=torch.float32, residual=got_res2)
+    finally:
+        kernels.DEQUANT_FIRST_ROWS = saved
+    torch.testing.assert_close(got, ref, rtol=0, atol=0)
+    torch.testing.assert_close(got_res, ref_res, rtol=0, atol=0)
+    torch.testing.assert_close(got_res2, ref_res2, rtol=0, atol=0)

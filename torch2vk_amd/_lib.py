@@ -95,6 +95,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "t2h_embedding_q8_0": (_i32, [_vp, _u64, _vp, _u32, _u32, _vp, _vp]),
     "t2h_q6k_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp]),
     "t2h_bf16_gemm": (_i32, [_vp, _vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp]),
+    "t2h_bf16_linear": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _u32, _u32, _u32, _vp]),
     "t2h_dequantize_bf16": (_i32, [_i32, _vp, _u32, _u32, _vp, _vp]),
     "t2h_gemm_swiglu": (_i32, [_i32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "t2h_gemm_splitk_bytes": (_sz, [_u32, _u32, _u32, _i32]),

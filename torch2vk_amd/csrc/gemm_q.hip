@@ -731,6 +731,11 @@ extern "C" int t2h_bf16_gemm(const void* x, const void* w, void* y, int out_dtyp
     return gemm_q_launch<GemmBF16>(x, w, nullptr, GQACT_NONE, y, out_dtype, residual, m, k, n, k, stream);
 }
 
+extern "C" int t2h_bf16_linear(const void* x, const void* w, const float* bias, int act, void* y, int out_dtype,
+                               const float* residual, uint32_t m, uint32_t k, uint32_t n, void* stream) {
+    return gemm_q_launch<GemmBF16>(x, w, bias, act, y, out_dtype, residual, m, k, n, k, stream);
+}
+
 extern "C" int t2h_dequantize_bf16(int wtype, const void* w, uint32_t rows, uint32_t k, void* out, void* stream) {
     switch (wtype) {
         case T2H_WTYPE_Q8_0: return gemm_dequant_launch<GemmQ80>(w, rows, k, out, stream);

@@ -511,7 +511,8 @@ def q8_0_linear(x: torch.Tensor, w: torch.Tensor, *, bias: torch.Tensor | None =
                 residual: torch.Tensor | None = None, splits: int | None = None) -> torch.Tensor:
     """y[M, N] = act(x[M, K] . deq(W)^T + bias) (+ residual) on the matrix cores (LINEAR_BIAS_Q8_0W_F32B_F32).
     x bf16 with K % 64 == 0; W Q8_0 rows of w_k = 32 * blocks <= K values (x's columns past w_k must be
-    finite: they multiply zeros); bias fp32 [N]; act None or "gelu" (exact erf)."""
+    finite: they multiply zeros); bias fp32 [N]; act None or "gelu" (exact erf).  From DEQUANT_FIRST_ROWS rows
+    with w_k == K, W is dequantised once and the bf16 rows run t2h_bf16_linear (the same bits)."""
     _check(x, "x", torch.bfloat16)
     _check(w, "weight", torch.uint8, align=1)
     k = int(x.shape[-1])
@@ -544,6 +545,11 @@ def q8_0_linear(x: torch.Tensor, w: torch.Tensor, *, bias: torch.Tensor | None =
     splits = gemm_splits(m, n, k) if splits is None else splits
     if splits > 1:
         _gemm_splitk("q8_0", x, w, None, out, m, k, n, w_k, splits, bias=bias, act=ACTS[act], residual=residual)
+        return out
+    if w_k == k and _dequant_first(m, "q8_0", splits):
+        wb = dequantize_bf16(w, "q8_0", k)
+        call("t2h_bf16_linear", ptr(x), ptr(wb), ptr(bias), ACTS[act], ptr(out), _OUT_DTYPES[out.dtype], ptr(residual),
+             m, k, n, stream_handle())
         return out
     call("t2h_q8_0_linear", ptr(x), ptr(w), ptr(bias), ACTS[act], ptr(out), _OUT_DTYPES[out.dtype], ptr(residual),
          m, k, n, w_k, stream_handle())
