@@ -1009,7 +1009,7 @@ def bench_prefill(args) -> int:
         "achieved_tflops": round(tflops, 1),
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_q_kernel<GemmBF16, SwiGLU epilogue> (gate|up over the Q8_0 weights dequantised to "
+            "kernel": "gemm_bf16_ring_kernel<SwiGLU epilogue> (gate|up over the Q8_0 weights dequantised to "
                       "bf16 once, M 16384 K 4096 N 2 x 12288)",
             "achieved": round(gu_tflops, 1),
             "peak": MFMA_BF16_PEAK_TFLOPS,
@@ -1023,7 +1023,7 @@ def bench_prefill(args) -> int:
                     "in_loop_dequant_us": round(gu_tile_us, 1),
                     "note": "with_dequant: the step's call (2 dequantisations + the bf16 GEMM); in_loop_dequant: "
                             "gemm_q_kernel<GemmQ80> dequantising every tile"},
-        "up_projection_gemm": {"kernel": "t2h_dequantize_bf16 + gemm_q_kernel<GemmBF16> (M 16384 K 4096 N 12288, "
+        "up_projection_gemm": {"kernel": "t2h_dequantize_bf16 + gemm_bf16_ring_kernel (M 16384 K 4096 N 12288, "
                                          "fp32 out)",
                                "avg_launch_us": round(gemm_step_us, 1), "tflops": round(gemm_tflops, 1),
                                "gemm_alone_us": round(gemm_us, 1), "in_loop_dequant_us": round(gemm_tile_us, 1),

@@ -229,6 +229,28 @@ def test_bf16_gemm_large_grid_equals_quantized_gemm(device, wtype, m, k, n):
     torch.testing.assert_close(ab, aq, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("k", [64, 128, 192, 1088])
+def test_bf16_large_grid_stage_counts_equal_quantized_gemm(device, k):
+    """The large-grid bf16 kernel (two LDS stages of 64 K, the last stage peeled, the stage after the end loaded
+    into a buffer nothing reads) at 1, 2, 3 and 17 stages: the quantized GEMM's bits, plain and SwiGLU."""
+    from torch2vk_amd import kernels
+
+    g = torch.Generator(device=device)
+    g.manual_seed(k)
+    m, n = 4096, 16384
+    w = kernels.quantize(torch.randn(n, k, generator=g, device=device) * 0.05, "q8_0")
+    wb = kernels.dequantize_bf16(w, "q8_0", k)
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    yq = kernels.gemm(x, w, "q8_0", out_dtype=torch.float32, splits=1)
+    yb = kernels.gemm(x, wb, "bf16", out_dtype=torch.float32, splits=1)
+    torch.testing.assert_close(yb, yq, rtol=0, atol=0)
+    del yq, yb
+    n_ff = n // 2
+    aq = kernels.gemm_swiglu(x, w[:n_ff].contiguous(), w[n_ff:].contiguous(), "q8_0", splits=1)
+    ab = kernels.gemm_swiglu(x, wb[:n_ff].contiguous(), wb[n_ff:].contiguous(), "bf16", splits=1)
+    torch.testing.assert_close(ab, aq, rtol=0, atol=0)
+
+
 def test_q8_0_linear_dequantise_once_equals_in_loop(device):
     """The encoder's linears at M >= 4096 (bias + GELU, and fp32 residual) over Q8_0 weights dequantised once
     (t2h_bf16_linear) give the in-loop GEMM's bits; weights shorter than x's rows (w_k < K) keep the in-loop
