@@ -697,17 +697,18 @@ __global__ __launch_bounds__(GR_THREADS) void gemm_bf16_ring_kernel(const GemmAr
     // epilogue: lane holds column (lane % 32) of each 32 x 32 tile, rows 8 (e / 4) + 4 (lane / 32) + e % 4
     const uint32_t row_base = m0 + wm * 128 + (lane >> 5) * 4;
     if constexpr (EPI == GQEPI_SWIGLU) {
-        // tile columns j = 2 p hold gate and j = 2 p + 1 up of feature f
+        // tile columns j = 2 p hold gate and j = 2 p + 1 up of feature f = f0 + 32 p; the two features of a row
+        // are stored back to back, so each 128-B line of the output is written whole
+        const uint32_t f0 = n0 / 2 + wn * 64 + (lane & 31);
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const uint32_t f = n0 / 2 + wn * 64 + p * 32 + (lane & 31);
-            if (f >= a.n_ff) continue;
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t row = row_base + i * 32 + (e >> 2) * 8 + (e & 3);
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const uint32_t row = row_base + i * 32 + (e >> 2) * 8 + (e & 3);
-                    if (row < a.m) {
+                for (int p = 0; p < 2; ++p) {
+                    const uint32_t f = f0 + p * 32;
+                    if (row < a.m && f < a.n_ff) {
                         const float g = acc[i][2 * p][e];
                         const float sg =
                             g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
@@ -715,12 +716,32 @@ __global__ __launch_bounds__(GR_THREADS) void gemm_bf16_ring_kernel(const GemmAr
                             (uint16_t)f32_to_bf16_bits(sg * acc[i][2 * p + 1][e]);
                     }
                 }
-        }
+            }
         return;
     }
+    const uint32_t col0 = n0 + wn * 128 + (lane & 31);
+    if constexpr (EPI == GQEPI_BF16) {
+        // a row's 4 tile columns (2 x 128 B) stored back to back
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t row = row_base + i * 32 + (e >> 2) * 8 + (e & 3);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t col = col0 + j * 32;
+                    if (row < a.m && col < a.n)
+                        reinterpret_cast<uint16_t*>(a.c)[(size_t)row * a.n + col] =
+                            (uint16_t)f32_to_bf16_bits(acc[i][j][e]);
+                }
+            }
+        return;
+    }
+    // fp32 (a tile column is a whole 128-B line per row), plus the residual: a tile's 16 residual values are
+    // loaded before any of its results is stored
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint32_t col = n0 + wn * 128 + j * 32 + (lane & 31);
+        const uint32_t col = col0 + j * 32;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float rv[16];
@@ -731,19 +752,12 @@ __global__ __launch_bounds__(GR_THREADS) void gemm_bf16_ring_kernel(const GemmAr
                     rv[e] = row < a.m && col < a.n ? a.residual[(size_t)row * a.n + col] : 0.0f;
                 }
             }
-            float ov[16];
-#pragma unroll
-            for (int e = 0; e < 16; ++e) ov[e] = EPI == GQEPI_RESID ? rv[e] + acc[i][j][e] : acc[i][j][e];
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const uint32_t row = row_base + i * 32 + (e >> 2) * 8 + (e & 3);
-                if (row < a.m && col < a.n) {
-                    const size_t idx = (size_t)row * a.n + col;
-                    if constexpr (EPI == GQEPI_BF16)
-                        reinterpret_cast<uint16_t*>(a.c)[idx] = (uint16_t)f32_to_bf16_bits(ov[e]);
-                    else
-                        reinterpret_cast<float*>(a.c)[idx] = ov[e];
-                }
+                if (row < a.m && col < a.n)
+                    reinterpret_cast<float*>(a.c)[(size_t)row * a.n + col] =
+                        EPI == GQEPI_RESID ? rv[e] + acc[i][j][e] : acc[i][j][e];
             }
         }
     }
