@@ -258,6 +258,10 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(MASK
         load_tile(t_first * FA_BN);
         store_tile(0);
     }
+    // Every load issued so far (the q fragments included) has landed before the loop: the compiler's wait
+    // analysis merges the state entering the loop with the state of its back edge, and with q possibly in
+    // flight on entry it made each score MFMA wait for the next tile's loads in flight on the back edge.
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
     __syncthreads();
 
     const float* mrow = nullptr;
