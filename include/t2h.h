@@ -269,8 +269,8 @@ int t2h_attn_decode(const float* q, const float* k_new, const float* v_new, cons
  * pass the activations between phases as epoch-tagged words and poll for them,
  * with no grid barrier (no host sync, graph-capturable).  Calls on one
  * workspace must not overlap in time.
- * Built for the Qwen3-8B shape (hidden 4096, mlp 12288, 32/8 heads) and the Qwen3-0.6B shape (hidden
- * 1024, mlp 3072, 16/8 heads), d 128, Q4_K weights with v and down each Q4_K or Q6_K per layer (the uniform
+ * Built for the Qwen3-8B shape (hidden 4096, mlp 12288, 32/8 heads), the Qwen3-1.7B shape (hidden 2048,
+ * mlp 6144, 16/8 heads) and the Qwen3-0.6B shape (hidden 1024, mlp 3072, 16/8 heads), d 128, Q4_K weights with v and down each Q4_K or Q6_K per layer (the uniform
  * and Q4_K_M policies), bf16 KV caches [s_cap, 8, 128] with s_cap <= 8192, n_layers <= 64 (otherwise
  * T2H_ERR_UNSUPPORTED; so is a GPU that cannot hold 256 blocks).
  * layer_table: device int64 [n_layers][14]: pointers in the order

@@ -287,6 +287,9 @@ struct DlShape {
 using DlQwen3_8B = DlShape<16, 48, 32, 3, DL_R_QKV, DL_PRE_QKV, 2, DL_R_O, DL_PRE_O, 6, DL_R_GU, DL_PRE_GU, 2, DL_R_DOWN,
                            DL_PRE_DOWN, true, DL_BLOCKS, true>;
 using DlQwen3_0_6B = DlShape<4, 12, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, false>;
+// Qwen3-1.7B (hidden 2048, MLP 6144, 16 / 8 heads): rows of 8 and 24 superblocks, 2 rows a unit; Q|K|V one unit
+// per wave, gate|up two, o and down spread
+using DlQwen3_1_7B = DlShape<8, 24, 16, 1, 1, 1, 1, 1, 1, 2, 2, 1, 1, 1, 1, false>;
 // four 0.6B sequences of 64 blocks each: every phase's units over 512 waves (Q|K|V 2 per wave, o 1, gate|up 2,
 // down spread), attention over 8 blocks per kv head
 using DlQwen3_0_6B_x4 = DlShape<4, 12, 16, 2, 2, 1, 1, 1, 1, 2, 2, 1, 1, 1, 1, false, 64>;
@@ -1568,6 +1571,7 @@ extern "C" size_t t2h_qwen3_decode_layers_workspace_bytes(uint32_t hidden, uint3
                                                          uint32_t d) {
     if (dl_is<DlQwen3_8B>(hidden, mlp, nh, nk, d)) return dl_layout<DlQwen3_8B>().total;
     if (dl_is<DlQwen3_0_6B>(hidden, mlp, nh, nk, d)) return dl_layout<DlQwen3_0_6B>().total;
+    if (dl_is<DlQwen3_1_7B>(hidden, mlp, nh, nk, d)) return dl_layout<DlQwen3_1_7B>().total;
     return 0;
 }
 
@@ -1576,17 +1580,21 @@ static int dl_entry(const uint64_t* layer_table, uint32_t n_layers, uint32_t hid
                     float theta, void* workspace, size_t workspace_bytes, uint32_t* status, uint64_t* trace,
                     void* stream) {
     if (!layer_table || !h || !cache_position || !workspace || !status) return T2H_ERR_NULL;
-    const bool is8b = dl_is<DlQwen3_8B>(hidden, mlp, nh, nk, d);
-    if (!is8b && !dl_is<DlQwen3_0_6B>(hidden, mlp, nh, nk, d)) return T2H_ERR_UNSUPPORTED;
+    const bool is8b = dl_is<DlQwen3_8B>(hidden, mlp, nh, nk, d), is1_7b = dl_is<DlQwen3_1_7B>(hidden, mlp, nh, nk, d);
+    if (!is8b && !is1_7b && !dl_is<DlQwen3_0_6B>(hidden, mlp, nh, nk, d)) return T2H_ERR_UNSUPPORTED;
     if (n_layers == 0) return T2H_OK;
     if (n_layers > DL_MAX_LAYERS) return T2H_ERR_UNSUPPORTED;
     if (s_cap == 0) return T2H_ERR_SHAPE;
     if ((size_t)(s_cap + DL_ATT_SLOTS * DL_WAVES - 1) / (DL_ATT_SLOTS * DL_WAVES) > DL_ATT_POS)
         return T2H_ERR_UNSUPPORTED;  // more than 32 positions per wave
-    return is8b ? dl_launch<DlQwen3_8B>(layer_table, n_layers, s_cap, h, cache_position, eps, theta, workspace,
-                                        workspace_bytes, status, trace, stream)
-                : dl_launch<DlQwen3_0_6B>(layer_table, n_layers, s_cap, h, cache_position, eps, theta, workspace,
-                                          workspace_bytes, status, trace, stream);
+    if (is8b)
+        return dl_launch<DlQwen3_8B>(layer_table, n_layers, s_cap, h, cache_position, eps, theta, workspace,
+                                     workspace_bytes, status, trace, stream);
+    if (is1_7b)
+        return dl_launch<DlQwen3_1_7B>(layer_table, n_layers, s_cap, h, cache_position, eps, theta, workspace,
+                                       workspace_bytes, status, trace, stream);
+    return dl_launch<DlQwen3_0_6B>(layer_table, n_layers, s_cap, h, cache_position, eps, theta, workspace,
+                                   workspace_bytes, status, trace, stream);
 }
 
 extern "C" int t2h_qwen3_decode_layers(const uint64_t* layer_table, uint32_t n_layers, uint32_t hidden, uint32_t mlp,

@@ -34,6 +34,8 @@ class Qwen3Config:
 
 QWEN3_0_6B = Qwen3Config("qwen3-0.6b", hidden=1024, layers=28, heads=16, kv_heads=8, head_dim=128, mlp=3072,
                          vocab=151936)
+QWEN3_1_7B = Qwen3Config("qwen3-1.7b", hidden=2048, layers=28, heads=16, kv_heads=8, head_dim=128, mlp=6144,
+                         vocab=151936)
 QWEN3_8B = Qwen3Config("qwen3-8b", hidden=4096, layers=36, heads=32, kv_heads=8, head_dim=128, mlp=12288,
                        vocab=151936)
 
