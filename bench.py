@@ -53,7 +53,7 @@ def parse_args():
                                                            "asr passes)")
     p.add_argument("--warmup", type=int, default=None, help="untimed steps (default 16 decode, 1 prefill/asr)")
     p.add_argument("--steps-per-graph", type=int, default=8)
-    p.add_argument("--model", choices=("8b", "0.6b"), default="8b")
+    p.add_argument("--model", choices=("8b", "0.6b", "1.7b"), default="8b")
     p.add_argument("--policy", choices=("uniform", "q4_k_m"), default="uniform",
                    help="weight types: uniform Q4_K (the headline int4 config) or the Q4_K_M mix")
     p.add_argument("--positions", type=int, default=PROMPT_POSITIONS, help="KV positions prefilled before timing")
@@ -298,7 +298,7 @@ def main() -> int:
     import torch
 
     from torch2vk_amd import kernels
-    from torch2vk_amd.qwen3.config import QWEN3_0_6B, QWEN3_8B
+    from torch2vk_amd.qwen3.config import QWEN3_1_7B, QWEN3_8B
     from torch2vk_amd.qwen3.model import Qwen3Decoder
     from torch2vk_amd.qwen3.weights import synthetic_weights
 
@@ -306,7 +306,7 @@ def main() -> int:
         print("no HIP device", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
-    cfg = QWEN3_8B if args.model == "8b" else QWEN3_0_6B
+    cfg = QWEN3_8B if args.model == "8b" else QWEN3_1_7B
     t_setup = time.time()
     weights = synthetic_weights(cfg, device=dev, seed=0, policy=args.policy)
     total_steps = args.warmup + args.steps + args.steps_per_graph
