@@ -288,8 +288,10 @@ using DlQwen3_8B = DlShape<16, 48, 32, 3, DL_R_QKV, DL_PRE_QKV, 2, DL_R_O, DL_PR
                            DL_PRE_DOWN, true, DL_BLOCKS, true>;
 using DlQwen3_0_6B = DlShape<4, 12, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, false>;
 // Qwen3-1.7B (hidden 2048, MLP 6144, 16 / 8 heads): rows of 8 and 24 superblocks, 2 rows a unit; Q|K|V one unit
-// per wave, gate|up two, o and down spread
-using DlQwen3_1_7B = DlShape<8, 24, 16, 1, 1, 1, 1, 1, 1, 2, 2, 1, 1, 1, 1, false>;
+// per wave, gate|up two, o and down spread.  The Q|K|V unit is issued once h is staged (647 against 654 us per
+// launch at KV 4096, 551 against 555 at 192; down after its input, a ring of one gate|up unit, late o_proj
+// units and matrix-core P.V measured equal or slower)
+using DlQwen3_1_7B = DlShape<8, 24, 16, 1, 1, 0, 1, 1, 1, 2, 2, 1, 1, 1, 1, false>;
 // four 0.6B sequences of 64 blocks each: every phase's units over 512 waves (Q|K|V 2 per wave, o 1, gate|up 2,
 // down spread), attention over 8 blocks per kv head.  The down units are issued once the input is staged, not
 // before the wait: 679 against 694 us per launch at KV 1540 (the single-sequence shapes measured slower so)
