@@ -3,6 +3,8 @@ CPU oracle, through the C ABI."""
 
 from __future__ import annotations
 
+from contextlib import contextmanager
+
 import numpy as np
 import pytest
 import torch
@@ -12,6 +14,20 @@ from oracle import reference as R
 from tests.conftest import assert_close
 
 pytestmark = pytest.mark.gpu
+
+
+@contextmanager
+def _in_loop():
+    """The quantized GEMM dequantising inside its tile loop at any M: without this, from
+    kernels.DEQUANT_FIRST_ROWS rows it dequantises once and runs the bf16-row kernels it is compared with."""
+    from torch2vk_amd import kernels
+
+    saved = kernels.DEQUANT_FIRST_ROWS
+    kernels.DEQUANT_FIRST_ROWS = 0
+    try:
+        yield
+    finally:
+        kernels.DEQUANT_FIRST_ROWS = saved
 
 
 def _problem(wtype, m, k, n, seed):
@@ -211,20 +227,54 @@ def test_bf16_gemm_large_grid_equals_quantized_gemm(device, wtype, m, k, n):
     w = kernels.quantize(torch.randn(n, k, generator=g, device=device) * 0.02, wtype)
     wb = kernels.dequantize_bf16(w, wtype, k)
     x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
-    yq = kernels.gemm(x, w, wtype, out_dtype=torch.float32, splits=1)
+    with _in_loop():
+        yq = kernels.gemm(x, w, wtype, out_dtype=torch.float32, splits=1)
     yb = kernels.gemm(x, wb, "bf16", out_dtype=torch.float32, splits=1)
     torch.testing.assert_close(yb, yq, rtol=0, atol=0)
-    yq16 = kernels.gemm(x, w, wtype, out_dtype=torch.bfloat16, splits=1)
+    with _in_loop():
+        yq16 = kernels.gemm(x, w, wtype, out_dtype=torch.bfloat16, splits=1)
     yb16 = kernels.gemm(x, wb, "bf16", out_dtype=torch.bfloat16, splits=1)
     torch.testing.assert_close(yb16, yq16, rtol=0, atol=0)
     r = torch.randn(m, n, generator=g, device=device)
     rq, rb = r.clone(), r.clone()
-    kernels.gemm(x, w, wtype, out=rq, residual=rq, splits=1)
+    with _in_loop():
+        kernels.gemm(x, w, wtype, out=rq, residual=rq, splits=1)
     kernels.gemm(x, wb, "bf16", out=rb, residual=rb, splits=1)
     torch.testing.assert_close(rb, rq, rtol=0, atol=0)
     del yq, yb, yq16, yb16, r, rq, rb
     n_ff = n // 2
-    aq = kernels.gemm_swiglu(x, w[:n_ff].contiguous(), w[n_ff:2 * n_ff].contiguous(), wtype, splits=1)
+    with _in_loop():
+        aq = kernels.gemm_swiglu(x, w[:n_ff].contiguous(), w[n_ff:2 * n_ff].contiguous(), wtype, splits=1)
+    ab = kernels.gemm_swiglu(x, wb[:n_ff].contiguous(), wb[n_ff:2 * n_ff].contiguous(), "bf16", splits=1)
+    torch.testing.assert_close(ab, aq, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("m,n", [(4096, 8192), (16384, 1024), (4000, 9000)])
+def test_bf16_ring_grid_sizes_equal_quantized_gemm(device, m, n):
+    """The ring kernel's smaller grids: 512 tiles of 256 x 256, exactly 256 (one round), and ragged M and N at
+    576 tiles: the quantized GEMM's bits, fp32, bf16, residual and SwiGLU."""
+    from torch2vk_amd import kernels
+
+    g = torch.Generator(device=device)
+    g.manual_seed(m + n)
+    k = 320
+    w = kernels.quantize(torch.randn(n, k, generator=g, device=device) * 0.05, "q8_0")
+    wb = kernels.dequantize_bf16(w, "q8_0", k)
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    for dt in (torch.float32, torch.bfloat16):
+        with _in_loop():
+            yq = kernels.gemm(x, w, "q8_0", out_dtype=dt, splits=1)
+        yb = kernels.gemm(x, wb, "bf16", out_dtype=dt, splits=1)
+        torch.testing.assert_close(yb, yq, rtol=0, atol=0)
+    r = torch.randn(m, n, generator=g, device=device)
+    rq, rb = r.clone(), r.clone()
+    with _in_loop():
+        kernels.gemm(x, w, "q8_0", out=rq, residual=rq, splits=1)
+    kernels.gemm(x, wb, "bf16", out=rb, residual=rb, splits=1)
+    torch.testing.assert_close(rb, rq, rtol=0, atol=0)
+    n_ff = n // 2
+    with _in_loop():
+        aq = kernels.gemm_swiglu(x, w[:n_ff].contiguous(), w[n_ff:2 * n_ff].contiguous(), "q8_0", splits=1)
     ab = kernels.gemm_swiglu(x, wb[:n_ff].contiguous(), wb[n_ff:2 * n_ff].contiguous(), "bf16", splits=1)
     torch.testing.assert_close(ab, aq, rtol=0, atol=0)
 
@@ -241,12 +291,14 @@ def test_bf16_large_grid_stage_counts_equal_quantized_gemm(device, k):
     w = kernels.quantize(torch.randn(n, k, generator=g, device=device) * 0.05, "q8_0")
     wb = kernels.dequantize_bf16(w, "q8_0", k)
     x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
-    yq = kernels.gemm(x, w, "q8_0", out_dtype=torch.float32, splits=1)
+    with _in_loop():
+        yq = kernels.gemm(x, w, "q8_0", out_dtype=torch.float32, splits=1)
     yb = kernels.gemm(x, wb, "bf16", out_dtype=torch.float32, splits=1)
     torch.testing.assert_close(yb, yq, rtol=0, atol=0)
     del yq, yb
     n_ff = n // 2
-    aq = kernels.gemm_swiglu(x, w[:n_ff].contiguous(), w[n_ff:].contiguous(), "q8_0", splits=1)
+    with _in_loop():
+        aq = kernels.gemm_swiglu(x, w[:n_ff].contiguous(), w[n_ff:].contiguous(), "q8_0", splits=1)
     ab = kernels.gemm_swiglu(x, wb[:n_ff].contiguous(), wb[n_ff:].contiguous(), "bf16", splits=1)
     torch.testing.assert_close(ab, aq, rtol=0, atol=0)
 

@@ -538,8 +538,8 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_q_kernel(const GemmArgs a) {
 
 // ------------------------------------------- bf16 rows: LDS-DMA ring ----
 
-// The same product over bf16 weight rows (the dequantise-once path) for grids of >= 1024 tiles of 256 x 256
-// without bias or activation, with nothing to convert between memory and the matrix cores:
+// The same product over bf16 weight rows (the dequantise-once path) for grids of >= 512 tiles of 256 x 256 (or
+// whole rounds of 256) without bias or activation, with nothing to convert between memory and the matrix cores:
 //   * 4 waves (2 x 2), each 128 x 128 of the tile: 16 accumulator tiles of 32 x 32 in the AGPRs, so every
 //     16-deep step reads 8 operand fragments from LDS for 16 MFMAs (the 8-wave loop reads 6 for 8);
 //   * A and W stages go from global memory straight into LDS (global_load_lds_dwordx4, no VGPR round trip,
@@ -770,20 +770,24 @@ static void gemm_q_dispatch(GemmArgs a, hipStream_t s) {
     // 256-row tiles for big grids; below ~4 tiles per CU the 128-row tile's
     // finer load balance wins over the bigger tile's operand reuse (measured)
     const uint32_t tiles_256 = (a.m + 255) / 256 * a.tiles_n;
+    if constexpr (std::is_same<F, GemmBF16>::value && EPI != GQEPI_GATED_F32) {
+        // bf16 rows over all of K in one pass: the LDS-DMA ring kernel (256 x 256 tiles, one block per CU) from
+        // two rounds of tiles, or from one when the tiles fill whole rounds; a partial round of these large tiles
+        // loses to the 128-row loop (measured at M 6000-16384: 288 tiles 3 % slower, 384 equal, 512 11 % and 576
+        // 12 % faster, 256 17 % faster)
+        const bool whole_rounds = tiles_256 >= 256 && tiles_256 % 256 == 0;
+        if ((tiles_256 >= 512 || whole_rounds) && a.split_stages == 0 && a.w_blocks * GQ_BK == a.k &&
+            a.bias == nullptr && a.act == GQACT_NONE) {
+            a.tiles_m = (a.m + 255) / 256;
+            hipLaunchKernelGGL((gemm_bf16_ring_kernel<EPI>), dim3(a.tiles_m * a.tiles_n), dim3(GR_THREADS), 0, s, a);
+            return;
+        }
+    }
     if (tiles_256 < 1024 && a.m > 128) {
         a.tiles_m = (a.m + 127) / 128;
         hipLaunchKernelGGL((gemm_q_kernel<F, EPI, 2>), dim3(a.tiles_m * a.tiles_n), block, 0, s, a);
     } else {
         a.tiles_m = (a.m + 255) / 256;
-        if constexpr (std::is_same<F, GemmBF16>::value && EPI != GQEPI_GATED_F32) {
-            // bf16 rows over all of K in one pass: the LDS-DMA ring kernel
-            if (tiles_256 >= 1024 && a.split_stages == 0 && a.w_blocks * GQ_BK == a.k && a.bias == nullptr &&
-                a.act == GQACT_NONE) {
-                hipLaunchKernelGGL((gemm_bf16_ring_kernel<EPI>), dim3(a.tiles_m * a.tiles_n), dim3(GR_THREADS), 0, s,
-                                   a);
-                return;
-            }
-        }
         hipLaunchKernelGGL((gemm_q_kernel<F, EPI, 4>), dim3(a.tiles_m * a.tiles_n), block, 0, s, a);
     }
 }
