@@ -120,12 +120,10 @@ struct GemmQ80 {
         r.q0 = load_u4_ua(p + 2);
         r.q1 = load_u4_ua(p + 18);
     }
-    // 32 bf16 values of this thread's block -> LDS row (t >> 1), columns 32 * (t & 1) ...
-    __device__ static __forceinline__ void store(const Raw& r, uint16_t* lds_b) {
-        const uint32_t t = threadIdx.x;
+    // the block's 32 values as bf16 pairs: d * q, rounded once
+    __device__ static __forceinline__ void convert(const Raw& r, uint32_t (&o)[16]) {
         const float d = r.inside ? f16_bits_to_f32(r.d) : 0.0f;
         const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-        uint32_t o[16];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             const uint32_t w = q[c];
@@ -136,6 +134,12 @@ struct GemmQ80 {
             o[2 * c] = pack_bf16x2(v0, v1);
             o[2 * c + 1] = pack_bf16x2(v2, v3);
         }
+    }
+    // 32 bf16 values of this thread's block -> LDS row (t >> 1), columns 32 * (t & 1) ...
+    __device__ static __forceinline__ void store(const Raw& r, uint16_t* lds_b) {
+        const uint32_t t = threadIdx.x;
+        uint32_t o[16];
+        convert(r, o);
         uint16_t* dst = lds_b + (t >> 1) * GQ_LDS_ROW + (t & 1) * 32;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -324,6 +328,27 @@ __global__ __launch_bounds__(GQ_THREADS) void gemm_dequant_bf16_kernel(const Gem
     for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(dst + 8 * i) = *reinterpret_cast<const uint4*>(src + 8 * i);
 }
 
+// Q8_0 rows straight to memory: thread i converts block i of the matrix (32 values, 34 B in, 64 B out) with
+// GemmQ80::convert, the tile loop's own conversion, with no LDS round trip (each thread writes back only what
+// it converted).
+__global__ __launch_bounds__(256) void gemm_dequant_q8_0_kernel(const uint8_t* __restrict__ w, uint32_t rows,
+                                                                uint32_t blocks_per_row, uint16_t* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)rows * blocks_per_row) return;
+    const uint8_t* p = w + i * 34;  // rows are whole blocks, so block i of the matrix starts at 34 i
+    GemmQ80::Raw r;
+    r.d = load_u16(p);
+    r.inside = true;
+    r.q0 = load_u4_ua(p + 2);
+    r.q1 = load_u4_ua(p + 18);
+    uint32_t o[16];
+    GemmQ80::convert(r, o);
+    uint16_t* dst = out + i * 32;  // and the bf16 rows are blocks_per_row * 32 values long
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<uint4*>(dst + 8 * j) = make_uint4(o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]);
+}
+
 template <class F>
 static int gemm_dequant_launch(const void* w, uint32_t rows, uint32_t k, void* out, void* stream) {
     if (!w || !out) return T2H_ERR_NULL;
@@ -337,8 +362,16 @@ static int gemm_dequant_launch(const void* w, uint32_t rows, uint32_t k, void* o
     a.k = k;
     a.w_blocks = k / F::BLOCK_VALUES;
     a.row_bytes = a.w_blocks * F::BLOCK_BYTES;
-    hipLaunchKernelGGL(gemm_dequant_bf16_kernel<F>, dim3((rows + GQ_BN - 1) / GQ_BN, k / GQ_BK), dim3(GQ_THREADS), 0,
-                       reinterpret_cast<hipStream_t>(stream), a, reinterpret_cast<uint16_t*>(out));
+    if constexpr (std::is_same<F, GemmQ80>::value) {
+        const size_t blocks = (size_t)rows * a.w_blocks;
+        hipLaunchKernelGGL(gemm_dequant_q8_0_kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
+                           reinterpret_cast<hipStream_t>(stream), a.w, rows, a.w_blocks,
+                           reinterpret_cast<uint16_t*>(out));
+    } else {
+        hipLaunchKernelGGL(gemm_dequant_bf16_kernel<F>, dim3((rows + GQ_BN - 1) / GQ_BN, k / GQ_BK),
+                           dim3(GQ_THREADS), 0, reinterpret_cast<hipStream_t>(stream), a,
+                           reinterpret_cast<uint16_t*>(out));
+    }
     T2H_LAUNCH_CHECK();
     return T2H_OK;
 }
