@@ -189,6 +189,10 @@ SEG_CASES = [
     (1, 300, 4, 4, 128, [0, 1, 2, 3, 50, 51, 177, 300]),
     (1, 129, 2, 2, 64, [0, 129]),
     (1, 200, 8, 2, 64, [0, 64, 128, 192, 200]),
+    # segments that start off the 64-key and 128-query grid, several tiles each (the C5 job's utterances)
+    (1, 3000, 4, 4, 64, [0, 1500, 3000]),
+    (1, 1000, 4, 2, 64, [0, 100, 700, 1000]),
+    (1, 700, 2, 2, 128, [0, 300, 700]),
 ]
 
 
@@ -214,8 +218,8 @@ def test_flash_attn_segments_matches_windowed_attention(device, b, t, nh, nk, d,
 
 
 def test_flash_attn_segments_strided_qkv_and_uncovered_tokens(device):
-    """q|k|v as column blocks of one [T, 3D] buffer (the encoder's fused projection); tokens past the last
-    bound get zeros."""
+    """q|k|v as column blocks of one [T, 3D] buffer (the encoder's fused projection); tokens outside the
+    bounds get zeros."""
     from torch2vk_amd import kernels
 
     t, nh, d = 150, 4, 64
@@ -229,6 +233,12 @@ def test_flash_attn_segments_strided_qkv_and_uncovered_tokens(device):
     ref = _segments_ref(cpu[0][:, :100], cpu[1][:, :100], cpu[2][:, :100], [0, 60, 100], d ** -0.5)
     assert_close(got[:, :100].numpy(), ref.numpy(), max_abs=2e-2, min_cos=0.9999, what="strided")
     assert not got[:, 100:].any()
+    # tokens before the first bound see nothing either
+    cu = torch.tensor([20, 60, 100], dtype=torch.int32, device=device)
+    got = kernels.flash_attn_segments(*views, cu).float().cpu()
+    ref = _segments_ref(cpu[0][:, 20:100], cpu[1][:, 20:100], cpu[2][:, 20:100], [0, 40, 80], d ** -0.5)
+    assert_close(got[:, 20:100].numpy(), ref.numpy(), max_abs=2e-2, min_cos=0.9999, what="head gap")
+    assert not got[:, :20].any() and not got[:, 100:].any()
 
 
 def _tower(cfg, device, seed, frames, n_window_infer=None):

@@ -18,8 +18,8 @@
 // 0 on diagonal blocks [cu[i], cu[i+1]) and -FLT_MAX elsewhere
 // (src/models/quantized_qwen3_asr/pytorch_modules.py:95-114).  Given the window
 // bounds cu[] instead of the mask, every query's keys are one interval
-// [lo, hi), a block visits only the key tiles its queries' intervals cover,
-// and only tiles that cross an interval end are masked.
+// [lo, hi): each block takes queries of one segment, visits its keys in tiles
+// from the segment's first key on, and masks only the last, partial tile.
 //
 // Work mapping.  A block of 4 waves takes 128 queries of one (batch, head);
 // wave w owns 32 of them.  Keys stream through LDS 64 at a time, double
@@ -115,31 +115,43 @@ __device__ __forceinline__ void fa_block(const FaArgs& a, int nqb, int& qb, int&
     }
 }
 
-// Keys [lo, hi) of the segment holding token q: the last i with cu[i] <= q.
-// A token outside [cu[0], cu[n_seg]) sees nothing: an empty range at the
-// nearer end of the table, so that ranges still never shrink as q grows.
-__device__ __forceinline__ int2 fa_segment(const FaArgs& a, int q) {
+// Segments: the query blocks of each segment start at its first token, so that no block holds queries of two
+// segments (it would visit the keys of both, twice the tiles of its neighbours).  The table is extended to
+// E = [0, cu[0], ..., cu[n_seg], t_len], each bound clamped to [0, t_len]; segment i of E is [E_i, E_i+1), the
+// first and the last being the tokens outside the table, which see no keys.  Segment i owns the blocks
+// [f(i), f(i + 1)) of a (batch, head), f(i) = floor(E_i / FA_BM) + i: at least ceil(len_i / FA_BM) of them
+// (a spare one finds no queries and exits), so f(n_seg + 2) blocks cover every token.  f ascends with E, and a
+// binary search finds a block's segment; a table that does not ascend gives wrong windows, never an access
+// outside [0, t_len).
+__device__ __forceinline__ int fa_ext_bound(const FaArgs& a, int i) {
+    if (i <= 0) return 0;
+    if (i >= (int)a.n_seg + 2) return (int)a.t_len;
+    return min(max(a.cu[i - 1], 0), (int)a.t_len);
+}
+
+// Queries [q0, q_end) and keys [lo, hi) of virtual block vb of a (batch, head); false when it has no queries.
+__device__ __forceinline__ bool fa_seg_block(const FaArgs& a, int vb, int& q0, int& q_end, int& lo, int& hi) {
     const int n = (int)a.n_seg;
-    if (q < a.cu[0]) return make_int2(a.cu[0], a.cu[0]);
-    if (q >= a.cu[n]) return make_int2(a.cu[n], a.cu[n]);
-    int lo = 0, hi = n;  // cu[lo] <= q < cu[hi]
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (a.cu[mid] <= q) lo = mid;
-        else hi = mid;
+    int l = 0, r = n + 2;  // f(l) <= vb < f(r)
+    while (r - l > 1) {
+        const int mid = (l + r) >> 1;
+        if (fa_ext_bound(a, mid) / FA_BM + mid <= vb) l = mid;
+        else r = mid;
     }
-    return make_int2(a.cu[lo], a.cu[lo + 1]);
+    const int s_lo = fa_ext_bound(a, l);
+    const int s_hi = max(s_lo, fa_ext_bound(a, l + 1));
+    q0 = (int)min((long long)s_lo + (long long)(vb - (s_lo / FA_BM + l)) * FA_BM, (long long)s_hi);
+    q_end = min(q0 + FA_BM, s_hi);
+    const bool in_table = l >= 1 && l <= n;
+    lo = in_table ? s_lo : 0;
+    hi = in_table ? s_hi : 0;
+    return q0 < q_end;
 }
 
 // Keys [lo, hi) that query q may see, clamped to [0, s_len).
-template <bool CAUSAL, bool SEG>
+template <bool CAUSAL>
 __device__ __forceinline__ int2 fa_key_range(const FaArgs& a, int q) {
     int lo = 0, hi = (int)a.s_len;
-    if constexpr (SEG) {
-        const int2 r = fa_segment(a, q);
-        lo = max(r.x, 0);
-        hi = min(r.y, hi);
-    }
     if constexpr (CAUSAL) hi = min(hi, q + a.causal_offset + 1);
     return make_int2(lo, max(lo, hi));
 }
@@ -163,23 +175,30 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(MASK
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int half = lane >> 5;
     int qb, b, h;
-    fa_block(a, ((int)a.t_len + FA_BM - 1) / FA_BM, qb, b, h);
+    fa_block(a, SEG ? (int)(a.t_len / FA_BM) + (int)a.n_seg + 2 : ((int)a.t_len + FA_BM - 1) / FA_BM, qb, b, h);
     const int kvh = h / a.group;
-    const int q0 = qb * FA_BM;
+    int q0, q_end = (int)a.t_len, seg_lo = 0, seg_hi = 0;
+    if constexpr (SEG) {
+        if (!fa_seg_block(a, qb, q0, q_end, seg_lo, seg_hi)) return;  // block-uniform, before any barrier
+    } else {
+        q0 = qb * FA_BM;
+    }
     const int qi = q0 + 32 * wave + (lane & 31);  // this lane's query
-    const bool q_valid = qi < (int)a.t_len;
-    const int qc = q_valid ? qi : (int)a.t_len - 1;
+    const bool q_valid = qi < q_end;
+    const int qc = q_valid ? qi : q_end - 1;
     const int s_len = (int)a.s_len;
 
     // Key ranges only grow with the query index, so the block's queries see
     // [range(q0).lo, range(q_last).hi) and a wave's need no mask on the keys
-    // between its last query's lo and its first query's hi.
-    const int q_last = min(q0 + FA_BM, (int)a.t_len) - 1;
-    const int2 rq = fa_key_range<CAUSAL, SEG>(a, qc);
-    const int blk_lo = fa_key_range<CAUSAL, SEG>(a, q0).x;
-    const int blk_hi = fa_key_range<CAUSAL, SEG>(a, q_last).y;
-    int t_first = blk_lo / FA_BN;
-    int t_end = blk_hi > blk_lo ? (blk_hi + FA_BN - 1) / FA_BN : t_first;
+    // between its last query's lo and its first query's hi.  A segment's
+    // queries all see its keys, in tiles from its first key on.
+    const int q_last = min(q0 + FA_BM, q_end) - 1;
+    const int2 rq = SEG ? make_int2(seg_lo, seg_hi) : fa_key_range<CAUSAL>(a, qc);
+    const int blk_lo = SEG ? seg_lo : fa_key_range<CAUSAL>(a, q0).x;
+    const int blk_hi = SEG ? seg_hi : fa_key_range<CAUSAL>(a, q_last).y;
+    const int key_base = SEG ? blk_lo : 0;  // key of tile 0
+    int t_first = SEG ? 0 : blk_lo / FA_BN;
+    int t_end = blk_hi > blk_lo ? (blk_hi - key_base + FA_BN - 1) / FA_BN : t_first;
     if constexpr (MASK) {
         // all-masked tiles at either end of the block's row of the mask are not visited at all
         if (a.tiles != nullptr) {
@@ -255,7 +274,7 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(MASK
     float l_part = 0.0f;      // this half-wave's share of the running sum
 
     if (t_end > t_first) {
-        load_tile(t_first * FA_BN);
+        load_tile(key_base + t_first * FA_BN);
         store_tile(0);
     }
     // Every load issued so far (the q fragments included) has landed before the loop: the compiler's wait
@@ -274,7 +293,7 @@ __global__ __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(MASK
 
     for (int t = t_first; t < t_end; ++t) {
         const int buf = (t - t_first) & 1;
-        const int t0 = t * FA_BN;
+        const int t0 = key_base + t * FA_BN;
         if (t + 1 < t_end) load_tile(t0 + FA_BN);
         const int cls = trow != nullptr ? (int)trow[t] : FA_TILE_MIXED;  // block-uniform
         if (cls != FA_TILE_MASKED) {
@@ -469,8 +488,10 @@ static int fa_prefill(const void* q, const void* k, const void* v, void* out, co
     if (nh == 0 || nk == 0 || nh % nk != 0) return T2H_ERR_SHAPE;
     if (batch == 0 || t_len == 0) return T2H_OK;
     if (s_len == 0) return T2H_ERR_SHAPE;
-    if ((size_t)batch * nh * ((t_len + FA_BM - 1) / FA_BM) > 0x7fffffffu || t_len > 0x7fffffffu - FA_BM ||
-        s_len > 0x7fffffffu)
+    // query blocks per (batch, head); with segments, a block per FA_BM tokens and one more per segment (the
+    // blocks of each segment start at its first token), and one each for the tokens before and after the table
+    const uint64_t nqb = cu ? (uint64_t)t_len / FA_BM + n_seg + 2 : ((uint64_t)t_len + FA_BM - 1) / FA_BM;
+    if ((uint64_t)batch * nh * nqb > 0x7fffffffu || t_len > 0x7fffffffu - FA_BM || s_len > 0x7fffffffu)
         return T2H_ERR_SHAPE;
     const int n_strides = mask ? 14 : 12;
     for (int i = 0; i < n_strides; ++i)
@@ -522,7 +543,7 @@ static int fa_prefill(const void* q, const void* k, const void* v, void* out, co
     a.causal_offset = causal_offset;
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf((float)d);
     a.scale_log2 = sc * FA_LOG2E;
-    const dim3 grid((uint32_t)((t_len + FA_BM - 1) / FA_BM * batch * nh));
+    const dim3 grid((uint32_t)(nqb * batch * nh));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (d == 128) fa_launch<128>(causal != 0, mask != nullptr, cu != nullptr, grid, a, s);
     else fa_launch<64>(causal != 0, mask != nullptr, cu != nullptr, grid, a, s);
