@@ -272,6 +272,9 @@ struct DlShape {
     static constexpr bool o_late = O_LATE;
     static_assert(NH % NK == 0 && NH / NK <= 4, "GQA group of 1..4 q heads");
 };
+#ifndef DL_QKV_SKIP
+#define DL_QKV_SKIP 1
+#endif
 #ifndef DL_R_QKV
 #define DL_R_QKV 2
 #endif
@@ -345,10 +348,13 @@ enum DlFmt { DL_FMT_Q4 = 0, DL_FMT_Q4_TAIL6 = 1, DL_FMT_Q6 = 2 };
 // (blockIdx.x % NB: one sequence, or one of 256 / NB).  Block-major when every
 // wave has a unit; SPREAD (fewer units than waves): across the blocks first, so
 // that every CU streams a share.
+// SPREAD with `skip`: the first `skip` blocks of the sequence take no unit (their index is past every unit) and
+// the units spread over the others.
 template <bool SPREAD, int NB>
-__device__ __forceinline__ uint32_t dl_unit(uint32_t wave, uint32_t i) {
+__device__ __forceinline__ uint32_t dl_unit(uint32_t wave, uint32_t i, uint32_t skip = 0) {
     constexpr uint32_t NW = NB * DL_WAVES;
     const uint32_t lb = blockIdx.x % NB;
+    if (SPREAD && skip != 0) return lb < skip ? 0xffffffffu : wave * (NB - skip) + (lb - skip) + i * NW;
     return SPREAD ? wave * NB + lb + i * NW : lb * DL_WAVES + wave + i * NW;
 }
 
@@ -359,6 +365,7 @@ struct DlRows {
     uint32_t n_rows;    // output rows of the phase
     uint32_t n_rows4;   // DL_FMT_Q4_TAIL6: rows 0 .. n_rows4 - 1 are w0's (Q4_K), the rest w6's rows (Q6_K)
     const uint8_t* w6;
+    uint32_t skip;      // SPREAD phases: leading blocks of the sequence that take no unit (dl_unit)
 };
 
 // Issue unit `unit` of a matrix of n_rows rows (Q4_K, or Q6_K with Q6).
@@ -695,7 +702,7 @@ __device__ __forceinline__ void dl_store_unit(const DlOut& o, uint32_t unit, uin
 template <int FMT, int UPW, bool SPREAD, int NB, int NSB, int NG>
 __device__ __forceinline__ void dl_issue_slot(DlUnit<NSB, NG>& u, const DlRows& r, int wave, int i) {
     constexpr int RPW = DlUnit<NSB, NG>::RPW;
-    const uint32_t unit = dl_unit<SPREAD, NB>(wave, i);
+    const uint32_t unit = dl_unit<SPREAD, NB>(wave, i, r.skip);
     if constexpr (FMT == DL_FMT_Q6) {
         dl_issue_unit<true>(u, r.w0, r.w1, r.n_rows, unit);
     } else if constexpr (FMT == DL_FMT_Q4_TAIL6) {
@@ -715,7 +722,7 @@ template <int NSB, int NG, int UPW, int PRE, bool SPREAD, int NB, int FMT = DL_F
 __device__ __forceinline__ void dl_issue_pre(DlUnit<NSB, NG> (&u)[UPW], const DlRows& rows) {
     constexpr int RPW = DlUnit<NSB, NG>::RPW;
     const int wave = __builtin_amdgcn_readfirstlane(dl_tid() >> 6);
-    if (SPREAD && dl_unit<SPREAD, NB>(wave, 0) >= (rows.n_rows + RPW - 1) / RPW) return;
+    if (SPREAD && dl_unit<SPREAD, NB>(wave, 0, rows.skip) >= (rows.n_rows + RPW - 1) / RPW) return;
 #pragma unroll
     for (int i = 0; i < PRE; ++i) dl_issue_slot<FMT, UPW, SPREAD, NB>(u[i], rows, wave, i);
 }
@@ -742,7 +749,7 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
     static_assert(!SPREAD || UPW == 1, "spread phases have one unit per wave");
     const int wave = __builtin_amdgcn_readfirstlane(dl_tid() >> 6);
     const uint32_t n_units = (rows.n_rows + RPW - 1) / RPW;
-    const bool active = !SPREAD || dl_unit<SPREAD, NB>(wave, 0) < n_units;  // wave-uniform
+    const bool active = !SPREAD || dl_unit<SPREAD, NB>(wave, 0, rows.skip) < n_units;  // wave-uniform
     __syncthreads();  // every wave is done with the previous phase's LDS
     DlHold hd = out.hold;
     hd.lds = sm.g.hold;
@@ -770,7 +777,7 @@ __device__ __forceinline__ void dl_gemv_phase(SH& sm, DlUnit<NSB, NG> (&u)[UPW],
     for (int i = 0; i < UPW; ++i) {
         __builtin_amdgcn_sched_barrier(0);
         float res[NG][RPW];
-        const uint32_t unit = dl_unit<SPREAD, NB>(wave, i);
+        const uint32_t unit = dl_unit<SPREAD, NB>(wave, i, rows.skip);
         if constexpr (FMT == DL_FMT_Q6) {
             dl_dot_unit6(u[i], sm.g.xp, sm.g.xsum16, res);
         } else if constexpr (FMT == DL_FMT_Q4_TAIL6) {
@@ -1245,6 +1252,7 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgsS
         r.w1 = dl_gptr<const uint8_t>(layer_ptr(layer, f1));
         r.n_rows = r.n_rows4 = n_rows;
         r.w6 = nullptr;
+        r.skip = 0;
         return r;
     };
     // q | k | v rows, contiguous (q | k only when v is Q6_K: the DL_FMT_Q4_TAIL6 phase sets n_rows4 and w6)
@@ -1266,6 +1274,9 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgsS
     constexpr bool o_sp = S::HID / DlUnit<S::QSB, 1>::RPW < S::NW;
     constexpr bool gu_sp = S::MLP / DlUnit<S::HSB, 2>::RPW < S::NW;
     constexpr bool dn_sp = S::HID / DlUnit<S::MSB, 1>::RPW < S::NW;
+    // spread Q|K|V units also fit the blocks other than the direct attention's 8
+    constexpr bool qkv_skip_ok =
+        DL_QKV_SKIP && qkv_sp && S::QKV_ROWS / DlUnit<S::HSB, 1>::RPW <= (NB - 8) * DL_WAVES;
     static_assert((S::QKV_ROWS / DlUnit<S::HSB, 1>::RPW + S::NW - 1) / S::NW <= S::qkv_u &&
                       (S::HID / DlUnit<S::QSB, 1>::RPW + S::NW - 1) / S::NW <= S::o_u &&
                       (S::MLP / DlUnit<S::HSB, 2>::RPW + S::NW - 1) / S::NW <= S::gu_u &&
@@ -1307,6 +1318,12 @@ __global__ __launch_bounds__(DL_THREADS) void decode_layers_kernel(const DlArgsS
         out.e_out = e_qkv;
         const bool v6 = wtypes & DL_WT_V_Q6;
         DlRows qrows = qkv_rows(layer);
+        // With the attention on one block per kv head (blocks 0..7), those blocks stream their kv head's whole
+        // K/V rows during this phase: spread Q|K|V units go to the other blocks, which otherwise finished the
+        // phase 0.8-1.4 us before them (traced at the 0.6B shape, KV 192)
+        if constexpr (qkv_skip_ok) {
+            if (att_direct) qrows.skip = 8;
+        }
         if (v6) {
             qrows.n_rows4 = S::QD + S::KVD;
             qrows.w6 = dl_gptr<const uint8_t>(layer_ptr(layer, DL_WV));
