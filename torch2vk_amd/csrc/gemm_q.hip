@@ -770,8 +770,45 @@ __global__ __launch_bounds__(GR_THREADS) void gemm_bf16_ring_kernel(const GemmAr
             }
         return;
     }
-    // fp32 (a tile column is a whole 128-B line per row), plus the residual: a tile's 16 residual values are
-    // loaded before any of its results is stored
+    if constexpr (EPI == GQEPI_RESID) {
+        // fp32 plus the residual, which may be the output itself: the compiler keeps every load behind the
+        // stores before it in program order, so the residuals of column group j + 1 (4 x 16 values a lane) are
+        // loaded before group j's results are stored, one group ahead (each element is still read before it
+        // is written, by the same lane).  Loaded just before each 16 stores, the loads of a tile made 16 round
+        // trips one after another.
+        // Buffer loads: a lane offset and a scalar offset per element, so the 64 loads in flight need no
+        // address registers; rows past M read as zeros (the resource's range), columns past N are not stored.
+        float rv[2][4][16];
+        const uint64_t mn4 = (uint64_t)a.m * a.n * 4u;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.residual), (short)0, (int)(mn4 < 0x7fffffffu ? mn4 : 0x7fffffffu), 0x00020000);
+        const uint32_t lane_off = (row_base * a.n + col0) * 4u;
+        auto load_group = [&](int j, float (&r)[4][16]) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t el = (uint32_t)(i * 32 + (e >> 2) * 8 + (e & 3)) * a.n + (uint32_t)j * 32;
+                    r[i][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, lane_off, el * 4u, 0));
+                }
+        };
+        load_group(0, rv[0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (j + 1 < 4) load_group(j + 1, rv[(j + 1) & 1]);
+            const uint32_t col = col0 + j * 32;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t row = row_base + i * 32 + (e >> 2) * 8 + (e & 3);
+                    if (row < a.m && col < a.n)
+                        reinterpret_cast<float*>(a.c)[(size_t)row * a.n + col] = rv[j & 1][i][e] + acc[i][j][e];
+                }
+        }
+        return;
+    }
+    // fp32 (a tile column is a whole 128-B line per row)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint32_t col = col0 + j * 32;
@@ -809,8 +846,10 @@ static void gemm_q_dispatch(GemmArgs a, hipStream_t s) {
         // loses to the 128-row loop (measured at M 6000-16384: 288 tiles 3 % slower, 384 equal, 512 11 % and 576
         // 12 % faster, 256 17 % faster)
         const bool whole_rounds = tiles_256 >= 256 && tiles_256 % 256 == 0;
+        // (the residual epilogue addresses the residual with 32-bit byte offsets)
+        const bool resid_fits = EPI != GQEPI_RESID || (uint64_t)a.m * a.n * 4u < 0x80000000ull;
         if ((tiles_256 >= 512 || whole_rounds) && a.split_stages == 0 && a.w_blocks * GQ_BK == a.k &&
-            a.bias == nullptr && a.act == GQACT_NONE) {
+            a.bias == nullptr && a.act == GQACT_NONE && resid_fits) {
             a.tiles_m = (a.m + 255) / 256;
             hipLaunchKernelGGL((gemm_bf16_ring_kernel<EPI>), dim3(a.tiles_m * a.tiles_n), dim3(GR_THREADS), 0, s, a);
             return;
