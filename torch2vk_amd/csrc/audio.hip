@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const TI* __restrict__ 
 
 // --------------------------------------------------------------- gelu --
 
-__device__ __forceinline__ float gelu_erf_f(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+__device__ __forceinline__ float gelu_erf_f(float v) { return gelu_as(v); }  // erf by Abramowitz-Stegun 7.1.26
 
 template <typename TI, typename TO>
 __global__ __launch_bounds__(256) void gelu_kernel(const TI* __restrict__ x, TO* __restrict__ out, uint64_t n4) {

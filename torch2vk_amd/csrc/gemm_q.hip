@@ -86,9 +86,8 @@ __device__ __forceinline__ const uint8_t* gemm_w_row(const GemmArgs& a, uint32_t
     }
 }
 
-// GELU with the exact erf (the reference's GELU_F32 evaluates erf by
-// Abramowitz-Stegun 7.1.26, |error| < 1.5e-7: src/models/quantized_qwen3_asr/shaders/gelu_f32.py:61-76)
-__device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+// GELU of the bias + GELU epilogues (gelu_as: erf by Abramowitz-Stegun 7.1.26, as the reference's GELU)
+__device__ __forceinline__ float gelu_erf(float v) { return gelu_as(v); }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
