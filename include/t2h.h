@@ -202,7 +202,8 @@ int t2h_q6k_gemm(const void* x, const void* w, void* y, int out_dtype, const flo
                  uint32_t k, uint32_t n, void* stream);
 /* y[m, n] = act(x[m, k] . deq(W[n, w_k])^T + bias) (+ residual), W Q8_0 rows of w_k / 32 blocks, w_k <= k,
  * w_k % 32 == 0, k % 64 == 0 (columns of x past w_k multiply zeros; keep them finite).  bias fp32 [n] or
- * NULL; act 0 = none, 1 = GELU (exact erf); out fp32 or bf16 (fp32 with residual, which may alias y).
+ * NULL; act 0 = none, 1 = GELU (erf by Abramowitz-Stegun 7.1.26, as the reference's GELU); out fp32 or bf16
+ * (fp32 with residual, which may alias y).
  * replaces LINEAR_BIAS_Q8_0W_F32B_F32 (src/models/quantized_qwen3_asr/shaders/linear_bias_q8_0w_f32b_f32.py:27-213)
  * and, after t2h_im2col, CONV2D_Q8_0W_F32B_F16{,_2,_3} (shaders/conv2d_q8_0w_f32b_f16.py:25-136); the GELU that
  * follows each of them in the audio tower (dispatch/audio_encoder.py:27-63) is fused here. */

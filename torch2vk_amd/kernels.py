@@ -511,8 +511,9 @@ def q8_0_linear(x: torch.Tensor, w: torch.Tensor, *, bias: torch.Tensor | None =
                 residual: torch.Tensor | None = None, splits: int | None = None) -> torch.Tensor:
     """y[M, N] = act(x[M, K] . deq(W)^T + bias) (+ residual) on the matrix cores (LINEAR_BIAS_Q8_0W_F32B_F32).
     x bf16 with K % 64 == 0; W Q8_0 rows of w_k = 32 * blocks <= K values (x's columns past w_k must be
-    finite: they multiply zeros); bias fp32 [N]; act None or "gelu" (exact erf).  From DEQUANT_FIRST_ROWS rows
-    with w_k == K, W is dequantised once and the bf16 rows run t2h_bf16_linear (the same bits)."""
+    finite: they multiply zeros); bias fp32 [N]; act None or "gelu" (erf by Abramowitz-Stegun 7.1.26, as the
+    reference).  From DEQUANT_FIRST_ROWS rows with w_k == K, W is dequantised once and the bf16 rows run
+    t2h_bf16_linear (the same bits)."""
     _check(x, "x", torch.bfloat16)
     _check(w, "weight", torch.uint8, align=1)
     k = int(x.shape[-1])
