@@ -1036,8 +1036,9 @@ def bench_prefill(args) -> int:
 
 
 def cpu_baseline_prefill(lw, c) -> dict:
-    """The CPU oracle's Qwen3 forward of one 8B-shape layer (weights dequantized from the same Q8_0 bytes) over
-    one 256-token chunk, scaled to 36 layers: tokens/s of prefill on the host cores."""
+    """The CPU oracle's Qwen3 forward of all 36 8B-shape layers over one 256-token chunk: tokens/s of prefill on
+    the host cores.  The layers share one weight set (layer 0's, dequantized from the same Q8_0 bytes; 773 MB of
+    fp32 per layer, far past any CPU cache, so re-reading one set costs what 36 distinct ones would)."""
     import torch
 
     import oracle
@@ -1055,26 +1056,30 @@ def cpu_baseline_prefill(lw, c) -> dict:
              "layers.0.down": torch.from_numpy(oracle.dequant_q8_0(lw["down"].cpu().numpy(), c.mlp))}
     for n in ("input_norm", "post_norm", "q_norm", "k_norm"):
         dense[f"layers.0.{n}"] = lw[n].cpu()
+    for i in range(1, c.layers):
+        for n in ("q", "k", "v", "o", "gate", "up", "down", "input_norm", "post_norm", "q_norm", "k_norm"):
+            dense[f"layers.{i}.{n}"] = dense[f"layers.0.{n}"]
     dense["embed"] = torch.randn(256, c.hidden)
     dense["norm"] = torch.ones(c.hidden)
     dense["lm_head"] = torch.zeros(1, c.hidden)
     shape = Qwen3Shape(hidden=c.hidden, layers=c.layers, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
                        mlp=c.mlp, vocab=c.vocab, rope_theta=c.rope_theta)
     times = []
-    for _ in range(5):
+    for _ in range(3):
         model = Qwen3CpuModel(shape, dense, max_positions=256)
         t0 = time.perf_counter()
         model.forward(torch.arange(256), start=0)
         times.append(time.perf_counter() - t0)
-    t_layer = statistics.median(times)
+    t_chunk = statistics.median(times)
     return {
-        "value": round(256 / (c.layers * t_layer), 2),
+        "value": round(256 / t_chunk, 2),
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
         "sample": f"CPU oracle Qwen3 forward (torch {torch.__version__}, fp32 dense weights dequantized from the "
-                  f"Q8_0 bytes) of 1 of {c.layers} layers over one 256-token chunk (median of 5 runs {t_layer * 1e3:.0f} ms), "
-                  f"x {c.layers}; attention at 256 rather than 2048 tokens, so this overstates the CPU rate",
+                  f"Q8_0 bytes, one weight set shared by the {c.layers} layers) of all {c.layers} layers over one "
+                  f"256-token chunk (median of 3 runs {t_chunk * 1e3:.0f} ms); attention at 256 rather than 2048 "
+                  f"tokens, so this overstates the CPU rate",
     }
 
 
@@ -1169,7 +1174,8 @@ def bench_asr(args) -> int:
     print(f"[bench] asr step {per_step * 1e3:.1f} ms ({frames_s:.0f} frames/s); encoder {enc_s * 1e3:.2f} ms, "
           f"{enc_tflops:.1f} TFLOP/s; fc1 {fc1_us:.1f} us {fc1_tflops:.1f} TFLOP/s; tokens {len(transcripts[0])}",
           file=sys.stderr, flush=True)
-    cpu = None if args.no_cpu_baseline else cpu_baseline_asr(enc, ecfg, frames)
+    cpu = None if args.no_cpu_baseline else cpu_baseline_asr(enc, ecfg, feats_in[:frames], tw, tcfg,
+                                                             ids.tolist(), audio_pos.tolist(), new_tokens)
     line = {
         "metric": "Qwen3-ASR-shape audio frames/s: 24-layer 1024-wide encoder over 4 x 1500 frames, then a "
                   "0.6B-shape int4 decoder, 64 greedy tokens per utterance",
@@ -1224,52 +1230,55 @@ def ecfg_audio_id() -> int:
     return AUDIO_TOKEN_ID
 
 
-def cpu_baseline_asr(enc, ecfg, frames: int) -> dict:
-    """The CPU oracle's encoder layer (weights dequantized from the same Q8_0 bytes) over one 1500-frame
-    utterance, scaled to 24 layers x 4 utterances: encoder frames/s on the host cores."""
-    from dataclasses import replace
-
-    import numpy as np
+def cpu_baseline_asr(enc, ecfg, feats: "torch.Tensor", tw, tcfg, ids: list[int], audio_pos: list[int],
+                     new_tokens: int) -> dict:
+    """One utterance's whole job on the host cores through the CPU oracle: the encoder (every layer, then the
+    head) over its frames, its states injected into the prompt's embeddings, the prompt prefilled through every
+    decoder layer, then ``new_tokens`` greedy tokens.  A CPU takes the utterances one after another, so
+    frames/s = frames / the job's time."""
     import torch
 
     from oracle import asr as oasr
-    from torch2vk_amd.qwen3_asr.encoder import PREFIX, audio_tensor_shapes
+    from oracle.qwen3_check import dense_weights
+    from oracle.reference import Qwen3CpuModel, Qwen3Shape
+    from torch2vk_amd.qwen3.weights import matrix_shapes
+    from torch2vk_amd.qwen3_asr.encoder import audio_tensor_shapes
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    one = replace(ecfg, layers=1)
-    shapes = {k: v for k, v in audio_tensor_shapes(one).items() if ".layers.0." in k}
-    w = oasr.dense_from_packed({k: enc.weights.packed[k].cpu().numpy() for k in shapes if len(shapes[k]) > 1},
-                               {k: enc.weights.vectors[k].cpu().numpy() for k in shapes if len(shapes[k]) == 1},
-                               shapes)
-    h = torch.randn(frames, ecfg.d_model)
-    lp = f"{PREFIX}layers.0."
-    hd = ecfg.head_dim
-    times = []
-    for _ in range(2):
-        t0 = time.perf_counter()
-        y = torch.nn.functional.layer_norm(h, (ecfg.d_model,), w[lp + "self_attn_layer_norm.weight"],
-                                           w[lp + "self_attn_layer_norm.bias"], eps=ecfg.eps)
-        q, k, v = (y @ w[lp + f"self_attn.{n}.weight"].T + w[lp + f"self_attn.{n}.bias"] for n in
-                   ("q_proj", "k_proj", "v_proj"))
-        q, k, v = (t.reshape(frames, ecfg.heads, hd).transpose(0, 1) for t in (q, k, v))
-        a = oasr.masked_attention(q, k, v, None, hd ** -0.5).transpose(0, 1).reshape(frames, -1)
-        h2 = h + a @ w[lp + "self_attn.out_proj.weight"].T + w[lp + "self_attn.out_proj.bias"]
-        y = torch.nn.functional.layer_norm(h2, (ecfg.d_model,), w[lp + "final_layer_norm.weight"],
-                                           w[lp + "final_layer_norm.bias"], eps=ecfg.eps)
-        y = torch.nn.functional.gelu(y @ w[lp + "fc1.weight"].T + w[lp + "fc1.bias"])
-        _ = h2 + y @ w[lp + "fc2.weight"].T + w[lp + "fc2.bias"]
-        times.append(time.perf_counter() - t0)
-    t_layer = min(times)
-    del np
+    frames = feats.shape[0]
+    w = oasr.dense_from_packed({k: v.cpu().numpy() for k, v in enc.weights.packed.items()},
+                               {k: v.cpu().numpy() for k, v in enc.weights.vectors.items()}, audio_tensor_shapes(ecfg))
+    dense = dense_weights({k: v.cpu().numpy() for k, v in tw.packed.items()}, tw.types,
+                          {k: v.cpu().numpy() for k, v in tw.norms.items()}, matrix_shapes(tcfg))
+    shape = Qwen3Shape(hidden=tcfg.hidden, layers=tcfg.layers, heads=tcfg.heads, kv_heads=tcfg.kv_heads,
+                       head_dim=tcfg.head_dim, mlp=tcfg.mlp, vocab=tcfg.vocab, rope_theta=tcfg.rope_theta)
+    model = Qwen3CpuModel(shape, dense, max_positions=len(ids) + new_tokens + 1)
+    tid = torch.tensor(ids)
+    pos = torch.tensor(audio_pos)
+    x = feats.float().cpu().clone()
+    t0 = time.perf_counter()
+    states = oasr.encoder_head_cpu(w, ecfg, oasr.encoder_layers_cpu(w, ecfg, x, cu_seqlens=[0, frames]))
+    t_enc = time.perf_counter() - t0
+    emb = dense["embed"][tid].clone()
+    emb[pos] = states.to(emb.dtype)
+    hidden = model.forward(tid, start=0, embeds=emb)
+    tok = int(torch.argmax(model.logits(hidden)))
+    t_prefill = time.perf_counter() - t0 - t_enc
+    for s in range(new_tokens - 1):
+        hidden = model.forward(torch.tensor([tok]), start=len(ids) + s)
+        tok = int(torch.argmax(model.logits(hidden)))
+    t_job = time.perf_counter() - t0
     return {
-        "value": round(frames / (ecfg.layers * t_layer), 2),
+        "value": round(frames / t_job, 2),
         "unit": "frames/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"CPU oracle encoder layer (torch {torch.__version__}, fp32, weights dequantized from the Q8_0 "
-                  f"bytes) over one {frames}-frame utterance (best of 2: {t_layer * 1e3:.0f} ms) x {ecfg.layers} "
-                  f"layers; encoder only, the decoder is not included",
+        "sample": f"CPU oracle (torch {torch.__version__}, fp32 weights dequantized from the same Q8_0 / Q4_K bytes): "
+                  f"one utterance's whole job, {t_job:.2f} s: the {ecfg.layers}-layer encoder and head over {frames} "
+                  f"frames ({t_enc:.2f} s), the {len(ids)}-position prompt with its states through all "
+                  f"{tcfg.layers} decoder layers ({t_prefill:.2f} s), {new_tokens} greedy tokens; a CPU runs the "
+                  f"utterances one after another",
     }
 
 
