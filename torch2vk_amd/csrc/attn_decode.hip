@@ -9,10 +9,10 @@
 //
 // The reference walks the whole cache serially in one workgroup per q head.
 // Here the grid is fixed at (slots, nk) with slots * nk = 256 blocks, one per
-// CU, whatever the length: block (slot, kv head) has 8 waves and wave w covers
-// span = ceil(L / (slots * 8)) consecutive positions for all GROUP q heads of
-// the kv head, so every K/V byte is read once per token and every CU streams
-// an equal share:
+// CU, whatever the length: block (slot, kv head) has W waves (8; 4 at GROUP 8)
+// and wave w covers span = ceil(L / (slots * W)) consecutive positions for all
+// GROUP q heads of the kv head, so every K/V byte is read once per token and
+// every CU streams an equal share:
 //   * K rows are loaded coalesced (4 lanes per row, 64 B each, 16 rows per
 //     load set) and a lane dots its quarter row with the GROUP q vectors
 //     (broadcast from LDS); a quad DPP reduction completes the dot;
@@ -37,7 +37,7 @@
 namespace t2h {
 
 constexpr int AD_D = 128;
-constexpr int AD_WAVES = 8;                   // waves per block
+constexpr int AD_WAVES = 8;                   // waves per block (4 for GROUP 8, see ad_waves)
 constexpr int AD_TILE = 32;                   // positions per wave per tile (two 16-row K load sets; 16 for GROUP 8)
 constexpr int AD_GRID = 256;                  // split blocks per call (slots * nk), one per CU
 constexpr int AD_QROW = 36;                   // LDS q row: 32 dims + 4 pad (conflict-free quarter reads)
@@ -97,14 +97,22 @@ __device__ __forceinline__ void ad_issue_tile(AdTile<TILE>& tl, const uint16_t* 
 // Split-K pass: see the file comment.  Block (slot, kv head); the new K/V row
 // at `pos` is produced by the wave whose span holds it, written to the cache
 // and substituted for the (stale) row it loaded.
+// Waves per split block.  At GROUP 8 a wave carries 8 heads' running state beside its tile, which does not fit
+// the 256 registers of two waves per SIMD: that instantiation runs 4 waves, one per SIMD with the whole
+// register file, each preparing q heads wave and wave + 4.
 template <int GROUP>
-__global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDecodeArgs a) {
+constexpr int ad_waves() { return GROUP >= 8 ? 4 : AD_WAVES; }
+
+template <int GROUP>
+__global__ __launch_bounds__(ad_waves<GROUP>() * 64) void attn_decode_kernel(const AttnDecodeArgs a) {
+    constexpr int W = ad_waves<GROUP>();
+    constexpr int QH = (GROUP + W - 1) / W;           // q heads prepared per wave: wave, wave + W, ...
     constexpr int TILE = GROUP >= 8 ? 16 : AD_TILE;  // registers: TILE V rows + GROUP accumulators
     constexpr int NR = TILE / 16;                     // 16-row K load sets per tile
     __shared__ __align__(16) float qs[GROUP][4][AD_QROW];
-    __shared__ __align__(16) float ps[AD_WAVES][TILE][GROUP];
-    __shared__ float wml[AD_WAVES][GROUP][2];
-    __shared__ __align__(16) float2 wo[AD_WAVES][GROUP][64];
+    __shared__ __align__(16) float ps[W][TILE][GROUP];
+    __shared__ float wml[W][GROUP][2];
+    __shared__ __align__(16) float2 wo[W][GROUP][64];
     __shared__ __align__(16) uint16_t knew[AD_D];
 
     const int tid = threadIdx.x;
@@ -115,9 +123,9 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
     const int pos = *a.pos_ptr;
     const int S = (int)a.s_cap;
     const int L = pos + 1 < S ? pos + 1 : S;
-    const int waves_per_head = (int)a.slots * AD_WAVES;
+    const int waves_per_head = (int)a.slots * W;
     const int span = (L + waves_per_head - 1) / waves_per_head;
-    const int pw = (slot * AD_WAVES + wave) * span;  // first position of this wave
+    const int pw = (slot * W + wave) * span;  // first position of this wave
     int rows = L - pw;
     rows = rows < 0 ? 0 : (rows > span ? span : rows);
     const size_t row_stride = (size_t)a.nk * AD_D;  // elements between positions
@@ -130,11 +138,15 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
     // 0. the small operands first: vmcnt retires in order, so anything loaded
     //    after the cache stream would wait for all of it
     const bool has_w = a.q_norm_w != nullptr;
-    float qx0 = 0.0f, qx1 = 0.0f;
-    if (wave < GROUP) {
-        const int h = kvh * GROUP + wave;
-        qx0 = a.q[h * AD_D + lane];
-        qx1 = a.q[h * AD_D + lane + 64];
+    float qx0[QH], qx1[QH];
+#pragma unroll
+    for (int i = 0; i < QH; ++i) {
+        qx0[i] = qx1[i] = 0.0f;
+        if (wave + i * W < GROUP) {
+            const int h = kvh * GROUP + wave + i * W;
+            qx0[i] = a.q[h * AD_D + lane];
+            qx1[i] = a.q[h * AD_D + lane + 64];
+        }
     }
     float qw0 = 1.0f, qw1 = 1.0f, kw0 = 1.0f, kw1 = 1.0f;
     if (has_w && needs_rope) {
@@ -161,11 +173,15 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
     if (rope && needs_rope) {
         rope_cos_sin(lane, pos, a.theta, cs, sn);
     }
-    if (wave < GROUP) {
-        float r0, r1;
-        norm_rope_pair(qx0, qx1, has_w, qw0, qw1, a.eps, cs, sn, rope, r0, r1);
-        qs[wave][lane >> 5][lane & 31] = r0 * a.scale;
-        qs[wave][2 + (lane >> 5)][lane & 31] = r1 * a.scale;
+#pragma unroll
+    for (int i = 0; i < QH; ++i) {
+        const int g = wave + i * W;
+        if (g < GROUP) {
+            float r0, r1;
+            norm_rope_pair(qx0[i], qx1[i], has_w, qw0, qw1, a.eps, cs, sn, rope, r0, r1);
+            qs[g][lane >> 5][lane & 31] = r0 * a.scale;
+            qs[g][2 + (lane >> 5)][lane & 31] = r1 * a.scale;
+        }
     }
 
     // 3. the wave holding `pos` produces the new K/V row and writes it back
@@ -307,15 +323,15 @@ __global__ __launch_bounds__(AD_WAVES * 64) void attn_decode_kernel(const AttnDe
     }
     __syncthreads();
     const size_t cbase = ((size_t)kvh * a.slots + slot) * GROUP;  // first partial of this block
-    for (int idx = tid; idx < GROUP * 64; idx += AD_WAVES * 64) {
+    for (int idx = tid; idx < GROUP * 64; idx += W * 64) {
         const int g = idx >> 6;
         const int dl = idx & 63;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < AD_WAVES; ++w) M = fmaxf(M, wml[w][g][0]);
+        for (int w = 0; w < W; ++w) M = fmaxf(M, wml[w][g][0]);
         float l = 0.0f, r0 = 0.0f, r1 = 0.0f;
 #pragma unroll
-        for (int w = 0; w < AD_WAVES; ++w) {
+        for (int w = 0; w < W; ++w) {
             const float m = wml[w][g][0];
             const float f = m == -INFINITY ? 0.0f : expf(m - M);
             l = fmaf(f, wml[w][g][1], l);
@@ -451,13 +467,13 @@ extern "C" int t2h_attn_decode(const float* q, const float* k_new, const float* 
     a.theta = theta;
     a.eps = eps;
     a.scale = 1.0f / sqrtf((float)d);
-    const dim3 grid(slots, nk), block(AD_WAVES * 64);
+    const dim3 grid(slots, nk);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const dim3 mgrid(nh), mblock(AD_MERGE_WAVES * 64);
     switch (group) {
 #define T2H_AD_CASE(G)                                                                   \
     case G:                                                                              \
-        hipLaunchKernelGGL(attn_decode_kernel<G>, grid, block, 0, s, a);                 \
+        hipLaunchKernelGGL(attn_decode_kernel<G>, grid, dim3(ad_waves<G>() * 64), 0, s, a); \
         T2H_LAUNCH_CHECK();                                                              \
         hipLaunchKernelGGL(attn_decode_merge_kernel<G>, mgrid, mblock, 0, s, a);         \
         break;
