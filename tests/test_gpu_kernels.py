@@ -364,7 +364,9 @@ def _attn_case(nh, nk, s_cap, pos, seed, device, norm=True, theta=1e6):
                                              # spans past one 32-row tile per wave (L > 8192 at 256 blocks)
                                              (32, 8, 9000, 8999), (32, 8, 20000, 17000), (64, 8, 9000, 8500),
                                              # one kv head: 256 blocks over it
-                                             (4, 1, 3000, 2999), (8, 1, 600, 37)])
+                                             (4, 1, 3000, 2999), (8, 1, 600, 37),
+                                             # GQA group 8 (4 waves a block): several 16-row tiles per wave
+                                             (64, 8, 20000, 17000), (8, 1, 20000, 19999)])
 def test_attn_decode(device, nh, nk, s_cap, pos):
     print(f"attn_decode nh={nh} nk={nk} S={s_cap} pos={pos}", flush=True)
     got, ref, kct, vct, kref, vref, L = _attn_case(nh, nk, s_cap, pos, seed=pos + nh, device=device)
